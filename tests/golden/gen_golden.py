@@ -1,0 +1,79 @@
+"""Writes the golden vectors of tests/golden/*.npz from the reference's own CPU implementation.
+
+The reference (src/core/ref/{quant,ops,f16}.cpp, src/core/{op,tensor,status}.cpp,
+src/tensor/tensor.cpp and the inline R32 pack of src/backends/opencl11/r32.h) is compiled from its
+sources by `make -C oracle ref` into oracle/_ref/libscrapgpu_ref.so; this script runs it on seeded
+inputs and stores inputs and outputs only (no reference code travels). Run in the build container:
+
+    make -C oracle ref && python tests/golden/gen_golden.py
+"""
+import os
+import sys
+
+import numpy as np
+
+sys.path.insert(0, os.path.join(os.path.dirname(__file__), "..", ".."))
+import oracle as O  # noqa: E402
+
+OUT = os.path.dirname(os.path.abspath(__file__))
+
+
+def quant_inputs(dtype, rng):
+    """8 blocks exercising the quantizers' branches: N(0,0.02) weights, N(0,1), a large range, an
+    all-negative block (Q4_K min), an all-zero block, a constant block, tiny values, mixed signs."""
+    bs = O.BLOCK[dtype]
+    parts = [
+        rng.standard_normal(bs) * 0.02,
+        rng.standard_normal(bs),
+        rng.standard_normal(bs) * 1000.0,
+        -1.0 - 0.5 * np.abs(rng.standard_normal(bs)),
+        np.zeros(bs),
+        np.full(bs, 0.375),
+        rng.standard_normal(bs) * 1e-6,
+        np.where(rng.random(bs) < 0.5, -1.0, 1.0) * rng.random(bs) * 3.0,
+    ]
+    return np.concatenate(parts).astype(np.float32)
+
+
+def main():
+    if not O.ref_available():
+        sys.exit("oracle/_ref/libscrapgpu_ref.so is missing: run `make -C oracle ref` first")
+    rng = np.random.default_rng(20261201)
+    out = {}
+    for dt in O.QTYPES:
+        name = O.NAMES[dt]
+        x = quant_inputs(dt, rng)
+        q = O.ref_quantize(dt, x)
+        out[f"{name}_quant_x"] = x
+        out[f"{name}_quant_q"] = q
+        out[f"{name}_quant_y"] = O.ref_dequantize(dt, q, x.size)
+        # random block bytes: dequantization of arbitrary bit patterns (finite scales)
+        nblk = 16
+        raw = rng.integers(0, 256, nblk * O.TYPE_SIZE[dt], dtype=np.uint8).reshape(nblk, -1)
+        scale_off = {O.Q4_0: [0], O.Q8_0: [0], O.Q4_K: [0, 2], O.Q6_K: [208]}[dt]
+        for off in scale_off:
+            h = (rng.integers(0x0400, 0x5000, nblk) | (rng.integers(0, 2, nblk) << 15)).astype(np.uint16)
+            raw[:, off:off + 2] = h.view(np.uint8).reshape(nblk, 2)
+        raw = raw.reshape(-1)
+        out[f"{name}_raw_q"] = raw
+        out[f"{name}_raw_y"] = O.ref_dequantize(dt, raw, nblk * O.BLOCK[dt])
+        # MUL_MAT through scrapgpu_ref_execute: the GPU test shapes of tests/ops/ops_tests.cpp:702-727
+        # plus ragged M and the column counts of the panel paths
+        K = 256 if O.BLOCK[dt] == 256 else 96
+        for M, N in ((24, 1), (24, 4), (37, 7), (37, 17)):
+            w = O.ref_quantize(dt, (rng.standard_normal(K * M) * 0.02).astype(np.float32))
+            xx = rng.standard_normal((N, K)).astype(np.float32)
+            out[f"{name}_mm_K{K}_M{M}_N{N}_w"] = w
+            out[f"{name}_mm_K{K}_M{M}_N{N}_x"] = xx
+            out[f"{name}_mm_K{K}_M{M}_N{N}_y"] = O.ref_mul_mat(dt, w, K, M, xx)
+        # R32 pack of the reference: 2 slices of 40 rows (one full group + a group of 8)
+        Kr, Mr, S = 2 * O.BLOCK[dt], 40, 2
+        nat = rng.integers(0, 256, O.row_bytes(dt, Kr) * Mr * S, dtype=np.uint8)
+        out[f"{name}_r32_K{Kr}_M{Mr}_S{S}_nat"] = nat
+        out[f"{name}_r32_K{Kr}_M{Mr}_S{S}_rep"] = O.ref_r32(dt, Kr, Mr, S, nat, True)
+    np.savez_compressed(os.path.join(OUT, "quant_mulmat_r32.npz"), **out)
+    print("wrote", len(out), "arrays")
+
+
+if __name__ == "__main__":
+    main()
