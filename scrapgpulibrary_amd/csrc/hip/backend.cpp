@@ -1,0 +1,945 @@
+// The `hip` backend: the scrapgpu_backend_vtable of one process over the visible gfx950 GPUs.
+//
+// Replaces, for the quantized MUL_MAT path, what the reference's OpenCL backend does in
+// src/backends/opencl11/api.cpp (objects :45-79, support :252-258,467-473, resolve :546,
+// dispatch :738-773, transfers :1234-1287, plans :1335-1443, vtable :1449-1473, registration
+// :1477-1498) -- redesigned around HIP: one hipStream_t per scrapgpu stream, hipMalloc'd buffers,
+// R32 packing done by a kernel in HBM instead of on the host, and kernel selection by shape
+// (N <= 8: decode matvec; N > 8: bf16 MFMA prefill).
+#include "scrapgpu/hip.h"
+
+#include "../core/tensor_math.h"
+#include "kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace {
+
+extern const scrapgpu_backend_vtable kVtable;
+
+// ---- errors -------------------------------------------------------------------------------------
+
+scrapgpu_status set_err(scrapgpu_status st, const std::string & msg) {
+    scrapgpu_set_last_error(msg.c_str());
+    return st;
+}
+
+scrapgpu_status invalid(const char * m) {
+    return set_err(SCRAPGPU_STATUS_INVALID_ARGUMENT, m);
+}
+
+scrapgpu_status unsupported(const char * m, const char ** reason = nullptr) {
+    if (reason) *reason = m;
+    return set_err(SCRAPGPU_STATUS_UNSUPPORTED, m);
+}
+
+scrapgpu_status hip_fail(hipError_t e, const char * what) {
+    const std::string msg = std::string(what) + ": " + hipGetErrorString(e);
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) return set_err(SCRAPGPU_STATUS_OUT_OF_MEMORY, msg);
+    if (e == hipErrorNoDevice || e == hipErrorInvalidDevice || e == hipErrorLaunchFailure || e == hipErrorIllegalAddress) {
+        return set_err(SCRAPGPU_STATUS_DEVICE_LOST, msg);
+    }
+    return set_err(SCRAPGPU_STATUS_BACKEND_ERROR, msg);
+}
+
+#define SG_HIP(expr, what)                          \
+    do {                                            \
+        const hipError_t e_ = (expr);               \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+// ---- objects --------------------------------------------------------------------------------------
+
+struct Device;
+
+struct Buffer {
+    scrapgpu_object_header hdr;
+    Device * dev;
+    uint8_t * ptr;
+    size_t size;
+    std::atomic<int> plan_refs{0};
+};
+
+struct Stream {
+    scrapgpu_object_header hdr;
+    Device * dev;
+    hipStream_t s;
+    sgk::Scratch scratch{nullptr, 0, nullptr, 0};
+};
+
+struct Device {
+    scrapgpu_object_header hdr;
+    int ordinal;
+    std::string name, arch, driver, tuning;
+    uint64_t total_mem = 0;
+    uint64_t lds = 0;
+    uint32_t cus = 0;
+    std::mutex mu;          // guards the staging buffer and the profiling records
+    uint8_t * staging = nullptr;
+    size_t staging_size = 0;
+};
+
+struct PlanNode {
+    scrapgpu_op_desc op;
+    std::vector<scrapgpu_tensor_desc> in, out;
+    std::vector<uint8_t> params;
+};
+
+struct Plan {
+    scrapgpu_object_header hdr;
+    Device * dev;
+    std::vector<PlanNode> nodes;
+    std::vector<Buffer *> buffers;
+};
+
+struct Registry {
+    std::mutex mu;
+    bool registered = false;
+    std::vector<std::unique_ptr<Device>> devices;
+};
+
+Registry & registry() {
+    static Registry r;
+    return r;
+}
+
+template <typename T>
+T * as(void * obj) {
+    T * t = static_cast<T *>(obj);
+    return t != nullptr && t->hdr.backend == &kVtable ? t : nullptr;
+}
+
+Device * dev_of(scrapgpu_device_t * d) {
+    return as<Device>(d);
+}
+Buffer * buf_of(scrapgpu_buffer_t * b) {
+    return as<Buffer>(b);
+}
+Stream * stream_of(scrapgpu_stream_t * s) {
+    return as<Stream>(s);
+}
+
+hipError_t use(Device * d) {
+    return hipSetDevice(d->ordinal);
+}
+
+// ---- profiling (per-launch HIP events) ----------------------------------------------------------
+
+struct ProfRecord {
+    std::string name;
+    hipEvent_t a, b;
+    double bytes, flops;
+};
+
+struct ProfEntry {
+    std::string name;
+    uint64_t launches = 0;
+    double ms = 0, bytes = 0, flops = 0;
+};
+
+std::atomic<bool> g_prof{false};
+std::mutex g_prof_mu;
+std::vector<ProfRecord> g_prof_pending;
+std::vector<ProfEntry> g_prof_table;
+
+struct ProfScope {
+    hipStream_t s;
+    const char * name = nullptr;
+    double bytes = 0, flops = 0;
+    hipEvent_t a = nullptr, b = nullptr;
+    explicit ProfScope(hipStream_t st) : s(st) {
+        if (g_prof.load(std::memory_order_relaxed) && hipEventCreate(&a) == hipSuccess && hipEventCreate(&b) == hipSuccess) {
+            hipEventRecord(a, s);
+        } else {
+            a = b = nullptr;
+        }
+    }
+    void done(const char * n, double by, double fl) {
+        if (a == nullptr) return;
+        hipEventRecord(b, s);
+        std::lock_guard<std::mutex> lock(g_prof_mu);
+        g_prof_pending.push_back({n ? n : "kernel", a, b, by, fl});
+        a = b = nullptr;
+    }
+    ~ProfScope() {
+        if (a) hipEventDestroy(a);
+        if (b) hipEventDestroy(b);
+    }
+};
+
+void prof_collect() {
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    for (ProfRecord & r : g_prof_pending) {
+        float ms = 0;
+        hipEventSynchronize(r.b);
+        hipEventElapsedTime(&ms, r.a, r.b);
+        auto it = std::find_if(g_prof_table.begin(), g_prof_table.end(), [&](const ProfEntry & e) { return e.name == r.name; });
+        if (it == g_prof_table.end()) {
+            g_prof_table.push_back({r.name});
+            it = g_prof_table.end() - 1;
+        }
+        it->launches += 1;
+        it->ms += ms;
+        it->bytes += r.bytes;
+        it->flops += r.flops;
+        hipEventDestroy(r.a);
+        hipEventDestroy(r.b);
+    }
+    g_prof_pending.clear();
+}
+
+// ---- descriptors ----------------------------------------------------------------------------------
+
+// a caller desc with a smaller struct_size: missing tail = buffer NULL, offset 0, NATURAL
+scrapgpu_tensor_desc load_desc(const scrapgpu_tensor_desc & in) {
+    scrapgpu_tensor_desc d;
+    std::memset(&d, 0, sizeof(d));
+    std::memcpy(&d, &in, std::min(in.struct_size, sizeof(d)));
+    d.struct_size = sizeof(d);
+    return d;
+}
+
+// the device address of a tensor after the bounds check against its buffer
+scrapgpu_status resolve(Device * dev, const scrapgpu_tensor_desc & t, uint8_t ** out, const char * what) {
+    Buffer * b = buf_of(t.buffer);
+    if (b == nullptr) return set_err(SCRAPGPU_STATUS_INVALID_ARGUMENT, std::string(what) + " has no hip buffer");
+    if (b->dev != dev) return set_err(SCRAPGPU_STATUS_INVALID_ARGUMENT, std::string(what) + " lives on another device");
+    const uint64_t n = sg::nbytes(t);
+    if (t.offset > b->size || n > b->size - t.offset) {
+        return set_err(SCRAPGPU_STATUS_INVALID_ARGUMENT, std::string(what) + " exceeds its buffer");
+    }
+    *out = b->ptr + t.offset;
+    return SCRAPGPU_STATUS_OK;
+}
+
+// ---- device enumeration -----------------------------------------------------------------------
+
+size_t api_device_count(void *) {
+    std::lock_guard<std::mutex> lock(registry().mu);
+    return registry().devices.size();
+}
+
+scrapgpu_status api_get_device(void *, size_t index, scrapgpu_device_t ** out) {
+    std::lock_guard<std::mutex> lock(registry().mu);
+    if (index >= registry().devices.size()) return invalid("device index out of range");
+    *out = reinterpret_cast<scrapgpu_device_t *>(registry().devices[index].get());
+    return SCRAPGPU_STATUS_OK;
+}
+
+#define SG_INFO_SET(field, value)                                                        \
+    do {                                                                                 \
+        if (info->struct_size >= offsetof(scrapgpu_device_info, field) + sizeof(info->field)) info->field = (value); \
+    } while (0)
+
+scrapgpu_status api_device_info(scrapgpu_device_t * device, scrapgpu_device_info * info) {
+    Device * d = dev_of(device);
+    if (d == nullptr) return invalid("not a hip device");
+    if (info->struct_size < sizeof(size_t)) return invalid("device info struct is too small");
+    SG_INFO_SET(name, d->name.c_str());
+    SG_INFO_SET(vendor, "AMD");
+    SG_INFO_SET(platform_name, "HIP");
+    SG_INFO_SET(driver_version, d->driver.c_str());
+    SG_INFO_SET(backend_name, "hip");
+    SG_INFO_SET(reported_api_version, d->driver.c_str());
+    SG_INFO_SET(used_api_version, d->driver.c_str());
+    SG_INFO_SET(generation, SCRAPGPU_DEVICE_GENERATION_AMD_GCN);
+    SG_INFO_SET(generation_reason, d->arch.c_str());
+    SG_INFO_SET(total_memory_bytes, d->total_mem);
+    SG_INFO_SET(max_allocation_reported_bytes, d->total_mem);
+    SG_INFO_SET(max_allocation_used_bytes, d->total_mem);
+    SG_INFO_SET(max_work_group_size, (uint64_t) 1024);
+    SG_INFO_SET(local_memory_bytes, d->lds);
+    SG_INFO_SET(compute_units, d->cus);
+    SG_INFO_SET(warp_or_wave_width, 64u);
+    SG_INFO_SET(quirks, (uint64_t) 0);
+    SG_INFO_SET(probed_quirks, (uint64_t) 0);
+    SG_INFO_SET(tuning_profile_name, d->tuning.c_str());
+    SG_INFO_SET(tuning_overrides, "");
+    return SCRAPGPU_STATUS_OK;
+}
+
+// ---- buffers --------------------------------------------------------------------------------------
+
+scrapgpu_status api_buffer_alloc(scrapgpu_device_t * device, size_t size, scrapgpu_buffer_t ** out) {
+    Device * d = dev_of(device);
+    if (d == nullptr) return invalid("not a hip device");
+    SG_HIP(use(d), "hipSetDevice");
+    void * p = nullptr;
+    SG_HIP(hipMalloc(&p, std::max<size_t>(size, 256)), "hipMalloc");
+    Buffer * b = new Buffer;
+    b->hdr.backend = &kVtable;
+    b->dev = d;
+    b->ptr = static_cast<uint8_t *>(p);
+    b->size = size;
+    *out = reinterpret_cast<scrapgpu_buffer_t *>(b);
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status api_buffer_free(scrapgpu_buffer_t * buffer) {
+    Buffer * b = buf_of(buffer);
+    if (b == nullptr) return invalid("not a hip buffer");
+    if (b->plan_refs.load() > 0) return invalid("the buffer is referenced by a live plan");
+    use(b->dev);
+    // work that still reads the buffer must finish before the memory is returned
+    hipDeviceSynchronize();
+    const hipError_t e = hipFree(b->ptr);
+    delete b;
+    if (e != hipSuccess) return hip_fail(e, "hipFree");
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status check_range(Stream * s, Buffer * b, uint64_t off, size_t size) {
+    if (s == nullptr || b == nullptr) return invalid("not a hip stream or buffer");
+    if (b->dev != s->dev) return invalid("buffer and stream belong to different devices");
+    if (off > b->size || size > b->size - off) return invalid("range exceeds the buffer");
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status finish(Stream * s, int blocking, const char * what) {
+    if (blocking) SG_HIP(hipStreamSynchronize(s->s), what);
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status api_buffer_write(scrapgpu_stream_t * stream, scrapgpu_buffer_t * buffer, uint64_t off, const void * data, size_t size, int blocking) {
+    Stream * s = stream_of(stream);
+    Buffer * b = buf_of(buffer);
+    scrapgpu_status st = check_range(s, b, off, size);
+    if (st != SCRAPGPU_STATUS_OK || size == 0) return st;
+    SG_HIP(use(s->dev), "hipSetDevice");
+    SG_HIP(hipMemcpyAsync(b->ptr + off, data, size, hipMemcpyHostToDevice, s->s), "hipMemcpyAsync");
+    // the host pointer may be reused on return (as for the reference's blocking writes)
+    return finish(s, 1, "buffer_write");
+}
+
+scrapgpu_status api_buffer_read(scrapgpu_stream_t * stream, scrapgpu_buffer_t * buffer, uint64_t off, void * data, size_t size, int blocking) {
+    Stream * s = stream_of(stream);
+    Buffer * b = buf_of(buffer);
+    scrapgpu_status st = check_range(s, b, off, size);
+    if (st != SCRAPGPU_STATUS_OK || size == 0) return st;
+    SG_HIP(use(s->dev), "hipSetDevice");
+    SG_HIP(hipMemcpyAsync(data, b->ptr + off, size, hipMemcpyDeviceToHost, s->s), "hipMemcpyAsync");
+    return finish(s, 1, "buffer_read");
+    (void) blocking;
+}
+
+scrapgpu_status api_buffer_copy(scrapgpu_stream_t * stream, scrapgpu_buffer_t * dst, uint64_t doff, scrapgpu_buffer_t * src, uint64_t soff, size_t size, int blocking) {
+    Stream * s = stream_of(stream);
+    Buffer * bd = buf_of(dst);
+    Buffer * bs = buf_of(src);
+    scrapgpu_status st = check_range(s, bd, doff, size);
+    if (st == SCRAPGPU_STATUS_OK) st = check_range(s, bs, soff, size);
+    if (st != SCRAPGPU_STATUS_OK || size == 0) return st;
+    SG_HIP(use(s->dev), "hipSetDevice");
+    SG_HIP(hipMemcpyAsync(bd->ptr + doff, bs->ptr + soff, size, hipMemcpyDeviceToDevice, s->s), "hipMemcpyAsync");
+    return finish(s, blocking, "buffer_copy");
+}
+
+scrapgpu_status api_buffer_fill(scrapgpu_stream_t * stream, scrapgpu_buffer_t * buffer, uint64_t off, size_t size, uint8_t byte, int blocking) {
+    Stream * s = stream_of(stream);
+    Buffer * b = buf_of(buffer);
+    scrapgpu_status st = check_range(s, b, off, size);
+    if (st != SCRAPGPU_STATUS_OK || size == 0) return st;
+    SG_HIP(use(s->dev), "hipSetDevice");
+    SG_HIP(hipMemsetD8Async(reinterpret_cast<hipDeviceptr_t>(b->ptr + off), byte, size, s->s), "hipMemsetD8Async");
+    return finish(s, blocking, "buffer_fill");
+}
+
+// ---- streams ----------------------------------------------------------------------------------------
+
+scrapgpu_status api_stream_create(scrapgpu_device_t * device, scrapgpu_stream_t ** out) {
+    Device * d = dev_of(device);
+    if (d == nullptr) return invalid("not a hip device");
+    SG_HIP(use(d), "hipSetDevice");
+    hipStream_t hs;
+    SG_HIP(hipStreamCreateWithFlags(&hs, hipStreamNonBlocking), "hipStreamCreate");
+    Stream * s = new Stream;
+    s->hdr.backend = &kVtable;
+    s->dev = d;
+    s->s = hs;
+    *out = reinterpret_cast<scrapgpu_stream_t *>(s);
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status api_stream_free(scrapgpu_stream_t * stream) {
+    Stream * s = stream_of(stream);
+    if (s == nullptr) return invalid("not a hip stream");
+    use(s->dev);
+    hipStreamSynchronize(s->s);
+    if (s->scratch.partials) hipFree(s->scratch.partials);
+    if (s->scratch.counters) hipFree(s->scratch.counters);
+    hipStreamDestroy(s->s);
+    delete s;
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status api_stream_sync(scrapgpu_stream_t * stream) {
+    Stream * s = stream_of(stream);
+    if (s == nullptr) return invalid("not a hip stream");
+    SG_HIP(use(s->dev), "hipSetDevice");
+    SG_HIP(hipStreamSynchronize(s->s), "kernel execution failed (reported at stream_sync)");
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_device_t * api_stream_device(scrapgpu_stream_t * stream) {
+    Stream * s = stream_of(stream);
+    return s ? reinterpret_cast<scrapgpu_device_t *>(s->dev) : nullptr;
+}
+
+// scratch of the split-K matvec: grown on demand (the stream is drained before a re-allocation)
+scrapgpu_status ensure_scratch(Stream * s, size_t partial_floats, size_t counters) {
+    sgk::Scratch & sc = s->scratch;
+    if (partial_floats > sc.partial_floats) {
+        SG_HIP(hipStreamSynchronize(s->s), "hipStreamSynchronize");
+        if (sc.partials) hipFree(sc.partials);
+        sc.partials = nullptr;
+        sc.partial_floats = 0;
+        const size_t n = std::max<size_t>(partial_floats, (size_t) 1 << 20);
+        SG_HIP(hipMalloc(reinterpret_cast<void **>(&sc.partials), n * sizeof(float)), "hipMalloc (scratch)");
+        sc.partial_floats = n;
+    }
+    if (counters > sc.counter_count) {
+        SG_HIP(hipStreamSynchronize(s->s), "hipStreamSynchronize");
+        if (sc.counters) hipFree(sc.counters);
+        sc.counters = nullptr;
+        sc.counter_count = 0;
+        const size_t n = std::max<size_t>(counters, (size_t) 1 << 16);
+        SG_HIP(hipMalloc(reinterpret_cast<void **>(&sc.counters), n * sizeof(uint32_t)), "hipMalloc (counters)");
+        SG_HIP(hipMemsetAsync(sc.counters, 0, n * sizeof(uint32_t), s->s), "hipMemsetAsync");
+        SG_HIP(hipStreamSynchronize(s->s), "hipStreamSynchronize");
+        sc.counter_count = n;
+    }
+    return SCRAPGPU_STATUS_OK;
+}
+
+// ---- tensor transfers with R32 packing in HBM ------------------------------------------------------
+
+constexpr size_t kStagingBytes = (size_t) 64 << 20;
+
+scrapgpu_status ensure_staging(Device * d) {
+    if (d->staging) return SCRAPGPU_STATUS_OK;
+    SG_HIP(hipMalloc(reinterpret_cast<void **>(&d->staging), kStagingBytes), "hipMalloc (staging)");
+    d->staging_size = kStagingBytes;
+    return SCRAPGPU_STATUS_OK;
+}
+
+// Copies the first `size` natural bytes of an R32 tensor between the host and the device, one chunk
+// of whole 32-row groups of a slice at a time through the device staging buffer. A chunk that the
+// host range only partly covers is unpacked first so the bytes beyond `size` are preserved.
+scrapgpu_status r32_transfer(Stream * s, const scrapgpu_tensor_desc & t, uint8_t * dev_base, uint8_t * host, size_t size, bool up) {
+    Device * d = s->dev;
+    const int64_t K = t.ne[0], M = sg::dim1(t.ne[1]);
+    const int64_t slices = sg::dim1(t.ne[2]) * sg::dim1(t.ne[3]);
+    const sg::R32Geom g = sg::r32_geometry(t.dtype, K, M);
+    if (g.rowb == 0) return invalid("R32 tensor has no whole block per row");
+    const size_t slice_bytes = (size_t) M * g.rowb;
+    std::lock_guard<std::mutex> lock(d->mu);
+    scrapgpu_status st = ensure_staging(d);
+    if (st != SCRAPGPU_STATUS_OK) return st;
+    const int64_t chunk_rows = std::max<int64_t>(32, (int64_t) (d->staging_size / g.rowb) / 32 * 32);
+    for (int64_t sl = 0; sl < slices; ++sl) {
+        const size_t slice_lo = (size_t) sl * slice_bytes;
+        if (slice_lo >= size) break;
+        uint8_t * rep = dev_base + slice_lo; // slices are stored back to back, like the natural layout
+        for (int64_t rA = 0; rA < M; rA += std::min<int64_t>(chunk_rows, 32 * 65535)) {
+            const int64_t rB = std::min<int64_t>(M, rA + std::min<int64_t>(chunk_rows, 32 * 65535));
+            const size_t nat_lo = slice_lo + (size_t) rA * g.rowb;
+            if (nat_lo >= size) break;
+            const size_t nat_len = (size_t) (rB - rA) * g.rowb;
+            const size_t have = std::min(nat_len, size - nat_lo);
+            if (up) {
+                if (have < nat_len) {
+                    SG_HIP(sgk::launch_r32_move(t.dtype, K, M, rA, rB - rA, d->staging, rep, false, s->s), "R32 unpack");
+                }
+                SG_HIP(hipMemcpyAsync(d->staging, host + nat_lo, have, hipMemcpyHostToDevice, s->s), "hipMemcpyAsync");
+                SG_HIP(sgk::launch_r32_move(t.dtype, K, M, rA, rB - rA, d->staging, rep, true, s->s), "R32 pack");
+            } else {
+                SG_HIP(sgk::launch_r32_move(t.dtype, K, M, rA, rB - rA, d->staging, rep, false, s->s), "R32 unpack");
+                SG_HIP(hipMemcpyAsync(host + nat_lo, d->staging, have, hipMemcpyDeviceToHost, s->s), "hipMemcpyAsync");
+            }
+            // the staging buffer is reused by the next chunk (same stream: ordered)
+        }
+    }
+    SG_HIP(hipStreamSynchronize(s->s), "R32 transfer");
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status tensor_transfer(scrapgpu_stream_t * stream, const scrapgpu_tensor_desc * raw, uint8_t * host, size_t size, bool up) {
+    Stream * s = stream_of(stream);
+    if (s == nullptr) return invalid("not a hip stream");
+    if (raw->struct_size < offsetof(scrapgpu_tensor_desc, offset) + sizeof(raw->offset)) return invalid("tensor desc is too small");
+    const scrapgpu_tensor_desc t = load_desc(*raw);
+    Buffer * b = buf_of(t.buffer);
+    if (b == nullptr) return invalid("tensor desc has no hip buffer");
+    if (b->dev != s->dev) return invalid("tensor buffer and stream belong to different devices");
+    if (t.offset > b->size || size > b->size - t.offset) return invalid("transfer exceeds the buffer");
+    if (size > sg::nbytes(t)) return invalid("transfer size exceeds the tensor");
+    if (size == 0) return SCRAPGPU_STATUS_OK;
+    SG_HIP(use(s->dev), "hipSetDevice");
+    if (t.layout == SCRAPGPU_LAYOUT_R32) {
+        if (!sg::r32_eligible(t)) return unsupported("the R32 layout needs a repackable dtype and contiguous slices with 16-byte strides");
+        return r32_transfer(s, t, b->ptr + t.offset, host, size, up);
+    }
+    if (!sg::contiguous_ggml(t)) return unsupported("tensor is not contiguous; use buffer_read / buffer_write for raw strided transfers");
+    if (up) {
+        SG_HIP(hipMemcpyAsync(b->ptr + t.offset, host, size, hipMemcpyHostToDevice, s->s), "hipMemcpyAsync");
+    } else {
+        SG_HIP(hipMemcpyAsync(host, b->ptr + t.offset, size, hipMemcpyDeviceToHost, s->s), "hipMemcpyAsync");
+    }
+    SG_HIP(hipStreamSynchronize(s->s), "tensor transfer");
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status api_tensor_upload(scrapgpu_stream_t * stream, const scrapgpu_tensor_desc * desc, const void * host, size_t size) {
+    return tensor_transfer(stream, desc, static_cast<uint8_t *>(const_cast<void *>(host)), size, true);
+}
+
+scrapgpu_status api_tensor_download(scrapgpu_stream_t * stream, const scrapgpu_tensor_desc * desc, void * host, size_t size) {
+    return tensor_transfer(stream, desc, static_cast<uint8_t *>(host), size, false);
+}
+
+// ---- MUL_MAT ------------------------------------------------------------------------------------------
+
+// the support rule of one product W x -> y; fills `a` (pointers left null) when supported
+scrapgpu_status mul_mat_rule(const scrapgpu_tensor_desc & w, const scrapgpu_tensor_desc & x, const scrapgpu_tensor_desc & y, int allow_broadcast,
+                             sgk::MatArgs * a, const char ** reason) {
+    if (!sg::is_quant(w.dtype)) {
+        return unsupported("the hip backend implements MUL_MAT for Q4_0 / Q8_0 / Q4_K / Q6_K weights only", reason);
+    }
+    if (w.layout != SCRAPGPU_LAYOUT_R32) {
+        return unsupported("a quantized src0 must use the R32 layout (scrapgpu_tensor_upload packs it on the way)", reason);
+    }
+    if (!sg::r32_eligible(w)) return unsupported("src0 is not R32-eligible (contiguous, whole blocks per row, 16-byte slice strides)", reason);
+    if (x.dtype != SCRAPGPU_DTYPE_F32 || y.dtype != SCRAPGPU_DTYPE_F32 || x.layout != SCRAPGPU_LAYOUT_NATURAL || y.layout != SCRAPGPU_LAYOUT_NATURAL) {
+        return unsupported("MUL_MAT expects an F32 natural-layout src1 and destination", reason);
+    }
+    if (x.nb[0] != 4 || y.nb[0] != 4) return unsupported("MUL_MAT needs contiguous rows of src1 and dst (nb0 == element size)", reason);
+    for (int i = 1; i < 4; ++i) {
+        if (x.nb[i] % 4 != 0 || y.nb[i] % 4 != 0) return unsupported("src1 / dst strides must be multiples of 4 bytes", reason);
+    }
+    if ((x.offset % 4) != 0 || (y.offset % 4) != 0) return unsupported("src1 / dst offsets must be multiples of 4 bytes", reason);
+    const int64_t K = sg::dim1(w.ne[0]), M = sg::dim1(w.ne[1]);
+    if (sg::dim1(x.ne[0]) != K) {
+        if (reason) *reason = "MUL_MAT: the inner dimensions of src0 and src1 differ";
+        return invalid("MUL_MAT: the inner dimensions of src0 and src1 differ");
+    }
+    const int64_t w2 = sg::dim1(w.ne[2]), w3 = sg::dim1(w.ne[3]);
+    const int64_t x2 = sg::dim1(x.ne[2]), x3 = sg::dim1(x.ne[3]);
+    if (x2 % w2 != 0 || x3 % w3 != 0) {
+        if (reason) *reason = "MUL_MAT: src1 dims 2 and 3 must be multiples of the src0 dims";
+        return invalid("MUL_MAT: src1 dims 2 and 3 must be multiples of the src0 dims");
+    }
+    if (!allow_broadcast && (x2 != w2 || x3 != w3)) return unsupported("MUL_MAT: broadcasting over dims 2/3 is not allowed", reason);
+    if (sg::dim1(y.ne[0]) != M || sg::dim1(y.ne[1]) != sg::dim1(x.ne[1]) || sg::dim1(y.ne[2]) != x2 || sg::dim1(y.ne[3]) != x3) {
+        if (reason) *reason = "MUL_MAT: dst must be [ne01, ne11, ne12, ne13]";
+        return invalid("MUL_MAT: dst must be [ne01, ne11, ne12, ne13]");
+    }
+    if (x2 * x3 > 65535) return unsupported("MUL_MAT: more than 65535 slices", reason);
+    if (a) {
+        a->dtype = w.dtype;
+        a->M = M;
+        a->K = K;
+        a->nb = K / (int64_t) sg::block_size(w.dtype);
+        a->w_s2 = w.nb[2];
+        a->w_s3 = w.nb[3];
+        a->x_s1 = (int64_t) (x.nb[1] / 4);
+        a->x_s2 = (int64_t) (x.nb[2] / 4);
+        a->x_s3 = (int64_t) (x.nb[3] / 4);
+        a->y_s1 = (int64_t) (y.nb[1] / 4);
+        a->y_s2 = (int64_t) (y.nb[2] / 4);
+        a->y_s3 = (int64_t) (y.nb[3] / 4);
+        a->N = sg::dim1(x.ne[1]);
+        a->ne12 = x2;
+        a->ne13 = x3;
+        a->r2 = x2 / w2;
+        a->r3 = x3 / w3;
+    }
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status api_supports(Device * d, const scrapgpu_op_desc * desc, const char ** reason) {
+    (void) d;
+    const scrapgpu_status v = scrapgpu_op_desc_validate(desc);
+    if (v != SCRAPGPU_STATUS_OK) {
+        if (reason) *reason = scrapgpu_last_error();
+        return v;
+    }
+    switch (desc->op) {
+        case SCRAPGPU_OP_MUL_MAT: {
+            const auto * p = static_cast<const scrapgpu_mul_mat_params *>(desc->params);
+            const int bc = p->struct_size >= offsetof(scrapgpu_mul_mat_params, allow_broadcast) + sizeof(int) ? p->allow_broadcast : 0;
+            return mul_mat_rule(desc->inputs[0], desc->inputs[1], desc->outputs[0], bc, nullptr, reason);
+        }
+        case SCRAPGPU_OP_MUL_MAT_MULTI: {
+            const size_t n = desc->output_count;
+            for (size_t i = 0; i < n; ++i) {
+                const scrapgpu_status st = mul_mat_rule(desc->inputs[i], desc->inputs[n], desc->outputs[i], 0, nullptr, reason);
+                if (st != SCRAPGPU_STATUS_OK) return st;
+            }
+            return SCRAPGPU_STATUS_OK;
+        }
+        default:
+            return unsupported("the hip backend implements the quantized MUL_MAT family only", reason);
+    }
+}
+
+scrapgpu_status api_op_supported(scrapgpu_device_t * device, const scrapgpu_op_desc * desc, const char ** reason) {
+    Device * d = dev_of(device);
+    if (d == nullptr) {
+        if (reason) *reason = "not a hip device";
+        return invalid("not a hip device");
+    }
+    return api_supports(d, desc, reason);
+}
+
+double weight_bytes(const sgk::MatArgs & a) {
+    const int64_t bs = a.dtype == sgk::Q4_K || a.dtype == sgk::Q6_K ? 256 : 32;
+    const double ts = a.dtype == sgk::Q4_0 ? 18 : a.dtype == sgk::Q8_0 ? 34 : a.dtype == sgk::Q4_K ? 144 : 210;
+    return (double) a.M * (double) (a.K / bs) * ts * (double) ((a.ne12 / a.r2) * (a.ne13 / a.r3));
+}
+
+// enqueues one product on the stream; pointers in `a` resolved
+scrapgpu_status run_product(Stream * s, sgk::MatArgs a) {
+    const int cus = (int) s->dev->cus;
+    if (a.N <= 8) {
+        // scratch for a possible K split (sized generously: groups * slices * 64 parts * 8 columns * 32)
+        const size_t groups = (size_t) ((a.M + 31) / 32) * (size_t) (a.ne12 * a.ne13);
+        scrapgpu_status st = ensure_scratch(s, groups * 64 * 8 * 32 > ((size_t) 1 << 26) ? ((size_t) 1 << 26) : groups * 64 * 8 * 32, groups);
+        if (st != SCRAPGPU_STATUS_OK) return st;
+        ProfScope prof(s->s);
+        const char * name = nullptr;
+        uint64_t grid = 0;
+        SG_HIP(sgk::launch_matvec(a, s->scratch, cus, s->s, &name, &grid), "matvec launch");
+        prof.done(name, weight_bytes(a), 2.0 * (double) a.M * (double) a.K * (double) a.N * (double) (a.ne12 * a.ne13));
+        return SCRAPGPU_STATUS_OK;
+    }
+    ProfScope prof(s->s);
+    const char * name = nullptr;
+    SG_HIP(sgk::launch_matmul_mfma(a, cus, s->s, &name), "matmul launch");
+    prof.done(name, weight_bytes(a), 2.0 * (double) a.M * (double) a.K * (double) a.N * (double) (a.ne12 * a.ne13));
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status product(Stream * s, const scrapgpu_tensor_desc & w, const scrapgpu_tensor_desc & x, const scrapgpu_tensor_desc & y, int bc) {
+    sgk::MatArgs a;
+    std::memset(&a, 0, sizeof(a));
+    scrapgpu_status st = mul_mat_rule(w, x, y, bc, &a, nullptr);
+    if (st != SCRAPGPU_STATUS_OK) return st;
+    uint8_t *pw, *px, *py;
+    if ((st = resolve(s->dev, w, &pw, "src0")) != SCRAPGPU_STATUS_OK) return st;
+    if ((st = resolve(s->dev, x, &px, "src1")) != SCRAPGPU_STATUS_OK) return st;
+    if ((st = resolve(s->dev, y, &py, "dst")) != SCRAPGPU_STATUS_OK) return st;
+    a.w = pw;
+    a.x = reinterpret_cast<const float *>(px);
+    a.y = reinterpret_cast<float *>(py);
+    return run_product(s, a);
+}
+
+scrapgpu_status exec_desc(Stream * s, const scrapgpu_op_desc * desc) {
+    const char * reason = nullptr;
+    scrapgpu_status st = api_supports(s->dev, desc, &reason);
+    if (st != SCRAPGPU_STATUS_OK) return st;
+    SG_HIP(use(s->dev), "hipSetDevice");
+    if (desc->op == SCRAPGPU_OP_MUL_MAT) {
+        const auto * p = static_cast<const scrapgpu_mul_mat_params *>(desc->params);
+        const int bc = p->struct_size >= offsetof(scrapgpu_mul_mat_params, allow_broadcast) + sizeof(int) ? p->allow_broadcast : 0;
+        return product(s, desc->inputs[0], desc->inputs[1], desc->outputs[0], bc);
+    }
+    const size_t n = desc->output_count; // MUL_MAT_MULTI
+    for (size_t i = 0; i < n; ++i) {
+        st = product(s, desc->inputs[i], desc->inputs[n], desc->outputs[i], 0);
+        if (st != SCRAPGPU_STATUS_OK) return st;
+    }
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status api_op_execute(scrapgpu_stream_t * stream, const scrapgpu_op_desc * desc) {
+    Stream * s = stream_of(stream);
+    if (s == nullptr) return invalid("not a hip stream");
+    if (desc == nullptr) return invalid("op desc is null");
+    return exec_desc(s, desc);
+}
+
+// ---- plans ------------------------------------------------------------------------------------------------
+
+void plan_release(Plan * p) {
+    for (Buffer * b : p->buffers) b->plan_refs.fetch_sub(1);
+    p->buffers.clear();
+}
+
+scrapgpu_status api_plan_build(scrapgpu_device_t * device, const scrapgpu_plan_desc * desc, scrapgpu_plan_t ** out) {
+    Device * d = dev_of(device);
+    if (d == nullptr) return invalid("not a hip device");
+    if (desc->struct_size < offsetof(scrapgpu_plan_desc, node_count) + sizeof(desc->node_count)) return invalid("plan desc is too small");
+    if (desc->node_count > 0 && desc->nodes == nullptr) return invalid("plan desc has no nodes");
+    std::unique_ptr<Plan> p(new Plan);
+    p->hdr.backend = &kVtable;
+    p->dev = d;
+    for (size_t i = 0; i < desc->node_count; ++i) {
+        const scrapgpu_op_desc & op = desc->nodes[i].op;
+        const char * reason = nullptr;
+        const scrapgpu_status st = api_supports(d, &op, &reason);
+        if (st != SCRAPGPU_STATUS_OK) {
+            plan_release(p.get());
+            return st;
+        }
+        PlanNode node;
+        node.op = op;
+        node.in.assign(op.inputs, op.inputs + op.input_count);
+        node.out.assign(op.outputs, op.outputs + op.output_count);
+        if (op.params && op.params_size) {
+            const uint8_t * pp = static_cast<const uint8_t *>(op.params);
+            node.params.assign(pp, pp + op.params_size);
+        }
+        for (const auto * list : {&node.in, &node.out}) {
+            for (const scrapgpu_tensor_desc & t : *list) {
+                Buffer * b = buf_of(t.buffer);
+                if (b == nullptr || b->dev != d) {
+                    plan_release(p.get());
+                    return invalid("a plan tensor is not in a buffer of the plan's device");
+                }
+                b->plan_refs.fetch_add(1);
+                p->buffers.push_back(b);
+            }
+        }
+        p->nodes.push_back(std::move(node));
+    }
+    for (PlanNode & n : p->nodes) {
+        n.op.inputs = n.in.data();
+        n.op.outputs = n.out.data();
+        n.op.params = n.params.empty() ? nullptr : n.params.data();
+    }
+    *out = reinterpret_cast<scrapgpu_plan_t *>(p.release());
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status api_plan_execute(scrapgpu_stream_t * stream, scrapgpu_plan_t * plan) {
+    Stream * s = stream_of(stream);
+    Plan * p = as<Plan>(plan);
+    if (s == nullptr || p == nullptr) return invalid("not a hip stream or plan");
+    if (p->dev != s->dev) return invalid("plan and stream belong to different devices");
+    for (PlanNode & n : p->nodes) {
+        const scrapgpu_status st = exec_desc(s, &n.op);
+        if (st != SCRAPGPU_STATUS_OK) return st;
+    }
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status api_plan_free(scrapgpu_plan_t * plan) {
+    Plan * p = as<Plan>(plan);
+    if (p == nullptr) return invalid("not a hip plan");
+    plan_release(p);
+    delete p;
+    return SCRAPGPU_STATUS_OK;
+}
+
+const scrapgpu_backend_vtable kVtable = {
+    sizeof(scrapgpu_backend_vtable),
+    "hip",
+    nullptr,
+    api_device_count,
+    api_get_device,
+    api_device_info,
+    api_buffer_alloc,
+    api_buffer_free,
+    api_buffer_write,
+    api_buffer_read,
+    api_buffer_copy,
+    api_buffer_fill,
+    api_stream_sync,
+    api_op_supported,
+    api_plan_build,
+    api_plan_execute,
+    api_plan_free,
+    api_stream_create,
+    api_stream_free,
+    api_tensor_upload,
+    api_tensor_download,
+    api_op_execute,
+    api_stream_device,
+};
+
+// ---- device-side weight conversion (extensions) ----------------------------------------------------
+
+scrapgpu_status convert_check(Stream * s, const scrapgpu_tensor_desc & q, const scrapgpu_tensor_desc & f) {
+    if (s == nullptr) return invalid("not a hip stream");
+    if (!sg::is_quant(q.dtype)) return unsupported("the quantized tensor must be Q4_0 / Q8_0 / Q4_K / Q6_K");
+    if (f.dtype != SCRAPGPU_DTYPE_F32 || f.layout != SCRAPGPU_LAYOUT_NATURAL) return unsupported("the float tensor must be F32 in the natural layout");
+    for (int i = 0; i < 4; ++i)
+        if (sg::dim1(q.ne[i]) != sg::dim1(f.ne[i])) return invalid("the two tensors must have the same shape");
+    if (sg::dim1(q.ne[0]) % (int64_t) sg::block_size(q.dtype) != 0) return invalid("rows must hold whole blocks");
+    if (q.layout == SCRAPGPU_LAYOUT_R32 ? !sg::r32_eligible(q) : !sg::contiguous_ggml(q)) return unsupported("the quantized tensor must be contiguous");
+    if (!sg::contiguous_ggml(f)) return unsupported("the float tensor must be contiguous");
+    return SCRAPGPU_STATUS_OK;
+}
+
+// runs `body(nat_chunk_ptr, rows)` over chunks of whole row groups of every slice, packing or
+// unpacking R32 around it
+template <typename F>
+scrapgpu_status over_chunks(Stream * s, const scrapgpu_tensor_desc & q, uint8_t * qdev, bool pack_after, F body) {
+    const int64_t K = sg::dim1(q.ne[0]), M = sg::dim1(q.ne[1]);
+    const int64_t slices = sg::dim1(q.ne[2]) * sg::dim1(q.ne[3]);
+    const sg::R32Geom g = sg::r32_geometry(q.dtype, K, M);
+    const bool r32 = q.layout == SCRAPGPU_LAYOUT_R32;
+    std::lock_guard<std::mutex> lock(s->dev->mu);
+    if (r32) {
+        const scrapgpu_status st = ensure_staging(s->dev);
+        if (st != SCRAPGPU_STATUS_OK) return st;
+    }
+    const int64_t chunk = r32 ? std::max<int64_t>(32, std::min<int64_t>((int64_t) (s->dev->staging_size / g.rowb) / 32 * 32, 32 * 65535)) : M;
+    for (int64_t sl = 0; sl < slices; ++sl) {
+        uint8_t * slice = qdev + (uint64_t) sl * M * g.rowb;
+        for (int64_t rA = 0; rA < M; rA += chunk) {
+            const int64_t rows = std::min(chunk, M - rA);
+            uint8_t * nat = r32 ? s->dev->staging : slice + (uint64_t) rA * g.rowb;
+            if (r32 && !pack_after) SG_HIP(sgk::launch_r32_move(q.dtype, K, M, rA, rows, nat, slice, false, s->s), "R32 unpack");
+            const scrapgpu_status st = body(nat, sl * M + rA, rows);
+            if (st != SCRAPGPU_STATUS_OK) return st;
+            if (r32 && pack_after) SG_HIP(sgk::launch_r32_move(q.dtype, K, M, rA, rows, nat, slice, true, s->s), "R32 pack");
+        }
+    }
+    // the staging buffer is free for the next caller once the stream has drained
+    SG_HIP(hipStreamSynchronize(s->s), "conversion");
+    return SCRAPGPU_STATUS_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+scrapgpu_status scrapgpu_hip_register(void) {
+    Registry & r = registry();
+    std::lock_guard<std::mutex> lock(r.mu);
+    if (r.registered) return SCRAPGPU_STATUS_OK;
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess && e != hipErrorNoDevice) return hip_fail(e, "hipGetDeviceCount");
+    if (e == hipErrorNoDevice) n = 0;
+    std::vector<int> allow;
+    if (const char * env = std::getenv("SCRAPGPU_HIP_DEVICES")) {
+        for (const char * p = env; *p;) {
+            char * end = nullptr;
+            const long v = std::strtol(p, &end, 10);
+            if (end == p) break;
+            allow.push_back((int) v);
+            p = *end == ',' ? end + 1 : end;
+        }
+    }
+    int rt = 0;
+    hipRuntimeGetVersion(&rt);
+    for (int i = 0; i < n; ++i) {
+        if (!allow.empty() && std::find(allow.begin(), allow.end(), i) == allow.end()) continue;
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, i) != hipSuccess) continue;
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) continue; // kernels are built for gfx950 only
+        std::unique_ptr<Device> d(new Device);
+        d->hdr.backend = &kVtable;
+        d->ordinal = i;
+        d->name = prop.name;
+        d->arch = std::string("gcnArchName ") + prop.gcnArchName;
+        d->driver = "HIP runtime " + std::to_string(rt);
+        d->tuning = "gfx950";
+        d->total_mem = prop.totalGlobalMem;
+        d->lds = prop.sharedMemPerBlock;
+        d->cus = (uint32_t) prop.multiProcessorCount;
+        r.devices.push_back(std::move(d));
+    }
+    if (const char * env = std::getenv("SCRAPGPU_HIP_PROFILE")) g_prof.store(env[0] == '1');
+    r.registered = true;
+    const scrapgpu_status st = scrapgpu_register_backend(&kVtable);
+    if (st != SCRAPGPU_STATUS_OK) r.registered = false;
+    return st;
+}
+
+scrapgpu_status scrapgpu_hip_quantize(scrapgpu_stream_t * stream, const scrapgpu_tensor_desc * src, const scrapgpu_tensor_desc * dst) {
+    Stream * s = stream_of(stream);
+    if (s == nullptr || src == nullptr || dst == nullptr) return invalid("stream, src or dst is null");
+    const scrapgpu_tensor_desc f = load_desc(*src), q = load_desc(*dst);
+    scrapgpu_status st = convert_check(s, q, f);
+    if (st != SCRAPGPU_STATUS_OK) return st;
+    uint8_t *pf, *pq;
+    if ((st = resolve(s->dev, f, &pf, "src")) != SCRAPGPU_STATUS_OK) return st;
+    if ((st = resolve(s->dev, q, &pq, "dst")) != SCRAPGPU_STATUS_OK) return st;
+    SG_HIP(use(s->dev), "hipSetDevice");
+    const int64_t K = sg::dim1(q.ne[0]);
+    const int64_t bpr = K / (int64_t) sg::block_size(q.dtype);
+    const float * fp = reinterpret_cast<const float *>(pf);
+    return over_chunks(s, q, pq, true, [&](uint8_t * nat, int64_t row, int64_t rows) -> scrapgpu_status {
+        SG_HIP(sgk::launch_quantize(q.dtype, fp + row * K, nat, rows * bpr, s->s), "quantize");
+        return SCRAPGPU_STATUS_OK;
+    });
+}
+
+scrapgpu_status scrapgpu_hip_dequantize(scrapgpu_stream_t * stream, const scrapgpu_tensor_desc * src, const scrapgpu_tensor_desc * dst) {
+    Stream * s = stream_of(stream);
+    if (s == nullptr || src == nullptr || dst == nullptr) return invalid("stream, src or dst is null");
+    const scrapgpu_tensor_desc q = load_desc(*src), f = load_desc(*dst);
+    scrapgpu_status st = convert_check(s, q, f);
+    if (st != SCRAPGPU_STATUS_OK) return st;
+    uint8_t *pf, *pq;
+    if ((st = resolve(s->dev, f, &pf, "dst")) != SCRAPGPU_STATUS_OK) return st;
+    if ((st = resolve(s->dev, q, &pq, "src")) != SCRAPGPU_STATUS_OK) return st;
+    SG_HIP(use(s->dev), "hipSetDevice");
+    const int64_t K = sg::dim1(q.ne[0]);
+    const int64_t bpr = K / (int64_t) sg::block_size(q.dtype);
+    float * fp = reinterpret_cast<float *>(pf);
+    return over_chunks(s, q, pq, false, [&](uint8_t * nat, int64_t row, int64_t rows) -> scrapgpu_status {
+        SG_HIP(sgk::launch_dequantize(q.dtype, nat, fp + row * K, rows * bpr, s->s), "dequantize");
+        return SCRAPGPU_STATUS_OK;
+    });
+}
+
+scrapgpu_status scrapgpu_hip_fill_normal(scrapgpu_stream_t * stream, const scrapgpu_tensor_desc * desc, uint64_t seed, float mean, float stddev) {
+    Stream * s = stream_of(stream);
+    if (s == nullptr || desc == nullptr) return invalid("stream or desc is null");
+    const scrapgpu_tensor_desc t = load_desc(*desc);
+    if (t.dtype != SCRAPGPU_DTYPE_F32 || !sg::contiguous_ggml(t)) return unsupported("fill_normal needs a contiguous F32 tensor");
+    uint8_t * p;
+    scrapgpu_status st = resolve(s->dev, t, &p, "tensor");
+    if (st != SCRAPGPU_STATUS_OK) return st;
+    SG_HIP(use(s->dev), "hipSetDevice");
+    const int64_t n = (int64_t) (sg::nbytes(t) / 4);
+    SG_HIP(sgk::launch_fill_normal(reinterpret_cast<float *>(p), n, seed, mean, stddev, s->s), "fill_normal");
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status scrapgpu_hip_profile_enable(int enable) {
+    g_prof.store(enable != 0);
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status scrapgpu_hip_profile_reset(void) {
+    prof_collect();
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    g_prof_table.clear();
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status scrapgpu_hip_profile_read(size_t index, const char ** name, uint64_t * launches, double * total_ms, double * bytes, double * flops) {
+    prof_collect();
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    if (index >= g_prof_table.size()) return invalid("no profile entry at this index");
+    const ProfEntry & e = g_prof_table[index];
+    if (name) *name = e.name.c_str();
+    if (launches) *launches = e.launches;
+    if (total_ms) *total_ms = e.ms;
+    if (bytes) *bytes = e.bytes;
+    if (flops) *flops = e.flops;
+    return SCRAPGPU_STATUS_OK;
+}
+
+void * scrapgpu_hip_stream_native(scrapgpu_stream_t * stream) {
+    Stream * s = stream_of(stream);
+    return s ? static_cast<void *>(s->s) : nullptr;
+}
+
+}

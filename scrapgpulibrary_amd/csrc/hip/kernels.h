@@ -1,0 +1,70 @@
+// Launch interface between the hip backend's host code and its gfx950 kernels. Plain pointers,
+// sizes and strides only; every function enqueues on `stream` and returns the launch error.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace sgk {
+
+enum : int { F32 = 0, Q4_0 = 16, Q8_0 = 17, Q4_K = 32, Q6_K = 33 };
+
+// R32 area table of one dtype (the same numbers as sg::r32_geometry)
+struct Areas {
+    int na;
+    int src[3];
+    int len[3];
+    uint8_t xr[3];
+};
+Areas areas_of(int dtype);
+
+// Quantized matrix product y[n, m] = sum_k W[m, k] x[n, k] over R32 weights.
+// W: slices of M rows, nb blocks each; slice (i2/r2, i3/r3) starts at w + i2w * w_s2 + i3w * w_s3
+// (bytes). x / y: float element strides (s1 between columns, s2 / s3 between slices).
+struct MatArgs {
+    int dtype;
+    const uint8_t * w;
+    uint64_t w_s2, w_s3;
+    int64_t M, K, nb;
+    const float * x;
+    int64_t x_s1, x_s2, x_s3;
+    float * y;
+    int64_t y_s1, y_s2, y_s3;
+    int64_t N;          // columns of x / y
+    int64_t ne12, ne13; // dst slices
+    int64_t r2, r3;     // broadcast factors
+};
+
+// Scratch a stream lends to kernels that split K over work-groups: per-part partial sums and
+// one arrival counter per row group (counters are zero between launches: the last work-group
+// of a group resets its counter).
+struct Scratch {
+    float * partials;
+    size_t partial_floats;
+    uint32_t * counters;
+    size_t counter_count;
+};
+
+// decode matvec for 1 <= N <= 8 (weights streamed once, every column reused in registers)
+hipError_t launch_matvec(const MatArgs & a, const Scratch & s, int cu_count, hipStream_t stream, const char ** kernel_name,
+                         uint64_t * grid_size);
+
+// prefill: bf16 MFMA with fp32 accumulate, weights dequantized into LDS (any N >= 1)
+hipError_t launch_matmul_mfma(const MatArgs & a, int cu_count, hipStream_t stream, const char ** kernel_name);
+
+// R32 pack (natural -> R32) or unpack of rows [row0, row0 + nrows) of one slice of M rows; row0 is
+// a multiple of 32. `nat` holds the natural bytes of those rows, `rep` is the slice's R32 base.
+hipError_t launch_r32_move(int dtype, int64_t K, int64_t M, int64_t row0, int64_t nrows, uint8_t * nat, uint8_t * rep, bool pack,
+                           hipStream_t stream);
+
+// bit-exact dequantization of n_blocks contiguous natural blocks into floats
+hipError_t launch_dequantize(int dtype, const uint8_t * src, float * dst, int64_t n_blocks, hipStream_t stream);
+
+// bit-exact (reference-identical) quantization of n_blocks blocks of floats into natural blocks
+hipError_t launch_quantize(int dtype, const float * src, uint8_t * dst, int64_t n_blocks, hipStream_t stream);
+
+// mean + stddev * N(0,1) with a counter-based generator (element i of stream seed uses counter i)
+hipError_t launch_fill_normal(float * dst, int64_t n, uint64_t seed, float mean, float stddev, hipStream_t stream);
+
+} // namespace sgk

@@ -1,0 +1,512 @@
+// Weight-format kernels of the upload path: R32 pack / unpack in HBM, bit-exact dequantization,
+// reference-identical quantization and the synthetic normal generator.
+//
+// Compiled with -ffp-contract=off (and the pragma below): the quantizer and the dequantizer must
+// perform one IEEE binary32 operation per source operation, in the order of the reference's
+// src/core/ref/quant.cpp, to reproduce its bytes and floats exactly. Division and sqrt are the
+// correctly rounded ones (HIP's default for fp32).
+#pragma clang fp contract(off)
+
+#include "kernels.h"
+
+#include <hip/hip_fp16.h>
+
+#include <cmath>
+
+namespace sgk {
+
+Areas areas_of(int dtype) {
+    switch (dtype) {
+        case Q8_0: return Areas{2, {2, 0, 0}, {32, 2, 0}, {0x80, 0, 0}};
+        case Q4_0: return Areas{2, {2, 0, 0}, {16, 2, 0}, {0, 0, 0}};
+        case Q4_K: return Areas{2, {16, 0, 0}, {128, 16, 0}, {0, 0, 0}};
+        case Q6_K: return Areas{3, {0, 192, 208}, {192, 16, 2}, {0, 0x80, 0}};
+        default: return Areas{0, {0, 0, 0}, {0, 0, 0}, {0, 0, 0}};
+    }
+}
+
+namespace {
+
+int block_elems(int dt) {
+    return dt == Q4_K || dt == Q6_K ? 256 : 32;
+}
+
+int block_bytes(int dt) {
+    switch (dt) {
+        case Q4_0: return 18;
+        case Q8_0: return 34;
+        case Q4_K: return 144;
+        default: return 210;
+    }
+}
+
+// ---- R32 ----------------------------------------------------------------------------------------
+// One thread per 16-byte unit (or 2-byte half) of one area. blockIdx.y is the row group inside the
+// chunk; the index inside a group runs over units u = b * U + j (slow) and lanes (fast), so that
+// consecutive threads write consecutive R32 bytes.
+struct MoveArgs {
+    uint8_t * nat;     // natural bytes of rows [row0, row0 + nrows)
+    uint8_t * area;    // R32 base of this area in the slice
+    int64_t M, nb, row0, nrows;
+    int bs, src, len;
+    uint8_t xr;
+    int pack;
+};
+
+__global__ __launch_bounds__(256) void k_r32_move(MoveArgs a) {
+    const int64_t g0 = a.row0 + 32 * (int64_t) blockIdx.y; // first row of the group (slice row)
+    const int rs = (int) min<int64_t>(32, a.M - g0);
+    const int U = a.len == 2 ? 1 : a.len / 16;
+    const int64_t per_group = 32 * a.nb * U;
+    uint8_t * grp = a.area + (uint64_t) g0 * a.nb * a.len;
+    for (int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; t < per_group; t += (int64_t) gridDim.x * blockDim.x) {
+        const int lane = (int) (t & 31);
+        const int64_t u = t >> 5;
+        if (lane >= rs) continue;
+        const int64_t b = u / U;
+        const int j = (int) (u - b * U);
+        uint8_t * p = a.nat + (uint64_t) (g0 - a.row0 + lane) * a.nb * a.bs + (uint64_t) b * a.bs + a.src;
+        if (a.len == 2) {
+            uint16_t * q = reinterpret_cast<uint16_t *>(grp + ((uint64_t) b * rs + lane) * 2);
+            uint16_t * pn = reinterpret_cast<uint16_t *>(p); // natural blocks are 2-byte aligned
+            if (a.pack) *q = *pn; else *pn = *q;
+            continue;
+        }
+        uint8_t * q = grp + (((uint64_t) u) * rs + lane) * 16;
+        uint16_t * pn = reinterpret_cast<uint16_t *>(p + 16 * j);
+        const uint32_t x2 = (uint32_t) a.xr * 0x0101u;
+        if (a.pack) {
+            uint32_t w[4];
+            for (int i = 0; i < 4; ++i) w[i] = ((uint32_t) pn[2 * i] | ((uint32_t) pn[2 * i + 1] << 16)) ^ (x2 * 0x00010001u);
+            *reinterpret_cast<uint4 *>(q) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+            const uint4 v = *reinterpret_cast<const uint4 *>(q);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t o = w[i] ^ (x2 * 0x00010001u);
+                pn[2 * i] = (uint16_t) (o & 0xFFFFu);
+                pn[2 * i + 1] = (uint16_t) (o >> 16);
+            }
+        }
+    }
+}
+
+// ---- binary16 <-> binary32 (same rules as the reference's src/core/ref/f16.cpp) ----------------
+
+__device__ float h2f(uint16_t h) {
+    return __half2float(__ushort_as_half(h));
+}
+
+__device__ uint16_t f2h(float f) {
+    const uint32_t u = __float_as_uint(f);
+    const uint16_t s = (uint16_t) ((u >> 16) & 0x8000u);
+    const uint32_t a = u & 0x7FFFFFFFu;
+    if (a >= 0x7F800000u) return (uint16_t) (s | 0x7C00u | (a > 0x7F800000u ? 0x200u : 0u));
+    if (a >= 0x477FF000u) return (uint16_t) (s | 0x7C00u);
+    if (a >= 0x38800000u) {
+        const uint32_t base = a - 0x38000000u;
+        const uint32_t keep = base >> 13, rest = base & 0x1FFFu;
+        return (uint16_t) (s | (keep + (rest > 0x1000u || (rest == 0x1000u && (keep & 1u)))));
+    }
+    if (a < 0x33000000u) return s;
+    const uint32_t shift = 126u - (a >> 23);
+    const uint32_t sig = (a & 0x7FFFFFu) | 0x800000u;
+    const uint32_t keep = sig >> shift, rest = sig & ((1u << shift) - 1u), halfway = 1u << (shift - 1u);
+    return (uint16_t) (s | (keep + (rest > halfway || (rest == halfway && (keep & 1u)))));
+}
+
+__device__ uint16_t rd16(const uint8_t * p) {
+    return (uint16_t) (p[0] | (p[1] << 8));
+}
+
+__device__ void wr16(uint8_t * p, uint16_t v) {
+    p[0] = (uint8_t) (v & 0xFF);
+    p[1] = (uint8_t) (v >> 8);
+}
+
+__device__ void k4_scale_min(int j, const uint8_t * s, uint8_t * sc, uint8_t * mn) {
+    if (j < 4) {
+        *sc = (uint8_t) (s[j] & 63);
+        *mn = (uint8_t) (s[j + 4] & 63);
+    } else {
+        *sc = (uint8_t) ((s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4));
+        *mn = (uint8_t) ((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+    }
+}
+
+// ---- dequantization: one thread per output element -------------------------------------------
+
+template <int DT>
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t * src, float * dst, int64_t n) {
+    for (int64_t e = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t) gridDim.x * blockDim.x) {
+        float y;
+        if (DT == Q4_0) {
+            const uint8_t * blk = src + (e / 32) * 18;
+            const int i = (int) (e % 32);
+            const float d = h2f(rd16(blk));
+            const int q = blk[2 + (i & 15)];
+            y = (float) ((i < 16 ? (q & 0x0F) : (q >> 4)) - 8) * d;
+        } else if (DT == Q8_0) {
+            const uint8_t * blk = src + (e / 32) * 34;
+            y = (float) (int8_t) blk[2 + e % 32] * h2f(rd16(blk));
+        } else if (DT == Q4_K) {
+            const uint8_t * blk = src + (e / 256) * 144;
+            const int i = (int) (e % 256), c = i / 64, l = i % 32, hi = (i % 64) >= 32;
+            uint8_t sc, mn;
+            k4_scale_min(2 * c + hi, blk + 4, &sc, &mn);
+            const float d1 = h2f(rd16(blk)) * (float) sc;
+            const float m1 = h2f(rd16(blk + 2)) * (float) mn;
+            const int q = blk[16 + 32 * c + l];
+            y = d1 * (float) (hi ? (q >> 4) : (q & 0x0F)) - m1;
+        } else {
+            const uint8_t * blk = src + (e / 256) * 210;
+            const int i = (int) (e % 256), h = i / 128, r = (i % 128) / 32, l = i % 32;
+            const uint8_t * ql = blk + 64 * h;
+            const uint8_t qh = blk[128 + 32 * h + l];
+            const int lowq = (r & 1) ? ql[l + 32] : ql[l];
+            const int nib = r < 2 ? (lowq & 0x0F) : (lowq >> 4);
+            const int v = (nib | (((qh >> (2 * r)) & 3) << 4)) - 32;
+            const int8_t sc = (int8_t) blk[192 + 8 * h + 2 * r + l / 16];
+            y = h2f(rd16(blk + 208)) * (float) sc * (float) v;
+        }
+        dst[e] = y;
+    }
+}
+
+// ---- quantization: one thread per block (the reference's ggml quantizers) --------------------
+
+__device__ int nearest_int(float v) {
+    return (int) (__float_as_uint(v + 12582912.0f) & 0x007FFFFFu) - 0x00400000;
+}
+
+__device__ int clampi(int v, int lo, int hi) {
+    return v < lo ? lo : v > hi ? hi : v;
+}
+
+__device__ void quant_q4_0(const float * x, uint8_t * dst) {
+    float amax = 0.0f, vmax = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+        if (amax < fabsf(x[j])) {
+            amax = fabsf(x[j]);
+            vmax = x[j];
+        }
+    }
+    const float d = vmax / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    wr16(dst, f2h(d));
+    for (int j = 0; j < 16; ++j) {
+        int lo = (int8_t) (int32_t) (x[j] * id + 8.5f);
+        int hi = (int8_t) (int32_t) (x[j + 16] * id + 8.5f);
+        lo = (uint8_t) lo > 15 ? 15 : (uint8_t) lo;
+        hi = (uint8_t) hi > 15 ? 15 : (uint8_t) hi;
+        dst[2 + j] = (uint8_t) (lo | (hi << 4));
+    }
+}
+
+__device__ void quant_q8_0(const float * x, uint8_t * dst) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+        const float a = fabsf(x[j]);
+        amax = amax < a ? a : amax;
+    }
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    wr16(dst, f2h(d));
+    for (int j = 0; j < 32; ++j) dst[2 + j] = (uint8_t) (int8_t) lroundf(x[j] * id);
+}
+
+__device__ float q6_group_scale(const float * x, int8_t * L) {
+    const int n = 16, nmax = 32;
+    float amax = 0.0f, vmax = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        if (fabsf(x[i]) > amax) {
+            amax = fabsf(x[i]);
+            vmax = x[i];
+        }
+    }
+    if (amax < 1e-15f) {
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        return 0.0f;
+    }
+    float iscale = -(float) nmax / vmax;
+    float sumlx = 0.0f, suml2 = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        const int l = clampi(nearest_int(iscale * x[i]), -nmax, nmax - 1);
+        L[i] = (int8_t) (l + nmax);
+        const float w = x[i] * x[i];
+        sumlx += w * x[i] * (float) l;
+        suml2 += w * (float) l * (float) l;
+    }
+    float scale = suml2 != 0.0f ? sumlx / suml2 : 0.0f;
+    float best = scale * sumlx;
+    for (int step = -9; step <= 9; ++step) {
+        if (step == 0) continue;
+        iscale = -((float) nmax + 0.1f * (float) step) / vmax;
+        sumlx = 0.0f;
+        suml2 = 0.0f;
+        for (int i = 0; i < n; ++i) {
+            const int l = clampi(nearest_int(iscale * x[i]), -nmax, nmax - 1);
+            const float w = x[i] * x[i];
+            sumlx += w * x[i] * (float) l;
+            suml2 += w * (float) l * (float) l;
+        }
+        if (suml2 > 0.0f && sumlx * sumlx > best * suml2) {
+            for (int i = 0; i < n; ++i) L[i] = (int8_t) (nmax + clampi(nearest_int(iscale * x[i]), -nmax, nmax - 1));
+            scale = sumlx / suml2;
+            best = scale * sumlx;
+        }
+    }
+    return scale;
+}
+
+__device__ float q4k_group_scale(const float * x, const float * w, uint8_t * L, float * neg_min) {
+    const int n = 32, nmax = 15, nstep = 20;
+    const float rmin = -1.0f, rdelta = 0.1f;
+    uint8_t Laux[32];
+    float lo = x[0], hi = x[0];
+    float sum_w = w[0];
+    float sum_x = sum_w * x[0];
+    for (int i = 1; i < n; ++i) {
+        if (x[i] < lo) lo = x[i];
+        if (x[i] > hi) hi = x[i];
+        sum_w += w[i];
+        sum_x += w[i] * x[i];
+    }
+    if (lo > 0.0f) lo = 0.0f;
+    if (hi == lo) {
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        *neg_min = -lo;
+        return 0.0f;
+    }
+    float iscale = (float) nmax / (hi - lo);
+    float scale = 1.0f / iscale;
+    float best_err = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        const int l = clampi(nearest_int(iscale * (x[i] - lo)), 0, nmax);
+        L[i] = (uint8_t) l;
+        const float diff = scale * (float) l + lo - x[i];
+        best_err += w[i] * (diff * diff);
+    }
+    for (int step = 0; step <= nstep; ++step) {
+        iscale = (rmin + rdelta * (float) step + (float) nmax) / (hi - lo);
+        float sum_l = 0.0f, sum_l2 = 0.0f, sum_xl = 0.0f;
+        for (int i = 0; i < n; ++i) {
+            const int l = clampi(nearest_int(iscale * (x[i] - lo)), 0, nmax);
+            Laux[i] = (uint8_t) l;
+            sum_l += w[i] * (float) l;
+            sum_l2 += w[i] * (float) l * (float) l;
+            sum_xl += w[i] * (float) l * x[i];
+        }
+        const float D = sum_w * sum_l2 - sum_l * sum_l;
+        if (D > 0.0f) {
+            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
+            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
+            if (this_min > 0.0f) {
+                this_min = 0.0f;
+                this_scale = sum_xl / sum_l2;
+            }
+            float err = 0.0f;
+            for (int i = 0; i < n; ++i) {
+                const float diff = this_scale * (float) Laux[i] + this_min - x[i];
+                err += w[i] * (diff * diff);
+            }
+            if (err < best_err) {
+                for (int i = 0; i < n; ++i) L[i] = Laux[i];
+                best_err = err;
+                scale = this_scale;
+                lo = this_min;
+            }
+        }
+    }
+    *neg_min = -lo;
+    return scale;
+}
+
+__device__ void quant_q4_k(const float * x, uint8_t * dst) {
+    uint8_t L[256];
+    float w[32], mins[8], scales[8];
+    for (int i = 0; i < 144; ++i) dst[i] = 0;
+    float max_scale = 0.0f, max_min = 0.0f;
+    for (int j = 0; j < 8; ++j) {
+        const float * xs = x + 32 * j;
+        float sum_x2 = 0.0f;
+        for (int l = 0; l < 32; ++l) sum_x2 += xs[l] * xs[l];
+        const float av_x = sqrtf(sum_x2 / 32.0f);
+        for (int l = 0; l < 32; ++l) w[l] = av_x + fabsf(xs[l]);
+        scales[j] = q4k_group_scale(xs, w, L + 32 * j, &mins[j]);
+        if (scales[j] > max_scale) max_scale = scales[j];
+        if (mins[j] > max_min) max_min = mins[j];
+    }
+    const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+    const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+    uint8_t * s = dst + 4;
+    for (int j = 0; j < 8; ++j) {
+        uint8_t ls = (uint8_t) nearest_int(inv_scale * scales[j]);
+        uint8_t lm = (uint8_t) nearest_int(inv_min * mins[j]);
+        if (ls > 63) ls = 63;
+        if (lm > 63) lm = 63;
+        if (j < 4) {
+            s[j] = ls;
+            s[j + 4] = lm;
+        } else {
+            s[j + 4] = (uint8_t) ((ls & 0x0F) | ((lm & 0x0F) << 4));
+            s[j - 4] = (uint8_t) (s[j - 4] | ((ls >> 4) << 6));
+            s[j] = (uint8_t) (s[j] | ((lm >> 4) << 6));
+        }
+    }
+    wr16(dst, f2h(max_scale / 63.0f));
+    wr16(dst + 2, f2h(max_min / 63.0f));
+    const float dh = h2f(rd16(dst)), mh = h2f(rd16(dst + 2));
+    for (int j = 0; j < 8; ++j) {
+        uint8_t sc, mn;
+        k4_scale_min(j, s, &sc, &mn);
+        const float d = dh * (float) sc;
+        if (d == 0.0f) continue;
+        const float dm = mh * (float) mn;
+        for (int i = 0; i < 32; ++i) L[32 * j + i] = (uint8_t) clampi(nearest_int((x[32 * j + i] + dm) / d), 0, 15);
+    }
+    for (int c = 0; c < 4; ++c)
+        for (int l = 0; l < 32; ++l) dst[16 + 32 * c + l] = (uint8_t) (L[64 * c + l] | (L[64 * c + 32 + l] << 4));
+}
+
+__device__ void quant_q6_k(const float * x, uint8_t * dst) {
+    int8_t L[256];
+    float scales[16];
+    float max_scale = 0.0f, max_abs = 0.0f;
+    for (int g = 0; g < 16; ++g) {
+        scales[g] = q6_group_scale(x + 16 * g, L + 16 * g);
+        if (fabsf(scales[g]) > max_abs) {
+            max_abs = fabsf(scales[g]);
+            max_scale = scales[g];
+        }
+    }
+    if (max_abs < 1e-15f) {
+        for (int i = 0; i < 210; ++i) dst[i] = 0;
+        return;
+    }
+    const float iscale = -128.0f / max_scale;
+    wr16(dst + 208, f2h(1.0f / iscale));
+    int8_t * sc = reinterpret_cast<int8_t *>(dst + 192);
+    for (int g = 0; g < 16; ++g) {
+        const int v = nearest_int(iscale * scales[g]);
+        sc[g] = (int8_t) (v < 127 ? v : 127);
+    }
+    const float dh = h2f(rd16(dst + 208));
+    for (int g = 0; g < 16; ++g) {
+        const float d = dh * (float) sc[g];
+        if (d == 0.0f) continue;
+        for (int i = 0; i < 16; ++i) L[16 * g + i] = (int8_t) (clampi(nearest_int(x[16 * g + i] / d), -32, 31) + 32);
+    }
+    for (int h = 0; h < 2; ++h) {
+        uint8_t * ql = dst + 64 * h;
+        uint8_t * qh = dst + 128 + 32 * h;
+        const int8_t * Lh = L + 128 * h;
+        for (int l = 0; l < 32; ++l) {
+            ql[l] = (uint8_t) ((Lh[l] & 0x0F) | ((Lh[l + 64] & 0x0F) << 4));
+            ql[l + 32] = (uint8_t) ((Lh[l + 32] & 0x0F) | ((Lh[l + 96] & 0x0F) << 4));
+            qh[l] = (uint8_t) ((Lh[l] >> 4) | ((Lh[l + 32] >> 4) << 2) | ((Lh[l + 64] >> 4) << 4) | ((Lh[l + 96] >> 4) << 6));
+        }
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(128) void k_quant(const float * src, uint8_t * dst, int64_t nblocks) {
+    const int64_t b = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    if (DT == Q4_0) quant_q4_0(src + 32 * b, dst + 18 * b);
+    if (DT == Q8_0) quant_q8_0(src + 32 * b, dst + 34 * b);
+    if (DT == Q4_K) quant_q4_k(src + 256 * b, dst + 144 * b);
+    if (DT == Q6_K) quant_q6_k(src + 256 * b, dst + 210 * b);
+}
+
+// ---- synthetic normals: splitmix64(seed, i) -> two 53-bit uniforms -> Box-Muller ---------------
+
+__device__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void k_fill_normal(float * dst, int64_t n, uint64_t seed, float mean, float stddev) {
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t) gridDim.x * blockDim.x) {
+        const uint64_t a = splitmix64(seed * 0xD1B54A32D192ED03ull + 2 * (uint64_t) i);
+        const uint64_t b = splitmix64(seed * 0xD1B54A32D192ED03ull + 2 * (uint64_t) i + 1);
+        const double u1 = ((double) (a >> 11) + 1.0) * (1.0 / 9007199254740993.0); // (0, 1]
+        const double u2 = (double) (b >> 11) * (1.0 / 9007199254740992.0);
+        const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+        dst[i] = (float) (mean + stddev * z);
+    }
+}
+
+unsigned grid_for(int64_t n, int threads) {
+    const int64_t g = (n + threads - 1) / threads;
+    return (unsigned) (g < 65536 * 8 ? (g < 1 ? 1 : g) : 65536 * 8);
+}
+
+} // namespace
+
+hipError_t launch_r32_move(int dtype, int64_t K, int64_t M, int64_t row0, int64_t nrows, uint8_t * nat, uint8_t * rep, bool pack,
+                           hipStream_t stream) {
+    const Areas ar = areas_of(dtype);
+    if (ar.na == 0 || nrows <= 0) return hipErrorInvalidValue;
+    const int64_t nb = K / block_elems(dtype);
+    const int64_t groups = (nrows + 31) / 32;
+    if (groups > 65535) return hipErrorInvalidValue; // the caller chunks
+    uint64_t before = 0;
+    for (int k = 0; k < ar.na; ++k) {
+        MoveArgs a;
+        a.nat = nat;
+        a.area = rep + (uint64_t) M * nb * before;
+        a.M = M;
+        a.nb = nb;
+        a.row0 = row0;
+        a.nrows = nrows;
+        a.bs = block_bytes(dtype);
+        a.src = ar.src[k];
+        a.len = ar.len[k];
+        a.xr = ar.xr[k];
+        a.pack = pack ? 1 : 0;
+        const int U = a.len == 2 ? 1 : a.len / 16;
+        const int64_t per_group = 32 * nb * U;
+        const unsigned gx = (unsigned) std::min<int64_t>((per_group + 255) / 256, 4096);
+        hipLaunchKernelGGL(k_r32_move, dim3(gx, (unsigned) groups), dim3(256), 0, stream, a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        before += (uint64_t) ar.len[k];
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_dequantize(int dtype, const uint8_t * src, float * dst, int64_t n_blocks, hipStream_t stream) {
+    const int64_t n = n_blocks * block_elems(dtype);
+    const unsigned g = grid_for(n, 256);
+    switch (dtype) {
+        case Q4_0: hipLaunchKernelGGL(k_dequant<Q4_0>, dim3(g), dim3(256), 0, stream, src, dst, n); break;
+        case Q8_0: hipLaunchKernelGGL(k_dequant<Q8_0>, dim3(g), dim3(256), 0, stream, src, dst, n); break;
+        case Q4_K: hipLaunchKernelGGL(k_dequant<Q4_K>, dim3(g), dim3(256), 0, stream, src, dst, n); break;
+        case Q6_K: hipLaunchKernelGGL(k_dequant<Q6_K>, dim3(g), dim3(256), 0, stream, src, dst, n); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize(int dtype, const float * src, uint8_t * dst, int64_t n_blocks, hipStream_t stream) {
+    const unsigned g = (unsigned) ((n_blocks + 127) / 128);
+    if (n_blocks <= 0 || (n_blocks + 127) / 128 > 0x7FFFFFFF) return hipErrorInvalidValue;
+    switch (dtype) {
+        case Q4_0: hipLaunchKernelGGL(k_quant<Q4_0>, dim3(g), dim3(128), 0, stream, src, dst, n_blocks); break;
+        case Q8_0: hipLaunchKernelGGL(k_quant<Q8_0>, dim3(g), dim3(128), 0, stream, src, dst, n_blocks); break;
+        case Q4_K: hipLaunchKernelGGL(k_quant<Q4_K>, dim3(g), dim3(128), 0, stream, src, dst, n_blocks); break;
+        case Q6_K: hipLaunchKernelGGL(k_quant<Q6_K>, dim3(g), dim3(128), 0, stream, src, dst, n_blocks); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(float * dst, int64_t n, uint64_t seed, float mean, float stddev, hipStream_t stream) {
+    hipLaunchKernelGGL(k_fill_normal, dim3(grid_for(n, 256)), dim3(256), 0, stream, dst, n, seed, mean, stddev);
+    return hipGetLastError();
+}
+
+} // namespace sgk

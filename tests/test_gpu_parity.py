@@ -1,0 +1,311 @@
+"""GPU parity of the hip backend against the CPU oracle, through the C-ABI only.
+
+Covers the drop-in path end to end: R32 upload (device-side pack) and download, bit-exact
+dequantization and quantization on the device, the decode matvec (N = 1..8) and the MFMA prefill
+(N > 8) for Q4_0 / Q8_0 / Q4_K / Q6_K, ragged rows, slices / broadcast, strides, MUL_MAT_MULTI and
+plans. The reference shapes of tests/ops/ops_tests.cpp:702-778 are included.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+import scrapgpulibrary_amd as sg
+from tests.gpu_util import check_matvec, nmse, quantized, run_mul_mat, upload_weights
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "quant_mulmat_r32.npz")
+
+
+def test_device_info(hip):
+    dev, st = hip
+    info = dev.info()
+    assert info.backend_name == b"hip"
+    assert info.warp_or_wave_width == 64
+    assert info.compute_units >= 1
+    assert b"gfx950" in info.generation_reason
+
+
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+@pytest.mark.parametrize("M,slices", [(1, 1), (40, 1), (72, 3), (100, 2)])
+def test_r32_device_layout_matches_reference_pack(hip, dtype, M, slices):
+    """Device bytes after an R32 upload == the oracle's (reference-pinned) pack; download == input."""
+    dev, st = hip
+    K = 2 * sg.BLOCK[dtype]
+    nat = np.random.default_rng(M * 7 + dtype).integers(0, 256, O.row_bytes(dtype, K) * M * slices, dtype=np.uint8)
+    buf, t = upload_weights(dev, st, dtype, nat, K, M, slices)
+    raw = st.read(buf, 0, nat.nbytes)
+    assert np.array_equal(raw, O.r32_pack(dtype, K, M, slices, nat))
+    assert np.array_equal(st.download(t, np.uint8), nat)
+    buf.free()
+
+
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+def test_r32_partial_upload_keeps_tail(hip, dtype):
+    """A partial upload (first `size` natural bytes) leaves the rest of the tensor intact."""
+    dev, st = hip
+    K, M = sg.BLOCK[dtype] * 2, 70
+    rb = O.row_bytes(dtype, K)
+    rng = np.random.default_rng(3)
+    a = rng.integers(0, 256, rb * M, dtype=np.uint8)
+    b = rng.integers(0, 256, rb * M, dtype=np.uint8)
+    buf, t = upload_weights(dev, st, dtype, a, K, M)
+    cut = rb * 33 + 5  # inside the second row group
+    st.upload(t, b, size=cut)
+    got = st.download(t, np.uint8)
+    assert np.array_equal(got[:cut], b[:cut])
+    assert np.array_equal(got[cut:], a[cut:])
+    buf.free()
+
+
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+@pytest.mark.parametrize("layout", [sg.NATURAL, sg.R32], ids=["natural", "r32"])
+def test_dequantize_bit_exact(hip, dtype, layout):
+    dev, st = hip
+    g = np.load(GOLD)
+    name = sg.NAMES[dtype]
+    for key in ("quant", "raw"):
+        q = g[f"{name}_{key}_q"]
+        want = g[f"{name}_{key}_y"]
+        K = sg.BLOCK[dtype]
+        M = want.size // K
+        buf, t = upload_weights(dev, st, dtype, q, K, M, layout=layout)
+        fb = dev.alloc(want.nbytes)
+        ft = sg.tdesc(sg.F32, (K, M), fb)
+        st.dequantize(t, ft)
+        got = st.download(ft)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"{key}: dequantization differs"
+        buf.free()
+        fb.free()
+    # a larger tensor: oracle dequantization of N(0, 0.02) weights
+    K, M = 4 * sg.BLOCK[dtype] * 4, 77
+    q, _ = quantized(dtype, K, M, 11)
+    buf, t = upload_weights(dev, st, dtype, q, K, M, layout=layout)
+    fb = dev.alloc(4 * K * M)
+    ft = sg.tdesc(sg.F32, (K, M), fb)
+    st.dequantize(t, ft)
+    assert np.array_equal(st.download(ft).view(np.uint32), O.dequantize(dtype, q, K * M).view(np.uint32))
+    buf.free()
+    fb.free()
+
+
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+@pytest.mark.parametrize("layout", [sg.NATURAL, sg.R32], ids=["natural", "r32"])
+def test_quantize_matches_reference_bytes(hip, dtype, layout):
+    dev, st = hip
+    g = np.load(GOLD)
+    name = sg.NAMES[dtype]
+    cases = [g[f"{name}_quant_x"]]
+    K = 4 * sg.BLOCK[dtype]
+    cases.append(O.normal(K * 33, 5, 0.0, 0.02))
+    cases.append(O.normal(K * 33, 6, 0.0, 1.0))
+    for x in cases:
+        M = x.size // K if x.size % K == 0 else x.size // sg.BLOCK[dtype]
+        KK = x.size // M
+        want = O.quantize(dtype, x)
+        fb = dev.alloc(x.nbytes)
+        ft = sg.tdesc(sg.F32, (KK, M), fb)
+        st.upload(ft, x)
+        qb = dev.alloc(want.nbytes)
+        qt = sg.tdesc(dtype, (KK, M), qb, layout=layout)
+        st.quantize(ft, qt)
+        got = st.download(qt, np.uint8)
+        assert np.array_equal(got, want), f"quantized bytes differ ({np.count_nonzero(got != want)} bytes)"
+        fb.free()
+        qb.free()
+
+
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+def test_golden_mul_mat(hip, dtype):
+    """The reference's own MUL_MAT outputs (scrapgpu_ref_execute, committed fixtures)."""
+    dev, st = hip
+    g = np.load(GOLD)
+    name = sg.NAMES[dtype]
+    K = 256 if sg.BLOCK[dtype] == 256 else 96
+    for M, N in ((24, 1), (24, 4), (37, 7), (37, 17)):
+        pre = f"{name}_mm_K{K}_M{M}_N{N}"
+        w, x, want = g[pre + "_w"], g[pre + "_x"], g[pre + "_y"]
+        y = run_mul_mat(dev, st, dtype, w, K, M, x)
+        deq = O.dequantize(dtype, w, K * M)
+        if N <= 8:
+            check_matvec(y, want, x, deq)
+        else:
+            assert nmse(y, want) <= 5e-5
+
+
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+@pytest.mark.parametrize("N", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_matvec_decode(hip, dtype, N):
+    dev, st = hip
+    for K, M in ((4096, 96), (sg.BLOCK[dtype] * 3, 37), (2048, 1000)):
+        q, deq = quantized(dtype, K, M, 100 + N)
+        x = O.normal(N * K, 200 + N).reshape(N, K)
+        y = run_mul_mat(dev, st, dtype, q, K, M, x)
+        ref = O.mul_mat(dtype, q, K, M, x, threads=8)
+        check_matvec(y, ref, x, deq)
+
+
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+def test_matvec_k_split_repeated(hip, dtype):
+    """Few row groups + long K: the split-K path with its arrival counters, run 3 times."""
+    dev, st = hip
+    K, M, N = 16384, 64, 2
+    q, deq = quantized(dtype, K, M, 7)
+    x = O.normal(N * K, 8).reshape(N, K)
+    ref = O.mul_mat(dtype, q, K, M, x, threads=8)
+    for _ in range(3):
+        y = run_mul_mat(dev, st, dtype, q, K, M, x)
+        check_matvec(y, ref, x, deq)
+
+
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+@pytest.mark.parametrize("N", [9, 16, 64, 130])
+def test_prefill_mfma(hip, dtype, N):
+    dev, st = hip
+    K, M = 1024, 200
+    q, _ = quantized(dtype, K, M, 300 + N)
+    x = O.normal(N * K, 400 + N).reshape(N, K)
+    y = run_mul_mat(dev, st, dtype, q, K, M, x)
+    ref = O.mul_mat(dtype, q, K, M, x, threads=8)
+    e = nmse(y, ref)
+    assert e <= 5e-5, f"NMSE {e:.3e}"
+
+
+@pytest.mark.parametrize("dtype", [sg.Q4_0, sg.Q4_K], ids=lambda d: sg.NAMES[d])
+@pytest.mark.parametrize("N", [1, 4, 33])
+def test_slices_broadcast_and_strides(hip, dtype, N):
+    """src0 with 2 slices broadcast over src1's 4 (r2 = 2); x and y with padded column strides."""
+    dev, st = hip
+    K, M = 2 * sg.BLOCK[dtype], 40
+    w2 = 2
+    q0, d0 = quantized(dtype, K, M, 1)
+    q1, d1 = quantized(dtype, K, M, 2)
+    wq = np.concatenate([q0, q1])
+    wb, wt = upload_weights(dev, st, dtype, wq, K, M, slices=w2)
+    S = 4
+    xs1 = K + 8  # padded column stride (floats)
+    ys1 = M + 5
+    x = O.normal(S * N * xs1, 9).reshape(S, N, xs1)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N, S), xb, nb=[4, 4 * xs1, 4 * xs1 * N, 4 * xs1 * N * S])
+    st.write(xb, 0, x)
+    yb = dev.alloc(4 * ys1 * N * S)
+    st.write(yb, 0, np.full(ys1 * N * S, -7.0, np.float32))
+    yt = sg.tdesc(sg.F32, (M, N, S), yb, nb=[4, 4 * ys1, 4 * ys1 * N, 4 * ys1 * N * S])
+    op, keep = sg.mul_mat_op(wt, xt, yt, allow_broadcast=1)
+    st.execute(op)
+    st.sync()
+    y = st.read(yb, 0, 4 * ys1 * N * S).view(np.float32).reshape(S, N, ys1)
+    for s in range(S):
+        qs, ds = (q0, d0) if s // 2 == 0 else (q1, d1)
+        ref = O.mul_mat(dtype, qs, K, M, x[s, :, :K].copy())
+        if N <= 8:
+            check_matvec(y[s, :, :M], ref, x[s, :, :K], ds)
+        else:
+            assert nmse(y[s, :, :M], ref) <= 5e-5
+        assert np.all(y[s, :, M:] == -7.0), "padding of dst was written"
+    # the same op without allow_broadcast is refused
+    op0, keep0 = sg.mul_mat_op(wt, xt, yt, allow_broadcast=0)
+    stt, reason = dev.supported(op0)
+    assert stt == sg.UNSUPPORTED and "broadcast" in reason
+    for b in (wb, xb, yb):
+        b.free()
+
+
+def test_support_rules(hip):
+    dev, st = hip
+    K, M = 256, 32
+    wb = dev.alloc(O.row_bytes(sg.Q4_K, K) * M)
+    xb, yb = dev.alloc(4 * K), dev.alloc(4 * M)
+    x, y = sg.tdesc(sg.F32, (K, 1), xb), sg.tdesc(sg.F32, (M, 1), yb)
+    natural = sg.tdesc(sg.Q4_K, (K, M), wb, layout=sg.NATURAL)
+    op, keep = sg.mul_mat_op(natural, x, y)
+    stt, reason = dev.supported(op)
+    assert stt == sg.UNSUPPORTED and "R32" in reason
+    f32w = sg.tdesc(sg.F32, (K, M), wb)
+    op, keep = sg.mul_mat_op(f32w, x, y)
+    assert dev.supported(op)[0] == sg.UNSUPPORTED
+    r32 = sg.tdesc(sg.Q4_K, (K, M), wb, layout=sg.R32)
+    op, keep = sg.mul_mat_op(r32, x, y)
+    assert dev.supported(op)[0] == sg.OK
+    bad_y = sg.tdesc(sg.F32, (M + 1, 1), yb)
+    op, keep = sg.mul_mat_op(r32, x, bad_y)
+    assert dev.supported(op)[0] == sg.INVALID_ARGUMENT
+    for b in (wb, xb, yb):
+        b.free()
+
+
+@pytest.mark.parametrize("n", [2, 3])
+def test_mul_mat_multi(hip, n):
+    """tests/ops/ops_tests.cpp:751-778: n Q4_0 weights sharing one x."""
+    dev, st = hip
+    K, M = 96, 8
+    ws, wts, qs = [], [], []
+    for i in range(n):
+        q, _ = quantized(sg.Q4_0, K, M, 50 + i, std=0.5)
+        b, t = upload_weights(dev, st, sg.Q4_0, q, K, M)
+        ws.append(b)
+        wts.append(t)
+        qs.append(q)
+    x = O.normal(K, 60).reshape(1, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, 1), xb)
+    st.upload(xt, x)
+    ybs = [dev.alloc(4 * M) for _ in range(n)]
+    yts = [sg.tdesc(sg.F32, (M, 1), b) for b in ybs]
+    op, keep = sg.multi_op(wts, xt, yts)
+    st.execute(op)
+    st.sync()
+    for i in range(n):
+        ref = O.mul_mat(sg.Q4_0, qs[i], K, M, x)
+        assert nmse(st.download(yts[i]).reshape(1, M), ref) <= 1e-6
+    for b in ws + ybs + [xb]:
+        b.free()
+
+
+def test_plan_and_buffer_lifetime(hip):
+    dev, st = hip
+    L = sg.lib()
+    K, M = 512, 64
+    q, deq = quantized(sg.Q6_K, K, M, 70)
+    wb, wt = upload_weights(dev, st, sg.Q6_K, q, K, M)
+    x = O.normal(2 * K, 71).reshape(2, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, 2), xb)
+    st.upload(xt, x)
+    yb = dev.alloc(4 * M * 2)
+    yt = sg.tdesc(sg.F32, (M, 2), yb)
+    op, keep = sg.mul_mat_op(wt, xt, yt)
+    node = sg.PlanNode(C.sizeof(sg.PlanNode), op, 0)
+    nodes = (sg.PlanNode * 1)(node)
+    pd = sg.PlanDesc(C.sizeof(sg.PlanDesc), nodes, 1)
+    plan = C.c_void_p()
+    sg.check(L.scrapgpu_plan_build(dev.handle, C.byref(pd), C.byref(plan)), "plan_build")
+    assert L.scrapgpu_buffer_free(wb.handle) == sg.INVALID_ARGUMENT  # referenced by a live plan
+    for _ in range(2):
+        sg.check(L.scrapgpu_plan_execute(st.handle, plan), "plan_execute")
+    st.sync()
+    check_matvec(st.download(yt).reshape(2, M), O.mul_mat(sg.Q6_K, q, K, M, x), x, deq)
+    sg.check(L.scrapgpu_plan_free(plan), "plan_free")
+    for b in (wb, xb, yb):
+        b.free()
+
+
+def test_profiler_counts_launches(hip):
+    dev, st = hip
+    L = sg.lib()
+    K, M = 1024, 256
+    q, _ = quantized(sg.Q4_K, K, M, 90)
+    L.scrapgpu_hip_profile_reset()
+    L.scrapgpu_hip_profile_enable(1)
+    try:
+        x = O.normal(K, 91).reshape(1, K)
+        run_mul_mat(dev, st, sg.Q4_K, q, K, M, x)
+    finally:
+        L.scrapgpu_hip_profile_enable(0)
+    rows = {r["name"]: r for r in sg.profile_table()}
+    assert rows["matvec_q4_k"]["launches"] == 1
+    assert rows["matvec_q4_k"]["bytes"] == O.row_bytes(sg.Q4_K, K) * M
