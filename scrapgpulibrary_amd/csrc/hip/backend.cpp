@@ -74,7 +74,6 @@ struct Stream {
     scrapgpu_object_header hdr;
     Device * dev;
     hipStream_t s;
-    sgk::Scratch scratch{nullptr, 0, nullptr, 0};
 };
 
 struct Device {
@@ -375,8 +374,6 @@ scrapgpu_status api_stream_free(scrapgpu_stream_t * stream) {
     if (s == nullptr) return invalid("not a hip stream");
     use(s->dev);
     hipStreamSynchronize(s->s);
-    if (s->scratch.partials) hipFree(s->scratch.partials);
-    if (s->scratch.counters) hipFree(s->scratch.counters);
     hipStreamDestroy(s->s);
     delete s;
     return SCRAPGPU_STATUS_OK;
@@ -393,32 +390,6 @@ scrapgpu_status api_stream_sync(scrapgpu_stream_t * stream) {
 scrapgpu_device_t * api_stream_device(scrapgpu_stream_t * stream) {
     Stream * s = stream_of(stream);
     return s ? reinterpret_cast<scrapgpu_device_t *>(s->dev) : nullptr;
-}
-
-// scratch of the split-K matvec: grown on demand (the stream is drained before a re-allocation)
-scrapgpu_status ensure_scratch(Stream * s, size_t partial_floats, size_t counters) {
-    sgk::Scratch & sc = s->scratch;
-    if (partial_floats > sc.partial_floats) {
-        SG_HIP(hipStreamSynchronize(s->s), "hipStreamSynchronize");
-        if (sc.partials) hipFree(sc.partials);
-        sc.partials = nullptr;
-        sc.partial_floats = 0;
-        const size_t n = std::max<size_t>(partial_floats, (size_t) 1 << 20);
-        SG_HIP(hipMalloc(reinterpret_cast<void **>(&sc.partials), n * sizeof(float)), "hipMalloc (scratch)");
-        sc.partial_floats = n;
-    }
-    if (counters > sc.counter_count) {
-        SG_HIP(hipStreamSynchronize(s->s), "hipStreamSynchronize");
-        if (sc.counters) hipFree(sc.counters);
-        sc.counters = nullptr;
-        sc.counter_count = 0;
-        const size_t n = std::max<size_t>(counters, (size_t) 1 << 16);
-        SG_HIP(hipMalloc(reinterpret_cast<void **>(&sc.counters), n * sizeof(uint32_t)), "hipMalloc (counters)");
-        SG_HIP(hipMemsetAsync(sc.counters, 0, n * sizeof(uint32_t), s->s), "hipMemsetAsync");
-        SG_HIP(hipStreamSynchronize(s->s), "hipStreamSynchronize");
-        sc.counter_count = n;
-    }
-    return SCRAPGPU_STATUS_OK;
 }
 
 // ---- tensor transfers with R32 packing in HBM ------------------------------------------------------
@@ -611,14 +582,10 @@ double weight_bytes(const sgk::MatArgs & a) {
 scrapgpu_status run_product(Stream * s, sgk::MatArgs a) {
     const int cus = (int) s->dev->cus;
     if (a.N <= 8) {
-        // scratch for a possible K split (sized generously: groups * slices * 64 parts * 8 columns * 32)
-        const size_t groups = (size_t) ((a.M + 31) / 32) * (size_t) (a.ne12 * a.ne13);
-        scrapgpu_status st = ensure_scratch(s, groups * 64 * 8 * 32 > ((size_t) 1 << 26) ? ((size_t) 1 << 26) : groups * 64 * 8 * 32, groups);
-        if (st != SCRAPGPU_STATUS_OK) return st;
         ProfScope prof(s->s);
         const char * name = nullptr;
         uint64_t grid = 0;
-        SG_HIP(sgk::launch_matvec(a, s->scratch, cus, s->s, &name, &grid), "matvec launch");
+        SG_HIP(sgk::launch_matvec(a, cus, s->s, &name, &grid), "matvec launch");
         prof.done(name, weight_bytes(a), 2.0 * (double) a.M * (double) a.K * (double) a.N * (double) (a.ne12 * a.ne13));
         return SCRAPGPU_STATUS_OK;
     }

@@ -36,18 +36,8 @@ struct MatArgs {
     int64_t r2, r3;     // broadcast factors
 };
 
-// Scratch a stream lends to kernels that split K over work-groups: per-part partial sums and
-// one arrival counter per row group (counters are zero between launches: the last work-group
-// of a group resets its counter).
-struct Scratch {
-    float * partials;
-    size_t partial_floats;
-    uint32_t * counters;
-    size_t counter_count;
-};
-
 // decode matvec for 1 <= N <= 8 (weights streamed once, every column reused in registers)
-hipError_t launch_matvec(const MatArgs & a, const Scratch & s, int cu_count, hipStream_t stream, const char ** kernel_name,
+hipError_t launch_matvec(const MatArgs & a, int cu_count, hipStream_t stream, const char ** kernel_name,
                          uint64_t * grid_size);
 
 // prefill: bf16 MFMA with fp32 accumulate, weights dequantized into LDS (any N >= 1)

@@ -1,72 +1,52 @@
 // Decode matvec over R32 weights for 1 <= N <= 8 columns (gfx950, wave64).
 //
-// Work decomposition. A work-group (256 threads = 4 waves) owns one 32-row group of one slice and
-// a contiguous range of "steps" along K (a step is one block: 32 elements of Q8_0, 256 of Q4_K /
-// Q6_K; for Q4_0 a step is two blocks). Lane l of a wave serves row (l & 31) of the group; its
-// half (l >> 5) selects which 16-byte units of the step it loads, so one wave-wide 128-bit load
-// reads 2 x 512 contiguous bytes of the R32 area (fully coalesced). The 4 waves take the steps of
-// the range round-robin.
+// Work decomposition. A work-group owns R consecutive rows (a whole R32 group or an aligned part
+// of one) of one slice and the whole K range, so no work-group ever waits for
+// another: on MI355X the 8 XCDs have separate L2s and any cross-work-group handshake inside a
+// kernel costs an L2 write-back/invalidate. R (32, 16, 8 or 4) is picked per shape so that the grid
+// holds at least two work-groups per CU. Its W waves (8, up to 16 for small grids) split K: wave w
+// takes steps w, w+W, ...; each wave keeps 4 steps of weight loads in flight in a register ring,
+// and issues the first ones before the x chunk is staged so that the two overlap.
 //
-// Arithmetic. A lane converts the bytes of a unit with one mask per 4 weights and one
-// byte->float conversion per weight, then one FMA per weight and column against x from LDS
-// (all 32 lanes of a half read the same LDS address: a broadcast). Block scales are factored out
-// of the inner sum, and every constant offset of a format (Q4_0's -8, Q8_0's stored xor 0x80,
-// Q6_K's -32, Q4_K's -dmin*m) is applied once per 16 weights through precomputed sums of 16
-// consecutive x values (also in LDS):
-//   Q4_0: d * (sum q x - 8 sum x)            Q8_0: d * (sum u x - 128 sum x)
+// Inside a wave, lane l serves row r = l % R of the tile through slot s = l / R (S = 64 / R slots).
+// A step covers `bps` blocks whose "tasks" (16-byte R32 units, or for Q6_K the three units that
+// hold one 64-element run) are dealt to the slots, so one wave-wide 128-bit load reads S runs of
+// 16*R contiguous bytes (>= 64 bytes): coalesced.
+//
+// Arithmetic. A lane converts bytes with one mask per 4 weights and one byte->float conversion per
+// weight, then one FMA per weight and column against x held in LDS (lanes of a slot read the same
+// LDS address: a broadcast). Block scales are factored out of the inner sums and every constant
+// offset of a format is applied once per 16 weights through precomputed sums of 16 consecutive x:
+//   Q4_0: d * (sum q x - 8 sum x)            Q8_0: d * (sum u x - 128 sum x)   (u = q xor 0x80)
 //   Q4_K: d*sc * sum q x - dmin*m * sum x    Q6_K: d*sc * (sum q x - 32 sum x)
-// The high nibble is used in place (value * 16) and the 1/16 folded into its scale.
+// The high nibble is used in place (value * 16) and the 1/16 folded into its scale. The slots and
+// then the waves of a row are added in a fixed order (shuffles, then LDS): deterministic.
 //
-// K split. When the row groups alone cannot fill the GPU, the K range is split over `ksplit`
-// work-groups per row group. Each writes its partial sums to stream scratch; the last to arrive
-// (an agent-scope atomic counter) adds the parts in part order -- deterministic -- writes y and
-// re-arms the counter. One launch, no memset.
+// x is staged per K chunk (all of K when it fits the LDS budget, else chunks of whole steps).
 #include "kernels.h"
 
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <cstdlib>
+#include <vector>
 
 namespace sgk {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
-constexpr int kLdsFloats = 16384; // 64 KiB of x (+ sums) per work-group at most
+constexpr int kMaxWaves = 8;
+constexpr int kDepth = 4;      // most steps in flight per wave
+constexpr int kLdsBudget = 56 * 1024; // bytes of x (+ sums) per work-group
 
 struct MvLaunch {
     MatArgs a;
-    int64_t groups;
-    int64_t steps;     // steps along K
-    int64_t per_part;  // steps per work-group
-    int ksplit;
-    int elems_step;    // K elements per step
-    float * partials;
-    uint32_t * counters;
+    int64_t tiles;      // row tiles per slice
+    int64_t kc;         // K elements staged per chunk (a multiple of the step)
+    int wt;             // waves that split the K steps of one tile
 };
 
 __device__ __forceinline__ float half_bits(uint32_t h) {
     return __half2float(__ushort_as_half((unsigned short) (h & 0xFFFFu)));
-}
-
-// sum over the 4 bytes of v of byte_i * x[i]
-__device__ __forceinline__ float dot4(uint32_t v, float4 x, float acc) {
-    acc = fmaf((float) (v & 0xFFu), x.x, acc);
-    acc = fmaf((float) ((v >> 8) & 0xFFu), x.y, acc);
-    acc = fmaf((float) ((v >> 16) & 0xFFu), x.z, acc);
-    acc = fmaf((float) (v >> 24), x.w, acc);
-    return acc;
-}
-
-// sum_i byte_i(q) * x[i] for the 16 bytes of q (already masked) and 16 floats of LDS
-__device__ __forceinline__ float dot16(uint4 q, const float * xs) {
-    const float4 * x4 = reinterpret_cast<const float4 *>(xs);
-    float acc = 0.0f;
-    acc = dot4(q.x, x4[0], acc);
-    acc = dot4(q.y, x4[1], acc);
-    acc = dot4(q.z, x4[2], acc);
-    acc = dot4(q.w, x4[3], acc);
-    return acc;
 }
 
 __device__ __forceinline__ uint4 mask4(uint4 q, uint32_t m) {
@@ -82,231 +62,447 @@ __device__ __forceinline__ uint32_t byte_of(uint4 v, int i) {
     return (w >> (8 * (i & 3))) & 0xFFu;
 }
 
-// ---- one step of one lane, per format ------------------------------------------------------
-// xs: this work-group's x slab, column n at xs + n * xlen, element e at (e - e0);
-// ss: sums of 16 consecutive x, column n at ss + n * nseg, segment (e - e0) / 16.
-
-template <int NC>
-__device__ __forceinline__ void step_q4_0(const MvLaunch & L, const uint8_t * w, int64_t g0, int rs, int row, int hf, int64_t s,
-                                          int64_t e0, const float * xs, int xlen, const float * ss, int nseg, float * acc) {
-    const int64_t b = 2 * s + hf;
-    if (b >= L.a.nb) return;
-    const int64_t nb = L.a.nb;
-    const uint4 q = load16(w + (uint64_t) g0 * nb * 16 + ((uint64_t) b * rs + row) * 16);
-    const uint32_t dh = *reinterpret_cast<const uint16_t *>(w + (uint64_t) L.a.M * nb * 16 + (uint64_t) g0 * nb * 2 + ((uint64_t) b * rs + row) * 2);
-    const float d = half_bits(dh);
-    const uint4 lo = mask4(q, 0x0F0F0F0Fu), hi = mask4(q, 0xF0F0F0F0u);
-    const int off = (int) (32 * b - e0);
-#pragma unroll
-    for (int n = 0; n < NC; ++n) {
-        const float * x = xs + n * xlen + off;
-        const float * sm = ss + n * nseg + off / 16;
-        const float t = (dot16(lo, x) - 8.0f * sm[0]) + (dot16(hi, x + 16) * 0.0625f - 8.0f * sm[1]);
-        acc[n] = fmaf(d, t, acc[n]);
-    }
+// steps in flight per wave: the largest power of two (<= kDepth) whose raw weight registers fit in
+// ~48 VGPRs; the host picks the waves per tile so that every wave's step count is a multiple of it
+constexpr int ring_depth(size_t raw_bytes) {
+    return (int) (raw_bytes / 4) * 4 <= 48 ? 4 : (int) (raw_bytes / 4) * 2 <= 48 ? 2 : 1;
 }
 
-template <int NC>
-__device__ __forceinline__ void step_q8_0(const MvLaunch & L, const uint8_t * w, int64_t g0, int rs, int row, int hf, int64_t b,
-                                          int64_t e0, const float * xs, int xlen, const float * ss, int nseg, float * acc) {
-    const int64_t nb = L.a.nb;
-    const uint4 u = load16(w + (uint64_t) g0 * nb * 32 + (((uint64_t) b * 2 + hf) * rs + row) * 16);
-    const uint32_t dh = *reinterpret_cast<const uint16_t *>(w + (uint64_t) L.a.M * nb * 32 + (uint64_t) g0 * nb * 2 + ((uint64_t) b * rs + row) * 2);
-    const float d = half_bits(dh);
-    const int off = (int) (32 * b + 16 * hf - e0);
-#pragma unroll
-    for (int n = 0; n < NC; ++n) {
-        const float t = dot16(u, xs + n * xlen + off) - 128.0f * ss[n * nseg + off / 16];
-        acc[n] = fmaf(d, t, acc[n]);
-    }
+// ---- per format: tasks per block, elements per block, raw registers of one task ----------------
+
+// The x chunk in LDS: for column n and 16-element segment g, xq[(n * nseg + g)] holds two int8
+// planes (a, b) with x ~= s * a + (s / 256) * b, and xf[(n * nseg + g)] = {s / 256, sum of the 16 x}.
+struct XSeg {
+    uint4 a, b;
+};
+
+// 256 * sum(q_i * a_i) + sum(q_i * b_i) over 16 int8 pairs: x dot q in units of s / 256
+__device__ __forceinline__ int dot16i(uint4 q, const XSeg & x) {
+    int t = __builtin_amdgcn_sdot4((int) q.x, (int) x.a.x, 0, false);
+    t = __builtin_amdgcn_sdot4((int) q.y, (int) x.a.y, t, false);
+    t = __builtin_amdgcn_sdot4((int) q.z, (int) x.a.z, t, false);
+    t = __builtin_amdgcn_sdot4((int) q.w, (int) x.a.w, t, false);
+    t <<= 8;
+    t = __builtin_amdgcn_sdot4((int) q.x, (int) x.b.x, t, false);
+    t = __builtin_amdgcn_sdot4((int) q.y, (int) x.b.y, t, false);
+    t = __builtin_amdgcn_sdot4((int) q.z, (int) x.b.z, t, false);
+    t = __builtin_amdgcn_sdot4((int) q.w, (int) x.b.w, t, false);
+    return t;
 }
 
-template <int NC>
-__device__ __forceinline__ void step_q4_k(const MvLaunch & L, const uint8_t * w, int64_t g0, int rs, int row, int hf, int64_t b,
-                                          int64_t e0, const float * xs, int xlen, const float * ss, int nseg, float * acc) {
-    const int64_t nb = L.a.nb;
-    const uint8_t * qb = w + (uint64_t) g0 * nb * 128 + ((uint64_t) b * 8 * rs + row) * 16;
-    uint4 q[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) q[c] = load16(qb + (uint64_t) (2 * c + hf) * rs * 16);
-    const uint4 hd = load16(w + (uint64_t) L.a.M * nb * 128 + (uint64_t) g0 * nb * 16 + ((uint64_t) b * rs + row) * 16);
-    const float d = half_bits(hd.x), dmin = half_bits(hd.x >> 16);
-    // 12 scale bytes s[0..11] = bytes 4..15 of the header
-    const uint4 sv = make_uint4(hd.y, hd.z, hd.w, 0u);
-    const int base = (int) (256 * b - e0);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        uint32_t sc0, m0, sc1, m1;
-        const int j0 = 2 * c, j1 = 2 * c + 1;
-        if (c < 2) {
-            sc0 = byte_of(sv, j0) & 63u;
-            m0 = byte_of(sv, j0 + 4) & 63u;
-            sc1 = byte_of(sv, j1) & 63u;
-            m1 = byte_of(sv, j1 + 4) & 63u;
-        } else {
-            sc0 = (byte_of(sv, j0 + 4) & 0x0Fu) | ((byte_of(sv, j0 - 4) >> 6) << 4);
-            m0 = (byte_of(sv, j0 + 4) >> 4) | ((byte_of(sv, j0) >> 6) << 4);
-            sc1 = (byte_of(sv, j1 + 4) & 0x0Fu) | ((byte_of(sv, j1 - 4) >> 6) << 4);
-            m1 = (byte_of(sv, j1 + 4) >> 4) | ((byte_of(sv, j1) >> 6) << 4);
+__device__ __forceinline__ uint4 shr4(uint4 q, int s) {
+    return make_uint4(q.x >> s, q.y >> s, q.z >> s, q.w >> s);
+}
+
+// ---- per format: the lane's view of one row tile ------------------------------------------------
+// A Stepper is built once per tile: 64-bit base pointers of the lane's row in every R32 area, then
+// 32-bit offsets per step. load(step) fetches all the lane's 16-byte units of one step (and the
+// block's scales once); compute() accumulates them against x.
+
+template <int DT, int R> struct Stepper;
+
+// blocks per step, tasks per lane and step, K elements per step of a format with T tasks per block
+template <int T, int R, int BE>
+struct Geo {
+    static constexpr int S = 64 / R;
+    static constexpr int BPS = S > T ? S / T : 1;
+    static constexpr int TPL = T * BPS / S;
+    static constexpr int EPS = BPS * BE;
+};
+
+template <int R>
+struct Stepper<Q4_0, R> : Geo<1, R, 32> {
+    using G = Geo<1, R, 32>;
+    struct Raw { uint4 q; uint32_t d; };
+    const uint8_t * qb;
+    const uint8_t * db;
+    uint32_t qblk, dblk;
+    int64_t nb;
+    int slot;
+    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int slot_) {
+        nb = nb_;
+        slot = slot_;
+        qb = w + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
+        db = w + (uint64_t) M * nb * 16 + (uint64_t) g0 * nb * 2 + (uint64_t) lr * 2;
+        qblk = (uint32_t) rs * 16;
+        dblk = (uint32_t) rs * 2;
+    }
+    __device__ int64_t block(int64_t step) const { return step * G::BPS + slot; }
+    __device__ Raw load(int64_t step) const {
+        Raw r{};
+        const int64_t b = block(step);
+        if (b < nb) {
+            r.q = load16(qb + (uint32_t) b * qblk);
+            r.d = *reinterpret_cast<const uint16_t *>(db + (uint32_t) b * dblk);
         }
-        const float dl = d * (float) sc0, ml = dmin * (float) m0;
-        const float dhh = d * (float) sc1 * 0.0625f, mh = dmin * (float) m1;
-        const uint4 lo = mask4(q[c], 0x0F0F0F0Fu), hi = mask4(q[c], 0xF0F0F0F0u);
-        const int off = base + 64 * c + 16 * hf;
+        return r;
+    }
+    template <int NC>
+    __device__ void compute(const Raw & r, int64_t step, int64_t kc0, const XSeg * xq, const float2 * xf, int nseg, float * acc) const {
+        const int64_t b = block(step);
+        if (b >= nb) return;
+        const int sg = (int) ((b * 32 - kc0) >> 4);
+        const float d = half_bits(r.d);
+        const uint4 lo = mask4(r.q, 0x0F0F0F0Fu), hi = mask4(shr4(r.q, 4), 0x0F0F0F0Fu);
 #pragma unroll
         for (int n = 0; n < NC; ++n) {
-            const float * x = xs + n * xlen + off;
-            const float * sm = ss + n * nseg + off / 16;
+            const int g = n * nseg + sg;
+            const float2 f0 = xf[g], f1 = xf[g + 1];
             float a = acc[n];
-            a = fmaf(dl, dot16(lo, x), a);
-            a = fmaf(-ml, sm[0], a);
-            a = fmaf(dhh, dot16(hi, x + 32), a);
-            a = fmaf(-mh, sm[2], a);
+            a = fmaf(d * f0.x, (float) dot16i(lo, xq[g]), a);
+            a = fmaf(d * f1.x, (float) dot16i(hi, xq[g + 1]), a);
+            a = fmaf(-8.0f * d, f0.y + f1.y, a);
             acc[n] = a;
         }
     }
+};
+
+template <int R>
+struct Stepper<Q8_0, R> : Geo<2, R, 32> {
+    using G = Geo<2, R, 32>;
+    struct Raw { uint4 q; uint32_t d; };
+    const uint8_t * qb;
+    const uint8_t * db;
+    uint32_t qblk, qunit, dblk;
+    int64_t nb;
+    int slot;
+    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int slot_) {
+        nb = nb_;
+        slot = slot_;
+        qb = w + (uint64_t) g0 * nb * 32 + (uint64_t) lr * 16;
+        db = w + (uint64_t) M * nb * 32 + (uint64_t) g0 * nb * 2 + (uint64_t) lr * 2;
+        qblk = (uint32_t) rs * 32;
+        qunit = (uint32_t) rs * 16;
+        dblk = (uint32_t) rs * 2;
+    }
+    // TPL == 1: the lane's task is slot -> block step * BPS + slot / 2, unit slot % 2
+    __device__ int64_t block(int64_t step) const { return step * G::BPS + slot / 2; }
+    __device__ Raw load(int64_t step) const {
+        Raw r{};
+        const int64_t b = block(step);
+        if (b < nb) {
+            r.q = load16(qb + (uint32_t) b * qblk + (uint32_t) (slot & 1) * qunit);
+            r.d = *reinterpret_cast<const uint16_t *>(db + (uint32_t) b * dblk);
+        }
+        return r;
+    }
+    template <int NC>
+    __device__ void compute(const Raw & r, int64_t step, int64_t kc0, const XSeg * xq, const float2 * xf, int nseg, float * acc) const {
+        const int64_t b = block(step);
+        if (b >= nb) return;
+        const int sg = (int) ((b * 32 - kc0) >> 4) + (slot & 1);
+        const float d = half_bits(r.d);
+        const uint4 q = make_uint4(r.q.x ^ 0x80808080u, r.q.y ^ 0x80808080u, r.q.z ^ 0x80808080u, r.q.w ^ 0x80808080u);
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            const int g = n * nseg + sg;
+            acc[n] = fmaf(d * xf[g].x, (float) dot16i(q, xq[g]), acc[n]);
+        }
+    }
+};
+
+// 6-bit scale and min of sub-block j (0..7) from the 12 packed bytes s[0..11] = {hd.y, hd.z, hd.w}
+__device__ __forceinline__ void k4_scale_min(uint4 hd, int j, float & sc, float & mn) {
+    const uint32_t lo4 = hd.y, hi4 = hd.z, top4 = hd.w; // s[0..3], s[4..7], s[8..11]
+    const int sh = 8 * (j & 3);
+    if (j < 4) {
+        sc = (float) ((lo4 >> sh) & 63u);
+        mn = (float) ((hi4 >> sh) & 63u);
+    } else {
+        const uint32_t t = (top4 >> sh) & 0xFFu;
+        sc = (float) ((t & 0x0Fu) | (((lo4 >> sh) >> 6 & 3u) << 4));
+        mn = (float) ((t >> 4) | (((hi4 >> sh) >> 6 & 3u) << 4));
+    }
 }
 
-template <int NC>
-__device__ __forceinline__ void step_q6_k(const MvLaunch & L, const uint8_t * w, int64_t g0, int rs, int row, int hf, int64_t b,
-                                          int64_t e0, const float * xs, int xlen, const float * ss, int nseg, float * acc) {
-    const int64_t nb = L.a.nb, M = L.a.M;
-    const uint8_t * qb = w + (uint64_t) g0 * nb * 192 + ((uint64_t) b * 12 * rs + row) * 16;
-    const uint4 scv = load16(w + (uint64_t) M * nb * 192 + (uint64_t) g0 * nb * 16 + ((uint64_t) b * rs + row) * 16);
-    const uint32_t dh = *reinterpret_cast<const uint16_t *>(w + (uint64_t) M * nb * 208 + (uint64_t) g0 * nb * 2 + ((uint64_t) b * rs + row) * 2);
-    const float d = half_bits(dh);
-    const int base = (int) (256 * b - e0);
+template <int R>
+struct Stepper<Q4_K, R> : Geo<8, R, 256> {
+    using G = Geo<8, R, 256>;
+    struct Raw { uint4 q[G::TPL]; uint4 hd; };
+    const uint8_t * qb;
+    const uint8_t * hb;
+    uint32_t qblk, qunit, hblk;
+    int slot;
+    __device__ void init(const uint8_t * w, int64_t M, int64_t nb, int64_t g0, int rs, int lr, int slot_) {
+        slot = slot_;
+        qb = w + (uint64_t) g0 * nb * 128 + (uint64_t) lr * 16;
+        hb = w + (uint64_t) M * nb * 128 + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
+        qblk = (uint32_t) rs * 128;
+        qunit = (uint32_t) rs * 16;
+        hblk = (uint32_t) rs * 16;
+    }
+    __device__ Raw load(int64_t step) const {
+        Raw r;
+        const uint8_t * p = qb + (uint32_t) step * qblk + (uint32_t) slot * qunit;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint4 qa = load16(qb + (uint64_t) (4 * h + hf) * rs * 16);     // ql[64h + 16hf + i]
-        const uint4 qc = load16(qb + (uint64_t) (4 * h + 2 + hf) * rs * 16); // ql[64h + 32 + 16hf + i]
-        const uint4 qh = load16(qb + (uint64_t) (8 + 2 * h + hf) * rs * 16); // qh[32h + 16hf + i]
-        uint4 v[4];
-        v[0] = make_uint4((qa.x & 0x0F0F0F0Fu) | ((qh.x << 4) & 0x30303030u), (qa.y & 0x0F0F0F0Fu) | ((qh.y << 4) & 0x30303030u),
-                          (qa.z & 0x0F0F0F0Fu) | ((qh.z << 4) & 0x30303030u), (qa.w & 0x0F0F0F0Fu) | ((qh.w << 4) & 0x30303030u));
-        v[1] = make_uint4((qc.x & 0x0F0F0F0Fu) | ((qh.x << 2) & 0x30303030u), (qc.y & 0x0F0F0F0Fu) | ((qh.y << 2) & 0x30303030u),
-                          (qc.z & 0x0F0F0F0Fu) | ((qh.z << 2) & 0x30303030u), (qc.w & 0x0F0F0F0Fu) | ((qh.w << 2) & 0x30303030u));
-        v[2] = make_uint4(((qa.x >> 4) & 0x0F0F0F0Fu) | (qh.x & 0x30303030u), ((qa.y >> 4) & 0x0F0F0F0Fu) | (qh.y & 0x30303030u),
-                          ((qa.z >> 4) & 0x0F0F0F0Fu) | (qh.z & 0x30303030u), ((qa.w >> 4) & 0x0F0F0F0Fu) | (qh.w & 0x30303030u));
-        v[3] = make_uint4(((qc.x >> 4) & 0x0F0F0F0Fu) | ((qh.x >> 2) & 0x30303030u), ((qc.y >> 4) & 0x0F0F0F0Fu) | ((qh.y >> 2) & 0x30303030u),
-                          ((qc.z >> 4) & 0x0F0F0F0Fu) | ((qh.z >> 2) & 0x30303030u), ((qc.w >> 4) & 0x0F0F0F0Fu) | ((qh.w >> 2) & 0x30303030u));
+        for (int t = 0; t < G::TPL; ++t) r.q[t] = load16(p + (uint32_t) (G::S * t) * qunit);
+        r.hd = load16(hb + (uint32_t) step * hblk);
+        return r;
+    }
+    template <int NC>
+    __device__ void compute(const Raw & r, int64_t step, int64_t kc0, const XSeg * xq, const float2 * xf, int nseg, float * acc) const {
+        const float d = half_bits(r.hd.x), dmin = half_bits(r.hd.x >> 16);
+        const int sg0 = (int) ((step * 256 - kc0) >> 4);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            // scale byte 8h + 2r + hf, stored xor 0x80
-            const int si = 8 * h + 2 * r + hf;
-            const float sc = (float) (int8_t) (byte_of(scv, si) ^ 0x80u);
-            const float ds = d * sc;
-            const int off = base + 128 * h + 32 * r + 16 * hf;
+        for (int t = 0; t < G::TPL; ++t) {
+            const int j = slot + G::S * t; // unit: bytes 16j..16j+15 of the 128 quant bytes
+            const int c = j >> 1, h = j & 1;
+            float sc0, m0, sc1, m1;
+            k4_scale_min(r.hd, 2 * c, sc0, m0);
+            k4_scale_min(r.hd, 2 * c + 1, sc1, m1);
+            const float dl = d * sc0, dh = d * sc1, ml = dmin * m0, mh = dmin * m1;
+            const uint4 lo = mask4(r.q[t], 0x0F0F0F0Fu), hi = mask4(shr4(r.q[t], 4), 0x0F0F0F0Fu);
+            const int sg = sg0 + 4 * c + h; // lo elements 64c + 16h + i, hi 32 further
 #pragma unroll
             for (int n = 0; n < NC; ++n) {
-                const float t = dot16(v[r], xs + n * xlen + off) - 32.0f * ss[n * nseg + off / 16];
-                acc[n] = fmaf(ds, t, acc[n]);
+                const int g = n * nseg + sg;
+                const float2 fl = xf[g], fh = xf[g + 2];
+                float a = acc[n];
+                a = fmaf(dl * fl.x, (float) dot16i(lo, xq[g]), a);
+                a = fmaf(dh * fh.x, (float) dot16i(hi, xq[g + 2]), a);
+                a = fmaf(-ml, fl.y, a);
+                a = fmaf(-mh, fh.y, a);
+                acc[n] = a;
             }
         }
     }
-}
+};
 
-template <int DT, int NC>
-__global__ __launch_bounds__(kThreads) void k_matvec(MvLaunch L) {
-    extern __shared__ float lds[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int row = lane & 31, hf = lane >> 5;
-    const int64_t gi = blockIdx.x / L.ksplit;
-    const int part = (int) (blockIdx.x % L.ksplit);
-    const int64_t sl = blockIdx.y;
-    const int64_t i2 = sl % L.a.ne12, i3 = sl / L.a.ne12;
-    const uint8_t * w = L.a.w + (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
-    const float * x = L.a.x + i2 * L.a.x_s2 + i3 * L.a.x_s3;
-    const int64_t g0 = gi * 32;
-    const int rs = (int) min<int64_t>(32, L.a.M - g0);
-    const int64_t s0 = part * L.per_part;
-    const int64_t s1 = min<int64_t>(L.steps, s0 + L.per_part);
-    const int64_t e0 = s0 * L.elems_step;
-    const int64_t e1 = min<int64_t>(L.a.K, s1 * L.elems_step);
-    const int xlen = (int) (e1 - e0);
-    const int nseg = xlen / 16;
-    float * xs = lds;
-    float * ss = lds + NC * xlen;
-
-    // stage x[e0, e1) of every column, then the sums of 16 consecutive values
-    for (int i = tid; i < NC * xlen; i += kThreads) {
-        const int n = i / xlen, e = i - n * xlen;
-        xs[i] = x[n * L.a.x_s1 + e0 + e];
+template <int R>
+struct Stepper<Q6_K, R> : Geo<4, R, 256> {
+    using G = Geo<4, R, 256>;
+    struct Raw { uint4 qa[G::TPL], qc[G::TPL], qh[G::TPL]; uint4 sc; uint32_t d; };
+    const uint8_t * qb;
+    const uint8_t * sb;
+    const uint8_t * db;
+    uint32_t qblk, qunit, sblk, dblk;
+    int64_t nb;
+    int slot;
+    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int slot_) {
+        nb = nb_;
+        slot = slot_;
+        qb = w + (uint64_t) g0 * nb * 192 + (uint64_t) lr * 16;
+        sb = w + (uint64_t) M * nb * 192 + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
+        db = w + (uint64_t) M * nb * 208 + (uint64_t) g0 * nb * 2 + (uint64_t) lr * 2;
+        qblk = (uint32_t) rs * 192;
+        qunit = (uint32_t) rs * 16;
+        sblk = (uint32_t) rs * 16;
+        dblk = (uint32_t) rs * 2;
     }
-    __syncthreads();
-    for (int i = tid; i < NC * nseg; i += kThreads) {
-        const int n = i / nseg, sg = i - n * nseg;
-        const float4 * p = reinterpret_cast<const float4 *>(xs + n * xlen + 16 * sg);
-        const float4 a = p[0], b = p[1], c = p[2], e = p[3];
-        ss[i] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)) + (((c.x + c.y) + (c.z + c.w)) + ((e.x + e.y) + (e.z + e.w)));
-    }
-    __syncthreads();
-
-    float acc[NC];
+    // task k = 0..3: h = k >> 1 (half of the block), hf = k & 1 (16-element half of each 32-run)
+    __device__ int task(int t) const { return (slot + G::S * t) % 4; }
+    __device__ int64_t block(int64_t step) const { return step * G::BPS + (G::BPS > 1 ? slot / 4 : 0); }
+    __device__ Raw load(int64_t step) const {
+        Raw r{};
+        const int64_t b = block(step);
+        if (G::BPS > 1 && b >= nb) return r;
+        const uint8_t * p = qb + (uint32_t) b * qblk;
 #pragma unroll
-    for (int n = 0; n < NC; ++n) acc[n] = 0.0f;
-    if (row < rs) {
-        for (int64_t s = s0 + wave; s < s1; s += kWaves) {
-            if (DT == Q4_0) step_q4_0<NC>(L, w, g0, rs, row, hf, s, e0, xs, xlen, ss, nseg, acc);
-            if (DT == Q8_0) step_q8_0<NC>(L, w, g0, rs, row, hf, s, e0, xs, xlen, ss, nseg, acc);
-            if (DT == Q4_K) step_q4_k<NC>(L, w, g0, rs, row, hf, s, e0, xs, xlen, ss, nseg, acc);
-            if (DT == Q6_K) step_q6_k<NC>(L, w, g0, rs, row, hf, s, e0, xs, xlen, ss, nseg, acc);
+        for (int t = 0; t < G::TPL; ++t) {
+            const int k = task(t), h = k >> 1, hf = k & 1;
+            r.qa[t] = load16(p + (uint32_t) (4 * h + hf) * qunit);     // ql[64h + 16hf + i]
+            r.qc[t] = load16(p + (uint32_t) (4 * h + 2 + hf) * qunit); // ql[64h + 32 + 16hf + i]
+            r.qh[t] = load16(p + (uint32_t) (8 + 2 * h + hf) * qunit); // qh[32h + 16hf + i]
+        }
+        r.sc = load16(sb + (uint32_t) b * sblk);
+        r.d = *reinterpret_cast<const uint16_t *>(db + (uint32_t) b * dblk);
+        return r;
+    }
+    template <int NC>
+    __device__ void compute(const Raw & r, int64_t step, int64_t kc0, const XSeg * xq, const float2 * xf, int nseg, float * acc) const {
+        const int64_t b = block(step);
+        if (G::BPS > 1 && b >= nb) return;
+        const float d = half_bits(r.d);
+        const int sg0 = (int) ((b * 256 - kc0) >> 4);
+#pragma unroll
+        for (int t = 0; t < G::TPL; ++t) {
+            const int k = task(t), h = k >> 1, hf = k & 1;
+            const uint4 qa = r.qa[t], qc = r.qc[t], qh = r.qh[t];
+            uint4 v[4];
+            v[0] = make_uint4((qa.x & 0x0F0F0F0Fu) | ((qh.x << 4) & 0x30303030u), (qa.y & 0x0F0F0F0Fu) | ((qh.y << 4) & 0x30303030u),
+                              (qa.z & 0x0F0F0F0Fu) | ((qh.z << 4) & 0x30303030u), (qa.w & 0x0F0F0F0Fu) | ((qh.w << 4) & 0x30303030u));
+            v[1] = make_uint4((qc.x & 0x0F0F0F0Fu) | ((qh.x << 2) & 0x30303030u), (qc.y & 0x0F0F0F0Fu) | ((qh.y << 2) & 0x30303030u),
+                              (qc.z & 0x0F0F0F0Fu) | ((qh.z << 2) & 0x30303030u), (qc.w & 0x0F0F0F0Fu) | ((qh.w << 2) & 0x30303030u));
+            v[2] = make_uint4(((qa.x >> 4) & 0x0F0F0F0Fu) | (qh.x & 0x30303030u), ((qa.y >> 4) & 0x0F0F0F0Fu) | (qh.y & 0x30303030u),
+                              ((qa.z >> 4) & 0x0F0F0F0Fu) | (qh.z & 0x30303030u), ((qa.w >> 4) & 0x0F0F0F0Fu) | (qh.w & 0x30303030u));
+            v[3] = make_uint4(((qc.x >> 4) & 0x0F0F0F0Fu) | ((qh.x >> 2) & 0x30303030u), ((qc.y >> 4) & 0x0F0F0F0Fu) | ((qh.y >> 2) & 0x30303030u),
+                              ((qc.z >> 4) & 0x0F0F0F0Fu) | ((qh.z >> 2) & 0x30303030u), ((qc.w >> 4) & 0x0F0F0F0Fu) | ((qh.w >> 2) & 0x30303030u));
+            // scale byte 8h + 2rr + hf (stored xor 0x80): the 4 bytes for rr = 0..3 are
+            // s[8h + hf], s[8h + hf + 2], ... -> word h*2 + (hf? odd bytes) of sc
+            const uint32_t sw0 = h ? r.sc.z : r.sc.x, sw1 = h ? r.sc.w : r.sc.y; // bytes 8h..8h+3, 8h+4..8h+7
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const uint32_t sw = rr < 2 ? sw0 : sw1;
+                const int bi = 2 * (rr & 1) + hf;
+                const float ds = d * (float) (int8_t) (((sw >> (8 * bi)) & 0xFFu) ^ 0x80u);
+                const int sg = sg0 + 8 * h + 2 * rr + hf; // elements 128h + 32rr + 16hf + i
+#pragma unroll
+                for (int n = 0; n < NC; ++n) {
+                    const int g = n * nseg + sg;
+                    const float2 f = xf[g];
+                    float a = acc[n];
+                    a = fmaf(ds * f.x, (float) dot16i(v[rr], xq[g]), a);
+                    a = fmaf(-32.0f * ds, f.y, a);
+                    acc[n] = a;
+                }
+            }
         }
     }
-    // the two halves of a wave hold the same rows
-#pragma unroll
-    for (int n = 0; n < NC; ++n) acc[n] += __shfl_xor(acc[n], 32);
+};
 
-    __syncthreads(); // the x slab is reused as the reduction buffer
-    float * red = lds;
-    if (hf == 0) {
-#pragma unroll
-        for (int n = 0; n < NC; ++n) red[(wave * NC + n) * 32 + row] = acc[n];
-    }
-    __syncthreads();
-    float v = 0.0f;
-    const int n = tid >> 5, r = tid & 31;
-    if (tid < NC * 32) {
-        v = (red[(0 * NC + n) * 32 + r] + red[(1 * NC + n) * 32 + r]) + (red[(2 * NC + n) * 32 + r] + red[(3 * NC + n) * 32 + r]);
-    }
+template <int DT, int NC, int R>
+__global__ __launch_bounds__(64 * kMaxWaves) void k_matvec(MvLaunch L) {
+    using ST = Stepper<DT, R>;
+    using Raw = typename ST::Raw;
+    constexpr int S = ST::S;
+    constexpr int EPS = ST::EPS;
+    constexpr int D = ring_depth(sizeof(Raw)); // steps in flight per wave
+    extern __shared__ float lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int W = blockDim.x >> 6;
+    const int WT = L.wt;                  // waves per tile
+    const int GW = W / WT;                // tiles in flight per work-group
+    const int grp = wave / WT, wt = wave % WT;
+    const int r = lane % R, slot = lane / R;
+    const int64_t sl = blockIdx.y;
+    const int64_t i2 = sl % L.a.ne12, i3 = sl / L.a.ne12;
+    const int64_t M = L.a.M, K = L.a.K;
+    const uint8_t * w = L.a.w + (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
+    const float * x = L.a.x + i2 * L.a.x_s2 + i3 * L.a.x_s3;
     float * y = L.a.y + i2 * L.a.y_s2 + i3 * L.a.y_s3;
-    if (L.ksplit == 1) {
-        if (tid < NC * 32 && r < rs) y[n * L.a.y_s1 + g0 + r] = v;
-        return;
+    // tiles of this work-group: iteration it, group g -> tile (it * gridDim.x + blockIdx.x) * GW + g
+    const int64_t per_iter = (int64_t) gridDim.x * GW;
+    const int64_t iters = (L.tiles + per_iter - 1) / per_iter;
+    auto tile_of = [&](int64_t it) { return (it * gridDim.x + blockIdx.x) * GW + grp; };
+    // the lane's addressing for the tile of iteration it (live: its row exists)
+    auto stepper_of = [&](int64_t it, ST & st) -> bool {
+        const int64_t tile = tile_of(it);
+        const int64_t m0 = tile * R;
+        if (tile >= L.tiles || m0 + r >= M) return false;
+        const int64_t g0 = m0 & ~(int64_t) 31;
+        st.init(w, M, L.a.nb, g0, (int) min<int64_t>(32, M - g0), (int) (m0 - g0) + r, slot);
+        return true;
+    };
+
+    Raw ring[D];
+    ST cur, nxt;
+
+    for (int64_t kc0 = 0; kc0 < K; kc0 += L.kc) {
+        const int xlen = (int) min<int64_t>(L.kc, K - kc0);
+        const int64_t st0 = kc0 / EPS;
+        const int nst = (int) ((kc0 + xlen + EPS - 1) / EPS - st0); // steps of this chunk
+        const int nw = wt < nst ? (nst - wt + WT - 1) / WT : 0;      // this wave's steps per tile
+        const int nwp = (nw + D - 1) / D * D;                        // padded to whole ring turns
+        bool live = stepper_of(0, cur);
+        bool live_n = stepper_of(1, nxt);
+        // weight loads first: they do not depend on x and overlap the staging below
+        if (live) {
+#pragma unroll
+            for (int j = 0; j < D; ++j)
+                if (j < nw) ring[j] = cur.load(st0 + wt + (int64_t) WT * j);
+        }
+
+        const int nseg = xlen / 16;
+        XSeg * xq = reinterpret_cast<XSeg *>(lds);
+        float2 * xf = reinterpret_cast<float2 *>(xq + NC * nseg);
+        float * red = reinterpret_cast<float *>(xf + NC * nseg); // [2][W][NC][R]
+        __syncthreads(); // the previous chunk is consumed
+        // one thread per (column, segment): two int8 planes, the plane scale and the plain sum
+        for (int i = tid; i < NC * nseg; i += blockDim.x) {
+            const int n = i / nseg, sg = i - n * nseg;
+            const float * xp = x + n * L.a.x_s1 + kc0 + 16 * sg;
+            float v[16];
+            float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                v[e] = xp[e];
+                amax = fmaxf(amax, fabsf(v[e]));
+                sum += v[e];
+            }
+            const float s1 = amax * (1.0f / 127.0f);
+            const float inv1 = amax > 0.0f ? 127.0f / amax : 0.0f;
+            uint32_t pa[4] = {0, 0, 0, 0}, pb[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float qa = fminf(127.0f, fmaxf(-127.0f, rintf(v[e] * inv1)));
+                const float res = fmaf(-qa, s1, v[e]);
+                const float qb = fminf(127.0f, fmaxf(-127.0f, rintf(res * (256.0f * inv1))));
+                pa[e >> 2] |= ((uint32_t) (int) qa & 0xFFu) << (8 * (e & 3));
+                pb[e >> 2] |= ((uint32_t) (int) qb & 0xFFu) << (8 * (e & 3));
+            }
+            XSeg xs_;
+            xs_.a = make_uint4(pa[0], pa[1], pa[2], pa[3]);
+            xs_.b = make_uint4(pb[0], pb[1], pb[2], pb[3]);
+            xq[i] = xs_;
+            xf[i] = make_float2(s1 * (1.0f / 256.0f), sum);
+        }
+        __syncthreads();
+
+        for (int64_t it = 0; it < iters; ++it) {
+            float acc[NC];
+#pragma unroll
+            for (int n = 0; n < NC; ++n) acc[n] = 0.0f;
+            for (int i = 0; i < nwp; i += D) {
+#pragma unroll
+                for (int j = 0; j < D; ++j) {
+                    const int ii = i + j;
+                    if (live && ii < nw) cur.template compute<NC>(ring[j], st0 + wt + (int64_t) WT * ii, kc0, xq, xf, nseg, acc);
+                    // refill this ring slot with the item D ahead (possibly of the next tile)
+                    const int ni = ii + D;
+                    if (ni < nwp) {
+                        if (live && ni < nw) ring[j] = cur.load(st0 + wt + (int64_t) WT * ni);
+                    } else if (live_n && ni - nwp < nw) {
+                        ring[j] = nxt.load(st0 + wt + (int64_t) WT * (ni - nwp));
+                    }
+                }
+            }
+            // slots of a row: lanes r, r + R, ... (fixed butterfly order)
+#pragma unroll
+            for (int off = R; off < 64; off <<= 1) {
+#pragma unroll
+                for (int n = 0; n < NC; ++n) acc[n] += __shfl_xor(acc[n], off);
+            }
+            float * rb = red + (it & 1) * (W * NC * R);
+            if (slot == 0) {
+#pragma unroll
+                for (int n = 0; n < NC; ++n) rb[(wave * NC + n) * R + r] = acc[n];
+            }
+            __syncthreads();
+            if (tid < GW * NC * R) {
+                const int g = tid / (NC * R), n = (tid / R) % NC, rr = tid % R;
+                const int64_t t2 = (it * gridDim.x + blockIdx.x) * GW + g;
+                const int64_t m = t2 * R + rr;
+                if (t2 < L.tiles && m < M) {
+                    float v = 0.0f;
+                    for (int w2 = 0; w2 < WT; ++w2) v += rb[((g * WT + w2) * NC + n) * R + rr];
+                    float * yp = y + n * L.a.y_s1 + m;
+                    *yp = kc0 == 0 ? v : *yp + v;
+                }
+            }
+            cur = nxt;
+            live = live_n;
+            live_n = stepper_of(it + 2, nxt);
+        }
     }
-    const int64_t slot = sl * L.groups + gi;
-    float * mine = L.partials + ((uint64_t) slot * L.ksplit + part) * (NC * 32);
-    if (tid < NC * 32) mine[tid] = v;
-    __threadfence();
-    __syncthreads();
-    __shared__ int last;
-    if (tid == 0) {
-        const uint32_t seen = __hip_atomic_fetch_add(L.counters + slot, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last = seen == (uint32_t) (L.ksplit - 1);
-        if (last) __hip_atomic_store(L.counters + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int DT, int R>
+void * pick_nc(int nc) {
+    switch (nc) {
+        case 1: return (void *) k_matvec<DT, 1, R>;
+        case 2: return (void *) k_matvec<DT, 2, R>;
+        case 3: return (void *) k_matvec<DT, 3, R>;
+        case 4: return (void *) k_matvec<DT, 4, R>;
+        case 5: return (void *) k_matvec<DT, 5, R>;
+        case 6: return (void *) k_matvec<DT, 6, R>;
+        case 7: return (void *) k_matvec<DT, 7, R>;
+        default: return (void *) k_matvec<DT, 8, R>;
     }
-    __syncthreads();
-    if (!last || tid >= NC * 32 || r >= rs) return;
-    const float * parts = L.partials + (uint64_t) slot * L.ksplit * (NC * 32);
-    float t = 0.0f;
-    for (int p = 0; p < L.ksplit; ++p) {
-        t += __hip_atomic_load(parts + (uint64_t) p * (NC * 32) + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    y[n * L.a.y_s1 + g0 + r] = t;
 }
 
 template <int DT>
-void * pick(int nc) {
-    switch (nc) {
-        case 1: return (void *) k_matvec<DT, 1>;
-        case 2: return (void *) k_matvec<DT, 2>;
-        case 3: return (void *) k_matvec<DT, 3>;
-        case 4: return (void *) k_matvec<DT, 4>;
-        case 5: return (void *) k_matvec<DT, 5>;
-        case 6: return (void *) k_matvec<DT, 6>;
-        case 7: return (void *) k_matvec<DT, 7>;
-        default: return (void *) k_matvec<DT, 8>;
-    }
+void * pick(int nc, int R) {
+    return R == 32 ? pick_nc<DT, 32>(nc) : R == 16 ? pick_nc<DT, 16>(nc) : pick_nc<DT, 8>(nc);
 }
 
 const char * name_of(int dt) {
@@ -318,51 +514,106 @@ const char * name_of(int dt) {
     }
 }
 
+// tuning overrides from the environment (read once; 0 / unset = automatic)
+int tuning(const char * name, int dflt) {
+    const char * v = std::getenv(name);
+    return v != nullptr && *v ? std::atoi(v) : dflt;
+}
+
+// resident work-groups per CU of a kernel at a block size and dynamic LDS (cached per thread)
+int occupancy(void * fn, int threads, size_t lds) {
+    struct Key {
+        void * fn;
+        size_t lds;
+        int n;
+    };
+    thread_local std::vector<Key> cache;
+    for (const Key & k : cache)
+        if (k.fn == fn && k.lds == lds) return k.n;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess || n < 1) n = 1;
+    cache.push_back({fn, lds, n});
+    return n;
+}
+
+int tasks_of(int dt) {
+    return dt == Q4_0 ? 1 : dt == Q8_0 ? 2 : dt == Q4_K ? 8 : 4;
+}
+
+template <int R>
+size_t raw_bytes_r(int dt) {
+    return dt == Q4_0 ? sizeof(typename Stepper<Q4_0, R>::Raw) : dt == Q8_0 ? sizeof(typename Stepper<Q8_0, R>::Raw)
+         : dt == Q4_K ? sizeof(typename Stepper<Q4_K, R>::Raw) : sizeof(typename Stepper<Q6_K, R>::Raw);
+}
+
+size_t raw_bytes_of(int dt, int R) {
+    return R == 32 ? raw_bytes_r<32>(dt) : R == 16 ? raw_bytes_r<16>(dt) : raw_bytes_r<8>(dt);
+}
+
 } // namespace
 
-hipError_t launch_matvec(const MatArgs & a, const Scratch & s, int cu_count, hipStream_t stream, const char ** kernel_name,
+hipError_t launch_matvec(const MatArgs & a, int cu_count, hipStream_t stream, const char ** kernel_name,
                          uint64_t * grid_size) {
     const int nc = (int) a.N;
     if (nc < 1 || nc > 8) return hipErrorInvalidValue;
+    const int64_t slices = a.ne12 * a.ne13;
+    if (slices > 65535) return hipErrorInvalidValue;
+    const int T = tasks_of(a.dtype);
+    const int be = a.dtype == Q4_K || a.dtype == Q6_K ? 256 : 32;
+    // x chunk: as much of K as fits the LDS budget, in whole steps (of the smallest row tile)
+    const int eps_max = (64 / 8 > T ? 64 / 8 / T : 1) * be;
+    const int64_t max_kc = std::max<int64_t>(eps_max, (int64_t) (kLdsBudget / (3 * nc)) / eps_max * eps_max); // 2 B + 8/16 B per element
     MvLaunch L;
     L.a = a;
-    L.groups = (a.M + 31) / 32;
-    L.elems_step = a.dtype == Q4_0 ? 64 : a.dtype == Q8_0 ? 32 : 256;
-    L.steps = a.dtype == Q4_0 ? (a.nb + 1) / 2 : a.nb;
-    const int64_t slices = a.ne12 * a.ne13;
-    // enough work-groups for ~8 per CU, at least 4 steps (one per wave) per work-group, and an x
-    // slab that fits the LDS budget
-    const int64_t want = (int64_t) cu_count * 8;
-    int64_t ksplit = 1;
-    if (L.groups * slices < want) ksplit = (want + L.groups * slices - 1) / (L.groups * slices);
-    ksplit = std::min<int64_t>(ksplit, std::max<int64_t>(1, L.steps / kWaves));
-    const int64_t max_xlen = kLdsFloats / (nc + 1) / L.elems_step * L.elems_step;
-    const int64_t min_split = (a.K + max_xlen - 1) / max_xlen;
-    ksplit = std::max(ksplit, min_split);
-    L.per_part = (L.steps + ksplit - 1) / ksplit;
-    L.ksplit = (int) ((L.steps + L.per_part - 1) / L.per_part);
-    if (L.ksplit > 1) {
-        const uint64_t need_p = (uint64_t) L.groups * slices * L.ksplit * nc * 32;
-        const uint64_t need_c = (uint64_t) L.groups * slices;
-        if (need_p > s.partial_floats || need_c > s.counter_count) return hipErrorOutOfMemory;
+    L.kc = std::min<int64_t>(a.K, max_kc);
+    // persistent grid: as many 8-wave work-groups as stay resident (occupancy of the chosen kernel
+    // with its LDS; SCRAPGPU_HIP_MV_WGS overrides the per-CU count), shared among the slices
+    const int waves = kMaxWaves;
+    auto pick_fn = [&](int R) -> void * {
+        switch (a.dtype) {
+            case Q4_0: return pick<Q4_0>(nc, R);
+            case Q8_0: return pick<Q8_0>(nc, R);
+            case Q4_K: return pick<Q4_K>(nc, R);
+            case Q6_K: return pick<Q6_K>(nc, R);
+            default: return nullptr;
+        }
+    };
+    auto lds_of = [&](int R) { return (size_t) nc * (L.kc / 16) * (32 + 8) + (size_t) 2 * waves * nc * R * sizeof(float); };
+    auto resident = [&](int R) -> int64_t {
+        int per_cu = tuning("SCRAPGPU_HIP_MV_WGS", 0);
+        if (per_cu <= 0) per_cu = occupancy(pick_fn(R), 64 * waves, lds_of(R));
+        return std::max<int64_t>(1, (int64_t) std::max(1, per_cu) * cu_count / slices);
+    };
+    // row tile: the largest (32, 16, 8) that still gives every wave group >= 2 tiles; the waves of
+    // a group split the K steps while each keeps >= 2 ring turns
+    int R = 8, WT = 1;
+    int64_t wgs = 1;
+    for (int cand : {32, 16, 8}) {
+        const int S = 64 / cand;
+        const int eps = (S > T ? S / T : 1) * be;
+        const int D = ring_depth(raw_bytes_of(a.dtype, cand));
+        const int64_t nst = (L.kc + eps - 1) / eps;
+        int wt = 1;
+        while (wt < waves && nst % (2 * wt) == 0 && (nst / (2 * wt)) % D == 0 && nst / (2 * wt) >= 2 * D) wt *= 2;
+        const int64_t tiles = (a.M + cand - 1) / cand;
+        R = cand;
+        WT = wt;
+        wgs = resident(cand);
+        if (tiles >= 2 * wgs * (waves / wt)) break;
     }
-    L.partials = s.partials;
-    L.counters = s.counters;
-    const int64_t xlen = std::min<int64_t>(a.K, L.per_part * L.elems_step);
-    const size_t lds = (size_t) std::max<int64_t>(nc * xlen + nc * (xlen / 16), kWaves * nc * 32) * sizeof(float);
-    void * fn = nullptr;
-    switch (a.dtype) {
-        case Q4_0: fn = pick<Q4_0>(nc); break;
-        case Q8_0: fn = pick<Q8_0>(nc); break;
-        case Q4_K: fn = pick<Q4_K>(nc); break;
-        case Q6_K: fn = pick<Q6_K>(nc); break;
-        default: return hipErrorInvalidValue;
-    }
-    const dim3 grid((unsigned) (L.groups * L.ksplit), (unsigned) slices, 1);
+    if (const int fr = tuning("SCRAPGPU_HIP_MV_R", 0)) R = fr;
+    if (const int fw = tuning("SCRAPGPU_HIP_MV_WT", 0)) WT = fw;
+    L.tiles = (a.M + R - 1) / R;
+    L.wt = WT;
+    wgs = resident(R);
+    const int64_t grid_x = std::max<int64_t>(1, std::min<int64_t>(wgs, (L.tiles + (waves / WT) - 1) / (waves / WT)));
+    const size_t lds = lds_of(R);
+    void * fn = pick_fn(R);
+    if (fn == nullptr) return hipErrorInvalidValue;
     if (kernel_name) *kernel_name = name_of(a.dtype);
-    if (grid_size) *grid_size = (uint64_t) grid.x * grid.y;
+    if (grid_size) *grid_size = (uint64_t) grid_x * (uint64_t) slices;
     void * args[] = {&L};
-    return hipLaunchKernel(fn, grid, dim3(kThreads), args, lds, stream);
+    return hipLaunchKernel(fn, dim3((unsigned) grid_x, (unsigned) slices), dim3((unsigned) (64 * waves)), args, lds, stream);
 }
 
 } // namespace sgk
