@@ -74,6 +74,8 @@ struct Stream {
     scrapgpu_object_header hdr;
     Device * dev;
     hipStream_t s;
+    uint8_t * scratch = nullptr; // bf16 activations of the prefill matmul (grown on demand)
+    size_t scratch_size = 0;
 };
 
 struct Device {
@@ -374,6 +376,7 @@ scrapgpu_status api_stream_free(scrapgpu_stream_t * stream) {
     if (s == nullptr) return invalid("not a hip stream");
     use(s->dev);
     hipStreamSynchronize(s->s);
+    if (s->scratch) hipFree(s->scratch);
     hipStreamDestroy(s->s);
     delete s;
     return SCRAPGPU_STATUS_OK;
@@ -384,6 +387,19 @@ scrapgpu_status api_stream_sync(scrapgpu_stream_t * stream) {
     if (s == nullptr) return invalid("not a hip stream");
     SG_HIP(use(s->dev), "hipSetDevice");
     SG_HIP(hipStreamSynchronize(s->s), "kernel execution failed (reported at stream_sync)");
+    return SCRAPGPU_STATUS_OK;
+}
+
+// stream scratch: grown on demand; the stream is drained before the old block is released
+scrapgpu_status ensure_scratch(Stream * s, size_t bytes) {
+    if (bytes <= s->scratch_size) return SCRAPGPU_STATUS_OK;
+    SG_HIP(hipStreamSynchronize(s->s), "hipStreamSynchronize");
+    if (s->scratch) hipFree(s->scratch);
+    s->scratch = nullptr;
+    s->scratch_size = 0;
+    const size_t n = std::max(bytes, (size_t) 16 << 20);
+    SG_HIP(hipMalloc(reinterpret_cast<void **>(&s->scratch), n), "hipMalloc (stream scratch)");
+    s->scratch_size = n;
     return SCRAPGPU_STATUS_OK;
 }
 
@@ -589,9 +605,11 @@ scrapgpu_status run_product(Stream * s, sgk::MatArgs a) {
         prof.done(name, weight_bytes(a), 2.0 * (double) a.M * (double) a.K * (double) a.N * (double) (a.ne12 * a.ne13));
         return SCRAPGPU_STATUS_OK;
     }
+    const scrapgpu_status st = ensure_scratch(s, sgk::matmul_scratch_bytes(a));
+    if (st != SCRAPGPU_STATUS_OK) return st;
     ProfScope prof(s->s);
     const char * name = nullptr;
-    SG_HIP(sgk::launch_matmul_mfma(a, cus, s->s, &name), "matmul launch");
+    SG_HIP(sgk::launch_matmul_mfma(a, reinterpret_cast<uint16_t *>(s->scratch), cus, s->s, &name), "matmul launch");
     prof.done(name, weight_bytes(a), 2.0 * (double) a.M * (double) a.K * (double) a.N * (double) (a.ne12 * a.ne13));
     return SCRAPGPU_STATUS_OK;
 }
