@@ -8,6 +8,7 @@
 // (N <= 8: decode matvec; N > 8: bf16 MFMA prefill).
 #include "scrapgpu/hip.h"
 
+#include "../core/registry_internal.h"
 #include "../core/tensor_math.h"
 #include "kernels.h"
 
@@ -804,7 +805,12 @@ extern "C" {
 scrapgpu_status scrapgpu_hip_register(void) {
     Registry & r = registry();
     std::lock_guard<std::mutex> lock(r.mu);
-    if (r.registered) return SCRAPGPU_STATUS_OK;
+    if (r.registered) {
+        // the devices are probed once; the vtable is registered again after
+        // scrapgpu_unregister_all_backends()
+        if (sg_registry_contains(api_device_count)) return SCRAPGPU_STATUS_OK;
+        return scrapgpu_register_backend(&kVtable);
+    }
     int n = 0;
     const hipError_t e = hipGetDeviceCount(&n);
     if (e != hipSuccess && e != hipErrorNoDevice) return hip_fail(e, "hipGetDeviceCount");
