@@ -56,7 +56,7 @@ def weight_bytes(dtype, K, M):
 class Model:
     """36 layers of R32 weights plus the activation / output vectors, all resident in HBM."""
 
-    def __init__(self, dev, st, layers):
+    def __init__(self, dev, st, layers, fuse=True):
         self.dev, self.st = dev, st
         self.bufs = []
         tmp = dev.alloc(4 * FFN * HIDDEN)
@@ -88,10 +88,16 @@ class Model:
         self.keep = []
         nodes = []
         for row in self.weights:
-            for name, dt, K, M, q in row:
-                x = self.xf if K == FFN else self.xh
-                y = sg.tdesc(sg.F32, (M, 1), self.y_bufs[name])
-                op, keep = sg.mul_mat_op(q, x, y)
+            by = {name: (q, sg.tdesc(sg.F32, (M, 1), self.y_bufs[name])) for name, dt, K, M, q in row}
+            # the decode step of one layer as the reference's ggml adapter issues it: q/k/v and
+            # gate/up each share x (MUL_MAT_MULTI), o and down are single MUL_MATs
+            groups = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)] if fuse else [(n,) for n, *_ in LAYER_SHAPES]
+            for g in groups:
+                x = self.xf if g[0] == "down" else self.xh
+                if len(g) == 1:
+                    op, keep = sg.mul_mat_op(by[g[0]][0], x, by[g[0]][1])
+                else:
+                    op, keep = sg.multi_op([by[n][0] for n in g], x, [by[n][1] for n in g])
                 self.keep.append((op, keep))
                 nodes.append(sg.PlanNode(C.sizeof(sg.PlanNode), op, 0))
         self.nodes = (sg.PlanNode * len(nodes))(*nodes)
@@ -194,6 +200,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-fuse", action="store_true", help="one MUL_MAT per weight instead of MUL_MAT_MULTI for q/k/v and gate/up")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one MI355X per run); use --gpus 1",
@@ -204,7 +211,7 @@ def main():
     st = dev.stream()
     info = dev.info()
     log("device:", info.name.decode(), info.compute_units, "CUs")
-    model = Model(dev, st, args.layers)
+    model = Model(dev, st, args.layers, fuse=not args.no_fuse)
     for _ in range(args.warmup):
         model.token()
     st.sync()
@@ -241,7 +248,8 @@ def main():
         "vs_baseline": None,
         "dtype": "q4_k/q6_k weights, f32 activations and accumulate",
         "data": "synthetic: weights ~N(0,0.02) quantized on device (bit-identical to the reference quantizer), x ~N(0,1)",
-        "config": {"workload": f"Qwen3-8B Q4_K_M decode token: {args.layers} layers x 7 matvecs (q,k,v,o,gate,up in Q4_K; down in Q6_K), bs=1",
+        "config": {"workload": f"Qwen3-8B Q4_K_M decode token: {args.layers} layers x 7 matvecs (q,k,v,o,gate,up in Q4_K; down in Q6_K), bs=1"
+                               + ("; q/k/v and gate/up as MUL_MAT_MULTI" if not args.no_fuse else ""),
                    "weight_bytes_per_token": model.bytes_per_token, "parallelism": "single GPU"},
         "tokens_per_s_equiv": round(1e3 / ms_step, 1),
         "kernel_sum_ms_per_token": round(ktime, 4),

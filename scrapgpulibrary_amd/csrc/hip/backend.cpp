@@ -77,7 +77,10 @@ struct Stream {
     hipStream_t s;
     uint8_t * scratch = nullptr; // bf16 activations of the prefill matmul (grown on demand)
     size_t scratch_size = 0;
+    uint64_t scratch_gen = 0;    // process-unique; renewed on every re-allocation (keys recorded graphs)
 };
+
+std::atomic<uint64_t> g_scratch_gen{1};
 
 struct Device {
     scrapgpu_object_header hdr;
@@ -102,6 +105,11 @@ struct Plan {
     Device * dev;
     std::vector<PlanNode> nodes;
     std::vector<Buffer *> buffers;
+    // the launches of all nodes recorded once as a HIP graph and replayed (per stream: the
+    // kernels use the recording stream's scratch)
+    hipGraphExec_t exec = nullptr;
+    Stream * exec_stream = nullptr;
+    uint64_t exec_gen = 0;
 };
 
 struct Registry {
@@ -368,6 +376,7 @@ scrapgpu_status api_stream_create(scrapgpu_device_t * device, scrapgpu_stream_t 
     s->hdr.backend = &kVtable;
     s->dev = d;
     s->s = hs;
+    s->scratch_gen = g_scratch_gen.fetch_add(1);
     *out = reinterpret_cast<scrapgpu_stream_t *>(s);
     return SCRAPGPU_STATUS_OK;
 }
@@ -401,6 +410,7 @@ scrapgpu_status ensure_scratch(Stream * s, size_t bytes) {
     const size_t n = std::max(bytes, (size_t) 16 << 20);
     SG_HIP(hipMalloc(reinterpret_cast<void **>(&s->scratch), n), "hipMalloc (stream scratch)");
     s->scratch_size = n;
+    s->scratch_gen = g_scratch_gen.fetch_add(1);
     return SCRAPGPU_STATUS_OK;
 }
 
@@ -595,39 +605,56 @@ double weight_bytes(const sgk::MatArgs & a) {
     return (double) a.M * (double) (a.K / bs) * ts * (double) ((a.ne12 / a.r2) * (a.ne13 / a.r3));
 }
 
-// enqueues one product on the stream; pointers in `a` resolved
-scrapgpu_status run_product(Stream * s, sgk::MatArgs a) {
+// enqueues 1..3 products on the stream (pointers resolved). Products that share x with one dtype,
+// K and N <= 8 run as one fused matvec launch; anything else as one launch per product.
+scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
     const int cus = (int) s->dev->cus;
-    if (a.N <= 8) {
-        ProfScope prof(s->s);
-        const char * name = nullptr;
-        uint64_t grid = 0;
-        SG_HIP(sgk::launch_matvec(a, cus, s->s, &name, &grid), "matvec launch");
-        prof.done(name, weight_bytes(a), 2.0 * (double) a.M * (double) a.K * (double) a.N * (double) (a.ne12 * a.ne13));
-        return SCRAPGPU_STATUS_OK;
+    bool fuse = n > 1 && mats[0].N <= 8;
+    for (int j = 1; j < n && fuse; ++j) {
+        fuse = mats[j].dtype == mats[0].dtype && mats[j].K == mats[0].K && mats[j].x == mats[0].x &&
+               mats[j].ne12 * mats[j].ne13 == 1 && mats[0].ne12 * mats[0].ne13 == 1;
     }
-    const scrapgpu_status st = ensure_scratch(s, sgk::matmul_scratch_bytes(a));
-    if (st != SCRAPGPU_STATUS_OK) return st;
-    ProfScope prof(s->s);
-    const char * name = nullptr;
-    SG_HIP(sgk::launch_matmul_mfma(a, reinterpret_cast<uint16_t *>(s->scratch), cus, s->s, &name), "matmul launch");
-    prof.done(name, weight_bytes(a), 2.0 * (double) a.M * (double) a.K * (double) a.N * (double) (a.ne12 * a.ne13));
+    const int groups = fuse ? 1 : n;
+    for (int gi = 0; gi < groups; ++gi) {
+        const sgk::MatArgs * m = fuse ? mats : mats + gi;
+        const int cnt = fuse ? n : 1;
+        double bytes = 0, flops = 0;
+        for (int j = 0; j < cnt; ++j) {
+            bytes += weight_bytes(m[j]);
+            flops += 2.0 * (double) m[j].M * (double) m[j].K * (double) m[j].N * (double) (m[j].ne12 * m[j].ne13);
+        }
+        if (m[0].N <= 8) {
+            ProfScope prof(s->s);
+            const char * name = nullptr;
+            uint64_t grid = 0;
+            SG_HIP(sgk::launch_matvec(m, cnt, cus, s->s, &name, &grid), "matvec launch");
+            prof.done(name, bytes, flops);
+        } else {
+            const scrapgpu_status st = ensure_scratch(s, sgk::matmul_scratch_bytes(m[0]));
+            if (st != SCRAPGPU_STATUS_OK) return st;
+            ProfScope prof(s->s);
+            const char * name = nullptr;
+            SG_HIP(sgk::launch_matmul_mfma(m[0], reinterpret_cast<uint16_t *>(s->scratch), cus, s->s, &name), "matmul launch");
+            prof.done(name, bytes, flops);
+        }
+    }
     return SCRAPGPU_STATUS_OK;
 }
 
-scrapgpu_status product(Stream * s, const scrapgpu_tensor_desc & w, const scrapgpu_tensor_desc & x, const scrapgpu_tensor_desc & y, int bc) {
-    sgk::MatArgs a;
-    std::memset(&a, 0, sizeof(a));
-    scrapgpu_status st = mul_mat_rule(w, x, y, bc, &a, nullptr);
+// the resolved arguments of one product W x -> y
+scrapgpu_status product_args(Stream * s, const scrapgpu_tensor_desc & w, const scrapgpu_tensor_desc & x, const scrapgpu_tensor_desc & y, int bc,
+                             sgk::MatArgs * a) {
+    std::memset(a, 0, sizeof(*a));
+    scrapgpu_status st = mul_mat_rule(w, x, y, bc, a, nullptr);
     if (st != SCRAPGPU_STATUS_OK) return st;
     uint8_t *pw, *px, *py;
     if ((st = resolve(s->dev, w, &pw, "src0")) != SCRAPGPU_STATUS_OK) return st;
     if ((st = resolve(s->dev, x, &px, "src1")) != SCRAPGPU_STATUS_OK) return st;
     if ((st = resolve(s->dev, y, &py, "dst")) != SCRAPGPU_STATUS_OK) return st;
-    a.w = pw;
-    a.x = reinterpret_cast<const float *>(px);
-    a.y = reinterpret_cast<float *>(py);
-    return run_product(s, a);
+    a->w = pw;
+    a->x = reinterpret_cast<const float *>(px);
+    a->y = reinterpret_cast<float *>(py);
+    return SCRAPGPU_STATUS_OK;
 }
 
 scrapgpu_status exec_desc(Stream * s, const scrapgpu_op_desc * desc) {
@@ -635,17 +662,19 @@ scrapgpu_status exec_desc(Stream * s, const scrapgpu_op_desc * desc) {
     scrapgpu_status st = api_supports(s->dev, desc, &reason);
     if (st != SCRAPGPU_STATUS_OK) return st;
     SG_HIP(use(s->dev), "hipSetDevice");
+    sgk::MatArgs mats[3];
     if (desc->op == SCRAPGPU_OP_MUL_MAT) {
         const auto * p = static_cast<const scrapgpu_mul_mat_params *>(desc->params);
         const int bc = p->struct_size >= offsetof(scrapgpu_mul_mat_params, allow_broadcast) + sizeof(int) ? p->allow_broadcast : 0;
-        return product(s, desc->inputs[0], desc->inputs[1], desc->outputs[0], bc);
+        st = product_args(s, desc->inputs[0], desc->inputs[1], desc->outputs[0], bc, &mats[0]);
+        return st != SCRAPGPU_STATUS_OK ? st : run_products(s, mats, 1);
     }
-    const size_t n = desc->output_count; // MUL_MAT_MULTI
+    const size_t n = desc->output_count; // MUL_MAT_MULTI: n weights sharing inputs[n]
     for (size_t i = 0; i < n; ++i) {
-        st = product(s, desc->inputs[i], desc->inputs[n], desc->outputs[i], 0);
+        st = product_args(s, desc->inputs[i], desc->inputs[n], desc->outputs[i], 0, &mats[i]);
         if (st != SCRAPGPU_STATUS_OK) return st;
     }
-    return SCRAPGPU_STATUS_OK;
+    return run_products(s, mats, (int) n);
 }
 
 scrapgpu_status api_op_execute(scrapgpu_stream_t * stream, const scrapgpu_op_desc * desc) {
@@ -708,21 +737,89 @@ scrapgpu_status api_plan_build(scrapgpu_device_t * device, const scrapgpu_plan_d
     return SCRAPGPU_STATUS_OK;
 }
 
+void plan_drop_graph(Plan * p) {
+    if (p->exec) hipGraphExecDestroy(p->exec);
+    p->exec = nullptr;
+    p->exec_stream = nullptr;
+}
+
+bool graphs_enabled() {
+    static const bool on = [] {
+        const char * v = std::getenv("SCRAPGPU_HIP_GRAPH");
+        return v == nullptr || v[0] != '0';
+    }();
+    return on;
+}
+
+// scratch every node of the plan needs on this stream (allocated before a recording: no
+// allocation or synchronization may happen while the stream records)
+scrapgpu_status plan_prepare(Stream * s, Plan * p) {
+    size_t need = 0;
+    for (PlanNode & n : p->nodes) {
+        const size_t cnt = n.op.op == SCRAPGPU_OP_MUL_MAT ? 1 : n.op.output_count;
+        for (size_t i = 0; i < cnt; ++i) {
+            sgk::MatArgs a;
+            std::memset(&a, 0, sizeof(a));
+            const scrapgpu_tensor_desc & x = n.op.op == SCRAPGPU_OP_MUL_MAT ? n.op.inputs[1] : n.op.inputs[cnt];
+            if (mul_mat_rule(n.op.inputs[i], x, n.op.outputs[i], 1, &a, nullptr) == SCRAPGPU_STATUS_OK && a.N > 8) {
+                need = std::max(need, sgk::matmul_scratch_bytes(a));
+            }
+        }
+    }
+    return need ? ensure_scratch(s, need) : SCRAPGPU_STATUS_OK;
+}
+
 scrapgpu_status api_plan_execute(scrapgpu_stream_t * stream, scrapgpu_plan_t * plan) {
     Stream * s = stream_of(stream);
     Plan * p = as<Plan>(plan);
     if (s == nullptr || p == nullptr) return invalid("not a hip stream or plan");
     if (p->dev != s->dev) return invalid("plan and stream belong to different devices");
-    for (PlanNode & n : p->nodes) {
-        const scrapgpu_status st = exec_desc(s, &n.op);
-        if (st != SCRAPGPU_STATUS_OK) return st;
+    SG_HIP(use(s->dev), "hipSetDevice");
+    // eager while the per-kernel profiler is on (its events are host-side records) or graphs are off
+    if (!graphs_enabled() || g_prof.load(std::memory_order_relaxed) || p->nodes.empty()) {
+        for (PlanNode & n : p->nodes) {
+            const scrapgpu_status st = exec_desc(s, &n.op);
+            if (st != SCRAPGPU_STATUS_OK) return st;
+        }
+        return SCRAPGPU_STATUS_OK;
     }
+    scrapgpu_status st = plan_prepare(s, p);
+    if (st != SCRAPGPU_STATUS_OK) return st;
+    if (p->exec == nullptr || p->exec_stream != s || p->exec_gen != s->scratch_gen) {
+        plan_drop_graph(p);
+        SG_HIP(hipStreamBeginCapture(s->s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        for (PlanNode & n : p->nodes) {
+            st = exec_desc(s, &n.op);
+            if (st != SCRAPGPU_STATUS_OK) break;
+        }
+        hipGraph_t g = nullptr;
+        const hipError_t ec = hipStreamEndCapture(s->s, &g);
+        if (st != SCRAPGPU_STATUS_OK) {
+            if (g) hipGraphDestroy(g);
+            return st;
+        }
+        if (ec != hipSuccess) return hip_fail(ec, "hipStreamEndCapture");
+        const hipError_t ei = hipGraphInstantiate(&p->exec, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (ei != hipSuccess) {
+            p->exec = nullptr;
+            return hip_fail(ei, "hipGraphInstantiate");
+        }
+        p->exec_stream = s;
+        p->exec_gen = s->scratch_gen;
+    }
+    SG_HIP(hipGraphLaunch(p->exec, s->s), "hipGraphLaunch");
     return SCRAPGPU_STATUS_OK;
 }
 
 scrapgpu_status api_plan_free(scrapgpu_plan_t * plan) {
     Plan * p = as<Plan>(plan);
     if (p == nullptr) return invalid("not a hip plan");
+    if (p->exec) {
+        // the recording stream may be gone already: wait for the device before dropping the graph
+        if (use(p->dev) == hipSuccess) hipDeviceSynchronize();
+        plan_drop_graph(p);
+    }
     plan_release(p);
     delete p;
     return SCRAPGPU_STATUS_OK;

@@ -36,8 +36,10 @@ struct MatArgs {
     int64_t r2, r3;     // broadcast factors
 };
 
-// decode matvec for 1 <= N <= 8 (weights streamed once, every column reused in registers)
-hipError_t launch_matvec(const MatArgs & a, int cu_count, hipStream_t stream, const char ** kernel_name,
+// decode matvec for 1 <= N <= 8 (weights streamed once, every column reused in registers).
+// nmat = 1, or 2..3 single-slice products of one dtype and K that share x (one fused launch;
+// mats[j].w / M / y / y_s1 per matrix, everything else from mats[0]).
+hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
                          uint64_t * grid_size);
 
 // prefill: bf16 MFMA with fp32 accumulate, weights dequantized into LDS (any N >= 1). `scratch`

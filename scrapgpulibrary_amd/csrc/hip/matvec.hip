@@ -28,6 +28,7 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <cstdint>
 #include <cstdlib>
 #include <vector>
 
@@ -39,10 +40,16 @@ constexpr int kDepth = 4;      // most steps in flight per wave
 constexpr int kLdsBudget = 56 * 1024; // bytes of x (+ sums) per work-group
 
 struct MvLaunch {
-    MatArgs a;
-    int64_t tiles;      // row tiles per slice
+    MatArgs a;          // K, nb, x, slices and strides (w / M / y per matrix below)
+    int64_t tiles;      // row tiles per slice, over all matrices
     int64_t kc;         // K elements staged per chunk (a multiple of the step)
     int wt;             // waves that split the K steps of one tile
+    int nmat;           // 1, or 2..3 weights sharing x (MUL_MAT_MULTI)
+    const uint8_t * wm[3];
+    int64_t Mm[3];
+    float * ym[3];
+    int64_t ys1[3];
+    int64_t tstart[4];  // matrix j owns tiles [tstart[j], tstart[j + 1])
 };
 
 __device__ __forceinline__ float half_bits(uint32_t h) {
@@ -366,10 +373,12 @@ __global__ __launch_bounds__(64 * kMaxWaves) void k_matvec(MvLaunch L) {
     const int r = lane % R, slot = lane / R;
     const int64_t sl = blockIdx.y;
     const int64_t i2 = sl % L.a.ne12, i3 = sl / L.a.ne12;
-    const int64_t M = L.a.M, K = L.a.K;
-    const uint8_t * w = L.a.w + (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
+    const int64_t K = L.a.K;
+    const uint64_t w_off = (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
+    const int64_t y_off = i2 * L.a.y_s2 + i3 * L.a.y_s3;
     const float * x = L.a.x + i2 * L.a.x_s2 + i3 * L.a.x_s3;
-    float * y = L.a.y + i2 * L.a.y_s2 + i3 * L.a.y_s3;
+    // matrix of a tile (tiles of matrix j are [tstart[j], tstart[j + 1]))
+    auto mat_of = [&](int64_t tile) { return tile >= L.tstart[1] ? (tile >= L.tstart[2] ? 2 : 1) : 0; };
     // tiles of this work-group: iteration it, group g -> tile (it * gridDim.x + blockIdx.x) * GW + g
     const int64_t per_iter = (int64_t) gridDim.x * GW;
     const int64_t iters = (L.tiles + per_iter - 1) / per_iter;
@@ -377,10 +386,12 @@ __global__ __launch_bounds__(64 * kMaxWaves) void k_matvec(MvLaunch L) {
     // the lane's addressing for the tile of iteration it (live: its row exists)
     auto stepper_of = [&](int64_t it, ST & st) -> bool {
         const int64_t tile = tile_of(it);
-        const int64_t m0 = tile * R;
-        if (tile >= L.tiles || m0 + r >= M) return false;
+        if (tile >= L.tiles) return false;
+        const int j = mat_of(tile);
+        const int64_t M = L.Mm[j], m0 = (tile - L.tstart[j]) * R;
+        if (m0 + r >= M) return false;
         const int64_t g0 = m0 & ~(int64_t) 31;
-        st.init(w, M, L.a.nb, g0, (int) min<int64_t>(32, M - g0), (int) (m0 - g0) + r, slot);
+        st.init(L.wm[j] + w_off, M, L.a.nb, g0, (int) min<int64_t>(32, M - g0), (int) (m0 - g0) + r, slot);
         return true;
     };
 
@@ -471,11 +482,12 @@ __global__ __launch_bounds__(64 * kMaxWaves) void k_matvec(MvLaunch L) {
             if (tid < GW * NC * R) {
                 const int g = tid / (NC * R), n = (tid / R) % NC, rr = tid % R;
                 const int64_t t2 = (it * gridDim.x + blockIdx.x) * GW + g;
-                const int64_t m = t2 * R + rr;
-                if (t2 < L.tiles && m < M) {
+                const int jm = mat_of(t2);
+                const int64_t m = (t2 - L.tstart[jm]) * R + rr;
+                if (t2 < L.tiles && m < L.Mm[jm]) {
                     float v = 0.0f;
                     for (int w2 = 0; w2 < WT; ++w2) v += rb[((g * WT + w2) * NC + n) * R + rr];
-                    float * yp = y + n * L.a.y_s1 + m;
+                    float * yp = L.ym[jm] + y_off + n * L.ys1[jm] + m;
                     *yp = kc0 == 0 ? v : *yp + v;
                 }
             }
@@ -505,7 +517,15 @@ void * pick(int nc, int R) {
     return R == 32 ? pick_nc<DT, 32>(nc) : R == 16 ? pick_nc<DT, 16>(nc) : pick_nc<DT, 8>(nc);
 }
 
-const char * name_of(int dt) {
+const char * name_of(int dt, int nmat) {
+    if (nmat > 1) {
+        switch (dt) {
+            case Q4_0: return "matvec_multi_q4_0";
+            case Q8_0: return "matvec_multi_q8_0";
+            case Q4_K: return "matvec_multi_q4_k";
+            default: return "matvec_multi_q6_k";
+        }
+    }
     switch (dt) {
         case Q4_0: return "matvec_q4_0";
         case Q8_0: return "matvec_q8_0";
@@ -552,8 +572,17 @@ size_t raw_bytes_of(int dt, int R) {
 
 } // namespace
 
-hipError_t launch_matvec(const MatArgs & a, int cu_count, hipStream_t stream, const char ** kernel_name,
+hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
                          uint64_t * grid_size) {
+    if (nmat < 1 || nmat > 3) return hipErrorInvalidValue;
+    const MatArgs & a = mats[0];
+    int64_t m_total = 0;
+    for (int j = 0; j < nmat; ++j) {
+        if (mats[j].dtype != a.dtype || mats[j].K != a.K || mats[j].N != a.N || (nmat > 1 && mats[j].ne12 * mats[j].ne13 != 1)) {
+            return hipErrorInvalidValue;
+        }
+        m_total += mats[j].M;
+    }
     const int nc = (int) a.N;
     if (nc < 1 || nc > 8) return hipErrorInvalidValue;
     const int64_t slices = a.ne12 * a.ne13;
@@ -595,7 +624,8 @@ hipError_t launch_matvec(const MatArgs & a, int cu_count, hipStream_t stream, co
         const int64_t nst = (L.kc + eps - 1) / eps;
         int wt = 1;
         while (wt < waves && nst % (2 * wt) == 0 && (nst / (2 * wt)) % D == 0 && nst / (2 * wt) >= 2 * D) wt *= 2;
-        const int64_t tiles = (a.M + cand - 1) / cand;
+        int64_t tiles = 0;
+        for (int j = 0; j < nmat; ++j) tiles += (mats[j].M + cand - 1) / cand;
         R = cand;
         WT = wt;
         wgs = resident(cand);
@@ -603,14 +633,26 @@ hipError_t launch_matvec(const MatArgs & a, int cu_count, hipStream_t stream, co
     }
     if (const int fr = tuning("SCRAPGPU_HIP_MV_R", 0)) R = fr;
     if (const int fw = tuning("SCRAPGPU_HIP_MV_WT", 0)) WT = fw;
-    L.tiles = (a.M + R - 1) / R;
     L.wt = WT;
+    L.nmat = nmat;
+    L.tstart[0] = 0;
+    for (int j = 0; j < 3; ++j) {
+        const bool has = j < nmat;
+        L.wm[j] = has ? mats[j].w : nullptr;
+        L.Mm[j] = has ? mats[j].M : 0;
+        L.ym[j] = has ? mats[j].y : nullptr;
+        L.ys1[j] = has ? mats[j].y_s1 : 0;
+        L.tstart[j + 1] = L.tstart[j] + (has ? (mats[j].M + R - 1) / R : 0);
+    }
+    for (int j = nmat + 1; j < 4; ++j) L.tstart[j] = INT64_MAX; // tiles past the last matrix never map there
+    L.tiles = L.tstart[nmat];
+    (void) m_total;
     wgs = resident(R);
     const int64_t grid_x = std::max<int64_t>(1, std::min<int64_t>(wgs, (L.tiles + (waves / WT) - 1) / (waves / WT)));
     const size_t lds = lds_of(R);
     void * fn = pick_fn(R);
     if (fn == nullptr) return hipErrorInvalidValue;
-    if (kernel_name) *kernel_name = name_of(a.dtype);
+    if (kernel_name) *kernel_name = name_of(a.dtype, nmat);
     if (grid_size) *grid_size = (uint64_t) grid_x * (uint64_t) slices;
     void * args[] = {&L};
     return hipLaunchKernel(fn, dim3((unsigned) grid_x, (unsigned) slices), dim3((unsigned) (64 * waves)), args, lds, stream);

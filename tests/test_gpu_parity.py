@@ -266,6 +266,69 @@ def test_mul_mat_multi(hip, n):
         b.free()
 
 
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+@pytest.mark.parametrize("N", [1, 3, 8])
+def test_mul_mat_multi_fused_qkv_shapes(hip, dtype, N):
+    """One fused launch for 3 weights of different row counts sharing x (QKV-like: 96 / 32 / 40 rows)."""
+    dev, st = hip
+    K = 4 * sg.BLOCK[dtype] if sg.BLOCK[dtype] == 256 else 1024
+    Ms = (96, 32, 40)
+    bufs, wts, qs, deqs = [], [], [], []
+    for i, M in enumerate(Ms):
+        q, d = quantized(dtype, K, M, 500 + i)
+        b, t = upload_weights(dev, st, dtype, q, K, M)
+        bufs.append(b)
+        wts.append(t)
+        qs.append(q)
+        deqs.append(d)
+    x = O.normal(N * K, 510 + N).reshape(N, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    st.upload(xt, x)
+    ybs = [dev.alloc(4 * M * N) for M in Ms]
+    yts = [sg.tdesc(sg.F32, (M, N), b) for M, b in zip(Ms, ybs)]
+    sg.lib().scrapgpu_hip_profile_reset()
+    sg.lib().scrapgpu_hip_profile_enable(1)
+    op, keep = sg.multi_op(wts, xt, yts)
+    st.execute(op)
+    st.sync()
+    sg.lib().scrapgpu_hip_profile_enable(0)
+    rows = sg.profile_table()
+    assert [r["name"] for r in rows] == [f"matvec_multi_{sg.NAMES[dtype]}"] and rows[0]["launches"] == 1
+    for i, M in enumerate(Ms):
+        ref = O.mul_mat(dtype, qs[i], K, M, x)
+        check_matvec(st.download(yts[i]).reshape(N, M), ref, x, deqs[i])
+    for b in bufs + ybs + [xb]:
+        b.free()
+
+
+def test_mul_mat_multi_mixed_dtypes_falls_back(hip):
+    """Weights of different dtypes share x: one launch per product, same results."""
+    dev, st = hip
+    K, M = 512, 64
+    specs = [(sg.Q4_K, 0), (sg.Q6_K, 1)]
+    bufs, wts, refs = [], [], []
+    x = O.normal(2 * K, 520).reshape(2, K)
+    for dt, i in specs:
+        q, d = quantized(dt, K, M, 530 + i)
+        b, t = upload_weights(dev, st, dt, q, K, M)
+        bufs.append(b)
+        wts.append(t)
+        refs.append((O.mul_mat(dt, q, K, M, x), d))
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, 2), xb)
+    st.upload(xt, x)
+    ybs = [dev.alloc(4 * M * 2) for _ in specs]
+    yts = [sg.tdesc(sg.F32, (M, 2), b) for b in ybs]
+    op, keep = sg.multi_op(wts, xt, yts)
+    st.execute(op)
+    st.sync()
+    for (ref, d), yt in zip(refs, yts):
+        check_matvec(st.download(yt).reshape(2, M), ref, x, d)
+    for b in bufs + ybs + [xb]:
+        b.free()
+
+
 def test_plan_and_buffer_lifetime(hip):
     dev, st = hip
     L = sg.lib()
@@ -309,3 +372,61 @@ def test_profiler_counts_launches(hip):
     rows = {r["name"]: r for r in sg.profile_table()}
     assert rows["matvec_q4_k"]["launches"] == 1
     assert rows["matvec_q4_k"]["bytes"] == O.row_bytes(sg.Q4_K, K) * M
+
+
+def _plan(dev, ops):
+    L = sg.lib()
+    nodes = (sg.PlanNode * len(ops))(*[sg.PlanNode(C.sizeof(sg.PlanNode), op, 0) for op in ops])
+    pd = sg.PlanDesc(C.sizeof(sg.PlanDesc), nodes, len(ops))
+    plan = C.c_void_p()
+    sg.check(L.scrapgpu_plan_build(dev.handle, C.byref(pd), C.byref(plan)), "plan_build")
+    return plan
+
+
+def test_plan_graph_replays_match_eager(hip):
+    """A plan is recorded once as a HIP graph and replayed: every replay, with new inputs written
+    and other eager work between the replays, matches the oracle; growing the stream's scratch
+    and switching streams re-record it."""
+    dev, st = hip
+    L = sg.lib()
+    K = 1024
+    specs = [(sg.Q4_K, 256, 1, 100), (sg.Q8_0, 96, 4, 101), (sg.Q6_K, 160, 64, 102), (sg.Q4_0, 128, 1, 103)]
+    items = []
+    for dtype, M, N, seed in specs:
+        q, deq = quantized(dtype, K, M, seed)
+        wb, wt = upload_weights(dev, st, dtype, q, K, M)
+        xb = dev.alloc(4 * K * N)
+        xt = sg.tdesc(sg.F32, (K, N), xb)
+        yb = dev.alloc(4 * M * N)
+        yt = sg.tdesc(sg.F32, (M, N), yb)
+        op, keep = sg.mul_mat_op(wt, xt, yt)
+        items.append(dict(dtype=dtype, M=M, N=N, q=q, deq=deq, bufs=(wb, xb, yb), xt=xt, yt=yt, op=op, keep=keep))
+    plan = _plan(dev, [it["op"] for it in items])
+    st2 = dev.stream()
+    try:
+        for rep in range(5):
+            if rep == 3:  # a large eager prefill grows the scratch of `st`: the graph is re-recorded
+                q, _ = quantized(sg.Q4_K, 2048, 128, 110)
+                run_mul_mat(dev, st, sg.Q4_K, q, 2048, 128, O.normal(512 * 2048, 111).reshape(512, 2048))
+            stream = st2 if rep == 4 else st
+            xs = []
+            for i, it in enumerate(items):
+                x = O.normal(it["N"] * K, 1000 * rep + i).reshape(it["N"], K)
+                st.upload(it["xt"], x)
+                xs.append(x)
+            st.sync()
+            sg.check(L.scrapgpu_plan_execute(stream.handle, plan), "plan_execute")
+            stream.sync()
+            for it, x in zip(items, xs):
+                y = st.download(it["yt"]).reshape(it["N"], it["M"])
+                ref = O.mul_mat(it["dtype"], it["q"], K, it["M"], x)
+                if it["N"] > 8:
+                    assert nmse(y, ref) <= 5e-5, f"replay {rep} {it['dtype']}"
+                else:
+                    check_matvec(y, ref, x, it["deq"])
+    finally:
+        sg.check(L.scrapgpu_plan_free(plan), "plan_free")
+        st2.free()
+        for it in items:
+            for b in it["bufs"]:
+                b.free()
