@@ -1,28 +1,38 @@
 // Decode matvec over R32 weights for 1 <= N <= 8 columns (gfx950, wave64).
 //
-// Work decomposition. A work-group owns R consecutive rows (a whole R32 group or an aligned part
-// of one) of one slice and the whole K range, so no work-group ever waits for
-// another: on MI355X the 8 XCDs have separate L2s and any cross-work-group handshake inside a
-// kernel costs an L2 write-back/invalidate. R (32, 16, 8 or 4) is picked per shape so that the grid
-// holds at least two work-groups per CU. Its W waves (8, up to 16 for small grids) split K: wave w
-// takes steps w, w+W, ...; each wave keeps 4 steps of weight loads in flight in a register ring,
-// and issues the first ones before the x chunk is staged so that the two overlap.
+// Replaces, for the hip backend, the reference's R32 matvec kernels k_mvr_* / k_mvrc_*
+// (src/backends/opencl11/kernels/mul_mv_r.cl:240-287), k_mvr_q4_k / k_mvr_q6_k (mul_mv_k.cl:396-450)
+// and, for 2-3 weights sharing x, k_mvm_* (mul_mv_multi.cl:46-99). Same products, new design.
 //
-// Inside a wave, lane l serves row r = l % R of the tile through slot s = l / R (S = 64 / R slots).
-// A step covers `bps` blocks whose "tasks" (16-byte R32 units, or for Q6_K the three units that
-// hold one 64-element run) are dealt to the slots, so one wave-wide 128-bit load reads S runs of
-// 16*R contiguous bytes (>= 64 bytes): coalesced.
+// Work decomposition. A work-group owns a tile of R rows (R = 16 or 32, inside one R32 group of
+// 32 rows) and all of K. Its W waves split K into contiguous ranges of steps (a step = 256
+// elements), so a wave only needs its own part of x, which it converts into its private LDS
+// region; the waves meet once, at the end, to add their partial row sums in a fixed order.
 //
-// Arithmetic. A lane converts bytes with one mask per 4 weights and one byte->float conversion per
-// weight, then one FMA per weight and column against x held in LDS (lanes of a slot read the same
-// LDS address: a broadcast). Block scales are factored out of the inner sums and every constant
-// offset of a format is applied once per 16 weights through precomputed sums of 16 consecutive x:
-//   Q4_0: d * (sum q x - 8 sum x)            Q8_0: d * (sum u x - 128 sum x)   (u = q xor 0x80)
+// Inside a wave, lane l serves row r = l % R through part p = l / R (P = 64 / R parts). A step's
+// bytes of one row are dealt to the parts by whole scale groups, so one 128-bit wave load reads P
+// runs of 16 * R contiguous bytes of one R32 unit area (256 B or 512 B): coalesced.
+//
+// Two forms:
+//  * burst (N = 1, K <= 64 steps): one tile per work-group, at most 4 steps per wave; the wave
+//    loads its x range, then issues every weight load, and only then converts x, so the x round
+//    trip hides under the weight round trip. No loop-carried state: few registers, 4-8 waves per
+//    SIMD, and the hardware dispatcher streams the work-groups.
+//  * streaming (N > 1, or longer K): a persistent grid; each work-group walks tiles, its waves
+//    convert their x range once (when it fits the LDS budget) and keep the next step's loads in
+//    flight while computing the current one.
+//
+// x conversion. Every 32-element segment of x is stored as two int8 planes a, b and a scale s
+// (s = max|x| / 127): x ~= s * a + (s / 253) * b, plus the plain sums of its two 16-element
+// halves. A weight run then costs one sdot4 per 4 weights and plane:
+//   sum_i q_i x_i ~= (s / 253) * (253 * sum q a + sum q b)
+// with block scales factored out and each format's constant offset applied once per run through
+// the segment sums:
+//   Q4_0: d * (sum q x - 8 sum x)            Q8_0: d * sum q x      (q = stored byte xor 0x80)
 //   Q4_K: d*sc * sum q x - dmin*m * sum x    Q6_K: d*sc * (sum q x - 32 sum x)
-// The high nibble is used in place (value * 16) and the 1/16 folded into its scale. The slots and
-// then the waves of a row are added in a fixed order (shuffles, then LDS): deterministic.
-//
-// x is staged per K chunk (all of K when it fits the LDS budget, else chunks of whole steps).
+// The two planes carry ~15 significant bits of each x relative to its segment's largest |x|, so
+// the product differs from the fp32 reference by ~1e-5 of max|x| per term, well inside the
+// NMSE <= 1e-7 bound of the decode path.
 #include "kernels.h"
 
 #include <hip/hip_fp16.h>
@@ -35,203 +45,116 @@
 namespace sgk {
 namespace {
 
-constexpr int kMaxWaves = 8;
-constexpr int kDepth = 4;      // most steps in flight per wave
-constexpr int kLdsBudget = 56 * 1024; // bytes of x (+ sums) per work-group
+constexpr int kStep = 256;     // K elements per step
+constexpr int kSegs = 8;       // 32-element x segments per step
+constexpr int kLdsX = 64 * 1024; // bytes of converted x per work-group (all waves)
 
-struct MvLaunch {
-    MatArgs a;          // K, nb, x, slices and strides (w / M / y per matrix below)
-    int64_t tiles;      // row tiles per slice, over all matrices
-    int64_t kc;         // K elements staged per chunk (a multiple of the step)
-    int wt;             // waves that split the K steps of one tile
-    int nmat;           // 1, or 2..3 weights sharing x (MUL_MAT_MULTI)
-    const uint8_t * wm[3];
-    int64_t Mm[3];
-    float * ym[3];
+struct MvArgs {
+    const uint8_t * w[3];
+    int64_t M[3];
+    float * y[3];
     int64_t ys1[3];
-    int64_t tstart[4];  // matrix j owns tiles [tstart[j], tstart[j + 1])
+    int64_t tstart[4]; // matrix j owns tiles [tstart[j], tstart[j + 1])
+    int64_t K, nb, nst; // elements, blocks and steps per row
+    const float * x;
+    int64_t x_s1, x_s2, x_s3;
+    uint64_t w_s2, w_s3;
+    int64_t y_s2, y_s3;
+    int64_t ne12, r2, r3;
+    int cs;   // steps per x chunk of one wave
+    int64_t tiles; // row tiles over all matrices
+    int xvec; // x columns are 16-byte aligned: float4 loads
 };
 
 __device__ __forceinline__ float half_bits(uint32_t h) {
     return __half2float(__ushort_as_half((unsigned short) (h & 0xFFFFu)));
 }
 
-__device__ __forceinline__ uint4 mask4(uint4 q, uint32_t m) {
-    return make_uint4(q.x & m, q.y & m, q.z & m, q.w & m);
-}
-
 __device__ __forceinline__ uint4 load16(const uint8_t * p) {
     return *reinterpret_cast<const uint4 *>(p);
 }
 
-__device__ __forceinline__ uint32_t byte_of(uint4 v, int i) {
-    const uint32_t w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
-    return (w >> (8 * (i & 3))) & 0xFFu;
+__device__ __forceinline__ uint32_t load_half(const uint8_t * p) {
+    return *reinterpret_cast<const uint16_t *>(p);
 }
 
-// steps in flight per wave: the largest power of two (<= kDepth) whose raw weight registers fit in
-// ~48 VGPRs; the host picks the waves per tile so that every wave's step count is a multiple of it
-constexpr int ring_depth(size_t raw_bytes) {
-    return (int) (raw_bytes / 4) * 4 <= 48 ? 4 : (int) (raw_bytes / 4) * 2 <= 48 ? 2 : 1;
-}
-
-// ---- per format: tasks per block, elements per block, raw registers of one task ----------------
-
-// The x chunk in LDS: for column n and 16-element segment g, xq[(n * nseg + g)] holds two int8
-// planes (a, b) with x ~= s * a + (s / 256) * b, and xf[(n * nseg + g)] = {s / 256, sum of the 16 x}.
+// one x segment in LDS: a plane (32 int8), b plane (32 int8)
 struct XSeg {
-    uint4 a, b;
+    uint4 a0, a1, b0, b1;
 };
 
-// 256 * sum(q_i * a_i) + sum(q_i * b_i) over 16 int8 pairs: x dot q in units of s / 256
-__device__ __forceinline__ int dot16i(uint4 q, const XSeg & x) {
-    int t = __builtin_amdgcn_sdot4((int) q.x, (int) x.a.x, 0, false);
-    t = __builtin_amdgcn_sdot4((int) q.y, (int) x.a.y, t, false);
-    t = __builtin_amdgcn_sdot4((int) q.z, (int) x.a.z, t, false);
-    t = __builtin_amdgcn_sdot4((int) q.w, (int) x.a.w, t, false);
-    t <<= 8;
-    t = __builtin_amdgcn_sdot4((int) q.x, (int) x.b.x, t, false);
-    t = __builtin_amdgcn_sdot4((int) q.y, (int) x.b.y, t, false);
-    t = __builtin_amdgcn_sdot4((int) q.z, (int) x.b.z, t, false);
-    t = __builtin_amdgcn_sdot4((int) q.w, (int) x.b.w, t, false);
-    return t;
+// 253 * (q . a) + (q . b) over 16 int8 pairs (four words of q against 16 bytes of each plane)
+__device__ __forceinline__ int dot16(uint4 q, uint4 a, uint4 b) {
+    int ta = __builtin_amdgcn_sdot4((int) q.x, (int) a.x, 0, false);
+    ta = __builtin_amdgcn_sdot4((int) q.y, (int) a.y, ta, false);
+    ta = __builtin_amdgcn_sdot4((int) q.z, (int) a.z, ta, false);
+    ta = __builtin_amdgcn_sdot4((int) q.w, (int) a.w, ta, false);
+    int tb = __builtin_amdgcn_sdot4((int) q.x, (int) b.x, 0, false);
+    tb = __builtin_amdgcn_sdot4((int) q.y, (int) b.y, tb, false);
+    tb = __builtin_amdgcn_sdot4((int) q.z, (int) b.z, tb, false);
+    tb = __builtin_amdgcn_sdot4((int) q.w, (int) b.w, tb, false);
+    return ta * 253 + tb;
 }
 
-__device__ __forceinline__ uint4 shr4(uint4 q, int s) {
-    return make_uint4(q.x >> s, q.y >> s, q.z >> s, q.w >> s);
+// the same over 32 pairs: q0 against the first 16 bytes of the segment, q1 against the last 16
+__device__ __forceinline__ int dot32(uint4 q0, uint4 q1, const XSeg & s) {
+    int ta = __builtin_amdgcn_sdot4((int) q0.x, (int) s.a0.x, 0, false);
+    ta = __builtin_amdgcn_sdot4((int) q0.y, (int) s.a0.y, ta, false);
+    ta = __builtin_amdgcn_sdot4((int) q0.z, (int) s.a0.z, ta, false);
+    ta = __builtin_amdgcn_sdot4((int) q0.w, (int) s.a0.w, ta, false);
+    ta = __builtin_amdgcn_sdot4((int) q1.x, (int) s.a1.x, ta, false);
+    ta = __builtin_amdgcn_sdot4((int) q1.y, (int) s.a1.y, ta, false);
+    ta = __builtin_amdgcn_sdot4((int) q1.z, (int) s.a1.z, ta, false);
+    ta = __builtin_amdgcn_sdot4((int) q1.w, (int) s.a1.w, ta, false);
+    int tb = __builtin_amdgcn_sdot4((int) q0.x, (int) s.b0.x, 0, false);
+    tb = __builtin_amdgcn_sdot4((int) q0.y, (int) s.b0.y, tb, false);
+    tb = __builtin_amdgcn_sdot4((int) q0.z, (int) s.b0.z, tb, false);
+    tb = __builtin_amdgcn_sdot4((int) q0.w, (int) s.b0.w, tb, false);
+    tb = __builtin_amdgcn_sdot4((int) q1.x, (int) s.b1.x, tb, false);
+    tb = __builtin_amdgcn_sdot4((int) q1.y, (int) s.b1.y, tb, false);
+    tb = __builtin_amdgcn_sdot4((int) q1.z, (int) s.b1.z, tb, false);
+    tb = __builtin_amdgcn_sdot4((int) q1.w, (int) s.b1.w, tb, false);
+    return ta * 253 + tb;
 }
 
-// ---- per format: the lane's view of one row tile ------------------------------------------------
-// A Stepper is built once per tile: 64-bit base pointers of the lane's row in every R32 area, then
-// 32-bit offsets per step. load(step) fetches all the lane's 16-byte units of one step (and the
-// block's scales once); compute() accumulates them against x.
-
-template <int DT, int R> struct Stepper;
-
-// blocks per step, tasks per lane and step, K elements per step of a format with T tasks per block
-template <int T, int R, int BE>
-struct Geo {
-    static constexpr int S = 64 / R;
-    static constexpr int BPS = S > T ? S / T : 1;
-    static constexpr int TPL = T * BPS / S;
-    static constexpr int EPS = BPS * BE;
-};
-
-template <int R>
-struct Stepper<Q4_0, R> : Geo<1, R, 32> {
-    using G = Geo<1, R, 32>;
-    struct Raw { uint4 q; uint32_t d; };
-    const uint8_t * qb;
-    const uint8_t * db;
-    uint32_t qblk, dblk;
-    int64_t nb;
-    int slot;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int slot_) {
-        nb = nb_;
-        slot = slot_;
-        qb = w + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
-        db = w + (uint64_t) M * nb * 16 + (uint64_t) g0 * nb * 2 + (uint64_t) lr * 2;
-        qblk = (uint32_t) rs * 16;
-        dblk = (uint32_t) rs * 2;
-    }
-    __device__ int64_t block(int64_t step) const { return step * G::BPS + slot; }
-    __device__ Raw load(int64_t step) const {
-        Raw r{};
-        const int64_t b = block(step);
-        if (b < nb) {
-            r.q = load16(qb + (uint32_t) b * qblk);
-            r.d = *reinterpret_cast<const uint16_t *>(db + (uint32_t) b * dblk);
-        }
-        return r;
-    }
-    template <int NC>
-    __device__ void compute(const Raw & r, int64_t step, int64_t kc0, const XSeg * xq, const float2 * xf, int nseg, float * acc) const {
-        const int64_t b = block(step);
-        if (b >= nb) return;
-        const int sg = (int) ((b * 32 - kc0) >> 4);
-        const float d = half_bits(r.d);
-        const uint4 lo = mask4(r.q, 0x0F0F0F0Fu), hi = mask4(shr4(r.q, 4), 0x0F0F0F0Fu);
-#pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            const int g = n * nseg + sg;
-            const float2 f0 = xf[g], f1 = xf[g + 1];
-            float a = acc[n];
-            a = fmaf(d * f0.x, (float) dot16i(lo, xq[g]), a);
-            a = fmaf(d * f1.x, (float) dot16i(hi, xq[g + 1]), a);
-            a = fmaf(-8.0f * d, f0.y + f1.y, a);
-            acc[n] = a;
-        }
-    }
-};
-
-template <int R>
-struct Stepper<Q8_0, R> : Geo<2, R, 32> {
-    using G = Geo<2, R, 32>;
-    struct Raw { uint4 q; uint32_t d; };
-    const uint8_t * qb;
-    const uint8_t * db;
-    uint32_t qblk, qunit, dblk;
-    int64_t nb;
-    int slot;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int slot_) {
-        nb = nb_;
-        slot = slot_;
-        qb = w + (uint64_t) g0 * nb * 32 + (uint64_t) lr * 16;
-        db = w + (uint64_t) M * nb * 32 + (uint64_t) g0 * nb * 2 + (uint64_t) lr * 2;
-        qblk = (uint32_t) rs * 32;
-        qunit = (uint32_t) rs * 16;
-        dblk = (uint32_t) rs * 2;
-    }
-    // TPL == 1: the lane's task is slot -> block step * BPS + slot / 2, unit slot % 2
-    __device__ int64_t block(int64_t step) const { return step * G::BPS + slot / 2; }
-    __device__ Raw load(int64_t step) const {
-        Raw r{};
-        const int64_t b = block(step);
-        if (b < nb) {
-            r.q = load16(qb + (uint32_t) b * qblk + (uint32_t) (slot & 1) * qunit);
-            r.d = *reinterpret_cast<const uint16_t *>(db + (uint32_t) b * dblk);
-        }
-        return r;
-    }
-    template <int NC>
-    __device__ void compute(const Raw & r, int64_t step, int64_t kc0, const XSeg * xq, const float2 * xf, int nseg, float * acc) const {
-        const int64_t b = block(step);
-        if (b >= nb) return;
-        const int sg = (int) ((b * 32 - kc0) >> 4) + (slot & 1);
-        const float d = half_bits(r.d);
-        const uint4 q = make_uint4(r.q.x ^ 0x80808080u, r.q.y ^ 0x80808080u, r.q.z ^ 0x80808080u, r.q.w ^ 0x80808080u);
-#pragma unroll
-        for (int n = 0; n < NC; ++n) {
-            const int g = n * nseg + sg;
-            acc[n] = fmaf(d * xf[g].x, (float) dot16i(q, xq[g]), acc[n]);
-        }
-    }
-};
-
-// 6-bit scale and min of sub-block j (0..7) from the 12 packed bytes s[0..11] = {hd.y, hd.z, hd.w}
-__device__ __forceinline__ void k4_scale_min(uint4 hd, int j, float & sc, float & mn) {
-    const uint32_t lo4 = hd.y, hi4 = hd.z, top4 = hd.w; // s[0..3], s[4..7], s[8..11]
-    const int sh = 8 * (j & 3);
-    if (j < 4) {
-        sc = (float) ((lo4 >> sh) & 63u);
-        mn = (float) ((hi4 >> sh) & 63u);
-    } else {
-        const uint32_t t = (top4 >> sh) & 0xFFu;
-        sc = (float) ((t & 0x0Fu) | (((lo4 >> sh) >> 6 & 3u) << 4));
-        mn = (float) ((t >> 4) | (((hi4 >> sh) >> 6 & 3u) << 4));
-    }
+__device__ __forceinline__ uint4 lo4(uint4 q) {
+    return make_uint4(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, q.z & 0x0F0F0F0Fu, q.w & 0x0F0F0F0Fu);
+}
+__device__ __forceinline__ uint4 hi4(uint4 q) {
+    return make_uint4((q.x >> 4) & 0x0F0F0F0Fu, (q.y >> 4) & 0x0F0F0F0Fu, (q.z >> 4) & 0x0F0F0F0Fu, (q.w >> 4) & 0x0F0F0F0Fu);
 }
 
+// The converted x of one wave's chunk: xs[n * nseg + g] (planes) and xf[n * nseg + g] =
+// {s / 253, sum of elements 0..15, sum of elements 16..31, sum of all 32}.
+struct XView {
+    const XSeg * xs;
+    const float4 * xf;
+    int nseg;
+};
+
+// ---- per format: the lane's slice of a step ------------------------------------------------------
+// init() resolves the lane's row in every R32 area once; load(step) fetches what the lane needs of
+// one step; compute() accumulates it for NC columns against x segments of the current chunk
+// (sg0 = index of the step's first segment inside the chunk).
+
+template <int DT, int R> struct Fmt;
+
+// Q4_K: a step is one block; part p takes chunks c = p, p + P, ... (64 elements: 32 bytes = units
+// 2c, 2c + 1 of the 128 nibble bytes), i.e. whole sub-blocks 2c (low nibbles), 2c + 1 (high).
 template <int R>
-struct Stepper<Q4_K, R> : Geo<8, R, 256> {
-    using G = Geo<8, R, 256>;
-    struct Raw { uint4 q[G::TPL]; uint4 hd; };
+struct Fmt<Q4_K, R> {
+    static constexpr int P = 64 / R;
+    static constexpr int CL = 4 / P; // chunks per lane
+    struct Raw {
+        uint4 q[CL][2];
+        uint4 hd;
+    };
     const uint8_t * qb;
     const uint8_t * hb;
     uint32_t qblk, qunit, hblk;
-    int slot;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb, int64_t g0, int rs, int lr, int slot_) {
-        slot = slot_;
+    int p;
+    __device__ void init(const uint8_t * w, int64_t M, int64_t nb, int64_t g0, int rs, int lr, int part, int64_t) {
+        p = part;
         qb = w + (uint64_t) g0 * nb * 128 + (uint64_t) lr * 16;
         hb = w + (uint64_t) M * nb * 128 + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
         qblk = (uint32_t) rs * 128;
@@ -240,54 +163,77 @@ struct Stepper<Q4_K, R> : Geo<8, R, 256> {
     }
     __device__ Raw load(int64_t step) const {
         Raw r;
-        const uint8_t * p = qb + (uint32_t) step * qblk + (uint32_t) slot * qunit;
+        const uint8_t * b = qb + (uint32_t) step * qblk;
 #pragma unroll
-        for (int t = 0; t < G::TPL; ++t) r.q[t] = load16(p + (uint32_t) (G::S * t) * qunit);
+        for (int i = 0; i < CL; ++i) {
+            const int c = p + P * i;
+            r.q[i][0] = load16(b + (uint32_t) (2 * c) * qunit);
+            r.q[i][1] = load16(b + (uint32_t) (2 * c + 1) * qunit);
+        }
         r.hd = load16(hb + (uint32_t) step * hblk);
         return r;
     }
     template <int NC>
-    __device__ void compute(const Raw & r, int64_t step, int64_t kc0, const XSeg * xq, const float2 * xf, int nseg, float * acc) const {
+    __device__ void compute(const Raw & r, int sg0, const XView & xv, float * acc) const {
         const float d = half_bits(r.hd.x), dmin = half_bits(r.hd.x >> 16);
-        const int sg0 = (int) ((step * 256 - kc0) >> 4);
+        const uint32_t s0 = r.hd.y, s1 = r.hd.z, s2 = r.hd.w; // scale bytes 0..3, 4..7, 8..11
 #pragma unroll
-        for (int t = 0; t < G::TPL; ++t) {
-            const int j = slot + G::S * t; // unit: bytes 16j..16j+15 of the 128 quant bytes
-            const int c = j >> 1, h = j & 1;
+        for (int i = 0; i < CL; ++i) {
+            const int c = p + P * i;
+            // sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles): 6-bit scale and min
             float sc0, m0, sc1, m1;
-            k4_scale_min(r.hd, 2 * c, sc0, m0);
-            k4_scale_min(r.hd, 2 * c + 1, sc1, m1);
-            const float dl = d * sc0, dh = d * sc1, ml = dmin * m0, mh = dmin * m1;
-            const uint4 lo = mask4(r.q[t], 0x0F0F0F0Fu), hi = mask4(shr4(r.q[t], 4), 0x0F0F0F0Fu);
-            const int sg = sg0 + 4 * c + h; // lo elements 64c + 16h + i, hi 32 further
+            const int sh0 = 16 * (c & 1), sh1 = sh0 + 8; // byte (2c) & 3, (2c + 1) & 3
+            if (c < 2) {
+                sc0 = (float) ((s0 >> sh0) & 63u);
+                m0 = (float) ((s1 >> sh0) & 63u);
+                sc1 = (float) ((s0 >> sh1) & 63u);
+                m1 = (float) ((s1 >> sh1) & 63u);
+            } else {
+                const uint32_t t0 = s2 >> sh0, t1 = s2 >> sh1;
+                sc0 = (float) ((t0 & 0x0Fu) | (((s0 >> sh0) >> 2) & 0x30u));
+                m0 = (float) (((t0 >> 4) & 0x0Fu) | (((s1 >> sh0) >> 2) & 0x30u));
+                sc1 = (float) ((t1 & 0x0Fu) | (((s0 >> sh1) >> 2) & 0x30u));
+                m1 = (float) (((t1 >> 4) & 0x0Fu) | (((s1 >> sh1) >> 2) & 0x30u));
+            }
+            const float d0 = d * sc0, d1 = d * sc1, n0 = -dmin * m0, n1 = -dmin * m1;
+            const uint4 l0 = lo4(r.q[i][0]), l1 = lo4(r.q[i][1]);
+            const uint4 h0 = hi4(r.q[i][0]), h1 = hi4(r.q[i][1]);
+            const int g = sg0 + 2 * c;
 #pragma unroll
             for (int n = 0; n < NC; ++n) {
-                const int g = n * nseg + sg;
-                const float2 fl = xf[g], fh = xf[g + 2];
+                const int gi = n * xv.nseg + g;
+                const float4 f0 = xv.xf[gi], f1 = xv.xf[gi + 1];
                 float a = acc[n];
-                a = fmaf(dl * fl.x, (float) dot16i(lo, xq[g]), a);
-                a = fmaf(dh * fh.x, (float) dot16i(hi, xq[g + 2]), a);
-                a = fmaf(-ml, fl.y, a);
-                a = fmaf(-mh, fh.y, a);
+                a = fmaf(d0 * f0.x, (float) dot32(l0, l1, xv.xs[gi]), a);
+                a = fmaf(n0, f0.w, a);
+                a = fmaf(d1 * f1.x, (float) dot32(h0, h1, xv.xs[gi + 1]), a);
+                a = fmaf(n1, f1.w, a);
                 acc[n] = a;
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
 };
 
+// Q6_K: a step is one block; part p takes tasks k = p, p + P, ... (h = k >> 1, hf = k & 1): the
+// 64 elements 128h + 32rr + 16hf + i (rr, i < 4, 16) built from ql units 4h + hf, 4h + 2 + hf and
+// qh unit 8 + 2h + hf; each 16-run has its own signed 8-bit scale.
 template <int R>
-struct Stepper<Q6_K, R> : Geo<4, R, 256> {
-    using G = Geo<4, R, 256>;
-    struct Raw { uint4 qa[G::TPL], qc[G::TPL], qh[G::TPL]; uint4 sc; uint32_t d; };
+struct Fmt<Q6_K, R> {
+    static constexpr int P = 64 / R;
+    static constexpr int TL = 4 / P; // tasks per lane
+    struct Raw {
+        uint4 qa[TL], qc[TL], qh[TL];
+        uint4 sc;
+        uint32_t d;
+    };
     const uint8_t * qb;
     const uint8_t * sb;
     const uint8_t * db;
     uint32_t qblk, qunit, sblk, dblk;
-    int64_t nb;
-    int slot;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int slot_) {
-        nb = nb_;
-        slot = slot_;
+    int p;
+    __device__ void init(const uint8_t * w, int64_t M, int64_t nb, int64_t g0, int rs, int lr, int part, int64_t) {
+        p = part;
         qb = w + (uint64_t) g0 * nb * 192 + (uint64_t) lr * 16;
         sb = w + (uint64_t) M * nb * 192 + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
         db = w + (uint64_t) M * nb * 208 + (uint64_t) g0 * nb * 2 + (uint64_t) lr * 2;
@@ -296,225 +242,488 @@ struct Stepper<Q6_K, R> : Geo<4, R, 256> {
         sblk = (uint32_t) rs * 16;
         dblk = (uint32_t) rs * 2;
     }
-    // task k = 0..3: h = k >> 1 (half of the block), hf = k & 1 (16-element half of each 32-run)
-    __device__ int task(int t) const { return (slot + G::S * t) % 4; }
-    __device__ int64_t block(int64_t step) const { return step * G::BPS + (G::BPS > 1 ? slot / 4 : 0); }
     __device__ Raw load(int64_t step) const {
-        Raw r{};
-        const int64_t b = block(step);
-        if (G::BPS > 1 && b >= nb) return r;
-        const uint8_t * p = qb + (uint32_t) b * qblk;
+        Raw r;
+        const uint8_t * b = qb + (uint32_t) step * qblk;
 #pragma unroll
-        for (int t = 0; t < G::TPL; ++t) {
-            const int k = task(t), h = k >> 1, hf = k & 1;
-            r.qa[t] = load16(p + (uint32_t) (4 * h + hf) * qunit);     // ql[64h + 16hf + i]
-            r.qc[t] = load16(p + (uint32_t) (4 * h + 2 + hf) * qunit); // ql[64h + 32 + 16hf + i]
-            r.qh[t] = load16(p + (uint32_t) (8 + 2 * h + hf) * qunit); // qh[32h + 16hf + i]
+        for (int t = 0; t < TL; ++t) {
+            const int k = p + P * t, h = k >> 1, hf = k & 1;
+            r.qa[t] = load16(b + (uint32_t) (4 * h + hf) * qunit);
+            r.qc[t] = load16(b + (uint32_t) (4 * h + 2 + hf) * qunit);
+            r.qh[t] = load16(b + (uint32_t) (8 + 2 * h + hf) * qunit);
         }
-        r.sc = load16(sb + (uint32_t) b * sblk);
-        r.d = *reinterpret_cast<const uint16_t *>(db + (uint32_t) b * dblk);
+        r.sc = load16(sb + (uint32_t) step * sblk);
+        r.d = load_half(db + (uint32_t) step * dblk);
         return r;
     }
     template <int NC>
-    __device__ void compute(const Raw & r, int64_t step, int64_t kc0, const XSeg * xq, const float2 * xf, int nseg, float * acc) const {
-        const int64_t b = block(step);
-        if (G::BPS > 1 && b >= nb) return;
+    __device__ void compute(const Raw & r, int sg0, const XView & xv, float * acc) const {
         const float d = half_bits(r.d);
-        const int sg0 = (int) ((b * 256 - kc0) >> 4);
 #pragma unroll
-        for (int t = 0; t < G::TPL; ++t) {
-            const int k = task(t), h = k >> 1, hf = k & 1;
+        for (int t = 0; t < TL; ++t) {
+            const int k = p + P * t, h = k >> 1, hf = k & 1;
             const uint4 qa = r.qa[t], qc = r.qc[t], qh = r.qh[t];
-            uint4 v[4];
-            v[0] = make_uint4((qa.x & 0x0F0F0F0Fu) | ((qh.x << 4) & 0x30303030u), (qa.y & 0x0F0F0F0Fu) | ((qh.y << 4) & 0x30303030u),
-                              (qa.z & 0x0F0F0F0Fu) | ((qh.z << 4) & 0x30303030u), (qa.w & 0x0F0F0F0Fu) | ((qh.w << 4) & 0x30303030u));
-            v[1] = make_uint4((qc.x & 0x0F0F0F0Fu) | ((qh.x << 2) & 0x30303030u), (qc.y & 0x0F0F0F0Fu) | ((qh.y << 2) & 0x30303030u),
-                              (qc.z & 0x0F0F0F0Fu) | ((qh.z << 2) & 0x30303030u), (qc.w & 0x0F0F0F0Fu) | ((qh.w << 2) & 0x30303030u));
-            v[2] = make_uint4(((qa.x >> 4) & 0x0F0F0F0Fu) | (qh.x & 0x30303030u), ((qa.y >> 4) & 0x0F0F0F0Fu) | (qh.y & 0x30303030u),
-                              ((qa.z >> 4) & 0x0F0F0F0Fu) | (qh.z & 0x30303030u), ((qa.w >> 4) & 0x0F0F0F0Fu) | (qh.w & 0x30303030u));
-            v[3] = make_uint4(((qc.x >> 4) & 0x0F0F0F0Fu) | ((qh.x >> 2) & 0x30303030u), ((qc.y >> 4) & 0x0F0F0F0Fu) | ((qh.y >> 2) & 0x30303030u),
-                              ((qc.z >> 4) & 0x0F0F0F0Fu) | ((qh.z >> 2) & 0x30303030u), ((qc.w >> 4) & 0x0F0F0F0Fu) | ((qh.w >> 2) & 0x30303030u));
-            // scale byte 8h + 2rr + hf (stored xor 0x80): the 4 bytes for rr = 0..3 are
-            // s[8h + hf], s[8h + hf + 2], ... -> word h*2 + (hf? odd bytes) of sc
-            const uint32_t sw0 = h ? r.sc.z : r.sc.x, sw1 = h ? r.sc.w : r.sc.y; // bytes 8h..8h+3, 8h+4..8h+7
+            // scale of run rr: byte 8h + hf + 2rr of the 16 (stored xor 0x80, so value = byte - 128)
+            const uint32_t sw0 = h ? r.sc.z : r.sc.x, sw1 = h ? r.sc.w : r.sc.y;
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
+                // 6-bit values of run rr: low nibbles of qa (rr 0) / qc (rr 1), high nibbles (rr 2, 3),
+                // with bits 2rr, 2rr + 1 of qh on top
+                const uint4 ql = (rr & 1) ? qc : qa;
+                const int ls = rr < 2 ? 0 : 4;
+                const int hs = 2 * rr;
+                const uint4 v = make_uint4(((ql.x >> ls) & 0x0F0F0F0Fu) | (((qh.x >> hs) << 4) & 0x30303030u),
+                                           ((ql.y >> ls) & 0x0F0F0F0Fu) | (((qh.y >> hs) << 4) & 0x30303030u),
+                                           ((ql.z >> ls) & 0x0F0F0F0Fu) | (((qh.z >> hs) << 4) & 0x30303030u),
+                                           ((ql.w >> ls) & 0x0F0F0F0Fu) | (((qh.w >> hs) << 4) & 0x30303030u));
                 const uint32_t sw = rr < 2 ? sw0 : sw1;
                 const int bi = 2 * (rr & 1) + hf;
-                const float ds = d * (float) (int8_t) (((sw >> (8 * bi)) & 0xFFu) ^ 0x80u);
-                const int sg = sg0 + 8 * h + 2 * rr + hf; // elements 128h + 32rr + 16hf + i
+                const float ds = d * ((float) ((sw >> (8 * bi)) & 0xFFu) - 128.0f);
+                const int g = sg0 + 4 * h + rr;
 #pragma unroll
                 for (int n = 0; n < NC; ++n) {
-                    const int g = n * nseg + sg;
-                    const float2 f = xf[g];
-                    float a = acc[n];
-                    a = fmaf(ds * f.x, (float) dot16i(v[rr], xq[g]), a);
-                    a = fmaf(-32.0f * ds, f.y, a);
-                    acc[n] = a;
+                    const int gi = n * xv.nseg + g;
+                    // this lane's 16-element half of the segment: planes and plain sum
+                    const uint4 * pl = reinterpret_cast<const uint4 *>(xv.xs + gi) + hf;
+                    const float * fp = reinterpret_cast<const float *>(xv.xf + gi);
+                    const int tq = dot16(v, pl[0], pl[2]);
+                    const float sum16 = fp[1 + hf];
+                    const float4 f = make_float4(fp[0], 0.0f, 0.0f, 0.0f);
+                    acc[n] = fmaf(ds, fmaf(f.x, (float) tq, -32.0f * sum16), acc[n]);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
         }
     }
 };
 
-template <int DT, int NC, int R>
-__global__ __launch_bounds__(64 * kMaxWaves) void k_matvec(MvLaunch L) {
-    using ST = Stepper<DT, R>;
-    using Raw = typename ST::Raw;
-    constexpr int S = ST::S;
-    constexpr int EPS = ST::EPS;
-    constexpr int D = ring_depth(sizeof(Raw)); // steps in flight per wave
-    extern __shared__ float lds[];
+// Q8_0 / Q4_0: a step is 8 blocks of 32; part p takes blocks p, p + P, ... of the step. Blocks past
+// the end of the row (K % 256 != 0) load block 0 and contribute with d = 0.
+template <int R>
+struct Fmt<Q8_0, R> {
+    static constexpr int P = 64 / R;
+    static constexpr int BL = 8 / P; // blocks per lane and step
+    struct Raw {
+        uint4 q[BL][2];
+        uint32_t d[BL];
+    };
+    const uint8_t * qb;
+    const uint8_t * db;
+    uint32_t qblk, qunit, dblk;
+    int64_t nb;
+    int p;
+    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int part, int64_t) {
+        p = part;
+        nb = nb_;
+        qb = w + (uint64_t) g0 * nb * 32 + (uint64_t) lr * 16;
+        db = w + (uint64_t) M * nb * 32 + (uint64_t) g0 * nb * 2 + (uint64_t) lr * 2;
+        qblk = (uint32_t) rs * 32;
+        qunit = (uint32_t) rs * 16;
+        dblk = (uint32_t) rs * 2;
+    }
+    __device__ Raw load(int64_t step) const {
+        Raw r;
+#pragma unroll
+        for (int i = 0; i < BL; ++i) {
+            int64_t b = step * 8 + p + P * i;
+            const bool ok = b < nb;
+            b = ok ? b : 0;
+            r.q[i][0] = load16(qb + (uint32_t) b * qblk);
+            r.q[i][1] = load16(qb + (uint32_t) b * qblk + qunit);
+            r.d[i] = ok ? load_half(db + (uint32_t) b * dblk) : 0u;
+        }
+        return r;
+    }
+    template <int NC>
+    __device__ void compute(const Raw & r, int sg0, const XView & xv, float * acc) const {
+#pragma unroll
+        for (int i = 0; i < BL; ++i) {
+            const float d = half_bits(r.d[i]);
+            const uint4 a = r.q[i][0], b = r.q[i][1];
+            const uint4 q0 = make_uint4(a.x ^ 0x80808080u, a.y ^ 0x80808080u, a.z ^ 0x80808080u, a.w ^ 0x80808080u);
+            const uint4 q1 = make_uint4(b.x ^ 0x80808080u, b.y ^ 0x80808080u, b.z ^ 0x80808080u, b.w ^ 0x80808080u);
+            const int g = sg0 + p + P * i;
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                const int gi = n * xv.nseg + g;
+                acc[n] = fmaf(d * xv.xf[gi].x, (float) dot32(q0, q1, xv.xs[gi]), acc[n]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+};
+
+template <int R>
+struct Fmt<Q4_0, R> {
+    static constexpr int P = 64 / R;
+    static constexpr int BL = 8 / P;
+    struct Raw {
+        uint4 q[BL];
+        uint32_t d[BL];
+    };
+    const uint8_t * qb;
+    const uint8_t * db;
+    uint32_t qblk, dblk;
+    int64_t nb;
+    int p;
+    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int part, int64_t) {
+        p = part;
+        nb = nb_;
+        qb = w + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
+        db = w + (uint64_t) M * nb * 16 + (uint64_t) g0 * nb * 2 + (uint64_t) lr * 2;
+        qblk = (uint32_t) rs * 16;
+        dblk = (uint32_t) rs * 2;
+    }
+    __device__ Raw load(int64_t step) const {
+        Raw r;
+#pragma unroll
+        for (int i = 0; i < BL; ++i) {
+            int64_t b = step * 8 + p + P * i;
+            const bool ok = b < nb;
+            b = ok ? b : 0;
+            r.q[i] = load16(qb + (uint32_t) b * qblk);
+            r.d[i] = ok ? load_half(db + (uint32_t) b * dblk) : 0u;
+        }
+        return r;
+    }
+    template <int NC>
+    __device__ void compute(const Raw & r, int sg0, const XView & xv, float * acc) const {
+#pragma unroll
+        for (int i = 0; i < BL; ++i) {
+            const float d = half_bits(r.d[i]);
+            const uint4 l = lo4(r.q[i]), h = hi4(r.q[i]); // elements 0..15, 16..31 of the block
+            const int g = sg0 + p + P * i;
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                const int gi = n * xv.nseg + g;
+                const float4 f = xv.xf[gi];
+                const int t = dot32(l, h, xv.xs[gi]);
+                acc[n] = fmaf(d, fmaf(f.x, (float) t, -8.0f * f.w), acc[n]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+};
+
+// ---- x conversion of one wave's chunk --------------------------------------------------------------
+// Lane l converts elements 8 (l % 4) .. +8 of segment l / 4 (16 segments per pass of the wave);
+// elements past K are zero.
+// Segment g (of nseg) of a wave's range, elements 8q .. 8q + 7 held by this lane in v (lanes
+// 4k .. 4k + 3 hold one segment): two int8 planes, the plane scale and the plain sums.
+__device__ __forceinline__ void convert_seg(const float (&v)[8], int g, int nseg, int q, XSeg * xs, float4 * xf) {
+    float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        sum += v[i];
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const float s16 = sum + __shfl_xor(sum, 1);
+    const float s32 = s16 + __shfl_xor(s16, 2);
+    const float s16o = __shfl_xor(s16, 2);
+    const float sc = amax * (1.0f / 127.0f);
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    const float invb = 253.0f * inv;
+    uint32_t pa[2], pb[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        uint32_t wa = 0, wb = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float t = v[4 * h + i];
+            const float qa = rintf(t * inv);                 // |qa| <= 127
+            const float qb = rintf(fmaf(-qa, sc, t) * invb); // |qb| <= 127 (253 < 254 leaves headroom)
+            wa |= ((uint32_t) (int) qa & 0xFFu) << (8 * i);
+            wb |= ((uint32_t) (int) qb & 0xFFu) << (8 * i);
+        }
+        pa[h] = wa;
+        pb[h] = wb;
+    }
+    if (g < nseg) {
+        uint8_t * sp = reinterpret_cast<uint8_t *>(xs + g);
+        *reinterpret_cast<uint2 *>(sp + 8 * q) = make_uint2(pa[0], pa[1]);
+        *reinterpret_cast<uint2 *>(sp + 32 + 8 * q) = make_uint2(pb[0], pb[1]);
+        if (q == 0) xf[g] = make_float4(sc * (1.0f / 253.0f), s16, s16o, s32);
+    }
+}
+
+// The wave's chunk of nseg segments starting at element e0, for NC columns. Lane l converts
+// elements 8 (l % 4) .. +8 of segment l / 4 (16 segments per pass); elements past K are zero.
+template <int NC>
+__device__ void convert_x(const MvArgs & A, const float * x, int64_t e0, int nseg, int lane, XSeg * xs, float4 * xf) {
+    const int q = lane & 3;
+    for (int base = 0; base < nseg; base += 16) {
+        const int g = base + (lane >> 2);
+        const int64_t e = e0 + 32 * (int64_t) g + 8 * q;
+#pragma unroll 1
+        for (int n = 0; n < NC; ++n) {
+            float v[8];
+            const float * xp = x + n * A.x_s1 + e;
+            if (g < nseg && e < A.K) {
+                if (A.xvec) {
+                    const float4 u = *reinterpret_cast<const float4 *>(xp);
+                    const float4 w = *reinterpret_cast<const float4 *>(xp + 4);
+                    v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+                    v[4] = w.x; v[5] = w.y; v[6] = w.z; v[7] = w.w;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[i] = xp[i];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+            }
+            convert_seg(v, g, nseg, q, xs + n * nseg, xf + n * nseg);
+        }
+    }
+}
+
+// Burst form for short wave ranges (<= SPW steps per wave, one column, one tile per work-group):
+// the wave first loads its x range, then issues every weight load, and only then converts x, so
+// the x round trip overlaps the weight round trip and a work-group costs about one HBM latency.
+template <int DT, int R, int W, int SPW>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_mvb(MvArgs A) {
+    using F = Fmt<DT, R>;
+    using Raw = typename F::Raw;
+    extern __shared__ uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int W = blockDim.x >> 6;
-    const int WT = L.wt;                  // waves per tile
-    const int GW = W / WT;                // tiles in flight per work-group
-    const int grp = wave / WT, wt = wave % WT;
-    const int r = lane % R, slot = lane / R;
+    const int r = lane % R, part = lane / R;
+
     const int64_t sl = blockIdx.y;
-    const int64_t i2 = sl % L.a.ne12, i3 = sl / L.a.ne12;
-    const int64_t K = L.a.K;
-    const uint64_t w_off = (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
-    const int64_t y_off = i2 * L.a.y_s2 + i3 * L.a.y_s3;
-    const float * x = L.a.x + i2 * L.a.x_s2 + i3 * L.a.x_s3;
-    // matrix of a tile (tiles of matrix j are [tstart[j], tstart[j + 1]))
-    auto mat_of = [&](int64_t tile) { return tile >= L.tstart[1] ? (tile >= L.tstart[2] ? 2 : 1) : 0; };
-    // tiles of this work-group: iteration it, group g -> tile (it * gridDim.x + blockIdx.x) * GW + g
-    const int64_t per_iter = (int64_t) gridDim.x * GW;
-    const int64_t iters = (L.tiles + per_iter - 1) / per_iter;
-    auto tile_of = [&](int64_t it) { return (it * gridDim.x + blockIdx.x) * GW + grp; };
-    // the lane's addressing for the tile of iteration it (live: its row exists)
-    auto stepper_of = [&](int64_t it, ST & st) -> bool {
-        const int64_t tile = tile_of(it);
-        if (tile >= L.tiles) return false;
-        const int j = mat_of(tile);
-        const int64_t M = L.Mm[j], m0 = (tile - L.tstart[j]) * R;
-        if (m0 + r >= M) return false;
+    const int64_t i2 = sl % A.ne12, i3 = sl / A.ne12;
+    const uint64_t w_off = (uint64_t) (i2 / A.r2) * A.w_s2 + (uint64_t) (i3 / A.r3) * A.w_s3;
+    const float * x = A.x + i2 * A.x_s2 + i3 * A.x_s3;
+
+    const int64_t tile = blockIdx.x;
+    const int j = tile >= A.tstart[1] ? (tile >= A.tstart[2] ? 2 : 1) : 0;
+    const int64_t M = A.M[j];
+    const int64_t m0 = (tile - A.tstart[j]) * R;
+    const int64_t g0 = m0 & ~(int64_t) 31;
+    const int rs = (int) min<int64_t>(32, M - g0);
+    const int lr = m0 + r < M ? (int) (m0 - g0) + r : rs - 1; // dead lanes read a real row and drop it
+
+    const int64_t s0 = A.nst * wave / W, s1 = A.nst * (wave + 1) / W;
+    const int ns = (int) (s1 - s0);
+
+    // x: lane l holds elements 8 (l % 4) .. +8 of segment l / 4 + 16 p of the wave's range (pass p)
+    constexpr int XP = (SPW * kSegs + 15) / 16; // passes of 16 segments
+    float xv[XP][8];
+    const int nseg = ns * kSegs;
+#pragma unroll
+    for (int p = 0; p < XP; ++p) {
+        const int g = 16 * p + (lane >> 2);
+        const int64_t e = s0 * kStep + 32 * (int64_t) g + 8 * (lane & 3);
+        if (g < nseg && e < A.K) {
+            const float4 u = *reinterpret_cast<const float4 *>(x + e);
+            const float4 w = *reinterpret_cast<const float4 *>(x + e + 4);
+            xv[p][0] = u.x; xv[p][1] = u.y; xv[p][2] = u.z; xv[p][3] = u.w;
+            xv[p][4] = w.x; xv[p][5] = w.y; xv[p][6] = w.z; xv[p][7] = w.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[p][i] = 0.0f;
+        }
+    }
+
+    F f;
+    f.init(A.w[j] + w_off, M, A.nb, g0, rs, lr, part, 0);
+    Raw buf[SPW];
+#pragma unroll
+    for (int i = 0; i < SPW; ++i)
+        if (i < ns) buf[i] = f.load(s0 + i);
+
+    XSeg * xs = reinterpret_cast<XSeg *>(lds) + (size_t) wave * SPW * kSegs;
+    float4 * xf = reinterpret_cast<float4 *>(reinterpret_cast<XSeg *>(lds) + (size_t) W * SPW * kSegs) + (size_t) wave * SPW * kSegs;
+    float * red = reinterpret_cast<float *>(reinterpret_cast<float4 *>(reinterpret_cast<XSeg *>(lds) + (size_t) W * SPW * kSegs) +
+                                            (size_t) W * SPW * kSegs);
+#pragma unroll
+    for (int p = 0; p < XP; ++p) convert_seg(xv[p], 16 * p + (lane >> 2), nseg, lane & 3, xs, xf);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+
+    float acc[1] = {0.0f};
+    const XView xw{xs, xf, nseg};
+#pragma unroll
+    for (int i = 0; i < SPW; ++i)
+        if (i < ns) f.template compute<1>(buf[i], i * kSegs, xw, acc);
+
+#pragma unroll
+    for (int off = R; off < 64; off <<= 1) acc[0] += __shfl_xor(acc[0], off);
+    if (part == 0) red[wave * R + r] = acc[0];
+    __syncthreads();
+    if (tid < R) {
+        const int64_t m = m0 + tid;
+        if (m < M) {
+            float v = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < W; ++w2) v += red[w2 * R + tid];
+            A.y[j][i2 * A.y_s2 + i3 * A.y_s3 + m] = v;
+        }
+    }
+}
+
+// One work-group walks tiles blockIdx.x, blockIdx.x + gridDim.x, ... (persistent). Its waves keep
+// the same K range for every tile, so each converts its x range once (when the range fits the LDS
+// budget; otherwise per chunk of cs steps and tile). The next step's loads (of this tile or the
+// first of the next) are in flight while the current step is computed.
+template <int DT, int NC, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_mvs(MvArgs A) {
+    constexpr int R = 16;
+    using F = Fmt<DT, R>;
+    using Raw = typename F::Raw;
+    extern __shared__ uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane % R, part = lane / R;
+
+    const int64_t sl = blockIdx.y;
+    const int64_t i2 = sl % A.ne12, i3 = sl / A.ne12;
+    const uint64_t w_off = (uint64_t) (i2 / A.r2) * A.w_s2 + (uint64_t) (i3 / A.r3) * A.w_s3;
+    const float * x = A.x + i2 * A.x_s2 + i3 * A.x_s3;
+
+    // the lane's row of a tile (dead lanes of a partial last tile read a real row and drop it)
+    struct Row {
+        int j;
+        int64_t M, m0;
+    };
+    auto row_of = [&](int64_t tile, F & f) -> Row {
+        const int j = tile >= A.tstart[1] ? (tile >= A.tstart[2] ? 2 : 1) : 0;
+        const int64_t M = A.M[j];
+        const int64_t m0 = (tile - A.tstart[j]) * R;
         const int64_t g0 = m0 & ~(int64_t) 31;
-        st.init(L.wm[j] + w_off, M, L.a.nb, g0, (int) min<int64_t>(32, M - g0), (int) (m0 - g0) + r, slot);
-        return true;
+        const int rs = (int) min<int64_t>(32, M - g0);
+        const int lr = m0 + r < M ? (int) (m0 - g0) + r : rs - 1;
+        f.init(A.w[j] + w_off, M, A.nb, g0, rs, lr, part, 0);
+        return Row{j, M, m0};
     };
 
-    Raw ring[D];
-    ST cur, nxt;
+    // this wave's steps, the same for every tile
+    const int64_t s0 = A.nst * wave / W, s1 = A.nst * (wave + 1) / W;
+    const int ns = (int) (s1 - s0);
+    const int cs = A.cs;
+    const bool once = cs >= ns;
+    XSeg * xs = reinterpret_cast<XSeg *>(lds) + (size_t) wave * cs * kSegs * NC;
+    float4 * xf = reinterpret_cast<float4 *>(reinterpret_cast<XSeg *>(lds) + (size_t) W * cs * kSegs * NC) + (size_t) wave * cs * kSegs * NC;
+    float * red = reinterpret_cast<float *>(reinterpret_cast<float4 *>(reinterpret_cast<XSeg *>(lds) + (size_t) W * cs * kSegs * NC) +
+                                            (size_t) W * cs * kSegs * NC); // [2][W][NC][R]
 
-    for (int64_t kc0 = 0; kc0 < K; kc0 += L.kc) {
-        const int xlen = (int) min<int64_t>(L.kc, K - kc0);
-        const int64_t st0 = kc0 / EPS;
-        const int nst = (int) ((kc0 + xlen + EPS - 1) / EPS - st0); // steps of this chunk
-        const int nw = wt < nst ? (nst - wt + WT - 1) / WT : 0;      // this wave's steps per tile
-        const int nwp = (nw + D - 1) / D * D;                        // padded to whole ring turns
-        bool live = stepper_of(0, cur);
-        bool live_n = stepper_of(1, nxt);
-        // weight loads first: they do not depend on x and overlap the staging below
-        if (live) {
+    int64_t tile = blockIdx.x;
+    F f, fn;
+    Row row = row_of(tile, f);
+    // two steps in registers: the next step's loads (possibly of the next tile) are issued before
+    // the current step's math
+    Raw cur;
+    if (ns > 0) cur = f.load(s0);
+    if (once && ns > 0) convert_x<NC>(A, x, s0 * kStep, ns * kSegs, lane, xs, xf);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+
+    for (int it = 0; tile < A.tiles; ++it) {
+        const int64_t ntile = tile + gridDim.x;
+        const bool has_n = ntile < A.tiles;
+        Row nrow{};
+        if (has_n) nrow = row_of(ntile, fn);
+
+        float acc[NC];
 #pragma unroll
-            for (int j = 0; j < D; ++j)
-                if (j < nw) ring[j] = cur.load(st0 + wt + (int64_t) WT * j);
+        for (int n = 0; n < NC; ++n) acc[n] = 0.0f;
+        for (int k = 0; k < ns; ++k) {
+            if (!once && k % cs == 0) {
+                // a new x chunk: steps [k, k + cs) of this wave
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                convert_x<NC>(A, x, (s0 + k) * kStep, min(cs, ns - k) * kSegs, lane, xs, xf);
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+            }
+            Raw nxt;
+            if (k + 1 < ns) {
+                nxt = f.load(s0 + k + 1);
+            } else if (has_n) {
+                nxt = fn.load(s0);
+            }
+            const XView xv{xs, xf, min(cs, ns - (k / cs) * cs) * kSegs};
+            f.template compute<NC>(cur, (k % cs) * kSegs, xv, acc);
+            cur = nxt;
         }
 
-        const int nseg = xlen / 16;
-        XSeg * xq = reinterpret_cast<XSeg *>(lds);
-        float2 * xf = reinterpret_cast<float2 *>(xq + NC * nseg);
-        float * red = reinterpret_cast<float *>(xf + NC * nseg); // [2][W][NC][R]
-        __syncthreads(); // the previous chunk is consumed
-        // one thread per (column, segment): two int8 planes, the plane scale and the plain sum
-        for (int i = tid; i < NC * nseg; i += blockDim.x) {
-            const int n = i / nseg, sg = i - n * nseg;
-            const float * xp = x + n * L.a.x_s1 + kc0 + 16 * sg;
-            float v[16];
-            float amax = 0.0f, sum = 0.0f;
+        // parts of a row (lanes r, r + R, ...), then the waves in order
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                v[e] = xp[e];
-                amax = fmaxf(amax, fabsf(v[e]));
-                sum += v[e];
-            }
-            const float s1 = amax * (1.0f / 127.0f);
-            const float inv1 = amax > 0.0f ? 127.0f / amax : 0.0f;
-            uint32_t pa[4] = {0, 0, 0, 0}, pb[4] = {0, 0, 0, 0};
+        for (int off = R; off < 64; off <<= 1) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float qa = fminf(127.0f, fmaxf(-127.0f, rintf(v[e] * inv1)));
-                const float res = fmaf(-qa, s1, v[e]);
-                const float qb = fminf(127.0f, fmaxf(-127.0f, rintf(res * (256.0f * inv1))));
-                pa[e >> 2] |= ((uint32_t) (int) qa & 0xFFu) << (8 * (e & 3));
-                pb[e >> 2] |= ((uint32_t) (int) qb & 0xFFu) << (8 * (e & 3));
-            }
-            XSeg xs_;
-            xs_.a = make_uint4(pa[0], pa[1], pa[2], pa[3]);
-            xs_.b = make_uint4(pb[0], pb[1], pb[2], pb[3]);
-            xq[i] = xs_;
-            xf[i] = make_float2(s1 * (1.0f / 256.0f), sum);
+            for (int n = 0; n < NC; ++n) acc[n] += __shfl_xor(acc[n], off);
+        }
+        float * rb = red + (it & 1) * (W * NC * R);
+        if (part == 0) {
+#pragma unroll
+            for (int n = 0; n < NC; ++n) rb[(wave * NC + n) * R + r] = acc[n];
         }
         __syncthreads();
-
-        for (int64_t it = 0; it < iters; ++it) {
-            float acc[NC];
+        if (tid < NC * R) {
+            const int n = tid / R, rr = tid % R;
+            const int64_t m = row.m0 + rr;
+            if (m < row.M) {
+                float v = 0.0f;
 #pragma unroll
-            for (int n = 0; n < NC; ++n) acc[n] = 0.0f;
-            for (int i = 0; i < nwp; i += D) {
-#pragma unroll
-                for (int j = 0; j < D; ++j) {
-                    const int ii = i + j;
-                    if (live && ii < nw) cur.template compute<NC>(ring[j], st0 + wt + (int64_t) WT * ii, kc0, xq, xf, nseg, acc);
-                    // refill this ring slot with the item D ahead (possibly of the next tile)
-                    const int ni = ii + D;
-                    if (ni < nwp) {
-                        if (live && ni < nw) ring[j] = cur.load(st0 + wt + (int64_t) WT * ni);
-                    } else if (live_n && ni - nwp < nw) {
-                        ring[j] = nxt.load(st0 + wt + (int64_t) WT * (ni - nwp));
-                    }
-                }
+                for (int w2 = 0; w2 < W; ++w2) v += rb[(w2 * NC + n) * R + rr];
+                A.y[row.j][i2 * A.y_s2 + i3 * A.y_s3 + n * A.ys1[row.j] + m] = v;
             }
-            // slots of a row: lanes r, r + R, ... (fixed butterfly order)
-#pragma unroll
-            for (int off = R; off < 64; off <<= 1) {
-#pragma unroll
-                for (int n = 0; n < NC; ++n) acc[n] += __shfl_xor(acc[n], off);
-            }
-            float * rb = red + (it & 1) * (W * NC * R);
-            if (slot == 0) {
-#pragma unroll
-                for (int n = 0; n < NC; ++n) rb[(wave * NC + n) * R + r] = acc[n];
-            }
-            __syncthreads();
-            if (tid < GW * NC * R) {
-                const int g = tid / (NC * R), n = (tid / R) % NC, rr = tid % R;
-                const int64_t t2 = (it * gridDim.x + blockIdx.x) * GW + g;
-                const int jm = mat_of(t2);
-                const int64_t m = (t2 - L.tstart[jm]) * R + rr;
-                if (t2 < L.tiles && m < L.Mm[jm]) {
-                    float v = 0.0f;
-                    for (int w2 = 0; w2 < WT; ++w2) v += rb[((g * WT + w2) * NC + n) * R + rr];
-                    float * yp = L.ym[jm] + y_off + n * L.ys1[jm] + m;
-                    *yp = kc0 == 0 ? v : *yp + v;
-                }
-            }
-            cur = nxt;
-            live = live_n;
-            live_n = stepper_of(it + 2, nxt);
         }
+        tile = ntile;
+        row = nrow;
+        f = fn;
     }
 }
 
 template <int DT, int R>
-void * pick_nc(int nc) {
-    switch (nc) {
-        case 1: return (void *) k_matvec<DT, 1, R>;
-        case 2: return (void *) k_matvec<DT, 2, R>;
-        case 3: return (void *) k_matvec<DT, 3, R>;
-        case 4: return (void *) k_matvec<DT, 4, R>;
-        case 5: return (void *) k_matvec<DT, 5, R>;
-        case 6: return (void *) k_matvec<DT, 6, R>;
-        case 7: return (void *) k_matvec<DT, 7, R>;
-        default: return (void *) k_matvec<DT, 8, R>;
-    }
+void * pick_burst_r(int W, int spw) {
+    if (spw <= 2) return W >= 16 ? (void *) k_mvb<DT, R, 16, 2> : W >= 8 ? (void *) k_mvb<DT, R, 8, 2> : (void *) k_mvb<DT, R, 4, 2>;
+    return W >= 16 ? (void *) k_mvb<DT, R, 16, 4> : W >= 8 ? (void *) k_mvb<DT, R, 8, 4> : (void *) k_mvb<DT, R, 4, 4>;
 }
 
 template <int DT>
-void * pick(int nc, int R) {
-    return R == 32 ? pick_nc<DT, 32>(nc) : R == 16 ? pick_nc<DT, 16>(nc) : pick_nc<DT, 8>(nc);
+void * pick_burst(int W, int spw, int R) {
+    if constexpr (DT == Q6_K || DT == Q8_0) {
+        if (R == 32 && spw <= 2) return W >= 16 ? (void *) k_mvb<DT, 32, 16, 2> : W >= 8 ? (void *) k_mvb<DT, 32, 8, 2> : (void *) k_mvb<DT, 32, 4, 2>;
+        return pick_burst_r<DT, 16>(W, spw);
+    } else {
+        return R == 32 ? pick_burst_r<DT, 32>(W, spw) : pick_burst_r<DT, 16>(W, spw);
+    }
+}
+
+// streaming variants: W = 8 for one column, 4 for several
+template <int DT>
+void * pick(int nc) {
+    switch (nc) {
+        case 1: return (void *) k_mvs<DT, 1, 8>;
+        case 2: return (void *) k_mvs<DT, 2, 4>;
+        case 3: return (void *) k_mvs<DT, 3, 4>;
+        case 4: return (void *) k_mvs<DT, 4, 4>;
+        case 5: return (void *) k_mvs<DT, 5, 4>;
+        case 6: return (void *) k_mvs<DT, 6, 4>;
+        case 7: return (void *) k_mvs<DT, 7, 4>;
+        default: return (void *) k_mvs<DT, 8, 4>;
+    }
+}
+
+// resident work-groups per CU of a kernel at a block size and dynamic LDS (cached per thread)
+int occupancy(void * fn, int threads, size_t lds) {
+    struct Key {
+        void * fn;
+        size_t lds;
+        int n;
+    };
+    thread_local std::vector<Key> cache;
+    for (const Key & k : cache)
+        if (k.fn == fn && k.lds == lds) return k.n;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess || n < 1) n = 1;
+    cache.push_back({fn, lds, n});
+    return n;
+}
+
+int tuning(const char * name, int dflt) {
+    const char * v = std::getenv(name);
+    return v != nullptr && *v ? std::atoi(v) : dflt;
 }
 
 const char * name_of(int dt, int nmat) {
@@ -534,128 +743,105 @@ const char * name_of(int dt, int nmat) {
     }
 }
 
-// tuning overrides from the environment (read once; 0 / unset = automatic)
-int tuning(const char * name, int dflt) {
-    const char * v = std::getenv(name);
-    return v != nullptr && *v ? std::atoi(v) : dflt;
-}
-
-// resident work-groups per CU of a kernel at a block size and dynamic LDS (cached per thread)
-int occupancy(void * fn, int threads, size_t lds) {
-    struct Key {
-        void * fn;
-        size_t lds;
-        int n;
-    };
-    thread_local std::vector<Key> cache;
-    for (const Key & k : cache)
-        if (k.fn == fn && k.lds == lds) return k.n;
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess || n < 1) n = 1;
-    cache.push_back({fn, lds, n});
-    return n;
-}
-
-int tasks_of(int dt) {
-    return dt == Q4_0 ? 1 : dt == Q8_0 ? 2 : dt == Q4_K ? 8 : 4;
-}
-
-template <int R>
-size_t raw_bytes_r(int dt) {
-    return dt == Q4_0 ? sizeof(typename Stepper<Q4_0, R>::Raw) : dt == Q8_0 ? sizeof(typename Stepper<Q8_0, R>::Raw)
-         : dt == Q4_K ? sizeof(typename Stepper<Q4_K, R>::Raw) : sizeof(typename Stepper<Q6_K, R>::Raw);
-}
-
-size_t raw_bytes_of(int dt, int R) {
-    return R == 32 ? raw_bytes_r<32>(dt) : R == 16 ? raw_bytes_r<16>(dt) : raw_bytes_r<8>(dt);
-}
-
 } // namespace
 
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
-                         uint64_t * grid_size) {
+                          uint64_t * grid_size) {
+    constexpr int R = 16;
     if (nmat < 1 || nmat > 3) return hipErrorInvalidValue;
     const MatArgs & a = mats[0];
-    int64_t m_total = 0;
     for (int j = 0; j < nmat; ++j) {
         if (mats[j].dtype != a.dtype || mats[j].K != a.K || mats[j].N != a.N || (nmat > 1 && mats[j].ne12 * mats[j].ne13 != 1)) {
             return hipErrorInvalidValue;
         }
-        m_total += mats[j].M;
     }
     const int nc = (int) a.N;
-    if (nc < 1 || nc > 8) return hipErrorInvalidValue;
+    if (nc < 1 || nc > 8 || a.K <= 0 || a.K % 32 != 0) return hipErrorInvalidValue;
     const int64_t slices = a.ne12 * a.ne13;
-    if (slices > 65535) return hipErrorInvalidValue;
-    const int T = tasks_of(a.dtype);
-    const int be = a.dtype == Q4_K || a.dtype == Q6_K ? 256 : 32;
-    // x chunk: as much of K as fits the LDS budget, in whole steps (of the smallest row tile)
-    const int eps_max = (64 / 8 > T ? 64 / 8 / T : 1) * be;
-    const int64_t max_kc = std::max<int64_t>(eps_max, (int64_t) (kLdsBudget / (3 * nc)) / eps_max * eps_max); // 2 B + 8/16 B per element
-    MvLaunch L;
-    L.a = a;
-    L.kc = std::min<int64_t>(a.K, max_kc);
-    // persistent grid: as many 8-wave work-groups as stay resident (occupancy of the chosen kernel
-    // with its LDS; SCRAPGPU_HIP_MV_WGS overrides the per-CU count), shared among the slices
-    const int waves = kMaxWaves;
-    auto pick_fn = [&](int R) -> void * {
-        switch (a.dtype) {
-            case Q4_0: return pick<Q4_0>(nc, R);
-            case Q8_0: return pick<Q8_0>(nc, R);
-            case Q4_K: return pick<Q4_K>(nc, R);
-            case Q6_K: return pick<Q6_K>(nc, R);
-            default: return nullptr;
-        }
-    };
-    auto lds_of = [&](int R) { return (size_t) nc * (L.kc / 16) * (32 + 8) + (size_t) 2 * waves * nc * R * sizeof(float); };
-    auto resident = [&](int R) -> int64_t {
-        int per_cu = tuning("SCRAPGPU_HIP_MV_WGS", 0);
-        if (per_cu <= 0) per_cu = occupancy(pick_fn(R), 64 * waves, lds_of(R));
-        return std::max<int64_t>(1, (int64_t) std::max(1, per_cu) * cu_count / slices);
-    };
-    // row tile: the largest (32, 16, 8) that still gives every wave group >= 2 tiles; the waves of
-    // a group split the K steps while each keeps >= 2 ring turns
-    int R = 8, WT = 1;
-    int64_t wgs = 1;
-    for (int cand : {32, 16, 8}) {
-        const int S = 64 / cand;
-        const int eps = (S > T ? S / T : 1) * be;
-        const int D = ring_depth(raw_bytes_of(a.dtype, cand));
-        const int64_t nst = (L.kc + eps - 1) / eps;
-        int wt = 1;
-        while (wt < waves && nst % (2 * wt) == 0 && (nst / (2 * wt)) % D == 0 && nst / (2 * wt) >= 2 * D) wt *= 2;
-        int64_t tiles = 0;
-        for (int j = 0; j < nmat; ++j) tiles += (mats[j].M + cand - 1) / cand;
-        R = cand;
-        WT = wt;
-        wgs = resident(cand);
-        if (tiles >= 2 * wgs * (waves / wt)) break;
-    }
-    if (const int fr = tuning("SCRAPGPU_HIP_MV_R", 0)) R = fr;
-    if (const int fw = tuning("SCRAPGPU_HIP_MV_WT", 0)) WT = fw;
-    L.wt = WT;
-    L.nmat = nmat;
+    if (slices < 1 || slices > 65535) return hipErrorInvalidValue;
+    const int dt = a.dtype;
+    if (dt != Q4_0 && dt != Q8_0 && dt != Q4_K && dt != Q6_K) return hipErrorInvalidValue;
+    int64_t rows = 0;
+    for (int j = 0; j < nmat; ++j) rows += mats[j].M;
+
+    MvArgs L;
     L.tstart[0] = 0;
     for (int j = 0; j < 3; ++j) {
         const bool has = j < nmat;
-        L.wm[j] = has ? mats[j].w : nullptr;
-        L.Mm[j] = has ? mats[j].M : 0;
-        L.ym[j] = has ? mats[j].y : nullptr;
+        L.w[j] = has ? mats[j].w : nullptr;
+        L.M[j] = has ? mats[j].M : 0;
+        L.y[j] = has ? mats[j].y : nullptr;
         L.ys1[j] = has ? mats[j].y_s1 : 0;
         L.tstart[j + 1] = L.tstart[j] + (has ? (mats[j].M + R - 1) / R : 0);
     }
-    for (int j = nmat + 1; j < 4; ++j) L.tstart[j] = INT64_MAX; // tiles past the last matrix never map there
-    L.tiles = L.tstart[nmat];
-    (void) m_total;
-    wgs = resident(R);
-    const int64_t grid_x = std::max<int64_t>(1, std::min<int64_t>(wgs, (L.tiles + (waves / WT) - 1) / (waves / WT)));
-    const size_t lds = lds_of(R);
-    void * fn = pick_fn(R);
-    if (fn == nullptr) return hipErrorInvalidValue;
-    if (kernel_name) *kernel_name = name_of(a.dtype, nmat);
+    for (int j = nmat + 1; j < 4; ++j) L.tstart[j] = INT64_MAX;
+    const int64_t tiles = L.tstart[nmat];
+    if (tiles < 1 || tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
+    const int64_t nst = (a.K + kStep - 1) / kStep;
+    L.K = a.K;
+    L.nb = a.K / (dt == Q4_K || dt == Q6_K ? 256 : 32);
+    L.nst = nst;
+    L.x = a.x;
+    L.x_s1 = a.x_s1;
+    L.x_s2 = a.x_s2;
+    L.x_s3 = a.x_s3;
+    L.w_s2 = a.w_s2;
+    L.w_s3 = a.w_s3;
+    L.y_s2 = a.y_s2;
+    L.y_s3 = a.y_s3;
+    L.ne12 = a.ne12;
+    L.r2 = a.r2;
+    L.r3 = a.r3;
+    L.xvec = ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (a.x_s1 & 3) == 0 && (a.x_s2 & 3) == 0 && (a.x_s3 & 3) == 0) ? 1 : 0;
+    L.tiles = tiles;
+
+    // burst form (one column, K <= 64 steps): every wave's steps (<= 4) loaded at once, one tile
+    // per work-group. 32-row tiles for large products (fewer x conversions per weight, 512-byte
+    // runs), 16-row tiles otherwise (more work-groups). 2 steps per wave up to K = 16 steps, then
+    // 4 (the 32-row Q6_K / Q8_0 forms hold too many registers at 4 steps: 16 rows there).
+    if (nc == 1 && L.xvec && nst <= 64 && tuning("SCRAPGPU_HIP_MV_BURST", 1)) {
+        int Rb = rows * slices >= (int64_t) 64 * cu_count ? 32 : 16;
+        const int sp = nst <= 32 ? 2 : 4;
+        int Wb = 4;
+        while (Wb < 16 && (nst + Wb - 1) / Wb > sp) Wb *= 2;
+        if (sp == 4 && (dt == Q6_K || dt == Q8_0)) Rb = 16;
+        if (const int fr = tuning("SCRAPGPU_HIP_MV_R", 0)) Rb = fr == 32 ? 32 : 16;
+        L.tstart[0] = 0;
+        for (int j = 0; j < 3; ++j) L.tstart[j + 1] = j < nmat ? L.tstart[j] + (mats[j].M + Rb - 1) / Rb : INT64_MAX;
+        const int64_t btiles = L.tstart[nmat];
+        L.tiles = btiles;
+        L.cs = sp;
+        const size_t lds = (size_t) Wb * sp * kSegs * (sizeof(XSeg) + sizeof(float4)) + (size_t) Wb * Rb * sizeof(float);
+        void * fn = dt == Q4_0 ? pick_burst<Q4_0>(Wb, sp, Rb) : dt == Q8_0 ? pick_burst<Q8_0>(Wb, sp, Rb)
+                  : dt == Q4_K ? pick_burst<Q4_K>(Wb, sp, Rb) : pick_burst<Q6_K>(Wb, sp, Rb);
+        if (kernel_name) *kernel_name = name_of(dt, nmat);
+        if (grid_size) *grid_size = (uint64_t) btiles * (uint64_t) slices;
+        void * args[] = {&L};
+        return hipLaunchKernel(fn, dim3((unsigned) btiles, (unsigned) slices), dim3((unsigned) (64 * Wb)), args, lds, stream);
+    }
+
+    // streaming form (several columns, or K too long for the burst form)
+    const int W = nc == 1 ? 8 : 4;
+    // x chunk per wave: all of the wave's steps when they fit the LDS budget, else as many as fit
+    const int64_t step_bytes = (int64_t) kSegs * nc * (sizeof(XSeg) + sizeof(float4));
+    const int64_t per_wave = std::max<int64_t>(1, (nst + W - 1) / W);
+    const int64_t cs = std::min<int64_t>(per_wave, std::max<int64_t>(1, kLdsX / W / step_bytes));
+    L.cs = (int) cs;
+    const size_t lds = (size_t) W * cs * step_bytes + (size_t) 2 * W * nc * R * sizeof(float);
+    if (lds > (size_t) 160 * 1024) return hipErrorInvalidValue;
+    void * fn = dt == Q4_0 ? pick<Q4_0>(nc) : dt == Q8_0 ? pick<Q8_0>(nc) : dt == Q4_K ? pick<Q4_K>(nc) : pick<Q6_K>(nc);
+
+    // persistent grid: as many work-groups as stay resident (at most one per tile), trimmed so
+    // that every work-group gets the same number of tiles
+    const int per_cu = std::max(1, tuning("SCRAPGPU_HIP_MV_WGS", occupancy(fn, 64 * W, lds)));
+    const int64_t cap = std::max<int64_t>(1, (int64_t) per_cu * cu_count / slices);
+    const int64_t rounds = (tiles + cap - 1) / cap;
+    const int64_t grid_x = (tiles + rounds - 1) / rounds;
+
+    if (kernel_name) *kernel_name = name_of(dt, nmat);
     if (grid_size) *grid_size = (uint64_t) grid_x * (uint64_t) slices;
     void * args[] = {&L};
-    return hipLaunchKernel(fn, dim3((unsigned) grid_x, (unsigned) slices), dim3((unsigned) (64 * waves)), args, lds, stream);
+    return hipLaunchKernel(fn, dim3((unsigned) grid_x, (unsigned) slices), dim3((unsigned) (64 * W)), args, lds, stream);
 }
 
 } // namespace sgk
