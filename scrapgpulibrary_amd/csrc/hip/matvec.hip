@@ -4,35 +4,46 @@
 // (src/backends/opencl11/kernels/mul_mv_r.cl:240-287), k_mvr_q4_k / k_mvr_q6_k (mul_mv_k.cl:396-450)
 // and, for 2-3 weights sharing x, k_mvm_* (mul_mv_multi.cl:46-99). Same products, new design.
 //
-// Work decomposition. A work-group owns a tile of R rows (R = 16 or 32, inside one R32 group of
-// 32 rows) and all of K. Its W waves split K into contiguous ranges of steps (a step = 256
-// elements), so a wave only needs its own part of x, which it converts into its private LDS
-// region; the waves meet once, at the end, to add their partial row sums in a fixed order.
+// Work decomposition. A work-group owns a tile of 16 * RG rows (inside one R32 group of 32 rows)
+// and all of K. Its W waves split K into contiguous ranges of steps (a step = 256 elements), so a
+// wave only needs its own part of x, which it converts into its private LDS region; the waves
+// meet once per tile, at the end, to add their partial row sums in a fixed order.
 //
-// Inside a wave, lane l serves row r = l % R through part p = l / R (P = 64 / R parts). A step's
-// bytes of one row are dealt to the parts by whole scale groups, so one 128-bit wave load reads P
-// runs of 16 * R contiguous bytes of one R32 unit area (256 B or 512 B): coalesced.
+// Inside a wave, lane l serves row r = l % 16 (of each 16-row group) through part p = l / 16. A
+// step's bytes of one row are dealt to the 4 parts by whole scale groups, so one 128-bit wave load
+// reads four runs of 256 contiguous bytes of one R32 unit area.
 //
-// Two forms:
-//  * burst (N = 1, K <= 64 steps): one tile per work-group, at most 4 steps per wave; the wave
-//    loads its x range, then issues every weight load, and only then converts x, so the x round
-//    trip hides under the weight round trip. No loop-carried state: few registers, 4-8 waves per
-//    SIMD, and the hardware dispatcher streams the work-groups.
-//  * streaming (N > 1, or longer K): a persistent grid; each work-group walks tiles, its waves
-//    convert their x range once (when it fits the LDS budget) and keep the next step's loads in
-//    flight while computing the current one.
+// Integer dot products on the matrix cores. x is converted to int8 (below); the weights' integer
+// codes (nibbles, 6-bit values, bytes) are unpacked to int8 in registers. One
+// v_mfma_i32_16x16x64_i8 then takes the 16 rows' codes as its B operand (lane (r, p) supplies 16
+// codes of row r: column r, k-group p) and x as its A operand. A decode product has only one x
+// column, so the 16 rows of A are used to keep apart what must be scaled separately: row 4c + k
+// of A holds, for k-group c only, plane k % 2 of x over the scale group that lane group c needs
+// (k / 2 selects one of two scale groups), and zeros elsewhere. After the 4 MFMAs of a step, lane
+// (r, p) finds in its 4 accumulator registers (rows 4p .. 4p + 3 of D, column r) exactly the 2 x 2
+// integer sums its part needs, and applies the block scales once per scale group. Per 64 weights a
+// lane spends ~30 VALU operations (unpack + scales) instead of ~110 with VALU dot products, which
+// leaves the VALU idle enough to overlap the HBM stream.
 //
 // x conversion. Every 32-element segment of x is stored as two int8 planes a, b and a scale s
 // (s = max|x| / 127): x ~= s * a + (s / 253) * b, plus the plain sums of its two 16-element
-// halves. A weight run then costs one sdot4 per 4 weights and plane:
+// halves:
 //   sum_i q_i x_i ~= (s / 253) * (253 * sum q a + sum q b)
-// with block scales factored out and each format's constant offset applied once per run through
-// the segment sums:
+// with each format's constant offset applied once per scale group through the segment sums:
 //   Q4_0: d * (sum q x - 8 sum x)            Q8_0: d * sum q x      (q = stored byte xor 0x80)
 //   Q4_K: d*sc * sum q x - dmin*m * sum x    Q6_K: d*sc * (sum q x - 32 sum x)
 // The two planes carry ~15 significant bits of each x relative to its segment's largest |x|, so
 // the product differs from the fp32 reference by ~1e-5 of max|x| per term, well inside the
 // NMSE <= 1e-7 bound of the decode path.
+//
+// Two forms:
+//  * burst (N = 1, K <= 64 steps): one tile per work-group, at most 4 steps per wave; the wave
+//    loads its x range, then issues every weight load, and only then converts x, so the x round
+//    trip hides under the weight round trip. No loop-carried state: few registers, many waves per
+//    SIMD, and the hardware dispatcher streams the work-groups.
+//  * streaming (N > 1, or longer K): a persistent grid; each work-group walks tiles, its waves
+//    convert their x range once (when it fits the LDS budget) and keep the next step's loads in
+//    flight while computing the current one.
 #include "kernels.h"
 
 #include <hip/hip_fp16.h>
@@ -45,8 +56,10 @@
 namespace sgk {
 namespace {
 
-constexpr int kStep = 256;     // K elements per step
-constexpr int kSegs = 8;       // 32-element x segments per step
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kStep = 256;       // K elements per step
+constexpr int kSegs = 8;         // 32-element x segments per step
 constexpr int kLdsX = 64 * 1024; // bytes of converted x per work-group (all waves)
 
 struct MvArgs {
@@ -61,9 +74,9 @@ struct MvArgs {
     uint64_t w_s2, w_s3;
     int64_t y_s2, y_s3;
     int64_t ne12, r2, r3;
-    int cs;   // steps per x chunk of one wave
     int64_t tiles; // row tiles over all matrices
-    int xvec; // x columns are 16-byte aligned: float4 loads
+    int cs;        // steps per x chunk of one wave
+    int xvec;      // x columns are 16-byte aligned: float4 loads
 };
 
 __device__ __forceinline__ float half_bits(uint32_t h) {
@@ -78,82 +91,70 @@ __device__ __forceinline__ uint32_t load_half(const uint8_t * p) {
     return *reinterpret_cast<const uint16_t *>(p);
 }
 
-// one x segment in LDS: a plane (32 int8), b plane (32 int8)
+__device__ __forceinline__ v4i as_v4i(uint4 q) {
+    v4i v;
+    v.x = (int) q.x;
+    v.y = (int) q.y;
+    v.z = (int) q.z;
+    v.w = (int) q.w;
+    return v;
+}
+
+__device__ __forceinline__ v4i lo4(uint4 q) {
+    return as_v4i(make_uint4(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, q.z & 0x0F0F0F0Fu, q.w & 0x0F0F0F0Fu));
+}
+__device__ __forceinline__ v4i hi4(uint4 q) {
+    return as_v4i(make_uint4((q.x >> 4) & 0x0F0F0F0Fu, (q.y >> 4) & 0x0F0F0F0Fu, (q.z >> 4) & 0x0F0F0F0Fu, (q.w >> 4) & 0x0F0F0F0Fu));
+}
+
+__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// 253 * (sum over plane a) + (sum over plane b), as float
+__device__ __forceinline__ float planes(int da, int db) {
+    return (float) (da * 253 + db);
+}
+
+// one x segment in LDS: plane a (32 int8), plane b (32 int8)
 struct XSeg {
     uint4 a0, a1, b0, b1;
 };
 
-// 253 * (q . a) + (q . b) over 16 int8 pairs (four words of q against 16 bytes of each plane)
-__device__ __forceinline__ int dot16(uint4 q, uint4 a, uint4 b) {
-    int ta = __builtin_amdgcn_sdot4((int) q.x, (int) a.x, 0, false);
-    ta = __builtin_amdgcn_sdot4((int) q.y, (int) a.y, ta, false);
-    ta = __builtin_amdgcn_sdot4((int) q.z, (int) a.z, ta, false);
-    ta = __builtin_amdgcn_sdot4((int) q.w, (int) a.w, ta, false);
-    int tb = __builtin_amdgcn_sdot4((int) q.x, (int) b.x, 0, false);
-    tb = __builtin_amdgcn_sdot4((int) q.y, (int) b.y, tb, false);
-    tb = __builtin_amdgcn_sdot4((int) q.z, (int) b.z, tb, false);
-    tb = __builtin_amdgcn_sdot4((int) q.w, (int) b.w, tb, false);
-    return ta * 253 + tb;
-}
-
-// the same over 32 pairs: q0 against the first 16 bytes of the segment, q1 against the last 16
-__device__ __forceinline__ int dot32(uint4 q0, uint4 q1, const XSeg & s) {
-    int ta = __builtin_amdgcn_sdot4((int) q0.x, (int) s.a0.x, 0, false);
-    ta = __builtin_amdgcn_sdot4((int) q0.y, (int) s.a0.y, ta, false);
-    ta = __builtin_amdgcn_sdot4((int) q0.z, (int) s.a0.z, ta, false);
-    ta = __builtin_amdgcn_sdot4((int) q0.w, (int) s.a0.w, ta, false);
-    ta = __builtin_amdgcn_sdot4((int) q1.x, (int) s.a1.x, ta, false);
-    ta = __builtin_amdgcn_sdot4((int) q1.y, (int) s.a1.y, ta, false);
-    ta = __builtin_amdgcn_sdot4((int) q1.z, (int) s.a1.z, ta, false);
-    ta = __builtin_amdgcn_sdot4((int) q1.w, (int) s.a1.w, ta, false);
-    int tb = __builtin_amdgcn_sdot4((int) q0.x, (int) s.b0.x, 0, false);
-    tb = __builtin_amdgcn_sdot4((int) q0.y, (int) s.b0.y, tb, false);
-    tb = __builtin_amdgcn_sdot4((int) q0.z, (int) s.b0.z, tb, false);
-    tb = __builtin_amdgcn_sdot4((int) q0.w, (int) s.b0.w, tb, false);
-    tb = __builtin_amdgcn_sdot4((int) q1.x, (int) s.b1.x, tb, false);
-    tb = __builtin_amdgcn_sdot4((int) q1.y, (int) s.b1.y, tb, false);
-    tb = __builtin_amdgcn_sdot4((int) q1.z, (int) s.b1.z, tb, false);
-    tb = __builtin_amdgcn_sdot4((int) q1.w, (int) s.b1.w, tb, false);
-    return ta * 253 + tb;
-}
-
-__device__ __forceinline__ uint4 lo4(uint4 q) {
-    return make_uint4(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, q.z & 0x0F0F0F0Fu, q.w & 0x0F0F0F0Fu);
-}
-__device__ __forceinline__ uint4 hi4(uint4 q) {
-    return make_uint4((q.x >> 4) & 0x0F0F0F0Fu, (q.y >> 4) & 0x0F0F0F0Fu, (q.z >> 4) & 0x0F0F0F0Fu, (q.w >> 4) & 0x0F0F0F0Fu);
-}
-
-// The converted x of one wave's chunk: xs[n * nseg + g] (planes) and xf[n * nseg + g] =
-// {s / 253, sum of elements 0..15, sum of elements 16..31, sum of all 32}.
+// The converted x of one wave's chunk, per column n: xs[n * nseg + g] (planes) and
+// xf[n * nseg + g] = {s / 253, sum of elements 0..15, sum of elements 16..31, sum of all 32}.
+// zpad: 16 zero bytes, the A operand of lanes that carry no x.
 struct XView {
     const XSeg * xs;
     const float4 * xf;
+    const uint8_t * zpad;
     int nseg;
 };
 
-// ---- per format: the lane's slice of a step ------------------------------------------------------
+// ---- per format ----------------------------------------------------------------------------------
 // init() resolves the lane's row in every R32 area once; load(step) fetches what the lane needs of
-// one step; compute() accumulates it for NC columns against x segments of the current chunk
-// (sg0 = index of the step's first segment inside the chunk).
+// one step; bop(raw, t) is the lane's B operand (16 int8 codes) for MFMA t = 0..3 of the step;
+// aoff(t, c, k, g) is the byte offset, inside the step's XSeg run, of the 16 x bytes that lane
+// (row 4c + k of A, k-group g) supplies to MFMA t, or -1 for zeros; flush() scales the integer
+// sums of lane part p into the row sum.
 
-template <int DT, int R> struct Fmt;
+template <int DT> struct Fmt;
 
-// Q4_K: a step is one block; part p takes chunks c = p, p + P, ... (64 elements: 32 bytes = units
-// 2c, 2c + 1 of the 128 nibble bytes), i.e. whole sub-blocks 2c (low nibbles), 2c + 1 (high).
-template <int R>
-struct Fmt<Q4_K, R> {
-    static constexpr int P = 64 / R;
-    static constexpr int CL = 4 / P; // chunks per lane
+// Q4_K: a step is one block; part p takes chunk p (64 elements: units 2p, 2p + 1 of the 128
+// nibble bytes): sub-block 2p (low nibbles), 2p + 1 (high). MFMA t takes elements 64p + 16t .. +15
+// (t = 0, 1: low nibbles of units 2p, 2p + 1; t = 2, 3: high nibbles). A row 4c + k: plane k % 2
+// of sub-block 2c + k / 2.
+template <>
+struct Fmt<Q4_K> {
+    static constexpr int ND = 1; // accumulator sets per step
     struct Raw {
-        uint4 q[CL][2];
-        uint4 hd;
+        uint4 q0, q1, hd;
     };
     const uint8_t * qb;
     const uint8_t * hb;
     uint32_t qblk, qunit, hblk;
     int p;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb, int64_t g0, int rs, int lr, int part, int64_t) {
+    __device__ void init(const uint8_t * w, int64_t M, int64_t nb, int64_t g0, int rs, int lr, int part) {
         p = part;
         qb = w + (uint64_t) g0 * nb * 128 + (uint64_t) lr * 16;
         hb = w + (uint64_t) M * nb * 128 + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
@@ -163,68 +164,54 @@ struct Fmt<Q4_K, R> {
     }
     __device__ Raw load(int64_t step) const {
         Raw r;
-        const uint8_t * b = qb + (uint32_t) step * qblk;
-#pragma unroll
-        for (int i = 0; i < CL; ++i) {
-            const int c = p + P * i;
-            r.q[i][0] = load16(b + (uint32_t) (2 * c) * qunit);
-            r.q[i][1] = load16(b + (uint32_t) (2 * c + 1) * qunit);
-        }
+        const uint8_t * b = qb + (uint32_t) step * qblk + (uint32_t) (2 * p) * qunit;
+        r.q0 = load16(b);
+        r.q1 = load16(b + qunit);
         r.hd = load16(hb + (uint32_t) step * hblk);
         return r;
     }
-    template <int NC>
-    __device__ void compute(const Raw & r, int sg0, const XView & xv, float * acc) const {
+    __device__ static v4i bop(const Raw & r, int t) {
+        return t == 0 ? lo4(r.q0) : t == 1 ? lo4(r.q1) : t == 2 ? hi4(r.q0) : hi4(r.q1);
+    }
+    __device__ static int aoff(int t, int c, int k, int g) {
+        if (c != g || (k >> 1) != (t >> 1)) return -1;
+        return (2 * g + (t >> 1)) * 64 + (k & 1) * 32 + (t & 1) * 16;
+    }
+    __device__ float flush(const Raw & r, const v4i * D, const float4 * xf) const {
         const float d = half_bits(r.hd.x), dmin = half_bits(r.hd.x >> 16);
         const uint32_t s0 = r.hd.y, s1 = r.hd.z, s2 = r.hd.w; // scale bytes 0..3, 4..7, 8..11
-#pragma unroll
-        for (int i = 0; i < CL; ++i) {
-            const int c = p + P * i;
-            // sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles): 6-bit scale and min
-            float sc0, m0, sc1, m1;
-            const int sh0 = 16 * (c & 1), sh1 = sh0 + 8; // byte (2c) & 3, (2c + 1) & 3
-            if (c < 2) {
-                sc0 = (float) ((s0 >> sh0) & 63u);
-                m0 = (float) ((s1 >> sh0) & 63u);
-                sc1 = (float) ((s0 >> sh1) & 63u);
-                m1 = (float) ((s1 >> sh1) & 63u);
-            } else {
-                const uint32_t t0 = s2 >> sh0, t1 = s2 >> sh1;
-                sc0 = (float) ((t0 & 0x0Fu) | (((s0 >> sh0) >> 2) & 0x30u));
-                m0 = (float) (((t0 >> 4) & 0x0Fu) | (((s1 >> sh0) >> 2) & 0x30u));
-                sc1 = (float) ((t1 & 0x0Fu) | (((s0 >> sh1) >> 2) & 0x30u));
-                m1 = (float) (((t1 >> 4) & 0x0Fu) | (((s1 >> sh1) >> 2) & 0x30u));
-            }
-            const float d0 = d * sc0, d1 = d * sc1, n0 = -dmin * m0, n1 = -dmin * m1;
-            const uint4 l0 = lo4(r.q[i][0]), l1 = lo4(r.q[i][1]);
-            const uint4 h0 = hi4(r.q[i][0]), h1 = hi4(r.q[i][1]);
-            const int g = sg0 + 2 * c;
-#pragma unroll
-            for (int n = 0; n < NC; ++n) {
-                const int gi = n * xv.nseg + g;
-                const float4 f0 = xv.xf[gi], f1 = xv.xf[gi + 1];
-                float a = acc[n];
-                a = fmaf(d0 * f0.x, (float) dot32(l0, l1, xv.xs[gi]), a);
-                a = fmaf(n0, f0.w, a);
-                a = fmaf(d1 * f1.x, (float) dot32(h0, h1, xv.xs[gi + 1]), a);
-                a = fmaf(n1, f1.w, a);
-                acc[n] = a;
-                __builtin_amdgcn_sched_barrier(0);
-            }
+        // 6-bit scale and min of sub-blocks 2p, 2p + 1 (get_scale_min_k4)
+        const int sh0 = 16 * (p & 1), sh1 = sh0 + 8;
+        float sc0, m0, sc1, m1;
+        if (p < 2) {
+            sc0 = (float) ((s0 >> sh0) & 63u);
+            m0 = (float) ((s1 >> sh0) & 63u);
+            sc1 = (float) ((s0 >> sh1) & 63u);
+            m1 = (float) ((s1 >> sh1) & 63u);
+        } else {
+            const uint32_t t0 = s2 >> sh0, t1 = s2 >> sh1;
+            sc0 = (float) ((t0 & 0x0Fu) | (((s0 >> sh0) >> 2) & 0x30u));
+            m0 = (float) (((t0 >> 4) & 0x0Fu) | (((s1 >> sh0) >> 2) & 0x30u));
+            sc1 = (float) ((t1 & 0x0Fu) | (((s0 >> sh1) >> 2) & 0x30u));
+            m1 = (float) (((t1 >> 4) & 0x0Fu) | (((s1 >> sh1) >> 2) & 0x30u));
         }
+        const float4 f0 = xf[2 * p], f1 = xf[2 * p + 1];
+        float a = (d * sc0) * f0.x * planes(D[0].x, D[0].y);
+        a = fmaf(-dmin * m0, f0.w, a);
+        a = fmaf((d * sc1) * f1.x, planes(D[0].z, D[0].w), a);
+        return fmaf(-dmin * m1, f1.w, a);
     }
 };
 
-// Q6_K: a step is one block; part p takes tasks k = p, p + P, ... (h = k >> 1, hf = k & 1): the
-// 64 elements 128h + 32rr + 16hf + i (rr, i < 4, 16) built from ql units 4h + hf, 4h + 2 + hf and
-// qh unit 8 + 2h + hf; each 16-run has its own signed 8-bit scale.
-template <int R>
-struct Fmt<Q6_K, R> {
-    static constexpr int P = 64 / R;
-    static constexpr int TL = 4 / P; // tasks per lane
+// Q6_K: a step is one block; part p takes task p = (h, hf): the 64 elements 128h + 32t + 16hf + i
+// (t, i < 4, 16) built from ql units 4h + hf, 4h + 2 + hf and qh unit 8 + 2h + hf; MFMA t takes
+// the 16 of run t, which has its own signed 8-bit scale. Two accumulator sets (t = 0, 1 and
+// t = 2, 3); A row 4c + k of set u: plane k % 2 of run 2u + k / 2 of task c.
+template <>
+struct Fmt<Q6_K> {
+    static constexpr int ND = 2;
     struct Raw {
-        uint4 qa[TL], qc[TL], qh[TL];
-        uint4 sc;
+        uint4 qa, qc, qh, sc;
         uint32_t d;
     };
     const uint8_t * qb;
@@ -232,7 +219,7 @@ struct Fmt<Q6_K, R> {
     const uint8_t * db;
     uint32_t qblk, qunit, sblk, dblk;
     int p;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb, int64_t g0, int rs, int lr, int part, int64_t) {
+    __device__ void init(const uint8_t * w, int64_t M, int64_t nb, int64_t g0, int rs, int lr, int part) {
         p = part;
         qb = w + (uint64_t) g0 * nb * 192 + (uint64_t) lr * 16;
         sb = w + (uint64_t) M * nb * 192 + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
@@ -244,75 +231,67 @@ struct Fmt<Q6_K, R> {
     }
     __device__ Raw load(int64_t step) const {
         Raw r;
+        const int h = p >> 1, hf = p & 1;
         const uint8_t * b = qb + (uint32_t) step * qblk;
-#pragma unroll
-        for (int t = 0; t < TL; ++t) {
-            const int k = p + P * t, h = k >> 1, hf = k & 1;
-            r.qa[t] = load16(b + (uint32_t) (4 * h + hf) * qunit);
-            r.qc[t] = load16(b + (uint32_t) (4 * h + 2 + hf) * qunit);
-            r.qh[t] = load16(b + (uint32_t) (8 + 2 * h + hf) * qunit);
-        }
+        r.qa = load16(b + (uint32_t) (4 * h + hf) * qunit);     // ql[64h + 16hf + i]
+        r.qc = load16(b + (uint32_t) (4 * h + 2 + hf) * qunit); // ql[64h + 32 + 16hf + i]
+        r.qh = load16(b + (uint32_t) (8 + 2 * h + hf) * qunit); // qh[32h + 16hf + i]
         r.sc = load16(sb + (uint32_t) step * sblk);
         r.d = load_half(db + (uint32_t) step * dblk);
         return r;
     }
-    template <int NC>
-    __device__ void compute(const Raw & r, int sg0, const XView & xv, float * acc) const {
+    // 6-bit codes of run t: low nibbles of qa (t 0) / qc (t 1), high nibbles (t 2, 3), with bits
+    // 2t, 2t + 1 of qh on top
+    __device__ static v4i bop(const Raw & r, int t) {
+        const uint4 ql = (t & 1) ? r.qc : r.qa;
+        const int ls = t < 2 ? 0 : 4;
+        const int hs = 2 * t;
+        return as_v4i(make_uint4(((ql.x >> ls) & 0x0F0F0F0Fu) | (((r.qh.x >> hs) << 4) & 0x30303030u),
+                                 ((ql.y >> ls) & 0x0F0F0F0Fu) | (((r.qh.y >> hs) << 4) & 0x30303030u),
+                                 ((ql.z >> ls) & 0x0F0F0F0Fu) | (((r.qh.z >> hs) << 4) & 0x30303030u),
+                                 ((ql.w >> ls) & 0x0F0F0F0Fu) | (((r.qh.w >> hs) << 4) & 0x30303030u)));
+    }
+    __device__ static int aoff(int t, int c, int k, int g) {
+        if (c != g || (k >> 1) != (t & 1)) return -1;
+        const int h = g >> 1, hf = g & 1;
+        return (4 * h + t) * 64 + (k & 1) * 32 + hf * 16;
+    }
+    __device__ float flush(const Raw & r, const v4i * D, const float4 * xf) const {
+        const int h = p >> 1, hf = p & 1;
         const float d = half_bits(r.d);
+        // scale of run t: byte 8h + hf + 2t of the 16 (stored xor 0x80, so value = byte - 128)
+        const uint32_t sw0 = h ? r.sc.z : r.sc.x, sw1 = h ? r.sc.w : r.sc.y;
+        float a = 0.0f;
 #pragma unroll
-        for (int t = 0; t < TL; ++t) {
-            const int k = p + P * t, h = k >> 1, hf = k & 1;
-            const uint4 qa = r.qa[t], qc = r.qc[t], qh = r.qh[t];
-            // scale of run rr: byte 8h + hf + 2rr of the 16 (stored xor 0x80, so value = byte - 128)
-            const uint32_t sw0 = h ? r.sc.z : r.sc.x, sw1 = h ? r.sc.w : r.sc.y;
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                // 6-bit values of run rr: low nibbles of qa (rr 0) / qc (rr 1), high nibbles (rr 2, 3),
-                // with bits 2rr, 2rr + 1 of qh on top
-                const uint4 ql = (rr & 1) ? qc : qa;
-                const int ls = rr < 2 ? 0 : 4;
-                const int hs = 2 * rr;
-                const uint4 v = make_uint4(((ql.x >> ls) & 0x0F0F0F0Fu) | (((qh.x >> hs) << 4) & 0x30303030u),
-                                           ((ql.y >> ls) & 0x0F0F0F0Fu) | (((qh.y >> hs) << 4) & 0x30303030u),
-                                           ((ql.z >> ls) & 0x0F0F0F0Fu) | (((qh.z >> hs) << 4) & 0x30303030u),
-                                           ((ql.w >> ls) & 0x0F0F0F0Fu) | (((qh.w >> hs) << 4) & 0x30303030u));
-                const uint32_t sw = rr < 2 ? sw0 : sw1;
-                const int bi = 2 * (rr & 1) + hf;
-                const float ds = d * ((float) ((sw >> (8 * bi)) & 0xFFu) - 128.0f);
-                const int g = sg0 + 4 * h + rr;
-#pragma unroll
-                for (int n = 0; n < NC; ++n) {
-                    const int gi = n * xv.nseg + g;
-                    // this lane's 16-element half of the segment: planes and plain sum
-                    const uint4 * pl = reinterpret_cast<const uint4 *>(xv.xs + gi) + hf;
-                    const float * fp = reinterpret_cast<const float *>(xv.xf + gi);
-                    const int tq = dot16(v, pl[0], pl[2]);
-                    const float sum16 = fp[1 + hf];
-                    const float4 f = make_float4(fp[0], 0.0f, 0.0f, 0.0f);
-                    acc[n] = fmaf(ds, fmaf(f.x, (float) tq, -32.0f * sum16), acc[n]);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            }
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t sw = t < 2 ? sw0 : sw1;
+            const float ds = d * ((float) ((sw >> (8 * (2 * (t & 1) + hf))) & 0xFFu) - 128.0f);
+            const v4i & Dt = D[t >> 1];
+            const int ia = (t & 1) ? Dt.z : Dt.x, ib = (t & 1) ? Dt.w : Dt.y;
+            const float4 f = xf[4 * h + t];
+            const float s16 = hf ? f.z : f.y;
+            a = fmaf(ds, fmaf(f.x, planes(ia, ib), -32.0f * s16), a);
         }
+        return a;
     }
 };
 
-// Q8_0 / Q4_0: a step is 8 blocks of 32; part p takes blocks p, p + P, ... of the step. Blocks past
-// the end of the row (K % 256 != 0) load block 0 and contribute with d = 0.
-template <int R>
-struct Fmt<Q8_0, R> {
-    static constexpr int P = 64 / R;
-    static constexpr int BL = 8 / P; // blocks per lane and step
+// Q8_0: a step is 8 blocks of 32; MFMA t takes blocks 2t, 2t + 1 (part p: half p % 2 of block
+// 2t + p / 2); part p scales blocks 2p, 2p + 1. A row 4c + k: plane k % 2 of block 2c + k / 2.
+// Blocks past the end of the row (K % 256 != 0) load block 0 and contribute with d = 0.
+template <>
+struct Fmt<Q8_0> {
+    static constexpr int ND = 1;
     struct Raw {
-        uint4 q[BL][2];
-        uint32_t d[BL];
+        uint4 u[4];
+        uint32_t d0, d1;
     };
     const uint8_t * qb;
     const uint8_t * db;
     uint32_t qblk, qunit, dblk;
     int64_t nb;
     int p;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int part, int64_t) {
+    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int part) {
         p = part;
         nb = nb_;
         qb = w + (uint64_t) g0 * nb * 32 + (uint64_t) lr * 16;
@@ -324,93 +303,135 @@ struct Fmt<Q8_0, R> {
     __device__ Raw load(int64_t step) const {
         Raw r;
 #pragma unroll
-        for (int i = 0; i < BL; ++i) {
-            int64_t b = step * 8 + p + P * i;
-            const bool ok = b < nb;
-            b = ok ? b : 0;
-            r.q[i][0] = load16(qb + (uint32_t) b * qblk);
-            r.q[i][1] = load16(qb + (uint32_t) b * qblk + qunit);
-            r.d[i] = ok ? load_half(db + (uint32_t) b * dblk) : 0u;
+        for (int t = 0; t < 4; ++t) {
+            int64_t b = step * 8 + 2 * t + (p >> 1);
+            b = b < nb ? b : 0;
+            r.u[t] = load16(qb + (uint32_t) b * qblk + (uint32_t) (p & 1) * qunit);
         }
+        const int64_t b0 = step * 8 + 2 * p, b1 = b0 + 1;
+        r.d0 = b0 < nb ? load_half(db + (uint32_t) b0 * dblk) : 0u;
+        r.d1 = b1 < nb ? load_half(db + (uint32_t) b1 * dblk) : 0u;
         return r;
     }
-    template <int NC>
-    __device__ void compute(const Raw & r, int sg0, const XView & xv, float * acc) const {
-#pragma unroll
-        for (int i = 0; i < BL; ++i) {
-            const float d = half_bits(r.d[i]);
-            const uint4 a = r.q[i][0], b = r.q[i][1];
-            const uint4 q0 = make_uint4(a.x ^ 0x80808080u, a.y ^ 0x80808080u, a.z ^ 0x80808080u, a.w ^ 0x80808080u);
-            const uint4 q1 = make_uint4(b.x ^ 0x80808080u, b.y ^ 0x80808080u, b.z ^ 0x80808080u, b.w ^ 0x80808080u);
-            const int g = sg0 + p + P * i;
-#pragma unroll
-            for (int n = 0; n < NC; ++n) {
-                const int gi = n * xv.nseg + g;
-                acc[n] = fmaf(d * xv.xf[gi].x, (float) dot32(q0, q1, xv.xs[gi]), acc[n]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
+    __device__ static v4i bop(const Raw & r, int t) {
+        const uint4 q = r.u[t];
+        return as_v4i(make_uint4(q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u));
+    }
+    __device__ static int aoff(int t, int c, int k, int g) {
+        if (c != t || (k >> 1) != (g >> 1)) return -1;
+        return (2 * t + (g >> 1)) * 64 + (k & 1) * 32 + (g & 1) * 16;
+    }
+    __device__ float flush(const Raw & r, const v4i * D, const float4 * xf) const {
+        const float a = half_bits(r.d0) * xf[2 * p].x * planes(D[0].x, D[0].y);
+        return fmaf(half_bits(r.d1) * xf[2 * p + 1].x, planes(D[0].z, D[0].w), a);
     }
 };
 
-template <int R>
-struct Fmt<Q4_0, R> {
-    static constexpr int P = 64 / R;
-    static constexpr int BL = 8 / P;
+// Q4_0: a step is 8 blocks of 32 (16 nibble bytes each: low nibbles = elements 0..15, high =
+// 16..31); part p takes blocks p and p + 4. MFMA t: blocks 0..3 (t < 2) or 4..7, half t % 2.
+// A row 4c + k: plane k % 2 of block c + 4 (k / 2).
+template <>
+struct Fmt<Q4_0> {
+    static constexpr int ND = 1;
     struct Raw {
-        uint4 q[BL];
-        uint32_t d[BL];
+        uint4 qa, qb;
+        uint32_t da, db;
     };
-    const uint8_t * qb;
-    const uint8_t * db;
+    const uint8_t * qp;
+    const uint8_t * dp;
     uint32_t qblk, dblk;
     int64_t nb;
     int p;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int part, int64_t) {
+    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int part) {
         p = part;
         nb = nb_;
-        qb = w + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
-        db = w + (uint64_t) M * nb * 16 + (uint64_t) g0 * nb * 2 + (uint64_t) lr * 2;
+        qp = w + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
+        dp = w + (uint64_t) M * nb * 16 + (uint64_t) g0 * nb * 2 + (uint64_t) lr * 2;
         qblk = (uint32_t) rs * 16;
         dblk = (uint32_t) rs * 2;
     }
     __device__ Raw load(int64_t step) const {
         Raw r;
-#pragma unroll
-        for (int i = 0; i < BL; ++i) {
-            int64_t b = step * 8 + p + P * i;
-            const bool ok = b < nb;
-            b = ok ? b : 0;
-            r.q[i] = load16(qb + (uint32_t) b * qblk);
-            r.d[i] = ok ? load_half(db + (uint32_t) b * dblk) : 0u;
-        }
+        int64_t ba = step * 8 + p, bb = ba + 4;
+        const bool oka = ba < nb, okb = bb < nb;
+        ba = oka ? ba : 0;
+        bb = okb ? bb : 0;
+        r.qa = load16(qp + (uint32_t) ba * qblk);
+        r.qb = load16(qp + (uint32_t) bb * qblk);
+        r.da = oka ? load_half(dp + (uint32_t) ba * dblk) : 0u;
+        r.db = okb ? load_half(dp + (uint32_t) bb * dblk) : 0u;
         return r;
     }
-    template <int NC>
-    __device__ void compute(const Raw & r, int sg0, const XView & xv, float * acc) const {
-#pragma unroll
-        for (int i = 0; i < BL; ++i) {
-            const float d = half_bits(r.d[i]);
-            const uint4 l = lo4(r.q[i]), h = hi4(r.q[i]); // elements 0..15, 16..31 of the block
-            const int g = sg0 + p + P * i;
-#pragma unroll
-            for (int n = 0; n < NC; ++n) {
-                const int gi = n * xv.nseg + g;
-                const float4 f = xv.xf[gi];
-                const int t = dot32(l, h, xv.xs[gi]);
-                acc[n] = fmaf(d, fmaf(f.x, (float) t, -8.0f * f.w), acc[n]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
+    __device__ static v4i bop(const Raw & r, int t) {
+        return t == 0 ? lo4(r.qa) : t == 1 ? hi4(r.qa) : t == 2 ? lo4(r.qb) : hi4(r.qb);
+    }
+    __device__ static int aoff(int t, int c, int k, int g) {
+        if (c != g || (k >> 1) != (t >> 1)) return -1;
+        return (g + 4 * (t >> 1)) * 64 + (k & 1) * 32 + (t & 1) * 16;
+    }
+    __device__ float flush(const Raw & r, const v4i * D, const float4 * xf) const {
+        const float4 fa = xf[p], fb = xf[p + 4];
+        const float a = half_bits(r.da) * fmaf(fa.x, planes(D[0].x, D[0].y), -8.0f * fa.w);
+        return fmaf(half_bits(r.db), fmaf(fb.x, planes(D[0].z, D[0].w), -8.0f * fb.w), a);
     }
 };
 
-// ---- x conversion of one wave's chunk --------------------------------------------------------------
-// Lane l converts elements 8 (l % 4) .. +8 of segment l / 4 (16 segments per pass of the wave);
-// elements past K are zero.
+// The lane's A operand addressing: byte offsets inside a step's XSeg run for MFMAs t = 0..3, or
+// -1 (zeros). Row of A = l % 16 = 4c + k, k-group g = l / 16.
+template <int DT>
+struct ALane {
+    int off[4];
+    __device__ explicit ALane(int lane) {
+        const int row = lane & 15, c = row >> 2, k = row & 3, g = lane >> 4;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) off[t] = Fmt<DT>::aoff(t, c, k, g);
+    }
+};
+
+// One step of RG row groups (raw[i] = rows r + 16 i) for NC columns: accumulates into acc[i][n].
+// sg0 = index of the step's first segment in the chunk.
+template <int DT, int RG, int NC>
+__device__ __forceinline__ void step_mfma(const Fmt<DT> (&f)[RG], const typename Fmt<DT>::Raw (&raw)[RG], const ALane<DT> & al, int sg0,
+                                          const XView & xv, float (&acc)[RG][NC]) {
+    constexpr int ND = Fmt<DT>::ND;
+    v4i B[RG][4];
+#pragma unroll
+    for (int i = 0; i < RG; ++i) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) B[i][t] = Fmt<DT>::bop(raw[i], t);
+    }
+#pragma unroll
+    for (int n = 0; n < NC; ++n) {
+        const uint8_t * base = reinterpret_cast<const uint8_t *>(xv.xs + n * xv.nseg + sg0);
+        v4i Aop[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint8_t * pa = al.off[t] >= 0 ? base + al.off[t] : xv.zpad;
+            Aop[t] = *reinterpret_cast<const v4i *>(pa);
+        }
+        const float4 * xf = xv.xf + n * xv.nseg + sg0;
+#pragma unroll
+        for (int i = 0; i < RG; ++i) {
+            v4i D[ND];
+#pragma unroll
+            for (int u = 0; u < ND; ++u) D[u] = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int u = ND == 1 ? 0 : (t >> 1);
+                D[u] = mfma(Aop[t], B[i][t], D[u]);
+            }
+            acc[i][n] += f[i].flush(raw[i], D, xf);
+        }
+    }
+}
+
+// ---- x conversion ----------------------------------------------------------------------------------
+
 // Segment g (of nseg) of a wave's range, elements 8q .. 8q + 7 held by this lane in v (lanes
-// 4k .. 4k + 3 hold one segment): two int8 planes, the plane scale and the plain sums.
+// 4k .. 4k + 3 hold one segment): two int8 planes, the plane scale and the plain sums. Rounding
+// to integers: adding 1.5 * 2^23 leaves the nearest integer in the low mantissa bits.
 __device__ __forceinline__ void convert_seg(const float (&v)[8], int g, int nseg, int q, XSeg * xs, float4 * xf) {
+    constexpr float kMagic = 12582912.0f; // 1.5 * 2^23
     float amax = 0.0f, sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -428,17 +449,20 @@ __device__ __forceinline__ void convert_seg(const float (&v)[8], int g, int nseg
     uint32_t pa[2], pb[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        uint32_t wa = 0, wb = 0;
+        uint32_t ba[4], bb[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float t = v[4 * h + i];
-            const float qa = rintf(t * inv);                 // |qa| <= 127
-            const float qb = rintf(fmaf(-qa, sc, t) * invb); // |qb| <= 127 (253 < 254 leaves headroom)
-            wa |= ((uint32_t) (int) qa & 0xFFu) << (8 * i);
-            wb |= ((uint32_t) (int) qb & 0xFFu) << (8 * i);
+            const float fa = fmaf(t, inv, kMagic);                          // |a| <= 127
+            const float fb = fmaf(fmaf(kMagic - fa, sc, t), invb, kMagic); // |b| <= 127 (253 < 254)
+            ba[i] = __float_as_uint(fa);
+            bb[i] = __float_as_uint(fb);
         }
-        pa[h] = wa;
-        pb[h] = wb;
+        // byte i of the result = byte 0 of word i
+        pa[h] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(ba[3], ba[2], 0x0c0c0400u), __builtin_amdgcn_perm(ba[1], ba[0], 0x0c0c0400u),
+                                      0x05040100u);
+        pb[h] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(bb[3], bb[2], 0x0c0c0400u), __builtin_amdgcn_perm(bb[1], bb[0], 0x0c0c0400u),
+                                      0x05040100u);
     }
     if (g < nseg) {
         uint8_t * sp = reinterpret_cast<uint8_t *>(xs + g);
@@ -479,35 +503,91 @@ __device__ void convert_x(const MvArgs & A, const float * x, int64_t e0, int nse
     }
 }
 
-// Burst form for short wave ranges (<= SPW steps per wave, one column, one tile per work-group):
-// the wave first loads its x range, then issues every weight load, and only then converts x, so
-// the x round trip overlaps the weight round trip and a work-group costs about one HBM latency.
-template <int DT, int R, int W, int SPW>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_mvb(MvArgs A) {
-    using F = Fmt<DT, R>;
-    using Raw = typename F::Raw;
-    extern __shared__ uint8_t lds[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = lane % R, part = lane / R;
+// the slice a work-group works on
+struct Where {
+    int64_t i2, i3;
+    uint64_t w_off;
+    const float * x;
+};
 
+__device__ __forceinline__ Where where_of(const MvArgs & A) {
+    Where w;
     const int64_t sl = blockIdx.y;
-    const int64_t i2 = sl % A.ne12, i3 = sl / A.ne12;
-    const uint64_t w_off = (uint64_t) (i2 / A.r2) * A.w_s2 + (uint64_t) (i3 / A.r3) * A.w_s3;
-    const float * x = A.x + i2 * A.x_s2 + i3 * A.x_s3;
+    w.i2 = sl % A.ne12;
+    w.i3 = sl / A.ne12;
+    w.w_off = (uint64_t) (w.i2 / A.r2) * A.w_s2 + (uint64_t) (w.i3 / A.r3) * A.w_s3;
+    w.x = A.x + w.i2 * A.x_s2 + w.i3 * A.x_s3;
+    return w;
+}
 
-    const int64_t tile = blockIdx.x;
+// the lane's rows of a tile of 16 * RG rows: f[i] serves row m0 + r + 16 i (dead lanes of a
+// partial last tile read a real row and drop the result)
+struct Row {
+    int j;
+    int64_t M, m0;
+};
+
+template <int DT, int RG>
+__device__ __forceinline__ Row row_of(const MvArgs & A, int64_t tile, uint64_t w_off, int r, int part, Fmt<DT> (&f)[RG]) {
+    constexpr int R = 16 * RG;
     const int j = tile >= A.tstart[1] ? (tile >= A.tstart[2] ? 2 : 1) : 0;
     const int64_t M = A.M[j];
     const int64_t m0 = (tile - A.tstart[j]) * R;
     const int64_t g0 = m0 & ~(int64_t) 31;
     const int rs = (int) min<int64_t>(32, M - g0);
-    const int lr = m0 + r < M ? (int) (m0 - g0) + r : rs - 1; // dead lanes read a real row and drop it
+#pragma unroll
+    for (int i = 0; i < RG; ++i) {
+        const int64_t m = m0 + r + 16 * i;
+        const int lr = m < M ? (int) (m - g0) : rs - 1;
+        f[i].init(A.w[j] + w_off, M, A.nb, g0, rs, lr, part);
+    }
+    return Row{j, M, m0};
+}
+
+// Adds the parts of each row (lanes r, r + 16, r + 32, r + 48) and then the waves in order; lanes
+// tid < 16 * RG * NC write y. red: [W][NC][16 * RG] floats.
+template <int RG, int NC, int W>
+__device__ __forceinline__ void reduce_store(const MvArgs & A, const Where & wh, const Row & row, float (&acc)[RG][NC], float * red, int tid) {
+    constexpr int R = 16 * RG;
+    const int lane = tid & 63, wave = tid >> 6, r = lane & 15;
+#pragma unroll
+    for (int i = 0; i < RG; ++i) {
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+            float v = acc[i][n];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            if (lane < 16) red[(wave * NC + n) * R + 16 * i + r] = v;
+        }
+    }
+    __syncthreads();
+    if (tid < NC * R) {
+        const int n = tid / R, rr = tid % R;
+        const int64_t m = row.m0 + rr;
+        if (m < row.M) {
+            float v = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < W; ++w2) v += red[(w2 * NC + n) * R + rr];
+            A.y[row.j][wh.i2 * A.y_s2 + wh.i3 * A.y_s3 + n * A.ys1[row.j] + m] = v;
+        }
+    }
+}
+
+// Burst form (one column, <= SPW steps per wave, one tile of 16 * RG rows per work-group): the wave
+// first loads its x range, then issues every weight load, and only then converts x.
+template <int DT, int RG, int W, int SPW>
+__global__ __launch_bounds__(64 * W) void k_mvb(MvArgs A) {
+    using F = Fmt<DT>;
+    using Raw = typename F::Raw;
+    extern __shared__ uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const Where wh = where_of(A);
 
     const int64_t s0 = A.nst * wave / W, s1 = A.nst * (wave + 1) / W;
     const int ns = (int) (s1 - s0);
 
     // x: lane l holds elements 8 (l % 4) .. +8 of segment l / 4 + 16 p of the wave's range (pass p)
-    constexpr int XP = (SPW * kSegs + 15) / 16; // passes of 16 segments
+    constexpr int XP = (SPW * kSegs + 15) / 16;
     float xv[XP][8];
     const int nseg = ns * kSegs;
 #pragma unroll
@@ -515,8 +595,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4, 8))) 
         const int g = 16 * p + (lane >> 2);
         const int64_t e = s0 * kStep + 32 * (int64_t) g + 8 * (lane & 3);
         if (g < nseg && e < A.K) {
-            const float4 u = *reinterpret_cast<const float4 *>(x + e);
-            const float4 w = *reinterpret_cast<const float4 *>(x + e + 4);
+            const float4 u = *reinterpret_cast<const float4 *>(wh.x + e);
+            const float4 w = *reinterpret_cast<const float4 *>(wh.x + e + 4);
             xv[p][0] = u.x; xv[p][1] = u.y; xv[p][2] = u.z; xv[p][3] = u.w;
             xv[p][4] = w.x; xv[p][5] = w.y; xv[p][6] = w.z; xv[p][7] = w.w;
         } else {
@@ -525,95 +605,71 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4, 8))) 
         }
     }
 
-    F f;
-    f.init(A.w[j] + w_off, M, A.nb, g0, rs, lr, part, 0);
-    Raw buf[SPW];
+    F f[RG];
+    const Row row = row_of<DT, RG>(A, blockIdx.x, wh.w_off, lane & 15, lane >> 4, f);
+    Raw buf[SPW][RG];
 #pragma unroll
-    for (int i = 0; i < SPW; ++i)
-        if (i < ns) buf[i] = f.load(s0 + i);
+    for (int s = 0; s < SPW; ++s) {
+        if (s < ns) {
+#pragma unroll
+            for (int i = 0; i < RG; ++i) buf[s][i] = f[i].load(s0 + s);
+        }
+    }
 
     XSeg * xs = reinterpret_cast<XSeg *>(lds) + (size_t) wave * SPW * kSegs;
     float4 * xf = reinterpret_cast<float4 *>(reinterpret_cast<XSeg *>(lds) + (size_t) W * SPW * kSegs) + (size_t) wave * SPW * kSegs;
     float * red = reinterpret_cast<float *>(reinterpret_cast<float4 *>(reinterpret_cast<XSeg *>(lds) + (size_t) W * SPW * kSegs) +
                                             (size_t) W * SPW * kSegs);
+    uint8_t * zpad = reinterpret_cast<uint8_t *>(red + W * 16 * RG);
+    if (lane < 4) reinterpret_cast<uint32_t *>(zpad)[lane] = 0u;
 #pragma unroll
     for (int p = 0; p < XP; ++p) convert_seg(xv[p], 16 * p + (lane >> 2), nseg, lane & 3, xs, xf);
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
 
-    float acc[1] = {0.0f};
-    const XView xw{xs, xf, nseg};
+    const ALane<DT> al(lane);
+    const XView xw{xs, xf, zpad, nseg};
+    float acc[RG][1];
 #pragma unroll
-    for (int i = 0; i < SPW; ++i)
-        if (i < ns) f.template compute<1>(buf[i], i * kSegs, xw, acc);
-
+    for (int i = 0; i < RG; ++i) acc[i][0] = 0.0f;
 #pragma unroll
-    for (int off = R; off < 64; off <<= 1) acc[0] += __shfl_xor(acc[0], off);
-    if (part == 0) red[wave * R + r] = acc[0];
-    __syncthreads();
-    if (tid < R) {
-        const int64_t m = m0 + tid;
-        if (m < M) {
-            float v = 0.0f;
-#pragma unroll
-            for (int w2 = 0; w2 < W; ++w2) v += red[w2 * R + tid];
-            A.y[j][i2 * A.y_s2 + i3 * A.y_s3 + m] = v;
-        }
+    for (int s = 0; s < SPW; ++s) {
+        if (s < ns) step_mfma<DT, RG, 1>(f, buf[s], al, s * kSegs, xw, acc);
     }
+    reduce_store<RG, 1, W>(A, wh, row, acc, red, tid);
 }
 
-// One work-group walks tiles blockIdx.x, blockIdx.x + gridDim.x, ... (persistent). Its waves keep
-// the same K range for every tile, so each converts its x range once (when the range fits the LDS
-// budget; otherwise per chunk of cs steps and tile). The next step's loads (of this tile or the
-// first of the next) are in flight while the current step is computed.
+// Streaming form: one work-group walks tiles blockIdx.x, blockIdx.x + gridDim.x, ... (16 rows
+// each). Its waves keep the same K range for every tile, so each converts its x range once (when
+// the range fits the LDS budget; otherwise per chunk of cs steps and tile). The next step's loads
+// (of this tile or the first of the next) are in flight while the current step is computed.
 template <int DT, int NC, int W>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_mvs(MvArgs A) {
-    constexpr int R = 16;
-    using F = Fmt<DT, R>;
+__global__ __launch_bounds__(64 * W) void k_mvs(MvArgs A) {
+    using F = Fmt<DT>;
     using Raw = typename F::Raw;
     extern __shared__ uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = lane % R, part = lane / R;
+    const int r = lane & 15, part = lane >> 4;
+    const Where wh = where_of(A);
 
-    const int64_t sl = blockIdx.y;
-    const int64_t i2 = sl % A.ne12, i3 = sl / A.ne12;
-    const uint64_t w_off = (uint64_t) (i2 / A.r2) * A.w_s2 + (uint64_t) (i3 / A.r3) * A.w_s3;
-    const float * x = A.x + i2 * A.x_s2 + i3 * A.x_s3;
-
-    // the lane's row of a tile (dead lanes of a partial last tile read a real row and drop it)
-    struct Row {
-        int j;
-        int64_t M, m0;
-    };
-    auto row_of = [&](int64_t tile, F & f) -> Row {
-        const int j = tile >= A.tstart[1] ? (tile >= A.tstart[2] ? 2 : 1) : 0;
-        const int64_t M = A.M[j];
-        const int64_t m0 = (tile - A.tstart[j]) * R;
-        const int64_t g0 = m0 & ~(int64_t) 31;
-        const int rs = (int) min<int64_t>(32, M - g0);
-        const int lr = m0 + r < M ? (int) (m0 - g0) + r : rs - 1;
-        f.init(A.w[j] + w_off, M, A.nb, g0, rs, lr, part, 0);
-        return Row{j, M, m0};
-    };
-
-    // this wave's steps, the same for every tile
     const int64_t s0 = A.nst * wave / W, s1 = A.nst * (wave + 1) / W;
     const int ns = (int) (s1 - s0);
     const int cs = A.cs;
-    const bool once = cs >= ns;
+    const bool once = cs >= ns; // the wave's whole x range stays in LDS for all tiles
     XSeg * xs = reinterpret_cast<XSeg *>(lds) + (size_t) wave * cs * kSegs * NC;
     float4 * xf = reinterpret_cast<float4 *>(reinterpret_cast<XSeg *>(lds) + (size_t) W * cs * kSegs * NC) + (size_t) wave * cs * kSegs * NC;
     float * red = reinterpret_cast<float *>(reinterpret_cast<float4 *>(reinterpret_cast<XSeg *>(lds) + (size_t) W * cs * kSegs * NC) +
-                                            (size_t) W * cs * kSegs * NC); // [2][W][NC][R]
+                                            (size_t) W * cs * kSegs * NC); // [2][W][NC][16]
+    uint8_t * zpad = reinterpret_cast<uint8_t *>(red + 2 * W * NC * 16);
+    if (lane < 4) reinterpret_cast<uint32_t *>(zpad)[lane] = 0u;
+    const ALane<DT> al(lane);
 
     int64_t tile = blockIdx.x;
-    F f, fn;
-    Row row = row_of(tile, f);
-    // two steps in registers: the next step's loads (possibly of the next tile) are issued before
-    // the current step's math
-    Raw cur;
-    if (ns > 0) cur = f.load(s0);
-    if (once && ns > 0) convert_x<NC>(A, x, s0 * kStep, ns * kSegs, lane, xs, xf);
+    F f[1], fn[1];
+    Row row = row_of<DT, 1>(A, tile, wh.w_off, r, part, f);
+    Raw cur[1];
+    if (ns > 0) cur[0] = f[0].load(s0);
+    if (once && ns > 0) convert_x<NC>(A, wh.x, s0 * kStep, ns * kSegs, lane, xs, xf);
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
 
@@ -621,78 +677,51 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4, 8))) 
         const int64_t ntile = tile + gridDim.x;
         const bool has_n = ntile < A.tiles;
         Row nrow{};
-        if (has_n) nrow = row_of(ntile, fn);
+        if (has_n) nrow = row_of<DT, 1>(A, ntile, wh.w_off, r, part, fn);
 
-        float acc[NC];
+        float acc[1][NC];
 #pragma unroll
-        for (int n = 0; n < NC; ++n) acc[n] = 0.0f;
+        for (int n = 0; n < NC; ++n) acc[0][n] = 0.0f;
         for (int k = 0; k < ns; ++k) {
             if (!once && k % cs == 0) {
                 // a new x chunk: steps [k, k + cs) of this wave
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
-                convert_x<NC>(A, x, (s0 + k) * kStep, min(cs, ns - k) * kSegs, lane, xs, xf);
+                convert_x<NC>(A, wh.x, (s0 + k) * kStep, min(cs, ns - k) * kSegs, lane, xs, xf);
                 __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
                 __builtin_amdgcn_wave_barrier();
             }
-            Raw nxt;
+            Raw nxt[1];
             if (k + 1 < ns) {
-                nxt = f.load(s0 + k + 1);
+                nxt[0] = f[0].load(s0 + k + 1);
             } else if (has_n) {
-                nxt = fn.load(s0);
+                nxt[0] = fn[0].load(s0);
             }
-            const XView xv{xs, xf, min(cs, ns - (k / cs) * cs) * kSegs};
-            f.template compute<NC>(cur, (k % cs) * kSegs, xv, acc);
-            cur = nxt;
+            const XView xv{xs, xf, zpad, min(cs, ns - (k / cs) * cs) * kSegs};
+            step_mfma<DT, 1, NC>(f, cur, al, (k % cs) * kSegs, xv, acc);
+            cur[0] = nxt[0];
         }
-
-        // parts of a row (lanes r, r + R, ...), then the waves in order
-#pragma unroll
-        for (int off = R; off < 64; off <<= 1) {
-#pragma unroll
-            for (int n = 0; n < NC; ++n) acc[n] += __shfl_xor(acc[n], off);
-        }
-        float * rb = red + (it & 1) * (W * NC * R);
-        if (part == 0) {
-#pragma unroll
-            for (int n = 0; n < NC; ++n) rb[(wave * NC + n) * R + r] = acc[n];
-        }
-        __syncthreads();
-        if (tid < NC * R) {
-            const int n = tid / R, rr = tid % R;
-            const int64_t m = row.m0 + rr;
-            if (m < row.M) {
-                float v = 0.0f;
-#pragma unroll
-                for (int w2 = 0; w2 < W; ++w2) v += rb[(w2 * NC + n) * R + rr];
-                A.y[row.j][i2 * A.y_s2 + i3 * A.y_s3 + n * A.ys1[row.j] + m] = v;
-            }
-        }
+        reduce_store<1, NC, W>(A, wh, row, acc, red + (it & 1) * (W * NC * 16), tid);
         tile = ntile;
         row = nrow;
-        f = fn;
+        f[0] = fn[0];
     }
 }
 
-template <int DT, int R>
-void * pick_burst_r(int W, int spw) {
-    if (spw <= 2) return W >= 16 ? (void *) k_mvb<DT, R, 16, 2> : W >= 8 ? (void *) k_mvb<DT, R, 8, 2> : (void *) k_mvb<DT, R, 4, 2>;
-    return W >= 16 ? (void *) k_mvb<DT, R, 16, 4> : W >= 8 ? (void *) k_mvb<DT, R, 8, 4> : (void *) k_mvb<DT, R, 4, 4>;
+template <int DT, int RG>
+void * pick_burst_rg(int W, int spw) {
+    if (spw <= 2) return W >= 16 ? (void *) k_mvb<DT, RG, 16, 2> : W >= 8 ? (void *) k_mvb<DT, RG, 8, 2> : (void *) k_mvb<DT, RG, 4, 2>;
+    return W >= 16 ? (void *) k_mvb<DT, RG, 16, 4> : W >= 8 ? (void *) k_mvb<DT, RG, 8, 4> : (void *) k_mvb<DT, RG, 4, 4>;
 }
 
 template <int DT>
-void * pick_burst(int W, int spw, int R) {
-    if constexpr (DT == Q6_K || DT == Q8_0) {
-        if (R == 32 && spw <= 2) return W >= 16 ? (void *) k_mvb<DT, 32, 16, 2> : W >= 8 ? (void *) k_mvb<DT, 32, 8, 2> : (void *) k_mvb<DT, 32, 4, 2>;
-        return pick_burst_r<DT, 16>(W, spw);
-    } else {
-        return R == 32 ? pick_burst_r<DT, 32>(W, spw) : pick_burst_r<DT, 16>(W, spw);
-    }
+void * pick_burst(int W, int spw, int rg) {
+    return rg == 2 ? pick_burst_rg<DT, 2>(W, spw) : pick_burst_rg<DT, 1>(W, spw);
 }
 
 // streaming variants: W = 8 for one column, 4 for several
 template <int DT>
-void * pick(int nc) {
+void * pick_stream(int nc) {
     switch (nc) {
         case 1: return (void *) k_mvs<DT, 1, 8>;
         case 2: return (void *) k_mvs<DT, 2, 4>;
@@ -721,6 +750,7 @@ int occupancy(void * fn, int threads, size_t lds) {
     return n;
 }
 
+// tuning overrides from the environment (0 / unset = automatic)
 int tuning(const char * name, int dflt) {
     const char * v = std::getenv(name);
     return v != nullptr && *v ? std::atoi(v) : dflt;
@@ -743,11 +773,16 @@ const char * name_of(int dt, int nmat) {
     }
 }
 
+void set_tiles(MvArgs & L, const MatArgs * mats, int nmat, int R) {
+    L.tstart[0] = 0;
+    for (int j = 0; j < 3; ++j) L.tstart[j + 1] = j < nmat ? L.tstart[j] + (mats[j].M + R - 1) / R : INT64_MAX;
+    L.tiles = L.tstart[nmat];
+}
+
 } // namespace
 
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
-                          uint64_t * grid_size) {
-    constexpr int R = 16;
+                         uint64_t * grid_size) {
     if (nmat < 1 || nmat > 3) return hipErrorInvalidValue;
     const MatArgs & a = mats[0];
     for (int j = 0; j < nmat; ++j) {
@@ -763,20 +798,16 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     if (dt != Q4_0 && dt != Q8_0 && dt != Q4_K && dt != Q6_K) return hipErrorInvalidValue;
     int64_t rows = 0;
     for (int j = 0; j < nmat; ++j) rows += mats[j].M;
+    if ((rows + 15) / 16 > 0x7FFFFFFF) return hipErrorInvalidValue;
 
     MvArgs L;
-    L.tstart[0] = 0;
     for (int j = 0; j < 3; ++j) {
         const bool has = j < nmat;
         L.w[j] = has ? mats[j].w : nullptr;
         L.M[j] = has ? mats[j].M : 0;
         L.y[j] = has ? mats[j].y : nullptr;
         L.ys1[j] = has ? mats[j].y_s1 : 0;
-        L.tstart[j + 1] = L.tstart[j] + (has ? (mats[j].M + R - 1) / R : 0);
     }
-    for (int j = nmat + 1; j < 4; ++j) L.tstart[j] = INT64_MAX;
-    const int64_t tiles = L.tstart[nmat];
-    if (tiles < 1 || tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
     const int64_t nst = (a.K + kStep - 1) / kStep;
     L.K = a.K;
     L.nb = a.K / (dt == Q4_K || dt == Q6_K ? 256 : 32);
@@ -793,52 +824,45 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     L.r2 = a.r2;
     L.r3 = a.r3;
     L.xvec = ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (a.x_s1 & 3) == 0 && (a.x_s2 & 3) == 0 && (a.x_s3 & 3) == 0) ? 1 : 0;
-    L.tiles = tiles;
+    if (kernel_name) *kernel_name = name_of(dt, nmat);
 
     // burst form (one column, K <= 64 steps): every wave's steps (<= 4) loaded at once, one tile
-    // per work-group. 32-row tiles for large products (fewer x conversions per weight, 512-byte
-    // runs), 16-row tiles otherwise (more work-groups). 2 steps per wave up to K = 16 steps, then
-    // 4 (the 32-row Q6_K / Q8_0 forms hold too many registers at 4 steps: 16 rows there).
+    // per work-group. 32-row tiles (two row groups sharing each x operand) for large products,
+    // 16-row tiles otherwise (more work-groups). 2 steps per wave up to K = 32 steps, then 4.
     if (nc == 1 && L.xvec && nst <= 64 && tuning("SCRAPGPU_HIP_MV_BURST", 1)) {
-        int Rb = rows * slices >= (int64_t) 64 * cu_count ? 32 : 16;
+        int rg = rows * slices >= (int64_t) 64 * cu_count ? 2 : 1;
+        if (const int fr = tuning("SCRAPGPU_HIP_MV_RG", 0)) rg = fr >= 2 ? 2 : 1;
         const int sp = nst <= 32 ? 2 : 4;
-        int Wb = 4;
-        while (Wb < 16 && (nst + Wb - 1) / Wb > sp) Wb *= 2;
-        if (sp == 4 && (dt == Q6_K || dt == Q8_0)) Rb = 16;
-        if (const int fr = tuning("SCRAPGPU_HIP_MV_R", 0)) Rb = fr == 32 ? 32 : 16;
-        L.tstart[0] = 0;
-        for (int j = 0; j < 3; ++j) L.tstart[j + 1] = j < nmat ? L.tstart[j] + (mats[j].M + Rb - 1) / Rb : INT64_MAX;
-        const int64_t btiles = L.tstart[nmat];
-        L.tiles = btiles;
+        int W = 4;
+        while (W < 16 && (nst + W - 1) / W > sp) W *= 2;
+        set_tiles(L, mats, nmat, 16 * rg);
         L.cs = sp;
-        const size_t lds = (size_t) Wb * sp * kSegs * (sizeof(XSeg) + sizeof(float4)) + (size_t) Wb * Rb * sizeof(float);
-        void * fn = dt == Q4_0 ? pick_burst<Q4_0>(Wb, sp, Rb) : dt == Q8_0 ? pick_burst<Q8_0>(Wb, sp, Rb)
-                  : dt == Q4_K ? pick_burst<Q4_K>(Wb, sp, Rb) : pick_burst<Q6_K>(Wb, sp, Rb);
-        if (kernel_name) *kernel_name = name_of(dt, nmat);
-        if (grid_size) *grid_size = (uint64_t) btiles * (uint64_t) slices;
+        const size_t lds = (size_t) W * sp * kSegs * (sizeof(XSeg) + sizeof(float4)) + (size_t) W * 16 * rg * sizeof(float) + 16;
+        void * fn = dt == Q4_0 ? pick_burst<Q4_0>(W, sp, rg) : dt == Q8_0 ? pick_burst<Q8_0>(W, sp, rg)
+                  : dt == Q4_K ? pick_burst<Q4_K>(W, sp, rg) : pick_burst<Q6_K>(W, sp, rg);
+        if (grid_size) *grid_size = (uint64_t) L.tiles * (uint64_t) slices;
         void * args[] = {&L};
-        return hipLaunchKernel(fn, dim3((unsigned) btiles, (unsigned) slices), dim3((unsigned) (64 * Wb)), args, lds, stream);
+        return hipLaunchKernel(fn, dim3((unsigned) L.tiles, (unsigned) slices), dim3((unsigned) (64 * W)), args, lds, stream);
     }
 
     // streaming form (several columns, or K too long for the burst form)
+    set_tiles(L, mats, nmat, 16);
     const int W = nc == 1 ? 8 : 4;
     // x chunk per wave: all of the wave's steps when they fit the LDS budget, else as many as fit
     const int64_t step_bytes = (int64_t) kSegs * nc * (sizeof(XSeg) + sizeof(float4));
     const int64_t per_wave = std::max<int64_t>(1, (nst + W - 1) / W);
     const int64_t cs = std::min<int64_t>(per_wave, std::max<int64_t>(1, kLdsX / W / step_bytes));
     L.cs = (int) cs;
-    const size_t lds = (size_t) W * cs * step_bytes + (size_t) 2 * W * nc * R * sizeof(float);
+    const size_t lds = (size_t) W * cs * step_bytes + (size_t) 2 * W * nc * 16 * sizeof(float) + 16;
     if (lds > (size_t) 160 * 1024) return hipErrorInvalidValue;
-    void * fn = dt == Q4_0 ? pick<Q4_0>(nc) : dt == Q8_0 ? pick<Q8_0>(nc) : dt == Q4_K ? pick<Q4_K>(nc) : pick<Q6_K>(nc);
+    void * fn = dt == Q4_0 ? pick_stream<Q4_0>(nc) : dt == Q8_0 ? pick_stream<Q8_0>(nc) : dt == Q4_K ? pick_stream<Q4_K>(nc) : pick_stream<Q6_K>(nc);
 
     // persistent grid: as many work-groups as stay resident (at most one per tile), trimmed so
     // that every work-group gets the same number of tiles
     const int per_cu = std::max(1, tuning("SCRAPGPU_HIP_MV_WGS", occupancy(fn, 64 * W, lds)));
     const int64_t cap = std::max<int64_t>(1, (int64_t) per_cu * cu_count / slices);
-    const int64_t rounds = (tiles + cap - 1) / cap;
-    const int64_t grid_x = (tiles + rounds - 1) / rounds;
-
-    if (kernel_name) *kernel_name = name_of(dt, nmat);
+    const int64_t rounds = (L.tiles + cap - 1) / cap;
+    const int64_t grid_x = (L.tiles + rounds - 1) / rounds;
     if (grid_size) *grid_size = (uint64_t) grid_x * (uint64_t) slices;
     void * args[] = {&L};
     return hipLaunchKernel(fn, dim3((unsigned) grid_x, (unsigned) slices), dim3((unsigned) (64 * W)), args, lds, stream);
