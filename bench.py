@@ -8,8 +8,10 @@ beyond the 256 MB MALL). A step = one token = the 252 matvecs, replayed from one
 
 Reported on one JSON line:
   value         weight GB/s of the whole token (all 252 kernels, wall clock over the timed steps)
-  roofline      dominant kernel (the Q4_K matvec): algorithmic weight bytes per launch / mean launch
-                duration from HIP events on its stream, vs 8 TB/s
+  roofline      the token's largest product, gate+up (2 x 12288x4096 Q4_K as one MUL_MAT_MULTI):
+                algorithmic weight bytes per launch / mean launch duration from HIP events on its
+                stream (a profiling pass over all 36 layers right after the timed region), vs 8 TB/s;
+                `traffic` = HBM bytes per launch from the committed rocprofv3 PMC summary
   prefill       Q4_K M=512 (N=512 tokens) MFMA TFLOP/s on the two MLP shapes, vs 2.5 PFLOP/s bf16
   cpu_baseline  the oracle's reference-faithful CPU MUL_MAT (1 thread) on one gate matrix, N=1
 """
@@ -31,6 +33,10 @@ sys.path.insert(0, ROOT)
 import scrapgpulibrary_amd as sg  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the dominant kernel, measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+# runs of this script (scaled by the counters' reading for a copy of known size); written by the
+# profiling run, see DESIGN.md
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_matvec_decode_token.json")
 BF16_PEAK_TFLOPS = 2500.0
 
 HIDDEN, KV, FFN, LAYERS = 4096, 1024, 12288, 36
@@ -86,6 +92,7 @@ class Model:
         st.fill_normal(self.xf, seed=8)
         self.y_bufs = {n: dev.alloc(4 * M) for n, _, _, M in LAYER_SHAPES}
         self.keep = []
+        self.by_group = {}  # "q+k+v", "o", "gate+up", "down" (or one name per weight) -> ops of all layers
         nodes = []
         for row in self.weights:
             by = {name: (q, sg.tdesc(sg.F32, (M, 1), self.y_bufs[name])) for name, dt, K, M, q in row}
@@ -99,6 +106,7 @@ class Model:
                 else:
                     op, keep = sg.multi_op([by[n][0] for n in g], x, [by[n][1] for n in g])
                 self.keep.append((op, keep))
+                self.by_group.setdefault("+".join(g), []).append(op)
                 nodes.append(sg.PlanNode(C.sizeof(sg.PlanNode), op, 0))
         self.nodes = (sg.PlanNode * len(nodes))(*nodes)
         self.pdesc = sg.PlanDesc(C.sizeof(sg.PlanDesc), self.nodes, len(nodes))
@@ -125,6 +133,26 @@ def profile_kernels(model, tokens):
     rows = sg.profile_table()
     L.scrapgpu_hip_profile_reset()
     return rows
+
+
+def profile_group(model, group, rounds):
+    """Mean launch time of one product of the token (all layers' instances, eagerly, `rounds`
+    times) from the library's per-launch HIP events on the model's stream."""
+    L = sg.lib()
+    model.st.sync()
+    L.scrapgpu_hip_profile_reset()
+    L.scrapgpu_hip_profile_enable(1)
+    try:
+        for _ in range(rounds):
+            for op in model.by_group[group]:
+                model.st.execute(op)
+        model.st.sync()
+    finally:
+        L.scrapgpu_hip_profile_enable(0)
+    rows = sg.profile_table()
+    L.scrapgpu_hip_profile_reset()
+    r = rows[0]
+    return r["name"], r["ms"] / r["launches"], r["bytes"] / r["launches"]
 
 
 def bench_prefill(dev, st, n_tokens, reps):
@@ -191,6 +219,30 @@ def cpu_baseline(dev, st, model, seconds):
                       f"host {cpu}, nproc {os.cpu_count()}"}
 
 
+def traffic_of(kernel):
+    """HBM bytes per launch of `kernel` from the committed PMC summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            t = json.load(fh)
+    except (OSError, ValueError):
+        return None
+    k = t.get("kernels", {}).get(kernel)
+    return None if k is None else k.get("hbm_bytes_per_launch")
+
+
+def calibrate():
+    """A plain device copy of 256 MiB, 5 times (torch): the reference reading of FETCH_SIZE and
+    WRITE_SIZE for rocprofv3 --pmc (each launch reads and writes exactly 256 MiB)."""
+    import torch
+
+    a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_per_launch": 256 << 20, "launches": 5}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -201,7 +253,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-fuse", action="store_true", help="one MUL_MAT per weight instead of MUL_MAT_MULTI for q/k/v and gate/up")
+    ap.add_argument("--calibrate", action="store_true", help="only run the 256 MiB copy that calibrates the PMC byte counters")
     args = ap.parse_args()
+    if args.calibrate:
+        calibrate()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one MI355X per run); use --gpus 1",
               file=sys.stderr)
@@ -225,9 +281,9 @@ def main():
 
     rows = profile_kernels(model, 3)
     ktime = sum(r["ms"] for r in rows) / 3
-    dom = max(rows, key=lambda r: r["ms"])
-    dom_ms = dom["ms"] / dom["launches"]
-    dom_bytes = dom["bytes"] / dom["launches"]
+    # the roofline kernel: the token's largest product (gate+up fused, 2 x 12288x4096 Q4_K)
+    dom_group = "gate+up" if "gate+up" in model.by_group else "gate"
+    dom_name, dom_ms, dom_bytes = profile_group(model, dom_group, 3)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     kernels = {r["name"]: {"launches_per_token": r["launches"] // 3, "mean_us": round(r["ms"] / r["launches"] * 1e3, 2),
                            "GBps": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1)} for r in rows}
@@ -255,8 +311,8 @@ def main():
         "kernel_sum_ms_per_token": round(ktime, 4),
         "kernel_GBps": round(model.bytes_per_token / (ktime * 1e-3) / 1e9, 1),
         "kernels": kernels,
-        "roofline": {"bound": "hbm", "kernel": dom["name"], "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+        "roofline": {"bound": "hbm", "kernel": f"{dom_name} ({dom_group})", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_of(dom_group),
                      "bytes_per_launch": dom_bytes, "mean_launch_us": round(dom_ms * 1e3, 3)},
         "prefill_M512": prefill,
         "prefill_peak_frac": None if prefill is None else round(max(v["tflops"] for v in prefill.values()) / BF16_PEAK_TFLOPS, 4),

@@ -6,7 +6,6 @@
 #include "scrapgpu/backend.h"
 #include "scrapgpu/stream.h"
 
-#include "registry_internal.h"
 
 #include <algorithm>
 #include <cstring>
@@ -37,13 +36,6 @@ scrapgpu_status forward(const void * obj, Fn scrapgpu_backend_vtable::*slot, con
 }
 
 } // namespace
-
-bool sg_registry_contains(size_t (*get_device_count)(void *)) {
-    std::lock_guard<std::mutex> lock(g_mu);
-    for (const auto & t : g_tables)
-        if (t.get_device_count == get_device_count) return true;
-    return false;
-}
 
 extern "C" {
 

@@ -8,7 +8,6 @@
 // (N <= 8: decode matvec; N > 8: bf16 MFMA prefill).
 #include "scrapgpu/hip.h"
 
-#include "../core/registry_internal.h"
 #include "../core/tensor_math.h"
 #include "kernels.h"
 
@@ -897,6 +896,21 @@ scrapgpu_status over_chunks(Stream * s, const scrapgpu_tensor_desc & q, uint8_t 
 
 } // namespace
 
+namespace {
+
+// true when the core currently lists this backend's devices (public API only, so the backend also
+// registers into a core it was not built with)
+bool core_lists_our_devices() {
+    const size_t n = scrapgpu_get_device_count();
+    for (size_t i = 0; i < n; ++i) {
+        scrapgpu_device_t * d = nullptr;
+        if (scrapgpu_get_device(i, &d) == SCRAPGPU_STATUS_OK && dev_of(d) != nullptr) return true;
+    }
+    return false;
+}
+
+} // namespace
+
 extern "C" {
 
 scrapgpu_status scrapgpu_hip_register(void) {
@@ -905,7 +919,7 @@ scrapgpu_status scrapgpu_hip_register(void) {
     if (r.registered) {
         // the devices are probed once; the vtable is registered again after
         // scrapgpu_unregister_all_backends()
-        if (sg_registry_contains(api_device_count)) return SCRAPGPU_STATUS_OK;
+        if (r.devices.empty() || core_lists_our_devices()) return SCRAPGPU_STATUS_OK;
         return scrapgpu_register_backend(&kVtable);
     }
     int n = 0;
