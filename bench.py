@@ -10,7 +10,8 @@ Reported on one JSON line:
   value         weight GB/s of the whole token (all 252 kernels, wall clock over the timed steps)
   roofline      the token's largest product, gate+up (2 x 12288x4096 Q4_K as one MUL_MAT_MULTI):
                 algorithmic weight bytes per launch / mean launch duration from HIP events on its
-                stream (a profiling pass over all 36 layers right after the timed region), vs 8 TB/s;
+                stream (the 36 layers' gate+up launches as one HIP graph, replayed right after the
+                timed region), vs 8 TB/s;
                 `traffic` = HBM bytes per launch from the committed rocprofv3 PMC summary
   prefill       Q4_K M=512 (N=512 tokens) MFMA TFLOP/s on the two MLP shapes, vs 2.5 PFLOP/s bf16
   cpu_baseline  the oracle's reference-faithful CPU MUL_MAT (1 thread) on one gate matrix, N=1
@@ -135,24 +136,58 @@ def profile_kernels(model, tokens):
     return rows
 
 
-def profile_group(model, group, rounds):
-    """Mean launch time of one product of the token (all layers' instances, eagerly, `rounds`
-    times) from the library's per-launch HIP events on the model's stream."""
-    L = sg.lib()
-    model.st.sync()
-    L.scrapgpu_hip_profile_reset()
-    L.scrapgpu_hip_profile_enable(1)
+def hip_runtime():
+    """The HIP runtime the library itself runs on (already loaded in this process), for events."""
+    h = C.CDLL("libamdhip64.so.7")  # the soname libscrapgpu_hip.so links: the same loaded runtime
+    for f in ("hipEventCreate", "hipEventRecord", "hipEventSynchronize", "hipEventElapsedTime", "hipEventDestroy"):
+        getattr(h, f).restype = C.c_int
+    h.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+    h.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+    h.hipEventSynchronize.argtypes = [C.c_void_p]
+    h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+    h.hipEventDestroy.argtypes = [C.c_void_p]
+    return h
+
+
+def hip_check(err, what):
+    if err != 0:
+        raise RuntimeError(f"{what}: hipError {err}")
+
+
+def profile_group(model, group, replays):
+    """Mean launch time of one product of the token: the 36 layers' instances recorded as one plan
+    (a HIP graph) and replayed `replays` times between two HIP events on the model's stream."""
+    ops = model.by_group[group]
+    nodes = (sg.PlanNode * len(ops))(*[sg.PlanNode(C.sizeof(sg.PlanNode), op, 0) for op in ops])
+    pdesc = sg.PlanDesc(C.sizeof(sg.PlanDesc), nodes, len(ops))
+    plan = C.c_void_p()
+    sg.check(sg.lib().scrapgpu_plan_build(model.dev.handle, C.byref(pdesc), C.byref(plan)), "plan_build")
+    hip = hip_runtime()
+    stream = C.c_void_p(sg.lib().scrapgpu_hip_stream_native(model.st.handle))
+    ev = [C.c_void_p(), C.c_void_p()]
     try:
-        for _ in range(rounds):
-            for op in model.by_group[group]:
-                model.st.execute(op)
+        for e in ev:
+            hip_check(hip.hipEventCreate(C.byref(e)), "hipEventCreate")
+        for _ in range(2):
+            sg.check(sg.lib().scrapgpu_plan_execute(model.st.handle, plan), "plan_execute")
         model.st.sync()
+        hip_check(hip.hipEventRecord(ev[0], stream), "hipEventRecord")
+        for _ in range(replays):
+            sg.check(sg.lib().scrapgpu_plan_execute(model.st.handle, plan), "plan_execute")
+        hip_check(hip.hipEventRecord(ev[1], stream), "hipEventRecord")
+        hip_check(hip.hipEventSynchronize(ev[1]), "hipEventSynchronize")
+        ms = C.c_float()
+        hip_check(hip.hipEventElapsedTime(C.byref(ms), ev[0], ev[1]), "hipEventElapsedTime")
+        ms = ms.value / (replays * len(ops))
     finally:
-        L.scrapgpu_hip_profile_enable(0)
-    rows = sg.profile_table()
-    L.scrapgpu_hip_profile_reset()
-    r = rows[0]
-    return r["name"], r["ms"] / r["launches"], r["bytes"] / r["launches"]
+        for e in ev:
+            if e.value:
+                hip.hipEventDestroy(e)
+        sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
+    name = {"q+k+v": "matvec_multi_q4_k", "gate+up": "matvec_multi_q4_k", "down": "matvec_q6_k"}.get(group, "matvec_q4_k")
+    weights = {"q+k+v": ("q", "k", "v"), "gate+up": ("gate", "up")}.get(group, (group,))
+    by = sum(weight_bytes(dt, K, M) for n, dt, K, M in LAYER_SHAPES if n in weights)
+    return name, ms, by
 
 
 def bench_prefill(dev, st, n_tokens, reps):
@@ -283,7 +318,7 @@ def main():
     ktime = sum(r["ms"] for r in rows) / 3
     # the roofline kernel: the token's largest product (gate+up fused, 2 x 12288x4096 Q4_K)
     dom_group = "gate+up" if "gate+up" in model.by_group else "gate"
-    dom_name, dom_ms, dom_bytes = profile_group(model, dom_group, 3)
+    dom_name, dom_ms, dom_bytes = profile_group(model, dom_group, 10)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     kernels = {r["name"]: {"launches_per_token": r["launches"] // 3, "mean_us": round(r["ms"] / r["launches"] * 1e3, 2),
                            "GBps": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1)} for r in rows}
