@@ -394,12 +394,6 @@ template <int DT, int RG, int NC>
 __device__ __forceinline__ void step_mfma(const Fmt<DT> (&f)[RG], const typename Fmt<DT>::Raw (&raw)[RG], const ALane<DT> & al, int sg0,
                                           const XView & xv, float (&acc)[RG][NC]) {
     constexpr int ND = Fmt<DT>::ND;
-    v4i B[RG][4];
-#pragma unroll
-    for (int i = 0; i < RG; ++i) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) B[i][t] = Fmt<DT>::bop(raw[i], t);
-    }
 #pragma unroll
     for (int n = 0; n < NC; ++n) {
         const uint8_t * base = reinterpret_cast<const uint8_t *>(xv.xs + n * xv.nseg + sg0);
@@ -418,7 +412,7 @@ __device__ __forceinline__ void step_mfma(const Fmt<DT> (&f)[RG], const typename
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int u = ND == 1 ? 0 : (t >> 1);
-                D[u] = mfma(Aop[t], B[i][t], D[u]);
+                D[u] = mfma(Aop[t], Fmt<DT>::bop(raw[i], t), D[u]);
             }
             acc[i][n] += f[i].flush(raw[i], D, xf);
         }
@@ -510,12 +504,21 @@ struct Where {
     const float * x;
 };
 
+// (32-bit divisions: slice counts are < 65536; the common single-slice case divides nothing, so
+// the first loads issue right away)
 __device__ __forceinline__ Where where_of(const MvArgs & A) {
     Where w;
-    const int64_t sl = blockIdx.y;
-    w.i2 = sl % A.ne12;
-    w.i3 = sl / A.ne12;
-    w.w_off = (uint64_t) (w.i2 / A.r2) * A.w_s2 + (uint64_t) (w.i3 / A.r3) * A.w_s3;
+    if (gridDim.y == 1) {
+        w.i2 = w.i3 = 0;
+        w.w_off = 0;
+        w.x = A.x;
+        return w;
+    }
+    const uint32_t sl = blockIdx.y, ne12 = (uint32_t) A.ne12;
+    const uint32_t i2 = sl % ne12, i3 = sl / ne12;
+    w.i2 = i2;
+    w.i3 = i3;
+    w.w_off = (uint64_t) (i2 / (uint32_t) A.r2) * A.w_s2 + (uint64_t) (i3 / (uint32_t) A.r3) * A.w_s3;
     w.x = A.x + w.i2 * A.x_s2 + w.i3 * A.x_s3;
     return w;
 }
@@ -576,7 +579,7 @@ __device__ __forceinline__ void reduce_store(const MvArgs & A, const Where & wh,
 // Burst form (one column, <= SPW steps per wave, one tile of 16 * RG rows per work-group): the wave
 // first loads its x range, then issues every weight load, and only then converts x.
 template <int DT, int RG, int W, int SPW>
-__global__ __launch_bounds__(64 * W) void k_mvb(MvArgs A) {
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2 && RG == 1 ? 6 : SPW <= 2 ? 5 : 4, 8))) void k_mvb(MvArgs A) {
     using F = Fmt<DT>;
     using Raw = typename F::Raw;
     extern __shared__ uint8_t lds[];
@@ -830,7 +833,8 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     // per work-group. 32-row tiles (two row groups sharing each x operand) for large products,
     // 16-row tiles otherwise (more work-groups). 2 steps per wave up to K = 32 steps, then 4.
     if (nc == 1 && L.xvec && nst <= 64 && tuning("SCRAPGPU_HIP_MV_BURST", 1)) {
-        int rg = rows * slices >= (int64_t) 64 * cu_count ? 2 : 1;
+        // (the 32-row Q8_0 / Q6_K forms need more registers than 5 waves per SIMD leave them)
+        int rg = (dt == Q4_K || dt == Q4_0) && rows * slices >= (int64_t) 64 * cu_count ? 2 : 1;
         if (const int fr = tuning("SCRAPGPU_HIP_MV_RG", 0)) rg = fr >= 2 ? 2 : 1;
         const int sp = nst <= 32 ? 2 : 4;
         int W = 4;
