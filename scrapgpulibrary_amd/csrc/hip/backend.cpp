@@ -74,7 +74,7 @@ struct Stream {
     scrapgpu_object_header hdr;
     Device * dev;
     hipStream_t s;
-    uint8_t * scratch = nullptr; // bf16 activations of the prefill matmul (grown on demand)
+    uint8_t * scratch = nullptr; // prefill matmul: bf16 activations and split-K partials (grown on demand)
     size_t scratch_size = 0;
     uint64_t scratch_gen = 0;    // process-unique; renewed on every re-allocation (keys recorded graphs)
 };
@@ -629,11 +629,11 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
             SG_HIP(sgk::launch_matvec(m, cnt, cus, s->s, &name, &grid), "matvec launch");
             prof.done(name, bytes, flops);
         } else {
-            const scrapgpu_status st = ensure_scratch(s, sgk::matmul_scratch_bytes(m[0]));
+            const scrapgpu_status st = ensure_scratch(s, sgk::matmul_scratch_bytes(m[0], cus));
             if (st != SCRAPGPU_STATUS_OK) return st;
             ProfScope prof(s->s);
             const char * name = nullptr;
-            SG_HIP(sgk::launch_matmul_mfma(m[0], reinterpret_cast<uint16_t *>(s->scratch), cus, s->s, &name), "matmul launch");
+            SG_HIP(sgk::launch_matmul_mfma(m[0], s->scratch, cus, s->s, &name), "matmul launch");
             prof.done(name, bytes, flops);
         }
     }
@@ -761,7 +761,7 @@ scrapgpu_status plan_prepare(Stream * s, Plan * p) {
             std::memset(&a, 0, sizeof(a));
             const scrapgpu_tensor_desc & x = n.op.op == SCRAPGPU_OP_MUL_MAT ? n.op.inputs[1] : n.op.inputs[cnt];
             if (mul_mat_rule(n.op.inputs[i], x, n.op.outputs[i], 1, &a, nullptr) == SCRAPGPU_STATUS_OK && a.N > 8) {
-                need = std::max(need, sgk::matmul_scratch_bytes(a));
+                need = std::max(need, sgk::matmul_scratch_bytes(a, (int) s->dev->cus));
             }
         }
     }

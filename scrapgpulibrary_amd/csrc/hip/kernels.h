@@ -42,10 +42,11 @@ struct MatArgs {
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
                          uint64_t * grid_size);
 
-// prefill: bf16 MFMA with fp32 accumulate, weights dequantized into LDS (any N >= 1). `scratch`
-// (matmul_scratch_bytes(a) bytes of device memory, owned by the stream) receives x as bf16.
-size_t matmul_scratch_bytes(const MatArgs & a);
-hipError_t launch_matmul_mfma(const MatArgs & a, uint16_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name);
+// prefill: bf16 MFMA with fp32 accumulate, weights dequantized in registers (any N >= 1).
+// `scratch` (matmul_scratch_bytes(a, cu_count) bytes of device memory, owned by the stream)
+// receives x as bf16 and, when K is split over work-groups, their partial sums.
+size_t matmul_scratch_bytes(const MatArgs & a, int cu_count);
+hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name);
 
 // R32 pack (natural -> R32) or unpack of rows [row0, row0 + nrows) of one slice of M rows; row0 is
 // a multiple of 32. `nat` holds the natural bytes of those rows, `rep` is the slice's R32 base.
