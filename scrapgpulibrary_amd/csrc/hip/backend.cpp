@@ -541,6 +541,13 @@ scrapgpu_status mul_mat_rule(const scrapgpu_tensor_desc & w, const scrapgpu_tens
         return invalid("MUL_MAT: dst must be [ne01, ne11, ne12, ne13]");
     }
     if (x2 * x3 > 65535) return unsupported("MUL_MAT: more than 65535 slices", reason);
+    // the kernels address one slice of weights, and one slice of x in f16, with 32-bit offsets
+    if (sg::sat_mul(sg::row_size(w.dtype, K), (uint64_t) M) >= ((uint64_t) 1 << 32)) {
+        return unsupported("MUL_MAT: one slice of src0 must be smaller than 4 GiB", reason);
+    }
+    if (sg::sat_mul((uint64_t) K, (uint64_t) sg::dim1(x.ne[1])) >= ((uint64_t) 1 << 31)) {
+        return unsupported("MUL_MAT: one slice of src1 must hold fewer than 2^31 elements", reason);
+    }
     if (a) {
         a->dtype = w.dtype;
         a->M = M;

@@ -1,52 +1,46 @@
-// Prefill matmul over R32 weights on the bf16 MFMA units of gfx950 (fp32 accumulate), N > 8.
+// Prefill matmul over R32 weights on the f16 MFMA units of gfx950 (fp32 accumulate), N > 8.
 //
 // Replaces, for the hip backend, the reference's tiled mat-mat kernels k_mm_* / k_mmx_*
 // (src/backends/opencl11/kernels/mul_mm.cl:270-355, mul_mm_x.cl:437-539). Same product, new design:
 //
-//   pre-pass  x (fp32, any column stride) -> xb (bf16, [slice][N][K] contiguous) in stream scratch,
-//             once per op, so the GEMM reads half the activation bytes and converts nothing twice.
-//   GEMM      a work-group (4 waves) owns 128 weight rows x 128 tokens and walks K in stages of
-//             128. Wave w owns rows 32w .. 32w + 31 (two 16-row groups) and all 128 tokens.
-//               * B operand (weights): lane (r, g) of a 16-row group loads, per stage, the R32 units
-//                 of row r that hold its 32 codes (one 16-byte unit for Q4_K / Q4_0 / Q8_0-half,
-//                 three for Q6_K), dequantizes them in registers (d*sc*q - dmin*m in fp32, packed
-//                 to bf16) and feeds 8 of them to each of the stage's 4 MFMA k-steps. No weight
-//                 tile goes through LDS: every weight is dequantized exactly once per work-group.
-//               * A operand (activations): the 128 x 128 bf16 x tile of the stage, staged in LDS
-//                 (double-buffered, XOR-swizzled 16-byte chunks) and read as 8 token fragments per
-//                 k-step. The k order inside a step is whatever the weight lanes hold; the A reads
-//                 follow it (chunk(g, t) below), which the MFMA allows because its A and B operands
-//                 share one k mapping per lane group.
-//               * v_mfma_f32_16x16x32_bf16, 2 row groups x 8 token fragments per k-step: each B
-//                 fragment serves 8 MFMAs, each A fragment 2.
+//   pre-pass  x (fp32, any row stride) -> f16 rows [slice][N][K] in stream scratch, each token
+//             row scaled by a power of two that puts its largest magnitude in [2^14, 2^15) (no
+//             f16 overflow, no precision lost to subnormals); the factor is undone on the products.
+//   GEMM      v_mfma_f32_32x32x16_f16 (the 32x32 tile sustains the chip's f16 rate; 16x16x32
+//             issues at about half of it). A work-group is 4 waves; wave w owns RG groups of 32
+//             weight rows and BN tokens and walks K in stages of 128.
+//               * B operand (weights): lane (j, h) of a 32-row group holds row j, k-half h. Per
+//                 stage it loads the R32 units of row j that hold its 64 codes, and dequantizes 8
+//                 of them per k-step straight into f16 (see "weight codes" below). No weight goes
+//                 through LDS and every weight is dequantized once per work-group.
+//               * A operand (activations): the BN x 128 f16 x tile of the stage, double-buffered in
+//                 LDS (XOR-swizzled 16-byte chunks); one ds_read_b128 per lane per MFMA, shared by
+//                 the wave's RG row groups. The k order inside a step is whatever the weight lanes
+//                 hold; the A reads follow it (chunk(h, t) below).
 //             The next stage's weights and x tile are loaded into registers while the current
 //             stage computes; one barrier per stage.
-//   split-K   when the tiles alone cannot fill the GPU, K is split over work-groups that write
-//             partial sums to scratch; a reduction kernel adds them in split order (deterministic).
+//   split-K   when the tiles alone leave CUs idle, K is split over work-groups that write partial
+//             sums to scratch; a reduction kernel adds them in split order (deterministic).
 #include "kernels.h"
 
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
+#include <vector>
 
 namespace sgk {
 namespace {
 
-constexpr int BM = 128, BK = 128;
+constexpr int BK = 128;
 constexpr int kThreads = 256;
 constexpr int kChunks = BK / 8; // 16-byte chunks per LDS row of the x tile
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
-
-// two floats -> two bf16 (round to nearest even) in one v_cvt_pk_bf16_f32
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-    const bf16x2 v = __builtin_convertvector((f32x2{a, b}), bf16x2);
-    return __builtin_bit_cast(uint32_t, v);
-}
 
 __device__ __forceinline__ float half_bits(uint32_t h) {
     return __half2float(__ushort_as_half((unsigned short) (h & 0xFFFFu)));
@@ -56,26 +50,87 @@ __device__ __forceinline__ uint4 load16(const uint8_t * p) {
     return *reinterpret_cast<const uint4 *>(p);
 }
 
-// byte i of w as a float (v_cvt_f32_ubyte<i>: one instruction; the compiler would otherwise
-// extract the byte first)
-template <int I>
-__device__ __forceinline__ float ubyte(uint32_t w) {
-    float f;
-    if constexpr (I == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(w));
-    else if constexpr (I == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(w));
-    else if constexpr (I == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(w));
-    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(w));
-    return f;
+__device__ __forceinline__ uint32_t load_u16(const uint8_t * p) {
+    return *reinterpret_cast<const uint16_t *>(p);
 }
 
-// 8 bf16 = scale * byte_i - offset for the bytes of words w0, w1 (byte values 0..255)
-__device__ __forceinline__ bf16x8 deq8(uint32_t w0, uint32_t w1, float scale, float offset) {
-    uint4 o;
-    o.x = pack2(fmaf(scale, ubyte<0>(w0), -offset), fmaf(scale, ubyte<1>(w0), -offset));
-    o.y = pack2(fmaf(scale, ubyte<2>(w0), -offset), fmaf(scale, ubyte<3>(w0), -offset));
-    o.z = pack2(fmaf(scale, ubyte<0>(w1), -offset), fmaf(scale, ubyte<1>(w1), -offset));
-    o.w = pack2(fmaf(scale, ubyte<2>(w1), -offset), fmaf(scale, ubyte<3>(w1), -offset));
-    return __builtin_bit_cast(bf16x8, o);
+__device__ __forceinline__ f16x2 h2(float v) {
+    const _Float16 h = (_Float16) v;
+    return f16x2{h, h};
+}
+
+__device__ __forceinline__ f16x2 as_h2(uint32_t v) {
+    return __builtin_bit_cast(f16x2, v);
+}
+
+__device__ __forceinline__ uint32_t mad24(uint32_t a, uint32_t b, uint32_t c) {
+    return __umul24(a, b) + c;
+}
+
+// ---- weight codes -> f16 B operands ----------------------------------------------------------
+// A code c (0..255) in the low byte of a 16-bit half or'ed with 0x6400 reads as the f16 value
+// 1024 + c exactly (f16 spacing is 1 on [1024, 2048)), so one v_and_or_b32 (or v_perm_b32) turns
+// two codes into an f16 pair, and one packed add (or a packed fma for a code held 4 bits up:
+// (1024 + 16c) / 16 - 64 = c) recovers the integers themselves. The scale is then one packed fma.
+// Every B fragment holds the 8 elements e0..e7 of a run in the order e0 e2 e1 e3 e4 e6 e5 e7 (the
+// pairs a dword of 4 byte codes gives), and the x rows in scratch carry the same order.
+__device__ __forceinline__ uint32_t codes2(uint32_t v, uint32_t mask) {
+    // one v_and_or_b32 (the compiler splits it when both constants are literals); the magic
+    // lives in a VGPR, the mask in an SGPR: one constant-bus operand
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask), "v"(0x64006400u));
+    return r;
+}
+
+// bytes 0, 2 / 1, 3 of w as the f16 pairs 1024 + byte
+__device__ __forceinline__ uint32_t bytes02(uint32_t w) {
+    return __builtin_amdgcn_perm(0x64646464u, w, 0x04020400u);
+}
+__device__ __forceinline__ uint32_t bytes13(uint32_t w) {
+    return __builtin_amdgcn_perm(0x64646464u, w, 0x04030401u);
+}
+
+// f16 pair s * (h + bias) + o for an f16 pair h of integers (exact up to the fma's rounding)
+__device__ __forceinline__ uint32_t affine(uint32_t h, f16x2 bias, f16x2 s, f16x2 o) {
+    const f16x2 c = as_h2(h) + bias;
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, s, o));
+}
+__device__ __forceinline__ uint32_t affine16(uint32_t h, f16x2 bias, f16x2 s, f16x2 o) {
+    const f16x2 c = __builtin_elementwise_fma(as_h2(h), f16x2{(_Float16) 0.0625f, (_Float16) 0.0625f}, bias);
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, s, o));
+}
+
+// 4-bit codes of the dwords w0, w1 (low nibbles, or high nibbles when HI) -> 8 f16 s * (c + cb) + o
+template <bool HI>
+__device__ __forceinline__ f16x8 nib8(uint32_t w0, uint32_t w1, _Float16 cb, f16x2 s, f16x2 o) {
+    const uint32_t mask = HI ? 0x00F000F0u : 0x000F000Fu;
+    uint4 v;
+    if constexpr (HI) {
+        const f16x2 b = f16x2{(_Float16) (cb - (_Float16) 64.0f), (_Float16) (cb - (_Float16) 64.0f)};
+        v.x = affine16(codes2(w0, mask), b, s, o);
+        v.y = affine16(codes2(w0 >> 8, mask), b, s, o);
+        v.z = affine16(codes2(w1, mask), b, s, o);
+        v.w = affine16(codes2(w1 >> 8, mask), b, s, o);
+    } else {
+        const f16x2 b = f16x2{(_Float16) (cb - (_Float16) 1024.0f), (_Float16) (cb - (_Float16) 1024.0f)};
+        v.x = affine(codes2(w0, mask), b, s, o);
+        v.y = affine(codes2(w0 >> 8, mask), b, s, o);
+        v.z = affine(codes2(w1, mask), b, s, o);
+        v.w = affine(codes2(w1 >> 8, mask), b, s, o);
+    }
+    return __builtin_bit_cast(f16x8, v);
+}
+
+// byte codes of the dwords w0, w1 -> 8 f16 s * (c + cb)
+__device__ __forceinline__ f16x8 byte8(uint32_t w0, uint32_t w1, _Float16 cb, f16x2 s) {
+    const f16x2 b = f16x2{(_Float16) (cb - (_Float16) 1024.0f), (_Float16) (cb - (_Float16) 1024.0f)};
+    const f16x2 z = f16x2{(_Float16) 0.0f, (_Float16) 0.0f};
+    uint4 v;
+    v.x = affine(bytes02(w0), b, s, z);
+    v.y = affine(bytes13(w0), b, s, z);
+    v.z = affine(bytes02(w1), b, s, z);
+    v.w = affine(bytes13(w1), b, s, z);
+    return __builtin_bit_cast(f16x8, v);
 }
 
 // 6-bit scale and min of Q4_K sub-block j (0..7) from the header words hd.y, hd.z, hd.w (get_scale_min_k4)
@@ -105,268 +160,279 @@ struct RowAddr {
     }
 };
 
-// ---- per format: one stage (128 elements of K) of one weight row for lane group g ---------------
-// init() resolves the lane's row and lane group once (64-bit bases, 32-bit per-stage strides);
-// load(s) fetches the lane's bytes of stage s into a Raw; prep() turns a Raw's block scales into
-// the stage's fp32 factors; bop(raw, sc, t) is the lane's B fragment (8 bf16) for k-step t;
-// chunk(g, t) is the 16-byte chunk (8 elements) of the stage's x row that the fragment pairs with.
+// ---- per format: one stage (128 elements of K) of one weight row for k-half h ----------------
+// init() resolves the lane's row and k-half once into 32-bit byte offsets from the slice's weight
+// base (one slice of weights is < 4 GiB, checked on the host) and the R32 unit stride
+// U = 16 * rows-in-group; load(w, s) fetches the lane's bytes of stage s into a Raw (24-bit
+// multiply-adds for the addresses); prep() turns a Raw's block scales into the stage's f16 factors;
+// bop(raw, sc, t) is the lane's B fragment (8 f16) for k-step t = 0..7; chunk(h, t) is the 16-byte
+// chunk (8 elements) of the stage's x row that the fragment pairs with.
 
 template <int DT> struct PFmt;
 
-// Q4_K: stage s = chunks 2 (s % 2), 2 (s % 2) + 1 of block s / 2; lane group g: unit 4 (s % 2) + g
-// of the block (chunk c = 2 (s % 2) + g / 2, unit u = g % 2). k-step t: low (t < 2) / high nibbles
-// of bytes 8 (t % 2) .. +7: elements 64c + 32 (t / 2) + 16u + 8 (t % 2) + e.
+// Q4_K: stage s = 64-element groups 2 (s % 2), 2 (s % 2) + 1 of block s / 2; k-half h takes group
+// c = 2 (s % 2) + h, i.e. its two 16-byte units (bytes 0..31 of the group). k-step t: low (t < 4)
+// or high nibbles of bytes 8 (t % 4) .. +7 = elements 64c + 8t + e of the block.
 template <> struct PFmt<Q4_K> {
     struct Raw {
-        uint4 q, hd;
+        uint4 q0, q1, hd;
     };
     struct Sc {
-        float s0, o0, s1, o1;
+        f16x2 s0, o0, s1, o1;
     };
-    const uint8_t * qb;
-    const uint8_t * hb;
-    uint32_t blk, half, hblk;
-    int g;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb, const RowAddr & ra, int g_) {
-        g = g_;
-        qb = w + (uint64_t) ra.g0 * nb * 128 + (uint64_t) ra.lr * 16 + (uint64_t) g * ra.rs * 16;
-        hb = w + (uint64_t) M * nb * 128 + (uint64_t) ra.g0 * nb * 16 + (uint64_t) ra.lr * 16;
-        blk = ra.rs * 128;
-        half = ra.rs * 64;
-        hblk = ra.rs * 16;
+    uint32_t qo, ho, u;
+    int h;
+    __device__ void init(int64_t M, int64_t nb, const RowAddr & ra, int h_) {
+        h = h_;
+        u = ra.rs * 16;
+        qo = (uint32_t) (ra.g0 * nb * 128 + ra.lr * 16) + 2 * h * u;
+        ho = (uint32_t) (M * nb * 128 + ra.g0 * nb * 16 + ra.lr * 16);
     }
-    __device__ Raw load(int64_t s) const {
-        const uint32_t b = (uint32_t) (s >> 1), h = (uint32_t) (s & 1);
-        return Raw{load16(qb + b * blk + h * half), load16(hb + b * hblk)};
+    // a block is 8 units; stage s starts at unit 4s
+    __device__ Raw load(const uint8_t * w, int64_t s) const {
+        const uint32_t q = mad24((uint32_t) s * 4, u, qo);
+        return Raw{load16(w + q), load16(w + q + u), load16(w + mad24((uint32_t) (s >> 1), u, ho))};
     }
     __device__ Sc prep(const Raw & r, int64_t s) const {
-        const int c = 2 * (int) (s & 1) + (g >> 1);
+        const int c = 2 * (int) (s & 1) + h;
         const float d = half_bits(r.hd.x), dmin = half_bits(r.hd.x >> 16);
         float sc0, m0, sc1, m1;
         k4_scale_min(r.hd, 2 * c, sc0, m0);
         k4_scale_min(r.hd, 2 * c + 1, sc1, m1);
-        return Sc{d * sc0, dmin * m0, d * sc1, dmin * m1};
+        return Sc{h2(d * sc0), h2(-(dmin * m0)), h2(d * sc1), h2(-(dmin * m1))};
     }
-    __device__ static bf16x8 bop(const Raw & r, const Sc & c, int t) {
-        const uint32_t w0 = (t & 1) ? r.q.z : r.q.x, w1 = (t & 1) ? r.q.w : r.q.y;
-        const int sh = (t >> 1) * 4;
-        return deq8((w0 >> sh) & 0x0F0F0F0Fu, (w1 >> sh) & 0x0F0F0F0Fu, t < 2 ? c.s0 : c.s1, t < 2 ? c.o0 : c.o1);
+    __device__ static f16x8 bop(const Raw & r, const Sc & c, int t) {
+        const uint4 & q = (t & 3) < 2 ? r.q0 : r.q1;
+        const uint32_t w0 = (t & 1) ? q.z : q.x, w1 = (t & 1) ? q.w : q.y;
+        return t < 4 ? nib8<false>(w0, w1, (_Float16) 0.0f, c.s0, c.o0) : nib8<true>(w0, w1, (_Float16) 0.0f, c.s1, c.o1);
     }
-    __device__ static int chunk(int g, int t) {
-        return 8 * (g >> 1) + 4 * (t >> 1) + 2 * (g & 1) + (t & 1);
+    __device__ static int chunk(int h, int t) {
+        return 8 * h + t;
     }
 };
 
-// Q6_K: stage s = half h = s % 2 of block s / 2; lane group g: hf = g % 2 and runs
-// rr = 2 (g / 2) + {0, 1} (units ql 4h + hf, ql 4h + 2 + hf, qh 8 + 2h + hf). k-step t: run
-// rr = 2 (g / 2) + t / 2, elements 128h + 32rr + 16hf + 8 (t % 2) + e.
+// Q6_K: stage s = half n = s % 2 of block s / 2 (128 elements: runs rr = 0..3 of 32). k-half h
+// takes elements l = 16h .. 16h + 15 of every run: units ql 4n + h (runs 0, 2), ql 4n + 2 + h
+// (runs 1, 3), qh 8 + 2n + h. k-step t: run rr = t / 2, elements 32rr + 16h + 8 (t % 2) + e.
 template <> struct PFmt<Q6_K> {
     struct Raw {
         uint4 qa, qc, qh, sc;
         uint32_t d;
     };
     struct Sc {
-        float s0, s1;
+        f16x2 s[4];
     };
-    const uint8_t * qb;
-    const uint8_t * sb;
-    const uint8_t * db;
-    uint32_t blk, unit, sblk, dblk;
-    int g;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb, const RowAddr & ra, int g_) {
-        g = g_;
-        qb = w + (uint64_t) ra.g0 * nb * 192 + (uint64_t) ra.lr * 16 + (uint64_t) (g & 1) * ra.rs * 16;
-        sb = w + (uint64_t) M * nb * 192 + (uint64_t) ra.g0 * nb * 16 + (uint64_t) ra.lr * 16;
-        db = w + (uint64_t) M * nb * 208 + (uint64_t) ra.g0 * nb * 2 + (uint64_t) ra.lr * 2;
-        blk = ra.rs * 192;
-        unit = ra.rs * 16;
-        sblk = ra.rs * 16;
-        dblk = ra.rs * 2;
+    uint32_t qo, so, dof, u;
+    int h;
+    __device__ void init(int64_t M, int64_t nb, const RowAddr & ra, int h_) {
+        h = h_;
+        u = ra.rs * 16;
+        qo = (uint32_t) (ra.g0 * nb * 192 + ra.lr * 16) + h * u;
+        so = (uint32_t) (M * nb * 192 + ra.g0 * nb * 16 + ra.lr * 16);
+        dof = (uint32_t) (M * nb * 208 + ra.g0 * nb * 2 + ra.lr * 2);
     }
-    __device__ Raw load(int64_t s) const {
-        const uint32_t b = (uint32_t) (s >> 1), h = (uint32_t) (s & 1);
-        const uint8_t * q = qb + b * blk;
+    // a block is 12 quant units (ql 0..7, qh 8..11), 1 scale unit and the d halves
+    __device__ Raw load(const uint8_t * w, int64_t s) const {
+        const uint32_t b = (uint32_t) (s >> 1), n = (uint32_t) (s & 1);
         Raw r;
-        r.qa = load16(q + (4 * h) * unit);     // ql[64h + 16hf + i]
-        r.qc = load16(q + (4 * h + 2) * unit); // ql[64h + 32 + 16hf + i]
-        r.qh = load16(q + (8 + 2 * h) * unit); // qh[32h + 16hf + i]
-        r.sc = load16(sb + b * sblk);
-        r.d = *reinterpret_cast<const uint16_t *>(db + b * dblk);
+        const uint32_t qa = mad24(12 * b + 4 * n, u, qo);
+        r.qa = load16(w + qa);                                 // ql[64n + l]
+        r.qc = load16(w + qa + 2 * u);                         // ql[64n + 32 + l]
+        r.qh = load16(w + mad24(12 * b + 8 + 2 * n, u, qo)); // qh[32n + l]
+        r.sc = load16(w + mad24(b, u, so));
+        r.d = load_u16(w + mad24(b, u >> 3, dof));
         return r;
     }
-    // the signed 8-bit scales of the lane's two runs: bytes 8h + hf + 2rr (stored xor 0x80)
+    // the signed 8-bit scale of run rr sits at byte 8n + h + 2rr (stored xor 0x80): word 2n (runs
+    // 0, 1) or 2n + 1 (runs 2, 3), byte h or h + 2
     __device__ Sc prep(const Raw & r, int64_t s) const {
-        const int h = (int) (s & 1), hf = g & 1, rr = 2 * (g >> 1);
+        const uint32_t lo = (s & 1) ? r.sc.z : r.sc.x, hi = (s & 1) ? r.sc.w : r.sc.y;
+        const int sh = 8 * h;
         const float d = half_bits(r.d);
-        const int b0 = 8 * h + hf + 2 * rr, b1 = b0 + 2;
-        const uint32_t w0 = b0 < 4 ? r.sc.x : b0 < 8 ? r.sc.y : b0 < 12 ? r.sc.z : r.sc.w;
-        const uint32_t w1 = b1 < 4 ? r.sc.x : b1 < 8 ? r.sc.y : b1 < 12 ? r.sc.z : r.sc.w;
-        return Sc{d * ((float) ((w0 >> (8 * (b0 & 3))) & 0xFFu) - 128.0f), d * ((float) ((w1 >> (8 * (b1 & 3))) & 0xFFu) - 128.0f)};
+        Sc c;
+        c.s[0] = h2(d * ((float) ((lo >> sh) & 0xFFu) - 128.0f));
+        c.s[1] = h2(d * ((float) ((lo >> (sh + 16)) & 0xFFu) - 128.0f));
+        c.s[2] = h2(d * ((float) ((hi >> sh) & 0xFFu) - 128.0f));
+        c.s[3] = h2(d * ((float) ((hi >> (sh + 16)) & 0xFFu) - 128.0f));
+        return c;
     }
-    // 6-bit codes: low nibbles of qa (rr 0) / qc (rr 1), high nibbles (rr 2, 3), bits 2rr, 2rr + 1 of qh
-    __device__ bf16x8 bop(const Raw & r, const Sc & c, int t) const {
-        const int rr = 2 * (g >> 1) + (t >> 1);
-        const uint4 ql = (t >> 1) ? r.qc : r.qa;
-        const int ls = (g >> 1) * 4, hs = 2 * rr;
+    // 6-bit codes of run rr: nibble rr / 2 of ql (qa for even rr, qc for odd), bits 2rr, 2rr + 1 of qh
+    __device__ static f16x8 bop(const Raw & r, const Sc & c, int t) {
+        const int rr = t >> 1;
+        const uint4 & ql = (rr & 1) ? r.qc : r.qa;
+        const int ls = 4 * (rr >> 1), hs = 2 * rr;
         const uint32_t l0 = (t & 1) ? ql.z : ql.x, l1 = (t & 1) ? ql.w : ql.y;
         const uint32_t h0 = (t & 1) ? r.qh.z : r.qh.x, h1 = (t & 1) ? r.qh.w : r.qh.y;
         const uint32_t v0 = ((l0 >> ls) & 0x0F0F0F0Fu) | (((h0 >> hs) << 4) & 0x30303030u);
         const uint32_t v1 = ((l1 >> ls) & 0x0F0F0F0Fu) | (((h1 >> hs) << 4) & 0x30303030u);
-        const float ds = (t >> 1) ? c.s1 : c.s0;
-        return deq8(v0, v1, ds, 32.0f * ds);
+        return byte8(v0, v1, (_Float16) -32.0f, c.s[rr]);
     }
-    __device__ static int chunk(int g, int t) {
-        return 4 * (2 * (g >> 1) + (t >> 1)) + 2 * (g & 1) + (t & 1);
+    __device__ static int chunk(int h, int t) {
+        return 4 * (t >> 1) + 2 * h + (t & 1);
     }
 };
 
-// Q8_0: stage s = blocks 4s .. 4s + 3; lane group g: block 4s + g (both units, d). k-step t: bytes
-// 8t .. 8t + 7 = elements 32g + 8t + e. Blocks past the end of the row contribute zero.
+// Q8_0: stage s = blocks 4s .. 4s + 3; k-half h takes blocks 4s + 2h + j, j = 0, 1 (2 units and a
+// d each). k-step t: block j = t / 4, bytes 8 (t % 4) .. +7 = elements 32 (2h + j) + 8 (t % 4) + e
+// of the stage. Blocks past the end of the row read the last block with scale 0.
 template <> struct PFmt<Q8_0> {
     struct Raw {
-        uint4 q0, q1;
-        uint32_t d;
+        uint4 q[4];
+        uint32_t d; // d of block j in bits 16j
     };
     struct Sc {
-        float s;
+        f16x2 s[2];
     };
-    const uint8_t * qb;
-    const uint8_t * db;
-    uint32_t stage, unit, dstage;
-    int64_t nb;
-    int g;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, const RowAddr & ra, int g_) {
-        g = g_;
-        nb = nb_;
-        qb = w + (uint64_t) ra.g0 * nb * 32 + (uint64_t) ra.lr * 16 + (uint64_t) g * ra.rs * 32;
-        db = w + (uint64_t) M * nb * 32 + (uint64_t) ra.g0 * nb * 2 + (uint64_t) ra.lr * 2 + (uint64_t) g * ra.rs * 2;
-        stage = ra.rs * 128;
-        unit = ra.rs * 16;
-        dstage = ra.rs * 8;
+    uint32_t qo, dof, u, last;
+    int h;
+    __device__ void init(int64_t M, int64_t nb, const RowAddr & ra, int h_) {
+        h = h_;
+        u = ra.rs * 16;
+        qo = (uint32_t) (ra.g0 * nb * 32 + ra.lr * 16);
+        dof = (uint32_t) (M * nb * 32 + ra.g0 * nb * 2 + ra.lr * 2);
+        last = (uint32_t) (nb - 1);
     }
-    __device__ Raw load(int64_t s) const {
-        const bool ok = s * 4 + g < nb;
-        const uint32_t ss = ok ? (uint32_t) s : 0u; // past the row: a real block, scale 0
+    // block b: units 2b, 2b + 1 at 2b U; its d at b U / 8 in the d area
+    __device__ Raw load(const uint8_t * w, int64_t s) const {
+        const uint32_t b0 = (uint32_t) s * 4 + 2 * h;
         Raw r;
-        r.q0 = load16(qb + ss * stage);
-        r.q1 = load16(qb + ss * stage + unit);
-        r.d = ok ? *reinterpret_cast<const uint16_t *>(db + ss * dstage) : 0u;
+        r.d = 0;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t b = min(b0 + j, last);
+            const uint32_t q = mad24(2 * b, u, qo);
+            r.q[2 * j] = load16(w + q);
+            r.q[2 * j + 1] = load16(w + q + u);
+            if (b0 + j <= last) r.d |= load_u16(w + mad24(b, u >> 3, dof)) << (16 * j);
+        }
         return r;
     }
     __device__ Sc prep(const Raw & r, int64_t) const {
-        return Sc{half_bits(r.d)};
+        return Sc{{h2(half_bits(r.d)), h2(half_bits(r.d >> 16))}};
     }
-    __device__ static bf16x8 bop(const Raw & r, const Sc & c, int t) {
-        const uint4 & q = t < 2 ? r.q0 : r.q1;
+    __device__ static f16x8 bop(const Raw & r, const Sc & c, int t) {
+        const uint4 & q = r.q[2 * (t >> 2) + ((t & 3) >> 1)];
         const uint32_t w0 = (t & 1) ? q.z : q.x, w1 = (t & 1) ? q.w : q.y;
-        return deq8(w0, w1, c.s, 128.0f * c.s); // stored xor 0x80: value = (u - 128) * d
+        return byte8(w0, w1, (_Float16) -128.0f, c.s[t >> 2]); // stored xor 0x80: value = (u - 128) d
     }
-    __device__ static int chunk(int g, int t) {
-        return 4 * g + t;
+    __device__ static int chunk(int h, int t) {
+        return 8 * h + t;
     }
 };
 
-// Q4_0: stage s = blocks 4s .. 4s + 3; lane group g: block 4s + g. k-step t: low (t < 2) / high
-// nibbles of bytes 8 (t % 2) .. +7 = elements 32g + 8t + e.
+// Q4_0: stage s = blocks 4s .. 4s + 3; k-half h takes blocks 4s + 2h + j, j = 0, 1 (1 unit and a d
+// each). k-step t: block j = t / 4; low (t % 4 < 2) or high nibbles of bytes 8 (t % 2) .. +7 =
+// elements 32 (2h + j) + 8 (t % 4) + e of the stage.
 template <> struct PFmt<Q4_0> {
     struct Raw {
-        uint4 q;
+        uint4 q[2];
         uint32_t d;
     };
     struct Sc {
-        float s;
+        f16x2 s[2];
     };
-    const uint8_t * qb;
-    const uint8_t * db;
-    uint32_t stage, dstage;
-    int64_t nb;
-    int g;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, const RowAddr & ra, int g_) {
-        g = g_;
-        nb = nb_;
-        qb = w + (uint64_t) ra.g0 * nb * 16 + (uint64_t) ra.lr * 16 + (uint64_t) g * ra.rs * 16;
-        db = w + (uint64_t) M * nb * 16 + (uint64_t) ra.g0 * nb * 2 + (uint64_t) ra.lr * 2 + (uint64_t) g * ra.rs * 2;
-        stage = ra.rs * 64;
-        dstage = ra.rs * 8;
+    uint32_t qo, dof, u, last;
+    int h;
+    __device__ void init(int64_t M, int64_t nb, const RowAddr & ra, int h_) {
+        h = h_;
+        u = ra.rs * 16;
+        qo = (uint32_t) (ra.g0 * nb * 16 + ra.lr * 16);
+        dof = (uint32_t) (M * nb * 16 + ra.g0 * nb * 2 + ra.lr * 2);
+        last = (uint32_t) (nb - 1);
     }
-    __device__ Raw load(int64_t s) const {
-        const bool ok = s * 4 + g < nb;
-        const uint32_t ss = ok ? (uint32_t) s : 0u;
+    __device__ Raw load(const uint8_t * w, int64_t s) const {
+        const uint32_t b0 = (uint32_t) s * 4 + 2 * h;
         Raw r;
-        r.q = load16(qb + ss * stage);
-        r.d = ok ? *reinterpret_cast<const uint16_t *>(db + ss * dstage) : 0u;
+        r.d = 0;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t b = min(b0 + j, last);
+            r.q[j] = load16(w + mad24(b, u, qo));
+            if (b0 + j <= last) r.d |= load_u16(w + mad24(b, u >> 3, dof)) << (16 * j);
+        }
         return r;
     }
     __device__ Sc prep(const Raw & r, int64_t) const {
-        return Sc{half_bits(r.d)};
+        return Sc{{h2(half_bits(r.d)), h2(half_bits(r.d >> 16))}};
     }
-    __device__ static bf16x8 bop(const Raw & r, const Sc & c, int t) {
-        const uint32_t w0 = (t & 1) ? r.q.z : r.q.x, w1 = (t & 1) ? r.q.w : r.q.y;
-        const int sh = (t >> 1) * 4;
-        return deq8((w0 >> sh) & 0x0F0F0F0Fu, (w1 >> sh) & 0x0F0F0F0Fu, c.s, 8.0f * c.s);
+    __device__ static f16x8 bop(const Raw & r, const Sc & c, int t) {
+        const uint4 & q = r.q[t >> 2];
+        const uint32_t w0 = (t & 1) ? q.z : q.x, w1 = (t & 1) ? q.w : q.y;
+        const f16x2 z = f16x2{(_Float16) 0.0f, (_Float16) 0.0f};
+        return (t & 3) < 2 ? nib8<false>(w0, w1, (_Float16) -8.0f, c.s[t >> 2], z) : nib8<true>(w0, w1, (_Float16) -8.0f, c.s[t >> 2], z);
     }
-    __device__ static int chunk(int g, int t) {
-        return 4 * g + t;
+    __device__ static int chunk(int h, int t) {
+        return 8 * h + t;
     }
 };
 
 struct MmArgs {
     MatArgs a;
-    const uint16_t * xb; // bf16 activations [slices][N][K]
+    const uint16_t * xb; // f16 activations [slices][N][K], each row scaled (k_x_to_f16)
+    const float * xs;    // [slices][N]: the factor that undoes a row's scaling
     float * part;        // split-K partial sums [split][slices][N][M] (split > 1)
     int64_t tiles_m, tiles_n;
     int64_t stages;      // stages of K (BK elements each)
     int split;           // work-groups along K per tile
 };
 
-// x tile in LDS: row n (token), 16-byte chunk c at (n * kChunks + (c ^ (n & 15))) * 8 bf16
+// x tile in LDS: row n (token), 16-byte chunk c at (n * kChunks + (c ^ (n & 15))) * 8 f16
 __device__ __forceinline__ int xsw(int n, int c) {
     return (n * kChunks + (c ^ (n & 15))) * 8;
 }
 
-// the x tile of one stage: BN tokens x 16 chunks, BN / 16 chunks per thread (token p / 16, chunk
-// p % 16 for p = threadIdx.x + 256 i); global pointers and LDS offsets resolved once
+// the x tile of one stage: BN tokens x 16 chunks; thread p loads chunk p % 16 of tokens
+// p / 16 + 16 i (i < BN / 16): one 32-bit element offset, LDS slot and row mask cover all of them
 template <int BN>
 struct XTile {
     static constexpr int NP = BN * kChunks / kThreads;
-    const uint16_t * src[NP];
-    int dst[NP];
-    uint32_t kc[NP]; // element offset of the chunk inside a stage
-    bool row_ok[NP];
+    uint32_t off;  // element offset of (token p / 16, chunk p % 16) in the slice's x rows
+    uint32_t step; // 16 tokens
+    uint32_t kc;   // element offset of the chunk inside a stage
+    int dst;
+    uint32_t ok;   // bit i: token p / 16 + 16 i < N
     uint4 v[NP];
-    __device__ void init(const uint16_t * xb, int64_t N, int64_t K, int64_t n0) {
+    __device__ void init(int64_t N, int64_t K, int64_t n0) {
+        const int p = threadIdx.x;
+        kc = 8 * (p & 15);
+        off = (uint32_t) ((n0 + (p >> 4)) * K) + kc;
+        step = (uint32_t) (16 * K);
+        dst = xsw(p >> 4, p & 15); // token + 16 i keeps the swizzle: slot dst + 16 i rows
+        ok = 0;
 #pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            const int p = threadIdx.x + kThreads * i;
-            const int64_t n = n0 + (p >> 4);
-            row_ok[i] = n < N;
-            kc[i] = 8 * (p & 15);
-            src[i] = xb + (row_ok[i] ? n : 0) * K + kc[i];
-            dst[i] = xsw(p >> 4, p & 15);
-        }
+        for (int i = 0; i < NP; ++i) ok |= (n0 + (p >> 4) + 16 * i < N ? 1u : 0u) << i;
     }
     // stage starting at element k0; `full` when all BK elements lie inside K
-    __device__ void load(int64_t k0, int64_t K, bool full) {
+    __device__ void load(const uint16_t * xb, int64_t k0, int64_t K, bool full) {
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
-            const bool ok = row_ok[i] && (full || k0 + kc[i] < K);
-            v[i] = ok ? *reinterpret_cast<const uint4 *>(src[i] + k0) : make_uint4(0, 0, 0, 0);
+            const bool in = ((ok >> i) & 1u) && (full || k0 + kc < K);
+            v[i] = in ? *reinterpret_cast<const uint4 *>(xb + (off + i * step + (uint32_t) k0)) : make_uint4(0, 0, 0, 0);
         }
     }
     __device__ void store(uint16_t * X) const {
 #pragma unroll
-        for (int i = 0; i < NP; ++i) *reinterpret_cast<uint4 *>(X + dst[i]) = v[i];
+        for (int i = 0; i < NP; ++i) *reinterpret_cast<uint4 *>(X + dst + i * 16 * BK) = v[i];
     }
 };
 
-template <int DT, int BN>
-__global__ __launch_bounds__(kThreads, BN == 64 ? 3 : 2) void k_matmul(MmArgs L) {
-    constexpr int NF = BN / 16; // token fragments per wave
+// work-groups per CU that the register file (and, at BN = 128, the LDS) holds
+constexpr int occupancy_of(int dt, int bn, int rg) {
+    return bn == 64 && rg == 1 ? (dt == Q6_K ? 2 : 3) : bn == 128 && rg == 2 ? 1 : 2;
+}
+
+template <int DT, int BN, int RG>
+__global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(MmArgs L) {
+    constexpr int NF = BN / 32; // token fragments per wave
+    constexpr int BMT = 128 * RG;
     using F = PFmt<DT>;
     using Raw = typename F::Raw;
+    struct RawSet {
+        Raw r[RG];
+    };
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_mm[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = lane & 15, g = lane >> 4;
+    const int j = lane & 31, h = lane >> 5;
     const int64_t tile = blockIdx.x / L.split;
     const int split = (int) (blockIdx.x % L.split);
     const int64_t tm = tile % L.tiles_m, tn = tile / L.tiles_m;
@@ -374,62 +440,82 @@ __global__ __launch_bounds__(kThreads, BN == 64 ? 3 : 2) void k_matmul(MmArgs L)
     const int64_t i2 = sl % L.a.ne12, i3 = sl / L.a.ne12;
     const uint8_t * w = L.a.w + (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
     const int64_t K = L.a.K, N = L.a.N, M = L.a.M, nb = L.a.nb;
-    const int64_t m0 = tm * BM, n0 = tn * BN;
+    const int64_t m0 = tm * BMT + 32 * RG * wave, n0 = tn * BN;
     const int64_t s0 = L.stages * split / L.split, s1 = L.stages * (split + 1) / L.split;
 
-    F f0, f1;
-    f0.init(w, M, nb, RowAddr(M, m0 + 32 * wave + r), g);
-    f1.init(w, M, nb, RowAddr(M, m0 + 32 * wave + 16 + r), g);
+    F f[RG];
+#pragma unroll
+    for (int i = 0; i < RG; ++i) f[i].init(M, nb, RowAddr(M, m0 + 32 * i + j), h);
+    const uint16_t * xb = L.xb + (uint64_t) sl * N * K;
     XTile<BN> xt;
-    xt.init(L.xb + (uint64_t) sl * N * K, N, K, n0);
-    // LDS element offsets of the lane's A fragments: k-step t, token fragment f at aoff[t] + 16 f rows
-    int aoff[4];
+    xt.init(N, K, n0);
+    // LDS element offsets of the lane's A fragments: k-step t, token fragment q at aoff[t] + 32 q rows
+    int aoff[8];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) aoff[t] = xsw(r, F::chunk(g, t));
+    for (int t = 0; t < 8; ++t) aoff[t] = xsw(j, F::chunk(h, t));
 
-    f32x4 acc[2][NF];
+    f32x16 acc[RG][NF];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < RG; ++i)
 #pragma unroll
-        for (int f = 0; f < NF; ++f) acc[i][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int q = 0; q < NF; ++q)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][q][v] = 0.0f;
 
-    // one stage: MFMAs over the x tile in LDS buffer `buf` with the weights cw0 / cw1 (rows r,
-    // r + 16 of the wave); meanwhile stage s + 1 is loaded into nw0 / nw1 and the x registers
-    auto stage = [&](int64_t s, const Raw & cw0, const Raw & cw1, Raw & nw0, Raw & nw1) {
+    // one stage: MFMAs over the x tile in LDS with the weights cw (row groups of the wave);
+    // meanwhile stage s + 1 is loaded into nw and the x registers
+    auto stage = [&](int64_t s, const RawSet & cw, RawSet & nw) __attribute__((always_inline)) {
         const bool more = s + 1 < s1;
         if (more) {
-            nw0 = f0.load(s + 1);
-            nw1 = f1.load(s + 1);
-            xt.load((s + 1) * BK, K, (s + 1) * BK + BK <= K);
+#pragma unroll
+            for (int i = 0; i < RG; ++i) nw.r[i] = f[i].load(w, s + 1);
+            xt.load(xb, (s + 1) * BK, K, (s + 1) * BK + BK <= K);
         }
         const uint16_t * X = lds_mm + ((s - s0) & 1) * (BN * BK);
-        const typename F::Sc sc0 = f0.prep(cw0, s), sc1 = f1.prep(cw1, s);
+        typename F::Sc sc[RG];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const bf16x8 b0 = f0.bop(cw0, sc0, t), b1 = f1.bop(cw1, sc1, t);
+        for (int i = 0; i < RG; ++i) sc[i] = f[i].prep(cw.r[i], s);
+        // software pipeline over the 8 k-steps: the A reads and B dequantization of step t + 1
+        // are issued while the MFMAs of step t run
+        f16x8 a[2][NF], b[2][RG];
 #pragma unroll
-            for (int f = 0; f < NF; ++f) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8 *>(X + aoff[t] + f * 16 * BK);
-                acc[0][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b0, acc[0][f], 0, 0, 0);
-                acc[1][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b1, acc[1][f], 0, 0, 0);
+        for (int q = 0; q < NF; ++q) a[0][q] = *reinterpret_cast<const f16x8 *>(X + aoff[0] + q * 32 * BK);
+#pragma unroll
+        for (int i = 0; i < RG; ++i) b[0][i] = F::bop(cw.r[i], sc[i], 0);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int c = t & 1, n = c ^ 1;
+            if (t < 7) {
+#pragma unroll
+                for (int q = 0; q < NF; ++q) a[n][q] = *reinterpret_cast<const f16x8 *>(X + aoff[t + 1] + q * 32 * BK);
             }
+            __builtin_amdgcn_sched_barrier(0); // keep the reads ahead of this step's MFMAs
+#pragma unroll
+            for (int q = 0; q < NF; ++q)
+#pragma unroll
+                for (int i = 0; i < RG; ++i) acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c][q], b[c][i], acc[i][q], 0, 0, 0);
+            if (t < 7) {
+#pragma unroll
+                for (int i = 0; i < RG; ++i) b[n][i] = F::bop(cw.r[i], sc[i], t + 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (more) xt.store(lds_mm + ((s + 1 - s0) & 1) * (BN * BK));
         __syncthreads();
     };
-    Raw a0{}, a1{}, b0r{}, b1r{};
+    RawSet ra{}, rb{};
     if (s0 < s1) {
-        a0 = f0.load(s0);
-        a1 = f1.load(s0);
-        xt.load(s0 * BK, K, s0 * BK + BK <= K);
+#pragma unroll
+        for (int i = 0; i < RG; ++i) ra.r[i] = f[i].load(w, s0);
+        xt.load(xb, s0 * BK, K, s0 * BK + BK <= K);
         xt.store(lds_mm);
     }
     __syncthreads();
     for (int64_t s = s0; s < s1; s += 2) {
-        stage(s, a0, a1, b0r, b1r);
-        if (s + 1 < s1) stage(s + 1, b0r, b1r, a0, a1);
+        stage(s, ra, rb);
+        if (s + 1 < s1) stage(s + 1, rb, ra);
     }
-    // acc[i][f], lane l: token 16 f + 4 (l / 16) + v, weight row 32 wave + 16 i + l % 16
+    // acc[i][q][v], lane (j, h): token n0 + 32q + 8 (v / 4) + 4h + v % 4, weight row m0 + 32i + j
     const int64_t slices = L.a.ne12 * L.a.ne13;
     float * y;
     int64_t ys1;
@@ -440,16 +526,18 @@ __global__ __launch_bounds__(kThreads, BN == 64 ? 3 : 2) void k_matmul(MmArgs L)
         y = L.part + ((uint64_t) split * slices + (uint64_t) sl) * N * M;
         ys1 = M;
     }
+    const float * xs = L.xs + (uint64_t) sl * N;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int64_t m = m0 + 32 * wave + 16 * i + r;
-        if (m >= M) continue;
+    for (int q = 0; q < NF; ++q) {
 #pragma unroll
-        for (int f = 0; f < NF; ++f) {
+        for (int v = 0; v < 16; ++v) {
+            const int64_t n = n0 + 32 * q + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (n >= N) continue;
+            const float u = xs[n];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int64_t n = n0 + 16 * f + 4 * g + v;
-                if (n < N) y[n * ys1 + m] = acc[i][f][v];
+            for (int i = 0; i < RG; ++i) {
+                const int64_t m = m0 + 32 * i + j;
+                if (m < M) y[n * ys1 + m] = acc[i][q][v] * u;
             }
         }
     }
@@ -478,72 +566,136 @@ __global__ __launch_bounds__(256) void k_split_reduce(MmArgs L) {
         }
         *reinterpret_cast<float4 *>(y + m) = v;
     } else {
-        for (int64_t j = m; j < m + 4 && j < M; ++j) {
+        for (int64_t e = m; e < m + 4 && e < M; ++e) {
             float v = 0.0f;
-            for (int sp = 0; sp < L.split; ++sp) v += p[sp * plane + j];
-            y[j] = v;
+            for (int sp = 0; sp < L.split; ++sp) v += p[sp * plane + e];
+            y[e] = v;
         }
     }
 }
 
-// x (f32, strided rows) -> bf16 rows of K contiguous elements. blockIdx.x is the row (token n of
-// slice sl), blockIdx.y covers 2048 elements of it; VEC when every row starts 16-byte aligned.
+// x (f32, strided rows) -> f16 rows of K contiguous elements, one work-group per row (token n of
+// slice sl = blockIdx.x / N). The row is scaled by 2^e so that its largest magnitude lands in
+// [2^14, 2^15): no row overflows f16 and none loses precision to its subnormals beyond 2^-24 of
+// the row's maximum; xs[row] = 2^-e undoes it on the products. Inside each group of 4 elements the
+// order is 0 2 1 3, the order of the weight pairs the matmul builds. VEC: rows 16-byte aligned.
+// The first kCached groups of 8 elements per thread stay in registers between the two passes.
 template <bool VEC>
-__global__ __launch_bounds__(256) void k_x_to_bf16(MatArgs a, uint16_t * xb) {
+__global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, float * xs) {
+    constexpr int kCached = 6; // K <= 12288 is read once
     const int64_t row = blockIdx.x, sl = row / a.N, n = row - sl * a.N;
     const int64_t i2 = sl % a.ne12, i3 = sl / a.ne12;
     const float * xp = a.x + i2 * a.x_s2 + i3 * a.x_s3 + n * a.x_s1;
     uint16_t * op = xb + row * a.K;
-    const int64_t k = ((int64_t) blockIdx.y * 256 + threadIdx.x) * 8;
-    if (k >= a.K) return; // K is a multiple of 32: a group of 8 lies inside the row or past it
-    if (VEC) {
-        const float4 u = *reinterpret_cast<const float4 *>(xp + k);
-        const float4 v = *reinterpret_cast<const float4 *>(xp + k + 4);
-        *reinterpret_cast<uint4 *>(op + k) = make_uint4(pack2(u.x, u.y), pack2(u.z, u.w), pack2(v.x, v.y), pack2(v.z, v.w));
-    } else {
-        uint32_t o[4];
+    auto load8 = [&](int64_t k, float * v) {
+        if (VEC) {
+            const float4 u = *reinterpret_cast<const float4 *>(xp + k);
+            const float4 t = *reinterpret_cast<const float4 *>(xp + k + 4);
+            v[0] = u.x, v[1] = u.y, v[2] = u.z, v[3] = u.w, v[4] = t.x, v[5] = t.y, v[6] = t.z, v[7] = t.w;
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = pack2(xp[k + 2 * j], xp[k + 2 * j + 1]);
-        *reinterpret_cast<uint4 *>(op + k) = make_uint4(o[0], o[1], o[2], o[3]);
+            for (int e = 0; e < 8; ++e) v[e] = xp[k + e];
+        }
+    };
+    auto store8 = [&](int64_t k, const float * v, int e2) {
+        float s[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[e] = ldexpf(v[e], e2);
+        const f16x2 p0 = __builtin_convertvector((f32x2{s[0], s[2]}), f16x2), p1 = __builtin_convertvector((f32x2{s[1], s[3]}), f16x2);
+        const f16x2 p2 = __builtin_convertvector((f32x2{s[4], s[6]}), f16x2), p3 = __builtin_convertvector((f32x2{s[5], s[7]}), f16x2);
+        *reinterpret_cast<uint4 *>(op + k) = make_uint4(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                                                        __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3));
+    };
+    const int64_t k0 = (int64_t) threadIdx.x * 8; // K is a multiple of 32: a group of 8 is whole
+    float cache[kCached][8];
+    float mx = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kCached; ++c) {
+        const int64_t k = k0 + (int64_t) c * 2048;
+        if (k < a.K) {
+            load8(k, cache[c]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(cache[c][e]));
+        }
+    }
+    for (int64_t k = k0 + (int64_t) kCached * 2048; k < a.K; k += 2048) {
+        float v[8];
+        load8(k, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    __shared__ float wmax[4];
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int e2 = 0;
+    if (mx > 0.0f && mx <= 3.4e38f) {
+        int ex;
+        frexpf(mx, &ex); // mx = f 2^ex, f in [0.5, 1)
+        e2 = min(15 - ex, 120);
+    }
+    if (threadIdx.x == 0) xs[row] = ldexpf(1.0f, -e2);
+#pragma unroll
+    for (int c = 0; c < kCached; ++c) {
+        const int64_t k = k0 + (int64_t) c * 2048;
+        if (k < a.K) store8(k, cache[c], e2);
+    }
+    for (int64_t k = k0 + (int64_t) kCached * 2048; k < a.K; k += 2048) {
+        float v[8];
+        load8(k, v);
+        store8(k, v, e2);
     }
 }
 
-// Tile width and work-groups along K per tile. BN=64 runs three work-groups per CU, BN=128 two
-// (the same MFMA rate per CU, half the dequantization per flop at BN=128). A problem with enough
-// 64-wide tiles for three per CU takes BN=64 unsplit; otherwise BN=128 with enough splits for
-// two work-groups per CU, each split keeping >= 8 stages of K.
+// Tile shape and work-groups along K per tile. A work-group is 4 waves; each wave owns RG groups
+// of 32 weight rows (the tile is 128 RG rows) and BN tokens. Every A fragment read from LDS feeds
+// RG MFMAs. Splits along K are added while the tiles leave the CUs' work-group slots empty, each
+// split keeping >= 8 stages of K.
 struct MmConfig {
-    int bn;
+    int bn, rg;
     int split;
 };
 
+int env_int(const char * name, int dflt) {
+    const char * v = std::getenv(name);
+    return v != nullptr && *v ? std::atoi(v) : dflt;
+}
+
 MmConfig config_of(const MatArgs & a, int cu_count) {
-    static const int env_bn = [] {
-        const char * v = std::getenv("SCRAPGPU_HIP_MM_BN");
-        return v != nullptr && *v ? (std::atoi(v) == 128 ? 128 : 64) : 0;
-    }();
-    static const int env_fill = [] {
-        const char * v = std::getenv("SCRAPGPU_HIP_MM_FILL");
-        return v != nullptr && *v ? std::max(1, std::atoi(v)) : 0;
-    }();
+    static const int env_bn = env_int("SCRAPGPU_HIP_MM_BN", 0), env_rg = env_int("SCRAPGPU_HIP_MM_RG", 0);
+    static const int env_split = env_int("SCRAPGPU_HIP_MM_SPLIT", 0);
     const int64_t slices = a.ne12 * a.ne13;
-    const int64_t tm = (a.M + BM - 1) / BM;
     const int64_t stages = (a.K + BK - 1) / BK;
-    auto tiles = [&](int bn) { return tm * ((a.N + bn - 1) / bn) * slices; };
     MmConfig c;
-    c.bn = env_bn ? env_bn : (tiles(64) >= 3 * (int64_t) cu_count ? 64 : 128);
-    const int64_t want = (int64_t) cu_count * (env_fill ? env_fill : (c.bn == 64 ? 3 : 2));
-    static const int env_split = [] {
-        const char * v = std::getenv("SCRAPGPU_HIP_MM_SPLIT");
-        return v != nullptr && *v ? std::max(1, std::min(8, std::atoi(v))) : 0;
-    }();
+    c.rg = env_rg == 1 || env_rg == 2 ? env_rg : 1;
+    const int64_t tm = (a.M + 128 * c.rg - 1) / (128 * c.rg);
+    auto tiles = [&](int bn) { return tm * ((a.N + bn - 1) / bn) * slices; };
+    c.bn = env_bn == 64 || env_bn == 128 ? env_bn : (tiles(64) >= occupancy_of(a.dtype, 64, c.rg) * (int64_t) cu_count ? 64 : 128);
+    const int64_t want = (int64_t) cu_count * occupancy_of(a.dtype, c.bn, c.rg);
     c.split = 1;
-    if (env_split) {
-        c.split = (int) std::max<int64_t>(1, std::min<int64_t>(env_split, stages));
+    if (env_split > 0) {
+        c.split = (int) std::max<int64_t>(1, std::min<int64_t>(std::min(env_split, 8), stages));
         return c;
     }
     while (tiles(c.bn) * c.split < want && stages / (c.split + 1) >= 8 && c.split < 8) ++c.split;
     return c;
+}
+
+template <int DT>
+void * kernel_of(const MmConfig & c) {
+    if (c.rg == 1) return c.bn == 64 ? (void *) k_matmul<DT, 64, 1> : (void *) k_matmul<DT, 128, 1>;
+    return c.bn == 64 ? (void *) k_matmul<DT, 64, 2> : (void *) k_matmul<DT, 128, 2>;
+}
+
+// scratch: x as f16 [slices][N][K] | row factors [slices][N] | split-K partials
+size_t xs_offset(const MatArgs & a) {
+    return ((size_t) a.N * (size_t) a.K * (size_t) (a.ne12 * a.ne13) * sizeof(uint16_t) + 255) / 256 * 256;
+}
+
+size_t part_offset(const MatArgs & a) {
+    return xs_offset(a) + ((size_t) a.N * (size_t) (a.ne12 * a.ne13) * sizeof(float) + 255) / 256 * 256;
 }
 
 size_t part_bytes(const MatArgs & a, int split) {
@@ -553,31 +705,30 @@ size_t part_bytes(const MatArgs & a, int split) {
 } // namespace
 
 size_t matmul_scratch_bytes(const MatArgs & a, int cu_count) {
-    const size_t xb = (size_t) a.N * (size_t) a.K * (size_t) (a.ne12 * a.ne13) * sizeof(uint16_t);
     const int split = config_of(a, cu_count).split;
-    return split == 1 ? xb : (xb + 255) / 256 * 256 + part_bytes(a, split);
+    return part_offset(a) + (split == 1 ? 0 : part_bytes(a, split));
 }
 
 hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name) {
-    const int64_t total = a.N * a.K * a.ne12 * a.ne13;
     uint16_t * xb = reinterpret_cast<uint16_t *>(scratch);
     const int64_t rows = a.N * a.ne12 * a.ne13;
+    float * xs = reinterpret_cast<float *>(scratch + xs_offset(a));
     const bool vec = (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && a.x_s1 % 4 == 0 && a.x_s2 % 4 == 0 && a.x_s3 % 4 == 0;
     if (rows > 0x7fffffff) return hipErrorInvalidValue;
-    const dim3 cg((unsigned) rows, (unsigned) ((a.K + 2047) / 2048));
     if (vec)
-        hipLaunchKernelGGL(k_x_to_bf16<true>, cg, dim3(256), 0, stream, a, xb);
+        hipLaunchKernelGGL(k_x_to_f16<true>, dim3((unsigned) rows), dim3(256), 0, stream, a, xb, xs);
     else
-        hipLaunchKernelGGL(k_x_to_bf16<false>, cg, dim3(256), 0, stream, a, xb);
+        hipLaunchKernelGGL(k_x_to_f16<false>, dim3((unsigned) rows), dim3(256), 0, stream, a, xb, xs);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     MmArgs L;
     L.a = a;
     L.xb = xb;
-    L.part = reinterpret_cast<float *>(scratch + ((size_t) total * sizeof(uint16_t) + 255) / 256 * 256);
-    L.tiles_m = (a.M + BM - 1) / BM;
+    L.xs = xs;
+    L.part = reinterpret_cast<float *>(scratch + part_offset(a));
     const MmConfig cfg = config_of(a, cu_count);
     const int BN = cfg.bn;
+    L.tiles_m = (a.M + 128 * cfg.rg - 1) / (128 * cfg.rg);
     L.tiles_n = (a.N + BN - 1) / BN;
     L.stages = (a.K + BK - 1) / BK;
     L.split = cfg.split;
@@ -587,19 +738,21 @@ hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count
     void * args[] = {&L};
     void * fn = nullptr;
     switch (a.dtype) {
-        case Q4_0: fn = BN == 64 ? (void *) k_matmul<Q4_0, 64> : (void *) k_matmul<Q4_0, 128>; if (kernel_name) *kernel_name = "matmul_mfma_q4_0"; break;
-        case Q8_0: fn = BN == 64 ? (void *) k_matmul<Q8_0, 64> : (void *) k_matmul<Q8_0, 128>; if (kernel_name) *kernel_name = "matmul_mfma_q8_0"; break;
-        case Q4_K: fn = BN == 64 ? (void *) k_matmul<Q4_K, 64> : (void *) k_matmul<Q4_K, 128>; if (kernel_name) *kernel_name = "matmul_mfma_q4_k"; break;
-        case Q6_K: fn = BN == 64 ? (void *) k_matmul<Q6_K, 64> : (void *) k_matmul<Q6_K, 128>; if (kernel_name) *kernel_name = "matmul_mfma_q6_k"; break;
+        case Q4_0: fn = kernel_of<Q4_0>(cfg); if (kernel_name) *kernel_name = "matmul_mfma_q4_0"; break;
+        case Q8_0: fn = kernel_of<Q8_0>(cfg); if (kernel_name) *kernel_name = "matmul_mfma_q8_0"; break;
+        case Q4_K: fn = kernel_of<Q4_K>(cfg); if (kernel_name) *kernel_name = "matmul_mfma_q4_k"; break;
+        case Q6_K: fn = kernel_of<Q6_K>(cfg); if (kernel_name) *kernel_name = "matmul_mfma_q6_k"; break;
         default: return hipErrorInvalidValue;
     }
-    static bool attr_set = false; // LDS beyond the 64 KiB default (gfx950 has 160 KiB per CU)
-    if (!attr_set) {
-        for (void * f : {(void *) k_matmul<Q4_0, 128>, (void *) k_matmul<Q8_0, 128>, (void *) k_matmul<Q4_K, 128>, (void *) k_matmul<Q6_K, 128>}) {
-            e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int) (2 * 128 * BK * sizeof(uint16_t)));
+    if (lds > 65536) { // LDS beyond the 64 KiB default (gfx950 has 160 KiB per CU); set once per kernel
+        static std::mutex mu;
+        static std::vector<void *> done;
+        std::lock_guard<std::mutex> lock(mu);
+        if (std::find(done.begin(), done.end(), fn) == done.end()) {
+            e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
             if (e != hipSuccess) return e;
+            done.push_back(fn);
         }
-        attr_set = true;
     }
     e = hipLaunchKernel(fn, grid, dim3(kThreads), args, lds, stream);
     if (e != hipSuccess || L.split == 1) return e;
