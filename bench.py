@@ -318,7 +318,12 @@ def main():
     ktime = sum(r["ms"] for r in rows) / 3
     # the roofline kernel: the token's largest product (gate+up fused, 2 x 12288x4096 Q4_K)
     dom_group = "gate+up" if "gate+up" in model.by_group else "gate"
-    dom_name, dom_ms, dom_bytes = profile_group(model, dom_group, 10)
+    groups = {}
+    for g in model.by_group:
+        g_name, g_ms, g_bytes = profile_group(model, g, 10)
+        groups[g] = {"kernel": g_name, "mean_us": round(g_ms * 1e3, 3), "bytes": g_bytes, "GBps": round(g_bytes / (g_ms * 1e-3) / 1e9, 1)}
+    dom_name, dom_bytes = groups[dom_group]["kernel"], groups[dom_group]["bytes"]
+    dom_ms = groups[dom_group]["mean_us"] * 1e-3
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     kernels = {r["name"]: {"launches_per_token": r["launches"] // 3, "mean_us": round(r["ms"] / r["launches"] * 1e3, 2),
                            "GBps": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1)} for r in rows}
@@ -346,6 +351,7 @@ def main():
         "kernel_sum_ms_per_token": round(ktime, 4),
         "kernel_GBps": round(model.bytes_per_token / (ktime * 1e-3) / 1e9, 1),
         "kernels": kernels,
+        "products": groups,
         "roofline": {"bound": "hbm", "kernel": f"{dom_name} ({dom_group})", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_of(dom_group),
                      "bytes_per_launch": dom_bytes, "mean_launch_us": round(dom_ms * 1e3, 3)},

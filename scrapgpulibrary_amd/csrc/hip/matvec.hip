@@ -593,31 +593,33 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2
     constexpr int XP = (SPW * kSegs + 15) / 16;
     float xv[XP][8];
     const int nseg = ns * kSegs;
+    // every load below is unconditional (out-of-range ones read a valid address and are
+    // discarded by a select), so the wait before the x conversion counts only the x loads: the
+    // conversion overlaps the weight loads instead of waiting for the last of them
 #pragma unroll
     for (int p = 0; p < XP; ++p) {
         const int g = 16 * p + (lane >> 2);
         const int64_t e = s0 * kStep + 32 * (int64_t) g + 8 * (lane & 3);
-        if (g < nseg && e < A.K) {
-            const float4 u = *reinterpret_cast<const float4 *>(wh.x + e);
-            const float4 w = *reinterpret_cast<const float4 *>(wh.x + e + 4);
-            xv[p][0] = u.x; xv[p][1] = u.y; xv[p][2] = u.z; xv[p][3] = u.w;
-            xv[p][4] = w.x; xv[p][5] = w.y; xv[p][6] = w.z; xv[p][7] = w.w;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) xv[p][i] = 0.0f;
-        }
+        const bool ok = g < nseg && e < A.K;
+        const float * xp = wh.x + (ok ? e : 0);
+        const float4 u = *reinterpret_cast<const float4 *>(xp);
+        const float4 w = *reinterpret_cast<const float4 *>(xp + 4);
+        xv[p][0] = ok ? u.x : 0.0f; xv[p][1] = ok ? u.y : 0.0f; xv[p][2] = ok ? u.z : 0.0f; xv[p][3] = ok ? u.w : 0.0f;
+        xv[p][4] = ok ? w.x : 0.0f; xv[p][5] = ok ? w.y : 0.0f; xv[p][6] = ok ? w.z : 0.0f; xv[p][7] = ok ? w.w : 0.0f;
     }
 
+    // the x loads stay ahead of the weight loads
+    __builtin_amdgcn_sched_barrier(0);
     F f[RG];
     const Row row = row_of<DT, RG>(A, blockIdx.x, wh.w_off, lane & 15, lane >> 4, f);
     Raw buf[SPW][RG];
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
-        if (s < ns) {
+        const int64_t ss = s < ns ? s0 + s : s0; // steps past the wave's range: reloaded, unused
 #pragma unroll
-            for (int i = 0; i < RG; ++i) buf[s][i] = f[i].load(s0 + s);
-        }
+        for (int i = 0; i < RG; ++i) buf[s][i] = f[i].load(ss);
     }
+    __builtin_amdgcn_sched_barrier(0);
 
     XSeg * xs = reinterpret_cast<XSeg *>(lds) + (size_t) wave * SPW * kSegs;
     float4 * xf = reinterpret_cast<float4 *>(reinterpret_cast<XSeg *>(lds) + (size_t) W * SPW * kSegs) + (size_t) wave * SPW * kSegs;
