@@ -13,7 +13,7 @@ Reported on one JSON line:
                 stream (the 36 layers' gate+up launches as one HIP graph, replayed right after the
                 timed region), vs 8 TB/s;
                 `traffic` = HBM bytes per launch from the committed rocprofv3 PMC summary
-  prefill       Q4_K M=512 (N=512 tokens) MFMA TFLOP/s on the two MLP shapes, vs 2.5 PFLOP/s bf16
+  prefill       Q4_K M=512 (N=512 tokens) MFMA TFLOP/s on the two MLP shapes, vs 2.5 PFLOP/s dense f16/bf16
   cpu_baseline  the oracle's reference-faithful CPU MUL_MAT (1 thread) on one gate matrix, N=1
 """
 from __future__ import annotations
@@ -38,7 +38,7 @@ HBM_PEAK_GBS = 8000.0
 # runs of this script (scaled by the counters' reading for a copy of known size); written by the
 # profiling run, see DESIGN.md
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_matvec_decode_token.json")
-BF16_PEAK_TFLOPS = 2500.0
+F16_PEAK_TFLOPS = 2500.0
 
 HIDDEN, KV, FFN, LAYERS = 4096, 1024, 12288, 36
 LAYER_SHAPES = [  # (name, dtype, K, M)
@@ -356,7 +356,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_of(dom_group),
                      "bytes_per_launch": dom_bytes, "mean_launch_us": round(dom_ms * 1e3, 3)},
         "prefill_M512": prefill,
-        "prefill_peak_frac": None if prefill is None else round(max(v["tflops"] for v in prefill.values()) / BF16_PEAK_TFLOPS, 4),
+        "prefill_peak_frac": None if prefill is None else round(max(v["tflops"] for v in prefill.values()) / F16_PEAK_TFLOPS, 4),
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

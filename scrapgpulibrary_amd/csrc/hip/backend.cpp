@@ -5,7 +5,7 @@
 // dispatch :738-773, transfers :1234-1287, plans :1335-1443, vtable :1449-1473, registration
 // :1477-1498) -- redesigned around HIP: one hipStream_t per scrapgpu stream, hipMalloc'd buffers,
 // R32 packing done by a kernel in HBM instead of on the host, and kernel selection by shape
-// (N <= 8: decode matvec; N > 8: bf16 MFMA prefill).
+// (N <= 8: decode matvec; N > 8: f16 MFMA prefill).
 #include "scrapgpu/hip.h"
 
 #include "../core/tensor_math.h"
@@ -74,7 +74,7 @@ struct Stream {
     scrapgpu_object_header hdr;
     Device * dev;
     hipStream_t s;
-    uint8_t * scratch = nullptr; // prefill matmul: bf16 activations and split-K partials (grown on demand)
+    uint8_t * scratch = nullptr; // prefill matmul: f16 activations, row factors and split-K partials (grown on demand)
     size_t scratch_size = 0;
     uint64_t scratch_gen = 0;    // process-unique; renewed on every re-allocation (keys recorded graphs)
 };

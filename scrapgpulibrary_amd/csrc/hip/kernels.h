@@ -42,9 +42,10 @@ struct MatArgs {
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
                          uint64_t * grid_size);
 
-// prefill: bf16 MFMA with fp32 accumulate, weights dequantized in registers (any N >= 1).
+// prefill: f16 MFMA with fp32 accumulate, weights dequantized in registers (any N >= 1).
 // `scratch` (matmul_scratch_bytes(a, cu_count) bytes of device memory, owned by the stream)
-// receives x as bf16 and, when K is split over work-groups, their partial sums.
+// receives x as scaled f16 rows with their factors and, when K is split over work-groups, the
+// partial sums.
 size_t matmul_scratch_bytes(const MatArgs & a, int cu_count);
 hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name);
 
