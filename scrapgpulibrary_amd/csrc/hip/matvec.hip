@@ -132,8 +132,10 @@ struct XView {
 };
 
 // ---- per format ----------------------------------------------------------------------------------
-// init() resolves the lane's row in every R32 area once; load(step) fetches what the lane needs of
-// one step; bop(raw, t) is the lane's B operand (16 int8 codes) for MFMA t = 0..3 of the step;
+// init() resolves the lane's row in every R32 area once (Q4_K, Q8_0, Q4_0: as 32-bit byte offsets
+// from the matrix slice's base w, which is uniform across the work-group and so stays in scalar
+// registers; a slice is < 4 GiB, checked on the host); load(step) fetches what the lane needs of
+// one step, branch-free; bop(raw, t) is the lane's B operand (16 int8 codes) for MFMA t = 0..3 of the step;
 // aoff(t, c, k, g) is the byte offset, inside the step's XSeg run, of the 16 x bytes that lane
 // (row 4c + k of A, k-group g) supplies to MFMA t, or -1 for zeros; flush() scales the integer
 // sums of lane part p into the row sum.
@@ -150,24 +152,22 @@ struct Fmt<Q4_K> {
     struct Raw {
         uint4 q0, q1, hd;
     };
-    const uint8_t * qb;
-    const uint8_t * hb;
-    uint32_t qblk, qunit, hblk;
+    const uint8_t * w;
+    uint32_t qo, ho, u; // unit stride u = 16 * rows in the group; a block is 8 units
     int p;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb, int64_t g0, int rs, int lr, int part) {
+    __device__ void init(const uint8_t * w_, int64_t M, int64_t nb, int64_t g0, int rs, int lr, int part) {
+        w = w_;
         p = part;
-        qb = w + (uint64_t) g0 * nb * 128 + (uint64_t) lr * 16;
-        hb = w + (uint64_t) M * nb * 128 + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
-        qblk = (uint32_t) rs * 128;
-        qunit = (uint32_t) rs * 16;
-        hblk = (uint32_t) rs * 16;
+        u = (uint32_t) rs * 16;
+        qo = (uint32_t) (g0 * nb * 128 + lr * 16) + (uint32_t) (2 * p) * u;
+        ho = (uint32_t) (M * nb * 128 + g0 * nb * 16 + lr * 16);
     }
     __device__ Raw load(int64_t step) const {
         Raw r;
-        const uint8_t * b = qb + (uint32_t) step * qblk + (uint32_t) (2 * p) * qunit;
-        r.q0 = load16(b);
-        r.q1 = load16(b + qunit);
-        r.hd = load16(hb + (uint32_t) step * hblk);
+        const uint32_t q = __umul24((uint32_t) step * 8, u) + qo;
+        r.q0 = load16(w + q);
+        r.q1 = load16(w + q + u);
+        r.hd = load16(w + (__umul24((uint32_t) step, u) + ho));
         return r;
     }
     __device__ static v4i bop(const Raw & r, int t) {
@@ -286,31 +286,30 @@ struct Fmt<Q8_0> {
         uint4 u[4];
         uint32_t d0, d1;
     };
-    const uint8_t * qb;
-    const uint8_t * db;
-    uint32_t qblk, qunit, dblk;
-    int64_t nb;
+    const uint8_t * w;
+    uint32_t qo, dof, u, nb; // block b: units 2b, 2b + 1 (2b u), d at b u / 8 in the d area
     int p;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int part) {
+    __device__ void init(const uint8_t * w_, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int part) {
+        w = w_;
         p = part;
-        nb = nb_;
-        qb = w + (uint64_t) g0 * nb * 32 + (uint64_t) lr * 16;
-        db = w + (uint64_t) M * nb * 32 + (uint64_t) g0 * nb * 2 + (uint64_t) lr * 2;
-        qblk = (uint32_t) rs * 32;
-        qunit = (uint32_t) rs * 16;
-        dblk = (uint32_t) rs * 2;
+        nb = (uint32_t) nb_;
+        u = (uint32_t) rs * 16;
+        qo = (uint32_t) (g0 * nb_ * 32 + lr * 16) + (uint32_t) (p & 1) * u;
+        dof = (uint32_t) (M * nb_ * 32 + g0 * nb_ * 2 + lr * 2);
     }
     __device__ Raw load(int64_t step) const {
         Raw r;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            int64_t b = step * 8 + 2 * t + (p >> 1);
+            uint32_t b = (uint32_t) step * 8 + 2 * t + (p >> 1);
             b = b < nb ? b : 0;
-            r.u[t] = load16(qb + (uint32_t) b * qblk + (uint32_t) (p & 1) * qunit);
+            r.u[t] = load16(w + (__umul24(2 * b, u) + qo));
         }
-        const int64_t b0 = step * 8 + 2 * p, b1 = b0 + 1;
-        r.d0 = b0 < nb ? load_half(db + (uint32_t) b0 * dblk) : 0u;
-        r.d1 = b1 < nb ? load_half(db + (uint32_t) b1 * dblk) : 0u;
+        const uint32_t b0 = (uint32_t) step * 8 + 2 * p, b1 = b0 + 1;
+        const uint32_t d0 = load_half(w + (__umul24(b0 < nb ? b0 : 0, u >> 3) + dof));
+        const uint32_t d1 = load_half(w + (__umul24(b1 < nb ? b1 : 0, u >> 3) + dof));
+        r.d0 = b0 < nb ? d0 : 0u;
+        r.d1 = b1 < nb ? d1 : 0u;
         return r;
     }
     __device__ static v4i bop(const Raw & r, int t) {
@@ -337,29 +336,29 @@ struct Fmt<Q4_0> {
         uint4 qa, qb;
         uint32_t da, db;
     };
-    const uint8_t * qp;
-    const uint8_t * dp;
-    uint32_t qblk, dblk;
-    int64_t nb;
+    const uint8_t * w;
+    uint32_t qo, dof, u, nb; // block b: unit at b u, d at b u / 8 in the d area
     int p;
-    __device__ void init(const uint8_t * w, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int part) {
+    __device__ void init(const uint8_t * w_, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int part) {
+        w = w_;
         p = part;
-        nb = nb_;
-        qp = w + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
-        dp = w + (uint64_t) M * nb * 16 + (uint64_t) g0 * nb * 2 + (uint64_t) lr * 2;
-        qblk = (uint32_t) rs * 16;
-        dblk = (uint32_t) rs * 2;
+        nb = (uint32_t) nb_;
+        u = (uint32_t) rs * 16;
+        qo = (uint32_t) (g0 * nb_ * 16 + lr * 16);
+        dof = (uint32_t) (M * nb_ * 16 + g0 * nb_ * 2 + lr * 2);
     }
     __device__ Raw load(int64_t step) const {
         Raw r;
-        int64_t ba = step * 8 + p, bb = ba + 4;
+        uint32_t ba = (uint32_t) step * 8 + p, bb = ba + 4;
         const bool oka = ba < nb, okb = bb < nb;
         ba = oka ? ba : 0;
         bb = okb ? bb : 0;
-        r.qa = load16(qp + (uint32_t) ba * qblk);
-        r.qb = load16(qp + (uint32_t) bb * qblk);
-        r.da = oka ? load_half(dp + (uint32_t) ba * dblk) : 0u;
-        r.db = okb ? load_half(dp + (uint32_t) bb * dblk) : 0u;
+        r.qa = load16(w + (__umul24(ba, u) + qo));
+        r.qb = load16(w + (__umul24(bb, u) + qo));
+        const uint32_t da = load_half(w + (__umul24(ba, u >> 3) + dof));
+        const uint32_t db = load_half(w + (__umul24(bb, u >> 3) + dof));
+        r.da = oka ? da : 0u;
+        r.db = okb ? db : 0u;
         return r;
     }
     __device__ static v4i bop(const Raw & r, int t) {
