@@ -19,7 +19,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libscrapgpu_ref.so")
 
-F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 16, 17, 32, 33
+F32, I32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 16, 17, 32, 33
 QTYPES = (Q4_0, Q8_0, Q4_K, Q6_K)
 NAMES = {F32: "f32", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
 BLOCK = {F32: 1, Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
@@ -56,6 +56,8 @@ def lib():
         L.sgo_quantize.argtypes = [C.c_int32, C.c_void_p, C.c_void_p, C.c_int64]
         L.sgo_mul_mat.argtypes = [C.POINTER(SgoTensor)] * 3 + [C.c_int]
         L.sgo_mul_mat_mt.argtypes = [C.POINTER(SgoTensor)] * 3 + [C.c_int, C.c_int]
+        L.sgo_mul_mat_id.argtypes = [C.POINTER(SgoTensor)] * 4
+        L.sgo_get_rows.argtypes = [C.POINTER(SgoTensor)] * 3
         for f in (L.sgo_r32_pack, L.sgo_r32_unpack):
             f.argtypes = [C.c_int32, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p]
         _lib = L
@@ -128,6 +130,44 @@ def mul_mat(dtype: int, w: np.ndarray, K: int, M: int, x: np.ndarray, threads: i
     st = lib().sgo_mul_mat_mt(C.byref(tw), C.byref(tx), C.byref(ty), 0, threads)
     if st != 0:
         raise ValueError(f"sgo_mul_mat status {st}")
+    return y
+
+
+def mul_mat_id(dtype: int, w: np.ndarray, K: int, M: int, E: int, x: np.ndarray, ids: np.ndarray) -> np.ndarray:
+    """MUL_MAT_ID on contiguous tensors: w holds E experts of M rows of natural blocks, x is float32
+    [T, n1, K] (n1 = 1 or n_used), ids int32 [T, n_used]. Returns float32 [T, n_used, M]; raises
+    ValueError on a status other than OK (an expert index out of range)."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    T, nu = ids.shape
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(T, -1, K)
+    n1 = x.shape[1]
+    rb = row_bytes(dtype, K) if dtype != F32 else 4 * K
+    w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
+    assert w.size == rb * M * E
+    y = np.zeros((T, nu, M), np.float32)
+    tw = _tensor(dtype, w, (K, M, E, 1), (TYPE_SIZE[dtype], rb, rb * M, rb * M * E))
+    tx = _tensor(F32, x, (K, n1, T, 1), (4, 4 * K, 4 * K * n1, 4 * K * n1 * T))
+    ti = _tensor(I32, ids, (nu, T, 1, 1), (4, 4 * nu, 4 * nu * T, 4 * nu * T))
+    ty = _tensor(F32, y, (M, nu, T, 1), (4, 4 * M, 4 * M * nu, 4 * M * nu * T))
+    st = lib().sgo_mul_mat_id(C.byref(tw), C.byref(tx), C.byref(ti), C.byref(ty))
+    if st != 0:
+        raise ValueError(f"sgo_mul_mat_id status {st}")
+    return y
+
+
+def get_rows(dtype: int, w: np.ndarray, K: int, R: int, ids: np.ndarray) -> np.ndarray:
+    """GET_ROWS of one slice: w holds R rows of natural blocks, ids int32 [n]. Returns float32 [n, K]."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
+    n = ids.size
+    rb = row_bytes(dtype, K) if dtype != F32 else 4 * K
+    w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
+    y = np.zeros((n, K), np.float32)
+    tw = _tensor(dtype, w, (K, R, 1, 1), (TYPE_SIZE[dtype], rb, rb * R, rb * R))
+    ti = _tensor(I32, ids, (n, 1, 1, 1), (4, 4 * n, 4 * n, 4 * n))
+    ty = _tensor(F32, y, (K, n, 1, 1), (4, 4 * K, 4 * K * n, 4 * K * n))
+    st = lib().sgo_get_rows(C.byref(tw), C.byref(ti), C.byref(ty))
+    if st != 0:
+        raise ValueError(f"sgo_get_rows status {st}")
     return y
 
 
@@ -261,3 +301,65 @@ def ref_mul_mat(dtype: int, w: np.ndarray, K: int, M: int, x: np.ndarray) -> np.
     st = ref().scrapgpu_ref_execute(C.byref(op), in_ptrs, out_ptrs)
     assert st == 0, st
     return y
+
+
+class _RefMulMatIdParams(C.Structure):
+    _fields_ = [("struct_size", C.c_size_t), ("n_used", C.c_uint32), ("max_prompt_tokens", C.c_uint32)]
+
+
+class _RefGetRowsParams(C.Structure):
+    _fields_ = [("struct_size", C.c_size_t), ("indices_are_i64", C.c_int)]
+
+
+def _ref_fill(t, dt, ne, nb):
+    t.struct_size = C.sizeof(_RefTensorDesc)
+    t.dtype = dt
+    for i in range(4):
+        t.ne[i] = ne[i]
+        t.nb[i] = nb[i]
+    t.offset = 0
+    t.layout = 0
+
+
+def ref_mul_mat_id(dtype: int, w: np.ndarray, K: int, M: int, E: int, x: np.ndarray, ids: np.ndarray):
+    """scrapgpu_ref_execute(MUL_MAT_ID) of the reference on contiguous tensors (shapes as
+    mul_mat_id). Returns (status, y)."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    T, nu = ids.shape
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(T, -1, K)
+    n1 = x.shape[1]
+    rb = row_bytes(dtype, K) if dtype != F32 else 4 * K
+    w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
+    y = np.zeros((T, nu, M), np.float32)
+    ins = (_RefTensorDesc * 3)()
+    outs = (_RefTensorDesc * 1)()
+    _ref_fill(ins[0], dtype, (K, M, E, 1), (TYPE_SIZE[dtype], rb, rb * M, rb * M * E))
+    _ref_fill(ins[1], F32, (K, n1, T, 1), (4, 4 * K, 4 * K * n1, 4 * K * n1 * T))
+    _ref_fill(ins[2], I32, (nu, T, 1, 1), (4, 4 * nu, 4 * nu * T, 4 * nu * T))
+    _ref_fill(outs[0], F32, (M, nu, T, 1), (4, 4 * M, 4 * M * nu, 4 * M * nu * T))
+    p = _RefMulMatIdParams(C.sizeof(_RefMulMatIdParams), nu, 0)
+    op = _RefOpDesc(C.sizeof(_RefOpDesc), 29, C.addressof(ins), 3, C.addressof(outs), 1, C.addressof(p), C.sizeof(p))
+    in_ptrs = (C.c_void_p * 3)(_p(w), _p(x), _p(ids))
+    out_ptrs = (C.c_void_p * 1)(_p(y))
+    st = ref().scrapgpu_ref_execute(C.byref(op), in_ptrs, out_ptrs)
+    return st, y
+
+
+def ref_get_rows(dtype: int, w: np.ndarray, K: int, R: int, ids: np.ndarray):
+    """scrapgpu_ref_execute(GET_ROWS) of the reference on one slice. Returns (status, y [n, K])."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
+    n = ids.size
+    rb = row_bytes(dtype, K) if dtype != F32 else 4 * K
+    w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
+    y = np.zeros((n, K), np.float32)
+    ins = (_RefTensorDesc * 2)()
+    outs = (_RefTensorDesc * 1)()
+    _ref_fill(ins[0], dtype, (K, R, 1, 1), (TYPE_SIZE[dtype], rb, rb * R, rb * R))
+    _ref_fill(ins[1], I32, (n, 1, 1, 1), (4, 4 * n, 4 * n, 4 * n))
+    _ref_fill(outs[0], F32, (K, n, 1, 1), (4, 4 * K, 4 * K * n, 4 * K * n))
+    p = _RefGetRowsParams(C.sizeof(_RefGetRowsParams), 0)
+    op = _RefOpDesc(C.sizeof(_RefOpDesc), 23, C.addressof(ins), 2, C.addressof(outs), 1, C.addressof(p), C.sizeof(p))
+    in_ptrs = (C.c_void_p * 2)(_p(w), _p(ids))
+    out_ptrs = (C.c_void_p * 1)(_p(y))
+    st = ref().scrapgpu_ref_execute(C.byref(op), in_ptrs, out_ptrs)
+    return st, y

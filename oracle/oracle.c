@@ -673,6 +673,92 @@ int sgo_mul_mat_mt(const sgo_tensor * w, const sgo_tensor * x, sgo_tensor * y, i
 }
 
 /* ---------------------------------------------------------------------------------------------
+ * MUL_MAT_ID (reference src/core/ref/ops.cpp:986-1024): expert matrices w [K, M, E], activations
+ * x [K, n1, T] (n1 = 1: shared by the slots, or n1 = n_used), ids I32 [n_used, T], dst
+ * [M, n_used, T]: dst[:, i, t] = w[:, :, ids[i, t]] x[:, i or 0, t]. Every output is the scalar
+ * increasing-K loop of MUL_MAT at one column; an expert index outside [0, E) is an error, found
+ * in (t, i) order (outputs of earlier pairs stay written, as in the reference).
+ * ------------------------------------------------------------------------------------------- */
+
+static int ids_i32(const sgo_tensor * ids, int64_t i, int64_t t, int32_t * e) {
+    memcpy(e, (const uint8_t *) ids->data + (uint64_t) i * ids->nb[0] + (uint64_t) t * ids->nb[1], 4);
+    return SGO_OK;
+}
+
+int sgo_mul_mat_id(const sgo_tensor * w, const sgo_tensor * x, const sgo_tensor * ids, sgo_tensor * y) {
+    if (w == NULL || x == NULL || ids == NULL || y == NULL || w->data == NULL || x->data == NULL || ids->data == NULL || y->data == NULL) return SGO_INVALID;
+    if (x->dtype != SGO_F32 || y->dtype != SGO_F32 || ids->dtype != SGO_I32) return SGO_UNSUPPORTED;
+    if (w->dtype != SGO_F32 && !is_quant(w->dtype)) return SGO_UNSUPPORTED;
+    if (w->nb[0] != sgo_type_size(w->dtype)) return SGO_UNSUPPORTED;
+    if (dim(w, 3) != 1 || dim(x, 3) != 1 || dim(ids, 2) != 1 || dim(ids, 3) != 1) return SGO_INVALID;
+    if (dim(w, 0) != dim(x, 0) || (dim(x, 1) != 1 && dim(x, 1) != dim(ids, 0)) || dim(x, 2) != dim(ids, 1) ||
+        dim(y, 0) != dim(w, 1) || dim(y, 1) != dim(ids, 0) || dim(y, 2) != dim(ids, 1) || dim(y, 3) != 1) {
+        return SGO_INVALID;
+    }
+    const int64_t K = dim(w, 0), M = dim(w, 1), E = dim(w, 2);
+    if (is_quant(w->dtype) && K % (int64_t) sgo_block_size(w->dtype) != 0) return SGO_UNSUPPORTED;
+    float * row = (float *) malloc((size_t) K * 4);
+    for (int64_t t = 0; t < dim(ids, 1); ++t) {
+        for (int64_t i = 0; i < dim(ids, 0); ++i) {
+            int32_t e;
+            ids_i32(ids, i, t, &e);
+            if (e < 0 || (int64_t) e >= E) {
+                free(row);
+                return SGO_INVALID;
+            }
+            const int64_t i11 = dim(x, 1) == 1 ? 0 : i;
+            const float * xv = (const float *) tptr(x, i11, t, 0);
+            for (int64_t m = 0; m < M; ++m) {
+                load_row(w, tptr(w, m, e, 0), K, row);
+                float acc = 0.0f;
+                for (int64_t k = 0; k < K; ++k) acc = acc + row[k] * xv[k];
+                memcpy((uint8_t *) tptr(y, i, t, 0) + m * 4, &acc, 4);
+            }
+        }
+    }
+    free(row);
+    return SGO_OK;
+}
+
+/* ---------------------------------------------------------------------------------------------
+ * GET_ROWS (reference src/core/ref/ops.cpp:690-721): src0 [K, R, S2, S3] (rows of K elements),
+ * ids I32 [n, i11 < S2, i12 < S3], dst F32 [K, n, ids ne1, ids ne2]: dst[:, a, b, c] = row
+ * ids[a, b, c] of slice (b, c) of src0, dequantized. A row index outside [0, R) is an error,
+ * found in (c, b, a) order.
+ * ------------------------------------------------------------------------------------------- */
+
+int sgo_get_rows(const sgo_tensor * w, const sgo_tensor * ids, sgo_tensor * y) {
+    if (w == NULL || ids == NULL || y == NULL || w->data == NULL || ids->data == NULL || y->data == NULL) return SGO_INVALID;
+    if (ids->dtype != SGO_I32 || y->dtype != SGO_F32) return SGO_UNSUPPORTED;
+    if (w->dtype != SGO_F32 && !is_quant(w->dtype)) return SGO_UNSUPPORTED;
+    if (w->nb[0] != sgo_type_size(w->dtype)) return SGO_UNSUPPORTED;
+    if (dim(ids, 3) != 1 || dim(ids, 1) > dim(w, 2) || dim(ids, 2) > dim(w, 3) || dim(y, 0) != dim(w, 0) || dim(y, 1) != dim(ids, 0) ||
+        dim(y, 2) != dim(ids, 1) || dim(y, 3) != dim(ids, 2)) {
+        return SGO_INVALID;
+    }
+    const int64_t K = dim(w, 0);
+    if (is_quant(w->dtype) && K % (int64_t) sgo_block_size(w->dtype) != 0) return SGO_UNSUPPORTED;
+    float * row = (float *) malloc((size_t) K * 4);
+    for (int64_t c = 0; c < dim(ids, 2); ++c) {
+        for (int64_t b = 0; b < dim(ids, 1); ++b) {
+            for (int64_t a = 0; a < dim(ids, 0); ++a) {
+                int32_t r;
+                memcpy(&r, (const uint8_t *) ids->data + (uint64_t) a * ids->nb[0] + (uint64_t) b * ids->nb[1] + (uint64_t) c * ids->nb[2], 4);
+                if (r < 0 || (int64_t) r >= dim(w, 1)) {
+                    free(row);
+                    return SGO_INVALID;
+                }
+                load_row(w, tptr(w, r, b, c), K, row);
+                uint8_t * out = (uint8_t *) y->data + (uint64_t) a * y->nb[1] + (uint64_t) b * y->nb[2] + (uint64_t) c * y->nb[3];
+                for (int64_t k = 0; k < K; ++k) memcpy(out + (uint64_t) k * y->nb[0], &row[k], 4);
+            }
+        }
+    }
+    free(row);
+    return SGO_OK;
+}
+
+/* ---------------------------------------------------------------------------------------------
  * R32 (reference src/tensor/tensor.cpp:5-19, src/backends/opencl11/r32.h:35-90)
  *
  * Per slice of M rows and nb blocks per row, the bytes of a block are split into areas stored one

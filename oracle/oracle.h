@@ -1,7 +1,7 @@
 /* CPU oracle for the quantized MUL_MAT path -- TEST INFRASTRUCTURE ONLY.
  *
  * A plain-C restatement of the reference's CPU implementation (src/core/ref/f16.cpp,
- * src/core/ref/quant.cpp, src/core/ref/ops.cpp:258-269,802-984) and of the R32 host pack/unpack
+ * src/core/ref/quant.cpp, src/core/ref/ops.cpp:258-269,690-721,802-1024) and of the R32 host pack/unpack
  * (src/backends/opencl11/r32.h:35-90, src/tensor/tensor.cpp:5-19). It is the checker of the GPU
  * path and the CPU baseline that bench.py times; only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py load it. The product library never links or calls it.
@@ -21,6 +21,10 @@
  *                        checksums (tools/cpu_bench.cpp)
  *   r32 pack/unpack      hand-checked layouts (r32_tests.cpp:104-181), pack/unpack identity,
  *                        golden vectors from the reference pack
+ *   mul_mat_id           golden vectors from the compiled reference (scrapgpu_ref_execute), and
+ *                        equality with per-pair mul_mat on the selected expert; out-of-range ids
+ *   get_rows             golden vectors from the compiled reference, and equality with the
+ *                        dequantized rows; out-of-range row indices
  */
 #ifndef SGO_ORACLE_H
 #define SGO_ORACLE_H
@@ -34,6 +38,7 @@ extern "C" {
 
 enum {
     SGO_F32 = 0,
+    SGO_I32 = 2,
     SGO_Q4_0 = 16,
     SGO_Q8_0 = 17,
     SGO_Q4_K = 32,
@@ -66,6 +71,13 @@ int sgo_mul_mat(const sgo_tensor * w, const sgo_tensor * x, sgo_tensor * y, int 
 /* Same, but the M rows of every slice are split over `threads` POSIX threads (an all-core variant
  * of the baseline; identical results). */
 int sgo_mul_mat_mt(const sgo_tensor * w, const sgo_tensor * x, sgo_tensor * y, int allow_broadcast, int threads);
+
+/* MUL_MAT_ID of ops.cpp:986-1024: dst[:, i, t] = w[:, :, ids[i, t]] x[:, i or 0, t] (scalar loop);
+ * SGO_INVALID for an expert index outside [0, E). */
+int sgo_mul_mat_id(const sgo_tensor * w, const sgo_tensor * x, const sgo_tensor * ids, sgo_tensor * y);
+
+/* GET_ROWS of ops.cpp:690-721: dst[:, a, b, c] = dequantized row ids[a, b, c] of slice (b, c). */
+int sgo_get_rows(const sgo_tensor * w, const sgo_tensor * ids, sgo_tensor * y);
 
 /* R32 pack / unpack of `slices` contiguous slices of M rows of K elements (natural <-> repacked). */
 int sgo_r32_pack(int32_t dtype, int64_t K, int64_t M, int64_t slices, const uint8_t * nat, uint8_t * rep);

@@ -1,4 +1,5 @@
-"""Writes the golden vectors of tests/golden/*.npz from the reference's own CPU implementation.
+"""Writes the golden vectors of tests/golden/*.npz from the reference's own CPU implementation
+(quantize, dequantize, MUL_MAT, R32 pack, MUL_MAT_ID, GET_ROWS).
 
 The reference (src/core/ref/{quant,ops,f16}.cpp, src/core/{op,tensor,status}.cpp,
 src/tensor/tensor.cpp and the inline R32 pack of src/backends/opencl11/r32.h) is compiled from its
@@ -72,6 +73,39 @@ def main():
         out[f"{name}_r32_K{Kr}_M{Mr}_S{S}_nat"] = nat
         out[f"{name}_r32_K{Kr}_M{Mr}_S{S}_rep"] = O.ref_r32(dt, Kr, Mr, S, nat, True)
     np.savez_compressed(os.path.join(OUT, "quant_mulmat_r32.npz"), **out)
+    print("wrote", len(out), "arrays")
+    moe_getrows()
+
+
+def moe_getrows():
+    """MUL_MAT_ID (E experts, n_used slots, T tokens; x shared by the slots or one column per slot)
+    and GET_ROWS (repeated, first and last rows) through scrapgpu_ref_execute."""
+    rng = np.random.default_rng(20261202)
+    out = {}
+    for dt in O.QTYPES:
+        name = O.NAMES[dt]
+        K = 256 if O.BLOCK[dt] == 256 else 96
+        M, E, T, nu = 40, 5, 3, 2
+        w = O.ref_quantize(dt, (rng.standard_normal(K * M * E) * 0.02).astype(np.float32))
+        ids = rng.integers(0, E, (T, nu)).astype(np.int32)
+        ids[0, 0] = E - 1
+        out[f"{name}_mid_w"] = w
+        out[f"{name}_mid_ids"] = ids
+        for n1 in (1, nu):
+            x = rng.standard_normal((T, n1, K)).astype(np.float32)
+            st, y = O.ref_mul_mat_id(dt, w, K, M, E, x, ids)
+            assert st == 0, st
+            out[f"{name}_mid_x{n1}"] = x
+            out[f"{name}_mid_y{n1}"] = y
+        R = 37
+        wr = O.ref_quantize(dt, rng.standard_normal(K * R).astype(np.float32))
+        rid = np.array([0, R - 1, 5, 5, 12, 30], np.int32)
+        st, g = O.ref_get_rows(dt, wr, K, R, rid)
+        assert st == 0, st
+        out[f"{name}_gr_w"] = wr
+        out[f"{name}_gr_ids"] = rid
+        out[f"{name}_gr_y"] = g
+    np.savez_compressed(os.path.join(OUT, "mul_mat_id_get_rows.npz"), **out)
     print("wrote", len(out), "arrays")
 
 

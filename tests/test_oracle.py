@@ -60,6 +60,57 @@ def test_golden_r32(gold, dt):
     assert np.array_equal(O.r32_unpack(dt, Kr, Mr, S, rep), nat)
 
 
+# golden MUL_MAT_ID / GET_ROWS of the reference, and the independent checks: a MUL_MAT_ID output
+# is the N = 1 MUL_MAT of the selected expert (pinned above); a GET_ROWS row is the dequantized row
+
+GOLD_ID = os.path.join(os.path.dirname(__file__), "golden", "mul_mat_id_get_rows.npz")
+
+
+@pytest.fixture(scope="module")
+def gold_id():
+    return np.load(GOLD_ID)
+
+
+@pytest.mark.parametrize("dt", O.QTYPES, ids=lambda d: O.NAMES[d])
+def test_golden_mul_mat_id(gold_id, dt):
+    n = O.NAMES[dt]
+    K = 256 if O.BLOCK[dt] == 256 else 96
+    M, E = 40, 5
+    w, ids = gold_id[f"{n}_mid_w"], gold_id[f"{n}_mid_ids"]
+    rb = O.row_bytes(dt, K) * M
+    for n1 in (1, ids.shape[1]):
+        x, y = gold_id[f"{n}_mid_x{n1}"], gold_id[f"{n}_mid_y{n1}"]
+        got = O.mul_mat_id(dt, w, K, M, E, x, ids)
+        assert np.array_equal(got.view(np.uint32), y.view(np.uint32))
+        for t in range(ids.shape[0]):
+            for i in range(ids.shape[1]):
+                e = ids[t, i]
+                one = O.mul_mat(dt, w[e * rb:(e + 1) * rb], K, M, x[t, i if n1 > 1 else 0])
+                assert np.array_equal(one[0].view(np.uint32), got[t, i].view(np.uint32))
+
+
+def test_mul_mat_id_expert_out_of_range():
+    w = O.quantize(O.Q4_0, O.normal(96 * 8 * 3, 3, 0.0, 0.02))
+    x = O.normal(2 * 96, 4).reshape(2, 1, 96)
+    for bad in (3, -1):
+        with pytest.raises(ValueError):
+            O.mul_mat_id(O.Q4_0, w, 96, 8, 3, x, np.array([[0], [bad]], np.int32))
+
+
+@pytest.mark.parametrize("dt", O.QTYPES, ids=lambda d: O.NAMES[d])
+def test_golden_get_rows(gold_id, dt):
+    n = O.NAMES[dt]
+    K = 256 if O.BLOCK[dt] == 256 else 96
+    R = 37
+    w, ids, y = gold_id[f"{n}_gr_w"], gold_id[f"{n}_gr_ids"], gold_id[f"{n}_gr_y"]
+    got = O.get_rows(dt, w, K, R, ids)
+    assert np.array_equal(got.view(np.uint32), y.view(np.uint32))
+    deq = O.dequantize(dt, w, K * R).reshape(R, K)
+    assert np.array_equal(got.view(np.uint32), deq[ids].view(np.uint32))
+    with pytest.raises(ValueError):
+        O.get_rows(dt, w, K, R, np.array([R], np.int32))
+
+
 # ---------------------------------------------------------------------------------------------
 # the reference's known-answer tests
 # ---------------------------------------------------------------------------------------------
@@ -310,3 +361,14 @@ def test_live_reference(dt):
         assert np.array_equal(O.mul_mat(dt, q, K, M, x).view(np.uint32), O.ref_mul_mat(dt, q, K, M, x).view(np.uint32))
     nat = rng.integers(0, 256, O.row_bytes(dt, K) * 72 * 2, dtype=np.uint8)  # 72 rows: 16-byte slice stride
     assert np.array_equal(O.r32_pack(dt, K, 72, 2, nat), O.ref_r32(dt, K, 72, 2, nat, True))
+    E, T, nu = 6, 4, 3
+    w = O.quantize(dt, O.normal(K * M * E, 13, 0.0, 0.02))
+    ids = rng.integers(0, E, (T, nu)).astype(np.int32)
+    for n1 in (1, nu):
+        x = O.normal(T * n1 * K, 14 + n1).reshape(T, n1, K)
+        st, yr = O.ref_mul_mat_id(dt, w, K, M, E, x, ids)
+        assert st == 0 and np.array_equal(O.mul_mat_id(dt, w, K, M, E, x, ids).view(np.uint32), yr.view(np.uint32))
+    assert O.ref_mul_mat_id(dt, w, K, M, E, x, np.full((T, nu), E, np.int32))[0] == 2
+    rid = rng.integers(0, M, 9).astype(np.int32)
+    st, gr = O.ref_get_rows(dt, q, K, M, rid)
+    assert st == 0 and np.array_equal(O.get_rows(dt, q, K, M, rid).view(np.uint32), gr.view(np.uint32))
