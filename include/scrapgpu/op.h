@@ -60,7 +60,10 @@ typedef struct scrapgpu_mul_mat_params {
     int allow_broadcast;
 } scrapgpu_mul_mat_params;
 
-/* MUL_MAT_ID (reference op.h:170-174); validated by the core, not executed by the hip backend. */
+/* MUL_MAT_ID (reference op.h:170-174): inputs [src0 = experts (K x M x E), src1 = x (K x 1|n_used
+ * x n_tokens), ids (I32 n_used x n_tokens)], output [dst (M x n_used x n_tokens)]. The hip backend
+ * reads the ids on the device (indices outside [0, E) are clamped, like the reference's GPU
+ * kernels); n_used and max_prompt_tokens are not needed by it. */
 typedef struct scrapgpu_mul_mat_id_params {
     size_t struct_size;
     uint32_t n_used;

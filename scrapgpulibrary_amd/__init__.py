@@ -40,6 +40,10 @@ class OpDesc(C.Structure):
                 ("params_size", C.c_size_t)]
 
 
+class MulMatIdParams(C.Structure):
+    _fields_ = [("struct_size", C.c_size_t), ("n_used", C.c_uint32), ("max_prompt_tokens", C.c_uint32)]
+
+
 class MulMatParams(C.Structure):
     _fields_ = [("struct_size", C.c_size_t), ("allow_broadcast", C.c_int)]
 
@@ -181,6 +185,15 @@ def mul_mat_op(w: TensorDesc, x: TensorDesc, y: TensorDesc, allow_broadcast: int
     outs = (TensorDesc * 1)(y)
     p = MulMatParams(C.sizeof(MulMatParams), allow_broadcast)
     op = OpDesc(C.sizeof(OpDesc), OP_MUL_MAT, ins, 2, outs, 1, C.cast(C.pointer(p), C.c_void_p), C.sizeof(p))
+    return op, (ins, outs, p)
+
+
+def mul_mat_id_op(w: TensorDesc, x: TensorDesc, ids: TensorDesc, y: TensorDesc, n_used: int):
+    """(OpDesc, keep-alive tuple) for MUL_MAT_ID y[:, i, t] = W[:, :, ids[i, t]] x[:, i or 0, t]."""
+    ins = (TensorDesc * 3)(w, x, ids)
+    outs = (TensorDesc * 1)(y)
+    p = MulMatIdParams(C.sizeof(MulMatIdParams), n_used, 0)
+    op = OpDesc(C.sizeof(OpDesc), OP_MUL_MAT_ID, ins, 3, outs, 1, C.cast(C.pointer(p), C.c_void_p), C.sizeof(p))
     return op, (ins, outs, p)
 
 

@@ -570,6 +570,66 @@ scrapgpu_status mul_mat_rule(const scrapgpu_tensor_desc & w, const scrapgpu_tens
     return SCRAPGPU_STATUS_OK;
 }
 
+// the support rule of MUL_MAT_ID (reference ops.cpp:986-1024, opencl11/ops_moe.cpp): experts
+// w [K, M, E] quantized R32, x F32 [K, 1 or n_used, T], ids I32 [n_used, T], dst F32 [M, n_used, T].
+// Fills `a` / `id` (pointers left null) when supported. One (slot, token) pair per matvec slice.
+scrapgpu_status mul_mat_id_rule(const scrapgpu_tensor_desc & w, const scrapgpu_tensor_desc & x, const scrapgpu_tensor_desc & ids,
+                                const scrapgpu_tensor_desc & y, sgk::MatArgs * a, sgk::IdArgs * id, const char ** reason) {
+    if (!sg::is_quant(w.dtype)) return unsupported("the hip backend implements MUL_MAT_ID for Q4_0 / Q8_0 / Q4_K / Q6_K experts only", reason);
+    if (w.layout != SCRAPGPU_LAYOUT_R32) {
+        return unsupported("quantized experts must use the R32 layout (scrapgpu_tensor_upload packs them on the way)", reason);
+    }
+    if (!sg::r32_eligible(w)) return unsupported("src0 is not R32-eligible (contiguous, whole blocks per row, 16-byte slice strides)", reason);
+    if (x.dtype != SCRAPGPU_DTYPE_F32 || y.dtype != SCRAPGPU_DTYPE_F32 || x.layout != SCRAPGPU_LAYOUT_NATURAL || y.layout != SCRAPGPU_LAYOUT_NATURAL) {
+        return unsupported("MUL_MAT_ID expects an F32 natural-layout src1 and destination", reason);
+    }
+    if (ids.dtype != SCRAPGPU_DTYPE_I32 || ids.layout != SCRAPGPU_LAYOUT_NATURAL) return unsupported("MUL_MAT_ID expects I32 ids", reason);
+    if (x.nb[0] != 4 || y.nb[0] != 4 || ids.nb[0] != 4) return unsupported("MUL_MAT_ID needs contiguous rows of src1, ids and dst", reason);
+    for (int i = 1; i < 4; ++i) {
+        if (x.nb[i] % 4 != 0 || y.nb[i] % 4 != 0 || ids.nb[i] % 4 != 0) return unsupported("src1 / ids / dst strides must be multiples of 4 bytes", reason);
+    }
+    if (x.offset % 4 != 0 || y.offset % 4 != 0 || ids.offset % 4 != 0) return unsupported("src1 / ids / dst offsets must be multiples of 4 bytes", reason);
+    const int64_t K = sg::dim1(w.ne[0]), M = sg::dim1(w.ne[1]), E = sg::dim1(w.ne[2]);
+    const int64_t nu = sg::dim1(ids.ne[0]), T = sg::dim1(ids.ne[1]);
+    if (sg::dim1(w.ne[3]) != 1 || sg::dim1(x.ne[3]) != 1 || sg::dim1(ids.ne[2]) != 1 || sg::dim1(ids.ne[3]) != 1 || sg::dim1(x.ne[0]) != K ||
+        (sg::dim1(x.ne[1]) != 1 && sg::dim1(x.ne[1]) != nu) || sg::dim1(x.ne[2]) != T || sg::dim1(y.ne[0]) != M || sg::dim1(y.ne[1]) != nu ||
+        sg::dim1(y.ne[2]) != T || sg::dim1(y.ne[3]) != 1) {
+        if (reason) *reason = "MUL_MAT_ID needs [K,M,E] src0, [K,n_used|1,n_tokens] src1, I32 [n_used,n_tokens] ids and [M,n_used,n_tokens] dst";
+        return invalid("MUL_MAT_ID: shapes do not match the contract");
+    }
+    if (nu * T > 65535) return unsupported("MUL_MAT_ID: more than 65535 (slot, token) pairs", reason);
+    if (sg::sat_mul(sg::row_size(w.dtype, K), (uint64_t) M) >= ((uint64_t) 1 << 32)) {
+        return unsupported("MUL_MAT_ID: one expert must be smaller than 4 GiB", reason);
+    }
+    if (a) {
+        std::memset(a, 0, sizeof(*a));
+        a->dtype = w.dtype;
+        a->M = M;
+        a->K = K;
+        a->nb = K / (int64_t) sg::block_size(w.dtype);
+        a->w_s2 = w.nb[2];
+        a->x_s1 = (int64_t) (x.nb[1] / 4);
+        a->x_s2 = (int64_t) (x.nb[2] / 4);
+        a->y_s1 = (int64_t) (y.nb[1] / 4);
+        a->y_s2 = (int64_t) (y.nb[2] / 4);
+        a->N = 1;
+        a->ne12 = 1;
+        a->ne13 = 1;
+        a->r2 = 1;
+        a->r3 = 1;
+    }
+    if (id) {
+        id->ids = nullptr;
+        id->s0 = (int64_t) (ids.nb[0] / 4);
+        id->s1 = (int64_t) (ids.nb[1] / 4);
+        id->n_used = nu;
+        id->n_tok = T;
+        id->n_exp = E;
+        id->x_shared = sg::dim1(x.ne[1]) == 1 ? 1 : 0;
+    }
+    return SCRAPGPU_STATUS_OK;
+}
+
 scrapgpu_status api_supports(Device * d, const scrapgpu_op_desc * desc, const char ** reason) {
     (void) d;
     const scrapgpu_status v = scrapgpu_op_desc_validate(desc);
@@ -591,6 +651,8 @@ scrapgpu_status api_supports(Device * d, const scrapgpu_op_desc * desc, const ch
             }
             return SCRAPGPU_STATUS_OK;
         }
+        case SCRAPGPU_OP_MUL_MAT_ID:
+            return mul_mat_id_rule(desc->inputs[0], desc->inputs[1], desc->inputs[2], desc->outputs[0], nullptr, nullptr, reason);
         default:
             return unsupported("the hip backend implements the quantized MUL_MAT family only", reason);
     }
@@ -669,6 +731,27 @@ scrapgpu_status exec_desc(Stream * s, const scrapgpu_op_desc * desc) {
     if (st != SCRAPGPU_STATUS_OK) return st;
     SG_HIP(use(s->dev), "hipSetDevice");
     sgk::MatArgs mats[3];
+    if (desc->op == SCRAPGPU_OP_MUL_MAT_ID) {
+        sgk::IdArgs id;
+        st = mul_mat_id_rule(desc->inputs[0], desc->inputs[1], desc->inputs[2], desc->outputs[0], &mats[0], &id, nullptr);
+        if (st != SCRAPGPU_STATUS_OK) return st;
+        uint8_t *pw, *px, *pi, *py;
+        if ((st = resolve(s->dev, desc->inputs[0], &pw, "src0")) != SCRAPGPU_STATUS_OK) return st;
+        if ((st = resolve(s->dev, desc->inputs[1], &px, "src1")) != SCRAPGPU_STATUS_OK) return st;
+        if ((st = resolve(s->dev, desc->inputs[2], &pi, "ids")) != SCRAPGPU_STATUS_OK) return st;
+        if ((st = resolve(s->dev, desc->outputs[0], &py, "dst")) != SCRAPGPU_STATUS_OK) return st;
+        mats[0].w = pw;
+        mats[0].x = reinterpret_cast<const float *>(px);
+        mats[0].y = reinterpret_cast<float *>(py);
+        id.ids = reinterpret_cast<const int32_t *>(pi);
+        const double pairs = (double) (id.n_used * id.n_tok);
+        ProfScope prof(s->s);
+        const char * name = nullptr;
+        uint64_t grid = 0;
+        SG_HIP(sgk::launch_matvec(mats, 1, (int) s->dev->cus, s->s, &name, &grid, &id), "matvec (MUL_MAT_ID) launch");
+        prof.done(name, weight_bytes(mats[0]) * pairs, 2.0 * (double) mats[0].M * (double) mats[0].K * pairs);
+        return SCRAPGPU_STATUS_OK;
+    }
     if (desc->op == SCRAPGPU_OP_MUL_MAT) {
         const auto * p = static_cast<const scrapgpu_mul_mat_params *>(desc->params);
         const int bc = p->struct_size >= offsetof(scrapgpu_mul_mat_params, allow_broadcast) + sizeof(int) ? p->allow_broadcast : 0;
@@ -762,6 +845,7 @@ bool graphs_enabled() {
 scrapgpu_status plan_prepare(Stream * s, Plan * p) {
     size_t need = 0;
     for (PlanNode & n : p->nodes) {
+        if (n.op.op != SCRAPGPU_OP_MUL_MAT && n.op.op != SCRAPGPU_OP_MUL_MAT_MULTI) continue;
         const size_t cnt = n.op.op == SCRAPGPU_OP_MUL_MAT ? 1 : n.op.output_count;
         for (size_t i = 0; i < cnt; ++i) {
             sgk::MatArgs a;

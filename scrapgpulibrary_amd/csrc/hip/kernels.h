@@ -36,11 +36,23 @@ struct MatArgs {
     int64_t r2, r3;     // broadcast factors
 };
 
+// MUL_MAT_ID: the slices of a matvec are the (slot i, token t) pairs, pair = t * n_used + i; the
+// expert e = ids[i * s0 + t * s1] (I32, read on the device, clamped to [0, n_exp)) selects the
+// weights at w + e * w_s2; x column (x_shared ? 0 : i) of token t (x + i * x_s1 + t * x_s2);
+// y column i of token t (y + i * y_s1 + t * y_s2).
+struct IdArgs {
+    const int32_t * ids;
+    int64_t s0, s1;       // element strides of ids
+    int64_t n_used, n_tok, n_exp;
+    int x_shared;         // src1 has one column per token, shared by the slots
+};
+
 // decode matvec for 1 <= N <= 8 (weights streamed once, every column reused in registers).
 // nmat = 1, or 2..3 single-slice products of one dtype and K that share x (one fused launch;
-// mats[j].w / M / y / y_s1 per matrix, everything else from mats[0]).
+// mats[j].w / M / y / y_s1 per matrix, everything else from mats[0]). With `id` (nmat = 1, N = 1):
+// the MUL_MAT_ID pairs above instead of the slices of mats[0].
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
-                         uint64_t * grid_size);
+                         uint64_t * grid_size, const IdArgs * id = nullptr);
 
 // prefill: f16 MFMA with fp32 accumulate, weights dequantized in registers (any N >= 1).
 // `scratch` (matmul_scratch_bytes(a, cu_count) bytes of device memory, owned by the stream)

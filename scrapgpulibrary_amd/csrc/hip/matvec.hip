@@ -77,6 +77,10 @@ struct MvArgs {
     int64_t tiles; // row tiles over all matrices
     int cs;        // steps per x chunk of one wave
     int xvec;      // x columns are 16-byte aligned: float4 loads
+    // MUL_MAT_ID (ids != nullptr): blockIdx.y is the pair t * n_used + i
+    const int32_t * ids;
+    int64_t ids_s0, ids_s1, n_used, n_exp;
+    int x_shared;
 };
 
 __device__ __forceinline__ float half_bits(uint32_t h) {
@@ -498,7 +502,7 @@ __device__ void convert_x(const MvArgs & A, const float * x, int64_t e0, int nse
 
 // the slice a work-group works on
 struct Where {
-    int64_t i2, i3;
+    int64_t y_off; // element offset of the slice's (pair's) output in y
     uint64_t w_off;
     const float * x;
 };
@@ -507,18 +511,28 @@ struct Where {
 // the first loads issue right away)
 __device__ __forceinline__ Where where_of(const MvArgs & A) {
     Where w;
+    if (A.ids != nullptr) {
+        // MUL_MAT_ID: the pair's expert, read once per work-group (a uniform scalar load)
+        const uint32_t pr = blockIdx.y, nu = (uint32_t) A.n_used;
+        const uint32_t t = pr / nu, i = pr - t * nu;
+        int32_t e = A.ids[(int64_t) i * A.ids_s0 + (int64_t) t * A.ids_s1];
+        e = e < 0 ? 0 : (e >= (int32_t) A.n_exp ? (int32_t) A.n_exp - 1 : e);
+        w.w_off = (uint64_t) e * A.w_s2;
+        w.x = A.x + (A.x_shared ? 0 : (int64_t) i * A.x_s1) + (int64_t) t * A.x_s2;
+        w.y_off = (int64_t) i * A.ys1[0] + (int64_t) t * A.y_s2;
+        return w;
+    }
     if (gridDim.y == 1) {
-        w.i2 = w.i3 = 0;
+        w.y_off = 0;
         w.w_off = 0;
         w.x = A.x;
         return w;
     }
     const uint32_t sl = blockIdx.y, ne12 = (uint32_t) A.ne12;
     const uint32_t i2 = sl % ne12, i3 = sl / ne12;
-    w.i2 = i2;
-    w.i3 = i3;
+    w.y_off = (int64_t) i2 * A.y_s2 + (int64_t) i3 * A.y_s3;
     w.w_off = (uint64_t) (i2 / (uint32_t) A.r2) * A.w_s2 + (uint64_t) (i3 / (uint32_t) A.r3) * A.w_s3;
-    w.x = A.x + w.i2 * A.x_s2 + w.i3 * A.x_s3;
+    w.x = A.x + (int64_t) i2 * A.x_s2 + (int64_t) i3 * A.x_s3;
     return w;
 }
 
@@ -570,7 +584,7 @@ __device__ __forceinline__ void reduce_store(const MvArgs & A, const Where & wh,
             float v = 0.0f;
 #pragma unroll
             for (int w2 = 0; w2 < W; ++w2) v += red[(w2 * NC + n) * R + rr];
-            A.y[row.j][wh.i2 * A.y_s2 + wh.i3 * A.y_s3 + n * A.ys1[row.j] + m] = v;
+            A.y[row.j][wh.y_off + n * A.ys1[row.j] + m] = v;
         }
     }
 }
@@ -786,7 +800,7 @@ void set_tiles(MvArgs & L, const MatArgs * mats, int nmat, int R) {
 } // namespace
 
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
-                         uint64_t * grid_size) {
+                         uint64_t * grid_size, const IdArgs * id) {
     if (nmat < 1 || nmat > 3) return hipErrorInvalidValue;
     const MatArgs & a = mats[0];
     for (int j = 0; j < nmat; ++j) {
@@ -796,7 +810,8 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     }
     const int nc = (int) a.N;
     if (nc < 1 || nc > 8 || a.K <= 0 || a.K % 32 != 0) return hipErrorInvalidValue;
-    const int64_t slices = a.ne12 * a.ne13;
+    if (id != nullptr && (nmat != 1 || nc != 1 || id->ids == nullptr || id->n_used < 1 || id->n_tok < 1 || id->n_exp < 1)) return hipErrorInvalidValue;
+    const int64_t slices = id != nullptr ? id->n_used * id->n_tok : a.ne12 * a.ne13;
     if (slices < 1 || slices > 65535) return hipErrorInvalidValue;
     const int dt = a.dtype;
     if (dt != Q4_0 && dt != Q8_0 && dt != Q4_K && dt != Q6_K) return hipErrorInvalidValue;
@@ -828,6 +843,12 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     L.r2 = a.r2;
     L.r3 = a.r3;
     L.xvec = ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (a.x_s1 & 3) == 0 && (a.x_s2 & 3) == 0 && (a.x_s3 & 3) == 0) ? 1 : 0;
+    L.ids = id != nullptr ? id->ids : nullptr;
+    L.ids_s0 = id != nullptr ? id->s0 : 0;
+    L.ids_s1 = id != nullptr ? id->s1 : 0;
+    L.n_used = id != nullptr ? id->n_used : 1;
+    L.n_exp = id != nullptr ? id->n_exp : 1;
+    L.x_shared = id != nullptr ? id->x_shared : 0;
     if (kernel_name) *kernel_name = name_of(dt, nmat);
 
     // burst form (one column, K <= 64 steps): every wave's steps (<= 4) loaded at once, one tile

@@ -1,0 +1,148 @@
+"""GPU parity of MUL_MAT_ID (expert matvecs with device-side ids) against the CPU oracle, through
+the C-ABI only. Reference semantics: src/core/ref/ops.cpp:986-1024; the reference's GPU kernels
+read the ids on the device and clamp them (src/backends/opencl11/kernels/mul_mv_r.cl:30-33)."""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+import scrapgpulibrary_amd as sg
+from tests.gpu_util import check_matvec, upload_weights
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "mul_mat_id_get_rows.npz")
+
+
+def run_mul_mat_id(dev, st, dtype, w, K, M, E, x, ids):
+    """y [T, n_used, M] for experts `w` (natural bytes of E slices), x [T, n1, K], ids [T, n_used]."""
+    T, nu = ids.shape
+    n1 = x.shape[1]
+    wb, wt = upload_weights(dev, st, dtype, w, K, M, slices=E)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, n1, T), xb)
+    st.upload(xt, x)
+    ib = dev.alloc(ids.nbytes)
+    it = sg.tdesc(sg.I32, (nu, T), ib)
+    st.upload(it, np.ascontiguousarray(ids, np.int32))
+    yb = dev.alloc(4 * M * nu * T)
+    yt = sg.tdesc(sg.F32, (M, nu, T), yb)
+    op, keep = sg.mul_mat_id_op(wt, xt, it, yt, nu)
+    st.execute(op)
+    st.sync()
+    y = st.download(yt).reshape(T, nu, M).copy()
+    for b in (wb, xb, ib, yb):
+        b.free()
+    return y
+
+
+def check_pairs(y, ref, x, deq, ids):
+    """The decode gates per (slot, token) pair: each output column against its expert's weights."""
+    T, nu = ids.shape
+    for t in range(T):
+        for i in range(nu):
+            xc = x[t, i if x.shape[1] > 1 else 0][None, :]
+            check_matvec(y[t, i][None, :], ref[t, i][None, :], xc, deq[ids[t, i]])
+
+
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+def test_golden_mul_mat_id(hip, dtype):
+    """The reference's own MUL_MAT_ID outputs (scrapgpu_ref_execute, committed fixtures)."""
+    dev, st = hip
+    g = np.load(GOLD)
+    name = sg.NAMES[dtype]
+    K = 256 if sg.BLOCK[dtype] == 256 else 96
+    M, E = 40, 5
+    w, ids = g[f"{name}_mid_w"], g[f"{name}_mid_ids"]
+    deq = O.dequantize(dtype, w, K * M * E).reshape(E, M, K)
+    for n1 in (1, ids.shape[1]):
+        x, want = g[f"{name}_mid_x{n1}"], g[f"{name}_mid_y{n1}"]
+        y = run_mul_mat_id(dev, st, dtype, w, K, M, E, x, ids)
+        check_pairs(y, want, x, deq, ids)
+
+
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+@pytest.mark.parametrize("shared", [True, False], ids=["x_shared", "x_per_slot"])
+def test_mul_mat_id_moe_shapes(hip, dtype, shared):
+    """An MoE decode step: 8 experts of 2048 x 264 (a partial row group), 4 slots, 3 tokens."""
+    dev, st = hip
+    K, M, E, T, nu = 2048, 264, 8, 3, 4
+    w = O.quantize(dtype, O.normal(K * M * E, 31, 0.0, 0.02))
+    deq = O.dequantize(dtype, w, K * M * E).reshape(E, M, K)
+    rng = np.random.default_rng(5)
+    ids = np.stack([rng.permutation(E)[:nu] for _ in range(T)]).astype(np.int32)
+    x = O.normal(T * (1 if shared else nu) * K, 32).reshape(T, 1 if shared else nu, K)
+    y = run_mul_mat_id(dev, st, dtype, w, K, M, E, x, ids)
+    ref = O.mul_mat_id(dtype, w, K, M, E, x, ids)
+    check_pairs(y, ref, x, deq, ids)
+
+
+def test_mul_mat_id_clamps_out_of_range_ids(hip):
+    """Indices outside [0, E) select the nearest expert on the device (the reference's GPU rule);
+    the CPU reference would report INVALID_ARGUMENT instead."""
+    dev, st = hip
+    dtype, K, M, E = sg.Q4_K, 512, 64, 3
+    w = O.quantize(dtype, O.normal(K * M * E, 41, 0.0, 0.02))
+    deq = O.dequantize(dtype, w, K * M * E).reshape(E, M, K)
+    ids = np.array([[-5, 1], [3, 2], [1000, 0]], np.int32)
+    x = O.normal(3 * K, 42).reshape(3, 1, K)
+    y = run_mul_mat_id(dev, st, dtype, w, K, M, E, x, ids)
+    clamped = np.clip(ids, 0, E - 1)
+    check_pairs(y, O.mul_mat_id(dtype, w, K, M, E, x, clamped), x, deq, clamped)
+
+
+def test_mul_mat_id_plan_reads_ids_on_device(hip):
+    """A recorded plan (HIP graph) replayed after the ids changed in device memory follows them."""
+    dev, st = hip
+    dtype, K, M, E, T, nu = sg.Q8_0, 1024, 96, 6, 2, 2
+    w = O.quantize(dtype, O.normal(K * M * E, 51, 0.0, 0.02))
+    deq = O.dequantize(dtype, w, K * M * E).reshape(E, M, K)
+    wb, wt = upload_weights(dev, st, dtype, w, K, M, slices=E)
+    x = O.normal(T * K, 52).reshape(T, 1, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, 1, T), xb)
+    st.upload(xt, x)
+    ib = dev.alloc(4 * nu * T)
+    it = sg.tdesc(sg.I32, (nu, T), ib)
+    yb = dev.alloc(4 * M * nu * T)
+    yt = sg.tdesc(sg.F32, (M, nu, T), yb)
+    op, keep = sg.mul_mat_id_op(wt, xt, it, yt, nu)
+    nodes = (sg.PlanNode * 1)(sg.PlanNode(C.sizeof(sg.PlanNode), op, 0))
+    pdesc = sg.PlanDesc(C.sizeof(sg.PlanDesc), nodes, 1)
+    plan = C.c_void_p()
+    sg.check(sg.lib().scrapgpu_plan_build(dev.handle, C.byref(pdesc), C.byref(plan)), "plan_build")
+    try:
+        for ids in (np.array([[0, 5], [2, 3]], np.int32), np.array([[4, 1], [1, 4]], np.int32), np.array([[3, 3], [0, 2]], np.int32)):
+            st.upload(it, ids)
+            sg.check(sg.lib().scrapgpu_plan_execute(st.handle, plan), "plan_execute")
+            st.sync()
+            y = st.download(yt).reshape(T, nu, M)
+            check_pairs(y, O.mul_mat_id(dtype, w, K, M, E, x, ids), x, deq, ids)
+    finally:
+        sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
+    for b in (wb, xb, ib, yb):
+        b.free()
+
+
+def test_mul_mat_id_support_rules(hip):
+    dev, st = hip
+    K, M, E = 256, 32, 4
+    wb = dev.alloc(O.row_bytes(sg.Q4_K, K) * M * E)
+    xb, ib, yb = dev.alloc(4 * K * 3), dev.alloc(4 * 2 * 3), dev.alloc(4 * M * 2 * 3)
+    wt = sg.tdesc(sg.Q4_K, (K, M, E), wb, layout=sg.R32)
+    xt = sg.tdesc(sg.F32, (K, 1, 3), xb)
+    it = sg.tdesc(sg.I32, (2, 3), ib)
+    yt = sg.tdesc(sg.F32, (M, 2, 3), yb)
+    op, keep = sg.mul_mat_id_op(wt, xt, it, yt, 2)
+    assert dev.supported(op)[0] == sg.OK
+    op, keep = sg.mul_mat_id_op(wt, xt, it, sg.tdesc(sg.F32, (M, 3, 3), yb), 2)
+    assert dev.supported(op)[0] == sg.INVALID_ARGUMENT
+    op, keep = sg.mul_mat_id_op(sg.tdesc(sg.Q4_K, (K, M, E), wb), xt, it, yt, 2)
+    stt, reason = dev.supported(op)
+    assert stt == sg.UNSUPPORTED and "R32" in reason
+    op, keep = sg.mul_mat_id_op(wt, xt, sg.tdesc(sg.F32, (2, 3), ib), yt, 2)
+    assert dev.supported(op)[0] == sg.UNSUPPORTED
+    for b in (wb, xb, ib, yb):
+        b.free()
