@@ -53,6 +53,14 @@ typedef enum scrapgpu_op {
     SCRAPGPU_OP_CONT_MUL_MAT = 104,
 } scrapgpu_op;
 
+/* GET_ROWS (reference op.h:145-148): inputs [src0 (K x R per slice), ids (I32)], output
+ * [dst F32 (K x ids)]: dst[:, a, b, c] = row ids[a, b, c] of slice (b, c), dequantized. The hip
+ * backend reads R32 rows; indices outside [0, R) read the nearest row. */
+typedef struct scrapgpu_get_rows_params {
+    size_t struct_size;
+    int indices_are_i64;
+} scrapgpu_get_rows_params;
+
 /* MUL_MAT: inputs [src0 = W (K x M per slice), src1 = x (K x N)], output [dst (M x N)].
  * allow_broadcast != 0 lets src1 dims 2/3 be multiples of src0's (reference op.h:165-168). */
 typedef struct scrapgpu_mul_mat_params {

@@ -26,7 +26,7 @@ BLOCK = {F32: 1, F16: 1, BF16: 1, I32: 1, Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 2
 TYPE_SIZE = {F32: 4, F16: 2, BF16: 2, I32: 4, Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}
 NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k", F32: "f32"}
 # ops (include/scrapgpu/op.h)
-OP_ADD, OP_MUL_MAT, OP_MUL_MAT_ID, OP_MUL_MAT_MULTI = 10, 28, 29, 103
+OP_ADD, OP_GET_ROWS, OP_MUL_MAT, OP_MUL_MAT_ID, OP_MUL_MAT_MULTI = 10, 23, 28, 29, 103
 
 
 class TensorDesc(C.Structure):
@@ -40,12 +40,20 @@ class OpDesc(C.Structure):
                 ("params_size", C.c_size_t)]
 
 
+class GetRowsParams(C.Structure):
+    _fields_ = [("struct_size", C.c_size_t), ("indices_are_i64", C.c_int)]
+
+
 class MulMatIdParams(C.Structure):
     _fields_ = [("struct_size", C.c_size_t), ("n_used", C.c_uint32), ("max_prompt_tokens", C.c_uint32)]
 
 
 class MulMatParams(C.Structure):
     _fields_ = [("struct_size", C.c_size_t), ("allow_broadcast", C.c_int)]
+
+
+class GetRowsParams(C.Structure):
+    _fields_ = [("struct_size", C.c_size_t), ("indices_are_i64", C.c_int)]
 
 
 class MulMatIdParams(C.Structure):
@@ -194,6 +202,15 @@ def mul_mat_id_op(w: TensorDesc, x: TensorDesc, ids: TensorDesc, y: TensorDesc, 
     outs = (TensorDesc * 1)(y)
     p = MulMatIdParams(C.sizeof(MulMatIdParams), n_used, 0)
     op = OpDesc(C.sizeof(OpDesc), OP_MUL_MAT_ID, ins, 3, outs, 1, C.cast(C.pointer(p), C.c_void_p), C.sizeof(p))
+    return op, (ins, outs, p)
+
+
+def get_rows_op(w: TensorDesc, ids: TensorDesc, y: TensorDesc):
+    """(OpDesc, keep-alive tuple) for GET_ROWS y[:, a, b, c] = row ids[a, b, c] of slice (b, c) of W."""
+    ins = (TensorDesc * 2)(w, ids)
+    outs = (TensorDesc * 1)(y)
+    p = GetRowsParams(C.sizeof(GetRowsParams), 0)
+    op = OpDesc(C.sizeof(OpDesc), OP_GET_ROWS, ins, 2, outs, 1, C.cast(C.pointer(p), C.c_void_p), C.sizeof(p))
     return op, (ins, outs, p)
 
 

@@ -630,6 +630,50 @@ scrapgpu_status mul_mat_id_rule(const scrapgpu_tensor_desc & w, const scrapgpu_t
     return SCRAPGPU_STATUS_OK;
 }
 
+// the support rule of GET_ROWS (reference ops.cpp:690-721, opencl11/ops_support.cpp:82-88) on
+// R32 weights: src0 [K, R, S2, S3] quantized R32, ids I32 [n0, n1 <= S2, n2 <= S3], dst F32
+// [K, n0, n1, n2]. Fills `g` (pointers left null) when supported.
+scrapgpu_status get_rows_rule(const scrapgpu_tensor_desc & w, const scrapgpu_tensor_desc & ids, const scrapgpu_tensor_desc & y,
+                              sgk::GetRowsLaunch * g, const char ** reason) {
+    if (!sg::is_quant(w.dtype)) return unsupported("the hip backend implements GET_ROWS for Q4_0 / Q8_0 / Q4_K / Q6_K rows only", reason);
+    if (w.layout != SCRAPGPU_LAYOUT_R32) {
+        return unsupported("quantized GET_ROWS sources must use the R32 layout (scrapgpu_tensor_upload packs them on the way)", reason);
+    }
+    if (!sg::r32_eligible(w)) return unsupported("src0 is not R32-eligible (contiguous, whole blocks per row, 16-byte slice strides)", reason);
+    if (ids.dtype != SCRAPGPU_DTYPE_I32 || ids.layout != SCRAPGPU_LAYOUT_NATURAL || y.dtype != SCRAPGPU_DTYPE_F32 || y.layout != SCRAPGPU_LAYOUT_NATURAL) {
+        return unsupported("GET_ROWS expects I32 indices and an F32 natural-layout destination", reason);
+    }
+    if (ids.nb[0] != 4 || y.nb[0] != 4) return unsupported("GET_ROWS needs contiguous rows of ids and dst", reason);
+    for (int i = 1; i < 4; ++i) {
+        if (ids.nb[i] % 4 != 0 || y.nb[i] % 4 != 0) return unsupported("ids / dst strides must be multiples of 4 bytes", reason);
+    }
+    if (ids.offset % 4 != 0 || y.offset % 4 != 0) return unsupported("ids / dst offsets must be multiples of 4 bytes", reason);
+    const int64_t K = sg::dim1(w.ne[0]);
+    if (sg::dim1(ids.ne[3]) != 1 || sg::dim1(ids.ne[1]) > sg::dim1(w.ne[2]) || sg::dim1(ids.ne[2]) > sg::dim1(w.ne[3]) || sg::dim1(y.ne[0]) != K ||
+        sg::dim1(y.ne[1]) != sg::dim1(ids.ne[0]) || sg::dim1(y.ne[2]) != sg::dim1(ids.ne[1]) || sg::dim1(y.ne[3]) != sg::dim1(ids.ne[2])) {
+        if (reason) *reason = "GET_ROWS: dst must be [ne00, ids] over the slices of src0";
+        return invalid("GET_ROWS: dst must be [ne00, ids] over the slices of src0");
+    }
+    if (g) {
+        std::memset(g, 0, sizeof(*g));
+        g->dtype = w.dtype;
+        g->w_s2 = w.nb[2];
+        g->w_s3 = w.nb[3];
+        g->i_s0 = (int64_t) (ids.nb[0] / 4);
+        g->i_s1 = (int64_t) (ids.nb[1] / 4);
+        g->i_s2 = (int64_t) (ids.nb[2] / 4);
+        g->y_s1 = (int64_t) (y.nb[1] / 4);
+        g->y_s2 = (int64_t) (y.nb[2] / 4);
+        g->y_s3 = (int64_t) (y.nb[3] / 4);
+        g->K = K;
+        g->M = sg::dim1(w.ne[1]);
+        g->n0 = sg::dim1(ids.ne[0]);
+        g->n1 = sg::dim1(ids.ne[1]);
+        g->n2 = sg::dim1(ids.ne[2]);
+    }
+    return SCRAPGPU_STATUS_OK;
+}
+
 scrapgpu_status api_supports(Device * d, const scrapgpu_op_desc * desc, const char ** reason) {
     (void) d;
     const scrapgpu_status v = scrapgpu_op_desc_validate(desc);
@@ -653,6 +697,8 @@ scrapgpu_status api_supports(Device * d, const scrapgpu_op_desc * desc, const ch
         }
         case SCRAPGPU_OP_MUL_MAT_ID:
             return mul_mat_id_rule(desc->inputs[0], desc->inputs[1], desc->inputs[2], desc->outputs[0], nullptr, nullptr, reason);
+        case SCRAPGPU_OP_GET_ROWS:
+            return get_rows_rule(desc->inputs[0], desc->inputs[1], desc->outputs[0], nullptr, reason);
         default:
             return unsupported("the hip backend implements the quantized MUL_MAT family only", reason);
     }
@@ -731,6 +777,23 @@ scrapgpu_status exec_desc(Stream * s, const scrapgpu_op_desc * desc) {
     if (st != SCRAPGPU_STATUS_OK) return st;
     SG_HIP(use(s->dev), "hipSetDevice");
     sgk::MatArgs mats[3];
+    if (desc->op == SCRAPGPU_OP_GET_ROWS) {
+        sgk::GetRowsLaunch g;
+        st = get_rows_rule(desc->inputs[0], desc->inputs[1], desc->outputs[0], &g, nullptr);
+        if (st != SCRAPGPU_STATUS_OK) return st;
+        uint8_t *pw, *pi, *py;
+        if ((st = resolve(s->dev, desc->inputs[0], &pw, "src0")) != SCRAPGPU_STATUS_OK) return st;
+        if ((st = resolve(s->dev, desc->inputs[1], &pi, "ids")) != SCRAPGPU_STATUS_OK) return st;
+        if ((st = resolve(s->dev, desc->outputs[0], &py, "dst")) != SCRAPGPU_STATUS_OK) return st;
+        g.w = pw;
+        g.ids = reinterpret_cast<const int32_t *>(pi);
+        g.y = reinterpret_cast<float *>(py);
+        const double rows = (double) (g.n0 * g.n1 * g.n2);
+        ProfScope prof(s->s);
+        SG_HIP(sgk::launch_get_rows(g, s->s), "get_rows launch");
+        prof.done("get_rows", rows * (double) sg::row_size(desc->inputs[0].dtype, g.K), 0.0);
+        return SCRAPGPU_STATUS_OK;
+    }
     if (desc->op == SCRAPGPU_OP_MUL_MAT_ID) {
         sgk::IdArgs id;
         st = mul_mat_id_rule(desc->inputs[0], desc->inputs[1], desc->inputs[2], desc->outputs[0], &mats[0], &id, nullptr);

@@ -61,6 +61,20 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
 size_t matmul_scratch_bytes(const MatArgs & a, int cu_count);
 hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name);
 
+// GET_ROWS on R32 weights: dst[:, a, b, c] = dequantized row ids[a, b, c] of slice (b, c) of src0
+// (bit-exact with the dequantizer; out-of-range indices read the nearest row).
+struct GetRowsLaunch {
+    int dtype;
+    const uint8_t * w;
+    uint64_t w_s2, w_s3;
+    const int32_t * ids;
+    int64_t i_s0, i_s1, i_s2; // element strides
+    float * y;
+    int64_t y_s1, y_s2, y_s3; // element strides
+    int64_t K, M, n0, n1, n2; // src0 ne0, ne1; ids ne0..2
+};
+hipError_t launch_get_rows(const GetRowsLaunch & g, hipStream_t stream);
+
 // R32 pack (natural -> R32) or unpack of rows [row0, row0 + nrows) of one slice of M rows; row0 is
 // a multiple of 32. `nat` holds the natural bytes of those rows, `rep` is the slice's R32 base.
 hipError_t launch_r32_move(int dtype, int64_t K, int64_t M, int64_t row0, int64_t nrows, uint8_t * nat, uint8_t * rep, bool pack,

@@ -439,6 +439,103 @@ __global__ __launch_bounds__(256) void k_fill_normal(float * dst, int64_t n, uin
     }
 }
 
+// ---- GET_ROWS on R32 weights: one work-group per output row ------------------------------------
+// Byte j of natural block b of the selected row is read where the R32 layout put it (the areas of
+// areas_of(): area k of the slice at M * nb * (bytes per block of the earlier areas); inside an
+// area of L bytes per block, group g0 starts at g0 * nb * L and 16-byte unit u of block b of row
+// `lane` sits at ((b * L / 16 + u) * rs + lane) * 16; a 2-byte area is an array of halves at
+// (b * rs + lane) * 2), and the element formulas are those of k_dequant (bit-exact).
+struct GetRowsArgs {
+    const uint8_t * w;    // slice (0, 0) of src0
+    uint64_t w_s2, w_s3;  // slice strides (bytes)
+    const int32_t * ids;
+    int64_t i_s0, i_s1, i_s2; // element strides of ids
+    float * y;
+    int64_t y_s1, y_s2, y_s3; // element strides of dst
+    int64_t K, M, nb, n0, n1; // n0, n1: ids ne0, ne1 (rows = n0 * n1 * ne2)
+    Areas ar;
+};
+
+struct R32Row {
+    const uint8_t * slice;
+    int64_t M, nb, g0;
+    int64_t rs, lane;
+    Areas ar;
+    __device__ uint8_t byte(int64_t b, int j) const {
+        uint64_t before = 0;
+        for (int k = 0; k < ar.na; ++k) {
+            const int src = ar.src[k], len = ar.len[k];
+            if (j >= src && j < src + len) {
+                const int o = j - src;
+                const uint8_t * area = slice + (uint64_t) M * (uint64_t) nb * before;
+                const uint8_t * p;
+                if (len == 2) {
+                    p = area + (uint64_t) g0 * nb * 2 + ((uint64_t) b * rs + lane) * 2 + o;
+                } else {
+                    p = area + (uint64_t) g0 * nb * len + (((uint64_t) b * (len / 16) + o / 16) * rs + lane) * 16 + (o % 16);
+                }
+                return (uint8_t) (*p ^ ar.xr[k]);
+            }
+            before += (uint64_t) len;
+        }
+        return 0;
+    }
+    __device__ uint16_t half(int64_t b, int j) const {
+        return (uint16_t) (byte(b, j) | (byte(b, j + 1) << 8));
+    }
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void k_get_rows(GetRowsArgs a) {
+    const int64_t row = blockIdx.x;
+    const int64_t c = row / (a.n0 * a.n1), rem = row - c * a.n0 * a.n1, bi = rem / a.n0, ai = rem - bi * a.n0;
+    int64_t r = a.ids[ai * a.i_s0 + bi * a.i_s1 + c * a.i_s2];
+    r = r < 0 ? 0 : (r >= a.M ? a.M - 1 : r); // out-of-range rows read the nearest row
+    R32Row rr;
+    rr.slice = a.w + (uint64_t) bi * a.w_s2 + (uint64_t) c * a.w_s3;
+    rr.M = a.M;
+    rr.nb = a.nb;
+    rr.g0 = r & ~(int64_t) 31;
+    rr.rs = a.M - rr.g0 < 32 ? a.M - rr.g0 : 32;
+    rr.lane = r - rr.g0;
+    rr.ar = a.ar;
+    float * y = a.y + ai * a.y_s1 + bi * a.y_s2 + c * a.y_s3;
+    for (int64_t e = threadIdx.x; e < a.K; e += blockDim.x) {
+        float v;
+        if (DT == Q4_0) {
+            const int64_t b = e / 32;
+            const int i = (int) (e % 32);
+            const float d = h2f(rr.half(b, 0));
+            const int q = rr.byte(b, 2 + (i & 15));
+            v = (float) ((i < 16 ? (q & 0x0F) : (q >> 4)) - 8) * d;
+        } else if (DT == Q8_0) {
+            const int64_t b = e / 32;
+            v = (float) (int8_t) rr.byte(b, 2 + (int) (e % 32)) * h2f(rr.half(b, 0));
+        } else if (DT == Q4_K) {
+            const int64_t b = e / 256;
+            const int i = (int) (e % 256), cc = i / 64, l = i % 32, hi = (i % 64) >= 32;
+            uint8_t sb[12];
+            for (int k = 0; k < 12; ++k) sb[k] = rr.byte(b, 4 + k);
+            uint8_t sc, mn;
+            k4_scale_min(2 * cc + hi, sb, &sc, &mn);
+            const float d1 = h2f(rr.half(b, 0)) * (float) sc;
+            const float m1 = h2f(rr.half(b, 2)) * (float) mn;
+            const int q = rr.byte(b, 16 + 32 * cc + l);
+            v = d1 * (float) (hi ? (q >> 4) : (q & 0x0F)) - m1;
+        } else {
+            const int64_t b = e / 256;
+            const int i = (int) (e % 256), h = i / 128, rq = (i % 128) / 32, l = i % 32;
+            const uint8_t qh = rr.byte(b, 128 + 32 * h + l);
+            const int lowq = (rq & 1) ? rr.byte(b, 64 * h + l + 32) : rr.byte(b, 64 * h + l);
+            const int nib = rq < 2 ? (lowq & 0x0F) : (lowq >> 4);
+            const int q = (nib | (((qh >> (2 * rq)) & 3) << 4)) - 32;
+            const int8_t sc = (int8_t) rr.byte(b, 192 + 8 * h + 2 * rq + l / 16);
+            v = h2f(rr.half(b, 208)) * (float) sc * (float) q;
+        }
+        y[e] = v;
+    }
+}
+
 unsigned grid_for(int64_t n, int threads) {
     const int64_t g = (n + threads - 1) / threads;
     return (unsigned) (g < 65536 * 8 ? (g < 1 ? 1 : g) : 65536 * 8);
@@ -476,6 +573,39 @@ hipError_t launch_r32_move(int dtype, int64_t K, int64_t M, int64_t row0, int64_
         before += (uint64_t) ar.len[k];
     }
     return hipSuccess;
+}
+
+hipError_t launch_get_rows(const GetRowsLaunch & g, hipStream_t stream) {
+    const int64_t rows = g.n0 * g.n1 * g.n2;
+    if (rows <= 0) return hipSuccess;
+    if (rows > 0x7FFFFFFF) return hipErrorInvalidValue;
+    GetRowsArgs a;
+    a.w = g.w;
+    a.w_s2 = g.w_s2;
+    a.w_s3 = g.w_s3;
+    a.ids = g.ids;
+    a.i_s0 = g.i_s0;
+    a.i_s1 = g.i_s1;
+    a.i_s2 = g.i_s2;
+    a.y = g.y;
+    a.y_s1 = g.y_s1;
+    a.y_s2 = g.y_s2;
+    a.y_s3 = g.y_s3;
+    a.K = g.K;
+    a.M = g.M;
+    a.nb = g.K / block_elems(g.dtype);
+    a.n0 = g.n0;
+    a.n1 = g.n1;
+    a.ar = areas_of(g.dtype);
+    const dim3 grid((unsigned) rows), block(256);
+    switch (g.dtype) {
+        case Q4_0: hipLaunchKernelGGL(k_get_rows<Q4_0>, grid, block, 0, stream, a); break;
+        case Q8_0: hipLaunchKernelGGL(k_get_rows<Q8_0>, grid, block, 0, stream, a); break;
+        case Q4_K: hipLaunchKernelGGL(k_get_rows<Q4_K>, grid, block, 0, stream, a); break;
+        case Q6_K: hipLaunchKernelGGL(k_get_rows<Q6_K>, grid, block, 0, stream, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_dequantize(int dtype, const uint8_t * src, float * dst, int64_t n_blocks, hipStream_t stream) {

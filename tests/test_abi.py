@@ -53,6 +53,7 @@ int main(void) {
     O(scrapgpu_op_desc, outputs) O(scrapgpu_op_desc, output_count) O(scrapgpu_op_desc, params) O(scrapgpu_op_desc, params_size)
     P(scrapgpu_mul_mat_params) O(scrapgpu_mul_mat_params, allow_broadcast)
     P(scrapgpu_mul_mat_id_params) O(scrapgpu_mul_mat_id_params, n_used) O(scrapgpu_mul_mat_id_params, max_prompt_tokens)
+    P(scrapgpu_get_rows_params) O(scrapgpu_get_rows_params, indices_are_i64)
     P(scrapgpu_device_info) O(scrapgpu_device_info, generation) O(scrapgpu_device_info, total_memory_bytes)
     O(scrapgpu_device_info, compute_units) O(scrapgpu_device_info, warp_or_wave_width) O(scrapgpu_device_info, quirks)
     O(scrapgpu_device_info, tuning_overrides)
@@ -63,6 +64,8 @@ int main(void) {
     O(scrapgpu_backend_vtable, stream_device)
     printf("SCRAPGPU_OP_MUL_MAT %d\nSCRAPGPU_OP_MUL_MAT_MULTI %d\nSCRAPGPU_DTYPE_Q6_K %d\nSCRAPGPU_LAYOUT_R32 %d\n",
            (int) SCRAPGPU_OP_MUL_MAT, (int) SCRAPGPU_OP_MUL_MAT_MULTI, (int) SCRAPGPU_DTYPE_Q6_K, (int) SCRAPGPU_LAYOUT_R32);
+    printf("SCRAPGPU_OP_MUL_MAT_ID %d\nSCRAPGPU_OP_GET_ROWS %d\nSCRAPGPU_DTYPE_I32 %d\n",
+           (int) SCRAPGPU_OP_MUL_MAT_ID, (int) SCRAPGPU_OP_GET_ROWS, (int) SCRAPGPU_DTYPE_I32);
     printf("ABI %u.%u\n", SCRAPGPU_ABI_VERSION_MAJOR, SCRAPGPU_ABI_VERSION_MINOR);
     return 0;
 }
@@ -85,6 +88,10 @@ def test_struct_layouts_match_ctypes():
     assert int(lines["scrapgpu_device_info"]) == C.sizeof(sg.DeviceInfo)
     assert int(lines["scrapgpu_plan_node"]) == C.sizeof(sg.PlanNode)
     assert int(lines["scrapgpu_mul_mat_params"]) == C.sizeof(sg.MulMatParams)
+    assert int(lines["scrapgpu_mul_mat_id_params"]) == C.sizeof(sg.MulMatIdParams)
+    assert int(lines["scrapgpu_get_rows_params"]) == C.sizeof(sg.GetRowsParams)
+    assert int(lines["SCRAPGPU_OP_MUL_MAT_ID"]) == sg.OP_MUL_MAT_ID
+    assert int(lines["SCRAPGPU_OP_GET_ROWS"]) == sg.OP_GET_ROWS
     assert int(lines["scrapgpu_tensor_desc.layout"]) == sg.TensorDesc.layout.offset
     assert int(lines["SCRAPGPU_OP_MUL_MAT"]) == sg.OP_MUL_MAT
     assert int(lines["SCRAPGPU_LAYOUT_R32"]) == sg.R32
