@@ -225,6 +225,119 @@ def bench_prefill(dev, st, n_tokens, reps):
     return out
 
 
+MOE_E, MOE_USED, MOE_HIDDEN, MOE_FFN, MOE_LAYERS = 128, 8, 2048, 768, 4
+
+
+def hip_events_ms(st, fn, reps):
+    """Mean time of fn() (enqueued work on the model's stream) between two HIP events, over reps."""
+    hip = hip_runtime()
+    stream = C.c_void_p(sg.lib().scrapgpu_hip_stream_native(st.handle))
+    ev = [C.c_void_p(), C.c_void_p()]
+    total = 0.0
+    try:
+        for e in ev:
+            hip_check(hip.hipEventCreate(C.byref(e)), "hipEventCreate")
+        for _ in range(reps):
+            st.sync()
+            hip_check(hip.hipEventRecord(ev[0], stream), "hipEventRecord")
+            fn()
+            hip_check(hip.hipEventRecord(ev[1], stream), "hipEventRecord")
+            hip_check(hip.hipEventSynchronize(ev[1]), "hipEventSynchronize")
+            ms = C.c_float()
+            hip_check(hip.hipEventElapsedTime(C.byref(ms), ev[0], ev[1]), "hipEventElapsedTime")
+            total += ms.value
+    finally:
+        for e in ev:
+            if e.value:
+                hip.hipEventDestroy(e)
+    return total / reps
+
+
+def bench_moe(dev, st, tokens):
+    """MUL_MAT_ID: a Qwen3-30B-A3B-shaped MoE decode token, bs = 1: per layer the gate and up experts
+    (Q4_K, 2048 -> 768) and the down experts (Q6_K, 768 -> 2048) of 128, 8 selected, as three
+    MUL_MAT_ID ops sharing the layer's ids; MOE_LAYERS layers (1.56 GB of experts, past the 256 MB
+    MALL); fresh random ids every token (read on the device by the recorded plan)."""
+    rng = np.random.default_rng(17)
+    bufs = []
+    tmp = dev.alloc(4 * MOE_HIDDEN * MOE_FFN * MOE_E)
+    bufs.append(tmp)
+    shapes = (("gate", sg.Q4_K, MOE_HIDDEN, MOE_FFN), ("up", sg.Q4_K, MOE_HIDDEN, MOE_FFN), ("down", sg.Q6_K, MOE_FFN, MOE_HIDDEN))
+    xh = sg.tdesc(sg.F32, (MOE_HIDDEN, 1, 1), dev.alloc(4 * MOE_HIDDEN))
+    st.fill_normal(xh, seed=21)
+    xf = sg.tdesc(sg.F32, (MOE_FFN, MOE_USED, 1), dev.alloc(4 * MOE_FFN * MOE_USED))
+    st.fill_normal(xf, seed=22)
+    ids_buf = dev.alloc(4 * MOE_USED * MOE_LAYERS)
+    bufs += [ids_buf]
+    keep, nodes = [], []
+    for li in range(MOE_LAYERS):
+        ids = sg.tdesc(sg.I32, (MOE_USED, 1), ids_buf, offset=4 * MOE_USED * li)
+        for name, dt, K, M in shapes:
+            b = dev.alloc(weight_bytes(dt, K, M) * MOE_E)
+            bufs.append(b)
+            f = sg.tdesc(sg.F32, (K, M * MOE_E), tmp)
+            st.fill_normal(f, seed=100 * li + len(nodes), mean=0.0, std=0.02)
+            st.quantize(f, sg.tdesc(dt, (K, M * MOE_E), b, layout=sg.R32))
+            w = sg.tdesc(dt, (K, M, MOE_E), b, layout=sg.R32)
+            y = sg.tdesc(sg.F32, (M, MOE_USED, 1), dev.alloc(4 * M * MOE_USED))
+            op, k = sg.mul_mat_id_op(w, xf if name == "down" else xh, ids, y, MOE_USED)
+            keep.append((op, k))
+            nodes.append(sg.PlanNode(C.sizeof(sg.PlanNode), op, 0))
+    st.sync()
+    arr = (sg.PlanNode * len(nodes))(*nodes)
+    pdesc = sg.PlanDesc(C.sizeof(sg.PlanDesc), arr, len(nodes))
+    plan = C.c_void_p()
+    sg.check(sg.lib().scrapgpu_plan_build(dev.handle, C.byref(pdesc), C.byref(plan)), "plan_build")
+    ids_all = sg.tdesc(sg.I32, (MOE_USED * MOE_LAYERS,), ids_buf)
+
+    def token():
+        sg.check(sg.lib().scrapgpu_plan_execute(st.handle, plan), "plan_execute")
+
+    try:
+        times = []
+        for t in range(tokens + 3):
+            sel = np.concatenate([rng.permutation(MOE_E)[:MOE_USED] for _ in range(MOE_LAYERS)]).astype(np.int32)
+            st.upload(ids_all, sel)
+            ms = hip_events_ms(st, token, 1)
+            if t >= 3:
+                times.append(ms)
+    finally:
+        sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
+    ms = float(np.mean(times))
+    by = MOE_LAYERS * MOE_USED * sum(weight_bytes(dt, K, M) for _, dt, K, M in shapes)
+    return {"workload": f"Qwen3-30B-A3B MoE experts: {MOE_LAYERS} layers x (gate, up Q4_K {MOE_HIDDEN}->{MOE_FFN}; down Q6_K "
+                        f"{MOE_FFN}->{MOE_HIDDEN}) x {MOE_E} experts, {MOE_USED} used, bs=1, MUL_MAT_ID with device ids",
+            "ms_per_token": round(ms, 4), "selected_weight_bytes_per_token": by, "GBps": round(by / (ms * 1e-3) / 1e9, 1),
+            "launches_per_token": len(nodes)}
+
+
+def bench_get_rows(dev, st, n_rows, reps):
+    """GET_ROWS: n_rows random rows of a Q6_K 151936 x 4096 table (the Qwen3 LM head / embedding
+    shape, 510 MB, R32) dequantized to f32."""
+    K, R = HIDDEN, 151936
+    tmp = dev.alloc(4 * K * R)
+    st.fill_normal(sg.tdesc(sg.F32, (K, R), tmp), seed=31, std=0.02)
+    wb = dev.alloc(weight_bytes(sg.Q6_K, K, R))
+    w = sg.tdesc(sg.Q6_K, (K, R), wb, layout=sg.R32)
+    st.quantize(sg.tdesc(sg.F32, (K, R), tmp), w)
+    tmp.free()
+    rng = np.random.default_rng(33)
+    ib = dev.alloc(4 * n_rows)
+    ids = sg.tdesc(sg.I32, (n_rows, 1, 1), ib)
+    st.upload(ids, rng.integers(0, R, n_rows).astype(np.int32))
+    yb = dev.alloc(4 * K * n_rows)
+    y = sg.tdesc(sg.F32, (K, n_rows, 1, 1), yb)
+    op, keep = sg.get_rows_op(w, ids, y)
+    for _ in range(3):
+        st.execute(op)
+    ms = hip_events_ms(st, lambda: [st.execute(op) for _ in range(10)], reps) / 10
+    rb = weight_bytes(sg.Q6_K, K, 1) * n_rows
+    for b in (wb, ib, yb):
+        b.free()
+    return {"workload": f"{n_rows} rows of a Q6_K {R}x{K} R32 table -> f32", "us": round(ms * 1e3, 2),
+            "rows_read_bytes": rb, "f32_written_bytes": 4 * K * n_rows, "GBps_read_plus_write": round((rb + 4 * K * n_rows) / (ms * 1e-3) / 1e9, 1)}
+
+
 def cpu_baseline(dev, st, model, seconds):
     """The oracle (reference-faithful C restatement, 1 thread) on one gate matrix at N=1."""
     import oracle as O
@@ -287,6 +400,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MUL_MAT_ID (MoE decode) line")
+    ap.add_argument("--no-get-rows", action="store_true", help="skip the GET_ROWS line")
     ap.add_argument("--no-fuse", action="store_true", help="one MUL_MAT per weight instead of MUL_MAT_MULTI for q/k/v and gate/up")
     ap.add_argument("--calibrate", action="store_true", help="only run the 256 MiB copy that calibrates the PMC byte counters")
     args = ap.parse_args()
@@ -329,6 +444,8 @@ def main():
                            "GBps": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1)} for r in rows}
 
     prefill = None if args.no_prefill else bench_prefill(dev, st, 512, 10)
+    moe = None if args.no_moe else bench_moe(dev, st, 20)
+    get_rows = None if args.no_get_rows else bench_get_rows(dev, st, 512, 5)
     cpu = None if args.no_cpu else cpu_baseline(dev, st, model, args.cpu_seconds)
 
     result = {
@@ -357,6 +474,8 @@ def main():
                      "bytes_per_launch": dom_bytes, "mean_launch_us": round(dom_ms * 1e3, 3)},
         "prefill_M512": prefill,
         "prefill_peak_frac": None if prefill is None else round(max(v["tflops"] for v in prefill.values()) / F16_PEAK_TFLOPS, 4),
+        "moe_decode_mul_mat_id": moe,
+        "get_rows": get_rows,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

@@ -136,40 +136,41 @@ __device__ void k4_scale_min(int j, const uint8_t * s, uint8_t * sc, uint8_t * m
 
 // ---- dequantization: one thread per output element -------------------------------------------
 
+// element i of the natural block at blk (the reference's dequantize_row_* formulas, quant.cpp:30-108)
+template <int DT>
+__device__ __forceinline__ float deq_elem(const uint8_t * blk, int i) {
+    if (DT == Q4_0) {
+        const float d = h2f(rd16(blk));
+        const int q = blk[2 + (i & 15)];
+        return (float) ((i < 16 ? (q & 0x0F) : (q >> 4)) - 8) * d;
+    } else if (DT == Q8_0) {
+        return (float) (int8_t) blk[2 + i] * h2f(rd16(blk));
+    } else if (DT == Q4_K) {
+        const int c = i / 64, l = i % 32, hi = (i % 64) >= 32;
+        uint8_t sc, mn;
+        k4_scale_min(2 * c + hi, blk + 4, &sc, &mn);
+        const float d1 = h2f(rd16(blk)) * (float) sc;
+        const float m1 = h2f(rd16(blk + 2)) * (float) mn;
+        const int q = blk[16 + 32 * c + l];
+        return d1 * (float) (hi ? (q >> 4) : (q & 0x0F)) - m1;
+    } else {
+        const int h = i / 128, r = (i % 128) / 32, l = i % 32;
+        const uint8_t * ql = blk + 64 * h;
+        const uint8_t qh = blk[128 + 32 * h + l];
+        const int lowq = (r & 1) ? ql[l + 32] : ql[l];
+        const int nib = r < 2 ? (lowq & 0x0F) : (lowq >> 4);
+        const int v = (nib | (((qh >> (2 * r)) & 3) << 4)) - 32;
+        const int8_t sc = (int8_t) blk[192 + 8 * h + 2 * r + l / 16];
+        return h2f(rd16(blk + 208)) * (float) sc * (float) v;
+    }
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t * src, float * dst, int64_t n) {
+    constexpr int BS = DT == Q4_K || DT == Q6_K ? 256 : 32;
+    constexpr int BB = DT == Q4_0 ? 18 : DT == Q8_0 ? 34 : DT == Q4_K ? 144 : 210;
     for (int64_t e = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t) gridDim.x * blockDim.x) {
-        float y;
-        if (DT == Q4_0) {
-            const uint8_t * blk = src + (e / 32) * 18;
-            const int i = (int) (e % 32);
-            const float d = h2f(rd16(blk));
-            const int q = blk[2 + (i & 15)];
-            y = (float) ((i < 16 ? (q & 0x0F) : (q >> 4)) - 8) * d;
-        } else if (DT == Q8_0) {
-            const uint8_t * blk = src + (e / 32) * 34;
-            y = (float) (int8_t) blk[2 + e % 32] * h2f(rd16(blk));
-        } else if (DT == Q4_K) {
-            const uint8_t * blk = src + (e / 256) * 144;
-            const int i = (int) (e % 256), c = i / 64, l = i % 32, hi = (i % 64) >= 32;
-            uint8_t sc, mn;
-            k4_scale_min(2 * c + hi, blk + 4, &sc, &mn);
-            const float d1 = h2f(rd16(blk)) * (float) sc;
-            const float m1 = h2f(rd16(blk + 2)) * (float) mn;
-            const int q = blk[16 + 32 * c + l];
-            y = d1 * (float) (hi ? (q >> 4) : (q & 0x0F)) - m1;
-        } else {
-            const uint8_t * blk = src + (e / 256) * 210;
-            const int i = (int) (e % 256), h = i / 128, r = (i % 128) / 32, l = i % 32;
-            const uint8_t * ql = blk + 64 * h;
-            const uint8_t qh = blk[128 + 32 * h + l];
-            const int lowq = (r & 1) ? ql[l + 32] : ql[l];
-            const int nib = r < 2 ? (lowq & 0x0F) : (lowq >> 4);
-            const int v = (nib | (((qh >> (2 * r)) & 3) << 4)) - 32;
-            const int8_t sc = (int8_t) blk[192 + 8 * h + 2 * r + l / 16];
-            y = h2f(rd16(blk + 208)) * (float) sc * (float) v;
-        }
-        dst[e] = y;
+        dst[e] = deq_elem<DT>(src + (e / BS) * BB, (int) (e % BS));
     }
 }
 
@@ -456,83 +457,54 @@ struct GetRowsArgs {
     Areas ar;
 };
 
-struct R32Row {
-    const uint8_t * slice;
-    int64_t M, nb, g0;
-    int64_t rs, lane;
-    Areas ar;
-    __device__ uint8_t byte(int64_t b, int j) const {
-        uint64_t before = 0;
-        for (int k = 0; k < ar.na; ++k) {
-            const int src = ar.src[k], len = ar.len[k];
-            if (j >= src && j < src + len) {
-                const int o = j - src;
-                const uint8_t * area = slice + (uint64_t) M * (uint64_t) nb * before;
-                const uint8_t * p;
-                if (len == 2) {
-                    p = area + (uint64_t) g0 * nb * 2 + ((uint64_t) b * rs + lane) * 2 + o;
-                } else {
-                    p = area + (uint64_t) g0 * nb * len + (((uint64_t) b * (len / 16) + o / 16) * rs + lane) * 16 + (o % 16);
-                }
-                return (uint8_t) (*p ^ ar.xr[k]);
-            }
-            before += (uint64_t) len;
-        }
-        return 0;
-    }
-    __device__ uint16_t half(int64_t b, int j) const {
-        return (uint16_t) (byte(b, j) | (byte(b, j + 1) << 8));
-    }
-};
+// the row's natural bytes are staged in LDS, kGetRowsBlocks blocks at a time: each R32 unit of the
+// row (16 bytes at ((b U + u) rs + lane) 16 of its area, or a 2-byte half at (b rs + lane) 2) is
+// one load; then every element is dequantized from LDS with the dequantizer's formula
+constexpr int kGetRowsBlocks = 64;
 
 template <int DT>
 __global__ __launch_bounds__(256) void k_get_rows(GetRowsArgs a) {
+    constexpr int BS = DT == Q4_K || DT == Q6_K ? 256 : 32;
+    constexpr int BB = DT == Q4_0 ? 18 : DT == Q8_0 ? 34 : DT == Q4_K ? 144 : 210;
+    __shared__ __attribute__((aligned(16))) uint8_t nat[kGetRowsBlocks * BB];
     const int64_t row = blockIdx.x;
     const int64_t c = row / (a.n0 * a.n1), rem = row - c * a.n0 * a.n1, bi = rem / a.n0, ai = rem - bi * a.n0;
     int64_t r = a.ids[ai * a.i_s0 + bi * a.i_s1 + c * a.i_s2];
     r = r < 0 ? 0 : (r >= a.M ? a.M - 1 : r); // out-of-range rows read the nearest row
-    R32Row rr;
-    rr.slice = a.w + (uint64_t) bi * a.w_s2 + (uint64_t) c * a.w_s3;
-    rr.M = a.M;
-    rr.nb = a.nb;
-    rr.g0 = r & ~(int64_t) 31;
-    rr.rs = a.M - rr.g0 < 32 ? a.M - rr.g0 : 32;
-    rr.lane = r - rr.g0;
-    rr.ar = a.ar;
+    const uint8_t * slice = a.w + (uint64_t) bi * a.w_s2 + (uint64_t) c * a.w_s3;
+    const int64_t g0 = r & ~(int64_t) 31;
+    const int64_t rs = a.M - g0 < 32 ? a.M - g0 : 32, lane = r - g0;
     float * y = a.y + ai * a.y_s1 + bi * a.y_s2 + c * a.y_s3;
-    for (int64_t e = threadIdx.x; e < a.K; e += blockDim.x) {
-        float v;
-        if (DT == Q4_0) {
-            const int64_t b = e / 32;
-            const int i = (int) (e % 32);
-            const float d = h2f(rr.half(b, 0));
-            const int q = rr.byte(b, 2 + (i & 15));
-            v = (float) ((i < 16 ? (q & 0x0F) : (q >> 4)) - 8) * d;
-        } else if (DT == Q8_0) {
-            const int64_t b = e / 32;
-            v = (float) (int8_t) rr.byte(b, 2 + (int) (e % 32)) * h2f(rr.half(b, 0));
-        } else if (DT == Q4_K) {
-            const int64_t b = e / 256;
-            const int i = (int) (e % 256), cc = i / 64, l = i % 32, hi = (i % 64) >= 32;
-            uint8_t sb[12];
-            for (int k = 0; k < 12; ++k) sb[k] = rr.byte(b, 4 + k);
-            uint8_t sc, mn;
-            k4_scale_min(2 * cc + hi, sb, &sc, &mn);
-            const float d1 = h2f(rr.half(b, 0)) * (float) sc;
-            const float m1 = h2f(rr.half(b, 2)) * (float) mn;
-            const int q = rr.byte(b, 16 + 32 * cc + l);
-            v = d1 * (float) (hi ? (q >> 4) : (q & 0x0F)) - m1;
-        } else {
-            const int64_t b = e / 256;
-            const int i = (int) (e % 256), h = i / 128, rq = (i % 128) / 32, l = i % 32;
-            const uint8_t qh = rr.byte(b, 128 + 32 * h + l);
-            const int lowq = (rq & 1) ? rr.byte(b, 64 * h + l + 32) : rr.byte(b, 64 * h + l);
-            const int nib = rq < 2 ? (lowq & 0x0F) : (lowq >> 4);
-            const int q = (nib | (((qh >> (2 * rq)) & 3) << 4)) - 32;
-            const int8_t sc = (int8_t) rr.byte(b, 192 + 8 * h + 2 * rq + l / 16);
-            v = h2f(rr.half(b, 208)) * (float) sc * (float) q;
+    for (int64_t b0 = 0; b0 < a.nb; b0 += kGetRowsBlocks) {
+        const int nblk = (int) min<int64_t>(kGetRowsBlocks, a.nb - b0);
+        uint64_t before = 0;
+        for (int k = 0; k < a.ar.na; ++k) {
+            const int src = a.ar.src[k], len = a.ar.len[k];
+            const uint8_t xr = a.ar.xr[k];
+            const uint8_t * area = slice + (uint64_t) a.M * (uint64_t) a.nb * before;
+            if (len == 2) {
+                for (int t = threadIdx.x; t < nblk; t += blockDim.x) {
+                    const uint8_t * p = area + (uint64_t) g0 * a.nb * 2 + ((uint64_t) (b0 + t) * rs + lane) * 2;
+                    nat[t * BB + src] = p[0];
+                    nat[t * BB + src + 1] = p[1];
+                }
+            } else {
+                const int U = len / 16;
+                for (int t = threadIdx.x; t < nblk * U; t += blockDim.x) {
+                    const int bl = t / U, u = t - bl * U;
+                    const uint4 v = *reinterpret_cast<const uint4 *>(area + (uint64_t) g0 * a.nb * len +
+                                                                        (((uint64_t) (b0 + bl) * U + u) * rs + lane) * 16);
+                    const uint32_t m = xr * 0x01010101u;
+                    const uint32_t w[4] = {v.x ^ m, v.y ^ m, v.z ^ m, v.w ^ m};
+                    uint8_t * d = nat + bl * BB + src + 16 * u; // natural offsets are not 4-aligned in general
+                    for (int q = 0; q < 16; ++q) d[q] = (uint8_t) (w[q >> 2] >> (8 * (q & 3)));
+                }
+            }
+            before += (uint64_t) len;
         }
-        y[e] = v;
+        __syncthreads();
+        for (int e = threadIdx.x; e < nblk * BS; e += blockDim.x) y[b0 * BS + e] = deq_elem<DT>(nat + (e / BS) * BB, e % BS);
+        __syncthreads();
     }
 }
 
