@@ -35,7 +35,7 @@ import scrapgpulibrary_amd as sg  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the dominant kernel, measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-# runs of this script (scaled by the counters' reading for a copy of known size); written by the
+# profiling run (the FETCH_SIZE and WRITE_SIZE commands are recorded in the file itself)
 # profiling run, see DESIGN.md
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_matvec_decode_token.json")
 F16_PEAK_TFLOPS = 2500.0

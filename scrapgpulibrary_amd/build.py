@@ -19,7 +19,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall", "-Wno-unused-function",
           "-I", os.path.join(ROOT, "include"), "-I", CSRC]
-# device flags: gfx950 only; packed-fp32 instruction selection disabled (GPU rules)
+# device flags: gfx950 only; packed-fp32 instruction selection disabled (some packed fp32 forms
+# have given wrong results on these machines)
 DEVICE = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-munsafe-fp-atomics"]
 
 SOURCES = [

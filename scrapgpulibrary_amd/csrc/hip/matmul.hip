@@ -177,8 +177,14 @@ template <> struct PFmt<Q4_K> {
     struct Raw {
         uint4 q0, q1, hd;
     };
+    // s: scale of the stage's two sub-blocks; o: their offsets (the exact form); n = -1024 s
+    // (exact in f16) for the single-fma form; om: the offsets times 32 as an f16 pair, the lane's
+    // two entries of the offset MFMA; big: a scale or offset too large for the single-fma form.
+    // prep(.., g) returns the factors of the row scaled by the power of two g (see k_matmul).
     struct Sc {
-        f16x2 s0, o0, s1, o1;
+        f16x2 s0, o0, s1, o1, n0, n1;
+        uint32_t om;
+        bool big;
     };
     uint32_t qo, ho, u;
     int h;
@@ -193,18 +199,45 @@ template <> struct PFmt<Q4_K> {
         const uint32_t q = mad24((uint32_t) s * 4, u, qo);
         return Raw{load16(w + q), load16(w + q + u), load16(w + mad24((uint32_t) (s >> 1), u, ho))};
     }
-    __device__ Sc prep(const Raw & r, int64_t s) const {
+    __device__ Sc prep(const Raw & r, int64_t s, float g = 1.0f) const {
         const int c = 2 * (int) (s & 1) + h;
-        const float d = half_bits(r.hd.x), dmin = half_bits(r.hd.x >> 16);
+        const float d = g * half_bits(r.hd.x), dmin = g * half_bits(r.hd.x >> 16);
         float sc0, m0, sc1, m1;
         k4_scale_min(r.hd, 2 * c, sc0, m0);
         k4_scale_min(r.hd, 2 * c + 1, sc1, m1);
-        return Sc{h2(d * sc0), h2(-(dmin * m0)), h2(d * sc1), h2(-(dmin * m1))};
+        const float fs0 = d * sc0, fs1 = d * sc1, fo0 = -32.0f * dmin * m0, fo1 = -32.0f * dmin * m1;
+        Sc r0;
+        r0.s0 = h2(fs0);
+        r0.s1 = h2(fs1);
+        r0.o0 = h2(-(dmin * m0));
+        r0.o1 = h2(-(dmin * m1));
+        const f16x2 k = f16x2{(_Float16) -1024.0f, (_Float16) -1024.0f};
+        r0.n0 = r0.s0 * k;
+        r0.n1 = r0.s1 * k;
+        r0.om = __builtin_bit_cast(uint32_t, (f16x2{(_Float16) fo0, (_Float16) fo1}));
+        r0.big = !(__builtin_fabsf(fs0) < 32.0f && __builtin_fabsf(fs1) < 32.0f && __builtin_fabsf(fo0) < 32768.0f && __builtin_fabsf(fo1) < 32768.0f);
+        return r0;
     }
+    // exact form: s (c + bias) + o per pair (low nibbles: s0, o0; high nibbles: s1, o1)
     __device__ static f16x8 bop(const Raw & r, const Sc & c, int t) {
         const uint4 & q = (t & 3) < 2 ? r.q0 : r.q1;
         const uint32_t w0 = (t & 1) ? q.z : q.x, w1 = (t & 1) ? q.w : q.y;
         return t < 4 ? nib8<false>(w0, w1, (_Float16) 0.0f, c.s0, c.o0) : nib8<true>(w0, w1, (_Float16) 0.0f, c.s1, c.o1);
+    }
+    // single-fma form: fma(1024 + c, s, -1024 s) = s c with one rounding (the addend is exact
+    // while |s| < 64); a high nibble arrives as 1024 + 16 c and gives 16 s c, which pairs with x
+    // stored divided by 16 at those positions. The offsets go through the offset MFMA instead.
+    __device__ static f16x8 bop_fast(const Raw & r, const Sc & c, int t) {
+        const uint4 & q = (t & 3) < 2 ? r.q0 : r.q1;
+        const uint32_t w0 = (t & 1) ? q.z : q.x, w1 = (t & 1) ? q.w : q.y;
+        const uint32_t mask = t < 4 ? 0x000F000Fu : 0x00F000F0u;
+        const f16x2 sc = t < 4 ? c.s0 : c.s1, nb = t < 4 ? c.n0 : c.n1;
+        uint4 v;
+        v.x = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(as_h2(codes2(w0, mask)), sc, nb));
+        v.y = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(as_h2(codes2(w0 >> 8, mask)), sc, nb));
+        v.z = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(as_h2(codes2(w1, mask)), sc, nb));
+        v.w = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(as_h2(codes2(w1 >> 8, mask)), sc, nb));
+        return __builtin_bit_cast(f16x8, v);
     }
     __device__ static int chunk(int h, int t) {
         return 8 * h + t;
@@ -371,6 +404,8 @@ struct MmArgs {
     const uint16_t * xb; // f16 activations [slices][N][K], each row scaled (k_x_to_f16)
     const float * xs;    // [slices][N]: the factor that undoes a row's scaling
     float * part;        // split-K partial sums [split][slices][N][M] (split > 1)
+    const uint16_t * xsum; // Q4_K: per token, the f16 sums / 32 of its 32-element sub-blocks (k_x_to_f16)
+    int64_t xsum_row;    // halves per token row of xsum (16 per 512 elements of K)
     int64_t tiles_m, tiles_n;
     int64_t stages;      // stages of K (BK elements each)
     int split;           // work-groups along K per tile
@@ -382,39 +417,57 @@ __device__ __forceinline__ int xsw(int n, int c) {
 }
 
 // the x tile of one stage: BN tokens x 16 chunks; thread p loads chunk p % 16 of tokens
-// p / 16 + 16 i (i < BN / 16): one 32-bit element offset, LDS slot and row mask cover all of them
+// p / 16 + 16 i (i < BN / 16). Every load is unconditional, so that the compiler's wait counting
+// stays exact (a load under a branch makes it wait for all loads in flight): tokens past N read
+// token N - 1 (their products land in outputs that are never stored), and chunks past K read the
+// row's last chunk and are zeroed when stored to LDS (the weights there are zero as well, but
+// x could hold an infinity)
 template <int BN>
 struct XTile {
     static constexpr int NP = BN * kChunks / kThreads;
-    uint32_t off;  // element offset of (token p / 16, chunk p % 16) in the slice's x rows
-    uint32_t step; // 16 tokens
-    uint32_t kc;   // element offset of the chunk inside a stage
+    uint32_t off;     // byte offset of (token p / 16, chunk p % 16) in the slice's x rows
+    uint32_t last;    // the same for token N - 1 (tokens past N read it)
+    uint32_t step;    // 16 tokens
+    uint32_t kc;      // element offset of the chunk inside a stage
     int dst;
-    uint32_t ok;   // bit i: token p / 16 + 16 i < N
+    bool tail;        // the last load's stage reaches past K (wave-uniform)
+    bool zero;        // ... and this thread's chunk lies past K
     uint4 v[NP];
     __device__ void init(int64_t N, int64_t K, int64_t n0) {
         const int p = threadIdx.x;
         kc = 8 * (p & 15);
-        off = (uint32_t) ((n0 + (p >> 4)) * K) + kc;
-        step = (uint32_t) (16 * K);
         dst = xsw(p >> 4, p & 15); // token + 16 i keeps the swizzle: slot dst + 16 i rows
-        ok = 0;
-#pragma unroll
-        for (int i = 0; i < NP; ++i) ok |= (n0 + (p >> 4) + 16 * i < N ? 1u : 0u) << i;
+        off = 2 * ((uint32_t) ((n0 + (p >> 4)) * K) + kc);
+        last = 2 * ((uint32_t) ((N - 1) * K) + kc);
+        step = (uint32_t) (32 * K);
+        tail = zero = false;
     }
-    // stage starting at element k0; `full` when all BK elements lie inside K
-    __device__ void load(const uint16_t * xb, int64_t k0, int64_t K, bool full) {
+    // the stage starting at element k0
+    // (32-bit byte offsets from the slice's base: one scalar base, no 64-bit address math)
+    __device__ void load(const uint16_t * xb, int64_t k0, int64_t K) {
+        tail = k0 + BK > K;
+        zero = k0 + kc >= K;
+        const uint32_t k = 2 * (zero ? (uint32_t) (K - 8) - kc : (uint32_t) k0);
+        const uint8_t * base = reinterpret_cast<const uint8_t *>(xb);
 #pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            const bool in = ((ok >> i) & 1u) && (full || k0 + kc < K);
-            v[i] = in ? *reinterpret_cast<const uint4 *>(xb + (off + i * step + (uint32_t) k0)) : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < NP; ++i) v[i] = *reinterpret_cast<const uint4 *>(base + (min(off + i * step, last) + k));
+    }
+    __device__ void store(uint16_t * X) {
+        if (tail) { // the last stage of a K that is not a multiple of the stage
+#pragma unroll
+            for (int i = 0; i < NP; ++i) v[i] = zero ? make_uint4(0, 0, 0, 0) : v[i];
         }
-    }
-    __device__ void store(uint16_t * X) const {
 #pragma unroll
         for (int i = 0; i < NP; ++i) *reinterpret_cast<uint4 *>(X + dst + i * 16 * BK) = v[i];
     }
 };
+
+// the B fragment of k-step t in the single-fma form (FAST: Q4_K) or the exact form (the others)
+template <bool FAST, class F>
+__device__ __forceinline__ f16x8 bop_of(const typename F::Raw & r, const typename F::Sc & c, int t) {
+    if constexpr (FAST) return F::bop_fast(r, c, t);
+    else return F::bop(r, c, t);
+}
 
 // work-groups per CU that the register file (and, at BN = 128, the LDS) holds
 constexpr int occupancy_of(int dt, int bn, int rg) {
@@ -454,6 +507,21 @@ __global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(M
 #pragma unroll
     for (int t = 0; t < 8; ++t) aoff[t] = xsw(j, F::chunk(h, t));
 
+    // Q4_K: the sub-block offsets o (the "min" term) are not folded into the B pairs but added by
+    // one extra MFMA per 4 stages (2 blocks = 16 sub-blocks): A = the tokens' sub-block sums of x,
+    // B = 32 o of the rows' sub-blocks. Lane (j, h) contributes the offsets of the two sub-blocks
+    // it dequantizes each stage (dword s % 4 of bm); the xsum rows are ordered to match.
+    constexpr bool kOff = DT == Q4_K;
+    uint32_t bm[RG][4];
+    f16x8 asum[NF];
+    uint32_t soff[NF];
+#pragma unroll
+    for (int i = 0; i < RG; ++i)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) bm[i][d] = 0u;
+#pragma unroll
+    for (int q = 0; q < NF; ++q) soff[q] = (uint32_t) (((uint64_t) sl * N + min<int64_t>(n0 + 32 * q + j, N - 1)) * L.xsum_row) + 8 * h;
+
     f32x16 acc[RG][NF];
 #pragma unroll
     for (int i = 0; i < RG; ++i)
@@ -463,25 +531,66 @@ __global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(M
             for (int v = 0; v < 16; ++v) acc[i][q][v] = 0.0f;
 
     // one stage: MFMAs over the x tile in LDS with the weights cw (row groups of the wave);
-    // meanwhile stage s + 1 is loaded into nw and the x registers
-    auto stage = [&](int64_t s, const RawSet & cw, RawSet & nw) __attribute__((always_inline)) {
-        const bool more = s + 1 < s1;
-        if (more) {
+    // meanwhile the weights of stage s + 1 are loaded into nw and the x tile of stage s + XD into
+    // xl, while xn (the x tile of stage s + 1) goes to the other LDS buffer at the end. XD = 2
+    // (two register sets, xn loaded a stage earlier) where the registers allow it, else 1 (xl
+    // and xn are one set)
+    constexpr int XD = BN == 64 ? 2 : 1;
+    auto stage = [&](int64_t s, const RawSet & cw, RawSet & nw, XTile<BN> & xn, XTile<BN> & xl) __attribute__((always_inline)) {
+        // past the split's last stage the loads repeat it (unused): no load sits under a branch.
+        // The x sums of this stage's group come first: waiting for them waits for nothing newer.
+        if constexpr (kOff) {
 #pragma unroll
-            for (int i = 0; i < RG; ++i) nw.r[i] = f[i].load(w, s + 1);
-            xt.load(xb, (s + 1) * BK, K, (s + 1) * BK + BK <= K);
+            for (int q = 0; q < NF; ++q)
+                asum[q] = *reinterpret_cast<const f16x8 *>(reinterpret_cast<const uint8_t *>(L.xsum) + 2 * (soff[q] + (uint32_t) (s >> 2) * 16));
         }
+        const int64_t sn = min(s + 1, s1 - 1), sx = min(s + XD, s1 - 1);
+#pragma unroll
+        for (int i = 0; i < RG; ++i) nw.r[i] = f[i].load(w, sn);
+        xl.load(xb, sx * BK, K);
         const uint16_t * X = lds_mm + ((s - s0) & 1) * (BN * BK);
         typename F::Sc sc[RG];
 #pragma unroll
         for (int i = 0; i < RG; ++i) sc[i] = f[i].prep(cw.r[i], s);
+        // Q4_K, a row whose stage has a scale or offset too large for the single-fma form (rare:
+        // weights in the hundreds): the row's factors are scaled by g = 2^-11 and its
+        // accumulators by g for the stage (by 1 / g after it), and the stage's offsets are added
+        // at once at that scale. Both lanes of a row (j, j + 32) agree on g; the branches are
+        // wave-uniform and hold no loads.
+        bool rare = false;
+        float g = 1.0f;
+        const int d = (int) (s & 3);
+        if constexpr (kOff) {
+            bool big = false;
+#pragma unroll
+            for (int i = 0; i < RG; ++i) big = big || sc[i].big;
+            rare = __builtin_amdgcn_ballot_w64(big) != 0;
+            if (rare) {
+                // the row's flag: either lane of it (the shuffle runs in every lane)
+                const int partner = __shfl_xor((int) big, 32);
+                g = big || partner != 0 ? 0.00048828125f : 1.0f;
+#pragma unroll
+                for (int i = 0; i < RG; ++i) {
+                    sc[i] = f[i].prep(cw.r[i], s, g);
+                    // the group's pending offsets first, at the unscaled level
+                    const f16x8 bo = __builtin_bit_cast(f16x8, make_uint4(bm[i][0], bm[i][1], bm[i][2], bm[i][3]));
+#pragma unroll
+                    for (int q = 0; q < NF; ++q) {
+                        acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(asum[q], bo, acc[i][q], 0, 0, 0);
+                        acc[i][q] *= g;
+                    }
+#pragma unroll
+                    for (int dd = 0; dd < 4; ++dd) bm[i][dd] = 0u;
+                }
+            }
+        }
         // software pipeline over the 8 k-steps: the A reads and B dequantization of step t + 1
         // are issued while the MFMAs of step t run
         f16x8 a[2][NF], b[2][RG];
 #pragma unroll
         for (int q = 0; q < NF; ++q) a[0][q] = *reinterpret_cast<const f16x8 *>(X + aoff[0] + q * 32 * BK);
 #pragma unroll
-        for (int i = 0; i < RG; ++i) b[0][i] = F::bop(cw.r[i], sc[i], 0);
+        for (int i = 0; i < RG; ++i) b[0][i] = bop_of<kOff, F>(cw.r[i], sc[i], 0);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const int c = t & 1, n = c ^ 1;
@@ -496,24 +605,66 @@ __global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(M
                 for (int i = 0; i < RG; ++i) acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c][q], b[c][i], acc[i][q], 0, 0, 0);
             if (t < 7) {
 #pragma unroll
-                for (int i = 0; i < RG; ++i) b[n][i] = F::bop(cw.r[i], sc[i], t + 1);
+                for (int i = 0; i < RG; ++i) b[n][i] = bop_of<kOff, F>(cw.r[i], sc[i], t + 1);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (more) xt.store(lds_mm + ((s + 1 - s0) & 1) * (BN * BK));
+        if constexpr (kOff) {
+            // this stage's offsets (dword s % 4 of the offset operand); the offset MFMA runs when
+            // the group of 4 stages or the split ends, or at once in a rare stage
+#pragma unroll
+            for (int i = 0; i < RG; ++i) {
+                const uint32_t v = sc[i].om;
+                bm[i][0] = d == 0 ? v : bm[i][0];
+                bm[i][1] = d == 1 ? v : bm[i][1];
+                bm[i][2] = d == 2 ? v : bm[i][2];
+                bm[i][3] = d == 3 ? v : bm[i][3];
+            }
+            if (rare || d == 3 || s + 1 == s1) {
+#pragma unroll
+                for (int i = 0; i < RG; ++i) {
+                    const f16x8 bo = __builtin_bit_cast(f16x8, make_uint4(bm[i][0], bm[i][1], bm[i][2], bm[i][3]));
+#pragma unroll
+                    for (int q = 0; q < NF; ++q) acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(asum[q], bo, acc[i][q], 0, 0, 0);
+#pragma unroll
+                    for (int dd = 0; dd < 4; ++dd) bm[i][dd] = 0u;
+                }
+            }
+            if (rare) {
+                const float ig = 1.0f / g;
+#pragma unroll
+                for (int i = 0; i < RG; ++i)
+#pragma unroll
+                    for (int q = 0; q < NF; ++q) acc[i][q] *= ig;
+            }
+        }
+        if (s + 1 < s1) xn.store(lds_mm + ((s + 1 - s0) & 1) * (BN * BK));
         __syncthreads();
     };
     RawSet ra{}, rb{};
-    if (s0 < s1) {
+    XTile<BN> xt2 = xt;
+    // every split has at least one stage (the host keeps split <= stages)
 #pragma unroll
-        for (int i = 0; i < RG; ++i) ra.r[i] = f[i].load(w, s0);
-        xt.load(xb, s0 * BK, K, s0 * BK + BK <= K);
-        xt.store(lds_mm);
-    }
+    for (int i = 0; i < RG; ++i) ra.r[i] = f[i].load(w, s0);
+    xt.load(xb, s0 * BK, K);
+    if constexpr (XD == 2) xt2.load(xb, min(s0 + 1, s1 - 1) * BK, K);
+    xt.store(lds_mm);
     __syncthreads();
-    for (int64_t s = s0; s < s1; s += 2) {
-        stage(s, ra, rb);
-        if (s + 1 < s1) stage(s + 1, rb, ra);
+    // pairs of stages, then an odd last one outside the loop (a stage under a branch inside the
+    // loop would end every iteration with a wait for all loads in flight)
+    int64_t s = s0;
+    for (; s + 1 < s1; s += 2) {
+        if constexpr (XD == 2) {
+            stage(s, ra, rb, xt2, xt);
+            stage(s + 1, rb, ra, xt, xt2);
+        } else {
+            stage(s, ra, rb, xt, xt);
+            stage(s + 1, rb, ra, xt, xt);
+        }
+    }
+    if (s < s1) {
+        if constexpr (XD == 2) stage(s, ra, rb, xt2, xt);
+        else stage(s, ra, rb, xt, xt);
     }
     // acc[i][q][v], lane (j, h): token n0 + 32q + 8 (v / 4) + 4h + v % 4, weight row m0 + 32i + j
     const int64_t slices = L.a.ne12 * L.a.ne13;
@@ -529,15 +680,17 @@ __global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(M
     const float * xs = L.xs + (uint64_t) sl * N;
 #pragma unroll
     for (int q = 0; q < NF; ++q) {
+        float u[16]; // the fragment's row factors, loaded together (tokens past N read N - 1)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) u[v] = xs[min<int64_t>(n0 + 32 * q + 8 * (v >> 2) + 4 * h + (v & 3), N - 1)];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int64_t n = n0 + 32 * q + 8 * (v >> 2) + 4 * h + (v & 3);
             if (n >= N) continue;
-            const float u = xs[n];
 #pragma unroll
             for (int i = 0; i < RG; ++i) {
                 const int64_t m = m0 + 32 * i + j;
-                if (m < M) y[n * ys1 + m] = acc[i][q][v] * u;
+                if (m < M) y[n * ys1 + m] = acc[i][q][v] * u[v];
             }
         }
     }
@@ -580,8 +733,12 @@ __global__ __launch_bounds__(256) void k_split_reduce(MmArgs L) {
 // the row's maximum; xs[row] = 2^-e undoes it on the products. Inside each group of 4 elements the
 // order is 0 2 1 3, the order of the weight pairs the matmul builds. VEC: rows 16-byte aligned.
 // The first kCached groups of 8 elements per thread stay in registers between the two passes.
-template <bool VEC>
-__global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, float * xs) {
+// Q4K (the single-fma weight form): elements 32..63 of every 64 (the high nibbles of a Q4_K group)
+// are stored divided by 16 more, and xsum gets the row's 32-element sub-block sums (of the scaled
+// x, times 1/32 so that they fit f16), 16 per 512 elements in the order the matmul's lanes hold
+// the sub-blocks: position 8 h + e <- sub-block 4 (e / 2) + 2 h + e % 2; missing ones are zero.
+template <bool VEC, bool Q4K>
+__global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, float * xs, uint16_t * xsum, int64_t xsum_row) {
     constexpr int kCached = 6; // K <= 12288 is read once
     const int64_t row = blockIdx.x, sl = row / a.N, n = row - sl * a.N;
     const int64_t i2 = sl % a.ne12, i3 = sl / a.ne12;
@@ -599,8 +756,26 @@ __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, floa
     };
     auto store8 = [&](int64_t k, const float * v, int e2) {
         float s[8];
+        float sum = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s[e] = ldexpf(v[e], e2);
+        for (int e = 0; e < 8; ++e) {
+            s[e] = ldexpf(v[e], e2);
+            sum += s[e];
+        }
+        if constexpr (Q4K) {
+            // the 4 threads of a 32-element sub-block are lanes 4m .. 4m + 3 of one wave
+            sum += __shfl_xor(sum, 1);
+            sum += __shfl_xor(sum, 2);
+            if ((threadIdx.x & 3) == 0) {
+                const int64_t jb = k >> 5, jj = jb & 15;
+                const int64_t pos = (jb >> 4) * 16 + 8 * ((jj >> 1) & 1) + 2 * (jj >> 2) + (jj & 1);
+                xsum[row * xsum_row + pos] = __half_as_ushort(__float2half(sum * 0.03125f));
+            }
+            if (k & 32) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s[e] *= 0.0625f;
+            }
+        }
         const f16x2 p0 = __builtin_convertvector((f32x2{s[0], s[2]}), f16x2), p1 = __builtin_convertvector((f32x2{s[1], s[3]}), f16x2);
         const f16x2 p2 = __builtin_convertvector((f32x2{s[4], s[6]}), f16x2), p3 = __builtin_convertvector((f32x2{s[5], s[7]}), f16x2);
         *reinterpret_cast<uint4 *>(op + k) = make_uint4(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
@@ -647,6 +822,12 @@ __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, floa
         load8(k, v);
         store8(k, v, e2);
     }
+    if constexpr (Q4K) {
+        for (int64_t jb = a.K / 32 + threadIdx.x; jb < xsum_row; jb += 256) {
+            const int64_t jj = jb & 15;
+            xsum[row * xsum_row + (jb >> 4) * 16 + 8 * ((jj >> 1) & 1) + 2 * (jj >> 2) + (jj & 1)] = 0;
+        }
+    }
 }
 
 // Tile shape and work-groups along K per tile. A work-group is 4 waves; each wave owns RG groups
@@ -689,13 +870,22 @@ void * kernel_of(const MmConfig & c) {
     return c.bn == 64 ? (void *) k_matmul<DT, 64, 2> : (void *) k_matmul<DT, 128, 2>;
 }
 
-// scratch: x as f16 [slices][N][K] | row factors [slices][N] | split-K partials
+// scratch: x as f16 [slices][N][K] | row factors [slices][N] | Q4_K sub-block sums
+// [slices][N][xsum_row] | split-K partials
 size_t xs_offset(const MatArgs & a) {
     return ((size_t) a.N * (size_t) a.K * (size_t) (a.ne12 * a.ne13) * sizeof(uint16_t) + 255) / 256 * 256;
 }
 
-size_t part_offset(const MatArgs & a) {
+int64_t xsum_row_of(const MatArgs & a) {
+    return a.dtype == Q4_K ? (a.K + 511) / 512 * 16 : 0;
+}
+
+size_t xsum_offset(const MatArgs & a) {
     return xs_offset(a) + ((size_t) a.N * (size_t) (a.ne12 * a.ne13) * sizeof(float) + 255) / 256 * 256;
+}
+
+size_t part_offset(const MatArgs & a) {
+    return xsum_offset(a) + ((size_t) a.N * (size_t) (a.ne12 * a.ne13) * (size_t) xsum_row_of(a) * sizeof(uint16_t) + 255) / 256 * 256;
 }
 
 size_t part_bytes(const MatArgs & a, int split) {
@@ -714,11 +904,21 @@ hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count
     const int64_t rows = a.N * a.ne12 * a.ne13;
     float * xs = reinterpret_cast<float *>(scratch + xs_offset(a));
     const bool vec = (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && a.x_s1 % 4 == 0 && a.x_s2 % 4 == 0 && a.x_s3 % 4 == 0;
+    uint16_t * xsum = reinterpret_cast<uint16_t *>(scratch + xsum_offset(a));
+    const int64_t xsum_row = xsum_row_of(a);
     if (rows > 0x7fffffff) return hipErrorInvalidValue;
-    if (vec)
-        hipLaunchKernelGGL(k_x_to_f16<true>, dim3((unsigned) rows), dim3(256), 0, stream, a, xb, xs);
-    else
-        hipLaunchKernelGGL(k_x_to_f16<false>, dim3((unsigned) rows), dim3(256), 0, stream, a, xb, xs);
+    const dim3 xg((unsigned) rows);
+    if (a.dtype == Q4_K) {
+        if (vec)
+            hipLaunchKernelGGL((k_x_to_f16<true, true>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
+        else
+            hipLaunchKernelGGL((k_x_to_f16<false, true>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
+    } else {
+        if (vec)
+            hipLaunchKernelGGL((k_x_to_f16<true, false>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
+        else
+            hipLaunchKernelGGL((k_x_to_f16<false, false>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     MmArgs L;
@@ -726,6 +926,8 @@ hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count
     L.xb = xb;
     L.xs = xs;
     L.part = reinterpret_cast<float *>(scratch + part_offset(a));
+    L.xsum = xsum;
+    L.xsum_row = xsum_row;
     const MmConfig cfg = config_of(a, cu_count);
     const int BN = cfg.bn;
     L.tiles_m = (a.M + 128 * cfg.rg - 1) / (128 * cfg.rg);

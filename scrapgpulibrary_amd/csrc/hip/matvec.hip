@@ -549,13 +549,13 @@ __device__ __forceinline__ Row row_of(const MvArgs & A, int64_t tile, uint64_t w
     const int j = tile >= A.tstart[1] ? (tile >= A.tstart[2] ? 2 : 1) : 0;
     const int64_t M = A.M[j];
     const int64_t m0 = (tile - A.tstart[j]) * R;
-    const int64_t g0 = m0 & ~(int64_t) 31;
-    const int rs = (int) min<int64_t>(32, M - g0);
 #pragma unroll
     for (int i = 0; i < RG; ++i) {
-        const int64_t m = m0 + r + 16 * i;
-        const int lr = m < M ? (int) (m - g0) : rs - 1;
-        f[i].init(A.w[j] + w_off, M, A.nb, g0, rs, lr, part);
+        // each 16-row group lies in one R32 group (48-row tiles straddle two); rows past M
+        // read the last row (their results are not stored)
+        const int64_t m = min(m0 + r + 16 * i, M - 1);
+        const int64_t g0 = m & ~(int64_t) 31;
+        f[i].init(A.w[j] + w_off, M, A.nb, g0, (int) min<int64_t>(32, M - g0), (int) (m - g0), part);
     }
     return Row{j, M, m0};
 }
@@ -592,7 +592,7 @@ __device__ __forceinline__ void reduce_store(const MvArgs & A, const Where & wh,
 // Burst form (one column, <= SPW steps per wave, one tile of 16 * RG rows per work-group): the wave
 // first loads its x range, then issues every weight load, and only then converts x.
 template <int DT, int RG, int W, int SPW>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2 && RG == 1 ? 6 : SPW <= 2 ? 5 : 4, 8))) void k_mvb(MvArgs A) {
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2 && RG == 1 ? 6 : SPW <= 2 && RG == 2 ? 5 : 4, 8))) void k_mvb(MvArgs A) {
     using F = Fmt<DT>;
     using Raw = typename F::Raw;
     extern __shared__ uint8_t lds[];
@@ -734,7 +734,7 @@ void * pick_burst_rg(int W, int spw) {
 
 template <int DT>
 void * pick_burst(int W, int spw, int rg) {
-    return rg == 2 ? pick_burst_rg<DT, 2>(W, spw) : pick_burst_rg<DT, 1>(W, spw);
+    return rg == 3 ? pick_burst_rg<DT, 3>(W, spw) : rg == 2 ? pick_burst_rg<DT, 2>(W, spw) : pick_burst_rg<DT, 1>(W, spw);
 }
 
 // streaming variants: W = 8 for one column, 4 for several
@@ -852,12 +852,14 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     if (kernel_name) *kernel_name = name_of(dt, nmat);
 
     // burst form (one column, K <= 64 steps): every wave's steps (<= 4) loaded at once, one tile
-    // per work-group. 32-row tiles (two row groups sharing each x operand) for large products,
-    // 16-row tiles otherwise (more work-groups). 2 steps per wave up to K = 32 steps, then 4.
+    // per work-group. 32- or 48-row tiles (two or three row groups sharing each x operand) for
+    // large products, 16-row tiles otherwise (more work-groups). 2 steps per wave up to K = 32 steps, then 4.
     if (nc == 1 && L.xvec && nst <= 64 && tuning("SCRAPGPU_HIP_MV_BURST", 1)) {
         // (the 32-row Q8_0 / Q6_K forms need more registers than 5 waves per SIMD leave them)
-        int rg = (dt == Q4_K || dt == Q4_0) && rows * slices >= (int64_t) 64 * cu_count ? 2 : 1;
-        if (const int fr = tuning("SCRAPGPU_HIP_MV_RG", 0)) rg = fr >= 2 ? 2 : 1;
+        // 48-row tiles once they give every CU two work-groups (one round at 4 waves per SIMD)
+        const bool q4 = dt == Q4_K || dt == Q4_0;
+        int rg = q4 && rows * slices >= (int64_t) 96 * cu_count ? 3 : q4 && rows * slices >= (int64_t) 64 * cu_count ? 2 : 1;
+        if (const int fr = tuning("SCRAPGPU_HIP_MV_RG", 0)) rg = fr >= 3 ? 3 : fr >= 2 ? 2 : 1;
         const int sp = nst <= 32 ? 2 : 4;
         int W = 4;
         while (W < 16 && (nst + W - 1) / W > sp) W *= 2;

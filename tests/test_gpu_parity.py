@@ -174,6 +174,29 @@ def test_prefill_mfma(hip, dtype, N):
     assert e <= 5e-5, f"NMSE {e:.3e}"
 
 
+@pytest.mark.parametrize("K", [2560, 2816])
+def test_prefill_q4k_large_scales_and_split_groups(hip, K):
+    """Q4_K prefill with rows whose sub-block scales (weights in the hundreds) or offsets (means
+    near -3000) are beyond the single-fma form, mixed with ordinary rows; K = 20 or 22 stages, so
+    the split-K halves start inside a group of 4 stages and K = 2816 ends in half a group. Every
+    row set meets the NMSE bound on its own."""
+    dev, st = hip
+    M, N = 200, 64
+    w = O.normal(K * M, 77, 0.0, 0.02).reshape(M, K)
+    w[0:10] *= 1e4                    # scales d * sc well above 32
+    w[20:30] += -3000.0               # offsets 32 * dmin * m well above 32768
+    w[40:45, :256] *= 1e4             # one large block in an ordinary row
+    w[46:50, :32] *= 1e4              # one large sub-block: the row's two lanes disagree
+    q = O.quantize(sg.Q4_K, w.reshape(-1))
+    x = O.normal(N * K, 78).reshape(N, K)
+    y = run_mul_mat(dev, st, sg.Q4_K, q, K, M, x)
+    ref = O.mul_mat(sg.Q4_K, q, K, M, x, threads=8)
+    assert np.all(np.isfinite(y))
+    for rows in (slice(0, 10), slice(20, 30), slice(40, 45), slice(46, 50), slice(50, M)):
+        e = nmse(y[:, rows], ref[:, rows])
+        assert e <= 5e-5, f"rows {rows}: NMSE {e:.3e}"
+
+
 @pytest.mark.parametrize("dtype", [sg.Q4_0, sg.Q4_K], ids=lambda d: sg.NAMES[d])
 @pytest.mark.parametrize("N", [1, 4, 33])
 def test_slices_broadcast_and_strides(hip, dtype, N):
