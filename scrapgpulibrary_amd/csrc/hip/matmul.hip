@@ -7,18 +7,21 @@
 //             row scaled by a power of two that puts its largest magnitude in [2^14, 2^15) (no
 //             f16 overflow, no precision lost to subnormals); the factor is undone on the products.
 //   GEMM      v_mfma_f32_32x32x16_f16 (the 32x32 tile sustains the chip's f16 rate; 16x16x32
-//             issues at about half of it). A work-group is 4 waves; wave w owns RG groups of 32
-//             weight rows and BN tokens and walks K in stages of 128.
+//             issues at about half of it). A work-group is W waves (4, or 12 = one per CU); wave w
+//             owns RG groups of 32 weight rows and BN tokens and walks K in stages of 128, the
+//             stages unrolled by 4 so that every position-dependent choice is static.
 //               * B operand (weights): lane (j, h) of a 32-row group holds row j, k-half h. Per
 //                 stage it loads the R32 units of row j that hold its 64 codes, and dequantizes 8
 //                 of them per k-step straight into f16 (see "weight codes" below). No weight goes
-//                 through LDS and every weight is dequantized once per work-group.
+//                 through LDS and every weight is dequantized once per work-group. Q4_K takes one
+//                 fma per f16 pair; its sub-block offsets enter through one extra MFMA per 4 stages.
 //               * A operand (activations): the BN x 128 f16 x tile of the stage, double-buffered in
 //                 LDS (XOR-swizzled 16-byte chunks); one ds_read_b128 per lane per MFMA, shared by
 //                 the wave's RG row groups. The k order inside a step is whatever the weight lanes
 //                 hold; the A reads follow it (chunk(h, t) below).
-//             The next stage's weights and x tile are loaded into registers while the current
-//             stage computes; one barrier per stage.
+//             The next stage's weights and the x tile two stages ahead (BN = 64) are loaded into
+//             registers while the current stage computes, every load outside branches; one
+//             barrier per stage.
 //   split-K   when the tiles alone leave CUs idle, K is split over work-groups that write partial
 //             sums to scratch; a reduction kernel adds them in split order (deterministic).
 #include "kernels.h"
@@ -26,6 +29,7 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 #include <mutex>
 #include <vector>
@@ -34,7 +38,6 @@ namespace sgk {
 namespace {
 
 constexpr int BK = 128;
-constexpr int kThreads = 256;
 constexpr int kChunks = BK / 8; // 16-byte chunks per LDS row of the x tile
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -416,18 +419,20 @@ __device__ __forceinline__ int xsw(int n, int c) {
     return (n * kChunks + (c ^ (n & 15))) * 8;
 }
 
-// the x tile of one stage: BN tokens x 16 chunks; thread p loads chunk p % 16 of tokens
-// p / 16 + 16 i (i < BN / 16). Every load is unconditional, so that the compiler's wait counting
+// the x tile of one stage: BN tokens x 16 chunks over the 64 W threads of the work-group; thread p
+// loads chunk p % 16 of tokens p / 16 + 4 W i (a thread whose token i lies past the tile repeats
+// its token 0: same data to the same LDS slot). Every load is unconditional, so that the compiler's wait counting
 // stays exact (a load under a branch makes it wait for all loads in flight): tokens past N read
 // token N - 1 (their products land in outputs that are never stored), and chunks past K read the
 // row's last chunk and are zeroed when stored to LDS (the weights there are zero as well, but
 // x could hold an infinity)
-template <int BN>
+template <int BN, int W>
 struct XTile {
-    static constexpr int NP = BN * kChunks / kThreads;
+    static constexpr int NP = (BN * kChunks + 64 * W - 1) / (64 * W);
+    static constexpr int TS = 4 * W; // tokens between a thread's loads
     uint32_t off;     // byte offset of (token p / 16, chunk p % 16) in the slice's x rows
     uint32_t last;    // the same for token N - 1 (tokens past N read it)
-    uint32_t step;    // 16 tokens
+    uint32_t step;    // TS tokens
     uint32_t kc;      // element offset of the chunk inside a stage
     int dst;
     bool tail;        // the last load's stage reaches past K (wave-uniform)
@@ -436,10 +441,10 @@ struct XTile {
     __device__ void init(int64_t N, int64_t K, int64_t n0) {
         const int p = threadIdx.x;
         kc = 8 * (p & 15);
-        dst = xsw(p >> 4, p & 15); // token + 16 i keeps the swizzle: slot dst + 16 i rows
+        dst = xsw(p >> 4, p & 15); // token + TS i (TS a multiple of 16) keeps the swizzle
         off = 2 * ((uint32_t) ((n0 + (p >> 4)) * K) + kc);
         last = 2 * ((uint32_t) ((N - 1) * K) + kc);
-        step = (uint32_t) (32 * K);
+        step = (uint32_t) (2 * TS * K);
         tail = zero = false;
     }
     // the stage starting at element k0
@@ -450,7 +455,10 @@ struct XTile {
         const uint32_t k = 2 * (zero ? (uint32_t) (K - 8) - kc : (uint32_t) k0);
         const uint8_t * base = reinterpret_cast<const uint8_t *>(xb);
 #pragma unroll
-        for (int i = 0; i < NP; ++i) v[i] = *reinterpret_cast<const uint4 *>(base + (min(off + i * step, last) + k));
+        for (int i = 0; i < NP; ++i) {
+            const uint32_t o = (threadIdx.x >> 4) + TS * i < BN ? off + i * step : off;
+            v[i] = *reinterpret_cast<const uint4 *>(base + (min(o, last) + k));
+        }
     }
     __device__ void store(uint16_t * X) {
         if (tail) { // the last stage of a K that is not a multiple of the stage
@@ -458,7 +466,7 @@ struct XTile {
             for (int i = 0; i < NP; ++i) v[i] = zero ? make_uint4(0, 0, 0, 0) : v[i];
         }
 #pragma unroll
-        for (int i = 0; i < NP; ++i) *reinterpret_cast<uint4 *>(X + dst + i * 16 * BK) = v[i];
+        for (int i = 0; i < NP; ++i) *reinterpret_cast<uint4 *>(X + ((threadIdx.x >> 4) + TS * i < BN ? dst + i * TS * BK : dst)) = v[i];
     }
 };
 
@@ -469,15 +477,19 @@ __device__ __forceinline__ f16x8 bop_of(const typename F::Raw & r, const typenam
     else return F::bop(r, c, t);
 }
 
-// work-groups per CU that the register file (and, at BN = 128, the LDS) holds
-constexpr int occupancy_of(int dt, int bn, int rg) {
-    return bn == 64 && rg == 1 ? (dt == Q6_K ? 2 : 3) : bn == 128 && rg == 2 ? 1 : 2;
+// work-groups of W waves per CU that the register file (and, at BN = 128, the LDS) holds
+constexpr int occupancy_of(int dt, int bn, int rg, int w = 4) {
+    return w == 12 ? 1 : bn == 64 && rg == 1 ? (dt == Q6_K ? 2 : 3) : bn == 128 && rg == 2 ? 1 : 2;
 }
 
-template <int DT, int BN, int RG>
-__global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(MmArgs L) {
+// W = 4: a work-group per SIMD quad, several per CU. W = 12: the CU's whole complement of 3 waves
+// per SIMD in one work-group (a tile of 384 rows): its waves keep in step at the stage barrier,
+// where separate work-groups on one CU drift apart (the oldest waves win the issue arbitration,
+// so the last work-group finishes alone with one wave per SIMD), and each x tile serves 3x the rows.
+template <int DT, int BN, int RG, int W>
+__global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(MmArgs L) {
     constexpr int NF = BN / 32; // token fragments per wave
-    constexpr int BMT = 128 * RG;
+    constexpr int BMT = 32 * RG * W;
     using F = PFmt<DT>;
     using Raw = typename F::Raw;
     struct RawSet {
@@ -494,13 +506,16 @@ __global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(M
     const uint8_t * w = L.a.w + (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
     const int64_t K = L.a.K, N = L.a.N, M = L.a.M, nb = L.a.nb;
     const int64_t m0 = tm * BMT + 32 * RG * wave, n0 = tn * BN;
-    const int64_t s0 = L.stages * split / L.split, s1 = L.stages * (split + 1) / L.split;
+    // splits cover whole groups of 4 stages (the host keeps split <= groups), so a stage's
+    // position in its group is (s - s0) % 4
+    const int64_t groups = (L.stages + 3) / 4;
+    const int64_t s0 = 4 * (groups * split / L.split), s1 = min(4 * (groups * (split + 1) / L.split), L.stages);
 
     F f[RG];
 #pragma unroll
     for (int i = 0; i < RG; ++i) f[i].init(M, nb, RowAddr(M, m0 + 32 * i + j), h);
     const uint16_t * xb = L.xb + (uint64_t) sl * N * K;
-    XTile<BN> xt;
+    XTile<BN, W> xt;
     xt.init(N, K, n0);
     // LDS element offsets of the lane's A fragments: k-step t, token fragment q at aoff[t] + 32 q rows
     int aoff[8];
@@ -536,10 +551,13 @@ __global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(M
     // (two register sets, xn loaded a stage earlier) where the registers allow it, else 1 (xl
     // and xn are one set)
     constexpr int XD = BN == 64 ? 2 : 1;
-    auto stage = [&](int64_t s, const RawSet & cw, RawSet & nw, XTile<BN> & xn, XTile<BN> & xl) __attribute__((always_inline)) {
+    // D = s % 4, a compile-time constant: the LDS buffer, the parity the formats' factors depend
+    // on and the offset-MFMA slot are static
+    auto stage = [&](auto dtag, int64_t s, const RawSet & cw, RawSet & nw, XTile<BN, W> & xn, XTile<BN, W> & xl) __attribute__((always_inline)) {
+        constexpr int D = decltype(dtag)::value;
         // past the split's last stage the loads repeat it (unused): no load sits under a branch.
-        // The x sums of this stage's group come first: waiting for them waits for nothing newer.
-        if constexpr (kOff) {
+        // The x sums of the group come first (waiting for them waits for nothing newer).
+        if constexpr (kOff && D == 0) {
 #pragma unroll
             for (int q = 0; q < NF; ++q)
                 asum[q] = *reinterpret_cast<const f16x8 *>(reinterpret_cast<const uint8_t *>(L.xsum) + 2 * (soff[q] + (uint32_t) (s >> 2) * 16));
@@ -548,10 +566,11 @@ __global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(M
 #pragma unroll
         for (int i = 0; i < RG; ++i) nw.r[i] = f[i].load(w, sn);
         xl.load(xb, sx * BK, K);
-        const uint16_t * X = lds_mm + ((s - s0) & 1) * (BN * BK);
+        const uint16_t * X = lds_mm + (D & 1) * (BN * BK);
+        const int64_t sp = (s & ~(int64_t) 3) | D; // = s, with its low bits visible to the compiler
         typename F::Sc sc[RG];
 #pragma unroll
-        for (int i = 0; i < RG; ++i) sc[i] = f[i].prep(cw.r[i], s);
+        for (int i = 0; i < RG; ++i) sc[i] = f[i].prep(cw.r[i], sp);
         // Q4_K, a row whose stage has a scale or offset too large for the single-fma form (rare:
         // weights in the hundreds): the row's factors are scaled by g = 2^-11 and its
         // accumulators by g for the stage (by 1 / g after it), and the stage's offsets are added
@@ -559,7 +578,6 @@ __global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(M
         // wave-uniform and hold no loads.
         bool rare = false;
         float g = 1.0f;
-        const int d = (int) (s & 3);
         if constexpr (kOff) {
             bool big = false;
 #pragma unroll
@@ -571,7 +589,7 @@ __global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(M
                 g = big || partner != 0 ? 0.00048828125f : 1.0f;
 #pragma unroll
                 for (int i = 0; i < RG; ++i) {
-                    sc[i] = f[i].prep(cw.r[i], s, g);
+                    sc[i] = f[i].prep(cw.r[i], sp, g);
                     // the group's pending offsets first, at the unscaled level
                     const f16x8 bo = __builtin_bit_cast(f16x8, make_uint4(bm[i][0], bm[i][1], bm[i][2], bm[i][3]));
 #pragma unroll
@@ -613,14 +631,8 @@ __global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(M
             // this stage's offsets (dword s % 4 of the offset operand); the offset MFMA runs when
             // the group of 4 stages or the split ends, or at once in a rare stage
 #pragma unroll
-            for (int i = 0; i < RG; ++i) {
-                const uint32_t v = sc[i].om;
-                bm[i][0] = d == 0 ? v : bm[i][0];
-                bm[i][1] = d == 1 ? v : bm[i][1];
-                bm[i][2] = d == 2 ? v : bm[i][2];
-                bm[i][3] = d == 3 ? v : bm[i][3];
-            }
-            if (rare || d == 3 || s + 1 == s1) {
+            for (int i = 0; i < RG; ++i) bm[i][D] = sc[i].om;
+            if (rare || D == 3 || s + 1 == s1) {
 #pragma unroll
                 for (int i = 0; i < RG; ++i) {
                     const f16x8 bo = __builtin_bit_cast(f16x8, make_uint4(bm[i][0], bm[i][1], bm[i][2], bm[i][3]));
@@ -638,11 +650,11 @@ __global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(M
                     for (int q = 0; q < NF; ++q) acc[i][q] *= ig;
             }
         }
-        if (s + 1 < s1) xn.store(lds_mm + ((s + 1 - s0) & 1) * (BN * BK));
+        if (s + 1 < s1) xn.store(lds_mm + ((D + 1) & 1) * (BN * BK));
         __syncthreads();
     };
     RawSet ra{}, rb{};
-    XTile<BN> xt2 = xt;
+    XTile<BN, W> xt2 = xt;
     // every split has at least one stage (the host keeps split <= stages)
 #pragma unroll
     for (int i = 0; i < RG; ++i) ra.r[i] = f[i].load(w, s0);
@@ -650,21 +662,27 @@ __global__ __launch_bounds__(kThreads, occupancy_of(DT, BN, RG)) void k_matmul(M
     if constexpr (XD == 2) xt2.load(xb, min(s0 + 1, s1 - 1) * BK, K);
     xt.store(lds_mm);
     __syncthreads();
-    // pairs of stages, then an odd last one outside the loop (a stage under a branch inside the
-    // loop would end every iteration with a wait for all loads in flight)
+    // groups of 4 stages, then the split's last 1..3 outside the loop (a stage under a branch
+    // inside the loop would end every iteration with a wait for all loads in flight)
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    XTile<BN, W> & xa = XD == 2 ? xt2 : xt; // x set of stages D = 0, 2 (the next tile's)
+    XTile<BN, W> & xc = xt;                 // of stages D = 1, 3
     int64_t s = s0;
-    for (; s + 1 < s1; s += 2) {
-        if constexpr (XD == 2) {
-            stage(s, ra, rb, xt2, xt);
-            stage(s + 1, rb, ra, xt, xt2);
-        } else {
-            stage(s, ra, rb, xt, xt);
-            stage(s + 1, rb, ra, xt, xt);
-        }
+    for (; s + 3 < s1; s += 4) {
+        stage(I0{}, s, ra, rb, xa, xc);
+        stage(I1{}, s + 1, rb, ra, xc, xa);
+        stage(I2{}, s + 2, ra, rb, xa, xc);
+        stage(I3{}, s + 3, rb, ra, xc, xa);
     }
     if (s < s1) {
-        if constexpr (XD == 2) stage(s, ra, rb, xt2, xt);
-        else stage(s, ra, rb, xt, xt);
+        stage(I0{}, s, ra, rb, xa, xc);
+        if (s + 1 < s1) {
+            stage(I1{}, s + 1, rb, ra, xc, xa);
+            if (s + 2 < s1) stage(I2{}, s + 2, ra, rb, xa, xc);
+        }
     }
     // acc[i][q][v], lane (j, h): token n0 + 32q + 8 (v / 4) + 4h + v % 4, weight row m0 + 32i + j
     const int64_t slices = L.a.ne12 * L.a.ne13;
@@ -837,6 +855,7 @@ __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, floa
 struct MmConfig {
     int bn, rg;
     int split;
+    int w; // waves per work-group: 4, or 12 (one work-group per CU, see k_matmul)
 };
 
 int env_int(const char * name, int dflt) {
@@ -849,7 +868,23 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
     static const int env_split = env_int("SCRAPGPU_HIP_MM_SPLIT", 0);
     const int64_t slices = a.ne12 * a.ne13;
     const int64_t stages = (a.K + BK - 1) / BK;
+    static const int env_w = env_int("SCRAPGPU_HIP_MM_W", 0);
     MmConfig c;
+    // one 12-wave work-group per CU when 384-row tiles of 64 tokens fill the CUs in whole rounds
+    // (or in enough rounds that the last one matters little) without splitting K, and the
+    // last row tile is mostly inside M
+    {
+        const int64_t t12 = (a.M + 383) / 384 * ((a.N + 63) / 64) * slices;
+        const bool fits = (t12 % cu_count == 0 || t12 >= 4 * (int64_t) cu_count) && (a.M % 384 == 0 || a.M >= 8 * 384);
+        if (env_w == 12 || (env_w == 0 && fits && env_bn != 128 && env_rg != 2 && env_split <= 1)) {
+            c.w = 12;
+            c.bn = 64;
+            c.rg = 1;
+            c.split = 1;
+            return c;
+        }
+    }
+    c.w = 4;
     c.rg = env_rg == 1 || env_rg == 2 ? env_rg : 1;
     const int64_t tm = (a.M + 128 * c.rg - 1) / (128 * c.rg);
     auto tiles = [&](int bn) { return tm * ((a.N + bn - 1) / bn) * slices; };
@@ -857,7 +892,7 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
     const int64_t want = (int64_t) cu_count * occupancy_of(a.dtype, c.bn, c.rg);
     c.split = 1;
     if (env_split > 0) {
-        c.split = (int) std::max<int64_t>(1, std::min<int64_t>(std::min(env_split, 8), stages));
+        c.split = (int) std::max<int64_t>(1, std::min<int64_t>(std::min(env_split, 8), (stages + 3) / 4)); // whole groups of 4 stages
         return c;
     }
     while (tiles(c.bn) * c.split < want && stages / (c.split + 1) >= 8 && c.split < 8) ++c.split;
@@ -866,8 +901,9 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
 
 template <int DT>
 void * kernel_of(const MmConfig & c) {
-    if (c.rg == 1) return c.bn == 64 ? (void *) k_matmul<DT, 64, 1> : (void *) k_matmul<DT, 128, 1>;
-    return c.bn == 64 ? (void *) k_matmul<DT, 64, 2> : (void *) k_matmul<DT, 128, 2>;
+    if (c.w == 12) return (void *) k_matmul<DT, 64, 1, 12>;
+    if (c.rg == 1) return c.bn == 64 ? (void *) k_matmul<DT, 64, 1, 4> : (void *) k_matmul<DT, 128, 1, 4>;
+    return c.bn == 64 ? (void *) k_matmul<DT, 64, 2, 4> : (void *) k_matmul<DT, 128, 2, 4>;
 }
 
 // scratch: x as f16 [slices][N][K] | row factors [slices][N] | Q4_K sub-block sums
@@ -930,7 +966,7 @@ hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count
     L.xsum_row = xsum_row;
     const MmConfig cfg = config_of(a, cu_count);
     const int BN = cfg.bn;
-    L.tiles_m = (a.M + 128 * cfg.rg - 1) / (128 * cfg.rg);
+    L.tiles_m = (a.M + 32 * cfg.rg * cfg.w - 1) / (32 * cfg.rg * cfg.w);
     L.tiles_n = (a.N + BN - 1) / BN;
     L.stages = (a.K + BK - 1) / BK;
     L.split = cfg.split;
@@ -956,7 +992,7 @@ hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count
             done.push_back(fn);
         }
     }
-    e = hipLaunchKernel(fn, grid, dim3(kThreads), args, lds, stream);
+    e = hipLaunchKernel(fn, grid, dim3((unsigned) (64 * cfg.w)), args, lds, stream);
     if (e != hipSuccess || L.split == 1) return e;
     const bool yvec = (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 && a.M % 4 == 0 && a.y_s1 % 4 == 0 && a.y_s2 % 4 == 0 && a.y_s3 % 4 == 0;
     const dim3 rg((unsigned) rows, (unsigned) ((a.M + 1023) / 1024));

@@ -174,14 +174,29 @@ def test_prefill_mfma(hip, dtype, N):
     assert e <= 5e-5, f"NMSE {e:.3e}"
 
 
-@pytest.mark.parametrize("K", [2560, 2816])
-def test_prefill_q4k_large_scales_and_split_groups(hip, K):
+@pytest.mark.parametrize("dtype,M,N,K", [(sg.Q4_0, 1536, 4096, 512), (sg.Q8_0, 1536, 4096, 544), (sg.Q4_K, 1536, 4096, 512),
+                                         (sg.Q6_K, 1536, 4096, 512), (sg.Q4_K, 3500, 6592, 256)],
+                         ids=["q4_0", "q8_0_ktail", "q4_k", "q6_k", "q4_k_partial_rows"])
+def test_prefill_one_workgroup_per_cu(hip, dtype, M, N, K):
+    """Shapes whose 384-row x 64-token tiles fill the CUs in whole rounds (or in many rounds):
+    the matmul runs one 12-wave work-group per CU. Q8_0 with K = 544 ends in a partial stage;
+    M = 3500 ends in a partial row tile."""
+    dev, st = hip
+    q, _ = quantized(dtype, K, M, 500 + M)
+    x = O.normal(N * K, 501).reshape(N, K)
+    y = run_mul_mat(dev, st, dtype, q, K, M, x)
+    ref = O.mul_mat(dtype, q, K, M, x, threads=8)
+    e = nmse(y, ref)
+    assert e <= 5e-5, f"NMSE {e:.3e}"
+
+
+@pytest.mark.parametrize("K,M,N", [(2560, 200, 64), (2816, 200, 64), (1024, 1536, 4096)])
+def test_prefill_q4k_large_scales_and_split_groups(hip, K, M, N):
     """Q4_K prefill with rows whose sub-block scales (weights in the hundreds) or offsets (means
     near -3000) are beyond the single-fma form, mixed with ordinary rows; K = 20 or 22 stages, so
-    the split-K halves start inside a group of 4 stages and K = 2816 ends in half a group. Every
-    row set meets the NMSE bound on its own."""
+    the split-K halves start inside a group of 4 stages and K = 2816 ends in half a group; the
+    1536 x 4096 shape runs on 12-wave work-groups. Every row set meets the NMSE bound on its own."""
     dev, st = hip
-    M, N = 200, 64
     w = O.normal(K * M, 77, 0.0, 0.02).reshape(M, K)
     w[0:10] *= 1e4                    # scales d * sc well above 32
     w[20:30] += -3000.0               # offsets 32 * dmin * m well above 32768
