@@ -438,8 +438,9 @@ struct XTile {
     bool tail;        // the last load's stage reaches past K (wave-uniform)
     bool zero;        // ... and this thread's chunk lies past K
     uint4 v[NP];
-    __device__ void init(int64_t N, int64_t K, int64_t n0) {
-        const int p = threadIdx.x;
+    int p;            // the thread's index among the 64 W threads that load the tile
+    __device__ void init(int64_t N, int64_t K, int64_t n0, int p_) {
+        p = p_;
         kc = 8 * (p & 15);
         dst = xsw(p >> 4, p & 15); // token + TS i (TS a multiple of 16) keeps the swizzle
         off = 2 * ((uint32_t) ((n0 + (p >> 4)) * K) + kc);
@@ -456,7 +457,7 @@ struct XTile {
         const uint8_t * base = reinterpret_cast<const uint8_t *>(xb);
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
-            const uint32_t o = (threadIdx.x >> 4) + TS * i < BN ? off + i * step : off;
+            const uint32_t o = (p >> 4) + TS * i < BN ? off + i * step : off;
             v[i] = *reinterpret_cast<const uint4 *>(base + (min(o, last) + k));
         }
     }
@@ -466,7 +467,7 @@ struct XTile {
             for (int i = 0; i < NP; ++i) v[i] = zero ? make_uint4(0, 0, 0, 0) : v[i];
         }
 #pragma unroll
-        for (int i = 0; i < NP; ++i) *reinterpret_cast<uint4 *>(X + ((threadIdx.x >> 4) + TS * i < BN ? dst + i * TS * BK : dst)) = v[i];
+        for (int i = 0; i < NP; ++i) *reinterpret_cast<uint4 *>(X + ((p >> 4) + TS * i < BN ? dst + i * TS * BK : dst)) = v[i];
     }
 };
 
@@ -483,20 +484,24 @@ constexpr int occupancy_of(int dt, int bn, int rg, int w = 4) {
 }
 
 // W = 4: a work-group per SIMD quad, several per CU. W = 12: the CU's whole complement of 3 waves
-// per SIMD in one work-group (a tile of 384 rows): its waves keep in step at the stage barrier,
-// where separate work-groups on one CU drift apart (the oldest waves win the issue arbitration,
-// so the last work-group finishes alone with one wave per SIMD), and each x tile serves 3x the rows.
-template <int DT, int BN, int RG, int W>
+// per SIMD in one work-group: its waves keep in step at the stage barrier, where separate
+// work-groups on one CU drift apart (the oldest waves win the issue arbitration, so the last
+// work-group finishes alone with one wave per SIMD). KG = 1: 12 row waves, a tile of 384 rows,
+// each x tile serving 3x the rows; KG = 3: 4 row waves x 3 groups that take a third of K each
+// (their own x tiles), added in LDS at the end (split-K without a second pass over memory).
+template <int DT, int BN, int RG, int W, int KG>
 __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(MmArgs L) {
     constexpr int NF = BN / 32; // token fragments per wave
-    constexpr int BMT = 32 * RG * W;
+    constexpr int RW = W / KG;  // row waves
+    constexpr int BMT = 32 * RG * RW;
     using F = PFmt<DT>;
     using Raw = typename F::Raw;
     struct RawSet {
         Raw r[RG];
     };
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_mm[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = (tid >> 6) % RW, kg = (tid >> 6) / RW; // row wave, K group
     const int j = lane & 31, h = lane >> 5;
     const int64_t tile = blockIdx.x / L.split;
     const int split = (int) (blockIdx.x % L.split);
@@ -508,15 +513,19 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     const int64_t m0 = tm * BMT + 32 * RG * wave, n0 = tn * BN;
     // splits cover whole groups of 4 stages (the host keeps split <= groups), so a stage's
     // position in its group is (s - s0) % 4
+    // (KG > 1: the host keeps the stages a multiple of 4 KG and split 1, so that every K group runs
+    // the same number of stages and barriers)
     const int64_t groups = (L.stages + 3) / 4;
-    const int64_t s0 = 4 * (groups * split / L.split), s1 = min(4 * (groups * (split + 1) / L.split), L.stages);
+    const int64_t s0 = KG > 1 ? kg * (L.stages / KG) : 4 * (groups * split / L.split);
+    const int64_t s1 = KG > 1 ? s0 + L.stages / KG : min(4 * (groups * (split + 1) / L.split), L.stages);
 
     F f[RG];
 #pragma unroll
     for (int i = 0; i < RG; ++i) f[i].init(M, nb, RowAddr(M, m0 + 32 * i + j), h);
     const uint16_t * xb = L.xb + (uint64_t) sl * N * K;
-    XTile<BN, W> xt;
-    xt.init(N, K, n0);
+    XTile<BN, RW> xt;
+    xt.init(N, K, n0, tid - kg * 64 * RW);
+    uint16_t * const lds_x = lds_mm + kg * (2 * BN * BK); // the K group's two x buffers
     // LDS element offsets of the lane's A fragments: k-step t, token fragment q at aoff[t] + 32 q rows
     int aoff[8];
 #pragma unroll
@@ -548,12 +557,12 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     // one stage: MFMAs over the x tile in LDS with the weights cw (row groups of the wave);
     // meanwhile the weights of stage s + 1 are loaded into nw and the x tile of stage s + XD into
     // xl, while xn (the x tile of stage s + 1) goes to the other LDS buffer at the end. XD = 2
-    // (two register sets, xn loaded a stage earlier) where the registers allow it, else 1 (xl
-    // and xn are one set)
-    constexpr int XD = BN == 64 ? 2 : 1;
+    // (two register sets, xn loaded a stage earlier) where the registers allow it (BN = 64 with
+    // one K group), else 1 (xl and xn are one set)
+    constexpr int XD = BN == 64 && KG == 1 ? 2 : 1;
     // D = s % 4, a compile-time constant: the LDS buffer, the parity the formats' factors depend
     // on and the offset-MFMA slot are static
-    auto stage = [&](auto dtag, int64_t s, const RawSet & cw, RawSet & nw, XTile<BN, W> & xn, XTile<BN, W> & xl) __attribute__((always_inline)) {
+    auto stage = [&](auto dtag, int64_t s, const RawSet & cw, RawSet & nw, XTile<BN, RW> & xn, XTile<BN, RW> & xl) __attribute__((always_inline)) {
         constexpr int D = decltype(dtag)::value;
         // past the split's last stage the loads repeat it (unused): no load sits under a branch.
         // The x sums of the group come first (waiting for them waits for nothing newer).
@@ -566,7 +575,7 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
 #pragma unroll
         for (int i = 0; i < RG; ++i) nw.r[i] = f[i].load(w, sn);
         xl.load(xb, sx * BK, K);
-        const uint16_t * X = lds_mm + (D & 1) * (BN * BK);
+        const uint16_t * X = lds_x + (D & 1) * (BN * BK);
         const int64_t sp = (s & ~(int64_t) 3) | D; // = s, with its low bits visible to the compiler
         typename F::Sc sc[RG];
 #pragma unroll
@@ -650,17 +659,17 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
                     for (int q = 0; q < NF; ++q) acc[i][q] *= ig;
             }
         }
-        if (s + 1 < s1) xn.store(lds_mm + ((D + 1) & 1) * (BN * BK));
+        if (s + 1 < s1) xn.store(lds_x + ((D + 1) & 1) * (BN * BK));
         __syncthreads();
     };
     RawSet ra{}, rb{};
-    XTile<BN, W> xt2 = xt;
+    XTile<BN, RW> xt2 = xt;
     // every split has at least one stage (the host keeps split <= stages)
 #pragma unroll
     for (int i = 0; i < RG; ++i) ra.r[i] = f[i].load(w, s0);
     xt.load(xb, s0 * BK, K);
     if constexpr (XD == 2) xt2.load(xb, min(s0 + 1, s1 - 1) * BK, K);
-    xt.store(lds_mm);
+    xt.store(lds_x);
     __syncthreads();
     // groups of 4 stages, then the split's last 1..3 outside the loop (a stage under a branch
     // inside the loop would end every iteration with a wait for all loads in flight)
@@ -668,8 +677,8 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
-    XTile<BN, W> & xa = XD == 2 ? xt2 : xt; // x set of stages D = 0, 2 (the next tile's)
-    XTile<BN, W> & xc = xt;                 // of stages D = 1, 3
+    XTile<BN, RW> & xa = XD == 2 ? xt2 : xt; // x set of stages D = 0, 2 (the next tile's)
+    XTile<BN, RW> & xc = xt;                 // of stages D = 1, 3
     int64_t s = s0;
     for (; s + 3 < s1; s += 4) {
         stage(I0{}, s, ra, rb, xa, xc);
@@ -682,6 +691,34 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
         if (s + 1 < s1) {
             stage(I1{}, s + 1, rb, ra, xc, xa);
             if (s + 2 < s1) stage(I2{}, s + 2, ra, rb, xa, xc);
+        }
+    }
+    if constexpr (KG > 1) {
+        // the K groups' sums, added in group order through LDS (the x buffers are free now):
+        // red[(group - 1) * RW + wave][element][lane]
+        constexpr int PER = RG * NF * 16;
+        float * red = reinterpret_cast<float *>(lds_mm);
+        __syncthreads();
+        if (kg > 0) {
+            float * r = red + ((size_t) ((kg - 1) * RW + wave) * PER) * 64 + lane;
+#pragma unroll
+            for (int i = 0; i < RG; ++i)
+#pragma unroll
+                for (int q = 0; q < NF; ++q)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) r[((i * NF + q) * 16 + v) * 64] = acc[i][q][v];
+        }
+        __syncthreads();
+        if (kg > 0) return;
+#pragma unroll
+        for (int g = 1; g < KG; ++g) {
+            const float * r = red + ((size_t) ((g - 1) * RW + wave) * PER) * 64 + lane;
+#pragma unroll
+            for (int i = 0; i < RG; ++i)
+#pragma unroll
+                for (int q = 0; q < NF; ++q)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[i][q][v] += r[((i * NF + q) * 16 + v) * 64];
         }
     }
     // acc[i][q][v], lane (j, h): token n0 + 32q + 8 (v / 4) + 4h + v % 4, weight row m0 + 32i + j
@@ -855,7 +892,8 @@ __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, floa
 struct MmConfig {
     int bn, rg;
     int split;
-    int w; // waves per work-group: 4, or 12 (one work-group per CU, see k_matmul)
+    int w;  // waves per work-group: 4, or 12 (one work-group per CU, see k_matmul)
+    int kg; // K groups of a 12-wave work-group: 1 or 3
 };
 
 int env_int(const char * name, int dflt) {
@@ -878,6 +916,19 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
         const bool fits = (t12 % cu_count == 0 || t12 >= 4 * (int64_t) cu_count) && (a.M % 384 == 0 || a.M >= 8 * 384);
         if (env_w == 12 || (env_w == 0 && fits && env_bn != 128 && env_rg != 2 && env_split <= 1)) {
             c.w = 12;
+            c.kg = 1;
+            c.bn = 64;
+            c.rg = 1;
+            c.split = 1;
+            return c;
+        }
+        // else 3 K groups of 128-row tiles, when those fill the CUs the same way and K divides
+        // into 3 equal runs of whole groups of 4 stages
+        const int64_t t4 = (a.M + 127) / 128 * ((a.N + 63) / 64) * slices;
+        const bool fits3 = (t4 % cu_count == 0 || t4 >= 4 * (int64_t) cu_count) && stages % 12 == 0 && stages >= 24;
+        if (env_w == 0 && fits3 && env_bn != 128 && env_rg != 2 && env_split <= 1) {
+            c.w = 12;
+            c.kg = 3;
             c.bn = 64;
             c.rg = 1;
             c.split = 1;
@@ -885,6 +936,7 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
         }
     }
     c.w = 4;
+    c.kg = 1;
     c.rg = env_rg == 1 || env_rg == 2 ? env_rg : 1;
     const int64_t tm = (a.M + 128 * c.rg - 1) / (128 * c.rg);
     auto tiles = [&](int bn) { return tm * ((a.N + bn - 1) / bn) * slices; };
@@ -901,9 +953,9 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
 
 template <int DT>
 void * kernel_of(const MmConfig & c) {
-    if (c.w == 12) return (void *) k_matmul<DT, 64, 1, 12>;
-    if (c.rg == 1) return c.bn == 64 ? (void *) k_matmul<DT, 64, 1, 4> : (void *) k_matmul<DT, 128, 1, 4>;
-    return c.bn == 64 ? (void *) k_matmul<DT, 64, 2, 4> : (void *) k_matmul<DT, 128, 2, 4>;
+    if (c.w == 12) return c.kg == 3 ? (void *) k_matmul<DT, 64, 1, 12, 3> : (void *) k_matmul<DT, 64, 1, 12, 1>;
+    if (c.rg == 1) return c.bn == 64 ? (void *) k_matmul<DT, 64, 1, 4, 1> : (void *) k_matmul<DT, 128, 1, 4, 1>;
+    return c.bn == 64 ? (void *) k_matmul<DT, 64, 2, 4, 1> : (void *) k_matmul<DT, 128, 2, 4, 1>;
 }
 
 // scratch: x as f16 [slices][N][K] | row factors [slices][N] | Q4_K sub-block sums
@@ -966,11 +1018,12 @@ hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count
     L.xsum_row = xsum_row;
     const MmConfig cfg = config_of(a, cu_count);
     const int BN = cfg.bn;
-    L.tiles_m = (a.M + 32 * cfg.rg * cfg.w - 1) / (32 * cfg.rg * cfg.w);
+    const int bmt = 32 * cfg.rg * (cfg.w / cfg.kg);
+    L.tiles_m = (a.M + bmt - 1) / bmt;
     L.tiles_n = (a.N + BN - 1) / BN;
     L.stages = (a.K + BK - 1) / BK;
     L.split = cfg.split;
-    const size_t lds = (size_t) 2 * BN * BK * sizeof(uint16_t);
+    const size_t lds = (size_t) cfg.kg * 2 * BN * BK * sizeof(uint16_t);
     const int64_t slices = a.ne12 * a.ne13;
     const dim3 grid((unsigned) (L.tiles_m * L.tiles_n * L.split), (unsigned) slices);
     void * args[] = {&L};

@@ -190,7 +190,23 @@ def test_prefill_one_workgroup_per_cu(hip, dtype, M, N, K):
     assert e <= 5e-5, f"NMSE {e:.3e}"
 
 
-@pytest.mark.parametrize("K,M,N", [(2560, 200, 64), (2816, 200, 64), (1024, 1536, 4096)])
+@pytest.mark.parametrize("dtype,M,N,K", [(sg.Q4_0, 512, 4096, 3072), (sg.Q4_K, 512, 4096, 3072), (sg.Q6_K, 512, 4096, 3072),
+                                         (sg.Q8_0, 200, 8192, 3040)],
+                         ids=["q4_0", "q4_k", "q6_k", "q8_0_partial_rows_ktail"])
+def test_prefill_k_groups(hip, dtype, M, N, K):
+    """Shapes whose 128-row tiles fill the CUs and whose K splits into 3 equal runs of whole
+    4-stage groups: one 12-wave work-group per CU, 3 K groups added in LDS. Q8_0 with K = 3040
+    ends in a partial stage and M = 200 in a partial row tile."""
+    dev, st = hip
+    q, _ = quantized(dtype, K, M, 600 + M)
+    x = O.normal(N * K, 601).reshape(N, K)
+    y = run_mul_mat(dev, st, dtype, q, K, M, x)
+    ref = O.mul_mat(dtype, q, K, M, x, threads=8)
+    e = nmse(y, ref)
+    assert e <= 5e-5, f"NMSE {e:.3e}"
+
+
+@pytest.mark.parametrize("K,M,N", [(2560, 200, 64), (2816, 200, 64), (1024, 1536, 4096), (3072, 512, 4096)])
 def test_prefill_q4k_large_scales_and_split_groups(hip, K, M, N):
     """Q4_K prefill with rows whose sub-block scales (weights in the hundreds) or offsets (means
     near -3000) are beyond the single-fma form, mixed with ordinary rows; K = 20 or 22 stages, so
