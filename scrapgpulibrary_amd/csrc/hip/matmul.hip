@@ -198,11 +198,11 @@ template <> struct PFmt<Q4_K> {
         ho = (uint32_t) (M * nb * 128 + ra.g0 * nb * 16 + ra.lr * 16);
     }
     // a block is 8 units; stage s starts at unit 4s
-    __device__ Raw load(const uint8_t * w, int64_t s) const {
+    __device__ Raw load(const uint8_t * w, int s) const {
         const uint32_t q = mad24((uint32_t) s * 4, u, qo);
-        return Raw{load16(w + q), load16(w + q + u), load16(w + mad24((uint32_t) (s >> 1), u, ho))};
+        return Raw{load16(w + q), load16(w + (q + u)), load16(w + mad24((uint32_t) (s >> 1), u, ho))};
     }
-    __device__ Sc prep(const Raw & r, int64_t s, float g = 1.0f) const {
+    __device__ Sc prep(const Raw & r, int s, float g = 1.0f) const {
         const int c = 2 * (int) (s & 1) + h;
         const float d = g * half_bits(r.hd.x), dmin = g * half_bits(r.hd.x >> 16);
         float sc0, m0, sc1, m1;
@@ -218,7 +218,8 @@ template <> struct PFmt<Q4_K> {
         r0.n0 = r0.s0 * k;
         r0.n1 = r0.s1 * k;
         r0.om = __builtin_bit_cast(uint32_t, (f16x2{(_Float16) fo0, (_Float16) fo1}));
-        r0.big = !(__builtin_fabsf(fs0) < 32.0f && __builtin_fabsf(fs1) < 32.0f && __builtin_fabsf(fo0) < 32768.0f && __builtin_fabsf(fo1) < 32768.0f);
+        // |d sc| <= 63 |d| < 32 and |32 dmin m| <= 2016 |dmin| < 32768 (a bound per block)
+        r0.big = !(__builtin_fabsf(d) < 0.5f && __builtin_fabsf(dmin) < 16.0f);
         return r0;
     }
     // exact form: s (c + bias) + o per pair (low nibbles: s0, o0; high nibbles: s1, o1)
@@ -268,7 +269,7 @@ template <> struct PFmt<Q6_K> {
         dof = (uint32_t) (M * nb * 208 + ra.g0 * nb * 2 + ra.lr * 2);
     }
     // a block is 12 quant units (ql 0..7, qh 8..11), 1 scale unit and the d halves
-    __device__ Raw load(const uint8_t * w, int64_t s) const {
+    __device__ Raw load(const uint8_t * w, int s) const {
         const uint32_t b = (uint32_t) (s >> 1), n = (uint32_t) (s & 1);
         Raw r;
         const uint32_t qa = mad24(12 * b + 4 * n, u, qo);
@@ -281,7 +282,7 @@ template <> struct PFmt<Q6_K> {
     }
     // the signed 8-bit scale of run rr sits at byte 8n + h + 2rr (stored xor 0x80): word 2n (runs
     // 0, 1) or 2n + 1 (runs 2, 3), byte h or h + 2
-    __device__ Sc prep(const Raw & r, int64_t s) const {
+    __device__ Sc prep(const Raw & r, int s) const {
         const uint32_t lo = (s & 1) ? r.sc.z : r.sc.x, hi = (s & 1) ? r.sc.w : r.sc.y;
         const int sh = 8 * h;
         const float d = half_bits(r.d);
@@ -329,7 +330,7 @@ template <> struct PFmt<Q8_0> {
         last = (uint32_t) (nb - 1);
     }
     // block b: units 2b, 2b + 1 at 2b U; its d at b U / 8 in the d area
-    __device__ Raw load(const uint8_t * w, int64_t s) const {
+    __device__ Raw load(const uint8_t * w, int s) const {
         const uint32_t b0 = (uint32_t) s * 4 + 2 * h;
         Raw r;
         r.d = 0;
@@ -343,7 +344,7 @@ template <> struct PFmt<Q8_0> {
         }
         return r;
     }
-    __device__ Sc prep(const Raw & r, int64_t) const {
+    __device__ Sc prep(const Raw & r, int) const {
         return Sc{{h2(half_bits(r.d)), h2(half_bits(r.d >> 16))}};
     }
     __device__ static f16x8 bop(const Raw & r, const Sc & c, int t) {
@@ -376,7 +377,7 @@ template <> struct PFmt<Q4_0> {
         dof = (uint32_t) (M * nb * 16 + ra.g0 * nb * 2 + ra.lr * 2);
         last = (uint32_t) (nb - 1);
     }
-    __device__ Raw load(const uint8_t * w, int64_t s) const {
+    __device__ Raw load(const uint8_t * w, int s) const {
         const uint32_t b0 = (uint32_t) s * 4 + 2 * h;
         Raw r;
         r.d = 0;
@@ -388,7 +389,7 @@ template <> struct PFmt<Q4_0> {
         }
         return r;
     }
-    __device__ Sc prep(const Raw & r, int64_t) const {
+    __device__ Sc prep(const Raw & r, int) const {
         return Sc{{h2(half_bits(r.d)), h2(half_bits(r.d >> 16))}};
     }
     __device__ static f16x8 bop(const Raw & r, const Sc & c, int t) {
@@ -434,9 +435,10 @@ struct XTile {
     uint32_t last;    // the same for token N - 1 (tokens past N read it)
     uint32_t step;    // TS tokens
     uint32_t kc;      // element offset of the chunk inside a stage
+    int kmax;         // K - 8 - kc: the stage offset at which the chunk is the row's last one
     int dst;
-    bool tail;        // the last load's stage reaches past K (wave-uniform)
-    bool zero;        // ... and this thread's chunk lies past K
+    int k0;           // the last load's stage start (wave-uniform)
+    bool tail;        // ... which reaches past K
     uint4 v[NP];
     int p;            // the thread's index among the 64 W threads that load the tile
     __device__ void init(int64_t N, int64_t K, int64_t n0, int p_) {
@@ -446,14 +448,16 @@ struct XTile {
         off = 2 * ((uint32_t) ((n0 + (p >> 4)) * K) + kc);
         last = 2 * ((uint32_t) ((N - 1) * K) + kc);
         step = (uint32_t) (2 * TS * K);
-        tail = zero = false;
+        kmax = (int) K - 8 - (int) kc;
+        k0 = 0;
+        tail = false;
     }
     // the stage starting at element k0
     // (32-bit byte offsets from the slice's base: one scalar base, no 64-bit address math)
-    __device__ void load(const uint16_t * xb, int64_t k0, int64_t K) {
+    __device__ void load(const uint16_t * xb, int k0_, int K) {
+        k0 = k0_;
         tail = k0 + BK > K;
-        zero = k0 + kc >= K;
-        const uint32_t k = 2 * (zero ? (uint32_t) (K - 8) - kc : (uint32_t) k0);
+        const uint32_t k = 2 * (uint32_t) min(k0, kmax); // chunks past K: the row's last chunk
         const uint8_t * base = reinterpret_cast<const uint8_t *>(xb);
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
@@ -463,6 +467,7 @@ struct XTile {
     }
     __device__ void store(uint16_t * X) {
         if (tail) { // the last stage of a K that is not a multiple of the stage
+            const bool zero = k0 > kmax + 7; // k0 + kc >= K
 #pragma unroll
             for (int i = 0; i < NP; ++i) v[i] = zero ? make_uint4(0, 0, 0, 0) : v[i];
         }
@@ -516,8 +521,9 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     // (KG > 1: the host keeps the stages a multiple of 4 KG and split 1, so that every K group runs
     // the same number of stages and barriers)
     const int64_t groups = (L.stages + 3) / 4;
-    const int64_t s0 = KG > 1 ? kg * (L.stages / KG) : 4 * (groups * split / L.split);
-    const int64_t s1 = KG > 1 ? s0 + L.stages / KG : min(4 * (groups * (split + 1) / L.split), L.stages);
+    // (stage indices in 32 bits: K < 2^31 elements, and scalar 32-bit compares)
+    const int s0 = (int) (KG > 1 ? kg * (L.stages / KG) : 4 * (groups * split / L.split));
+    const int s1 = (int) (KG > 1 ? s0 + L.stages / KG : min(4 * (groups * (split + 1) / L.split), L.stages));
 
     F f[RG];
 #pragma unroll
@@ -562,7 +568,7 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     constexpr int XD = BN == 64 && KG == 1 ? 2 : 1;
     // D = s % 4, a compile-time constant: the LDS buffer, the parity the formats' factors depend
     // on and the offset-MFMA slot are static
-    auto stage = [&](auto dtag, int64_t s, const RawSet & cw, RawSet & nw, XTile<BN, RW> & xn, XTile<BN, RW> & xl) __attribute__((always_inline)) {
+    auto stage = [&](auto dtag, int s, const RawSet & cw, RawSet & nw, XTile<BN, RW> & xn, XTile<BN, RW> & xl) __attribute__((always_inline)) {
         constexpr int D = decltype(dtag)::value;
         // past the split's last stage the loads repeat it (unused): no load sits under a branch.
         // The x sums of the group come first (waiting for them waits for nothing newer).
@@ -571,12 +577,12 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
             for (int q = 0; q < NF; ++q)
                 asum[q] = *reinterpret_cast<const f16x8 *>(reinterpret_cast<const uint8_t *>(L.xsum) + 2 * (soff[q] + (uint32_t) (s >> 2) * 16));
         }
-        const int64_t sn = min(s + 1, s1 - 1), sx = min(s + XD, s1 - 1);
+        const int sn = min(s + 1, s1 - 1), sx = min(s + XD, s1 - 1);
 #pragma unroll
         for (int i = 0; i < RG; ++i) nw.r[i] = f[i].load(w, sn);
-        xl.load(xb, sx * BK, K);
+        xl.load(xb, sx * BK, (int) K);
         const uint16_t * X = lds_x + (D & 1) * (BN * BK);
-        const int64_t sp = (s & ~(int64_t) 3) | D; // = s, with its low bits visible to the compiler
+        const int sp = (s & ~3) | D; // = s, with its low bits visible to the compiler
         typename F::Sc sc[RG];
 #pragma unroll
         for (int i = 0; i < RG; ++i) sc[i] = f[i].prep(cw.r[i], sp);
@@ -667,8 +673,8 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     // every split has at least one stage (the host keeps split <= stages)
 #pragma unroll
     for (int i = 0; i < RG; ++i) ra.r[i] = f[i].load(w, s0);
-    xt.load(xb, s0 * BK, K);
-    if constexpr (XD == 2) xt2.load(xb, min(s0 + 1, s1 - 1) * BK, K);
+    xt.load(xb, s0 * BK, (int) K);
+    if constexpr (XD == 2) xt2.load(xb, min(s0 + 1, s1 - 1) * BK, (int) K);
     xt.store(lds_x);
     __syncthreads();
     // groups of 4 stages, then the split's last 1..3 outside the loop (a stage under a branch
@@ -679,7 +685,7 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     using I3 = std::integral_constant<int, 3>;
     XTile<BN, RW> & xa = XD == 2 ? xt2 : xt; // x set of stages D = 0, 2 (the next tile's)
     XTile<BN, RW> & xc = xt;                 // of stages D = 1, 3
-    int64_t s = s0;
+    int s = s0;
     for (; s + 3 < s1; s += 4) {
         stage(I0{}, s, ra, rb, xa, xc);
         stage(I1{}, s + 1, rb, ra, xc, xa);
