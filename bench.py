@@ -14,7 +14,7 @@ Reported on one JSON line:
                 timed region), vs 8 TB/s;
                 `traffic` = HBM bytes per launch from the committed rocprofv3 PMC summary
   prefill       Q4_K M=512 (N=512 tokens) MFMA TFLOP/s on the two MLP shapes, vs 2.5 PFLOP/s dense f16/bf16
-  cpu_baseline  the oracle's reference-faithful CPU MUL_MAT (1 thread) on one gate matrix, N=1
+  cpu_baseline  the reference's CPU MUL_MAT (oracle/_ref; the oracle when absent), 1 thread, one gate matrix, N=1
 """
 from __future__ import annotations
 
@@ -339,18 +339,22 @@ def bench_get_rows(dev, st, n_rows, reps):
 
 
 def cpu_baseline(dev, st, model, seconds):
-    """The oracle (reference-faithful C restatement, 1 thread) on one gate matrix at N=1."""
+    """The reference's own CPU MUL_MAT (oracle/_ref, compiled from the reference sources; its CPU
+    backend runs one thread) on one gate matrix at N=1; the oracle's C restatement of it when
+    that library was not built."""
     import oracle as O
 
     name, dt, K, M, q = model.weights[0][4]
     nat = st.download(q, np.uint8)
     x = st.download(model.xh)[:K].reshape(1, K).copy()
-    O.mul_mat(dt, nat, K, M, x)  # warm-up
+    use_ref = O.ref_available()
+    run = (lambda: O.ref_mul_mat(dt, nat, K, M, x)) if use_ref else (lambda: O.mul_mat(dt, nat, K, M, x))
+    run()  # warm-up
     times = []
     t_end = time.time() + seconds
     while time.time() < t_end or len(times) < 3:
         t0 = time.perf_counter()
-        O.mul_mat(dt, nat, K, M, x)
+        run()
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
     cpu = "unknown"
@@ -362,8 +366,10 @@ def cpu_baseline(dev, st, model, seconds):
                     break
     except OSError:
         pass
-    return {"value": round(weight_bytes(dt, K, M) / med / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle MUL_MAT Q4_K {M}x{K} N=1 (one layer's gate), median of {len(times)} runs of {med * 1e3:.1f} ms; "
+    what = "reference CPU backend (oracle/_ref)" if use_ref else "oracle (C restatement)"
+    return {"value": round(weight_bytes(dt, K, M) / med / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "reference" if use_ref else "port",
+            "sample": f"{what} MUL_MAT Q4_K {M}x{K} N=1 (one layer's gate), median of {len(times)} runs of {med * 1e3:.1f} ms; "
                       f"host {cpu}, nproc {os.cpu_count()}"}
 
 
