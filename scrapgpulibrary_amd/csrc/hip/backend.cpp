@@ -729,6 +729,14 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
                mats[j].ne12 * mats[j].ne13 == 1 && mats[0].ne12 * mats[0].ne13 == 1;
     }
     const int groups = fuse ? 1 : n;
+    if (!fuse && n > 1 && mats[0].N > 8) {
+        // prefill products of one MUL_MAT_MULTI: scratch for the largest first, so that products
+        // reading the same x share one x pre-pass (the scratch stays in place between them)
+        size_t need = 0;
+        for (int j = 0; j < n; ++j) need = std::max(need, sgk::matmul_scratch_bytes(mats[j], cus));
+        const scrapgpu_status st = ensure_scratch(s, need);
+        if (st != SCRAPGPU_STATUS_OK) return st;
+    }
     for (int gi = 0; gi < groups; ++gi) {
         const sgk::MatArgs * m = fuse ? mats : mats + gi;
         const int cnt = fuse ? n : 1;
@@ -748,7 +756,8 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
             if (st != SCRAPGPU_STATUS_OK) return st;
             ProfScope prof(s->s);
             const char * name = nullptr;
-            SG_HIP(sgk::launch_matmul_mfma(m[0], s->scratch, cus, s->s, &name), "matmul launch");
+            const bool x_ready = !fuse && gi > 0 && mats[gi - 1].N > 8 && sgk::matmul_same_x(mats[gi - 1], m[0]);
+            SG_HIP(sgk::launch_matmul_mfma(m[0], s->scratch, cus, s->s, &name, x_ready), "matmul launch");
             prof.done(name, bytes, flops);
         }
     }

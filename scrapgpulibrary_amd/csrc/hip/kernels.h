@@ -59,7 +59,11 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
 // receives x as scaled f16 rows with their factors and, when K is split over work-groups, the
 // partial sums.
 size_t matmul_scratch_bytes(const MatArgs & a, int cu_count);
-hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name);
+hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name,
+                              bool x_ready = false);
+// true when b's x pre-pass would write what a's did (same x, shape and dtype class): a product
+// launched right after a's on the same scratch may then pass x_ready and skip its own
+bool matmul_same_x(const MatArgs & a, const MatArgs & b);
 
 // GET_ROWS on R32 weights: dst[:, a, b, c] = dequantized row ids[a, b, c] of slice (b, c) of src0
 // (bit-exact with the dequantizer; out-of-range indices read the nearest row).

@@ -993,7 +993,12 @@ size_t matmul_scratch_bytes(const MatArgs & a, int cu_count) {
     return part_offset(a) + (split == 1 ? 0 : part_bytes(a, split));
 }
 
-hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name) {
+bool matmul_same_x(const MatArgs & a, const MatArgs & b) {
+    return a.x == b.x && a.x_s1 == b.x_s1 && a.x_s2 == b.x_s2 && a.x_s3 == b.x_s3 && a.N == b.N && a.K == b.K && a.ne12 == b.ne12 &&
+           a.ne13 == b.ne13 && (a.dtype == Q4_K) == (b.dtype == Q4_K);
+}
+
+hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name, bool x_ready) {
     uint16_t * xb = reinterpret_cast<uint16_t *>(scratch);
     const int64_t rows = a.N * a.ne12 * a.ne13;
     float * xs = reinterpret_cast<float *>(scratch + xs_offset(a));
@@ -1002,7 +1007,9 @@ hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count
     const int64_t xsum_row = xsum_row_of(a);
     if (rows > 0x7fffffff) return hipErrorInvalidValue;
     const dim3 xg((unsigned) rows);
-    if (a.dtype == Q4_K) {
+    if (x_ready) {
+        // x converted by the previous product's pre-pass (matmul_same_x)
+    } else if (a.dtype == Q4_K) {
         if (vec)
             hipLaunchKernelGGL((k_x_to_f16<true, true>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
         else

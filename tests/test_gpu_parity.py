@@ -356,6 +356,37 @@ def test_mul_mat_multi_fused_qkv_shapes(hip, dtype, N):
         b.free()
 
 
+@pytest.mark.parametrize("specs", [[(sg.Q4_K, 384), (sg.Q4_K, 200), (sg.Q6_K, 96)], [(sg.Q6_K, 96), (sg.Q4_K, 200), (sg.Q4_K, 64)]],
+                         ids=["share_then_convert", "convert_then_share"])
+def test_mul_mat_multi_prefill_shares_x(hip, specs):
+    """Prefill MUL_MAT_MULTI (N = 64): consecutive products that read the same x in the same form
+    share one x pre-pass (Q4_K, Q4_K); a Q6_K product converts x in its own form, and a Q4_K after
+    it converts again. Every output against the oracle."""
+    dev, st = hip
+    K, N = 512, 64
+    x = O.normal(N * K, 530).reshape(N, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    st.upload(xt, x)
+    bufs, wts, yts, refs = [], [], [], []
+    for i, (dt, M) in enumerate(specs):
+        q, _ = quantized(dt, K, M, 540 + i)
+        b, t = upload_weights(dev, st, dt, q, K, M)
+        yb = dev.alloc(4 * M * N)
+        bufs += [b, yb]
+        wts.append(t)
+        yts.append(sg.tdesc(sg.F32, (M, N), yb))
+        refs.append(O.mul_mat(dt, q, K, M, x, threads=8))
+    op, keep = sg.multi_op(wts, xt, yts)
+    st.execute(op)
+    st.sync()
+    for (dt, M), yt, ref in zip(specs, yts, refs):
+        e = nmse(st.download(yt).reshape(N, M), ref)
+        assert e <= 5e-5, f"{sg.NAMES[dt]} {M} rows: NMSE {e:.3e}"
+    for b in bufs + [xb]:
+        b.free()
+
+
 def test_mul_mat_multi_mixed_dtypes_falls_back(hip):
     """Weights of different dtypes share x: one launch per product, same results."""
     dev, st = hip
