@@ -311,6 +311,40 @@ def bench_moe(dev, st, tokens):
             "launches_per_token": len(nodes)}
 
 
+def bench_moe_prefill(dev, st, n_tokens, reps):
+    """MUL_MAT_ID at prefill size: the Qwen3-30B-A3B gate experts (Q4_K 2048->768, 128 experts,
+    8 used) over n_tokens tokens with random distinct ids per token (the grouped MFMA path)."""
+    K, M, E, U = MOE_HIDDEN, MOE_FFN, MOE_E, MOE_USED
+    wb = dev.alloc(weight_bytes(sg.Q4_K, K, M) * E)
+    tmp = dev.alloc(4 * K * M)
+    for e in range(E):
+        f = sg.tdesc(sg.F32, (K, M), tmp)
+        st.fill_normal(f, seed=5000 + e, std=0.02)
+        st.quantize(f, sg.tdesc(sg.Q4_K, (K, M), wb, layout=sg.R32, offset=weight_bytes(sg.Q4_K, K, M) * e))
+    w = sg.tdesc(sg.Q4_K, (K, M, E), wb, layout=sg.R32)
+    xb = dev.alloc(4 * K * n_tokens)
+    x = sg.tdesc(sg.F32, (K, 1, n_tokens), xb)
+    st.fill_normal(x, seed=6)
+    rng = np.random.default_rng(7)
+    ids = np.stack([rng.permutation(E)[:U] for _ in range(n_tokens)]).astype(np.int32)
+    ib = dev.alloc(ids.nbytes)
+    it = sg.tdesc(sg.I32, (U, n_tokens), ib)
+    st.upload(it, ids)
+    yb = dev.alloc(4 * M * U * n_tokens)
+    y = sg.tdesc(sg.F32, (M, U, n_tokens), yb)
+    op, keep = sg.mul_mat_id_op(w, x, it, y, U)
+    st.execute(op)
+    st.sync()
+    ms = hip_events_ms(st, lambda: [st.execute(op) for _ in range(reps)], 3) / reps
+    for b in (wb, tmp, xb, ib, yb):
+        b.free()
+    flops = 2.0 * M * K * U * n_tokens
+    used = len(np.unique(ids))
+    return {"workload": f"Qwen3-30B-A3B gate experts (Q4_K {K}->{M}) x {E}, {U} used, {n_tokens} tokens, MUL_MAT_ID (device-grouped MFMA)",
+            "us": round(ms * 1e3, 2), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "experts_read": used, "weight_GBps": round(used * weight_bytes(sg.Q4_K, K, M) / (ms * 1e-3) / 1e9, 1)}
+
+
 def bench_get_rows(dev, st, n_rows, reps):
     """GET_ROWS: n_rows random rows of a Q6_K 151936 x 4096 table (the Qwen3 LM head / embedding
     shape, 510 MB, R32) dequantized to f32."""
@@ -406,7 +440,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--no-moe", action="store_true", help="skip the MUL_MAT_ID (MoE decode) line")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MUL_MAT_ID (MoE decode and prefill) lines")
     ap.add_argument("--no-get-rows", action="store_true", help="skip the GET_ROWS line")
     ap.add_argument("--no-fuse", action="store_true", help="one MUL_MAT per weight instead of MUL_MAT_MULTI for q/k/v and gate/up")
     ap.add_argument("--calibrate", action="store_true", help="only run the 256 MiB copy that calibrates the PMC byte counters")
@@ -451,6 +485,7 @@ def main():
 
     prefill = None if args.no_prefill else bench_prefill(dev, st, 512, 10)
     moe = None if args.no_moe else bench_moe(dev, st, 20)
+    moe_pf = None if args.no_moe else bench_moe_prefill(dev, st, 512, 10)
     get_rows = None if args.no_get_rows else bench_get_rows(dev, st, 512, 5)
     cpu = None if args.no_cpu else cpu_baseline(dev, st, model, args.cpu_seconds)
 
@@ -481,6 +516,7 @@ def main():
         "prefill_M512": prefill,
         "prefill_peak_frac": None if prefill is None else round(max(v["tflops"] for v in prefill.values()) / F16_PEAK_TFLOPS, 4),
         "moe_decode_mul_mat_id": moe,
+        "moe_prefill_mul_mat_id": moe_pf,
         "get_rows": get_rows,
         "cpu_baseline": cpu,
     }

@@ -721,6 +721,14 @@ double weight_bytes(const sgk::MatArgs & a) {
 
 // enqueues 1..3 products on the stream (pointers resolved). Products that share x with one dtype,
 // K and N <= 8 run as one fused matvec launch; anything else as one launch per product.
+// MUL_MAT_ID takes the grouped MFMA path for more than 8 tokens once the experts average 4 pairs
+// or more (the matvec path reads an expert once per pair; with fewer pairs per expert it is as
+// fast), within the routing kernel's limits
+bool mul_mat_id_grouped(const sgk::MatArgs & a, const sgk::IdArgs & id) {
+    const int64_t rows = (id.x_shared ? 1 : id.n_used) * id.n_tok;
+    return id.n_tok > 8 && id.n_used * id.n_tok >= 4 * id.n_exp && id.n_exp <= 1024 && rows * a.K < ((int64_t) 1 << 31);
+}
+
 scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
     const int cus = (int) s->dev->cus;
     bool fuse = n > 1 && mats[0].N <= 8;
@@ -817,6 +825,16 @@ scrapgpu_status exec_desc(Stream * s, const scrapgpu_op_desc * desc) {
         mats[0].y = reinterpret_cast<float *>(py);
         id.ids = reinterpret_cast<const int32_t *>(pi);
         const double pairs = (double) (id.n_used * id.n_tok);
+        if (mul_mat_id_grouped(mats[0], id)) {
+            // many tokens: pairs grouped by expert on the device, one MFMA GEMM over them
+            st = ensure_scratch(s, sgk::mul_mat_id_scratch_bytes(mats[0], id));
+            if (st != SCRAPGPU_STATUS_OK) return st;
+            ProfScope prof(s->s);
+            const char * name = nullptr;
+            SG_HIP(sgk::launch_mul_mat_id_mfma(mats[0], id, s->scratch, s->s, &name), "grouped MUL_MAT_ID launch");
+            prof.done(name, weight_bytes(mats[0]) * (double) id.n_exp, 2.0 * (double) mats[0].M * (double) mats[0].K * pairs);
+            return SCRAPGPU_STATUS_OK;
+        }
         ProfScope prof(s->s);
         const char * name = nullptr;
         uint64_t grid = 0;
@@ -917,6 +935,15 @@ bool graphs_enabled() {
 scrapgpu_status plan_prepare(Stream * s, Plan * p) {
     size_t need = 0;
     for (PlanNode & n : p->nodes) {
+        if (n.op.op == SCRAPGPU_OP_MUL_MAT_ID) {
+            sgk::MatArgs a;
+            sgk::IdArgs id;
+            if (mul_mat_id_rule(n.op.inputs[0], n.op.inputs[1], n.op.inputs[2], n.op.outputs[0], &a, &id, nullptr) == SCRAPGPU_STATUS_OK &&
+                mul_mat_id_grouped(a, id)) {
+                need = std::max(need, sgk::mul_mat_id_scratch_bytes(a, id));
+            }
+            continue;
+        }
         if (n.op.op != SCRAPGPU_OP_MUL_MAT && n.op.op != SCRAPGPU_OP_MUL_MAT_MULTI) continue;
         const size_t cnt = n.op.op == SCRAPGPU_OP_MUL_MAT ? 1 : n.op.output_count;
         for (size_t i = 0; i < cnt; ++i) {

@@ -65,6 +65,14 @@ hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count
 // launched right after a's on the same scratch may then pass x_ready and skip its own
 bool matmul_same_x(const MatArgs & a, const MatArgs & b);
 
+// MUL_MAT_ID with many tokens (prefill): the (slot, token) pairs are grouped by expert on the
+// device (ids clamped as above), x goes through the matmul's pre-pass once, and the f16 MFMA GEMM
+// runs over (expert, 32- or 64-pair tile, 128-row tile) with gathered x rows and scattered
+// outputs; each expert's weights are read once per row tile instead of once per pair. `scratch`:
+// mul_mat_id_scratch_bytes(a, id) bytes (a as mul_mat_id_rule fills it; a.N = 1).
+size_t mul_mat_id_scratch_bytes(const MatArgs & a, const IdArgs & id);
+hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t * scratch, hipStream_t stream, const char ** kernel_name);
+
 // GET_ROWS on R32 weights: dst[:, a, b, c] = dequantized row ids[a, b, c] of slice (b, c) of src0
 // (bit-exact with the dequantizer; out-of-range indices read the nearest row).
 struct GetRowsLaunch {

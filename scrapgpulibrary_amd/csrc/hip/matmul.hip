@@ -31,6 +31,7 @@
 #include <algorithm>
 #include <type_traits>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <vector>
 
@@ -413,6 +414,13 @@ struct MmArgs {
     int64_t tiles_m, tiles_n;
     int64_t stages;      // stages of K (BK elements each)
     int split;           // work-groups along K per tile
+    // grouped MUL_MAT_ID (GA kernels): pair p = t * n_used + slot; pairs[] grouped by expert,
+    // expert e's pairs at e_off[e] .. e_off[e + 1] and token tiles at t_start[e] .. t_start[e + 1];
+    // x row of a pair: t * x_cols + (x_cols > 1 ? slot : 0); y of a pair: a.y + slot * a.y_s1 + t * a.y_s2
+    const int32_t * pairs;
+    const int32_t * e_off;
+    const int32_t * t_start;
+    int32_t n_used, n_exp, x_cols;
 };
 
 // x tile in LDS: row n (token), 16-byte chunk c at (n * kChunks + (c ^ (n & 15))) * 8 f16
@@ -427,9 +435,10 @@ __device__ __forceinline__ int xsw(int n, int c) {
 // token N - 1 (their products land in outputs that are never stored), and chunks past K read the
 // row's last chunk and are zeroed when stored to LDS (the weights there are zero as well, but
 // x could hold an infinity)
-template <int BN, int W>
+template <int BN, int W, bool GA = false>
 struct XTile {
     static constexpr int NP = (BN * kChunks + 64 * W - 1) / (64 * W);
+    uint32_t offs[GA ? NP : 1]; // GA: byte offset of each load's (gathered row, chunk)
     static constexpr int TS = 4 * W; // tokens between a thread's loads
     uint32_t off;     // byte offset of (token p / 16, chunk p % 16) in the slice's x rows
     uint32_t last;    // the same for token N - 1 (tokens past N read it)
@@ -452,6 +461,21 @@ struct XTile {
         k0 = 0;
         tail = false;
     }
+    // GA: the tile's tokens are the x rows rows[0 .. BN) (gathered pairs, repeated past the count)
+    __device__ void init_rows(int64_t K, const int32_t * rows, int p_) {
+        p = p_;
+        kc = 8 * (p & 15);
+        dst = xsw(p >> 4, p & 15);
+        off = last = step = 0;
+        kmax = (int) K - 8 - (int) kc;
+        k0 = 0;
+        tail = false;
+#pragma unroll
+        for (int i = 0; i < (GA ? NP : 1); ++i) {
+            const int n = (p >> 4) + TS * i;
+            offs[i] = 2 * ((uint32_t) rows[n < BN ? n : (p >> 4)] * (uint32_t) K + kc);
+        }
+    }
     // the stage starting at element k0
     // (32-bit byte offsets from the slice's base: one scalar base, no 64-bit address math)
     __device__ void load(const uint16_t * xb, int k0_, int K) {
@@ -461,8 +485,12 @@ struct XTile {
         const uint8_t * base = reinterpret_cast<const uint8_t *>(xb);
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
-            const uint32_t o = (p >> 4) + TS * i < BN ? off + i * step : off;
-            v[i] = *reinterpret_cast<const uint4 *>(base + (min(o, last) + k));
+            if constexpr (GA) {
+                v[i] = *reinterpret_cast<const uint4 *>(base + (offs[i] + k));
+            } else {
+                const uint32_t o = (p >> 4) + TS * i < BN ? off + i * step : off;
+                v[i] = *reinterpret_cast<const uint4 *>(base + (min(o, last) + k));
+            }
         }
     }
     __device__ void store(uint16_t * X) {
@@ -485,7 +513,7 @@ __device__ __forceinline__ f16x8 bop_of(const typename F::Raw & r, const typenam
 
 // work-groups of W waves per CU that the register file (and, at BN = 128, the LDS) holds
 constexpr int occupancy_of(int dt, int bn, int rg, int w = 4) {
-    return w == 12 ? 1 : bn == 64 && rg == 1 ? (dt == Q6_K ? 2 : 3) : bn == 128 && rg == 2 ? 1 : 2;
+    return w == 12 ? 1 : bn == 32 ? 3 : bn == 64 && rg == 1 ? (dt == Q6_K ? 2 : 3) : bn == 128 && rg == 2 ? 1 : 2;
 }
 
 // W = 4: a work-group per SIMD quad, several per CU. W = 12: the CU's whole complement of 3 waves
@@ -494,7 +522,10 @@ constexpr int occupancy_of(int dt, int bn, int rg, int w = 4) {
 // work-group finishes alone with one wave per SIMD). KG = 1: 12 row waves, a tile of 384 rows,
 // each x tile serving 3x the rows; KG = 3: 4 row waves x 3 groups that take a third of K each
 // (their own x tiles), added in LDS at the end (split-K without a second pass over memory).
-template <int DT, int BN, int RG, int W, int KG>
+// GA: grouped MUL_MAT_ID (W = 4, KG = 1, no split): blockIdx.x = token tile * tiles_m + row tile;
+// a token tile belongs to one expert, whose weights the work-group reads, and gathers its pairs'
+// x rows / scatters their outputs through a table in LDS after the x buffers.
+template <int DT, int BN, int RG, int W, int KG, bool GA = false>
 __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(MmArgs L) {
     constexpr int NF = BN / 32; // token fragments per wave
     constexpr int RW = W / KG;  // row waves
@@ -514,8 +545,36 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     const int64_t sl = blockIdx.y;
     const int64_t i2 = sl % L.a.ne12, i3 = sl / L.a.ne12;
     const uint8_t * w = L.a.w + (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
-    const int64_t K = L.a.K, N = L.a.N, M = L.a.M, nb = L.a.nb;
-    const int64_t m0 = tm * BMT + 32 * RG * wave, n0 = tn * BN;
+    const int64_t K = L.a.K, M = L.a.M, nb = L.a.nb;
+    int64_t N = L.a.N;
+    int64_t n0 = tn * BN;
+    const int64_t m0 = tm * BMT + 32 * RG * wave;
+    int32_t * ga_rows = reinterpret_cast<int32_t *>(lds_mm + 2 * BN * BK);    // GA: x row of tile token n
+    int64_t * ga_y = reinterpret_cast<int64_t *>(ga_rows + BN);               // GA: its y element offset
+    int32_t ga_cnt = BN;                                                      // GA: the tile's pairs
+    if constexpr (GA) {
+        // the expert owning token tile tn: the last e with t_start[e] <= tn (an empty expert
+        // shares its start with the next one)
+        if (tn >= L.t_start[L.n_exp]) return; // past this call's tiles (the whole work-group)
+        int lo = 0, hi = L.n_exp - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (L.t_start[mid] <= tn) lo = mid;
+            else hi = mid - 1;
+        }
+        const int32_t pb = L.e_off[lo] + (int32_t) (tn - L.t_start[lo]) * BN;
+        ga_cnt = min(BN, L.e_off[lo + 1] - pb);
+        w = L.a.w + (uint64_t) lo * L.a.w_s2;
+        if (tid < BN) {
+            const int32_t pr = L.pairs[pb + min(tid, ga_cnt - 1)]; // tokens past the count repeat the last pair
+            const int32_t t = pr / L.n_used, slot = pr - t * L.n_used;
+            ga_rows[tid] = t * L.x_cols + (L.x_cols > 1 ? slot : 0);
+            ga_y[tid] = (int64_t) slot * L.a.y_s1 + (int64_t) t * L.a.y_s2;
+        }
+        __syncthreads();
+        N = BN;
+        n0 = 0;
+    }
     // splits cover whole groups of 4 stages (the host keeps split <= groups), so a stage's
     // position in its group is (s - s0) % 4
     // (KG > 1: the host keeps the stages a multiple of 4 KG and split 1, so that every K group runs
@@ -529,8 +588,9 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
 #pragma unroll
     for (int i = 0; i < RG; ++i) f[i].init(M, nb, RowAddr(M, m0 + 32 * i + j), h);
     const uint16_t * xb = L.xb + (uint64_t) sl * N * K;
-    XTile<BN, RW> xt;
-    xt.init(N, K, n0, tid - kg * 64 * RW);
+    XTile<BN, RW, GA> xt;
+    if constexpr (GA) xt.init_rows(K, ga_rows, tid);
+    else xt.init(N, K, n0, tid - kg * 64 * RW);
     uint16_t * const lds_x = lds_mm + kg * (2 * BN * BK); // the K group's two x buffers
     // LDS element offsets of the lane's A fragments: k-step t, token fragment q at aoff[t] + 32 q rows
     int aoff[8];
@@ -550,7 +610,10 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
 #pragma unroll
         for (int d = 0; d < 4; ++d) bm[i][d] = 0u;
 #pragma unroll
-    for (int q = 0; q < NF; ++q) soff[q] = (uint32_t) (((uint64_t) sl * N + min<int64_t>(n0 + 32 * q + j, N - 1)) * L.xsum_row) + 8 * h;
+    for (int q = 0; q < NF; ++q) {
+        const int64_t row = GA ? ga_rows[32 * q + j] : (int64_t) sl * N + min<int64_t>(n0 + 32 * q + j, N - 1);
+        soff[q] = (uint32_t) (row * L.xsum_row) + 8 * h;
+    }
 
     f32x16 acc[RG][NF];
 #pragma unroll
@@ -568,7 +631,7 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     constexpr int XD = BN == 64 && KG == 1 ? 2 : 1;
     // D = s % 4, a compile-time constant: the LDS buffer, the parity the formats' factors depend
     // on and the offset-MFMA slot are static
-    auto stage = [&](auto dtag, int s, const RawSet & cw, RawSet & nw, XTile<BN, RW> & xn, XTile<BN, RW> & xl) __attribute__((always_inline)) {
+    auto stage = [&](auto dtag, int s, const RawSet & cw, RawSet & nw, XTile<BN, RW, GA> & xn, XTile<BN, RW, GA> & xl) __attribute__((always_inline)) {
         constexpr int D = decltype(dtag)::value;
         // past the split's last stage the loads repeat it (unused): no load sits under a branch.
         // The x sums of the group come first (waiting for them waits for nothing newer).
@@ -669,7 +732,7 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
         __syncthreads();
     };
     RawSet ra{}, rb{};
-    XTile<BN, RW> xt2 = xt;
+    XTile<BN, RW, GA> xt2 = xt;
     // every split has at least one stage (the host keeps split <= stages)
 #pragma unroll
     for (int i = 0; i < RG; ++i) ra.r[i] = f[i].load(w, s0);
@@ -683,8 +746,8 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
-    XTile<BN, RW> & xa = XD == 2 ? xt2 : xt; // x set of stages D = 0, 2 (the next tile's)
-    XTile<BN, RW> & xc = xt;                 // of stages D = 1, 3
+    XTile<BN, RW, GA> & xa = XD == 2 ? xt2 : xt; // x set of stages D = 0, 2 (the next tile's)
+    XTile<BN, RW, GA> & xc = xt;                 // of stages D = 1, 3
     int s = s0;
     for (; s + 3 < s1; s += 4) {
         stage(I0{}, s, ra, rb, xa, xc);
@@ -739,6 +802,27 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
         ys1 = M;
     }
     const float * xs = L.xs + (uint64_t) sl * N;
+    if constexpr (GA) {
+        // scatter: token n of the tile is pair ga_y[n] (the pairs past ga_cnt are not stored)
+#pragma unroll
+        for (int q = 0; q < NF; ++q) {
+            float u[16];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) u[v] = L.xs[ga_rows[32 * q + 8 * (v >> 2) + 4 * h + (v & 3)]];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int n = 32 * q + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (n >= ga_cnt) continue;
+                float * yn = L.a.y + ga_y[n];
+#pragma unroll
+                for (int i = 0; i < RG; ++i) {
+                    const int64_t m = m0 + 32 * i + j;
+                    if (m < M) yn[m] = acc[i][q][v] * u[v];
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int q = 0; q < NF; ++q) {
         float u[16]; // the fragment's row factors, loaded together (tokens past N read N - 1)
@@ -889,6 +973,62 @@ __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, floa
             xsum[row * xsum_row + (jb >> 4) * 16 + 8 * ((jj >> 1) & 1) + 2 * (jj >> 2) + (jj & 1)] = 0;
         }
     }
+}
+
+// MUL_MAT_ID routing, one work-group of 1024 threads (E <= 1024 experts, P <= 65535 pairs): the
+// pairs p = t * n_used + slot grouped by expert (ids clamped to [0, E)); e_off[e] / t_start[e] =
+// the first pair / token tile (bn pairs) of expert e, [E] = the totals. The order of the pairs
+// inside an expert follows the LDS atomics; no output depends on it (each is one pair's own sum
+// over K). Each pair's expert is kept in LDS (dynamic, 2 bytes a pair) for the second pass.
+__global__ __launch_bounds__(1024) void k_moe_route(const int32_t * ids, int64_t s0, int64_t s1, int nu, int T, int E, int bn,
+                                                   int32_t * e_off, int32_t * t_start, int32_t * pairs) {
+    __shared__ int32_t cnt[1024], cur[1024], wsum[2][16];
+    extern __shared__ uint16_t pe[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    cnt[tid] = 0;
+    __syncthreads();
+    const int P = nu * T;
+    for (int p = tid; p < P; p += 1024) {
+        const int t = p / nu, slot = p - t * nu;
+        const int e = min(max(ids[slot * s0 + t * s1], 0), E - 1);
+        pe[p] = (uint16_t) e;
+        atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    // exclusive scans of the counts and of the tile counts over the experts (one per thread)
+    const int c = tid < E ? cnt[tid] : 0;
+    const int tl = (c + bn - 1) / bn;
+    int a = c, b = tl;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int ua = __shfl_up(a, o), ub = __shfl_up(b, o);
+        if (lane >= o) {
+            a += ua;
+            b += ub;
+        }
+    }
+    if (lane == 63) {
+        wsum[0][wave] = a;
+        wsum[1][wave] = b;
+    }
+    __syncthreads();
+    int pa = 0, pb = 0;
+    for (int w2 = 0; w2 < wave; ++w2) {
+        pa += wsum[0][w2];
+        pb += wsum[1][w2];
+    }
+    const int ea = pa + a - c, eb = pb + b - tl; // exclusive prefixes
+    if (tid < E) {
+        e_off[tid] = ea;
+        t_start[tid] = eb;
+        cur[tid] = ea;
+    }
+    if (tid == E - 1) {
+        e_off[E] = ea + c;
+        t_start[E] = eb + tl;
+    }
+    __syncthreads();
+    for (int p = tid; p < P; p += 1024) pairs[atomicAdd(&cur[pe[p]], 1)] = p;
 }
 
 // Tile shape and work-groups along K per tile. A work-group is 4 waves; each wave owns RG groups
@@ -1067,6 +1207,111 @@ hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count
     else
         hipLaunchKernelGGL(k_split_reduce<false>, rg, dim3(256), 0, stream, L);
     return hipGetLastError();
+}
+
+namespace {
+
+// grouped MUL_MAT_ID: 64-pair tiles once the experts average 16 pairs or more, else 32. An
+// expert's last tile is part empty (its MFMAs wasted), but a 32-pair tile feeds each dequantized
+// B fragment to one MFMA instead of two: measured (128 experts, 8 used) 32 wins at 8 pairs per
+// expert (34 vs 44 us), 64 at 32 (50 vs 56 us)
+int ga_bn(const IdArgs & id) {
+    static const int env = env_int("SCRAPGPU_HIP_MMID_BN", 0);
+    if (env == 32 || env == 64) return env;
+    return id.n_used * id.n_tok >= 16 * id.n_exp ? 64 : 32;
+}
+
+// the pre-pass's view of MUL_MAT_ID's x: rows t * x_cols + c at x + c * x_s1 + t * x_s2
+MatArgs ga_xargs(const MatArgs & a, const IdArgs & id) {
+    MatArgs px = a;
+    px.N = id.x_shared ? 1 : id.n_used;
+    px.ne12 = id.n_tok;
+    px.ne13 = 1;
+    px.r2 = px.r3 = 1;
+    px.x_s3 = 0;
+    return px;
+}
+
+template <int DT>
+void * ga_kernel(int bn) {
+    return bn == 64 ? (void *) k_matmul<DT, 64, 1, 4, 1, true> : (void *) k_matmul<DT, 32, 1, 4, 1, true>;
+}
+
+} // namespace
+
+size_t mul_mat_id_scratch_bytes(const MatArgs & a, const IdArgs & id) {
+    const MatArgs px = ga_xargs(a, id);
+    return part_offset(px) + (size_t) (2 * (id.n_exp + 1) + id.n_used * id.n_tok) * sizeof(int32_t);
+}
+
+hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t * scratch, hipStream_t stream, const char ** kernel_name) {
+    const MatArgs px = ga_xargs(a, id);
+    const int64_t rows = px.N * id.n_tok;
+    if (id.n_exp < 1 || id.n_exp > 1024 || rows * a.K >= ((int64_t) 1 << 31) || id.n_used * id.n_tok >= ((int64_t) 1 << 24)) return hipErrorInvalidValue;
+    uint16_t * xb = reinterpret_cast<uint16_t *>(scratch);
+    float * xs = reinterpret_cast<float *>(scratch + xs_offset(px));
+    uint16_t * xsum = reinterpret_cast<uint16_t *>(scratch + xsum_offset(px));
+    const int64_t xsum_row = xsum_row_of(px);
+    const bool vec = (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && a.x_s1 % 4 == 0 && a.x_s2 % 4 == 0;
+    const dim3 xg((unsigned) rows);
+    if (a.dtype == Q4_K) {
+        if (vec)
+            hipLaunchKernelGGL((k_x_to_f16<true, true>), xg, dim3(256), 0, stream, px, xb, xs, xsum, xsum_row);
+        else
+            hipLaunchKernelGGL((k_x_to_f16<false, true>), xg, dim3(256), 0, stream, px, xb, xs, xsum, xsum_row);
+    } else {
+        if (vec)
+            hipLaunchKernelGGL((k_x_to_f16<true, false>), xg, dim3(256), 0, stream, px, xb, xs, xsum, xsum_row);
+        else
+            hipLaunchKernelGGL((k_x_to_f16<false, false>), xg, dim3(256), 0, stream, px, xb, xs, xsum, xsum_row);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int bn = ga_bn(id);
+    int32_t * e_off = reinterpret_cast<int32_t *>(scratch + part_offset(px));
+    int32_t * t_start = e_off + id.n_exp + 1;
+    int32_t * pairs = t_start + id.n_exp + 1;
+    const size_t route_lds = ((size_t) id.n_used * (size_t) id.n_tok * sizeof(uint16_t) + 15) / 16 * 16;
+    if (route_lds > 65536) { // the dynamic LDS beyond the 64 KiB default (16-bit experts of up to 65535 pairs)
+        static std::once_flag once;
+        std::call_once(once, [] { (void) hipFuncSetAttribute((const void *) k_moe_route, hipFuncAttributeMaxDynamicSharedMemorySize, 136 * 1024); });
+    }
+    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), route_lds, stream, id.ids, id.s0, id.s1, (int) id.n_used, (int) id.n_tok, (int) id.n_exp, bn,
+                       e_off, t_start, pairs);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    MmArgs L;
+    std::memset(&L, 0, sizeof(L));
+    L.a = a;
+    L.a.N = bn;
+    L.a.ne12 = L.a.ne13 = 1;
+    L.xb = xb;
+    L.xs = xs;
+    L.xsum = xsum;
+    L.xsum_row = xsum_row;
+    L.part = nullptr;
+    L.split = 1;
+    L.stages = (a.K + BK - 1) / BK;
+    L.tiles_m = (a.M + 127) / 128;
+    L.tiles_n = (id.n_used * id.n_tok + bn - 1) / bn + id.n_exp; // at least the tiles the routing makes
+    L.pairs = pairs;
+    L.e_off = e_off;
+    L.t_start = t_start;
+    L.n_used = (int32_t) id.n_used;
+    L.n_exp = (int32_t) id.n_exp;
+    L.x_cols = (int32_t) px.N;
+    const size_t lds = (size_t) 2 * bn * BK * sizeof(uint16_t) + (size_t) bn * (sizeof(int32_t) + sizeof(int64_t));
+    void * fn = nullptr;
+    switch (a.dtype) {
+        case Q4_0: fn = ga_kernel<Q4_0>(bn); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q4_0"; break;
+        case Q8_0: fn = ga_kernel<Q8_0>(bn); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q8_0"; break;
+        case Q4_K: fn = ga_kernel<Q4_K>(bn); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q4_k"; break;
+        case Q6_K: fn = ga_kernel<Q6_K>(bn); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q6_k"; break;
+        default: return hipErrorInvalidValue;
+    }
+    const int64_t grid = L.tiles_m * L.tiles_n;
+    if (grid >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
+    void * args[] = {&L};
+    return hipLaunchKernel(fn, dim3((unsigned) grid), dim3(256), args, lds, stream);
 }
 
 } // namespace sgk

@@ -146,3 +146,91 @@ def test_mul_mat_id_support_rules(hip):
     assert dev.supported(op)[0] == sg.UNSUPPORTED
     for b in (wb, xb, ib, yb):
         b.free()
+
+
+def check_grouped(y, ref, tol=5e-5):
+    """The prefill tolerance (f16 MFMA path): NMSE over all pairs and for each pair."""
+    from tests.gpu_util import nmse
+    e = nmse(y, ref)
+    assert e <= tol, f"NMSE {e:.3e}"
+    T, nu, M = ref.shape
+    for t in range(T):
+        for i in range(nu):
+            ep = nmse(y[t, i], ref[t, i])
+            assert ep <= 20 * tol, f"pair (token {t}, slot {i}): NMSE {ep:.3e}"
+
+
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+@pytest.mark.parametrize("shared", [True, False], ids=["x_shared", "x_per_slot"])
+def test_mul_mat_id_grouped_prefill(hip, dtype, shared):
+    """More than 8 tokens: pairs grouped by expert on the device, one MFMA GEMM (32-pair tiles,
+    16 experts, 200 rows = a partial row tile)."""
+    dev, st = hip
+    K, M, E, T, nu = 512, 200, 16, 40, 4
+    w = O.quantize(dtype, O.normal(K * M * E, 61, 0.0, 0.02))
+    rng = np.random.default_rng(62)
+    ids = np.stack([rng.permutation(E)[:nu] for _ in range(T)]).astype(np.int32)
+    x = O.normal(T * (1 if shared else nu) * K, 63).reshape(T, 1 if shared else nu, K)
+    y = run_mul_mat_id(dev, st, dtype, w, K, M, E, x, ids)
+    check_grouped(y, O.mul_mat_id(dtype, w, K, M, E, x, ids))
+
+
+@pytest.mark.parametrize("case", ["tiles64", "skewed", "clamped", "q8_0_ktail"])
+def test_mul_mat_id_grouped_cases(hip, case):
+    """64-pair tiles (>= 64 pairs per expert); a skewed routing (most pairs on one expert, most
+    experts empty); out-of-range ids (clamped on the device); a K that ends inside a stage."""
+    dev, st = hip
+    dtype, K, M, E, T, nu = sg.Q4_K, 512, 256, 4, 64, 2
+    rng = np.random.default_rng(71)
+    if case == "tiles64":
+        E = 2
+        ids = np.stack([rng.permutation(E)[:nu] for _ in range(T)]).astype(np.int32)
+    elif case == "skewed":
+        E, T, nu = 32, 96, 2
+        ids = np.where(rng.random((T, nu)) < 0.8, 5, rng.integers(0, 3, (T, nu))).astype(np.int32)
+        ids[:, 1] = np.where(ids[:, 0] == ids[:, 1], 31, ids[:, 1])
+    elif case == "clamped":
+        E, T, nu = 6, 24, 3
+        ids = rng.integers(-4, E + 4, (T, nu)).astype(np.int32)
+    else:
+        dtype, K, E, T, nu = sg.Q8_0, 544, 5, 20, 3
+        ids = np.stack([rng.permutation(E)[:nu] for _ in range(T)]).astype(np.int32)
+    w = O.quantize(dtype, O.normal(K * M * E, 72, 0.0, 0.02))
+    x = O.normal(T * K, 73).reshape(T, 1, K)
+    y = run_mul_mat_id(dev, st, dtype, w, K, M, E, x, ids)
+    check_grouped(y, O.mul_mat_id(dtype, w, K, M, E, x, np.clip(ids, 0, E - 1)))
+
+
+def test_mul_mat_id_grouped_plan_reads_ids_on_device(hip):
+    """A recorded plan (HIP graph) of a grouped MUL_MAT_ID replayed after the ids changed in device
+    memory: the routing runs on the device each replay."""
+    dev, st = hip
+    dtype, K, M, E, T, nu = sg.Q4_K, 256, 128, 8, 32, 2
+    w = O.quantize(dtype, O.normal(K * M * E, 81, 0.0, 0.02))
+    wb, wt = upload_weights(dev, st, dtype, w, K, M, slices=E)
+    x = O.normal(T * K, 82).reshape(T, 1, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, 1, T), xb)
+    st.upload(xt, x)
+    ib = dev.alloc(4 * nu * T)
+    it = sg.tdesc(sg.I32, (nu, T), ib)
+    yb = dev.alloc(4 * M * nu * T)
+    yt = sg.tdesc(sg.F32, (M, nu, T), yb)
+    op, keep = sg.mul_mat_id_op(wt, xt, it, yt, nu)
+    nodes = (sg.PlanNode * 1)(sg.PlanNode(C.sizeof(sg.PlanNode), op, 0))
+    pdesc = sg.PlanDesc(C.sizeof(sg.PlanDesc), nodes, 1)
+    plan = C.c_void_p()
+    sg.check(sg.lib().scrapgpu_plan_build(dev.handle, C.byref(pdesc), C.byref(plan)), "plan_build")
+    rng = np.random.default_rng(83)
+    try:
+        for _ in range(3):
+            ids = np.stack([rng.permutation(E)[:nu] for _ in range(T)]).astype(np.int32)
+            st.upload(it, ids)
+            sg.check(sg.lib().scrapgpu_plan_execute(st.handle, plan), "plan_execute")
+            st.sync()
+            y = st.download(yt).reshape(T, nu, M)
+            check_grouped(y, O.mul_mat_id(dtype, w, K, M, E, x, ids))
+    finally:
+        sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
+    for b in (wb, xb, ib, yb):
+        b.free()
