@@ -301,6 +301,18 @@ def bench_moe(dev, st, tokens):
             ms = hip_events_ms(st, token, 1)
             if t >= 3:
                 times.append(ms)
+        # launches per token: one eager replay under the event profiler (the plan launches a
+        # layer's gate and up, which share x and ids, as one kernel)
+        st.sync()
+        sg.lib().scrapgpu_hip_profile_reset()
+        sg.lib().scrapgpu_hip_profile_enable(1)
+        try:
+            token()
+            st.sync()
+        finally:
+            sg.lib().scrapgpu_hip_profile_enable(0)
+        launches = sum(r["launches"] for r in sg.profile_table())
+        sg.lib().scrapgpu_hip_profile_reset()
     finally:
         sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
     ms = float(np.mean(times))
@@ -308,7 +320,7 @@ def bench_moe(dev, st, tokens):
     return {"workload": f"Qwen3-30B-A3B MoE experts: {MOE_LAYERS} layers x (gate, up Q4_K {MOE_HIDDEN}->{MOE_FFN}; down Q6_K "
                         f"{MOE_FFN}->{MOE_HIDDEN}) x {MOE_E} experts, {MOE_USED} used, bs=1, MUL_MAT_ID with device ids",
             "ms_per_token": round(ms, 4), "selected_weight_bytes_per_token": by, "GBps": round(by / (ms * 1e-3) / 1e9, 1),
-            "launches_per_token": len(nodes)}
+            "ops_per_token": len(nodes), "launches_per_token": launches}
 
 
 def bench_moe_prefill(dev, st, n_tokens, reps):

@@ -97,6 +97,7 @@ struct PlanNode {
     scrapgpu_op_desc op;
     std::vector<scrapgpu_tensor_desc> in, out;
     std::vector<uint8_t> params;
+    int fuse = 0; // the next `fuse` nodes run in this node's launch (MUL_MAT_ID sharing x and ids)
 };
 
 struct Plan {
@@ -856,6 +857,75 @@ scrapgpu_status exec_desc(Stream * s, const scrapgpu_op_desc * desc) {
     return run_products(s, mats, (int) n);
 }
 
+bool same_tensor(const scrapgpu_tensor_desc & a, const scrapgpu_tensor_desc & b) {
+    if (a.buffer != b.buffer || a.offset != b.offset || a.dtype != b.dtype || a.layout != b.layout) return false;
+    for (int i = 0; i < 4; ++i) {
+        if (a.ne[i] != b.ne[i] || a.nb[i] != b.nb[i]) return false;
+    }
+    return true;
+}
+
+// consecutive MUL_MAT_ID nodes of a plan that may share one launch: the same x and ids, experts
+// of one dtype, K, count and stride, outputs of one layout in buffers of their own (none read by
+// another node of the group), and the decode path (the grouped path runs one op per launch)
+bool id_fusable(const PlanNode * group, int n, const PlanNode & b) {
+    const PlanNode & a = group[0];
+    if (a.op.op != SCRAPGPU_OP_MUL_MAT_ID || b.op.op != SCRAPGPU_OP_MUL_MAT_ID) return false;
+    sgk::MatArgs ma, mb;
+    sgk::IdArgs ia, ib;
+    if (mul_mat_id_rule(a.op.inputs[0], a.op.inputs[1], a.op.inputs[2], a.op.outputs[0], &ma, &ia, nullptr) != SCRAPGPU_STATUS_OK ||
+        mul_mat_id_rule(b.op.inputs[0], b.op.inputs[1], b.op.inputs[2], b.op.outputs[0], &mb, &ib, nullptr) != SCRAPGPU_STATUS_OK) {
+        return false;
+    }
+    if (mul_mat_id_grouped(ma, ia) || mul_mat_id_grouped(mb, ib)) return false;
+    if (!same_tensor(a.op.inputs[1], b.op.inputs[1]) || !same_tensor(a.op.inputs[2], b.op.inputs[2])) return false;
+    if (ma.dtype != mb.dtype || ma.K != mb.K || ma.w_s2 != mb.w_s2 || ia.n_exp != ib.n_exp || ia.n_used != ib.n_used) return false;
+    if (ma.y_s1 != mb.y_s1 || ma.y_s2 != mb.y_s2) return false;
+    const void * xb = a.op.inputs[1].buffer;
+    const void * ids = a.op.inputs[2].buffer;
+    const void * yb = b.op.outputs[0].buffer;
+    if (yb == xb || yb == ids) return false;
+    for (int k = 0; k < n; ++k) {
+        const void * yk = group[k].op.outputs[0].buffer;
+        if (yk == yb || yk == xb || yk == ids) return false;
+    }
+    return true;
+}
+
+// a plan node and the nodes fused into it (one matvec launch over all their experts)
+scrapgpu_status exec_node(Stream * s, const PlanNode * nodes) {
+    if (nodes[0].fuse == 0) return exec_desc(s, &nodes[0].op);
+    const int n = nodes[0].fuse + 1;
+    sgk::MatArgs mats[3];
+    sgk::IdArgs id;
+    double bytes = 0, flops = 0;
+    for (int k = 0; k < n; ++k) {
+        const scrapgpu_op_desc & op = nodes[k].op;
+        sgk::IdArgs idk;
+        scrapgpu_status st = mul_mat_id_rule(op.inputs[0], op.inputs[1], op.inputs[2], op.outputs[0], &mats[k], &idk, nullptr);
+        if (st != SCRAPGPU_STATUS_OK) return st;
+        uint8_t *pw, *px, *pi, *py;
+        if ((st = resolve(s->dev, op.inputs[0], &pw, "src0")) != SCRAPGPU_STATUS_OK) return st;
+        if ((st = resolve(s->dev, op.inputs[1], &px, "src1")) != SCRAPGPU_STATUS_OK) return st;
+        if ((st = resolve(s->dev, op.inputs[2], &pi, "ids")) != SCRAPGPU_STATUS_OK) return st;
+        if ((st = resolve(s->dev, op.outputs[0], &py, "dst")) != SCRAPGPU_STATUS_OK) return st;
+        mats[k].w = pw;
+        mats[k].x = reinterpret_cast<const float *>(px);
+        mats[k].y = reinterpret_cast<float *>(py);
+        idk.ids = reinterpret_cast<const int32_t *>(pi);
+        if (k == 0) id = idk;
+        const double pairs = (double) (idk.n_used * idk.n_tok);
+        bytes += weight_bytes(mats[k]) * pairs;
+        flops += 2.0 * (double) mats[k].M * (double) mats[k].K * pairs;
+    }
+    ProfScope prof(s->s);
+    const char * name = nullptr;
+    uint64_t grid = 0;
+    SG_HIP(sgk::launch_matvec(mats, n, (int) s->dev->cus, s->s, &name, &grid, &id), "matvec (fused MUL_MAT_ID) launch");
+    prof.done(name, bytes, flops);
+    return SCRAPGPU_STATUS_OK;
+}
+
 scrapgpu_status api_op_execute(scrapgpu_stream_t * stream, const scrapgpu_op_desc * desc) {
     Stream * s = stream_of(stream);
     if (s == nullptr) return invalid("not a hip stream");
@@ -912,6 +982,13 @@ scrapgpu_status api_plan_build(scrapgpu_device_t * device, const scrapgpu_plan_d
         n.op.outputs = n.out.data();
         n.op.params = n.params.empty() ? nullptr : n.params.data();
     }
+    // MUL_MAT_ID runs sharing x and ids (a MoE layer's gate and up) become one launch
+    for (size_t i = 0; i < p->nodes.size();) {
+        int f = 0;
+        while (f < 2 && i + f + 1 < p->nodes.size() && id_fusable(&p->nodes[i], f + 1, p->nodes[i + f + 1])) ++f;
+        p->nodes[i].fuse = f;
+        i += (size_t) f + 1;
+    }
     *out = reinterpret_cast<scrapgpu_plan_t *>(p.release());
     return SCRAPGPU_STATUS_OK;
 }
@@ -966,8 +1043,8 @@ scrapgpu_status api_plan_execute(scrapgpu_stream_t * stream, scrapgpu_plan_t * p
     SG_HIP(use(s->dev), "hipSetDevice");
     // eager while the per-kernel profiler is on (its events are host-side records) or graphs are off
     if (!graphs_enabled() || g_prof.load(std::memory_order_relaxed) || p->nodes.empty()) {
-        for (PlanNode & n : p->nodes) {
-            const scrapgpu_status st = exec_desc(s, &n.op);
+        for (size_t i = 0; i < p->nodes.size(); i += (size_t) p->nodes[i].fuse + 1) {
+            const scrapgpu_status st = exec_node(s, &p->nodes[i]);
             if (st != SCRAPGPU_STATUS_OK) return st;
         }
         return SCRAPGPU_STATUS_OK;
@@ -977,8 +1054,8 @@ scrapgpu_status api_plan_execute(scrapgpu_stream_t * stream, scrapgpu_plan_t * p
     if (p->exec == nullptr || p->exec_stream != s || p->exec_gen != s->scratch_gen) {
         plan_drop_graph(p);
         SG_HIP(hipStreamBeginCapture(s->s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-        for (PlanNode & n : p->nodes) {
-            st = exec_desc(s, &n.op);
+        for (size_t i = 0; i < p->nodes.size(); i += (size_t) p->nodes[i].fuse + 1) {
+            st = exec_node(s, &p->nodes[i]);
             if (st != SCRAPGPU_STATUS_OK) break;
         }
         hipGraph_t g = nullptr;

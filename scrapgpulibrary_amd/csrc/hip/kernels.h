@@ -49,8 +49,9 @@ struct IdArgs {
 
 // decode matvec for 1 <= N <= 8 (weights streamed once, every column reused in registers).
 // nmat = 1, or 2..3 single-slice products of one dtype and K that share x (one fused launch;
-// mats[j].w / M / y / y_s1 per matrix, everything else from mats[0]). With `id` (nmat = 1, N = 1):
-// the MUL_MAT_ID pairs above instead of the slices of mats[0].
+// mats[j].w / M / y / y_s1 per matrix, everything else from mats[0]). With `id` (N = 1): the
+// MUL_MAT_ID pairs above instead of the slices; nmat > 1 expert tensors then share the ids, x, the
+// expert stride w_s2 and the output strides y_s1 / y_s2.
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
                          uint64_t * grid_size, const IdArgs * id = nullptr);
 

@@ -810,7 +810,11 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     }
     const int nc = (int) a.N;
     if (nc < 1 || nc > 8 || a.K <= 0 || a.K % 32 != 0) return hipErrorInvalidValue;
-    if (id != nullptr && (nmat != 1 || nc != 1 || id->ids == nullptr || id->n_used < 1 || id->n_tok < 1 || id->n_exp < 1)) return hipErrorInvalidValue;
+    if (id != nullptr && (nc != 1 || id->ids == nullptr || id->n_used < 1 || id->n_tok < 1 || id->n_exp < 1)) return hipErrorInvalidValue;
+    for (int j = 1; j < nmat && id != nullptr; ++j) {
+        // several expert tensors under one ids: one expert stride and one output layout
+        if (mats[j].w_s2 != a.w_s2 || mats[j].y_s1 != a.y_s1 || mats[j].y_s2 != a.y_s2) return hipErrorInvalidValue;
+    }
     const int64_t slices = id != nullptr ? id->n_used * id->n_tok : a.ne12 * a.ne13;
     if (slices < 1 || slices > 65535) return hipErrorInvalidValue;
     const int dt = a.dtype;

@@ -234,3 +234,58 @@ def test_mul_mat_id_grouped_plan_reads_ids_on_device(hip):
         sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
     for b in (wb, xb, ib, yb):
         b.free()
+
+
+def test_mul_mat_id_plan_fuses_gate_up(hip):
+    """A plan of a MoE layer's gate and up (same x and ids: one launch) and down (other x): every
+    output against the oracle, on graph replays with new ids and in eager plan mode (profiler on),
+    where the fused pair counts as one launch."""
+    dev, st = hip
+    E, nu, T, H, F = 8, 2, 1, 512, 256
+    rng = np.random.default_rng(91)
+    specs = [("gate", sg.Q4_K, H, F), ("up", sg.Q4_K, H, F), ("down", sg.Q6_K, F, H)]
+    ws, bufs, descs = {}, [], {}
+    for i, (name, dt, K, M) in enumerate(specs):
+        w = O.quantize(dt, O.normal(K * M * E, 92 + i, 0.0, 0.02))
+        b, t = upload_weights(dev, st, dt, w, K, M, slices=E)
+        ws[name] = w
+        descs[name] = t
+        bufs.append(b)
+    xh = O.normal(T * H, 95).reshape(T, 1, H)
+    xf = O.normal(T * nu * F, 96).reshape(T, nu, F)
+    xhb, xfb = dev.alloc(xh.nbytes), dev.alloc(xf.nbytes)
+    xht, xft = sg.tdesc(sg.F32, (H, 1, T), xhb), sg.tdesc(sg.F32, (F, nu, T), xfb)
+    st.upload(xht, xh)
+    st.upload(xft, xf)
+    ib = dev.alloc(4 * nu * T)
+    it = sg.tdesc(sg.I32, (nu, T), ib)
+    ybs = {name: dev.alloc(4 * M * nu * T) for name, _, _, M in specs}
+    yts = {name: sg.tdesc(sg.F32, (M, nu, T), ybs[name]) for name, _, _, M in specs}
+    ops = [sg.mul_mat_id_op(descs[name], xft if name == "down" else xht, it, yts[name], nu) for name, *_ in specs]
+    nodes = (sg.PlanNode * 3)(*[sg.PlanNode(C.sizeof(sg.PlanNode), op, 0) for op, _ in ops])
+    pdesc = sg.PlanDesc(C.sizeof(sg.PlanDesc), nodes, 3)
+    plan = C.c_void_p()
+    sg.check(sg.lib().scrapgpu_plan_build(dev.handle, C.byref(pdesc), C.byref(plan)), "plan_build")
+    try:
+        for rep in range(4):
+            ids = np.stack([rng.permutation(E)[:nu] for _ in range(T)]).astype(np.int32)
+            st.upload(it, ids)
+            eager = rep == 3
+            if eager:
+                sg.lib().scrapgpu_hip_profile_reset()
+                sg.lib().scrapgpu_hip_profile_enable(1)
+            sg.check(sg.lib().scrapgpu_plan_execute(st.handle, plan), "plan_execute")
+            st.sync()
+            if eager:
+                sg.lib().scrapgpu_hip_profile_enable(0)
+                rows = sg.profile_table()
+                assert sum(r["launches"] for r in rows) == 2, rows
+            for name, dt, K, M in specs:
+                x = xf if name == "down" else xh
+                y = st.download(yts[name]).reshape(T, nu, M)
+                deq = O.dequantize(dt, ws[name], K * M * E).reshape(E, M, K)
+                check_pairs(y, O.mul_mat_id(dt, ws[name], K, M, E, x, ids), x, deq, ids)
+    finally:
+        sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
+    for b in bufs + list(ybs.values()) + [xhb, xfb, ib]:
+        b.free()
