@@ -228,6 +228,37 @@ def test_prefill_q4k_large_scales_and_split_groups(hip, K, M, N):
         assert e <= 5e-5, f"rows {rows}: NMSE {e:.3e}"
 
 
+@pytest.mark.parametrize("M,K", [(768, 256), (256, 3072)], ids=["one_k_group", "three_k_groups"])
+def test_prefill_workgroup_per_cu_slices_broadcast_strides(hip, M, K):
+    """The 12-wave prefill kernels over 4 x slices with 2 weight slices (broadcast r2 = 2) and
+    padded x / y column strides: 384-row tiles (M = 768) and 3 K groups (K = 3072), each filling
+    the CUs with 4 slices x 2048 tokens."""
+    dev, st = hip
+    dtype, N, S = sg.Q4_K, 2048, 4
+    q0, _ = quantized(dtype, K, M, 11)
+    q1, _ = quantized(dtype, K, M, 12)
+    wb, wt = upload_weights(dev, st, dtype, np.concatenate([q0, q1]), K, M, slices=2)
+    xs1, ys1 = K + 8, M + 4
+    x = O.normal(S * N * xs1, 13).reshape(S, N, xs1)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N, S), xb, nb=[4, 4 * xs1, 4 * xs1 * N, 4 * xs1 * N * S])
+    st.write(xb, 0, x)
+    yb = dev.alloc(4 * ys1 * N * S)
+    st.write(yb, 0, np.full(ys1 * N * S, -7.0, np.float32))
+    yt = sg.tdesc(sg.F32, (M, N, S), yb, nb=[4, 4 * ys1, 4 * ys1 * N, 4 * ys1 * N * S])
+    op, keep = sg.mul_mat_op(wt, xt, yt, allow_broadcast=1)
+    st.execute(op)
+    st.sync()
+    y = st.read(yb, 0, 4 * ys1 * N * S).view(np.float32).reshape(S, N, ys1)
+    for s in range(S):
+        ref = O.mul_mat(dtype, q0 if s // 2 == 0 else q1, K, M, x[s, :, :K].copy(), threads=8)
+        e = nmse(y[s, :, :M], ref)
+        assert e <= 5e-5, f"slice {s}: NMSE {e:.3e}"
+        assert np.all(y[s, :, M:] == -7.0), "padding of dst was written"
+    for b in (wb, xb, yb):
+        b.free()
+
+
 @pytest.mark.parametrize("dtype", [sg.Q4_0, sg.Q4_K], ids=lambda d: sg.NAMES[d])
 @pytest.mark.parametrize("N", [1, 4, 33])
 def test_slices_broadcast_and_strides(hip, dtype, N):
