@@ -175,7 +175,7 @@ def test_mul_mat_id_grouped_prefill(hip, dtype, shared):
     check_grouped(y, O.mul_mat_id(dtype, w, K, M, E, x, ids))
 
 
-@pytest.mark.parametrize("case", ["tiles64", "skewed", "clamped", "q8_0_ktail"])
+@pytest.mark.parametrize("case", ["tiles64", "skewed", "clamped", "q8_0_ktail", "one_expert_one_slot"])
 def test_mul_mat_id_grouped_cases(hip, case):
     """64-pair tiles (>= 64 pairs per expert); a skewed routing (most pairs on one expert, most
     experts empty); out-of-range ids (clamped on the device); a K that ends inside a stage."""
@@ -192,9 +192,12 @@ def test_mul_mat_id_grouped_cases(hip, case):
     elif case == "clamped":
         E, T, nu = 6, 24, 3
         ids = rng.integers(-4, E + 4, (T, nu)).astype(np.int32)
-    else:
+    elif case == "q8_0_ktail":
         dtype, K, E, T, nu = sg.Q8_0, 544, 5, 20, 3
         ids = np.stack([rng.permutation(E)[:nu] for _ in range(T)]).astype(np.int32)
+    else:
+        E, T, nu = 1, 70, 1
+        ids = np.zeros((T, nu), np.int32)
     w = O.quantize(dtype, O.normal(K * M * E, 72, 0.0, 0.02))
     x = O.normal(T * K, 73).reshape(T, 1, K)
     y = run_mul_mat_id(dev, st, dtype, w, K, M, E, x, ids)
