@@ -430,11 +430,11 @@ __device__ __forceinline__ int xsw(int n, int c) {
 
 // the x tile of one stage: BN tokens x 16 chunks over the 64 W threads of the work-group; thread p
 // loads chunk p % 16 of tokens p / 16 + 4 W i (a thread whose token i lies past the tile repeats
-// its token 0: same data to the same LDS slot). Every load is unconditional, so that the compiler's wait counting
-// stays exact (a load under a branch makes it wait for all loads in flight): tokens past N read
-// token N - 1 (their products land in outputs that are never stored), and chunks past K read the
-// row's last chunk and are zeroed when stored to LDS (the weights there are zero as well, but
-// x could hold an infinity)
+// its token 0: same data to the same LDS slot). Every load is unconditional, so that the
+// compiler's wait counting stays exact (a load under a branch makes it wait for all loads in
+// flight): tokens past N read token N - 1 (their products land in outputs that are never stored),
+// and chunks past K read the row's last chunk and are zeroed when stored to LDS (the weights there
+// are zero as well, but x could hold an infinity). GA: the tokens are gathered rows (init_rows).
 template <int BN, int W, bool GA = false>
 struct XTile {
     static constexpr int NP = (BN * kChunks + 64 * W - 1) / (64 * W);
