@@ -190,6 +190,47 @@ def profile_group(model, group, replays):
     return name, ms, by
 
 
+def bench_layer_prefill(dev, st, model, n_tokens, reps):
+    """One Qwen3-8B Q4_K_M layer's products at prefill (layer 0's weights: q/k/v and gate/up as
+    MUL_MAT_MULTI, o, down in Q6_K) over n_tokens tokens, recorded as one plan; TFLOP/s of the plan
+    replay from HIP events. x: synthetic activations of the products' input widths."""
+    by = {name: (dt, K, M, q) for name, dt, K, M, q in model.weights[0]}
+    bufs = [dev.alloc(4 * HIDDEN * n_tokens), dev.alloc(4 * FFN * n_tokens)]
+    xh = sg.tdesc(sg.F32, (HIDDEN, n_tokens), bufs[0])
+    xf = sg.tdesc(sg.F32, (FFN, n_tokens), bufs[1])
+    st.fill_normal(xh, seed=31)
+    st.fill_normal(xf, seed=32)
+    ys = {}
+    for name, (_, _, M, _) in by.items():
+        bufs.append(dev.alloc(4 * M * n_tokens))
+        ys[name] = sg.tdesc(sg.F32, (M, n_tokens), bufs[-1])
+    keep, nodes = [], []
+    for group in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
+        x = xf if group[0] == "down" else xh
+        if len(group) == 1:
+            op, k = sg.mul_mat_op(by[group[0]][3], x, ys[group[0]])
+        else:
+            op, k = sg.multi_op([by[n][3] for n in group], x, [ys[n] for n in group])
+        keep.append((op, k))
+        nodes.append(sg.PlanNode(C.sizeof(sg.PlanNode), op, 0))
+    arr = (sg.PlanNode * len(nodes))(*nodes)
+    pdesc = sg.PlanDesc(C.sizeof(sg.PlanDesc), arr, len(nodes))
+    plan = C.c_void_p()
+    sg.check(sg.lib().scrapgpu_plan_build(dev.handle, C.byref(pdesc), C.byref(plan)), "plan_build")
+    try:
+        run = lambda: [sg.check(sg.lib().scrapgpu_plan_execute(st.handle, plan), "plan_execute") for _ in range(reps)]
+        run()
+        ms = hip_events_ms(st, run, 3) / reps
+    finally:
+        sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
+        st.sync()
+        for b in bufs:
+            b.free()
+    flops = 2.0 * n_tokens * sum(K * M for dt, K, M, _ in by.values())
+    return {"workload": f"Qwen3-8B Q4_K_M layer products (q/k/v, o, gate/up Q4_K; down Q6_K) at {n_tokens} tokens, one plan",
+            "ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+
+
 def bench_prefill(dev, st, n_tokens, reps):
     """Q4_K prefill: W 12288x4096 and 4096x12288 with x [n_tokens, K]; TFLOP/s from HIP events."""
     L = sg.lib()
@@ -496,6 +537,7 @@ def main():
                            "GBps": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1)} for r in rows}
 
     prefill = None if args.no_prefill else bench_prefill(dev, st, 512, 10)
+    layer_pf = None if args.no_prefill else bench_layer_prefill(dev, st, model, 512, 5)
     moe = None if args.no_moe else bench_moe(dev, st, 20)
     moe_pf = None if args.no_moe else bench_moe_prefill(dev, st, 512, 10)
     get_rows = None if args.no_get_rows else bench_get_rows(dev, st, 512, 5)
@@ -526,6 +568,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_of(dom_group),
                      "bytes_per_launch": dom_bytes, "mean_launch_us": round(dom_ms * 1e3, 3)},
         "prefill_M512": prefill,
+        "prefill_layer_M512": layer_pf,
         "prefill_peak_frac": None if prefill is None else round(max(v["tflops"] for v in prefill.values()) / F16_PEAK_TFLOPS, 4),
         "moe_decode_mul_mat_id": moe,
         "moe_prefill_mul_mat_id": moe_pf,

@@ -737,6 +737,27 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
         fuse = mats[j].dtype == mats[0].dtype && mats[j].K == mats[0].K && mats[j].x == mats[0].x &&
                mats[j].ne12 * mats[j].ne13 == 1 && mats[0].ne12 * mats[0].ne13 == 1;
     }
+    // prefill weights of one dtype reading the same x (one slice each): one GEMM launch over all
+    bool fuse_mm = n > 1 && mats[0].N > 8 && mats[0].ne12 * mats[0].ne13 == 1;
+    for (int j = 1; j < n && fuse_mm; ++j) {
+        fuse_mm = mats[j].dtype == mats[0].dtype && sgk::matmul_same_x(mats[j], mats[0]) && mats[j].ne12 * mats[j].ne13 == 1;
+    }
+    if (fuse_mm) {
+        sgk::MatArgs all = mats[0];
+        double bytes = 0, flops = 0;
+        for (int j = 0; j < n; ++j) {
+            if (j > 0) all.M += mats[j].M;
+            bytes += weight_bytes(mats[j]);
+            flops += 2.0 * (double) mats[j].M * (double) mats[j].K * (double) mats[j].N;
+        }
+        const scrapgpu_status st = ensure_scratch(s, sgk::matmul_scratch_bytes(all, cus));
+        if (st != SCRAPGPU_STATUS_OK) return st;
+        ProfScope prof(s->s);
+        const char * name = nullptr;
+        SG_HIP(sgk::launch_matmul_mfma(mats, n, s->scratch, cus, s->s, &name), "matmul (MULTI) launch");
+        prof.done(name, bytes, flops);
+        return SCRAPGPU_STATUS_OK;
+    }
     const int groups = fuse ? 1 : n;
     if (!fuse && n > 1 && mats[0].N > 8) {
         // prefill products of one MUL_MAT_MULTI: scratch for the largest first, so that products
@@ -766,7 +787,7 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
             ProfScope prof(s->s);
             const char * name = nullptr;
             const bool x_ready = !fuse && gi > 0 && mats[gi - 1].N > 8 && sgk::matmul_same_x(mats[gi - 1], m[0]);
-            SG_HIP(sgk::launch_matmul_mfma(m[0], s->scratch, cus, s->s, &name, x_ready), "matmul launch");
+            SG_HIP(sgk::launch_matmul_mfma(m, 1, s->scratch, cus, s->s, &name, x_ready), "matmul launch");
             prof.done(name, bytes, flops);
         }
     }
@@ -1023,12 +1044,18 @@ scrapgpu_status plan_prepare(Stream * s, Plan * p) {
         }
         if (n.op.op != SCRAPGPU_OP_MUL_MAT && n.op.op != SCRAPGPU_OP_MUL_MAT_MULTI) continue;
         const size_t cnt = n.op.op == SCRAPGPU_OP_MUL_MAT ? 1 : n.op.output_count;
+        sgk::MatArgs all;
+        std::memset(&all, 0, sizeof(all));
         for (size_t i = 0; i < cnt; ++i) {
             sgk::MatArgs a;
             std::memset(&a, 0, sizeof(a));
             const scrapgpu_tensor_desc & x = n.op.op == SCRAPGPU_OP_MUL_MAT ? n.op.inputs[1] : n.op.inputs[cnt];
             if (mul_mat_rule(n.op.inputs[i], x, n.op.outputs[i], 1, &a, nullptr) == SCRAPGPU_STATUS_OK && a.N > 8) {
                 need = std::max(need, sgk::matmul_scratch_bytes(a, (int) s->dev->cus));
+                // a prefill MULTI may run as one launch over all its rows (run_products)
+                if (all.M == 0) all = a;
+                else all.M += a.M;
+                if (i + 1 == cnt && cnt > 1) need = std::max(need, sgk::matmul_scratch_bytes(all, (int) s->dev->cus));
             }
         }
     }

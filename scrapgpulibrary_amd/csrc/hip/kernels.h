@@ -59,8 +59,11 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
 // `scratch` (matmul_scratch_bytes(a, cu_count) bytes of device memory, owned by the stream)
 // receives x as scaled f16 rows with their factors and, when K is split over work-groups, the
 // partial sums.
+// nmat = 1, or 2..3 single-slice weights of one dtype that read the same x (matmul_same_x): one
+// launch over all their row tiles; matmul_scratch_bytes then takes mats[0] with M = the sum of the
+// matrices' M.
 size_t matmul_scratch_bytes(const MatArgs & a, int cu_count);
-hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name,
+hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name,
                               bool x_ready = false);
 // true when b's x pre-pass would write what a's did (same x, shape and dtype class): a product
 // launched right after a's on the same scratch may then pass x_ready and skip its own

@@ -421,6 +421,15 @@ struct MmArgs {
     const int32_t * e_off;
     const int32_t * t_start;
     int32_t n_used, n_exp, x_cols;
+    // nmat weights sharing x (prefill MUL_MAT_MULTI; one slice when nmat > 1): matrix j owns row
+    // tiles mt[j] .. mt[j + 1] and columns mo[j] .. mo[j + 1] of the split-K partials (entries
+    // from nmat on repeat the totals); nmat = 1 mirrors `a`
+    int nmat;
+    int64_t mt[4], mo[4];
+    const uint8_t * wm[3];
+    int64_t Mm[3];
+    float * ym[3];
+    int64_t ys1m[3];
 };
 
 // x tile in LDS: row n (token), 16-byte chunk c at (n * kChunks + (c ^ (n & 15))) * 8 f16
@@ -544,11 +553,14 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     const int64_t tm = tile % L.tiles_m, tn = tile / L.tiles_m;
     const int64_t sl = blockIdx.y;
     const int64_t i2 = sl % L.a.ne12, i3 = sl / L.a.ne12;
-    const uint8_t * w = L.a.w + (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
-    const int64_t K = L.a.K, M = L.a.M, nb = L.a.nb;
+    // the tile's matrix (several when weights share x)
+    const int mj = L.nmat > 1 ? (tm >= L.mt[1] ? (tm >= L.mt[2] ? 2 : 1) : 0) : 0;
+    const uint8_t * w = L.nmat > 1 ? L.wm[mj] : L.a.w + (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
+    const int64_t K = L.a.K, nb = L.a.nb;
+    const int64_t M = L.nmat > 1 ? L.Mm[mj] : L.a.M;
     int64_t N = L.a.N;
     int64_t n0 = tn * BN;
-    const int64_t m0 = tm * BMT + 32 * RG * wave;
+    const int64_t m0 = (tm - L.mt[mj]) * BMT + 32 * RG * wave;
     int32_t * ga_rows = reinterpret_cast<int32_t *>(lds_mm + 2 * BN * BK);    // GA: x row of tile token n
     int64_t * ga_y = reinterpret_cast<int64_t *>(ga_rows + BN);               // GA: its y element offset
     int32_t ga_cnt = BN;                                                      // GA: the tile's pairs
@@ -795,11 +807,12 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     float * y;
     int64_t ys1;
     if (L.split == 1) {
-        y = L.a.y + i2 * L.a.y_s2 + i3 * L.a.y_s3;
-        ys1 = L.a.y_s1;
+        y = L.nmat > 1 ? L.ym[mj] : L.a.y + i2 * L.a.y_s2 + i3 * L.a.y_s3;
+        ys1 = L.nmat > 1 ? L.ys1m[mj] : L.a.y_s1;
     } else {
-        y = L.part + ((uint64_t) split * slices + (uint64_t) sl) * N * M;
-        ys1 = M;
+        const int64_t mt_all = L.mo[L.nmat]; // the partials' row length: all matrices' rows
+        y = L.part + ((uint64_t) split * slices + (uint64_t) sl) * N * mt_all + L.mo[mj];
+        ys1 = mt_all;
     }
     const float * xs = L.xs + (uint64_t) sl * N;
     if constexpr (GA) {
@@ -842,18 +855,23 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
 }
 
 // y = sum of the split-K partials, in split order. blockIdx.x is the row (token n of slice sl),
-// blockIdx.y covers 1024 outputs of it; VEC when M and y's row starts allow float4 accesses.
+// blockIdx.y covers 1024 columns of it (all matrices' rows when several share x; column c is row
+// c - mo[j] of matrix j); VEC when every matrix's rows and y's row starts allow float4 accesses.
 template <bool VEC>
 __global__ __launch_bounds__(256) void k_split_reduce(MmArgs L) {
-    const int64_t N = L.a.N, M = L.a.M;
+    const int64_t N = L.a.N, Mt = L.mo[L.nmat];
     const int64_t row = blockIdx.x, sl = row / N, n = row - sl * N;
     const int64_t i2 = sl % L.a.ne12, i3 = sl / L.a.ne12;
-    const uint64_t plane = (uint64_t) L.a.ne12 * L.a.ne13 * N * M;
-    const float * p = L.part + row * M;
-    float * y = L.a.y + i2 * L.a.y_s2 + i3 * L.a.y_s3 + n * L.a.y_s1;
+    const uint64_t plane = (uint64_t) L.a.ne12 * L.a.ne13 * N * Mt;
+    const float * p = L.part + row * Mt;
+    auto out = [&](int64_t c) -> float * { // y element of column c
+        const int j = c >= L.mo[1] ? (c >= L.mo[2] ? 2 : 1) : 0;
+        float * y = L.nmat > 1 ? L.ym[j] + n * L.ys1m[j] : L.a.y + i2 * L.a.y_s2 + i3 * L.a.y_s3 + n * L.a.y_s1;
+        return y + (c - L.mo[j]);
+    };
     const int64_t m = ((int64_t) blockIdx.y * 256 + threadIdx.x) * 4;
     if (VEC) {
-        if (m >= M) return;
+        if (m >= Mt) return;
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         for (int sp = 0; sp < L.split; ++sp) {
             const float4 u = *reinterpret_cast<const float4 *>(p + sp * plane + m);
@@ -862,12 +880,12 @@ __global__ __launch_bounds__(256) void k_split_reduce(MmArgs L) {
             v.z += u.z;
             v.w += u.w;
         }
-        *reinterpret_cast<float4 *>(y + m) = v;
+        *reinterpret_cast<float4 *>(out(m)) = v;
     } else {
-        for (int64_t e = m; e < m + 4 && e < M; ++e) {
+        for (int64_t e = m; e < m + 4 && e < Mt; ++e) {
             float v = 0.0f;
             for (int sp = 0; sp < L.split; ++sp) v += p[sp * plane + e];
-            y[e] = v;
+            *out(e) = v;
         }
     }
 }
@@ -1138,7 +1156,16 @@ bool matmul_same_x(const MatArgs & a, const MatArgs & b) {
            a.ne13 == b.ne13 && (a.dtype == Q4_K) == (b.dtype == Q4_K);
 }
 
-hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name, bool x_ready) {
+hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name,
+                              bool x_ready) {
+    if (nmat < 1 || nmat > 3) return hipErrorInvalidValue;
+    // several weights: one slice each, one dtype, the same x; the launch sees them as one matrix
+    // of all their rows for its shape choice and scratch
+    MatArgs a = mats[0];
+    for (int j = 1; j < nmat; ++j) {
+        if (mats[j].dtype != a.dtype || !matmul_same_x(mats[j], a) || mats[j].ne12 * mats[j].ne13 != 1 || a.ne12 * a.ne13 != 1) return hipErrorInvalidValue;
+        a.M += mats[j].M;
+    }
     uint16_t * xb = reinterpret_cast<uint16_t *>(scratch);
     const int64_t rows = a.N * a.ne12 * a.ne13;
     float * xs = reinterpret_cast<float *>(scratch + xs_offset(a));
@@ -1163,6 +1190,7 @@ hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     MmArgs L;
+    std::memset(&L, 0, sizeof(L));
     L.a = a;
     L.xb = xb;
     L.xs = xs;
@@ -1172,7 +1200,19 @@ hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count
     const MmConfig cfg = config_of(a, cu_count);
     const int BN = cfg.bn;
     const int bmt = 32 * cfg.rg * (cfg.w / cfg.kg);
-    L.tiles_m = (a.M + bmt - 1) / bmt;
+    // each matrix's rows tiled on their own
+    L.nmat = nmat;
+    L.mt[0] = L.mo[0] = 0;
+    for (int j = 0; j < 3; ++j) {
+        const bool has = j < nmat;
+        L.wm[j] = has ? mats[j].w : nullptr;
+        L.Mm[j] = has ? mats[j].M : 0;
+        L.ym[j] = has ? mats[j].y : nullptr;
+        L.ys1m[j] = has ? mats[j].y_s1 : 0;
+        L.mt[j + 1] = L.mt[j] + (has ? (mats[j].M + bmt - 1) / bmt : 0);
+        L.mo[j + 1] = L.mo[j] + (has ? mats[j].M : 0);
+    }
+    L.tiles_m = L.mt[nmat];
     L.tiles_n = (a.N + BN - 1) / BN;
     L.stages = (a.K + BK - 1) / BK;
     L.split = cfg.split;
@@ -1200,7 +1240,8 @@ hipError_t launch_matmul_mfma(const MatArgs & a, uint8_t * scratch, int cu_count
     }
     e = hipLaunchKernel(fn, grid, dim3((unsigned) (64 * cfg.w)), args, lds, stream);
     if (e != hipSuccess || L.split == 1) return e;
-    const bool yvec = (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 && a.M % 4 == 0 && a.y_s1 % 4 == 0 && a.y_s2 % 4 == 0 && a.y_s3 % 4 == 0;
+    bool yvec = a.y_s2 % 4 == 0 && a.y_s3 % 4 == 0;
+    for (int j = 0; j < nmat; ++j) yvec = yvec && (reinterpret_cast<uintptr_t>(mats[j].y) & 15) == 0 && mats[j].M % 4 == 0 && mats[j].y_s1 % 4 == 0;
     const dim3 rg((unsigned) rows, (unsigned) ((a.M + 1023) / 1024));
     if (yvec)
         hipLaunchKernelGGL(k_split_reduce<true>, rg, dim3(256), 0, stream, L);
@@ -1290,8 +1331,11 @@ hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t 
     L.xsum_row = xsum_row;
     L.part = nullptr;
     L.split = 1;
+    L.nmat = 1;
+    L.mo[1] = L.mo[2] = L.mo[3] = a.M;
     L.stages = (a.K + BK - 1) / BK;
     L.tiles_m = (a.M + 127) / 128;
+    L.mt[1] = L.mt[2] = L.mt[3] = L.tiles_m;
     L.tiles_n = (id.n_used * id.n_tok + bn - 1) / bn + id.n_exp; // at least the tiles the routing makes
     L.pairs = pairs;
     L.e_off = e_off;

@@ -418,6 +418,42 @@ def test_mul_mat_multi_prefill_shares_x(hip, specs):
         b.free()
 
 
+@pytest.mark.parametrize("Ms,K,N", [((200, 64, 40), 1024, 64), ((256, 128, 98), 4096, 64), ((768, 768), 256, 4096)],
+                         ids=["small", "split_k_odd_rows", "workgroup_per_cu"])
+def test_mul_mat_multi_prefill_one_launch(hip, Ms, K, N):
+    """Prefill MUL_MAT_MULTI of one dtype: one GEMM launch over all the weights' row tiles (split-K
+    partials over all their rows, scattered back per weight; 98 rows take the scalar reduce; two
+    768-row weights at 4096 tokens run on 12-wave work-groups). Every output against the oracle."""
+    dev, st = hip
+    dtype = sg.Q4_K
+    x = O.normal(N * K, 550).reshape(N, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    st.upload(xt, x)
+    bufs, wts, yts, refs = [], [], [], []
+    for i, M in enumerate(Ms):
+        q, _ = quantized(dtype, K, M, 560 + i)
+        b, t = upload_weights(dev, st, dtype, q, K, M)
+        yb = dev.alloc(4 * M * N)
+        bufs += [b, yb]
+        wts.append(t)
+        yts.append(sg.tdesc(sg.F32, (M, N), yb))
+        refs.append(O.mul_mat(dtype, q, K, M, x, threads=8))
+    op, keep = sg.multi_op(wts, xt, yts)
+    sg.lib().scrapgpu_hip_profile_reset()
+    sg.lib().scrapgpu_hip_profile_enable(1)
+    st.execute(op)
+    st.sync()
+    sg.lib().scrapgpu_hip_profile_enable(0)
+    rows = sg.profile_table()
+    assert [r["launches"] for r in rows] == [1], rows
+    for M, yt, ref in zip(Ms, yts, refs):
+        e = nmse(st.download(yt).reshape(N, M), ref)
+        assert e <= 5e-5, f"{M} rows: NMSE {e:.3e}"
+    for b in bufs + [xb]:
+        b.free()
+
+
 def test_mul_mat_multi_mixed_dtypes_falls_back(hip):
     """Weights of different dtypes share x: one launch per product, same results."""
     dev, st = hip
