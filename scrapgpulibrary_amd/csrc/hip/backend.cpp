@@ -730,15 +730,28 @@ bool mul_mat_id_grouped(const sgk::MatArgs & a, const sgk::IdArgs & id) {
     return id.n_tok > 8 && id.n_used * id.n_tok >= 4 * id.n_exp && id.n_exp <= 1024 && rows * a.K < ((int64_t) 1 << 31);
 }
 
+// the largest column count that takes the decode matvec (above it: the f16 MFMA GEMM). 8 keeps
+// batch decode on the matvec's integer path (NMSE ~1e-10; the GEMM's f16 operands give ~1e-7);
+// by speed the GEMM wins from 8 columns on the MLP shapes and from 4 (Q6_K, K = 12288)
+int64_t matvec_max_n(const sgk::MatArgs & a) {
+    static const int env = [] {
+        const char * v = std::getenv("SCRAPGPU_HIP_MV_MAXN");
+        return v != nullptr && *v ? std::atoi(v) : 0;
+    }();
+    (void) a;
+    return env >= 1 && env <= 8 ? env : 8;
+}
+
 scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
     const int cus = (int) s->dev->cus;
-    bool fuse = n > 1 && mats[0].N <= 8;
+    const int64_t mv_n = matvec_max_n(mats[0]);
+    bool fuse = n > 1 && mats[0].N <= mv_n;
     for (int j = 1; j < n && fuse; ++j) {
         fuse = mats[j].dtype == mats[0].dtype && mats[j].K == mats[0].K && mats[j].x == mats[0].x &&
                mats[j].ne12 * mats[j].ne13 == 1 && mats[0].ne12 * mats[0].ne13 == 1;
     }
     // prefill weights of one dtype reading the same x (one slice each): one GEMM launch over all
-    bool fuse_mm = n > 1 && mats[0].N > 8 && mats[0].ne12 * mats[0].ne13 == 1;
+    bool fuse_mm = n > 1 && mats[0].N > mv_n && mats[0].ne12 * mats[0].ne13 == 1;
     for (int j = 1; j < n && fuse_mm; ++j) {
         fuse_mm = mats[j].dtype == mats[0].dtype && sgk::matmul_same_x(mats[j], mats[0]) && mats[j].ne12 * mats[j].ne13 == 1;
     }
@@ -759,7 +772,7 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
         return SCRAPGPU_STATUS_OK;
     }
     const int groups = fuse ? 1 : n;
-    if (!fuse && n > 1 && mats[0].N > 8) {
+    if (!fuse && n > 1 && mats[0].N > mv_n) {
         // prefill products of one MUL_MAT_MULTI: scratch for the largest first, so that products
         // reading the same x share one x pre-pass (the scratch stays in place between them)
         size_t need = 0;
@@ -775,7 +788,7 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
             bytes += weight_bytes(m[j]);
             flops += 2.0 * (double) m[j].M * (double) m[j].K * (double) m[j].N * (double) (m[j].ne12 * m[j].ne13);
         }
-        if (m[0].N <= 8) {
+        if (m[0].N <= mv_n) {
             ProfScope prof(s->s);
             const char * name = nullptr;
             uint64_t grid = 0;
@@ -786,7 +799,7 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
             if (st != SCRAPGPU_STATUS_OK) return st;
             ProfScope prof(s->s);
             const char * name = nullptr;
-            const bool x_ready = !fuse && gi > 0 && mats[gi - 1].N > 8 && sgk::matmul_same_x(mats[gi - 1], m[0]);
+            const bool x_ready = !fuse && gi > 0 && mats[gi - 1].N > mv_n && sgk::matmul_same_x(mats[gi - 1], m[0]);
             SG_HIP(sgk::launch_matmul_mfma(m, 1, s->scratch, cus, s->s, &name, x_ready), "matmul launch");
             prof.done(name, bytes, flops);
         }
@@ -1050,7 +1063,7 @@ scrapgpu_status plan_prepare(Stream * s, Plan * p) {
             sgk::MatArgs a;
             std::memset(&a, 0, sizeof(a));
             const scrapgpu_tensor_desc & x = n.op.op == SCRAPGPU_OP_MUL_MAT ? n.op.inputs[1] : n.op.inputs[cnt];
-            if (mul_mat_rule(n.op.inputs[i], x, n.op.outputs[i], 1, &a, nullptr) == SCRAPGPU_STATUS_OK && a.N > 8) {
+            if (mul_mat_rule(n.op.inputs[i], x, n.op.outputs[i], 1, &a, nullptr) == SCRAPGPU_STATUS_OK && a.N > matvec_max_n(a)) {
                 need = std::max(need, sgk::matmul_scratch_bytes(a, (int) s->dev->cus));
                 // a prefill MULTI may run as one launch over all its rows (run_products)
                 if (all.M == 0) all = a;
