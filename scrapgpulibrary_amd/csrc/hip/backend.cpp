@@ -926,10 +926,45 @@ bool id_fusable(const PlanNode * group, int n, const PlanNode & b) {
     return true;
 }
 
-// a plan node and the nodes fused into it (one matvec launch over all their experts)
+// consecutive MUL_MAT nodes of a plan that may run as one MUL_MAT_MULTI: the same x tensor,
+// weights of one dtype and K, one slice, no broadcast, outputs in buffers of their own (none read
+// by another node of the group)
+bool mm_fusable(const PlanNode * group, int n, const PlanNode & b) {
+    const PlanNode & a = group[0];
+    if (a.op.op != SCRAPGPU_OP_MUL_MAT || b.op.op != SCRAPGPU_OP_MUL_MAT) return false;
+    sgk::MatArgs ma, mb;
+    std::memset(&ma, 0, sizeof(ma));
+    std::memset(&mb, 0, sizeof(mb));
+    if (mul_mat_rule(a.op.inputs[0], a.op.inputs[1], a.op.outputs[0], 0, &ma, nullptr) != SCRAPGPU_STATUS_OK ||
+        mul_mat_rule(b.op.inputs[0], b.op.inputs[1], b.op.outputs[0], 0, &mb, nullptr) != SCRAPGPU_STATUS_OK) {
+        return false;
+    }
+    if (!same_tensor(a.op.inputs[1], b.op.inputs[1])) return false;
+    if (ma.dtype != mb.dtype || ma.K != mb.K || ma.ne12 * ma.ne13 != 1 || mb.ne12 * mb.ne13 != 1) return false;
+    const void * xb = a.op.inputs[1].buffer;
+    const void * yb = b.op.outputs[0].buffer;
+    if (yb == xb) return false;
+    for (int k = 0; k < n; ++k) {
+        const void * yk = group[k].op.outputs[0].buffer;
+        if (yk == yb || yk == xb) return false;
+    }
+    return true;
+}
+
+// a plan node and the nodes fused into it: MUL_MAT_IDs sharing x and ids (one matvec launch over
+// all their experts) or MUL_MATs sharing x (run as one MUL_MAT_MULTI)
 scrapgpu_status exec_node(Stream * s, const PlanNode * nodes) {
     if (nodes[0].fuse == 0) return exec_desc(s, &nodes[0].op);
     const int n = nodes[0].fuse + 1;
+    if (nodes[0].op.op == SCRAPGPU_OP_MUL_MAT) {
+        sgk::MatArgs mats[3];
+        for (int k = 0; k < n; ++k) {
+            const scrapgpu_op_desc & op = nodes[k].op;
+            const scrapgpu_status st = product_args(s, op.inputs[0], op.inputs[1], op.outputs[0], 0, &mats[k]);
+            if (st != SCRAPGPU_STATUS_OK) return st;
+        }
+        return run_products(s, mats, n);
+    }
     sgk::MatArgs mats[3];
     sgk::IdArgs id;
     double bytes = 0, flops = 0;
@@ -1016,10 +1051,14 @@ scrapgpu_status api_plan_build(scrapgpu_device_t * device, const scrapgpu_plan_d
         n.op.outputs = n.out.data();
         n.op.params = n.params.empty() ? nullptr : n.params.data();
     }
-    // MUL_MAT_ID runs sharing x and ids (a MoE layer's gate and up) become one launch
+    // runs of MUL_MAT_IDs sharing x and ids (a MoE layer's gate and up) become one launch, runs of
+    // MUL_MATs sharing x (q/k/v, gate/up issued one by one) one MUL_MAT_MULTI
     for (size_t i = 0; i < p->nodes.size();) {
         int f = 0;
-        while (f < 2 && i + f + 1 < p->nodes.size() && id_fusable(&p->nodes[i], f + 1, p->nodes[i + f + 1])) ++f;
+        while (f < 2 && i + f + 1 < p->nodes.size() &&
+               (id_fusable(&p->nodes[i], f + 1, p->nodes[i + f + 1]) || mm_fusable(&p->nodes[i], f + 1, p->nodes[i + f + 1]))) {
+            ++f;
+        }
         p->nodes[i].fuse = f;
         i += (size_t) f + 1;
     }
@@ -1056,6 +1095,20 @@ scrapgpu_status plan_prepare(Stream * s, Plan * p) {
             continue;
         }
         if (n.op.op != SCRAPGPU_OP_MUL_MAT && n.op.op != SCRAPGPU_OP_MUL_MAT_MULTI) continue;
+        if (n.op.op == SCRAPGPU_OP_MUL_MAT && n.fuse > 0) {
+            // MUL_MATs fused into one MULTI: the prefill launch over all their rows
+            sgk::MatArgs all;
+            std::memset(&all, 0, sizeof(all));
+            for (int k = 0; k <= n.fuse; ++k) {
+                const PlanNode & m = (&n)[k];
+                sgk::MatArgs a;
+                std::memset(&a, 0, sizeof(a));
+                if (mul_mat_rule(m.op.inputs[0], m.op.inputs[1], m.op.outputs[0], 0, &a, nullptr) != SCRAPGPU_STATUS_OK) break;
+                if (k == 0) all = a;
+                else all.M += a.M;
+            }
+            if (all.N > matvec_max_n(all)) need = std::max(need, sgk::matmul_scratch_bytes(all, (int) s->dev->cus));
+        }
         const size_t cnt = n.op.op == SCRAPGPU_OP_MUL_MAT ? 1 : n.op.output_count;
         sgk::MatArgs all;
         std::memset(&all, 0, sizeof(all));

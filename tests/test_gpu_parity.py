@@ -454,6 +454,54 @@ def test_mul_mat_multi_prefill_one_launch(hip, Ms, K, N):
         b.free()
 
 
+@pytest.mark.parametrize("N", [1, 64])
+def test_plan_fuses_mul_mats_sharing_x(hip, N):
+    """A plan of separate MUL_MATs q, k, v (same x) and o (another x): the three run as one
+    MUL_MAT_MULTI launch; every output against the oracle, on a graph replay and in eager plan mode
+    (profiler on: 2 launches for the 4 nodes)."""
+    dev, st = hip
+    K, dtype = 512, sg.Q4_K
+    Ms = {"q": 256, "k": 64, "v": 64, "o": 256}
+    x1 = O.normal(N * K, 570).reshape(N, K)
+    x2 = O.normal(N * K, 571).reshape(N, K)
+    bufs, descs, qs, yts = [], {}, {}, {}
+    x1b, x2b = dev.alloc(x1.nbytes), dev.alloc(x2.nbytes)
+    x1t, x2t = sg.tdesc(sg.F32, (K, N), x1b), sg.tdesc(sg.F32, (K, N), x2b)
+    st.upload(x1t, x1)
+    st.upload(x2t, x2)
+    for i, (name, M) in enumerate(Ms.items()):
+        q, _ = quantized(dtype, K, M, 580 + i)
+        b, t = upload_weights(dev, st, dtype, q, K, M)
+        yb = dev.alloc(4 * M * N)
+        bufs += [b, yb]
+        descs[name], qs[name] = t, q
+        yts[name] = sg.tdesc(sg.F32, (M, N), yb)
+    ops = [sg.mul_mat_op(descs[n], x2t if n == "o" else x1t, yts[n]) for n in Ms]
+    nodes = (sg.PlanNode * 4)(*[sg.PlanNode(C.sizeof(sg.PlanNode), op, 0) for op, _ in ops])
+    pdesc = sg.PlanDesc(C.sizeof(sg.PlanDesc), nodes, 4)
+    plan = C.c_void_p()
+    sg.check(sg.lib().scrapgpu_plan_build(dev.handle, C.byref(pdesc), C.byref(plan)), "plan_build")
+    try:
+        for eager in (False, True):
+            if eager:
+                sg.lib().scrapgpu_hip_profile_reset()
+                sg.lib().scrapgpu_hip_profile_enable(1)
+            sg.check(sg.lib().scrapgpu_plan_execute(st.handle, plan), "plan_execute")
+            st.sync()
+            if eager:
+                sg.lib().scrapgpu_hip_profile_enable(0)
+                assert sum(r["launches"] for r in sg.profile_table()) == 2
+            for n, M in Ms.items():
+                x = x2 if n == "o" else x1
+                y = st.download(yts[n]).reshape(N, M)
+                ref = O.mul_mat(dtype, qs[n], K, M, x)
+                assert nmse(y, ref) <= (1e-7 if N == 1 else 5e-5), n
+    finally:
+        sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
+    for b in bufs + [x1b, x2b]:
+        b.free()
+
+
 def test_mul_mat_multi_mixed_dtypes_falls_back(hip):
     """Weights of different dtypes share x: one launch per product, same results."""
     dev, st = hip
