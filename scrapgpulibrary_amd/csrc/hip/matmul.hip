@@ -589,12 +589,16 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     }
     // splits cover whole groups of 4 stages (the host keeps split <= groups), so a stage's
     // position in its group is (s - s0) % 4
-    // (KG > 1: the host keeps the stages a multiple of 4 KG and split 1, so that every K group runs
-    // the same number of stages and barriers)
+    // (KG > 1, split 1: every K group walks gsz = 4 ceil(groups / KG) stages, so that all waves
+    // meet the same barriers; stages past a group's share of K (s >= s1) are inactive: their loads
+    // repeat a valid stage, their k-steps and offsets are skipped)
     const int64_t groups = (L.stages + 3) / 4;
     // (stage indices in 32 bits: K < 2^31 elements, and scalar 32-bit compares)
-    const int s0 = (int) (KG > 1 ? kg * (L.stages / KG) : 4 * (groups * split / L.split));
-    const int s1 = (int) (KG > 1 ? s0 + L.stages / KG : min(4 * (groups * (split + 1) / L.split), L.stages));
+    const int gsz = (int) (4 * ((groups + KG - 1) / KG));
+    const int s0 = (int) (KG > 1 ? kg * gsz : 4 * (groups * split / L.split));
+    const int s1 = (int) (KG > 1 ? min<int64_t>(s0 + gsz, L.stages) : min(4 * (groups * (split + 1) / L.split), L.stages));
+    const int send = KG > 1 ? s0 + gsz : s1;                      // the loop's end (KG > 1: the same count for all)
+    const int lim = s1 > s0 ? s1 - 1 : (int) L.stages - 1;       // the last stage a load may read
 
     F f[RG];
 #pragma unroll
@@ -650,14 +654,17 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
         if constexpr (kOff && D == 0) {
 #pragma unroll
             for (int q = 0; q < NF; ++q)
-                asum[q] = *reinterpret_cast<const f16x8 *>(reinterpret_cast<const uint8_t *>(L.xsum) + 2 * (soff[q] + (uint32_t) (s >> 2) * 16));
+                asum[q] = *reinterpret_cast<const f16x8 *>(reinterpret_cast<const uint8_t *>(L.xsum) + 2 * (soff[q] + (uint32_t) (min(s, lim) >> 2) * 16));
         }
-        const int sn = min(s + 1, s1 - 1), sx = min(s + XD, s1 - 1);
+        const int sn = min(s + 1, lim), sx = min(s + XD, lim);
 #pragma unroll
         for (int i = 0; i < RG; ++i) nw.r[i] = f[i].load(w, sn);
         xl.load(xb, sx * BK, (int) K);
         const uint16_t * X = lds_x + (D & 1) * (BN * BK);
         const int sp = (s & ~3) | D; // = s, with its low bits visible to the compiler
+        // an inactive stage (KG > 1, past the group's share of K) skips everything but its loads,
+        // its x store and the barrier (a wave-uniform branch without global loads)
+        if (KG == 1 || s < s1) {
         typename F::Sc sc[RG];
 #pragma unroll
         for (int i = 0; i < RG; ++i) sc[i] = f[i].prep(cw.r[i], sp);
@@ -740,6 +747,7 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
                     for (int q = 0; q < NF; ++q) acc[i][q] *= ig;
             }
         }
+        } // active stage
         if (s + 1 < s1) xn.store(lds_x + ((D + 1) & 1) * (BN * BK));
         __syncthreads();
     };
@@ -747,9 +755,9 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     XTile<BN, RW, GA> xt2 = xt;
     // every split has at least one stage (the host keeps split <= stages)
 #pragma unroll
-    for (int i = 0; i < RG; ++i) ra.r[i] = f[i].load(w, s0);
-    xt.load(xb, s0 * BK, (int) K);
-    if constexpr (XD == 2) xt2.load(xb, min(s0 + 1, s1 - 1) * BK, (int) K);
+    for (int i = 0; i < RG; ++i) ra.r[i] = f[i].load(w, min(s0, lim));
+    xt.load(xb, min(s0, lim) * BK, (int) K);
+    if constexpr (XD == 2) xt2.load(xb, min(s0 + 1, lim) * BK, (int) K);
     xt.store(lds_x);
     __syncthreads();
     // groups of 4 stages, then the split's last 1..3 outside the loop (a stage under a branch
@@ -761,13 +769,13 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     XTile<BN, RW, GA> & xa = XD == 2 ? xt2 : xt; // x set of stages D = 0, 2 (the next tile's)
     XTile<BN, RW, GA> & xc = xt;                 // of stages D = 1, 3
     int s = s0;
-    for (; s + 3 < s1; s += 4) {
+    for (; s + 3 < send; s += 4) {
         stage(I0{}, s, ra, rb, xa, xc);
         stage(I1{}, s + 1, rb, ra, xc, xa);
         stage(I2{}, s + 2, ra, rb, xa, xc);
         stage(I3{}, s + 3, rb, ra, xc, xa);
     }
-    if (s < s1) {
+    if (s < send) { // (KG > 1: send - s0 is a multiple of 4, no tail)
         stage(I0{}, s, ra, rb, xa, xc);
         if (s + 1 < s1) {
             stage(I1{}, s + 1, rb, ra, xc, xa);
@@ -1089,7 +1097,10 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
         // else 3 K groups of 128-row tiles, when those fill the CUs the same way and K divides
         // into 3 equal runs of whole groups of 4 stages
         const int64_t t4 = (a.M + 127) / 128 * ((a.N + 63) / 64) * slices;
-        const bool fits3 = (t4 % cu_count == 0 || t4 >= 4 * (int64_t) cu_count) && stages % 12 == 0 && stages >= 24;
+        // (the groups take 4 ceil(stages / 12) stages each; the last one's inactive stages, at
+        // most an eighth of the work, wait at the barriers)
+        const int64_t gsz = 4 * (((stages + 3) / 4 + 2) / 3);
+        const bool fits3 = (t4 % cu_count == 0 || t4 >= 4 * (int64_t) cu_count) && stages >= 24 && (3 * gsz - stages) * 8 <= stages;
         if (env_w == 0 && fits3 && env_bn != 128 && env_rg != 2 && env_split <= 1) {
             c.w = 12;
             c.kg = 3;

@@ -191,12 +191,14 @@ def test_prefill_one_workgroup_per_cu(hip, dtype, M, N, K):
 
 
 @pytest.mark.parametrize("dtype,M,N,K", [(sg.Q4_0, 512, 4096, 3072), (sg.Q4_K, 512, 4096, 3072), (sg.Q6_K, 512, 4096, 3072),
-                                         (sg.Q8_0, 200, 8192, 3040)],
-                         ids=["q4_0", "q4_k", "q6_k", "q8_0_partial_rows_ktail"])
+                                         (sg.Q8_0, 200, 8192, 3040), (sg.Q4_K, 512, 4096, 4096), (sg.Q6_K, 512, 4096, 4096),
+                                         (sg.Q8_0, 512, 4096, 4064)],
+                         ids=["q4_0", "q4_k", "q6_k", "q8_0_partial_rows_ktail", "q4_k_uneven", "q6_k_uneven", "q8_0_uneven_ktail"])
 def test_prefill_k_groups(hip, dtype, M, N, K):
-    """Shapes whose 128-row tiles fill the CUs and whose K splits into 3 equal runs of whole
-    4-stage groups: one 12-wave work-group per CU, 3 K groups added in LDS. Q8_0 with K = 3040
-    ends in a partial stage and M = 200 in a partial row tile."""
+    """Shapes whose 128-row tiles fill the CUs: one 12-wave work-group per CU, 3 K groups added in
+    LDS. K = 3072 splits into 3 equal runs; K = 4096 (32 stages) into 12 + 12 + 8 with 4 inactive
+    stages in the last group. Q8_0 with K = 3040 / 4064 ends in a partial stage and M = 200 in a
+    partial row tile."""
     dev, st = hip
     q, _ = quantized(dtype, K, M, 600 + M)
     x = O.normal(N * K, 601).reshape(N, K)
