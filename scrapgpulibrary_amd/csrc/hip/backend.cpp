@@ -866,7 +866,7 @@ scrapgpu_status exec_desc(Stream * s, const scrapgpu_op_desc * desc) {
             if (st != SCRAPGPU_STATUS_OK) return st;
             ProfScope prof(s->s);
             const char * name = nullptr;
-            SG_HIP(sgk::launch_mul_mat_id_mfma(mats[0], id, s->scratch, s->s, &name), "grouped MUL_MAT_ID launch");
+            SG_HIP(sgk::launch_mul_mat_id_mfma(mats[0], id, s->scratch, (int) s->dev->cus, s->s, &name), "grouped MUL_MAT_ID launch");
             prof.done(name, weight_bytes(mats[0]) * (double) id.n_exp, 2.0 * (double) mats[0].M * (double) mats[0].K * pairs);
             return SCRAPGPU_STATUS_OK;
         }

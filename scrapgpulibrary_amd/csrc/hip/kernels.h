@@ -75,7 +75,8 @@ bool matmul_same_x(const MatArgs & a, const MatArgs & b);
 // outputs; each expert's weights are read once per row tile instead of once per pair. `scratch`:
 // mul_mat_id_scratch_bytes(a, id) bytes (a as mul_mat_id_rule fills it; a.N = 1).
 size_t mul_mat_id_scratch_bytes(const MatArgs & a, const IdArgs & id);
-hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t * scratch, hipStream_t stream, const char ** kernel_name);
+hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t * scratch, int cu_count, hipStream_t stream,
+                                  const char ** kernel_name);
 
 // GET_ROWS on R32 weights: dst[:, a, b, c] = dequantized row ids[a, b, c] of slice (b, c) of src0
 // (bit-exact with the dequantizer; out-of-range indices read the nearest row).

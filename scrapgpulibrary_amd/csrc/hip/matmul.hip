@@ -438,8 +438,8 @@ __device__ __forceinline__ int xsw(int n, int c) {
 }
 
 // the x tile of one stage: BN tokens x 16 chunks over the 64 W threads of the work-group; thread p
-// loads chunk p % 16 of tokens p / 16 + 4 W i (a thread whose token i lies past the tile repeats
-// its token 0: same data to the same LDS slot). Every load is unconditional, so that the
+// loads chunk p % 16 of tokens tb + 4 W i, tb = (p / 16) % BN (a thread whose token i lies past
+// the tile repeats its token tb: same data to the same LDS slot). Every load is unconditional, so that the
 // compiler's wait counting stays exact (a load under a branch makes it wait for all loads in
 // flight): tokens past N read token N - 1 (their products land in outputs that are never stored),
 // and chunks past K read the row's last chunk and are zeroed when stored to LDS (the weights there
@@ -459,11 +459,13 @@ struct XTile {
     bool tail;        // ... which reaches past K
     uint4 v[NP];
     int p;            // the thread's index among the 64 W threads that load the tile
+    int tb;           // its first token, (p / 16) % BN (more threads than chunks: repeats)
     __device__ void init(int64_t N, int64_t K, int64_t n0, int p_) {
         p = p_;
+        tb = (p >> 4) % BN;
         kc = 8 * (p & 15);
-        dst = xsw(p >> 4, p & 15); // token + TS i (TS a multiple of 16) keeps the swizzle
-        off = 2 * ((uint32_t) ((n0 + (p >> 4)) * K) + kc);
+        dst = xsw(tb, p & 15); // token + TS i (TS a multiple of 16) keeps the swizzle
+        off = 2 * ((uint32_t) ((n0 + tb) * K) + kc);
         last = 2 * ((uint32_t) ((N - 1) * K) + kc);
         step = (uint32_t) (2 * TS * K);
         kmax = (int) K - 8 - (int) kc;
@@ -473,16 +475,17 @@ struct XTile {
     // GA: the tile's tokens are the x rows rows[0 .. BN) (gathered pairs, repeated past the count)
     __device__ void init_rows(int64_t K, const int32_t * rows, int p_) {
         p = p_;
+        tb = (p >> 4) % BN;
         kc = 8 * (p & 15);
-        dst = xsw(p >> 4, p & 15);
+        dst = xsw(tb, p & 15);
         off = last = step = 0;
         kmax = (int) K - 8 - (int) kc;
         k0 = 0;
         tail = false;
 #pragma unroll
         for (int i = 0; i < (GA ? NP : 1); ++i) {
-            const int n = (p >> 4) + TS * i;
-            offs[i] = 2 * ((uint32_t) rows[n < BN ? n : (p >> 4)] * (uint32_t) K + kc);
+            const int n = tb + TS * i;
+            offs[i] = 2 * ((uint32_t) rows[n < BN ? n : tb] * (uint32_t) K + kc);
         }
     }
     // the stage starting at element k0
@@ -497,7 +500,7 @@ struct XTile {
             if constexpr (GA) {
                 v[i] = *reinterpret_cast<const uint4 *>(base + (offs[i] + k));
             } else {
-                const uint32_t o = (p >> 4) + TS * i < BN ? off + i * step : off;
+                const uint32_t o = tb + TS * i < BN ? off + i * step : off;
                 v[i] = *reinterpret_cast<const uint4 *>(base + (min(o, last) + k));
             }
         }
@@ -509,7 +512,7 @@ struct XTile {
             for (int i = 0; i < NP; ++i) v[i] = zero ? make_uint4(0, 0, 0, 0) : v[i];
         }
 #pragma unroll
-        for (int i = 0; i < NP; ++i) *reinterpret_cast<uint4 *>(X + ((p >> 4) + TS * i < BN ? dst + i * TS * BK : dst)) = v[i];
+        for (int i = 0; i < NP; ++i) *reinterpret_cast<uint4 *>(X + (tb + TS * i < BN ? dst + i * TS * BK : dst)) = v[i];
     }
 };
 
@@ -1285,8 +1288,17 @@ MatArgs ga_xargs(const MatArgs & a, const IdArgs & id) {
 }
 
 template <int DT>
-void * ga_kernel(int bn) {
+void * ga_kernel(int bn, int w) {
+    if (w == 12) return bn == 64 ? (void *) k_matmul<DT, 64, 1, 12, 1, true> : (void *) k_matmul<DT, 32, 1, 12, 1, true>;
     return bn == 64 ? (void *) k_matmul<DT, 64, 1, 4, 1, true> : (void *) k_matmul<DT, 32, 1, 4, 1, true>;
+}
+
+// grouped MUL_MAT_ID work-groups: 12 waves (384-row tiles, one work-group per CU in step) when
+// the experts' row tiles alone (at least one token tile each) come to half the CUs or more
+int ga_waves(const MatArgs & a, const IdArgs & id, int cu_count) {
+    static const int env = env_int("SCRAPGPU_HIP_MMID_W", 0);
+    if (env == 4 || env == 12) return env;
+    return id.n_exp * ((a.M + 383) / 384) * 2 >= cu_count ? 12 : 4;
 }
 
 } // namespace
@@ -1296,7 +1308,7 @@ size_t mul_mat_id_scratch_bytes(const MatArgs & a, const IdArgs & id) {
     return part_offset(px) + (size_t) (2 * (id.n_exp + 1) + id.n_used * id.n_tok) * sizeof(int32_t);
 }
 
-hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t * scratch, hipStream_t stream, const char ** kernel_name) {
+hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name) {
     const MatArgs px = ga_xargs(a, id);
     const int64_t rows = px.N * id.n_tok;
     if (id.n_exp < 1 || id.n_exp > 1024 || rows * a.K >= ((int64_t) 1 << 31) || id.n_used * id.n_tok >= ((int64_t) 1 << 24)) return hipErrorInvalidValue;
@@ -1345,7 +1357,8 @@ hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t 
     L.nmat = 1;
     L.mo[1] = L.mo[2] = L.mo[3] = a.M;
     L.stages = (a.K + BK - 1) / BK;
-    L.tiles_m = (a.M + 127) / 128;
+    const int waves = ga_waves(a, id, cu_count);
+    L.tiles_m = (a.M + 32 * waves - 1) / (32 * waves);
     L.mt[1] = L.mt[2] = L.mt[3] = L.tiles_m;
     L.tiles_n = (id.n_used * id.n_tok + bn - 1) / bn + id.n_exp; // at least the tiles the routing makes
     L.pairs = pairs;
@@ -1357,16 +1370,16 @@ hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t 
     const size_t lds = (size_t) 2 * bn * BK * sizeof(uint16_t) + (size_t) bn * (sizeof(int32_t) + sizeof(int64_t));
     void * fn = nullptr;
     switch (a.dtype) {
-        case Q4_0: fn = ga_kernel<Q4_0>(bn); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q4_0"; break;
-        case Q8_0: fn = ga_kernel<Q8_0>(bn); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q8_0"; break;
-        case Q4_K: fn = ga_kernel<Q4_K>(bn); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q4_k"; break;
-        case Q6_K: fn = ga_kernel<Q6_K>(bn); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q6_k"; break;
+        case Q4_0: fn = ga_kernel<Q4_0>(bn, waves); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q4_0"; break;
+        case Q8_0: fn = ga_kernel<Q8_0>(bn, waves); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q8_0"; break;
+        case Q4_K: fn = ga_kernel<Q4_K>(bn, waves); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q4_k"; break;
+        case Q6_K: fn = ga_kernel<Q6_K>(bn, waves); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q6_k"; break;
         default: return hipErrorInvalidValue;
     }
     const int64_t grid = L.tiles_m * L.tiles_n;
     if (grid >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
     void * args[] = {&L};
-    return hipLaunchKernel(fn, dim3((unsigned) grid), dim3(256), args, lds, stream);
+    return hipLaunchKernel(fn, dim3((unsigned) grid), dim3((unsigned) (64 * waves)), args, lds, stream);
 }
 
 } // namespace sgk

@@ -175,9 +175,9 @@ def test_mul_mat_id_grouped_prefill(hip, dtype, shared):
     check_grouped(y, O.mul_mat_id(dtype, w, K, M, E, x, ids))
 
 
-@pytest.mark.parametrize("case", ["tiles64", "skewed", "clamped", "q8_0_ktail", "one_expert_one_slot"])
+@pytest.mark.parametrize("case", ["tiles64", "skewed", "clamped", "q8_0_ktail", "one_expert_one_slot", "w12_bn32", "w12_bn64"])
 def test_mul_mat_id_grouped_cases(hip, case):
-    """64-pair tiles (>= 64 pairs per expert); a skewed routing (most pairs on one expert, most
+    """64-pair tiles (>= 16 pairs per expert); a skewed routing (most pairs on one expert, most
     experts empty); out-of-range ids (clamped on the device); a K that ends inside a stage."""
     dev, st = hip
     dtype, K, M, E, T, nu = sg.Q4_K, 512, 256, 4, 64, 2
@@ -195,9 +195,15 @@ def test_mul_mat_id_grouped_cases(hip, case):
     elif case == "q8_0_ktail":
         dtype, K, E, T, nu = sg.Q8_0, 544, 5, 20, 3
         ids = np.stack([rng.permutation(E)[:nu] for _ in range(T)]).astype(np.int32)
-    else:
+    elif case == "one_expert_one_slot":
         E, T, nu = 1, 70, 1
         ids = np.zeros((T, nu), np.int32)
+    else:
+        # 128 experts of 384 rows: one 12-wave work-group per (expert, token tile); 4 pairs per
+        # expert on average (32-pair tiles) or 16 (64-pair tiles)
+        M, E, nu = 384, 128, 8
+        T = 64 if case == "w12_bn32" else 256
+        ids = np.stack([rng.permutation(E)[:nu] for _ in range(T)]).astype(np.int32)
     w = O.quantize(dtype, O.normal(K * M * E, 72, 0.0, 0.02))
     x = O.normal(T * K, 73).reshape(T, 1, K)
     y = run_mul_mat_id(dev, st, dtype, w, K, M, E, x, ids)
