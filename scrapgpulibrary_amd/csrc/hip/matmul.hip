@@ -203,6 +203,11 @@ template <> struct PFmt<Q4_K> {
         const uint32_t q = mad24((uint32_t) s * 4, u, qo);
         return Raw{load16(w + q), load16(w + (q + u)), load16(w + mad24((uint32_t) (s >> 1), u, ho))};
     }
+    // stage s = the second half of prev's block: the header is prev's
+    __device__ Raw load_half2(const uint8_t * w, int s, const Raw & prev) const {
+        const uint32_t q = mad24((uint32_t) s * 4, u, qo);
+        return Raw{load16(w + q), load16(w + (q + u)), prev.hd};
+    }
     __device__ Sc prep(const Raw & r, int s, float g = 1.0f) const {
         const int c = 2 * (int) (s & 1) + h;
         const float d = g * half_bits(r.hd.x), dmin = g * half_bits(r.hd.x >> 16);
@@ -281,6 +286,18 @@ template <> struct PFmt<Q6_K> {
         r.d = load_u16(w + mad24(b, u >> 3, dof));
         return r;
     }
+    // stage s = the second half of prev's block: the scales and d are prev's
+    __device__ Raw load_half2(const uint8_t * w, int s, const Raw & prev) const {
+        const uint32_t b = (uint32_t) (s >> 1), n = (uint32_t) (s & 1);
+        Raw r;
+        const uint32_t qa = mad24(12 * b + 4 * n, u, qo);
+        r.qa = load16(w + qa);
+        r.qc = load16(w + qa + 2 * u);
+        r.qh = load16(w + mad24(12 * b + 8 + 2 * n, u, qo));
+        r.sc = prev.sc;
+        r.d = prev.d;
+        return r;
+    }
     // the signed 8-bit scale of run rr sits at byte 8n + h + 2rr (stored xor 0x80): word 2n (runs
     // 0, 1) or 2n + 1 (runs 2, 3), byte h or h + 2
     __device__ Sc prep(const Raw & r, int s) const {
@@ -345,6 +362,8 @@ template <> struct PFmt<Q8_0> {
         }
         return r;
     }
+    // one block per stage: nothing to share between stages
+    __device__ Raw load_half2(const uint8_t * w, int s, const Raw &) const { return load(w, s); }
     __device__ Sc prep(const Raw & r, int) const {
         return Sc{{h2(half_bits(r.d)), h2(half_bits(r.d >> 16))}};
     }
@@ -390,6 +409,8 @@ template <> struct PFmt<Q4_0> {
         }
         return r;
     }
+    // one block per stage: nothing to share between stages
+    __device__ Raw load_half2(const uint8_t * w, int s, const Raw &) const { return load(w, s); }
     __device__ Sc prep(const Raw & r, int) const {
         return Sc{{h2(half_bits(r.d)), h2(half_bits(r.d >> 16))}};
     }
@@ -661,7 +682,12 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
         }
         const int sn = min(s + 1, lim), sx = min(s + XD, lim);
 #pragma unroll
-        for (int i = 0; i < RG; ++i) nw.r[i] = f[i].load(w, sn);
+        for (int i = 0; i < RG; ++i) {
+            // K-quants: a stage is half a block; the odd half reuses the even half's block fields
+            // (sn = s + 1 in the same block, or s itself at the end)
+            if constexpr ((DT == Q4_K || DT == Q6_K) && (D & 1) == 0) nw.r[i] = f[i].load_half2(w, sn, cw.r[i]);
+            else nw.r[i] = f[i].load(w, sn);
+        }
         xl.load(xb, sx * BK, (int) K);
         const uint16_t * X = lds_x + (D & 1) * (BN * BK);
         const int sp = (s & ~3) | D; // = s, with its low bits visible to the compiler
