@@ -444,8 +444,10 @@ struct MmArgs {
     int32_t n_used, n_exp, x_cols;
     // nmat weights sharing x (prefill MUL_MAT_MULTI; one slice when nmat > 1): matrix j owns row
     // tiles mt[j] .. mt[j + 1] and columns mo[j] .. mo[j + 1] of the split-K partials (entries
-    // from nmat on repeat the totals); nmat = 1 mirrors `a`
-    int nmat;
+    // from nmat on repeat the totals); nmat = 1 mirrors `a`. packed: the row tiles run over all
+    // matrices' rows end to end instead (every matrix but the last a whole number of a wave's
+    // 32 RG rows), each wave taking the matrix its rows are in
+    int nmat, packed;
     int64_t mt[4], mo[4];
     const uint8_t * wm[3];
     int64_t Mm[3];
@@ -577,14 +579,17 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     const int64_t tm = tile % L.tiles_m, tn = tile / L.tiles_m;
     const int64_t sl = blockIdx.y;
     const int64_t i2 = sl % L.a.ne12, i3 = sl / L.a.ne12;
-    // the tile's matrix (several when weights share x)
-    const int mj = L.nmat > 1 ? (tm >= L.mt[1] ? (tm >= L.mt[2] ? 2 : 1) : 0) : 0;
+    // the wave's matrix (several when weights share x)
+    const int64_t grow = tm * BMT + 32 * RG * wave; // packed: the wave's first row over all matrices
+    const int mj = L.nmat == 1 ? 0
+                 : L.packed    ? min(L.nmat - 1, grow >= L.mo[1] ? (grow >= L.mo[2] ? 2 : 1) : 0)
+                               : (tm >= L.mt[1] ? (tm >= L.mt[2] ? 2 : 1) : 0);
     const uint8_t * w = L.nmat > 1 ? L.wm[mj] : L.a.w + (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
     const int64_t K = L.a.K, nb = L.a.nb;
     const int64_t M = L.nmat > 1 ? L.Mm[mj] : L.a.M;
     int64_t N = L.a.N;
     int64_t n0 = tn * BN;
-    const int64_t m0 = (tm - L.mt[mj]) * BMT + 32 * RG * wave;
+    const int64_t m0 = L.packed ? grow - L.mo[mj] : (tm - L.mt[mj]) * BMT + 32 * RG * wave;
     int32_t * ga_rows = reinterpret_cast<int32_t *>(lds_mm + 2 * BN * BK);    // GA: x row of tile token n
     int64_t * ga_y = reinterpret_cast<int64_t *>(ga_rows + BN);               // GA: its y element offset
     int32_t ga_cnt = BN;                                                      // GA: the tile's pairs
@@ -1113,14 +1118,20 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
     // (or in enough rounds that the last one matters little) without splitting K, and the
     // last row tile is mostly inside M
     {
+        // (or, with too few tiles for that, when splitting K in 2..4 makes them fit and leaves
+        // every split at least 8 stages)
         const int64_t t12 = (a.M + 383) / 384 * ((a.N + 63) / 64) * slices;
-        const bool fits = (t12 % cu_count == 0 || t12 >= 4 * (int64_t) cu_count) && (a.M % 384 == 0 || a.M >= 8 * 384);
-        if (env_w == 12 || (env_w == 0 && fits && env_bn != 128 && env_rg != 2 && env_split <= 1)) {
+        int s12 = 0;
+        if (a.M % 384 == 0 || a.M >= 8 * 384)
+            for (int sp = 1; sp <= 4 && s12 == 0; ++sp)
+                if (((t12 * sp) % cu_count == 0 || t12 * sp >= 4 * (int64_t) cu_count) && (sp == 1 || stages / sp >= 8)) s12 = sp;
+        if (env_w == 12 || (env_w == 0 && s12 > 0 && env_bn != 128 && env_rg != 2 && env_split <= 1)) {
             c.w = 12;
             c.kg = 1;
             c.bn = 64;
             c.rg = 1;
-            c.split = 1;
+            c.split = env_w == 12 && env_split > 0 ? (int) std::max<int64_t>(1, std::min<int64_t>(std::min(env_split, 8), (stages + 3) / 4))
+                                                   : std::max(s12, 1);
             return c;
         }
         // else 3 K groups of 128-row tiles, when those fill the CUs the same way and K divides
@@ -1252,7 +1263,13 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
         L.mt[j + 1] = L.mt[j] + (has ? (mats[j].M + bmt - 1) / bmt : 0);
         L.mo[j + 1] = L.mo[j] + (has ? mats[j].M : 0);
     }
-    L.tiles_m = L.mt[nmat];
+    L.packed = 0;
+    if (nmat > 1) {
+        L.packed = 1;
+        for (int j = 0; j + 1 < nmat; ++j)
+            if (mats[j].M % (32 * cfg.rg) != 0) L.packed = 0;
+    }
+    L.tiles_m = L.packed ? (a.M + bmt - 1) / bmt : L.mt[nmat];
     L.tiles_n = (a.N + BN - 1) / BN;
     L.stages = (a.K + BK - 1) / BK;
     L.split = cfg.split;
