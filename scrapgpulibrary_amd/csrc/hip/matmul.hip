@@ -487,7 +487,7 @@ struct XTile {
         p = p_;
         tb = (p >> 4) % BN;
         kc = 8 * (p & 15);
-        dst = xsw(tb, p & 15); // token + TS i (TS a multiple of 16) keeps the swizzle
+        dst = xsw(tb, p & 15); // token + TS i keeps the swizzle when TS is a multiple of 16
         off = 2 * ((uint32_t) ((n0 + tb) * K) + kc);
         last = 2 * ((uint32_t) ((N - 1) * K) + kc);
         step = (uint32_t) (2 * TS * K);
@@ -535,7 +535,12 @@ struct XTile {
             for (int i = 0; i < NP; ++i) v[i] = zero ? make_uint4(0, 0, 0, 0) : v[i];
         }
 #pragma unroll
-        for (int i = 0; i < NP; ++i) *reinterpret_cast<uint4 *>(X + (tb + TS * i < BN ? dst + i * TS * BK : dst)) = v[i];
+        for (int i = 0; i < NP; ++i) {
+            const int n = tb + TS * i;
+            // (TS = 24 with 6 loading waves: the token's own swizzle)
+            const int at = n < BN ? (TS % 16 == 0 ? dst + i * TS * BK : xsw(n, p & 15)) : dst;
+            *reinterpret_cast<uint4 *>(X + at) = v[i];
+        }
     }
 };
 
@@ -1125,6 +1130,21 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
         if (a.M % 384 == 0 || a.M >= 8 * 384)
             for (int sp = 1; sp <= 4 && s12 == 0; ++sp)
                 if (((t12 * sp) % cu_count == 0 || t12 * sp >= 4 * (int64_t) cu_count) && (sp == 1 || stages / sp >= 8)) s12 = sp;
+        // 2 K groups of 192-row tiles (6 row waves each) when those fill the CUs with K in two
+        // equal runs of whole groups of 4 stages: no partial sums in HBM
+        const int64_t t6 = (a.M + 191) / 192 * ((a.N + 63) / 64) * slices;
+        const int64_t gsz2 = 4 * (((stages + 3) / 4 + 1) / 2);
+        const bool fits2 = (t6 % cu_count == 0 || t6 >= 4 * (int64_t) cu_count) && (a.M % 192 == 0 || a.M >= 8 * 192) && stages >= 16 &&
+                           (2 * gsz2 - stages) * 8 <= stages;
+        static const int env_kg = env_int("SCRAPGPU_HIP_MM_KG", 0);
+        if (env_w == 0 && s12 > 1 && fits2 && env_kg != 1 && env_bn != 128 && env_rg != 2 && env_split <= 1) {
+            c.w = 12;
+            c.kg = 2;
+            c.bn = 64;
+            c.rg = 1;
+            c.split = 1;
+            return c;
+        }
         if (env_w == 12 || (env_w == 0 && s12 > 0 && env_bn != 128 && env_rg != 2 && env_split <= 1)) {
             c.w = 12;
             c.kg = 1;
@@ -1168,7 +1188,7 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
 
 template <int DT>
 void * kernel_of(const MmConfig & c) {
-    if (c.w == 12) return c.kg == 3 ? (void *) k_matmul<DT, 64, 1, 12, 3> : (void *) k_matmul<DT, 64, 1, 12, 1>;
+    if (c.w == 12) return c.kg == 3 ? (void *) k_matmul<DT, 64, 1, 12, 3> : c.kg == 2 ? (void *) k_matmul<DT, 64, 1, 12, 2> : (void *) k_matmul<DT, 64, 1, 12, 1>;
     if (c.rg == 1) return c.bn == 64 ? (void *) k_matmul<DT, 64, 1, 4, 1> : (void *) k_matmul<DT, 128, 1, 4, 1>;
     return c.bn == 64 ? (void *) k_matmul<DT, 64, 2, 4, 1> : (void *) k_matmul<DT, 128, 2, 4, 1>;
 }

@@ -190,12 +190,14 @@ def test_prefill_one_workgroup_per_cu(hip, dtype, M, N, K):
     assert e <= 5e-5, f"NMSE {e:.3e}"
 
 
-@pytest.mark.parametrize("dtype,M,N,K", [(sg.Q4_K, 768, 4096, 2048), (sg.Q8_0, 768, 4096, 2080), (sg.Q6_K, 384, 8192, 2048)],
-                         ids=["q4_k", "q8_0_ktail", "q6_k"])
-def test_prefill_workgroup_per_cu_split_k(hip, dtype, M, N, K):
-    """Too few 384-row x 64-token tiles to fill the CUs (128): K split in 2 over 12-wave
-    work-groups, partials added in split order. Q8_0 with K = 2080 splits 17 stages into 8 + 9,
-    the last one partial."""
+@pytest.mark.parametrize("dtype,M,N,K", [(sg.Q4_K, 768, 4096, 2048), (sg.Q6_K, 384, 8192, 2048), (sg.Q4_K, 768, 4096, 2304),
+                                         (sg.Q8_0, 768, 4096, 2080)],
+                         ids=["q4_k_kgroups2", "q6_k_kgroups2", "q4_k_split", "q8_0_split_ktail"])
+def test_prefill_workgroup_per_cu_few_tiles(hip, dtype, M, N, K):
+    """Too few 384-row x 64-token tiles to fill the CUs (128). K = 2048 (16 stages): 2 K groups of
+    6 row waves on 192-row tiles (256), added in LDS. K = 2304 / 2080 (18 / 17 stages, not two
+    equal runs of whole groups of 4): K split in 2 over 12-wave work-groups, partials added in split
+    order; Q8_0 with K = 2080 splits 17 stages into 8 + 9, the last one partial."""
     dev, st = hip
     q, _ = quantized(dtype, K, M, 700 + M)
     x = O.normal(N * K, 701).reshape(N, K)
@@ -436,13 +438,15 @@ def test_mul_mat_multi_prefill_shares_x(hip, specs):
 
 
 @pytest.mark.parametrize("Ms,K,N", [((200, 64, 40), 1024, 64), ((256, 128, 98), 4096, 64), ((768, 768), 256, 4096),
-                                    ((512, 128, 128), 2048, 4096)],
-                         ids=["small", "split_k_odd_rows", "workgroup_per_cu", "tiles_across_weights_split_k"])
+                                    ((512, 128, 128), 2048, 4096), ((512, 128, 128), 2304, 4096)],
+                         ids=["small", "split_k_odd_rows", "workgroup_per_cu", "tiles_across_weights_kgroups2",
+                              "tiles_across_weights_split_k"])
 def test_mul_mat_multi_prefill_one_launch(hip, Ms, K, N):
     """Prefill MUL_MAT_MULTI of one dtype: one GEMM launch over all the weights' row tiles (split-K
     partials over all their rows, scattered back per weight; 98 rows take the scalar reduce; two
-    768-row weights at 4096 tokens run on 12-wave work-groups; 512 + 128 + 128 rows as two 384-row
-    tiles that cross the weights' boundaries, K split in 2). Every output against the oracle."""
+    768-row weights at 4096 tokens run on 12-wave work-groups; 512 + 128 + 128 rows as 192-row tiles
+    that cross the weights' boundaries, 2 K groups, or at K = 2304 as 384-row tiles with K split
+    in 2). Every output against the oracle."""
     dev, st = hip
     dtype = sg.Q4_K
     x = O.normal(N * K, 550).reshape(N, K)
