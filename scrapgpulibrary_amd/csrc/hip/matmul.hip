@@ -562,7 +562,7 @@ constexpr int occupancy_of(int dt, int bn, int rg, int w = 4) {
 // work-group finishes alone with one wave per SIMD). KG = 1: 12 row waves, a tile of 384 rows,
 // each x tile serving 3x the rows; KG = 3: 4 row waves x 3 groups that take a third of K each
 // (their own x tiles), added in LDS at the end (split-K without a second pass over memory).
-// GA: grouped MUL_MAT_ID (W = 4, KG = 1, no split): blockIdx.x = token tile * tiles_m + row tile;
+// GA: grouped MUL_MAT_ID (KG = 1, no split): blockIdx.x = token tile * tiles_m + row tile;
 // a token tile belongs to one expert, whose weights the work-group reads, and gathers its pairs'
 // x rows / scatters their outputs through a table in LDS after the x buffers.
 template <int DT, int BN, int RG, int W, int KG, bool GA = false>
@@ -595,7 +595,7 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     int64_t N = L.a.N;
     int64_t n0 = tn * BN;
     const int64_t m0 = L.packed ? grow - L.mo[mj] : (tm - L.mt[mj]) * BMT + 32 * RG * wave;
-    int32_t * ga_rows = reinterpret_cast<int32_t *>(lds_mm + 2 * BN * BK);    // GA: x row of tile token n
+    int32_t * ga_rows = reinterpret_cast<int32_t *>(lds_mm + KG * 2 * BN * BK); // GA: x row of tile token n
     int64_t * ga_y = reinterpret_cast<int64_t *>(ga_rows + BN);               // GA: its y element offset
     int32_t ga_cnt = BN;                                                      // GA: the tile's pairs
     if constexpr (GA) {
@@ -639,7 +639,7 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     for (int i = 0; i < RG; ++i) f[i].init(M, nb, RowAddr(M, m0 + 32 * i + j), h);
     const uint16_t * xb = L.xb + (uint64_t) sl * N * K;
     XTile<BN, RW, GA> xt;
-    if constexpr (GA) xt.init_rows(K, ga_rows, tid);
+    if constexpr (GA) xt.init_rows(K, ga_rows, tid - kg * 64 * RW);
     else xt.init(N, K, n0, tid - kg * 64 * RW);
     uint16_t * const lds_x = lds_mm + kg * (2 * BN * BK); // the K group's two x buffers
     // LDS element offsets of the lane's A fragments: k-step t, token fragment q at aoff[t] + 32 q rows
@@ -1217,6 +1217,21 @@ size_t part_bytes(const MatArgs & a, int split) {
 
 } // namespace
 
+// dynamic LDS beyond the 64 KiB default (gfx950 has 160 KiB per CU): set once per kernel (a
+// kernel's LDS size is fixed by its template arguments)
+static hipError_t allow_lds(void * fn, size_t lds) {
+    if (lds <= 65536) return hipSuccess;
+    static std::mutex mu;
+    static std::vector<void *> done;
+    std::lock_guard<std::mutex> lock(mu);
+    if (std::find(done.begin(), done.end(), fn) == done.end()) {
+        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
+        if (e != hipSuccess) return e;
+        done.push_back(fn);
+    }
+    return hipSuccess;
+}
+
 size_t matmul_scratch_bytes(const MatArgs & a, int cu_count) {
     const int split = config_of(a, cu_count).split;
     return part_offset(a) + (split == 1 ? 0 : part_bytes(a, split));
@@ -1305,16 +1320,7 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
         case Q6_K: fn = kernel_of<Q6_K>(cfg); if (kernel_name) *kernel_name = "matmul_mfma_q6_k"; break;
         default: return hipErrorInvalidValue;
     }
-    if (lds > 65536) { // LDS beyond the 64 KiB default (gfx950 has 160 KiB per CU); set once per kernel
-        static std::mutex mu;
-        static std::vector<void *> done;
-        std::lock_guard<std::mutex> lock(mu);
-        if (std::find(done.begin(), done.end(), fn) == done.end()) {
-            e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
-            if (e != hipSuccess) return e;
-            done.push_back(fn);
-        }
-    }
+    if ((e = allow_lds(fn, lds)) != hipSuccess) return e;
     e = hipLaunchKernel(fn, grid, dim3((unsigned) (64 * cfg.w)), args, lds, stream);
     if (e != hipSuccess || L.split == 1) return e;
     bool yvec = a.y_s2 % 4 == 0 && a.y_s3 % 4 == 0;
@@ -1441,6 +1447,7 @@ hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t 
     }
     const int64_t grid = L.tiles_m * L.tiles_n;
     if (grid >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
+    if ((e = allow_lds(fn, lds)) != hipSuccess) return e;
     void * args[] = {&L};
     return hipLaunchKernel(fn, dim3((unsigned) grid), dim3((unsigned) (64 * waves)), args, lds, stream);
 }
