@@ -190,14 +190,15 @@ def test_prefill_one_workgroup_per_cu(hip, dtype, M, N, K):
     assert e <= 5e-5, f"NMSE {e:.3e}"
 
 
-@pytest.mark.parametrize("dtype,M,N,K", [(sg.Q4_K, 768, 4096, 2048), (sg.Q6_K, 384, 8192, 2048), (sg.Q4_K, 768, 4096, 2304),
-                                         (sg.Q8_0, 768, 4096, 2080)],
-                         ids=["q4_k_kgroups2", "q6_k_kgroups2", "q4_k_split", "q8_0_split_ktail"])
+@pytest.mark.parametrize("dtype,M,N,K", [(sg.Q4_K, 768, 4096, 2048), (sg.Q6_K, 384, 8192, 2048), (sg.Q4_0, 768, 4096, 2048),
+                                         (sg.Q8_0, 768, 4096, 2016), (sg.Q4_K, 768, 4096, 2304), (sg.Q8_0, 768, 4096, 2080)],
+                         ids=["q4_k_kgroups2", "q6_k_kgroups2", "q4_0_kgroups2", "q8_0_kgroups2_ktail", "q4_k_split", "q8_0_split_ktail"])
 def test_prefill_workgroup_per_cu_few_tiles(hip, dtype, M, N, K):
     """Too few 384-row x 64-token tiles to fill the CUs (128). K = 2048 (16 stages): 2 K groups of
     6 row waves on 192-row tiles (256), added in LDS. K = 2304 / 2080 (18 / 17 stages, not two
     equal runs of whole groups of 4): K split in 2 over 12-wave work-groups, partials added in split
-    order; Q8_0 with K = 2080 splits 17 stages into 8 + 9, the last one partial."""
+    order; Q8_0 with K = 2080 splits 17 stages into 8 + 9, the last one partial (K = 2016: 16
+    stages on 2 K groups, the last one partial)."""
     dev, st = hip
     q, _ = quantized(dtype, K, M, 700 + M)
     x = O.normal(N * K, 701).reshape(N, K)
