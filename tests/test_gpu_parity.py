@@ -149,6 +149,20 @@ def test_matvec_decode(hip, dtype, N):
 
 
 @pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+@pytest.mark.parametrize("K", [8448, 12288])
+def test_matvec_decode_three_steps_per_wave(hip, dtype, K):
+    """N = 1 with 33..48 steps of K (the Q6_K down projection's K = 12288): 16 waves of 3 steps;
+    K = 8448 (33 steps) leaves the last waves 2."""
+    dev, st = hip
+    M = 200
+    q, deq = quantized(dtype, K, M, 900 + K % 97)
+    x = O.normal(K, 901).reshape(1, K)
+    y = run_mul_mat(dev, st, dtype, q, K, M, x)
+    ref = O.mul_mat(dtype, q, K, M, x, threads=8)
+    check_matvec(y, ref, x, deq)
+
+
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
 def test_matvec_k_split_repeated(hip, dtype):
     """Few row groups + long K: the split-K path with its arrival counters, run 3 times."""
     dev, st = hip
