@@ -1119,55 +1119,42 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
     const int64_t stages = (a.K + BK - 1) / BK;
     static const int env_w = env_int("SCRAPGPU_HIP_MM_W", 0);
     MmConfig c;
-    // one 12-wave work-group per CU when 384-row tiles of 64 tokens fill the CUs in whole rounds
-    // (or in enough rounds that the last one matters little) without splitting K, and the
-    // last row tile is mostly inside M
+    // 12-wave work-groups, one per CU, in this order of preference:
+    //  1. KG = 1: 384-row tiles of 64 tokens that fill the CUs in whole rounds (or in enough
+    //     rounds that the last one matters little), the last row tile mostly inside M;
+    //  2. KG = 2: 192-row tiles that fill them, K in two equal runs of whole groups of 4 stages;
+    //  3. KG = 3: 128-row tiles that fill them, K in three such runs (the groups take
+    //     4 ceil(stages / 12) stages each; the last one's inactive stages, at most an eighth of
+    //     the work, wait at the barriers);
+    //  4. KG = 1 with K split over 2..4 work-groups (partial sums in HBM, then k_split_reduce)
+    //     when that makes the 384-row tiles fill them, every split at least 8 stages.
     {
-        // (or, with too few tiles for that, when splitting K in 2..4 makes them fit and leaves
-        // every split at least 8 stages)
-        const int64_t t12 = (a.M + 383) / 384 * ((a.N + 63) / 64) * slices;
+        static const int env_kg = env_int("SCRAPGPU_HIP_MM_KG", 0);
+        const bool free_choice = env_w == 0 && env_bn != 128 && env_rg != 2 && env_split <= 1;
+        auto fill = [&](int64_t t) { return t % cu_count == 0 || t >= 4 * (int64_t) cu_count; };
+        const int64_t nt = (a.N + 63) / 64 * slices;
+        const int64_t t12 = (a.M + 383) / 384 * nt, t6 = (a.M + 191) / 192 * nt, t4 = (a.M + 127) / 128 * nt;
         int s12 = 0;
         if (a.M % 384 == 0 || a.M >= 8 * 384)
             for (int sp = 1; sp <= 4 && s12 == 0; ++sp)
-                if (((t12 * sp) % cu_count == 0 || t12 * sp >= 4 * (int64_t) cu_count) && (sp == 1 || stages / sp >= 8)) s12 = sp;
-        // 2 K groups of 192-row tiles (6 row waves each) when those fill the CUs with K in two
-        // equal runs of whole groups of 4 stages: no partial sums in HBM
-        const int64_t t6 = (a.M + 191) / 192 * ((a.N + 63) / 64) * slices;
-        const int64_t gsz2 = 4 * (((stages + 3) / 4 + 1) / 2);
-        const bool fits2 = (t6 % cu_count == 0 || t6 >= 4 * (int64_t) cu_count) && (a.M % 192 == 0 || a.M >= 8 * 192) && stages >= 16 &&
-                           (2 * gsz2 - stages) * 8 <= stages;
-        static const int env_kg = env_int("SCRAPGPU_HIP_MM_KG", 0);
-        if (env_w == 0 && s12 > 1 && fits2 && env_kg != 1 && env_bn != 128 && env_rg != 2 && env_split <= 1) {
-            c.w = 12;
-            c.kg = 2;
-            c.bn = 64;
-            c.rg = 1;
-            c.split = 1;
-            return c;
-        }
-        if (env_w == 12 || (env_w == 0 && s12 > 0 && env_bn != 128 && env_rg != 2 && env_split <= 1)) {
-            c.w = 12;
+                if (fill(t12 * sp) && (sp == 1 || stages / sp >= 8)) s12 = sp;
+        const int64_t gsz2 = 4 * (((stages + 3) / 4 + 1) / 2), gsz3 = 4 * (((stages + 3) / 4 + 2) / 3);
+        const bool fits2 = fill(t6) && (a.M % 192 == 0 || a.M >= 8 * 192) && stages >= 16 && (2 * gsz2 - stages) * 8 <= stages;
+        const bool fits3 = fill(t4) && stages >= 24 && (3 * gsz3 - stages) * 8 <= stages;
+        c.w = 12;
+        c.bn = 64;
+        c.rg = 1;
+        c.split = 1;
+        if (env_w == 12) { // forced: KG = 1, split from SCRAPGPU_HIP_MM_SPLIT
             c.kg = 1;
-            c.bn = 64;
-            c.rg = 1;
-            c.split = env_w == 12 && env_split > 0 ? (int) std::max<int64_t>(1, std::min<int64_t>(std::min(env_split, 8), (stages + 3) / 4))
-                                                   : std::max(s12, 1);
+            if (env_split > 0) c.split = (int) std::max<int64_t>(1, std::min<int64_t>(std::min(env_split, 8), (stages + 3) / 4));
             return c;
         }
-        // else 3 K groups of 128-row tiles, when those fill the CUs the same way and K divides
-        // into 3 equal runs of whole groups of 4 stages
-        const int64_t t4 = (a.M + 127) / 128 * ((a.N + 63) / 64) * slices;
-        // (the groups take 4 ceil(stages / 12) stages each; the last one's inactive stages, at
-        // most an eighth of the work, wait at the barriers)
-        const int64_t gsz = 4 * (((stages + 3) / 4 + 2) / 3);
-        const bool fits3 = (t4 % cu_count == 0 || t4 >= 4 * (int64_t) cu_count) && stages >= 24 && (3 * gsz - stages) * 8 <= stages;
-        if (env_w == 0 && fits3 && env_bn != 128 && env_rg != 2 && env_split <= 1) {
-            c.w = 12;
-            c.kg = 3;
-            c.bn = 64;
-            c.rg = 1;
-            c.split = 1;
-            return c;
+        if (free_choice) {
+            if (s12 == 1 && env_kg != 2 && env_kg != 3) { c.kg = 1; return c; }
+            if (fits2 && env_kg != 1 && env_kg != 3) { c.kg = 2; return c; }
+            if (fits3 && env_kg != 1 && env_kg != 2) { c.kg = 3; return c; }
+            if (s12 > 1 && env_kg != 2 && env_kg != 3) { c.kg = 1; c.split = s12; return c; }
         }
     }
     c.w = 4;
