@@ -598,6 +598,7 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     int32_t * ga_rows = reinterpret_cast<int32_t *>(lds_mm + KG * 2 * BN * BK); // GA: x row of tile token n
     int64_t * ga_y = reinterpret_cast<int64_t *>(ga_rows + BN);               // GA: its y element offset
     int32_t ga_cnt = BN;                                                      // GA: the tile's pairs
+    bool half_tile = false;                                                   // GA: ga_cnt <= 32 (wave-uniform)
     if constexpr (GA) {
         // the expert owning token tile tn: the last e with t_start[e] <= tn (an empty expert
         // shares its start with the next one)
@@ -610,6 +611,7 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
         }
         const int32_t pb = L.e_off[lo] + (int32_t) (tn - L.t_start[lo]) * BN;
         ga_cnt = min(BN, L.e_off[lo + 1] - pb);
+        half_tile = ga_cnt <= 32;
         w = L.a.w + (uint64_t) lo * L.a.w_s2;
         if (tid < BN) {
             const int32_t pr = L.pairs[pb + min(tid, ga_cnt - 1)]; // tokens past the count repeat the last pair
@@ -754,9 +756,12 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
             }
             __builtin_amdgcn_sched_barrier(0); // keep the reads ahead of this step's MFMAs
 #pragma unroll
-            for (int q = 0; q < NF; ++q)
+            for (int q = 0; q < NF; ++q) {
+                // GA: a tile of at most 32 pairs leaves the second token fragment to padding
+                if (GA && q > 0 && half_tile) continue;
 #pragma unroll
                 for (int i = 0; i < RG; ++i) acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c][q], b[c][i], acc[i][q], 0, 0, 0);
+            }
             if (t < 7) {
 #pragma unroll
                 for (int i = 0; i < RG; ++i) b[n][i] = bop_of<kOff, F>(cw.r[i], sc[i], t + 1);
