@@ -60,7 +60,8 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
 // receives x as scaled f16 rows with their factors and, when K is split over work-groups, the
 // partial sums.
 // nmat = 1, or 2..3 single-slice weights of one dtype that read the same x (matmul_same_x): one
-// launch over all their row tiles; matmul_scratch_bytes then takes mats[0] with M = the sum of the
+// launch over all their row tiles (run end to end over all their rows when every weight but the
+// last has a multiple of 32 rows); matmul_scratch_bytes then takes mats[0] with M = the sum of the
 // matrices' M.
 size_t matmul_scratch_bytes(const MatArgs & a, int cu_count);
 hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name,
@@ -71,7 +72,7 @@ bool matmul_same_x(const MatArgs & a, const MatArgs & b);
 
 // MUL_MAT_ID with many tokens (prefill): the (slot, token) pairs are grouped by expert on the
 // device (ids clamped as above), x goes through the matmul's pre-pass once, and the f16 MFMA GEMM
-// runs over (expert, 32- or 64-pair tile, 128-row tile) with gathered x rows and scattered
+// runs over (expert, 32- or 64-pair tile, 128- or 384-row tile) with gathered x rows and scattered
 // outputs; each expert's weights are read once per row tile instead of once per pair. `scratch`:
 // mul_mat_id_scratch_bytes(a, id) bytes (a as mul_mat_id_rule fills it; a.N = 1).
 size_t mul_mat_id_scratch_bytes(const MatArgs & a, const IdArgs & id);
