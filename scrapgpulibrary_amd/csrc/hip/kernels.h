@@ -61,7 +61,7 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
 // partial sums.
 // nmat = 1, or 2..3 single-slice weights of one dtype that read the same x (matmul_same_x): one
 // launch over all their row tiles (run end to end over all their rows when every weight but the
-// last has a multiple of 32 rows); matmul_scratch_bytes then takes mats[0] with M = the sum of the
+// last has a whole number of a wave's 32 or 64 rows); matmul_scratch_bytes then takes mats[0] with M = the sum of the
 // matrices' M.
 size_t matmul_scratch_bytes(const MatArgs & a, int cu_count);
 hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name,
