@@ -729,7 +729,9 @@ __global__ __launch_bounds__(64 * W) void k_mvs(MvArgs A) {
 template <int DT, int RG>
 void * pick_burst_rg(int W, int spw) {
     if (spw <= 2) return W >= 16 ? (void *) k_mvb<DT, RG, 16, 2> : W >= 8 ? (void *) k_mvb<DT, RG, 8, 2> : (void *) k_mvb<DT, RG, 4, 2>;
-    if (spw == 3) return (void *) k_mvb<DT, RG, 16, 3>; // (W = 16 only)
+    if constexpr (RG == 1) {
+        if (spw == 3) return (void *) k_mvb<DT, 1, 16, 3>; // (W = 16 only; 16-row tiles only)
+    }
     return W >= 16 ? (void *) k_mvb<DT, RG, 16, 4> : W >= 8 ? (void *) k_mvb<DT, RG, 8, 4> : (void *) k_mvb<DT, RG, 4, 4>;
 }
 
@@ -865,8 +867,9 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         const bool q4 = dt == Q4_K || dt == Q4_0;
         int rg = q4 && rows * slices >= (int64_t) 96 * cu_count ? 3 : q4 && rows * slices >= (int64_t) 64 * cu_count ? 2 : 1;
         if (const int fr = tuning("SCRAPGPU_HIP_MV_RG", 0)) rg = fr >= 3 ? 3 : fr >= 2 ? 2 : 1;
-        // 3 steps per wave for 33..48 steps (16 waves: no wave loads a step it does not use)
-        const int sp = nst <= 32 ? 2 : nst <= 48 && tuning("SCRAPGPU_HIP_MV_SPW3", 1) ? 3 : 4;
+        // 3 steps per wave for 33..48 steps (16 waves: no wave loads a step it does not use; 16-row
+        // tiles only, the 32- and 48-row ones would spill)
+        const int sp = nst <= 32 ? 2 : nst <= 48 && rg == 1 && tuning("SCRAPGPU_HIP_MV_SPW3", 1) ? 3 : 4;
         int W = 4;
         while (W < 16 && (nst + W - 1) / W > sp) W *= 2;
         set_tiles(L, mats, nmat, 16 * rg);
