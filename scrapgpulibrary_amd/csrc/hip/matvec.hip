@@ -865,10 +865,10 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         // (the 32-row Q8_0 / Q6_K forms need more registers than 5 waves per SIMD leave them)
         // 48-row tiles once they give every CU two work-groups (one round at 4 waves per SIMD)
         const bool q4 = dt == Q4_K || dt == Q4_0;
-        int rg = q4 && rows * slices >= (int64_t) 96 * cu_count ? 3 : q4 && rows * slices >= (int64_t) 64 * cu_count ? 2 : 1;
+        // (past 32 steps of K, 16-row tiles: the 32- and 48-row forms spill at 3-4 steps per wave)
+        int rg = nst > 32 ? 1 : q4 && rows * slices >= (int64_t) 96 * cu_count ? 3 : q4 && rows * slices >= (int64_t) 64 * cu_count ? 2 : 1;
         if (const int fr = tuning("SCRAPGPU_HIP_MV_RG", 0)) rg = fr >= 3 ? 3 : fr >= 2 ? 2 : 1;
-        // 3 steps per wave for 33..48 steps (16 waves: no wave loads a step it does not use; 16-row
-        // tiles only, the 32- and 48-row ones would spill)
+        // 3 steps per wave for 33..48 steps (16 waves: no wave loads a step it does not use)
         const int sp = nst <= 32 ? 2 : nst <= 48 && rg == 1 && tuning("SCRAPGPU_HIP_MV_SPW3", 1) ? 3 : 4;
         int W = 4;
         while (W < 16 && (nst + W - 1) / W > sp) W *= 2;

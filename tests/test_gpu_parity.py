@@ -162,6 +162,20 @@ def test_matvec_decode_three_steps_per_wave(hip, dtype, K):
     check_matvec(y, ref, x, deq)
 
 
+@pytest.mark.parametrize("dtype", [sg.Q4_0, sg.Q4_K], ids=["q4_0", "q4_k"])
+def test_matvec_decode_long_k_many_rows(hip, dtype):
+    """N = 1, K = 12288 (48 steps) over 24576 rows: enough rows for 48-row tiles, which past 32
+    steps give way to 16-row tiles of 3 steps per wave."""
+    dev, st = hip
+    K, M = 12288, 24576
+    q0, d0 = quantized(dtype, K, 96, 950) # 96 rows, repeated (rows are independent)
+    q, deq = np.tile(q0, M // 96), np.tile(d0, (M // 96, 1))
+    x = O.normal(K, 951).reshape(1, K)
+    y = run_mul_mat(dev, st, dtype, q, K, M, x)
+    ref = O.mul_mat(dtype, q, K, M, x, threads=8)
+    check_matvec(y, ref, x, deq)
+
+
 @pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
 def test_matvec_k_split_repeated(hip, dtype):
     """Few row groups + long K: the split-K path with its arrival counters, run 3 times."""
