@@ -46,6 +46,12 @@ SCRAPGPU_API scrapgpu_status scrapgpu_hip_profile_reset(void);
 SCRAPGPU_API scrapgpu_status scrapgpu_hip_profile_read(size_t index, const char ** name, uint64_t * launches, double * total_ms,
                                                       double * bytes, double * flops);
 
+/* The kernel form (a short text such as "burst rg=3 W=4 spw=2" or "gemm w=12 kg=1 bn=64 rg=1
+ * split=1") and work-group count of the calling thread's last matvec / matmul launch, for tests
+ * that pin which kernel a shape selects. `form` receives at most `capacity` bytes including the
+ * terminating NUL. Diagnostic extension; no counterpart in the reference. */
+SCRAPGPU_API scrapgpu_status scrapgpu_hip_last_launch(char * form, size_t capacity, uint64_t * grid);
+
 /* The native hipStream_t of a hip-backend stream (for callers that interoperate with other HIP
  * code); NULL for a stream of another backend. */
 SCRAPGPU_API void * scrapgpu_hip_stream_native(scrapgpu_stream_t * stream);

@@ -86,13 +86,32 @@ def float_to_half(f: np.ndarray) -> np.ndarray:
     return out
 
 
-def quantize(dtype: int, x: np.ndarray) -> np.ndarray:
-    """Natural-layout blocks of the float array x (its size a multiple of the block size)."""
-    x = np.ascontiguousarray(x, dtype=np.float32)
-    out = np.zeros(x.size // BLOCK[dtype] * TYPE_SIZE[dtype], np.uint8)
-    st = lib().sgo_quantize(dtype, _p(x), _p(out), x.size)
-    if st != 0:
-        raise ValueError(f"sgo_quantize status {st}")
+def quantize(dtype: int, x: np.ndarray, threads: int = 1) -> np.ndarray:
+    """Natural-layout blocks of the float array x (its size a multiple of the block size). Blocks
+    are quantized independently, so `threads` > 1 splits x into runs of whole blocks quantized in
+    parallel (ctypes releases the GIL); the bytes are the same."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    bs, ts = BLOCK[dtype], TYPE_SIZE[dtype]
+    out = np.zeros(x.size // bs * ts, np.uint8)
+    nblk = x.size // bs
+    if threads <= 1 or nblk < 4096:
+        st = lib().sgo_quantize(dtype, _p(x), _p(out), x.size)
+        if st != 0:
+            raise ValueError(f"sgo_quantize status {st}")
+        return out
+    import concurrent.futures as cf
+
+    cuts = [nblk * i // threads for i in range(threads + 1)]
+
+    def run(i):
+        b0, b1 = cuts[i], cuts[i + 1]
+        xs, qs = x[b0 * bs:b1 * bs], out[b0 * ts:b1 * ts]
+        return lib().sgo_quantize(dtype, _p(xs), _p(qs), xs.size) if b1 > b0 else 0
+
+    with cf.ThreadPoolExecutor(threads) as ex:
+        sts = list(ex.map(run, range(threads)))
+    if any(sts):
+        raise ValueError(f"sgo_quantize status {max(sts)}")
     return out
 
 

@@ -52,14 +52,6 @@ class MulMatParams(C.Structure):
     _fields_ = [("struct_size", C.c_size_t), ("allow_broadcast", C.c_int)]
 
 
-class GetRowsParams(C.Structure):
-    _fields_ = [("struct_size", C.c_size_t), ("indices_are_i64", C.c_int)]
-
-
-class MulMatIdParams(C.Structure):
-    _fields_ = [("struct_size", C.c_size_t), ("n_used", C.c_uint32), ("max_prompt_tokens", C.c_uint32)]
-
-
 class DeviceInfo(C.Structure):
     _fields_ = [("struct_size", C.c_size_t), ("name", C.c_char_p), ("vendor", C.c_char_p), ("platform_name", C.c_char_p),
                 ("driver_version", C.c_char_p), ("backend_name", C.c_char_p), ("reported_api_version", C.c_char_p),
@@ -124,6 +116,7 @@ _SIGS = {
     "scrapgpu_hip_profile_read": (C.c_int, [C.c_size_t, C.POINTER(C.c_char_p), C.POINTER(C.c_uint64), C.POINTER(C.c_double),
                                             C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "scrapgpu_hip_stream_native": (C.c_void_p, [C.c_void_p]),
+    "scrapgpu_hip_last_launch": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_uint64)]),
 }
 
 
@@ -311,6 +304,14 @@ class Device:
         r = C.c_char_p()
         st = lib().scrapgpu_op_supported(self.handle, C.byref(op), C.byref(r))
         return st, (r.value.decode() if r.value else "")
+
+
+def last_launch() -> tuple[str, int]:
+    """(form, work-groups) of this thread's last matvec / matmul launch (scrapgpu_hip_last_launch)."""
+    buf = C.create_string_buffer(96)
+    grid = C.c_uint64()
+    check(lib().scrapgpu_hip_last_launch(buf, 96, C.byref(grid)), "hip_last_launch")
+    return buf.value.decode(), grid.value
 
 
 def profile_table() -> list[dict]:

@@ -899,9 +899,36 @@ bool same_tensor(const scrapgpu_tensor_desc & a, const scrapgpu_tensor_desc & b)
     return true;
 }
 
+// true when the byte ranges of two tensors share a byte of one buffer
+bool overlap(const scrapgpu_tensor_desc & a, const scrapgpu_tensor_desc & b) {
+    if (a.buffer == nullptr || a.buffer != b.buffer) return false;
+    const uint64_t ea = a.offset + sg::nbytes(a), eb = b.offset + sg::nbytes(b);
+    return a.offset < eb && b.offset < ea;
+}
+
+// node b may join a fused group (nodes group[0..n)) only when running them as one launch reads
+// and writes what running them in order would: b's output overlaps no input or output of the
+// group, and no output of the group overlaps an input of b (checked by byte ranges, so that
+// tensors that share one buffer at different offsets still fuse)
+bool outputs_apart(const PlanNode * group, int n, const PlanNode & b) {
+    const scrapgpu_tensor_desc & yb = b.op.outputs[0];
+    for (int k = 0; k < n; ++k) {
+        const scrapgpu_op_desc & g = group[k].op;
+        const scrapgpu_tensor_desc & yk = g.outputs[0];
+        if (overlap(yk, yb)) return false;
+        for (size_t i = 0; i < g.input_count; ++i)
+            if (overlap(g.inputs[i], yb)) return false;
+        for (size_t i = 0; i < b.op.input_count; ++i)
+            if (overlap(yk, b.op.inputs[i])) return false;
+    }
+    for (size_t i = 0; i < b.op.input_count; ++i)
+        if (overlap(b.op.inputs[i], yb)) return false;
+    return true;
+}
+
 // consecutive MUL_MAT_ID nodes of a plan that may share one launch: the same x and ids, experts
-// of one dtype, K, count and stride, outputs of one layout in buffers of their own (none read by
-// another node of the group), and the decode path (the grouped path runs one op per launch)
+// of one dtype, K, count and stride, outputs of one layout apart from every tensor of the group
+// (outputs_apart), and the decode path (the grouped path runs one op per launch)
 bool id_fusable(const PlanNode * group, int n, const PlanNode & b) {
     const PlanNode & a = group[0];
     if (a.op.op != SCRAPGPU_OP_MUL_MAT_ID || b.op.op != SCRAPGPU_OP_MUL_MAT_ID) return false;
@@ -915,20 +942,12 @@ bool id_fusable(const PlanNode * group, int n, const PlanNode & b) {
     if (!same_tensor(a.op.inputs[1], b.op.inputs[1]) || !same_tensor(a.op.inputs[2], b.op.inputs[2])) return false;
     if (ma.dtype != mb.dtype || ma.K != mb.K || ma.w_s2 != mb.w_s2 || ia.n_exp != ib.n_exp || ia.n_used != ib.n_used) return false;
     if (ma.y_s1 != mb.y_s1 || ma.y_s2 != mb.y_s2) return false;
-    const void * xb = a.op.inputs[1].buffer;
-    const void * ids = a.op.inputs[2].buffer;
-    const void * yb = b.op.outputs[0].buffer;
-    if (yb == xb || yb == ids) return false;
-    for (int k = 0; k < n; ++k) {
-        const void * yk = group[k].op.outputs[0].buffer;
-        if (yk == yb || yk == xb || yk == ids) return false;
-    }
-    return true;
+    return outputs_apart(group, n, b);
 }
 
 // consecutive MUL_MAT nodes of a plan that may run as one MUL_MAT_MULTI: the same x tensor,
-// weights of one dtype and K, one slice, no broadcast, outputs in buffers of their own (none read
-// by another node of the group)
+// weights of one dtype and K, one slice, no broadcast, outputs apart from every tensor of the
+// group (outputs_apart)
 bool mm_fusable(const PlanNode * group, int n, const PlanNode & b) {
     const PlanNode & a = group[0];
     if (a.op.op != SCRAPGPU_OP_MUL_MAT || b.op.op != SCRAPGPU_OP_MUL_MAT) return false;
@@ -941,14 +960,7 @@ bool mm_fusable(const PlanNode * group, int n, const PlanNode & b) {
     }
     if (!same_tensor(a.op.inputs[1], b.op.inputs[1])) return false;
     if (ma.dtype != mb.dtype || ma.K != mb.K || ma.ne12 * ma.ne13 != 1 || mb.ne12 * mb.ne13 != 1) return false;
-    const void * xb = a.op.inputs[1].buffer;
-    const void * yb = b.op.outputs[0].buffer;
-    if (yb == xb) return false;
-    for (int k = 0; k < n; ++k) {
-        const void * yk = group[k].op.outputs[0].buffer;
-        if (yk == yb || yk == xb) return false;
-    }
-    return true;
+    return outputs_apart(group, n, b);
 }
 
 // a plan node and the nodes fused into it: MUL_MAT_IDs sharing x and ids (one matvec launch over
@@ -1396,6 +1408,16 @@ scrapgpu_status scrapgpu_hip_profile_read(size_t index, const char ** name, uint
     if (total_ms) *total_ms = e.ms;
     if (bytes) *bytes = e.bytes;
     if (flops) *flops = e.flops;
+    return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status scrapgpu_hip_last_launch(char * form, size_t capacity, uint64_t * grid) {
+    const sgk::LaunchForm & f = sgk::last_form();
+    if (form != nullptr && capacity > 0) {
+        std::strncpy(form, f.form, capacity - 1);
+        form[capacity - 1] = '\0';
+    }
+    if (grid != nullptr) *grid = f.grid;
     return SCRAPGPU_STATUS_OK;
 }
 

@@ -10,6 +10,14 @@ namespace sgk {
 
 enum : int { F32 = 0, Q4_0 = 16, Q8_0 = 17, Q4_K = 32, Q6_K = 33 };
 
+// The form the calling thread's last matvec / matmul launch chose ("burst rg=3 W=4 spw=2", ...)
+// and its work-group count: a diagnostic that lets tests pin the kernel a shape selects.
+struct LaunchForm {
+    char form[96];
+    uint64_t grid;
+};
+LaunchForm & last_form();
+
 // R32 area table of one dtype (the same numbers as sg::r32_geometry)
 struct Areas {
     int na;

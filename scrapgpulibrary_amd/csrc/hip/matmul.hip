@@ -30,6 +30,7 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -1313,6 +1314,8 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
         default: return hipErrorInvalidValue;
     }
     if ((e = allow_lds(fn, lds)) != hipSuccess) return e;
+    std::snprintf(last_form().form, sizeof(last_form().form), "gemm w=%d kg=%d bn=%d rg=%d split=%d", cfg.w, cfg.kg, BN, cfg.rg, L.split);
+    last_form().grid = (uint64_t) grid.x * grid.y;
     e = hipLaunchKernel(fn, grid, dim3((unsigned) (64 * cfg.w)), args, lds, stream);
     if (e != hipSuccess || L.split == 1) return e;
     bool yvec = a.y_s2 % 4 == 0 && a.y_s3 % 4 == 0;

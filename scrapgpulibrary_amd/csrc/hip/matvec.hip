@@ -50,10 +50,16 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdio>
 #include <cstdlib>
 #include <vector>
 
 namespace sgk {
+
+LaunchForm & last_form() {
+    thread_local LaunchForm f{{0}, 0};
+    return f;
+}
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -866,8 +872,9 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         // 48-row tiles once they give every CU two work-groups (one round at 4 waves per SIMD)
         const bool q4 = dt == Q4_K || dt == Q4_0;
         // (past 32 steps of K, 16-row tiles: the 32- and 48-row forms spill at 3-4 steps per wave)
-        int rg = nst > 32 ? 1 : q4 && rows * slices >= (int64_t) 96 * cu_count ? 3 : q4 && rows * slices >= (int64_t) 64 * cu_count ? 2 : 1;
+        int rg = q4 && rows * slices >= (int64_t) 96 * cu_count ? 3 : q4 && rows * slices >= (int64_t) 64 * cu_count ? 2 : 1;
         if (const int fr = tuning("SCRAPGPU_HIP_MV_RG", 0)) rg = fr >= 3 ? 3 : fr >= 2 ? 2 : 1;
+        if (nst > 32) rg = 1; // (also over the override)
         // 3 steps per wave for 33..48 steps (16 waves: no wave loads a step it does not use)
         const int sp = nst <= 32 ? 2 : nst <= 48 && rg == 1 && tuning("SCRAPGPU_HIP_MV_SPW3", 1) ? 3 : 4;
         int W = 4;
@@ -878,6 +885,8 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         void * fn = dt == Q4_0 ? pick_burst<Q4_0>(W, sp, rg) : dt == Q8_0 ? pick_burst<Q8_0>(W, sp, rg)
                   : dt == Q4_K ? pick_burst<Q4_K>(W, sp, rg) : pick_burst<Q6_K>(W, sp, rg);
         if (grid_size) *grid_size = (uint64_t) L.tiles * (uint64_t) slices;
+        std::snprintf(last_form().form, sizeof(last_form().form), "burst rg=%d W=%d spw=%d", rg, W, sp);
+        last_form().grid = (uint64_t) L.tiles * (uint64_t) slices;
         void * args[] = {&L};
         return hipLaunchKernel(fn, dim3((unsigned) L.tiles, (unsigned) slices), dim3((unsigned) (64 * W)), args, lds, stream);
     }
@@ -901,6 +910,8 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     const int64_t rounds = (L.tiles + cap - 1) / cap;
     const int64_t grid_x = (L.tiles + rounds - 1) / rounds;
     if (grid_size) *grid_size = (uint64_t) grid_x * (uint64_t) slices;
+    std::snprintf(last_form().form, sizeof(last_form().form), "stream nc=%d W=%d", nc, W);
+    last_form().grid = (uint64_t) grid_x * (uint64_t) slices;
     void * args[] = {&L};
     return hipLaunchKernel(fn, dim3((unsigned) grid_x, (unsigned) slices), dim3((unsigned) (64 * W)), args, lds, stream);
 }

@@ -164,21 +164,24 @@ def test_matvec_decode_three_steps_per_wave(hip, dtype, K):
 
 @pytest.mark.parametrize("dtype", [sg.Q4_0, sg.Q4_K], ids=["q4_0", "q4_k"])
 def test_matvec_decode_long_k_many_rows(hip, dtype):
-    """N = 1, K = 12288 (48 steps) over 24576 rows: enough rows for 48-row tiles, which past 32
-    steps give way to 16-row tiles of 3 steps per wave."""
+    """N = 1, K = 12288 (48 steps) over 96 rows per CU: enough rows for 48-row tiles, which past 32
+    steps give way to 16-row tiles of 3 steps per wave (the launch must show 16-row tiles)."""
     dev, st = hip
-    K, M = 12288, 24576
+    K, M = 12288, 96 * dev.info().compute_units
     q0, d0 = quantized(dtype, K, 96, 950) # 96 rows, repeated (rows are independent)
     q, deq = np.tile(q0, M // 96), np.tile(d0, (M // 96, 1))
     x = O.normal(K, 951).reshape(1, K)
     y = run_mul_mat(dev, st, dtype, q, K, M, x)
+    form, grid = sg.last_launch()
+    assert form == "burst rg=1 W=16 spw=3" and grid == M // 16, (form, grid)
     ref = O.mul_mat(dtype, q, K, M, x, threads=8)
     check_matvec(y, ref, x, deq)
 
 
 @pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
 def test_matvec_k_split_repeated(hip, dtype):
-    """Few row groups + long K: the split-K path with its arrival counters, run 3 times."""
+    """Few row groups + long K (N = 2, 64 steps): the streaming matvec, whose waves split K and
+    add their partial sums in LDS in wave order; three runs, each against the oracle."""
     dev, st = hip
     K, M, N = 16384, 64, 2
     q, deq = quantized(dtype, K, M, 7)

@@ -253,6 +253,13 @@ def test_mul_mat_threads_identical():
     assert np.array_equal(O.mul_mat(O.Q6_K, q, K, M, x, threads=1), O.mul_mat(O.Q6_K, q, K, M, x, threads=7))
 
 
+@pytest.mark.parametrize("dt", [16, 17, 32, 33])
+def test_quantize_threads_identical(dt):
+    """quantize(threads=n) splits x into runs of whole blocks: the same bytes as one call."""
+    x = O.normal(256 * 4099, 41, 0.0, 0.5)
+    assert np.array_equal(O.quantize(dt, x, threads=7), O.quantize(dt, x))
+
+
 def test_mul_mat_broadcast_and_strides():
     """dst[i2] = W[i2 / r2] x[i2] with padded strides (ops.cpp:909-917, ref_ops_tests.cpp:659-753)."""
     K, M, N = 64, 5, 3
