@@ -46,6 +46,19 @@ SCRAPGPU_API scrapgpu_status scrapgpu_hip_profile_reset(void);
 SCRAPGPU_API scrapgpu_status scrapgpu_hip_profile_read(size_t index, const char ** name, uint64_t * launches, double * total_ms,
                                                       double * bytes, double * flops);
 
+/* scrapgpu_op_execute for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * It runs the same kernels as scrapgpu_op_execute, but the scratch those kernels need (the prefill
+ * GEMM's f16 activations and split-K partial sums, the grouped MUL_MAT_ID's routing tables) comes
+ * from a static array of 32 MiB per GPU that the library holds until the process ends, instead of
+ * the stream's scratch, which scrapgpu_op_execute grows with hipMalloc; it calls no hipMalloc or
+ * hipFree, and the event profiler stays off during the call. An op that needs more than 32 MiB of
+ * scratch is refused with SCRAPGPU_STATUS_UNSUPPORTED and a reason (decode matvecs need none;
+ * prefill needs about 2 * N * K bytes plus, for split-K shapes, 4 * splits * N * M bytes).
+ * Every call on one GPU shares that GPU's array: calls whose work overlaps on one GPU (two
+ * streams, two threads) race on it; serialize them. */
+SCRAPGPU_API scrapgpu_status scrapgpu_hip_op_execute_static(scrapgpu_stream_t * stream, const scrapgpu_op_desc * desc);
+
 /* The kernel form (a short text such as "burst rg=3 W=4 spw=2" or "gemm w=12 kg=1 bn=64 rg=1
  * split=1") and work-group count of the calling thread's last matvec / matmul launch, for tests
  * that pin which kernel a shape selects. `form` receives at most `capacity` bytes including the

@@ -116,6 +116,7 @@ _SIGS = {
     "scrapgpu_hip_profile_read": (C.c_int, [C.c_size_t, C.POINTER(C.c_char_p), C.POINTER(C.c_uint64), C.POINTER(C.c_double),
                                             C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "scrapgpu_hip_stream_native": (C.c_void_p, [C.c_void_p]),
+    "scrapgpu_hip_op_execute_static": (C.c_int, [C.c_void_p, C.POINTER(OpDesc)]),
     "scrapgpu_hip_last_launch": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_uint64)]),
 }
 

@@ -91,6 +91,7 @@ struct Device {
     std::mutex mu;          // guards the staging buffer and the profiling records
     uint8_t * staging = nullptr;
     size_t staging_size = 0;
+    uint8_t * static_scratch = nullptr; // this device's copy of `scratch` (below), or null
 };
 
 struct PlanNode {
@@ -158,6 +159,9 @@ struct ProfEntry {
 };
 
 std::atomic<bool> g_prof{false};
+// while a scrapgpu_hip_op_execute_static call runs on this thread: its device's static scratch
+// (the profiler stays off then: its events are allocations)
+thread_local uint8_t * t_static_scratch = nullptr;
 std::mutex g_prof_mu;
 std::vector<ProfRecord> g_prof_pending;
 std::vector<ProfEntry> g_prof_table;
@@ -168,7 +172,7 @@ struct ProfScope {
     double bytes = 0, flops = 0;
     hipEvent_t a = nullptr, b = nullptr;
     explicit ProfScope(hipStream_t st) : s(st) {
-        if (g_prof.load(std::memory_order_relaxed) && hipEventCreate(&a) == hipSuccess && hipEventCreate(&b) == hipSuccess) {
+        if (g_prof.load(std::memory_order_relaxed) && t_static_scratch == nullptr && hipEventCreate(&a) == hipSuccess && hipEventCreate(&b) == hipSuccess) {
             hipEventRecord(a, s);
         } else {
             a = b = nullptr;
@@ -400,6 +404,17 @@ scrapgpu_status api_stream_sync(scrapgpu_stream_t * stream) {
     return SCRAPGPU_STATUS_OK;
 }
 
+} // namespace
+
+// The scratch of scrapgpu_hip_op_execute_static: a file-scope device array, so that entry point
+// allocates nothing. Each GPU holds its own copy (its address comes from hipGetSymbolAddress at
+// registration, per device; the host-side name is not a device address and is never passed to a
+// kernel). Every static call on one GPU shares it.
+constexpr size_t kStaticScratchBytes = (size_t) 32 << 20;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+namespace {
+
 // stream scratch: grown on demand; the stream is drained before the old block is released
 scrapgpu_status ensure_scratch(Stream * s, size_t bytes) {
     if (bytes <= s->scratch_size) return SCRAPGPU_STATUS_OK;
@@ -412,6 +427,24 @@ scrapgpu_status ensure_scratch(Stream * s, size_t bytes) {
     s->scratch_size = n;
     s->scratch_gen = g_scratch_gen.fetch_add(1);
     return SCRAPGPU_STATUS_OK;
+}
+
+// `bytes` of scratch for the op being enqueued: the device's static array inside
+// scrapgpu_hip_op_execute_static (refused past its size, nothing allocated), else the stream's
+// scratch, grown on demand
+scrapgpu_status scratch_for(Stream * s, size_t bytes, uint8_t ** out) {
+    if (t_static_scratch != nullptr) {
+        if (bytes > kStaticScratchBytes) {
+            return set_err(SCRAPGPU_STATUS_UNSUPPORTED, "the op needs " + std::to_string(bytes) + " bytes of scratch; the static scratch of "
+                                                        "scrapgpu_hip_op_execute_static holds " + std::to_string(kStaticScratchBytes) +
+                                                        " (run it with scrapgpu_op_execute)");
+        }
+        *out = t_static_scratch;
+        return SCRAPGPU_STATUS_OK;
+    }
+    const scrapgpu_status st = ensure_scratch(s, bytes);
+    *out = s->scratch;
+    return st;
 }
 
 scrapgpu_device_t * api_stream_device(scrapgpu_stream_t * stream) {
@@ -763,11 +796,12 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
             bytes += weight_bytes(mats[j]);
             flops += 2.0 * (double) mats[j].M * (double) mats[j].K * (double) mats[j].N;
         }
-        const scrapgpu_status st = ensure_scratch(s, sgk::matmul_scratch_bytes(all, cus));
+        uint8_t * scr = nullptr;
+        const scrapgpu_status st = scratch_for(s, sgk::matmul_scratch_bytes(all, cus), &scr);
         if (st != SCRAPGPU_STATUS_OK) return st;
         ProfScope prof(s->s);
         const char * name = nullptr;
-        SG_HIP(sgk::launch_matmul_mfma(mats, n, s->scratch, cus, s->s, &name), "matmul (MULTI) launch");
+        SG_HIP(sgk::launch_matmul_mfma(mats, n, scr, cus, s->s, &name), "matmul (MULTI) launch");
         prof.done(name, bytes, flops);
         return SCRAPGPU_STATUS_OK;
     }
@@ -777,7 +811,8 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
         // reading the same x share one x pre-pass (the scratch stays in place between them)
         size_t need = 0;
         for (int j = 0; j < n; ++j) need = std::max(need, sgk::matmul_scratch_bytes(mats[j], cus));
-        const scrapgpu_status st = ensure_scratch(s, need);
+        uint8_t * scr = nullptr;
+        const scrapgpu_status st = scratch_for(s, need, &scr);
         if (st != SCRAPGPU_STATUS_OK) return st;
     }
     for (int gi = 0; gi < groups; ++gi) {
@@ -795,12 +830,13 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
             SG_HIP(sgk::launch_matvec(m, cnt, cus, s->s, &name, &grid), "matvec launch");
             prof.done(name, bytes, flops);
         } else {
-            const scrapgpu_status st = ensure_scratch(s, sgk::matmul_scratch_bytes(m[0], cus));
+            uint8_t * scr = nullptr;
+            const scrapgpu_status st = scratch_for(s, sgk::matmul_scratch_bytes(m[0], cus), &scr);
             if (st != SCRAPGPU_STATUS_OK) return st;
             ProfScope prof(s->s);
             const char * name = nullptr;
             const bool x_ready = !fuse && gi > 0 && mats[gi - 1].N > mv_n && sgk::matmul_same_x(mats[gi - 1], m[0]);
-            SG_HIP(sgk::launch_matmul_mfma(m, 1, s->scratch, cus, s->s, &name, x_ready), "matmul launch");
+            SG_HIP(sgk::launch_matmul_mfma(m, 1, scr, cus, s->s, &name, x_ready), "matmul launch");
             prof.done(name, bytes, flops);
         }
     }
@@ -862,11 +898,12 @@ scrapgpu_status exec_desc(Stream * s, const scrapgpu_op_desc * desc) {
         const double pairs = (double) (id.n_used * id.n_tok);
         if (mul_mat_id_grouped(mats[0], id)) {
             // many tokens: pairs grouped by expert on the device, one MFMA GEMM over them
-            st = ensure_scratch(s, sgk::mul_mat_id_scratch_bytes(mats[0], id));
+            uint8_t * scr = nullptr;
+            st = scratch_for(s, sgk::mul_mat_id_scratch_bytes(mats[0], id), &scr);
             if (st != SCRAPGPU_STATUS_OK) return st;
             ProfScope prof(s->s);
             const char * name = nullptr;
-            SG_HIP(sgk::launch_mul_mat_id_mfma(mats[0], id, s->scratch, (int) s->dev->cus, s->s, &name), "grouped MUL_MAT_ID launch");
+            SG_HIP(sgk::launch_mul_mat_id_mfma(mats[0], id, scr, (int) s->dev->cus, s->s, &name), "grouped MUL_MAT_ID launch");
             prof.done(name, weight_bytes(mats[0]) * (double) id.n_exp, 2.0 * (double) mats[0].M * (double) mats[0].K * pairs);
             return SCRAPGPU_STATUS_OK;
         }
@@ -1308,8 +1345,9 @@ scrapgpu_status scrapgpu_hip_register(void) {
             p = *end == ',' ? end + 1 : end;
         }
     }
-    int rt = 0;
+    int rt = 0, cur = 0;
     hipRuntimeGetVersion(&rt);
+    const bool had_cur = hipGetDevice(&cur) == hipSuccess;
     for (int i = 0; i < n; ++i) {
         if (!allow.empty() && std::find(allow.begin(), allow.end(), i) == allow.end()) continue;
         hipDeviceProp_t prop;
@@ -1325,8 +1363,13 @@ scrapgpu_status scrapgpu_hip_register(void) {
         d->total_mem = prop.totalGlobalMem;
         d->lds = prop.sharedMemPerBlock;
         d->cus = (uint32_t) prop.multiProcessorCount;
+        // this device's copy of the static scratch (scrapgpu_hip_op_execute_static refuses to run
+        // where the lookup failed)
+        void * sp = nullptr;
+        if (hipSetDevice(i) == hipSuccess && hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)) == hipSuccess) d->static_scratch = static_cast<uint8_t *>(sp);
         r.devices.push_back(std::move(d));
     }
+    if (had_cur) hipSetDevice(cur); // (the static scratch lookups made each device current in turn)
     if (const char * env = std::getenv("SCRAPGPU_HIP_PROFILE")) g_prof.store(env[0] == '1');
     r.registered = true;
     const scrapgpu_status st = scrapgpu_register_backend(&kVtable);
@@ -1409,6 +1452,19 @@ scrapgpu_status scrapgpu_hip_profile_read(size_t index, const char ** name, uint
     if (bytes) *bytes = e.bytes;
     if (flops) *flops = e.flops;
     return SCRAPGPU_STATUS_OK;
+}
+
+scrapgpu_status scrapgpu_hip_op_execute_static(scrapgpu_stream_t * stream, const scrapgpu_op_desc * desc) {
+    Stream * s = stream_of(stream);
+    if (s == nullptr) return invalid("not a hip stream");
+    if (desc == nullptr) return invalid("op desc is null");
+    if (s->dev->static_scratch == nullptr) {
+        return set_err(SCRAPGPU_STATUS_BACKEND_ERROR, "the static scratch of this device could not be located (hipGetSymbolAddress failed at registration)");
+    }
+    t_static_scratch = s->dev->static_scratch;
+    const scrapgpu_status st = exec_desc(s, desc);
+    t_static_scratch = nullptr;
+    return st;
 }
 
 scrapgpu_status scrapgpu_hip_last_launch(char * form, size_t capacity, uint64_t * grid) {

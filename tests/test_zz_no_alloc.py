@@ -1,0 +1,68 @@
+"""scrapgpu_hip_op_execute_static: the no-allocation variant of scrapgpu_op_execute, through the
+C-ABI. Its output must equal scrapgpu_op_execute's (the same kernels run on the same inputs, so
+bit for bit) on consecutive calls that share the static scratch, the second on a smaller input;
+an op needing more scratch than the static array holds is refused with a reason."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as O
+import scrapgpulibrary_amd as sg
+from tests.gpu_util import quantized, upload_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(dev, st, wt, x, M, static):
+    N, K = x.shape
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    st.upload(xt, x)
+    yb = dev.alloc(4 * M * N)
+    st.write(yb, 0, np.full(M * N, np.nan, np.float32))
+    yt = sg.tdesc(sg.F32, (M, N), yb)
+    op, keep = sg.mul_mat_op(wt, xt, yt)
+    if static:
+        sg.check(sg.lib().scrapgpu_hip_op_execute_static(st.handle, C.byref(op)), "hip_op_execute_static")
+    else:
+        st.execute(op)
+    st.sync()
+    y = st.download(yt).reshape(N, M).copy()
+    xb.free()
+    yb.free()
+    return y
+
+
+@pytest.mark.parametrize("dtype", [sg.Q4_K, sg.Q6_K], ids=lambda d: sg.NAMES[d])
+def test_static_scratch_matches_op_execute(hip, dtype):
+    dev, st = hip
+    K, M = 4096, 1536
+    q, _ = quantized(dtype, K, M, 1500)
+    wb, wt = upload_weights(dev, st, dtype, q, K, M)
+    # prefill at 512 tokens (f16 x in the scratch), then 64 tokens (split-K partials as well), then
+    # one decode column (no scratch): each against scrapgpu_op_execute and the oracle
+    for N in (512, 64, 1):
+        x = O.normal(N * K, 1501 + N).reshape(N, K)
+        y_static = _run(dev, st, wt, x, M, True)
+        form = sg.last_launch()[0]
+        y_plain = _run(dev, st, wt, x, M, False)
+        assert np.array_equal(y_static.view(np.uint32), y_plain.view(np.uint32)), f"N={N} [{form}]: outputs differ"
+        ref = O.mul_mat(dtype, q, K, M, x, threads=8)
+        e = float(np.sum((y_static.astype(np.float64) - ref) ** 2) / np.sum(ref.astype(np.float64) ** 2))
+        assert e <= (1e-7 if N <= 8 else 5e-5), f"N={N}: NMSE {e:.3e}"
+    wb.free()
+
+
+def test_static_scratch_refuses_large_ops(hip):
+    dev, st = hip
+    K, M, N = 12288, 256, 2048  # 2 N K = 48 MiB of f16 activations > 32 MiB
+    q, _ = quantized(sg.Q4_K, K, M, 1502)
+    wb, wt = upload_weights(dev, st, sg.Q4_K, q, K, M)
+    xb, yb = dev.alloc(4 * N * K), dev.alloc(4 * M * N)
+    op, keep = sg.mul_mat_op(wt, sg.tdesc(sg.F32, (K, N), xb), sg.tdesc(sg.F32, (M, N), yb))
+    stt = sg.lib().scrapgpu_hip_op_execute_static(st.handle, C.byref(op))
+    assert stt == sg.UNSUPPORTED
+    assert b"static scratch" in sg.lib().scrapgpu_last_error()
+    for b in (wb, xb, yb):
+        b.free()
