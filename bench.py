@@ -15,6 +15,10 @@ Reported on one JSON line:
                 `traffic` = HBM bytes per launch from the committed rocprofv3 PMC summary
   prefill       Q4_K M=512 (N=512 tokens) MFMA TFLOP/s on the two MLP shapes, vs 2.5 PFLOP/s dense f16/bf16
   cpu_baseline  the reference's CPU MUL_MAT (oracle/_ref; the oracle when absent), 1 thread, one gate matrix, N=1
+  configs       BASELINE.json's other workloads, one line each at their own shapes (Q4_0 4096x4096;
+                Q8_0 Llama-7B MLP at N=1,4,8; Q4_K prefill at N=64..2048; the Q6_K LM head at
+                N=1,8,64; the 70B-class Q4_K MLP), decode weights cycled over distinct copies that
+                exceed the MALL, each with the reference CPU MUL_MAT (1 thread) timed beside it
 """
 from __future__ import annotations
 
@@ -118,22 +122,6 @@ class Model:
 
     def token(self):
         sg.check(sg.lib().scrapgpu_plan_execute(self.st.handle, self.plan), "plan_execute")
-
-
-def profile_kernels(model, tokens):
-    L = sg.lib()
-    model.st.sync()
-    L.scrapgpu_hip_profile_reset()
-    L.scrapgpu_hip_profile_enable(1)
-    try:
-        for _ in range(tokens):
-            model.token()
-        model.st.sync()
-    finally:
-        L.scrapgpu_hip_profile_enable(0)
-    rows = sg.profile_table()
-    L.scrapgpu_hip_profile_reset()
-    return rows
 
 
 def hip_runtime():
@@ -460,6 +448,142 @@ def cpu_baseline(dev, st, model, seconds):
                       f"host {cpu}, nproc {os.cpu_count()}"}
 
 
+# ---- BASELINE.json's other workloads, one line each ---------------------------------------------
+
+MALL_BYTES = 256 << 20
+
+
+def device_weights(dev, st, dtype, K, M, copies, seed):
+    """`copies` distinct R32 weights M x K ~ N(0, 0.02), quantized on the device (the reference
+    quantizer's bytes); copies > 1 so that a timing loop over them streams from HBM, not the MALL."""
+    tmp = dev.alloc(4 * K * M)
+    out = []
+    for c in range(copies):
+        b = dev.alloc(weight_bytes(dtype, K, M))
+        st.fill_normal(sg.tdesc(sg.F32, (K, M), tmp), seed=seed + c, mean=0.0, std=0.02)
+        d = sg.tdesc(dtype, (K, M), b, layout=sg.R32)
+        st.quantize(sg.tdesc(sg.F32, (K, M), tmp), d)
+        out.append((b, d))
+    st.sync()
+    tmp.free()
+    return out
+
+
+def copies_for(nbytes):
+    """Distinct copies whose total exceeds the 256 MB MALL 1.5 times over (at least one)."""
+    return max(1, -(-int(1.5 * MALL_BYTES) // nbytes))
+
+
+def time_plan(dev, st, ops, replays):
+    """Mean ms per op of `ops` recorded as one plan (a HIP graph) and replayed between HIP events."""
+    nodes = (sg.PlanNode * len(ops))(*[sg.PlanNode(C.sizeof(sg.PlanNode), op, 0) for op in ops])
+    pdesc = sg.PlanDesc(C.sizeof(sg.PlanDesc), nodes, len(ops))
+    plan = C.c_void_p()
+    sg.check(sg.lib().scrapgpu_plan_build(dev.handle, C.byref(pdesc), C.byref(plan)), "plan_build")
+    try:
+        run = lambda: [sg.check(sg.lib().scrapgpu_plan_execute(st.handle, plan), "plan_execute") for _ in range(replays)]
+        run()
+        ms = hip_events_ms(st, run, 3) / (replays * len(ops))
+    finally:
+        sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
+    return ms
+
+
+def cpu_ms(dtype, nat, K, M, x, budget_s):
+    """Median ms of the reference's CPU MUL_MAT (oracle/_ref; the oracle's C restatement when that
+    library is absent), one thread, over as many calls as fit `budget_s` (at least one)."""
+    import oracle as O
+
+    run = (lambda: O.ref_mul_mat(dtype, nat, K, M, x)) if O.ref_available() else (lambda: O.mul_mat(dtype, nat, K, M, x))
+    times = []
+    t_end = time.time() + budget_s
+    while not times or (time.time() < t_end and len(times) < 7):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)) * 1e3, len(times)
+
+
+def decode_line(dev, st, dtype, K, M, N, copies, seed, cpu_budget):
+    """GB/s of weights for W x at N columns (weights streamed from HBM: distinct copies cycled),
+    with the CPU reference beside it."""
+    ws = device_weights(dev, st, dtype, K, M, copies, seed)
+    xb, yb = dev.alloc(4 * K * N), dev.alloc(4 * M * N)
+    xt, yt = sg.tdesc(sg.F32, (K, N), xb), sg.tdesc(sg.F32, (M, N), yb)
+    st.fill_normal(xt, seed=seed + 99)
+    keep = [sg.mul_mat_op(d, xt, yt) for _, d in ws]
+    st.execute(keep[0][0])
+    st.sync()
+    form = sg.last_launch()[0]
+    ms = time_plan(dev, st, [op for op, _ in keep], max(3, 40 // len(keep)))
+    by = weight_bytes(dtype, K, M)
+    out = {"kernel": form, "us": round(ms * 1e3, 2), "GBps": round(by / (ms * 1e-3) / 1e9, 1),
+           "hbm_frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "GFLOPs": round(2.0 * M * K * N / (ms * 1e-3) / 1e9, 1)}
+    if cpu_budget > 0:
+        nat = st.download(ws[0][1], np.uint8)
+        x = st.download(xt).reshape(N, K).copy()
+        cms, n = cpu_ms(dtype, nat, K, M, x, cpu_budget)
+        out["cpu"] = {"ms": round(cms, 2), "GBps": round(by / (cms * 1e-3) / 1e9, 3), "GFLOPs": round(2.0 * M * K * N / (cms * 1e-3) / 1e9, 2),
+                      "runs": n}
+    for b, _ in ws:
+        b.free()
+    xb.free()
+    yb.free()
+    return out
+
+
+def prefill_line(dev, st, dtype, K, M, N, seed, cpu_budget):
+    """TFLOP/s of W x at N tokens on the MFMA path, with the CPU reference beside it."""
+    ws = device_weights(dev, st, dtype, K, M, 2, seed)
+    xb, yb = dev.alloc(4 * K * N), dev.alloc(4 * M * N)
+    xt, yt = sg.tdesc(sg.F32, (K, N), xb), sg.tdesc(sg.F32, (M, N), yb)
+    st.fill_normal(xt, seed=seed + 99)
+    keep = [sg.mul_mat_op(d, xt, yt) for _, d in ws]
+    st.execute(keep[0][0])
+    st.sync()
+    form = sg.last_launch()[0]
+    ms = time_plan(dev, st, [op for op, _ in keep], 10)
+    fl = 2.0 * M * K * N
+    out = {"kernel": form, "us": round(ms * 1e3, 2), "TFLOPs": round(fl / (ms * 1e-3) / 1e12, 1),
+           "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / F16_PEAK_TFLOPS, 4)}
+    if cpu_budget > 0:
+        nat = st.download(ws[0][1], np.uint8)
+        x = st.download(xt).reshape(N, K).copy()
+        cms, n = cpu_ms(dtype, nat, K, M, x, cpu_budget)
+        out["cpu"] = {"ms": round(cms, 1), "GFLOPs": round(fl / (cms * 1e-3) / 1e9, 2), "runs": n}
+    for b, _ in ws:
+        b.free()
+    xb.free()
+    yb.free()
+    return out
+
+
+def bench_configs(dev, st, cpu_budget):
+    """BASELINE.json configs[0], [1], [3], [4] (configs[2] is the main line)."""
+    res = {}
+    by = weight_bytes(sg.Q4_0, 4096, 4096)
+    res["1_q4_0_4096x4096"] = {"N1": decode_line(dev, st, sg.Q4_0, 4096, 4096, 1, copies_for(by), 100, cpu_budget)}
+    log("config 1 done")
+    c2 = {}
+    for K, M in ((4096, 11008), (11008, 4096)):
+        by = weight_bytes(sg.Q8_0, K, M)
+        c2[f"{M}x{K}"] = {f"N{N}": decode_line(dev, st, sg.Q8_0, K, M, N, copies_for(by), 200 + N, cpu_budget) for N in (1, 4, 8)}
+    res["2_q8_0_llama7b_mlp"] = c2
+    log("config 2 done")
+    c4 = {}
+    for K, M in ((4096, 12288), (12288, 4096)):
+        c4[f"{M}x{K}"] = {f"N{N}": prefill_line(dev, st, sg.Q4_K, K, M, N, 300 + N, cpu_budget) for N in (64, 128, 512, 2048)}
+    res["4_q4_k_prefill"] = c4
+    log("config 4 done")
+    by = weight_bytes(sg.Q6_K, 4096, 151936)
+    res["5_q6_k_lm_head_151936x4096"] = {f"N{N}": (decode_line(dev, st, sg.Q6_K, 4096, 151936, N, 1, 400 + N, cpu_budget) if N <= 8
+                                                   else prefill_line(dev, st, sg.Q6_K, 4096, 151936, N, 400 + N, cpu_budget)) for N in (1, 8, 64)}
+    by = weight_bytes(sg.Q4_K, 8192, 28672)
+    res["5_q4_k_70b_mlp_28672x8192"] = {"N1": decode_line(dev, st, sg.Q4_K, 8192, 28672, 1, copies_for(by), 500, cpu_budget)}
+    log("config 5 done")
+    return res
+
+
 def traffic_of(kernel):
     """HBM bytes per launch of `kernel` from the committed PMC summary, or None."""
     try:
@@ -469,19 +593,6 @@ def traffic_of(kernel):
         return None
     k = t.get("kernels", {}).get(kernel)
     return None if k is None else k.get("hbm_bytes_per_launch")
-
-
-def calibrate():
-    """A plain device copy of 256 MiB, 5 times (torch): the reference reading of FETCH_SIZE and
-    WRITE_SIZE for rocprofv3 --pmc (each launch reads and writes exactly 256 MiB)."""
-    import torch
-
-    a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
-    b = torch.empty_like(a)
-    for _ in range(5):
-        b.copy_(a)
-    torch.cuda.synchronize()
-    print(json.dumps({"calibration": "device copy", "bytes_per_launch": 256 << 20, "launches": 5}))
 
 
 def main():
@@ -495,12 +606,10 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-moe", action="store_true", help="skip the MUL_MAT_ID (MoE decode and prefill) lines")
     ap.add_argument("--no-get-rows", action="store_true", help="skip the GET_ROWS line")
+    ap.add_argument("--no-configs", action="store_true", help="skip the lines of BASELINE.json's other workloads")
+    ap.add_argument("--config-cpu-seconds", type=float, default=2.0, help="CPU reference budget per config line (at least one call)")
     ap.add_argument("--no-fuse", action="store_true", help="one MUL_MAT per weight instead of MUL_MAT_MULTI for q/k/v and gate/up")
-    ap.add_argument("--calibrate", action="store_true", help="only run the 256 MiB copy that calibrates the PMC byte counters")
     args = ap.parse_args()
-    if args.calibrate:
-        calibrate()
-        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one MI355X per run); use --gpus 1",
               file=sys.stderr)
@@ -522,8 +631,6 @@ def main():
     ms_step = dt / args.steps * 1e3
     gbs = model.bytes_per_token * args.steps / dt / 1e9
 
-    rows = profile_kernels(model, 3)
-    ktime = sum(r["ms"] for r in rows) / 3
     # the roofline kernel: the token's largest product (gate+up fused, 2 x 12288x4096 Q4_K)
     dom_group = "gate+up" if "gate+up" in model.by_group else "gate"
     groups = {}
@@ -533,8 +640,6 @@ def main():
     dom_name, dom_bytes = groups[dom_group]["kernel"], groups[dom_group]["bytes"]
     dom_ms = groups[dom_group]["mean_us"] * 1e-3
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
-    kernels = {r["name"]: {"launches_per_token": r["launches"] // 3, "mean_us": round(r["ms"] / r["launches"] * 1e3, 2),
-                           "GBps": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1)} for r in rows}
 
     prefill = None if args.no_prefill else bench_prefill(dev, st, 512, 10)
     layer_pf = None if args.no_prefill else bench_layer_prefill(dev, st, model, 512, 5)
@@ -542,6 +647,7 @@ def main():
     moe_pf = None if args.no_moe else bench_moe_prefill(dev, st, 512, 10)
     get_rows = None if args.no_get_rows else bench_get_rows(dev, st, 512, 5)
     cpu = None if args.no_cpu else cpu_baseline(dev, st, model, args.cpu_seconds)
+    configs = None if args.no_configs else bench_configs(dev, st, 0.0 if args.no_cpu else args.config_cpu_seconds)
 
     result = {
         "metric": "Q4_K matvec weight GB/s (% HBM peak) at bs=1; prefill TFLOP/s at M=512",
@@ -554,15 +660,12 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k/q6_k weights, f32 activations and accumulate",
+        "dtype": "decode: q4_k/q6_k weight codes x int8 two-plane x (x ~ s*a + s/253*b per 32 elements) on i8 MFMA, int32 sums scaled and accumulated in f32; prefill: f16 MFMA, f32 accumulate",
         "data": "synthetic: weights ~N(0,0.02) quantized on device (bit-identical to the reference quantizer), x ~N(0,1)",
         "config": {"workload": f"Qwen3-8B Q4_K_M decode token: {args.layers} layers x 7 matvecs (q,k,v,o,gate,up in Q4_K; down in Q6_K), bs=1"
                                + ("; q/k/v and gate/up as MUL_MAT_MULTI" if not args.no_fuse else ""),
                    "weight_bytes_per_token": model.bytes_per_token, "parallelism": "single GPU"},
         "tokens_per_s_equiv": round(1e3 / ms_step, 1),
-        "kernel_sum_ms_per_token": round(ktime, 4),
-        "kernel_GBps": round(model.bytes_per_token / (ktime * 1e-3) / 1e9, 1),
-        "kernels": kernels,
         "products": groups,
         "roofline": {"bound": "hbm", "kernel": f"{dom_name} ({dom_group})", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_of(dom_group),
@@ -574,6 +677,7 @@ def main():
         "moe_prefill_mul_mat_id": moe_pf,
         "get_rows": get_rows,
         "cpu_baseline": cpu,
+        "configs": configs,
     }
     print(json.dumps(result), flush=True)
 

@@ -45,6 +45,21 @@ def _compile(src: str, extra: list[str]) -> str:
     return out
 
 
+C_CALLER_SRC = os.path.join(ROOT, "tests", "c", "standalone_matmul.c")
+C_CALLER = os.path.join(ROOT, "tests", "c", "standalone_matmul")
+
+
+def build_c_caller() -> str:
+    """The C99 test caller of the public API (tests/c/standalone_matmul.c), linked against the
+    library in-tree (rpath to the package directory)."""
+    cmd = ["gcc", "-std=c99", "-O2", "-Wall", "-Wextra", "-Werror", "-I", os.path.join(ROOT, "include"), C_CALLER_SRC,
+           "-L", PKG, "-lscrapgpu_hip", "-Wl,-rpath,$ORIGIN/../../scrapgpulibrary_amd", "-o", C_CALLER]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"C caller build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    return C_CALLER
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(OBJ, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:
@@ -55,6 +70,7 @@ def build(verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_c_caller()
     if verbose:
         print("built", LIB)
     return LIB

@@ -6,7 +6,7 @@
 // MUL_MAT_MULTI: n weights + the shared x, n outputs, 2 <= n <= 3; MUL_MAT_ID: 3 inputs, 1 output,
 // params present). For the remaining op ids only the arity and the parameter block are checked:
 // the hip backend reports them UNSUPPORTED with a reason.
-#include "scrapgpu/backend.h"
+#include "dispatch.h"
 
 #include <cstddef>
 #include <cstring>
@@ -55,7 +55,7 @@ const Arity kArity[] = {
 
 scrapgpu_status counts(const scrapgpu_op_desc * d, size_t in, size_t out) {
     if (d->input_count != in || d->output_count != out || d->inputs == nullptr || d->outputs == nullptr) {
-        return bad("op desc has the wrong input or output count");
+        return bad("this op takes a different number of inputs or outputs");
     }
     return SCRAPGPU_STATUS_OK;
 }
@@ -70,15 +70,15 @@ extern "C" {
 
 scrapgpu_status scrapgpu_op_desc_validate(const scrapgpu_op_desc * d) {
     if (d == nullptr) return bad("op desc is null");
-    if (d->struct_size < offsetof(scrapgpu_op_desc, params_size) + sizeof(d->params_size)) return bad("op desc is null or too small");
-    if (d->input_count > kMaxTensors || d->output_count > kMaxTensors) return bad("op desc has an invalid input or output count");
-    if ((d->input_count && d->inputs == nullptr) || (d->output_count && d->outputs == nullptr)) return bad("op desc has a null input or output array");
-    if (d->params == nullptr && d->params_size > 0) return bad("op desc params_size is set but params is null");
-    if (d->params_size > kMaxParams) return bad("op desc params_size is too large");
+    if (d->struct_size < offsetof(scrapgpu_op_desc, params_size) + sizeof(d->params_size)) return bad("the op desc is null or shorter than its required fields");
+    if (d->input_count > kMaxTensors || d->output_count > kMaxTensors) return bad("the op desc's input or output count is out of range");
+    if ((d->input_count && d->inputs == nullptr) || (d->output_count && d->outputs == nullptr)) return bad("the op desc lists tensors but its input or output array is null");
+    if (d->params == nullptr && d->params_size > 0) return bad("the op desc has a params_size but no params");
+    if (d->params_size > kMaxParams) return bad("the op desc's params_size is implausibly large");
     for (size_t i = 0; i < d->input_count; ++i)
-        if (d->inputs[i].struct_size < sizeof(scrapgpu_tensor_desc)) return bad("input tensor descriptor is too small");
+        if (d->inputs[i].struct_size < sizeof(scrapgpu_tensor_desc)) return bad("an input tensor desc is shorter than its required fields");
     for (size_t i = 0; i < d->output_count; ++i)
-        if (d->outputs[i].struct_size < sizeof(scrapgpu_tensor_desc)) return bad("output tensor descriptor is too small");
+        if (d->outputs[i].struct_size < sizeof(scrapgpu_tensor_desc)) return bad("an output tensor desc is shorter than its required fields");
     int op_id;
     std::memcpy(&op_id, &d->op, sizeof(op_id));
     switch (op_id) {
@@ -88,22 +88,22 @@ scrapgpu_status scrapgpu_op_desc_validate(const scrapgpu_op_desc * d) {
         case SCRAPGPU_OP_PERMUTE:
         case SCRAPGPU_OP_TRANSPOSE: return SCRAPGPU_STATUS_OK;
         case SCRAPGPU_OP_MUL_MAT: {
-            if (!params_at_least(d, sizeof(scrapgpu_mul_mat_params))) return bad("MUL_MAT params are missing");
+            if (!params_at_least(d, sizeof(scrapgpu_mul_mat_params))) return bad("MUL_MAT needs its params (scrapgpu_mul_mat_params)");
             const scrapgpu_status st = counts(d, 2, 1);
             if (st != SCRAPGPU_STATUS_OK) return st;
             if (!float_weight_or_quant(d->inputs[0].dtype) || d->inputs[1].dtype != SCRAPGPU_DTYPE_F32 ||
                 d->outputs[0].dtype != SCRAPGPU_DTYPE_F32) {
-                return bad("MUL_MAT dtype contract failed");
+                return bad("MUL_MAT: src0 must be F32/F16/BF16/Q4_0/Q8_0/Q4_K/Q6_K and src1, dst F32");
             }
             return SCRAPGPU_STATUS_OK;
         }
         case SCRAPGPU_OP_MUL_MAT_MULTI:
             if (d->output_count < 2 || d->output_count > 3 || d->input_count != d->output_count + 1) {
-                return bad("MUL_MAT_MULTI takes n+1 inputs and n outputs (2 <= n <= 3)");
+                return bad("MUL_MAT_MULTI: 2 or 3 weights, then the shared src1, and one output per weight");
             }
             return SCRAPGPU_STATUS_OK;
         case SCRAPGPU_OP_MUL_MAT_ID:
-            if (!params_at_least(d, sizeof(scrapgpu_mul_mat_id_params))) return bad("MUL_MAT_ID params are missing");
+            if (!params_at_least(d, sizeof(scrapgpu_mul_mat_id_params))) return bad("MUL_MAT_ID needs its params (scrapgpu_mul_mat_id_params)");
             return counts(d, 3, 1);
         default: break;
     }
@@ -113,30 +113,33 @@ scrapgpu_status scrapgpu_op_desc_validate(const scrapgpu_op_desc * d) {
         if (a.in < 0) return counts(d, d->input_count, (size_t) a.out);
         return counts(d, (size_t) a.in, (size_t) a.out);
     }
-    return bad("unknown operation");
+    return bad("the op id is not one this API defines");
 }
 
 scrapgpu_status scrapgpu_op_supported(scrapgpu_device_t * device, const scrapgpu_op_desc * desc, const char ** reason) {
+    const char * call = "scrapgpu_op_supported";
     scrapgpu_status st = scrapgpu_op_desc_validate(desc);
     if (st == SCRAPGPU_STATUS_OK) {
-        const scrapgpu_backend_vtable * vt = device ? reinterpret_cast<const scrapgpu_object_header *>(device)->backend : nullptr;
-        if (vt != nullptr && vt->op_supported != nullptr) return vt->op_supported(device, desc, reason);
-        scrapgpu_set_last_error("no backend registered for op support query");
-        st = SCRAPGPU_STATUS_UNSUPPORTED;
+        const scrapgpu_backend_vtable * t = sgcore::owner_table(device, call, "device");
+        if (t == nullptr) {
+            st = SCRAPGPU_STATUS_UNSUPPORTED; // (no backend to ask: the op is not supported here)
+        } else if (t->op_supported == nullptr) {
+            st = sgcore::not_implemented(call, t, "op_supported");
+        } else {
+            return t->op_supported(device, desc, reason);
+        }
     }
     if (reason != nullptr) *reason = scrapgpu_last_error();
     return st;
 }
 
 scrapgpu_status scrapgpu_op_execute(scrapgpu_stream_t * stream, const scrapgpu_op_desc * desc) {
-    if (stream == nullptr || desc == nullptr) return bad("stream or op desc is null");
-    const scrapgpu_backend_vtable * vt = reinterpret_cast<const scrapgpu_object_header *>(stream)->backend;
-    if (vt == nullptr) return bad("stream does not belong to a registered backend");
-    if (vt->op_execute == nullptr) {
-        scrapgpu_set_last_error("the stream backend cannot execute ops");
-        return SCRAPGPU_STATUS_UNSUPPORTED;
-    }
-    return vt->op_execute(stream, desc);
+    const char * call = "scrapgpu_op_execute";
+    if (desc == nullptr) return sgcore::null_argument(call, "desc");
+    const scrapgpu_backend_vtable * t = sgcore::owner_table(stream, call, "stream");
+    if (t == nullptr) return SCRAPGPU_STATUS_INVALID_ARGUMENT;
+    if (t->op_execute == nullptr) return sgcore::not_implemented(call, t, "op_execute");
+    return t->op_execute(stream, desc);
 }
 
 }

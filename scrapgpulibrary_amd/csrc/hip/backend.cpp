@@ -230,7 +230,7 @@ scrapgpu_status resolve(Device * dev, const scrapgpu_tensor_desc & t, uint8_t **
     if (b->dev != dev) return set_err(SCRAPGPU_STATUS_INVALID_ARGUMENT, std::string(what) + " lives on another device");
     const uint64_t n = sg::nbytes(t);
     if (t.offset > b->size || n > b->size - t.offset) {
-        return set_err(SCRAPGPU_STATUS_INVALID_ARGUMENT, std::string(what) + " exceeds its buffer");
+        return set_err(SCRAPGPU_STATUS_INVALID_ARGUMENT, std::string(what) + " reaches past the end of its buffer");
     }
     *out = b->ptr + t.offset;
     return SCRAPGPU_STATUS_OK;
@@ -245,7 +245,7 @@ size_t api_device_count(void *) {
 
 scrapgpu_status api_get_device(void *, size_t index, scrapgpu_device_t ** out) {
     std::lock_guard<std::mutex> lock(registry().mu);
-    if (index >= registry().devices.size()) return invalid("device index out of range");
+    if (index >= registry().devices.size()) return invalid("no hip device has this index");
     *out = reinterpret_cast<scrapgpu_device_t *>(registry().devices[index].get());
     return SCRAPGPU_STATUS_OK;
 }
@@ -258,7 +258,7 @@ scrapgpu_status api_get_device(void *, size_t index, scrapgpu_device_t ** out) {
 scrapgpu_status api_device_info(scrapgpu_device_t * device, scrapgpu_device_info * info) {
     Device * d = dev_of(device);
     if (d == nullptr) return invalid("not a hip device");
-    if (info->struct_size < sizeof(size_t)) return invalid("device info struct is too small");
+    if (info->struct_size < sizeof(size_t)) return invalid("the device info struct cannot hold its size field");
     SG_INFO_SET(name, d->name.c_str());
     SG_INFO_SET(vendor, "AMD");
     SG_INFO_SET(platform_name, "HIP");
@@ -314,7 +314,7 @@ scrapgpu_status api_buffer_free(scrapgpu_buffer_t * buffer) {
 
 scrapgpu_status check_range(Stream * s, Buffer * b, uint64_t off, size_t size) {
     if (s == nullptr || b == nullptr) return invalid("not a hip stream or buffer");
-    if (b->dev != s->dev) return invalid("buffer and stream belong to different devices");
+    if (b->dev != s->dev) return invalid("the buffer lives on another device than the stream");
     if (off > b->size || size > b->size - off) return invalid("range exceeds the buffer");
     return SCRAPGPU_STATUS_OK;
 }
@@ -507,20 +507,20 @@ scrapgpu_status r32_transfer(Stream * s, const scrapgpu_tensor_desc & t, uint8_t
 scrapgpu_status tensor_transfer(scrapgpu_stream_t * stream, const scrapgpu_tensor_desc * raw, uint8_t * host, size_t size, bool up) {
     Stream * s = stream_of(stream);
     if (s == nullptr) return invalid("not a hip stream");
-    if (raw->struct_size < offsetof(scrapgpu_tensor_desc, offset) + sizeof(raw->offset)) return invalid("tensor desc is too small");
+    if (raw->struct_size < offsetof(scrapgpu_tensor_desc, offset) + sizeof(raw->offset)) return invalid("the tensor desc is shorter than its required fields");
     const scrapgpu_tensor_desc t = load_desc(*raw);
     Buffer * b = buf_of(t.buffer);
     if (b == nullptr) return invalid("tensor desc has no hip buffer");
-    if (b->dev != s->dev) return invalid("tensor buffer and stream belong to different devices");
-    if (t.offset > b->size || size > b->size - t.offset) return invalid("transfer exceeds the buffer");
-    if (size > sg::nbytes(t)) return invalid("transfer size exceeds the tensor");
+    if (b->dev != s->dev) return invalid("the tensor's buffer lives on another device than the stream");
+    if (t.offset > b->size || size > b->size - t.offset) return invalid("the transfer reaches past the end of the buffer");
+    if (size > sg::nbytes(t)) return invalid("the transfer is larger than the tensor");
     if (size == 0) return SCRAPGPU_STATUS_OK;
     SG_HIP(use(s->dev), "hipSetDevice");
     if (t.layout == SCRAPGPU_LAYOUT_R32) {
-        if (!sg::r32_eligible(t)) return unsupported("the R32 layout needs a repackable dtype and contiguous slices with 16-byte strides");
+        if (!sg::r32_eligible(t)) return unsupported("R32 needs a Q4_0/Q8_0/Q4_K/Q6_K tensor with contiguous rows, whole blocks per row and slice strides that are multiples of 16 bytes");
         return r32_transfer(s, t, b->ptr + t.offset, host, size, up);
     }
-    if (!sg::contiguous_ggml(t)) return unsupported("tensor is not contiguous; use buffer_read / buffer_write for raw strided transfers");
+    if (!sg::contiguous_ggml(t)) return unsupported("only contiguous tensors transfer through tensor_upload/download; strided data goes through buffer_write/buffer_read");
     if (up) {
         SG_HIP(hipMemcpyAsync(b->ptr + t.offset, host, size, hipMemcpyHostToDevice, s->s), "hipMemcpyAsync");
     } else {
@@ -547,32 +547,32 @@ scrapgpu_status mul_mat_rule(const scrapgpu_tensor_desc & w, const scrapgpu_tens
         return unsupported("the hip backend implements MUL_MAT for Q4_0 / Q8_0 / Q4_K / Q6_K weights only", reason);
     }
     if (w.layout != SCRAPGPU_LAYOUT_R32) {
-        return unsupported("a quantized src0 must use the R32 layout (scrapgpu_tensor_upload packs it on the way)", reason);
+        return unsupported("quantized weights run from the R32 layout only: upload them with layout R32 (the upload repacks natural blocks)", reason);
     }
     if (!sg::r32_eligible(w)) return unsupported("src0 is not R32-eligible (contiguous, whole blocks per row, 16-byte slice strides)", reason);
     if (x.dtype != SCRAPGPU_DTYPE_F32 || y.dtype != SCRAPGPU_DTYPE_F32 || x.layout != SCRAPGPU_LAYOUT_NATURAL || y.layout != SCRAPGPU_LAYOUT_NATURAL) {
         return unsupported("MUL_MAT expects an F32 natural-layout src1 and destination", reason);
     }
-    if (x.nb[0] != 4 || y.nb[0] != 4) return unsupported("MUL_MAT needs contiguous rows of src1 and dst (nb0 == element size)", reason);
+    if (x.nb[0] != 4 || y.nb[0] != 4) return unsupported("MUL_MAT: src1 and dst rows must be packed floats (nb0 == 4)", reason);
     for (int i = 1; i < 4; ++i) {
         if (x.nb[i] % 4 != 0 || y.nb[i] % 4 != 0) return unsupported("src1 / dst strides must be multiples of 4 bytes", reason);
     }
     if ((x.offset % 4) != 0 || (y.offset % 4) != 0) return unsupported("src1 / dst offsets must be multiples of 4 bytes", reason);
     const int64_t K = sg::dim1(w.ne[0]), M = sg::dim1(w.ne[1]);
     if (sg::dim1(x.ne[0]) != K) {
-        if (reason) *reason = "MUL_MAT: the inner dimensions of src0 and src1 differ";
-        return invalid("MUL_MAT: the inner dimensions of src0 and src1 differ");
+        if (reason) *reason = "MUL_MAT: src0 and src1 disagree on K (ne0)";
+        return invalid("MUL_MAT: src0 and src1 disagree on K (ne0)");
     }
     const int64_t w2 = sg::dim1(w.ne[2]), w3 = sg::dim1(w.ne[3]);
     const int64_t x2 = sg::dim1(x.ne[2]), x3 = sg::dim1(x.ne[3]);
     if (x2 % w2 != 0 || x3 % w3 != 0) {
-        if (reason) *reason = "MUL_MAT: src1 dims 2 and 3 must be multiples of the src0 dims";
-        return invalid("MUL_MAT: src1 dims 2 and 3 must be multiples of the src0 dims");
+        if (reason) *reason = "MUL_MAT: src1 slice counts (ne2, ne3) must be whole multiples of src0's";
+        return invalid("MUL_MAT: src1 slice counts (ne2, ne3) must be whole multiples of src0's");
     }
-    if (!allow_broadcast && (x2 != w2 || x3 != w3)) return unsupported("MUL_MAT: broadcasting over dims 2/3 is not allowed", reason);
+    if (!allow_broadcast && (x2 != w2 || x3 != w3)) return unsupported("MUL_MAT: src0 has fewer slices than src1 and allow_broadcast is 0 (no broadcast)", reason);
     if (sg::dim1(y.ne[0]) != M || sg::dim1(y.ne[1]) != sg::dim1(x.ne[1]) || sg::dim1(y.ne[2]) != x2 || sg::dim1(y.ne[3]) != x3) {
-        if (reason) *reason = "MUL_MAT: dst must be [ne01, ne11, ne12, ne13]";
-        return invalid("MUL_MAT: dst must be [ne01, ne11, ne12, ne13]");
+        if (reason) *reason = "MUL_MAT: dst shape is not [src0 ne1, src1 ne1, src1 ne2, src1 ne3]";
+        return invalid("MUL_MAT: dst shape is not [src0 ne1, src1 ne1, src1 ne2, src1 ne3]");
     }
     if (x2 * x3 > 65535) return unsupported("MUL_MAT: more than 65535 slices", reason);
     // the kernels address one slice of weights, and one slice of x in f16, with 32-bit offsets
@@ -629,7 +629,7 @@ scrapgpu_status mul_mat_id_rule(const scrapgpu_tensor_desc & w, const scrapgpu_t
         (sg::dim1(x.ne[1]) != 1 && sg::dim1(x.ne[1]) != nu) || sg::dim1(x.ne[2]) != T || sg::dim1(y.ne[0]) != M || sg::dim1(y.ne[1]) != nu ||
         sg::dim1(y.ne[2]) != T || sg::dim1(y.ne[3]) != 1) {
         if (reason) *reason = "MUL_MAT_ID needs [K,M,E] src0, [K,n_used|1,n_tokens] src1, I32 [n_used,n_tokens] ids and [M,n_used,n_tokens] dst";
-        return invalid("MUL_MAT_ID: shapes do not match the contract");
+        return invalid("MUL_MAT_ID: src1, ids and dst shapes are inconsistent with src0 and n_used");
     }
     if (nu * T > 65535) return unsupported("MUL_MAT_ID: more than 65535 (slot, token) pairs", reason);
     if (sg::sat_mul(sg::row_size(w.dtype, K), (uint64_t) M) >= ((uint64_t) 1 << 32)) {
@@ -685,8 +685,8 @@ scrapgpu_status get_rows_rule(const scrapgpu_tensor_desc & w, const scrapgpu_ten
     const int64_t K = sg::dim1(w.ne[0]);
     if (sg::dim1(ids.ne[3]) != 1 || sg::dim1(ids.ne[1]) > sg::dim1(w.ne[2]) || sg::dim1(ids.ne[2]) > sg::dim1(w.ne[3]) || sg::dim1(y.ne[0]) != K ||
         sg::dim1(y.ne[1]) != sg::dim1(ids.ne[0]) || sg::dim1(y.ne[2]) != sg::dim1(ids.ne[1]) || sg::dim1(y.ne[3]) != sg::dim1(ids.ne[2])) {
-        if (reason) *reason = "GET_ROWS: dst must be [ne00, ids] over the slices of src0";
-        return invalid("GET_ROWS: dst must be [ne00, ids] over the slices of src0");
+        if (reason) *reason = "GET_ROWS: dst shape is not [src0 ne0, ids ne0, ids ne1, ids ne2]";
+        return invalid("GET_ROWS: dst shape is not [src0 ne0, ids ne0, ids ne1, ids ne2]");
     }
     if (g) {
         std::memset(g, 0, sizeof(*g));
@@ -1181,7 +1181,7 @@ scrapgpu_status api_plan_execute(scrapgpu_stream_t * stream, scrapgpu_plan_t * p
     Stream * s = stream_of(stream);
     Plan * p = as<Plan>(plan);
     if (s == nullptr || p == nullptr) return invalid("not a hip stream or plan");
-    if (p->dev != s->dev) return invalid("plan and stream belong to different devices");
+    if (p->dev != s->dev) return invalid("the plan was built for another device than the stream's");
     SG_HIP(use(s->dev), "hipSetDevice");
     // eager while the per-kernel profiler is on (its events are host-side records) or graphs are off
     if (!graphs_enabled() || g_prof.load(std::memory_order_relaxed) || p->nodes.empty()) {
@@ -1379,7 +1379,7 @@ scrapgpu_status scrapgpu_hip_register(void) {
 
 scrapgpu_status scrapgpu_hip_quantize(scrapgpu_stream_t * stream, const scrapgpu_tensor_desc * src, const scrapgpu_tensor_desc * dst) {
     Stream * s = stream_of(stream);
-    if (s == nullptr || src == nullptr || dst == nullptr) return invalid("stream, src or dst is null");
+    if (s == nullptr || src == nullptr || dst == nullptr) return invalid("a null stream, src or dst");
     const scrapgpu_tensor_desc f = load_desc(*src), q = load_desc(*dst);
     scrapgpu_status st = convert_check(s, q, f);
     if (st != SCRAPGPU_STATUS_OK) return st;
@@ -1398,7 +1398,7 @@ scrapgpu_status scrapgpu_hip_quantize(scrapgpu_stream_t * stream, const scrapgpu
 
 scrapgpu_status scrapgpu_hip_dequantize(scrapgpu_stream_t * stream, const scrapgpu_tensor_desc * src, const scrapgpu_tensor_desc * dst) {
     Stream * s = stream_of(stream);
-    if (s == nullptr || src == nullptr || dst == nullptr) return invalid("stream, src or dst is null");
+    if (s == nullptr || src == nullptr || dst == nullptr) return invalid("a null stream, src or dst");
     const scrapgpu_tensor_desc q = load_desc(*src), f = load_desc(*dst);
     scrapgpu_status st = convert_check(s, q, f);
     if (st != SCRAPGPU_STATUS_OK) return st;
