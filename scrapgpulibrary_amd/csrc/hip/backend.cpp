@@ -824,10 +824,15 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
             flops += 2.0 * (double) m[j].M * (double) m[j].K * (double) m[j].N * (double) (m[j].ne12 * m[j].ne13);
         }
         if (m[0].N <= mv_n) {
+            uint8_t * scr = nullptr;
+            if (const size_t need = sgk::matvec_scratch_bytes(m, cnt)) {
+                const scrapgpu_status st = scratch_for(s, need, &scr);
+                if (st != SCRAPGPU_STATUS_OK) return st;
+            }
             ProfScope prof(s->s);
             const char * name = nullptr;
             uint64_t grid = 0;
-            SG_HIP(sgk::launch_matvec(m, cnt, cus, s->s, &name, &grid), "matvec launch");
+            SG_HIP(sgk::launch_matvec(m, cnt, cus, s->s, &name, &grid, nullptr, scr), "matvec launch");
             prof.done(name, bytes, flops);
         } else {
             uint8_t * scr = nullptr;
@@ -1144,6 +1149,25 @@ scrapgpu_status plan_prepare(Stream * s, Plan * p) {
             continue;
         }
         if (n.op.op != SCRAPGPU_OP_MUL_MAT && n.op.op != SCRAPGPU_OP_MUL_MAT_MULTI) continue;
+        {
+            // decode with several columns: the x planes (and K-chunk partial sums) of the launch
+            // over the node's weights, and of each weight alone
+            sgk::MatArgs mats[3];
+            int cnt = 0;
+            const int total = n.op.op == SCRAPGPU_OP_MUL_MAT ? n.fuse + 1 : (int) n.op.output_count;
+            for (int k = 0; k < total && k < 3; ++k) {
+                const scrapgpu_op_desc & op = n.op.op == SCRAPGPU_OP_MUL_MAT ? (&n)[k].op : n.op;
+                const int wi = n.op.op == SCRAPGPU_OP_MUL_MAT ? 0 : k;
+                const scrapgpu_tensor_desc & x = n.op.op == SCRAPGPU_OP_MUL_MAT ? op.inputs[1] : op.inputs[op.output_count];
+                sgk::MatArgs a;
+                std::memset(&a, 0, sizeof(a));
+                if (mul_mat_rule(op.inputs[wi], x, op.outputs[n.op.op == SCRAPGPU_OP_MUL_MAT ? 0 : k], 1, &a, nullptr) != SCRAPGPU_STATUS_OK) continue;
+                if (a.N > matvec_max_n(a)) continue;
+                mats[cnt++] = a;
+                need = std::max(need, sgk::matvec_scratch_bytes(&a, 1));
+            }
+            if (cnt > 1) need = std::max(need, sgk::matvec_scratch_bytes(mats, cnt));
+        }
         if (n.op.op == SCRAPGPU_OP_MUL_MAT && n.fuse > 0) {
             // MUL_MATs fused into one MULTI: the prefill launch over all their rows
             sgk::MatArgs all;

@@ -52,6 +52,8 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
+#include <mutex>
 #include <vector>
 
 namespace sgk {
@@ -732,6 +734,620 @@ __global__ __launch_bounds__(64 * W) void k_mvs(MvArgs A) {
     }
 }
 
+// ---- several columns: the columns share each MFMA ---------------------------------------------------
+//
+// For N = 2..8 the columns go into the rows of the MFMA's A operand, so each weight code is
+// unpacked once for all of them. This needs every MFMA to span few scale groups: the lane parts
+// are mapped so that parts {0, 1} of an MFMA lie in one scale group and parts {2, 3} in one other
+// (G = 2: Q4_0, Q8_0, Q4_K), or each part in its own 16-element group (G = 4: Q6_K). A row i of A
+// is (column, group, plane): rows 4c .. 4c + 3 = column c of the set, groups 0 / 1, planes a / b
+// (G = 2, 4 columns per MFMA set), or rows 8c .. 8c + 7 (G = 4, 2 columns per set). A row holds
+// its column's x plane only at the k positions of its group (zeros elsewhere), so row (c, g, .)
+// of D is column c's integer dot product over group g alone. Lane (r, p) receives rows
+// 4p .. 4p + 3 of D: for G = 2 all of column p's pairs (both groups, both planes); for G = 4 two
+// groups of column p / 2. It scales them with the groups' block scales and x-segment factors and
+// accumulates column p (or p / 2) of weight row r.
+//
+// Per format, for MFMA t = 0..3 of a step and lane part p: the segment (32 elements of the step)
+// and 16-byte half that part p supplies, the group it belongs to, and the flush of the lane's D.
+
+template <int DT> struct FmtN;
+
+// Q4_K: part p loads units p and p + 4 of the block's 8 (16 bytes each): MFMA 0 / 1 take the low
+// / high nibbles of unit p, MFMA 2 / 3 those of unit p + 4. Unit u holds chunk u / 2, half u % 2:
+// its low nibbles are sub-block 2 (u / 2), its high nibbles sub-block 2 (u / 2) + 1. So MFMA t,
+// group g (= p / 2) is sub-block 4 (t / 2) + t % 2 + 2 g, elements 16 (p % 2) .. +15 of it.
+template <>
+struct FmtN<Q4_K> {
+    static constexpr int G = 2;
+    struct Raw {
+        uint4 qa, qb, hd;
+    };
+    const uint8_t * w;
+    uint32_t qo, ho, u;
+    int p;
+    __device__ void init(const uint8_t * w_, int64_t M, int64_t nb, int64_t g0, int rs, int lr, int part) {
+        w = w_;
+        p = part;
+        u = (uint32_t) rs * 16;
+        qo = (uint32_t) (g0 * nb * 128 + lr * 16) + (uint32_t) p * u;
+        ho = (uint32_t) (M * nb * 128 + g0 * nb * 16 + lr * 16);
+    }
+    __device__ Raw load(int64_t step) const {
+        Raw r;
+        const uint32_t q = __umul24((uint32_t) step * 8, u) + qo;
+        r.qa = load16(w + q);
+        r.qb = load16(w + q + 4 * u);
+        r.hd = load16(w + (__umul24((uint32_t) step, u) + ho));
+        return r;
+    }
+    __device__ static v4i bop(const Raw & r, int t) {
+        return t == 0 ? lo4(r.qa) : t == 1 ? hi4(r.qa) : t == 2 ? lo4(r.qb) : hi4(r.qb);
+    }
+    __device__ static int seg(int t, int g) {
+        return 4 * (t >> 1) + (t & 1) + 2 * g;
+    }
+    // scale and min of sub-block s (get_scale_min_k4)
+    __device__ static void scale_min(const Raw & r, int s, float & sc, float & m) {
+        const uint32_t s0 = r.hd.y, s1 = r.hd.z, s2 = r.hd.w;
+        const int sh = 8 * (s & 3);
+        if (s < 4) {
+            sc = (float) ((s0 >> sh) & 63u);
+            m = (float) ((s1 >> sh) & 63u);
+        } else {
+            const uint32_t t0 = s2 >> sh;
+            sc = (float) ((t0 & 0x0Fu) | (((s0 >> sh) >> 2) & 0x30u));
+            m = (float) (((t0 >> 4) & 0x0Fu) | (((s1 >> sh) >> 2) & 0x30u));
+        }
+    }
+    // the factors of MFMA t's two groups (the same for every column set): d * sc, -dmin * m
+    struct Sc {
+        float k[2], o[2];
+    };
+    __device__ Sc scales(const Raw & r, int t, const uint32_t (&)[2]) const {
+        const float d = half_bits(r.hd.x), dmin = half_bits(r.hd.x >> 16);
+        Sc c;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            float sc, m;
+            scale_min(r, seg(t, g), sc, m);
+            c.k[g] = d * sc;
+            c.o[g] = -dmin * m;
+        }
+        return c;
+    }
+    // D rows (group g, plane): the lane's column over MFMA t's two groups
+    __device__ static float apply(const Sc & c, int t, const v4i & D, const float4 * xf) {
+        const float4 f0 = xf[seg(t, 0)], f1 = xf[seg(t, 1)];
+        float a = c.k[0] * f0.x * planes(D.x, D.y);
+        a = fmaf(c.o[0], f0.w, a);
+        a = fmaf(c.k[1] * f1.x, planes(D.z, D.w), a);
+        return fmaf(c.o[1], f1.w, a);
+    }
+};
+
+// Q4_0: MFMA t, group g is block 2t + g; part p supplies nibble half p % 2 (elements 16 (p % 2)
+// .. +15) of block 2t + p / 2. Part p loads those 4 blocks' units and scales; the scales of the
+// other group's blocks come from lane + 32 (part p ^ 2).
+template <>
+struct FmtN<Q4_0> {
+    static constexpr int G = 2;
+    struct Raw {
+        uint4 q[4];
+        uint32_t d[2]; // own blocks' scales (t = 0, 1 | t = 2, 3 as 16-bit halves)
+    };
+    const uint8_t * w;
+    uint32_t qo, dof, u, nb;
+    int p;
+    __device__ void init(const uint8_t * w_, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int part) {
+        w = w_;
+        p = part;
+        nb = (uint32_t) nb_;
+        u = (uint32_t) rs * 16;
+        qo = (uint32_t) (g0 * nb_ * 16 + lr * 16);
+        dof = (uint32_t) (M * nb_ * 16 + g0 * nb_ * 2 + lr * 2);
+    }
+    __device__ Raw load(int64_t step) const {
+        Raw r;
+        uint32_t dh[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint32_t b = (uint32_t) step * 8 + 2 * t + (p >> 1);
+            const bool ok = b < nb;
+            b = ok ? b : 0;
+            r.q[t] = load16(w + (__umul24(b, u) + qo));
+            const uint32_t d = load_half(w + (__umul24(b, u >> 3) + dof));
+            dh[t] = ok ? d : 0u;
+        }
+        r.d[0] = dh[0] | (dh[1] << 16);
+        r.d[1] = dh[2] | (dh[3] << 16);
+        return r;
+    }
+    // the codes minus 8 as int8: (c + 0x78) ^ 0x80 per byte (no carries: c < 16)
+    __device__ v4i bop(const Raw & r, int t) const {
+        const uint4 q = r.q[t];
+        const int sh = (p & 1) ? 4 : 0;
+        return as_v4i(make_uint4((((q.x >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u, (((q.y >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u,
+                                 (((q.z >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u, (((q.w >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u));
+    }
+    __device__ static int seg(int t, int g) {
+        return 2 * t + g;
+    }
+    // the scales of MFMA t's two blocks: the lane's own group p / 2, the other from part p ^ 2
+    struct Sc {
+        float k[2];
+    };
+    __device__ Sc scales(const Raw & r, int t, const uint32_t (&other)[2]) const {
+        const uint32_t mine = r.d[t >> 1] >> (16 * (t & 1)), theirs = other[t >> 1] >> (16 * (t & 1));
+        return Sc{{half_bits((p >> 1) ? theirs : mine), half_bits((p >> 1) ? mine : theirs)}};
+    }
+    __device__ static float apply(const Sc & c, int t, const v4i & D, const float4 * xf) {
+        const float a = c.k[0] * xf[seg(t, 0)].x * planes(D.x, D.y);
+        return fmaf(c.k[1] * xf[seg(t, 1)].x, planes(D.z, D.w), a);
+    }
+};
+
+// Q8_0: MFMA t, group g is block 2t + g; part p supplies half p % 2 of block 2t + p / 2 (the
+// single-column mapping). Scales as for Q4_0.
+template <>
+struct FmtN<Q8_0> {
+    static constexpr int G = 2;
+    struct Raw {
+        uint4 q[4];
+        uint32_t d[2];
+    };
+    const uint8_t * w;
+    uint32_t qo, dof, u, nb;
+    int p;
+    __device__ void init(const uint8_t * w_, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int part) {
+        w = w_;
+        p = part;
+        nb = (uint32_t) nb_;
+        u = (uint32_t) rs * 16;
+        qo = (uint32_t) (g0 * nb_ * 32 + lr * 16) + (uint32_t) (p & 1) * u;
+        dof = (uint32_t) (M * nb_ * 32 + g0 * nb_ * 2 + lr * 2);
+    }
+    __device__ Raw load(int64_t step) const {
+        Raw r;
+        uint32_t dh[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint32_t b = (uint32_t) step * 8 + 2 * t + (p >> 1);
+            const bool ok = b < nb;
+            b = ok ? b : 0;
+            r.q[t] = load16(w + (__umul24(2 * b, u) + qo));
+            const uint32_t d = load_half(w + (__umul24(b, u >> 3) + dof));
+            dh[t] = ok ? d : 0u;
+        }
+        r.d[0] = dh[0] | (dh[1] << 16);
+        r.d[1] = dh[2] | (dh[3] << 16);
+        return r;
+    }
+    __device__ v4i bop(const Raw & r, int t) const {
+        const uint4 q = r.q[t];
+        return as_v4i(make_uint4(q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u));
+    }
+    __device__ static int seg(int t, int g) {
+        return 2 * t + g;
+    }
+    struct Sc {
+        float k[2];
+    };
+    __device__ Sc scales(const Raw & r, int t, const uint32_t (&other)[2]) const {
+        const uint32_t mine = r.d[t >> 1] >> (16 * (t & 1)), theirs = other[t >> 1] >> (16 * (t & 1));
+        return Sc{{half_bits((p >> 1) ? theirs : mine), half_bits((p >> 1) ? mine : theirs)}};
+    }
+    __device__ static float apply(const Sc & c, int t, const v4i & D, const float4 * xf) {
+        const float a = c.k[0] * xf[seg(t, 0)].x * planes(D.x, D.y);
+        return fmaf(c.k[1] * xf[seg(t, 1)].x, planes(D.z, D.w), a);
+    }
+};
+
+// Q6_K: the single-column mapping (part p = task (h, hf) = (p / 2, p % 2): elements
+// 128 h + 32 t + 16 hf + i in MFMA t), each part its own 16-element group (G = 4). Lane (r, p)
+// flushes groups 2 (p % 2) and 2 (p % 2) + 1 of column p / 2 of its set.
+template <>
+struct FmtN<Q6_K> : Fmt<Q6_K> {
+    static constexpr int G = 4;
+    __device__ static int seg(int t, int g) { // the segment of group (task) g in MFMA t
+        return 4 * (g >> 1) + t;
+    }
+    // the 6-bit codes minus 32 as int8: (c + 0x60) ^ 0x80 per byte (no carries: c < 64)
+    __device__ static v4i bop(const Raw & r, int t) {
+        const v4i b = Fmt<Q6_K>::bop(r, t);
+        return as_v4i(make_uint4(((uint32_t) b.x + 0x60606060u) ^ 0x80808080u, ((uint32_t) b.y + 0x60606060u) ^ 0x80808080u,
+                                 ((uint32_t) b.z + 0x60606060u) ^ 0x80808080u, ((uint32_t) b.w + 0x60606060u) ^ 0x80808080u));
+    }
+    // d * scale of the lane's groups 2 (p % 2) + k in MFMA t (scale index 8 h + 2 t + hf, stored
+    // xor 0x80)
+    struct Sc {
+        float k[2];
+    };
+    __device__ Sc scales(const Raw & r, int t, const uint32_t (&)[2]) const {
+        const float d = half_bits(r.d);
+        Sc c;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int g = 2 * (p & 1) + k, h = g >> 1, hf = g & 1;
+            const uint32_t sw = h ? (t < 2 ? r.sc.z : r.sc.w) : (t < 2 ? r.sc.x : r.sc.y);
+            c.k[k] = d * ((float) ((sw >> (8 * (2 * (t & 1) + hf))) & 0xFFu) - 128.0f);
+        }
+        return c;
+    }
+    __device__ float apply(const Sc & c, int t, const v4i & D, const float4 * xf) const {
+        const int g0 = 2 * (p & 1);
+        const float a = c.k[0] * xf[seg(t, g0)].x * planes(D.x, D.y);
+        return fmaf(c.k[1] * xf[seg(t, g0 + 1)].x, planes(D.z, D.w), a);
+    }
+};
+
+// The lane's A operand for MFMA t of set s: byte offset inside its column's XSeg run of the step,
+// the column, or -1 (zeros). Row i = l % 16, part p = l / 16.
+template <int DT, int NC>
+struct ALaneN {
+    static constexpr int G = FmtN<DT>::G;
+    static constexpr int CPS = 16 / (2 * G); // columns per MFMA set
+    static constexpr int NS = (NC + CPS - 1) / CPS;
+    int off[NS][4];
+    int col[NS];
+    __device__ explicit ALaneN(int lane) {
+        const int i = lane & 15, p = lane >> 4;
+        const int c = i / (2 * G), g = (i >> 1) % G, plane = i & 1;
+        const int pg = G == 2 ? p >> 1 : p; // the group of part p
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int n = s * CPS + c;
+            col[s] = n;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                off[s][t] = (g == pg && n < NC) ? FmtN<DT>::seg(t, pg) * 64 + plane * 32 + (p & 1) * 16 : -1;
+        }
+    }
+};
+
+// one step of NC columns: acc[s] is the lane's column of set s (column s * CPS + p, or
+// s * CPS + p / 2 for G = 4)
+// (sets S0 .. S1 only; column n's x sits in slot n - c0 of the view)
+template <int DT, int NC, int S0 = 0, int S1 = ALaneN<DT, NC>::NS>
+__device__ __forceinline__ void step_mfma_n(const FmtN<DT> & f, const typename FmtN<DT>::Raw & raw, const ALaneN<DT, NC> & al, int sg0,
+                                            const XView & xv, float (&acc)[ALaneN<DT, NC>::NS], int lane, int c0 = 0) {
+    constexpr int G = FmtN<DT>::G, CPS = ALaneN<DT, NC>::CPS, NS = ALaneN<DT, NC>::NS;
+    const int p = lane >> 4;
+    uint32_t other[2] = {0u, 0u};
+    if constexpr (DT == Q4_0 || DT == Q8_0) {
+        other[0] = __shfl_xor(raw.d[0], 32);
+        other[1] = __shfl_xor(raw.d[1], 32);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const v4i B = f.bop(raw, t);
+        const typename FmtN<DT>::Sc sc = f.scales(raw, t, other);
+#pragma unroll
+        for (int s = S0; s < S1; ++s) {
+            const int n = al.col[s];
+            const uint8_t * base = reinterpret_cast<const uint8_t *>(xv.xs + (n < NC ? n - c0 : 0) * xv.nseg + sg0);
+            const uint8_t * pa = al.off[s][t] >= 0 ? base + al.off[s][t] : xv.zpad;
+            const v4i A = *reinterpret_cast<const v4i *>(pa);
+            const v4i D = mfma(A, B, v4i{0, 0, 0, 0});
+            // the lane's column of this set
+            const int nl = s * CPS + (G == 2 ? p : p >> 1);
+            if (nl < NC) acc[s] += f.apply(sc, t, D, xv.xf + (nl - c0) * xv.nseg + sg0);
+        }
+    }
+}
+
+// Streaming form for N = 2..8 with the columns in the MFMA's A rows (see above); otherwise as
+// k_mvs: a persistent grid of 16-row tiles, x converted once per wave (when its range fits the
+// LDS budget), the next step's loads in flight while the current one is computed.
+template <int DT, int NC, int W>
+__global__ __launch_bounds__(64 * W) void k_mvn(MvArgs A) {
+    using F = FmtN<DT>;
+    using Raw = typename F::Raw;
+    using AL = ALaneN<DT, NC>;
+    constexpr int G = F::G, CPS = AL::CPS, NS = AL::NS;
+    extern __shared__ uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, part = lane >> 4;
+    const Where wh = where_of(A);
+
+    const int64_t s0 = A.nst * wave / W, s1 = A.nst * (wave + 1) / W;
+    const int ns = (int) (s1 - s0);
+    const int cs = A.cs;
+    const bool once = cs >= ns;
+    XSeg * xs = reinterpret_cast<XSeg *>(lds) + (size_t) wave * cs * kSegs * NC;
+    float4 * xf = reinterpret_cast<float4 *>(reinterpret_cast<XSeg *>(lds) + (size_t) W * cs * kSegs * NC) + (size_t) wave * cs * kSegs * NC;
+    float * red = reinterpret_cast<float *>(reinterpret_cast<float4 *>(reinterpret_cast<XSeg *>(lds) + (size_t) W * cs * kSegs * NC) +
+                                            (size_t) W * cs * kSegs * NC); // [2][W][NC][16]
+    uint8_t * zpad = reinterpret_cast<uint8_t *>(red + 2 * W * NC * 16);
+    if (lane < 4) reinterpret_cast<uint32_t *>(zpad)[lane] = 0u;
+    const AL al(lane);
+
+    int64_t tile = blockIdx.x;
+    F f, fn;
+    Row row;
+    {
+        const int j = tile >= A.tstart[1] ? (tile >= A.tstart[2] ? 2 : 1) : 0;
+        row = Row{j, A.M[j], (tile - A.tstart[j]) * 16};
+        const int64_t m = min(row.m0 + r, row.M - 1), g0 = m & ~(int64_t) 31;
+        f.init(A.w[j] + wh.w_off, row.M, A.nb, g0, (int) min<int64_t>(32, row.M - g0), (int) (m - g0), part);
+    }
+    Raw cur;
+    if (ns > 0) cur = f.load(s0);
+    if (once && ns > 0) convert_x<NC>(A, wh.x, s0 * kStep, ns * kSegs, lane, xs, xf);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+
+    for (int it = 0; tile < A.tiles; ++it) {
+        const int64_t ntile = tile + gridDim.x;
+        const bool has_n = ntile < A.tiles;
+        Row nrow{};
+        if (has_n) {
+            const int j = ntile >= A.tstart[1] ? (ntile >= A.tstart[2] ? 2 : 1) : 0;
+            nrow = Row{j, A.M[j], (ntile - A.tstart[j]) * 16};
+            const int64_t m = min(nrow.m0 + r, nrow.M - 1), g0 = m & ~(int64_t) 31;
+            fn.init(A.w[j] + wh.w_off, nrow.M, A.nb, g0, (int) min<int64_t>(32, nrow.M - g0), (int) (m - g0), part);
+        }
+        float acc[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) acc[s] = 0.0f;
+        for (int k = 0; k < ns; ++k) {
+            if (!once && k % cs == 0) {
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                convert_x<NC>(A, wh.x, (s0 + k) * kStep, min(cs, ns - k) * kSegs, lane, xs, xf);
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+            }
+            Raw nxt;
+            if (k + 1 < ns) {
+                nxt = f.load(s0 + k + 1);
+            } else if (has_n) {
+                nxt = fn.load(s0);
+            }
+            const XView xv{xs, xf, zpad, min(cs, ns - (k / cs) * cs) * kSegs};
+            step_mfma_n<DT, NC>(f, cur, al, (k % cs) * kSegs, xv, acc, lane);
+            cur = nxt;
+        }
+        // the parts of a row: none to add for G = 2 (lane (r, p) holds column p of each set);
+        // for G = 4 parts 2c and 2c + 1 hold the two halves of column c's groups
+        float * rb = red + (it & 1) * (W * NC * 16);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            float v = acc[s];
+            if constexpr (G == 4) v += __shfl_xor(v, 16);
+            const int n = s * CPS + (G == 2 ? part : part >> 1);
+            if (n < NC && (G == 2 || (part & 1) == 0)) rb[(wave * NC + n) * 16 + r] = v;
+        }
+        __syncthreads();
+        if (tid < NC * 16) {
+            const int n = tid / 16, rr = tid % 16;
+            const int64_t m = row.m0 + rr;
+            if (m < row.M) {
+                float v = 0.0f;
+#pragma unroll
+                for (int w2 = 0; w2 < W; ++w2) v += rb[(w2 * NC + n) * 16 + rr];
+                A.y[row.j][wh.y_off + n * A.ys1[row.j] + m] = v;
+            }
+        }
+        tile = ntile;
+        row = nrow;
+        f = fn;
+    }
+}
+
+template <int DT>
+void * pick_columns(int nc) {
+    switch (nc) {
+        case 2: return (void *) k_mvn<DT, 2, 4>;
+        case 3: return (void *) k_mvn<DT, 3, 4>;
+        case 4: return (void *) k_mvn<DT, 4, 4>;
+        case 5: return (void *) k_mvn<DT, 5, 4>;
+        case 6: return (void *) k_mvn<DT, 6, 4>;
+        case 7: return (void *) k_mvn<DT, 7, 4>;
+        default: return (void *) k_mvn<DT, 8, 4>;
+    }
+}
+
+// ---- several columns, one tile per work-group (the form for N = 2..8, one slice) -----------------
+//
+// x goes through a pre-pass first (k_x_planes: every 32-element segment of every column as its
+// two int8 planes and factors, in scratch), so the matvec work-groups only copy their part of it
+// into LDS. A work-group owns 16 rows and one K chunk of 16 steps (4096 elements): its 8 waves take
+// 2 steps each and issue all their loads at once (x planes first, then weights), like the
+// one-column burst form. With several chunks the work-groups write partial sums and
+// k_mvc_reduce adds them in chunk order.
+
+constexpr int kMcW = 8, kMcSpw = 2, kMcChunk = kMcW * kMcSpw; // waves, steps per wave, steps per chunk
+
+struct McArgs {
+    const uint8_t * w[3];
+    int64_t M[3];
+    float * y[3];
+    int64_t ys1[3];
+    int64_t tstart[4];   // matrix j owns row tiles [tstart[j], tstart[j + 1])
+    int64_t nb, nst, nchunks;
+    const XSeg * planes; // [NC][nsegp]
+    const float4 * fac;  // [NC][nsegp]
+    int64_t nsegp;       // segments per column in the scratch (nchunks * 128)
+    float * part;        // nchunks > 1: [nchunks][NC][tiles * 16]
+    int64_t prow;        // tiles * 16
+    const float * x;     // !PRE: x itself (columns x_s1 floats apart, 16-byte aligned), K elements
+    int64_t x_s1, K;
+};
+
+// one work-group per 16 x 32 = 512 elements... (64 threads: 16 segments, 4 lanes each)
+__global__ __launch_bounds__(64) void k_x_planes(const float * x, int64_t x_s1, int64_t K, int64_t nsegp, XSeg * planes, float4 * fac) {
+    const int lane = threadIdx.x, q = lane & 3;
+    const int64_t n = blockIdx.y;
+    const int64_t g = (int64_t) blockIdx.x * 16 + (lane >> 2);
+    const int64_t e = 32 * g + 8 * q;
+    float v[8];
+    const float * xp = x + n * x_s1 + e;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = e < K ? xp[i] : 0.0f;
+    // convert_seg writes segment (lane >> 2) of the 16 starting at this block's first
+    convert_seg(v, lane >> 2, 16, q, planes + n * nsegp + (int64_t) blockIdx.x * 16, fac + n * nsegp + (int64_t) blockIdx.x * 16);
+}
+
+// PRE: x comes converted from k_x_planes; else each wave converts its own range of x here (after
+// issuing its weight loads), which saves the pre-pass launch where the columns are few
+// 4 waves per SIMD (two work-groups per CU) where that fits without spilling
+constexpr int mc_waves(int dt, int nc) {
+    return (dt == Q4_K && nc == 8) || (dt == Q6_K && nc == 7) ? 3 : 4;
+}
+
+template <int DT, int NC, bool PRE>
+__global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(mc_waves(DT, NC), 8))) void k_mvc(McArgs A) {
+    using F = FmtN<DT>;
+    using Raw = typename F::Raw;
+    using AL = ALaneN<DT, NC>;
+    constexpr int G = F::G, CPS = AL::CPS, NS = AL::NS, W = kMcW, SPW = kMcSpw, SEGS = SPW * kSegs;
+    extern __shared__ uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, part = lane >> 4;
+    const int64_t rt = blockIdx.x;
+    const int c = (int) blockIdx.y;
+    const int64_t sb = (int64_t) c * kMcChunk + wave * SPW;
+    const int ns = (int) max<int64_t>(0, min<int64_t>(SPW, A.nst - sb));
+
+    // x planes of the wave's 2 steps for every column (the scratch holds whole chunks, zero past K)
+    // (plain scalars: arrays of vector types end up in scratch memory). x of the first pass of
+    // columns now, ahead of the weights; the second pass's (NC > 4) once the first is in LDS
+    constexpr int PC = NC < 4 ? NC : 4, NP = (NC + 3) / 4;
+    uint32_t xq[PC][4];
+    float xfq[PC][4];
+    float xe[PC][8];
+    const int64_t e = sb * kStep + 32 * (lane >> 2) + 8 * (lane & 3); // !PRE: lane's 8 elements
+    const bool xok = e < A.K && (lane >> 2) < ns * kSegs;
+    auto load_x = [&](int c0) {
+#pragma unroll
+        for (int k = 0; k < PC; ++k) {
+            const int n = c0 + k < NC ? c0 + k : c0; // (a column past NC re-reads the pass's first)
+            if constexpr (PRE) {
+                const uint4 q = reinterpret_cast<const uint4 *>(A.planes + n * A.nsegp + sb * kSegs)[lane];
+                const float4 fq = A.fac[n * A.nsegp + sb * kSegs + (lane & 15)];
+                xq[k][0] = q.x; xq[k][1] = q.y; xq[k][2] = q.z; xq[k][3] = q.w;
+                xfq[k][0] = fq.x; xfq[k][1] = fq.y; xfq[k][2] = fq.z; xfq[k][3] = fq.w;
+            } else {
+                // branch-free: past K (or past the wave's steps) re-read element 0 and drop it
+                const float * xp = A.x + n * A.x_s1 + (xok ? e : 0);
+                const float4 u = *reinterpret_cast<const float4 *>(xp);
+                const float4 w = *reinterpret_cast<const float4 *>(xp + 4);
+                xe[k][0] = xok ? u.x : 0.0f; xe[k][1] = xok ? u.y : 0.0f; xe[k][2] = xok ? u.z : 0.0f; xe[k][3] = xok ? u.w : 0.0f;
+                xe[k][4] = xok ? w.x : 0.0f; xe[k][5] = xok ? w.y : 0.0f; xe[k][6] = xok ? w.z : 0.0f; xe[k][7] = xok ? w.w : 0.0f;
+            }
+        }
+    };
+    load_x(0);
+    __builtin_amdgcn_sched_barrier(0);
+    const int j = rt >= A.tstart[1] ? (rt >= A.tstart[2] ? 2 : 1) : 0;
+    const int64_t M = A.M[j], m0 = (rt - A.tstart[j]) * 16;
+    F f;
+    {
+        const int64_t m = min(m0 + r, M - 1), g0 = m & ~(int64_t) 31;
+        f.init(A.w[j], M, A.nb, g0, (int) min<int64_t>(32, M - g0), (int) (m - g0), part);
+    }
+    Raw buf[SPW];
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) buf[s] = f.load(s < ns ? sb + s : (ns > 0 ? sb : 0));
+    __builtin_amdgcn_sched_barrier(0);
+
+    // LDS holds PC columns' x at a time: columns go through it in passes of up to 4 (the
+    // weights stay in registers), so that NC = 5..8 still leaves room for two work-groups per CU
+    XSeg * xs = reinterpret_cast<XSeg *>(lds) + (size_t) wave * PC * SEGS;
+    float4 * xf = reinterpret_cast<float4 *>(reinterpret_cast<XSeg *>(lds) + (size_t) W * PC * SEGS) + (size_t) wave * PC * SEGS;
+    float * red = reinterpret_cast<float *>(reinterpret_cast<float4 *>(reinterpret_cast<XSeg *>(lds) + (size_t) W * PC * SEGS) + (size_t) W * PC * SEGS);
+    uint8_t * zpad = reinterpret_cast<uint8_t *>(red + W * NC * 16);
+    if (tid < 4) reinterpret_cast<uint32_t *>(zpad)[tid] = 0u;
+    __syncthreads(); // (zpad is written by wave 0 for all)
+
+    const AL al(lane);
+    const XView xv{xs, xf, zpad, SEGS};
+    float acc[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) acc[s] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+        if (q > 0) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+#pragma unroll
+        for (int k = 0; k < PC; ++k) {
+            if (4 * q + k < NC) {
+                if constexpr (PRE) {
+                    reinterpret_cast<uint4 *>(xs + k * SEGS)[lane] = make_uint4(xq[k][0], xq[k][1], xq[k][2], xq[k][3]);
+                    if (lane < 16) xf[k * SEGS + lane] = make_float4(xfq[k][0], xfq[k][1], xfq[k][2], xfq[k][3]);
+                } else {
+                    convert_seg(xe[k], lane >> 2, SEGS, lane & 3, xs + k * SEGS, xf + k * SEGS);
+                }
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (q + 1 < NP) load_x(4 * (q + 1)); // the next pass's x, in flight during this pass
+        // pass q: the sets of columns 4q .. 4q + 3
+#pragma unroll
+        for (int s = 0; s < SPW; ++s) {
+            if (s < ns) {
+                if (q == 0) step_mfma_n<DT, NC, 0, (4 / CPS < NS ? 4 / CPS : NS)>(f, buf[s], al, s * kSegs, xv, acc, lane, 0);
+                else step_mfma_n<DT, NC, (4 / CPS < NS ? 4 / CPS : NS), NS>(f, buf[s], al, s * kSegs, xv, acc, lane, 4);
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        float v = acc[s];
+        if constexpr (G == 4) v += __shfl_xor(v, 16);
+        const int n = s * CPS + (G == 2 ? part : part >> 1);
+        if (n < NC && (G == 2 || (part & 1) == 0)) red[(wave * NC + n) * 16 + r] = v;
+    }
+    __syncthreads();
+    if (tid < NC * 16) {
+        const int n = tid / 16, rr = tid % 16;
+        float v = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < W; ++w2) v += red[(w2 * NC + n) * 16 + rr];
+        if (A.nchunks == 1) {
+            if (m0 + rr < M) A.y[j][n * A.ys1[j] + m0 + rr] = v;
+        } else {
+            A.part[((int64_t) c * NC + n) * A.prow + rt * 16 + rr] = v;
+        }
+    }
+}
+
+// the chunks' partial sums of row tile rows, added in chunk order
+__global__ __launch_bounds__(256) void k_mvc_reduce(McArgs A, int nc) {
+    const int64_t gr = (int64_t) blockIdx.x * 256 + threadIdx.x; // row over all row tiles
+    const int n = blockIdx.y;
+    if (gr >= A.prow) return;
+    const int64_t rt = gr / 16;
+    const int j = rt >= A.tstart[1] ? (rt >= A.tstart[2] ? 2 : 1) : 0;
+    const int64_t m = (rt - A.tstart[j]) * 16 + gr % 16;
+    if (m >= A.M[j]) return;
+    float v = 0.0f;
+    for (int64_t c = 0; c < A.nchunks; ++c) v += A.part[(c * nc + n) * A.prow + gr];
+    A.y[j][n * A.ys1[j] + m] = v;
+}
+
+template <int DT, bool PRE>
+void * pick_mvc_p(int nc) {
+    switch (nc) {
+        case 2: return (void *) k_mvc<DT, 2, PRE>;
+        case 3: return (void *) k_mvc<DT, 3, PRE>;
+        case 4: return (void *) k_mvc<DT, 4, PRE>;
+        case 5: return (void *) k_mvc<DT, 5, PRE>;
+        case 6: return (void *) k_mvc<DT, 6, PRE>;
+        case 7: return (void *) k_mvc<DT, 7, PRE>;
+        default: return (void *) k_mvc<DT, 8, PRE>;
+    }
+}
+
+template <int DT>
+void * pick_mvc(int nc, bool pre) {
+    return pre ? pick_mvc_p<DT, true>(nc) : pick_mvc_p<DT, false>(nc);
+}
+
 template <int DT, int RG>
 void * pick_burst_rg(int W, int spw) {
     if (spw <= 2) return W >= 16 ? (void *) k_mvb<DT, RG, 16, 2> : W >= 8 ? (void *) k_mvb<DT, RG, 8, 2> : (void *) k_mvb<DT, RG, 4, 2>;
@@ -808,8 +1424,29 @@ void set_tiles(MvArgs & L, const MatArgs * mats, int nmat, int R) {
 
 } // namespace
 
+// the multi-column form applies (several columns, one slice, not MUL_MAT_ID)
+static bool mc_form(const MatArgs * mats, int nmat, const IdArgs * id) {
+    static const bool on = [] {
+        const char * v = std::getenv("SCRAPGPU_HIP_MV_MC");
+        return v == nullptr || v[0] != '0';
+    }();
+    (void) nmat;
+    return on && id == nullptr && mats[0].N >= 2 && mats[0].N <= 8 && mats[0].ne12 * mats[0].ne13 == 1;
+}
+
+size_t matvec_scratch_bytes(const MatArgs * mats, int nmat, const IdArgs * id) {
+    if (nmat < 1 || !mc_form(mats, nmat, id)) return 0;
+    const int64_t nst = (mats[0].K + kStep - 1) / kStep, nchunks = (nst + kMcChunk - 1) / kMcChunk, nsegp = nchunks * kMcChunk * kSegs;
+    int64_t tiles = 0;
+    for (int j = 0; j < nmat; ++j) tiles += (mats[j].M + 15) / 16;
+    const size_t nc = (size_t) mats[0].N;
+    size_t b = (nc * (size_t) nsegp * sizeof(XSeg) + 255) / 256 * 256 + (nc * (size_t) nsegp * sizeof(float4) + 255) / 256 * 256;
+    if (nchunks > 1) b += (size_t) nchunks * nc * (size_t) tiles * 16 * sizeof(float);
+    return b;
+}
+
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
-                         uint64_t * grid_size, const IdArgs * id) {
+                         uint64_t * grid_size, const IdArgs * id, uint8_t * scratch) {
     if (nmat < 1 || nmat > 3) return hipErrorInvalidValue;
     const MatArgs & a = mats[0];
     for (int j = 0; j < nmat; ++j) {
@@ -891,6 +1528,59 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         return hipLaunchKernel(fn, dim3((unsigned) L.tiles, (unsigned) slices), dim3((unsigned) (64 * W)), args, lds, stream);
     }
 
+    if (scratch != nullptr && mc_form(mats, nmat, id)) {
+        // several columns: x pre-pass, then one work-group per 16 rows and K chunk
+        McArgs C;
+        std::memset(&C, 0, sizeof(C));
+        C.tstart[0] = 0;
+        for (int j = 0; j < 3; ++j) {
+            const bool has = j < nmat;
+            C.w[j] = has ? mats[j].w : nullptr;
+            C.M[j] = has ? mats[j].M : 0;
+            C.y[j] = has ? mats[j].y : nullptr;
+            C.ys1[j] = has ? mats[j].y_s1 : 0;
+            C.tstart[j + 1] = has ? C.tstart[j] + (mats[j].M + 15) / 16 : INT64_MAX;
+        }
+        const int64_t tiles = C.tstart[nmat];
+        C.nb = L.nb;
+        C.nst = nst;
+        C.nchunks = (nst + kMcChunk - 1) / kMcChunk;
+        C.nsegp = C.nchunks * kMcChunk * kSegs;
+        XSeg * planes = reinterpret_cast<XSeg *>(scratch);
+        float4 * fac = reinterpret_cast<float4 *>(scratch + ((size_t) nc * C.nsegp * sizeof(XSeg) + 255) / 256 * 256);
+        C.planes = planes;
+        C.fac = fac;
+        C.prow = tiles * 16;
+        C.part = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(fac) + ((size_t) nc * C.nsegp * sizeof(float4) + 255) / 256 * 256);
+        C.x = a.x;
+        C.x_s1 = a.x_s1;
+        C.K = a.K;
+        // the x pre-pass once the columns are many (SCRAPGPU_HIP_MV_PRE: the smallest column count
+        // that takes it; x must be 16-byte aligned for the in-kernel conversion)
+        static const int pre_from = tuning("SCRAPGPU_HIP_MV_PRE", 4);
+        const bool pre = nc >= pre_from || !L.xvec;
+        hipError_t e = hipSuccess;
+        if (pre) {
+            hipLaunchKernelGGL(k_x_planes, dim3((unsigned) (C.nsegp / 16), (unsigned) nc), dim3(64), 0, stream, a.x, a.x_s1, a.K, C.nsegp, planes, fac);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+        void * fn = dt == Q4_0 ? pick_mvc<Q4_0>(nc, pre) : dt == Q8_0 ? pick_mvc<Q8_0>(nc, pre) : dt == Q4_K ? pick_mvc<Q4_K>(nc, pre) : pick_mvc<Q6_K>(nc, pre);
+        const size_t lds = (size_t) kMcW * std::min(nc, 4) * kMcSpw * kSegs * (sizeof(XSeg) + sizeof(float4)) + (size_t) kMcW * nc * 16 * sizeof(float) + 16;
+        if (lds > 65536) {
+            static std::mutex mu;
+            std::lock_guard<std::mutex> lock(mu);
+            if ((e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds)) != hipSuccess) return e;
+        }
+        if (grid_size) *grid_size = (uint64_t) tiles * (uint64_t) C.nchunks;
+        std::snprintf(last_form().form, sizeof(last_form().form), "columns nc=%d chunks=%d%s", nc, (int) C.nchunks, pre ? " pre" : "");
+        last_form().grid = (uint64_t) tiles * (uint64_t) C.nchunks;
+        void * args[] = {&C};
+        e = hipLaunchKernel(fn, dim3((unsigned) tiles, (unsigned) C.nchunks), dim3(64 * kMcW), args, lds, stream);
+        if (e != hipSuccess || C.nchunks == 1) return e;
+        hipLaunchKernelGGL(k_mvc_reduce, dim3((unsigned) ((C.prow + 255) / 256), (unsigned) nc), dim3(256), 0, stream, C, nc);
+        return hipGetLastError();
+    }
+
     // streaming form (several columns, or K too long for the burst form)
     set_tiles(L, mats, nmat, 16);
     const int W = nc == 1 ? 8 : 4;
@@ -901,7 +1591,14 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     L.cs = (int) cs;
     const size_t lds = (size_t) W * cs * step_bytes + (size_t) 2 * W * nc * 16 * sizeof(float) + 16;
     if (lds > (size_t) 160 * 1024) return hipErrorInvalidValue;
-    void * fn = dt == Q4_0 ? pick_stream<Q4_0>(nc) : dt == Q8_0 ? pick_stream<Q8_0>(nc) : dt == Q4_K ? pick_stream<Q4_K>(nc) : pick_stream<Q6_K>(nc);
+    // several columns: the columns share each MFMA (k_mvn); SCRAPGPU_HIP_MV_COLS=0 runs one MFMA
+    // set per column (k_mvs)
+    void * fn = nullptr;
+    if (nc >= 2 && tuning("SCRAPGPU_HIP_MV_COLS", 1)) {
+        fn = dt == Q4_0 ? pick_columns<Q4_0>(nc) : dt == Q8_0 ? pick_columns<Q8_0>(nc) : dt == Q4_K ? pick_columns<Q4_K>(nc) : pick_columns<Q6_K>(nc);
+    } else {
+        fn = dt == Q4_0 ? pick_stream<Q4_0>(nc) : dt == Q8_0 ? pick_stream<Q8_0>(nc) : dt == Q4_K ? pick_stream<Q4_K>(nc) : pick_stream<Q6_K>(nc);
+    }
 
     // persistent grid: as many work-groups as stay resident (at most one per tile), trimmed so
     // that every work-group gets the same number of tiles
@@ -910,7 +1607,7 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     const int64_t rounds = (L.tiles + cap - 1) / cap;
     const int64_t grid_x = (L.tiles + rounds - 1) / rounds;
     if (grid_size) *grid_size = (uint64_t) grid_x * (uint64_t) slices;
-    std::snprintf(last_form().form, sizeof(last_form().form), "stream nc=%d W=%d", nc, W);
+    std::snprintf(last_form().form, sizeof(last_form().form), "%s nc=%d W=%d", nc >= 2 && tuning("SCRAPGPU_HIP_MV_COLS", 1) ? "stream-columns" : "stream", nc, W);
     last_form().grid = (uint64_t) grid_x * (uint64_t) slices;
     void * args[] = {&L};
     return hipLaunchKernel(fn, dim3((unsigned) grid_x, (unsigned) slices), dim3((unsigned) (64 * W)), args, lds, stream);

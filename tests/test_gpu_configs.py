@@ -111,7 +111,7 @@ def test_config2_q8_0_llama_mlp(hip, K, M, N):
     q, _, wt = weights(hip, sg.Q8_0, K, M, 10 + K)
     x = O.normal(N * K, 20 + N).reshape(N, K)
     (y,), (form, grid) = run(hip, [wt], x)
-    assert form.startswith("burst" if N == 1 else "stream"), form
+    assert form.startswith("burst" if N == 1 else "columns"), form
     check(sg.Q8_0, q, K, M, x, y, f"Q8_0 {M}x{K} N={N} [{form}]")
 
 
@@ -184,7 +184,7 @@ def test_config5_q6_k_lm_head(hip, N):
     q, _, wt = weights(hip, sg.Q6_K, K, M, 700)
     x = O.normal(N * K, 70 + N).reshape(N, K)
     (y,), (form, grid) = run(hip, [wt], x)
-    assert form.startswith("burst" if N == 1 else "stream" if N <= 8 else "gemm"), form
+    assert form.startswith("burst" if N == 1 else "columns" if N <= 8 else "gemm"), form
     check(sg.Q6_K, q, K, M, x, y, f"Q6_K {M}x{K} N={N} [{form}]")
 
 
