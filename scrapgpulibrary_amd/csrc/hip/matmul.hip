@@ -1168,7 +1168,9 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
     c.rg = env_rg == 1 || env_rg == 2 ? env_rg : 1;
     const int64_t tm = (a.M + 128 * c.rg - 1) / (128 * c.rg);
     auto tiles = [&](int bn) { return tm * ((a.N + bn - 1) / bn) * slices; };
-    c.bn = env_bn == 64 || env_bn == 128 ? env_bn : (tiles(64) >= occupancy_of(a.dtype, 64, c.rg) * (int64_t) cu_count ? 64 : 128);
+    // (64 tokens or fewer: BN = 64 and K split to fill the CUs, rather than a half-padding
+    // 128-token tile: 38.6 -> 31.0 us on 12288x4096 at N = 64)
+    c.bn = env_bn == 64 || env_bn == 128 ? env_bn : (a.N <= 64 || tiles(64) >= occupancy_of(a.dtype, 64, c.rg) * (int64_t) cu_count ? 64 : 128);
     const int64_t want = (int64_t) cu_count * occupancy_of(a.dtype, c.bn, c.rg);
     c.split = 1;
     if (env_split > 0) {

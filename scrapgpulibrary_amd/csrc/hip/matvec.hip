@@ -1154,8 +1154,8 @@ void * pick_columns(int nc) {
 // two int8 planes and factors, in scratch), so the matvec work-groups only copy their part of it
 // into LDS. A work-group owns 16 rows and one K chunk of 16 steps (4096 elements): its 8 waves take
 // 2 steps each and issue all their loads at once (x planes first, then weights), like the
-// one-column burst form. With several chunks the work-groups write partial sums and
-// k_mvc_reduce adds them in chunk order.
+// one-column burst form. With several chunks the work-groups write partial sums, and the last
+// chunk of a row tile to finish (arrival counters cleared by the pre-pass) adds them in chunk order.
 
 constexpr int kMcW = 8, kMcSpw = 2, kMcChunk = kMcW * kMcSpw; // waves, steps per wave, steps per chunk
 
@@ -1170,14 +1170,18 @@ struct McArgs {
     const float4 * fac;  // [NC][nsegp]
     int64_t nsegp;       // segments per column in the scratch (nchunks * 128)
     float * part;        // nchunks > 1: [nchunks][NC][tiles * 16]
+    uint32_t * arrive;   // nchunks > 1: chunks done per row tile (zeroed by k_x_planes)
     int64_t prow;        // tiles * 16
     const float * x;     // !PRE: x itself (columns x_s1 floats apart, 16-byte aligned), K elements
     int64_t x_s1, K;
 };
 
 // one work-group per 16 x 32 = 512 elements... (64 threads: 16 segments, 4 lanes each)
-__global__ __launch_bounds__(64) void k_x_planes(const float * x, int64_t x_s1, int64_t K, int64_t nsegp, XSeg * planes, float4 * fac) {
+__global__ __launch_bounds__(64) void k_x_planes(const float * x, int64_t x_s1, int64_t K, int64_t nsegp, XSeg * planes, float4 * fac,
+                                                 uint32_t * arrive, int64_t narrive) {
     const int lane = threadIdx.x, q = lane & 3;
+    // the K-chunk arrival counters of the matvec that follows start at zero
+    for (int64_t i = ((int64_t) blockIdx.y * gridDim.x + blockIdx.x) * 64 + lane; i < narrive; i += (int64_t) gridDim.x * gridDim.y * 64) arrive[i] = 0u;
     const int64_t n = blockIdx.y;
     const int64_t g = (int64_t) blockIdx.x * 16 + (lane >> 2);
     const int64_t e = 32 * g + 8 * q;
@@ -1311,23 +1315,30 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(mc_wa
         if (A.nchunks == 1) {
             if (m0 + rr < M) A.y[j][n * A.ys1[j] + m0 + rr] = v;
         } else {
-            A.part[((int64_t) c * NC + n) * A.prow + rt * 16 + rr] = v;
+            // the chunk's partial sums, visible to every XCD before the row tile's count moves
+            // (agent-scope stores write through the L2; then wait for them)
+            __hip_atomic_store(A.part + ((int64_t) c * NC + n) * A.prow + rt * 16 + rr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-}
-
-// the chunks' partial sums of row tile rows, added in chunk order
-__global__ __launch_bounds__(256) void k_mvc_reduce(McArgs A, int nc) {
-    const int64_t gr = (int64_t) blockIdx.x * 256 + threadIdx.x; // row over all row tiles
-    const int n = blockIdx.y;
-    if (gr >= A.prow) return;
-    const int64_t rt = gr / 16;
-    const int j = rt >= A.tstart[1] ? (rt >= A.tstart[2] ? 2 : 1) : 0;
-    const int64_t m = (rt - A.tstart[j]) * 16 + gr % 16;
-    if (m >= A.M[j]) return;
-    float v = 0.0f;
-    for (int64_t c = 0; c < A.nchunks; ++c) v += A.part[(c * nc + n) * A.prow + gr];
-    A.y[j][n * A.ys1[j] + m] = v;
+    if (A.nchunks == 1) return;
+    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this wave's partial-sum stores are done
+    __syncthreads();
+    // (in the dynamic LDS after zpad: a static __shared__ would shift the dynamic block off its
+    // 16-byte alignment)
+    uint32_t & last = *reinterpret_cast<uint32_t *>(zpad + 16);
+    if (tid == 0) last = __hip_atomic_fetch_add(A.arrive + rt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t) A.nchunks - 1;
+    __syncthreads();
+    // the last chunk of the row tile to finish adds all of them, in chunk order (agent-scope
+    // loads: the other chunks' sums may come from other XCDs)
+    if (last && tid < NC * 16) {
+        const int n = tid / 16, rr = tid % 16;
+        if (m0 + rr < M) {
+            float v = 0.0f;
+            for (int64_t cc = 0; cc < A.nchunks; ++cc)
+                v += __hip_atomic_load(A.part + (cc * NC + n) * A.prow + rt * 16 + rr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            A.y[j][n * A.ys1[j] + m0 + rr] = v;
+        }
+    }
 }
 
 template <int DT, bool PRE>
@@ -1441,7 +1452,7 @@ size_t matvec_scratch_bytes(const MatArgs * mats, int nmat, const IdArgs * id) {
     for (int j = 0; j < nmat; ++j) tiles += (mats[j].M + 15) / 16;
     const size_t nc = (size_t) mats[0].N;
     size_t b = (nc * (size_t) nsegp * sizeof(XSeg) + 255) / 256 * 256 + (nc * (size_t) nsegp * sizeof(float4) + 255) / 256 * 256;
-    if (nchunks > 1) b += (size_t) nchunks * nc * (size_t) tiles * 16 * sizeof(float);
+    if (nchunks > 1) b += ((size_t) nchunks * nc * (size_t) tiles * 16 * sizeof(float) + 255) / 256 * 256 + (size_t) tiles * sizeof(uint32_t);
     return b;
 }
 
@@ -1552,20 +1563,23 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         C.fac = fac;
         C.prow = tiles * 16;
         C.part = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(fac) + ((size_t) nc * C.nsegp * sizeof(float4) + 255) / 256 * 256);
+        C.arrive = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(C.part) + ((size_t) C.nchunks * nc * (size_t) tiles * 16 * sizeof(float) + 255) / 256 * 256);
         C.x = a.x;
         C.x_s1 = a.x_s1;
         C.K = a.K;
         // the x pre-pass once the columns are many (SCRAPGPU_HIP_MV_PRE: the smallest column count
         // that takes it; x must be 16-byte aligned for the in-kernel conversion)
         static const int pre_from = tuning("SCRAPGPU_HIP_MV_PRE", 4);
-        const bool pre = nc >= pre_from || !L.xvec;
+        // (several K chunks: the pre-pass also clears their arrival counters)
+        const bool pre = nc >= pre_from || !L.xvec || C.nchunks > 1;
         hipError_t e = hipSuccess;
         if (pre) {
-            hipLaunchKernelGGL(k_x_planes, dim3((unsigned) (C.nsegp / 16), (unsigned) nc), dim3(64), 0, stream, a.x, a.x_s1, a.K, C.nsegp, planes, fac);
+            hipLaunchKernelGGL(k_x_planes, dim3((unsigned) (C.nsegp / 16), (unsigned) nc), dim3(64), 0, stream, a.x, a.x_s1, a.K, C.nsegp, planes, fac,
+                               C.arrive, C.nchunks > 1 ? tiles : (int64_t) 0);
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
         void * fn = dt == Q4_0 ? pick_mvc<Q4_0>(nc, pre) : dt == Q8_0 ? pick_mvc<Q8_0>(nc, pre) : dt == Q4_K ? pick_mvc<Q4_K>(nc, pre) : pick_mvc<Q6_K>(nc, pre);
-        const size_t lds = (size_t) kMcW * std::min(nc, 4) * kMcSpw * kSegs * (sizeof(XSeg) + sizeof(float4)) + (size_t) kMcW * nc * 16 * sizeof(float) + 16;
+        const size_t lds = (size_t) kMcW * std::min(nc, 4) * kMcSpw * kSegs * (sizeof(XSeg) + sizeof(float4)) + (size_t) kMcW * nc * 16 * sizeof(float) + 32;
         if (lds > 65536) {
             static std::mutex mu;
             std::lock_guard<std::mutex> lock(mu);
@@ -1575,10 +1589,7 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         std::snprintf(last_form().form, sizeof(last_form().form), "columns nc=%d chunks=%d%s", nc, (int) C.nchunks, pre ? " pre" : "");
         last_form().grid = (uint64_t) tiles * (uint64_t) C.nchunks;
         void * args[] = {&C};
-        e = hipLaunchKernel(fn, dim3((unsigned) tiles, (unsigned) C.nchunks), dim3(64 * kMcW), args, lds, stream);
-        if (e != hipSuccess || C.nchunks == 1) return e;
-        hipLaunchKernelGGL(k_mvc_reduce, dim3((unsigned) ((C.prow + 255) / 256), (unsigned) nc), dim3(256), 0, stream, C, nc);
-        return hipGetLastError();
+        return hipLaunchKernel(fn, dim3((unsigned) tiles, (unsigned) C.nchunks), dim3(64 * kMcW), args, lds, stream);
     }
 
     // streaming form (several columns, or K too long for the burst form)
