@@ -786,7 +786,7 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
     // prefill weights of one dtype reading the same x (one slice each): one GEMM launch over all
     bool fuse_mm = n > 1 && mats[0].N > mv_n && mats[0].ne12 * mats[0].ne13 == 1;
     for (int j = 1; j < n && fuse_mm; ++j) {
-        fuse_mm = mats[j].dtype == mats[0].dtype && sgk::matmul_same_x(mats[j], mats[0]) && mats[j].ne12 * mats[j].ne13 == 1;
+        fuse_mm = mats[j].dtype == mats[0].dtype && sgk::matmul_reads_same_x(mats[j], mats[0]) && mats[j].ne12 * mats[j].ne13 == 1;
     }
     if (fuse_mm) {
         sgk::MatArgs all = mats[0];
@@ -840,7 +840,7 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
             if (st != SCRAPGPU_STATUS_OK) return st;
             ProfScope prof(s->s);
             const char * name = nullptr;
-            const bool x_ready = !fuse && gi > 0 && mats[gi - 1].N > mv_n && sgk::matmul_same_x(mats[gi - 1], m[0]);
+            const bool x_ready = !fuse && gi > 0 && mats[gi - 1].N > mv_n && sgk::matmul_same_x(mats[gi - 1], m[0], cus);
             SG_HIP(sgk::launch_matmul_mfma(m, 1, scr, cus, s->s, &name, x_ready), "matmul launch");
             prof.done(name, bytes, flops);
         }

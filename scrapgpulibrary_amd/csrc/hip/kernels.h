@@ -71,16 +71,19 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
 // `scratch` (matmul_scratch_bytes(a, cu_count) bytes of device memory, owned by the stream)
 // receives x as scaled f16 rows with their factors and, when K is split over work-groups, the
 // partial sums.
-// nmat = 1, or 2..3 single-slice weights of one dtype that read the same x (matmul_same_x): one
+// nmat = 1, or 2..3 single-slice weights of one dtype that read the same x (matmul_reads_same_x): one
 // launch over all their row tiles (run end to end over all their rows when every weight but the
 // last has a whole number of a wave's 32 or 64 rows); matmul_scratch_bytes then takes mats[0] with M = the sum of the
 // matrices' M.
 size_t matmul_scratch_bytes(const MatArgs & a, int cu_count);
 hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name,
                               bool x_ready = false);
-// true when b's x pre-pass would write what a's did (same x, shape and dtype class): a product
+// true when b's x pre-pass would write what a's did (same x and shape, and the same x form: the
+// Q4_K single-fma kernels read x in a form of their own): a product
 // launched right after a's on the same scratch may then pass x_ready and skip its own
-bool matmul_same_x(const MatArgs & a, const MatArgs & b);
+bool matmul_same_x(const MatArgs & a, const MatArgs & b, int cu_count);
+// true when a and b read the same x with the same shape (what one fused launch over both needs)
+bool matmul_reads_same_x(const MatArgs & a, const MatArgs & b);
 
 // MUL_MAT_ID with many tokens (prefill): the (slot, token) pairs are grouped by expert on the
 // device (ids clamped as above), x goes through the matmul's pre-pass once, and the f16 MFMA GEMM

@@ -456,6 +456,11 @@ struct MmArgs {
     int64_t ys1m[3];
 };
 
+// padded x tile rows (the wide GEMM): 16-byte chunk c of token n at n * XR + 8 c (f16). The 16
+// bytes of padding put consecutive tokens 4 banks apart, so the 16 lanes of one ds_read_b128
+// cycle (16 tokens, one chunk) cover all 64 banks, and a lane's 8 k-steps are immediate offsets.
+constexpr int XR = BK + 8;
+
 // x tile in LDS: row n (token), 16-byte chunk c at (n * kChunks + (c ^ (n & 15))) * 8 f16
 __device__ __forceinline__ int xsw(int n, int c) {
     return (n * kChunks + (c ^ (n & 15))) * 8;
@@ -907,6 +912,177 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
     }
 }
 
+// The wide GEMM's x tile, straight from the f16 rows into LDS (global_load_lds_dwordx4: lane i of
+// one instruction writes 16 bytes at the instruction's LDS base + 16 i, no registers on the way).
+// A token row is 17 slots of 16 bytes (16 chunks + the pad, which receives a second copy of chunk
+// 15), so the 128-token tile is 2176 slots = exactly 34 wave instructions; LW loading waves take
+// instructions w, w + LW, ...; a wave's index past the 34th repeats the 34th (the same bytes to the
+// same slots). Tokens past N read token N - 1 (their products are never stored); K is a multiple
+// of the stage, so no chunk lies past the row.
+template <int LW, int BN = 128>
+struct XDma {
+    static constexpr int INS = BN * 17 / 64;
+    static constexpr int NI = (INS + LW - 1) / LW;
+    uint32_t off[NI]; // byte offset of the lane's (token, chunk) in the slice's x rows at stage 0
+    int wv;
+    __device__ void init(int64_t N, int64_t K, int64_t n0, int wv_, int lane) {
+        wv = wv_;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int ins = min(wv + LW * i, INS - 1);
+            const int slot = ins * 64 + lane, n = slot / 17, c = min(slot - 17 * n, 15);
+            off[i] = 2 * ((uint32_t) (min<int64_t>(n0 + n, N - 1) * K) + 8 * c);
+        }
+    }
+    // the stage starting at element k0 into the LDS tile X
+    __device__ void load(const uint16_t * xb, int k0, uint16_t * X) const {
+        const uint8_t * base = reinterpret_cast<const uint8_t *>(xb) + 2 * (uint32_t) k0;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int ins = min(wv + LW * i, INS - 1);
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(base + off[i]),
+                                             (__attribute__((address_space(3))) void *) (X + ins * 64 * 8), 16, 0, 0);
+        }
+    }
+};
+
+// The wide GEMM: one 12-wave work-group per CU as in the 12-wave k_matmul, but each wave owns 32
+// weight rows x 128 tokens (4 token fragments), so every dequantized B fragment feeds 4 MFMAs
+// instead of 2 (a 384-row x 128-token tile). The dequantization VALU per MFMA halves; the
+// registers for the extra accumulators come from the exact Q4_K form (s (c + bias) + o per pair,
+// from plain x: no offset MFMA, no sub-block sums, no rare-scale branch), one set of A fragments
+// (each read again right after the MFMA that consumed it), x tiles loaded straight into LDS and
+// padded x rows (immediate LDS offsets). Measured on 12288 x 4096: 273 against 295 us at 2048
+// tokens, and gate+up (24576 rows) at 512 tokens 132 against 141 us. Splitting K over 2 groups of
+// 6 waves in the work-group (192-row tiles, for shapes these tiles do not fill) measured slower
+// than the 64-token form (70 against 65 us at 12288 x 4096 x 512), as did wave tiles of 64 rows x
+// 64 tokens (half the LDS reads per MFMA, twice the dequantization: 96 us). Split-K over
+// work-groups (partials + k_split_reduce) as in k_matmul.
+template <int DT>
+__global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
+    constexpr int W = 12, NF = 4, BN = 32 * NF, BMT = 32 * W;
+    using F = PFmt<DT>;
+    using Raw = typename F::Raw;
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds_mm[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // wave-uniform: scalar addressing
+    const int j = lane & 31, h = lane >> 5;
+    const int64_t tile = blockIdx.x / L.split;
+    const int split = (int) (blockIdx.x % L.split);
+    const int64_t tm = tile % L.tiles_m, tn = tile / L.tiles_m;
+    const int64_t sl = blockIdx.y;
+    const int64_t i2 = sl % L.a.ne12, i3 = sl / L.a.ne12;
+    const int64_t grow = tm * BMT + 32 * wave;
+    const int mj = L.nmat == 1 ? 0
+                 : L.packed    ? min(L.nmat - 1, grow >= L.mo[1] ? (grow >= L.mo[2] ? 2 : 1) : 0)
+                               : (tm >= L.mt[1] ? (tm >= L.mt[2] ? 2 : 1) : 0);
+    const uint8_t * w = L.nmat > 1 ? L.wm[mj] : L.a.w + (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
+    const int64_t K = L.a.K, nb = L.a.nb, N = L.a.N;
+    const int64_t M = L.nmat > 1 ? L.Mm[mj] : L.a.M;
+    const int64_t n0 = tn * BN;
+    const int64_t m0 = L.packed ? grow - L.mo[mj] : (tm - L.mt[mj]) * BMT + 32 * wave;
+    // the split's stages (whole groups of 4, as in k_matmul)
+    const int64_t groups = (L.stages + 3) / 4;
+    const int s0 = (int) (4 * (groups * split / L.split));
+    const int s1 = (int) min(4 * (groups * (split + 1) / L.split), L.stages);
+    const int lim = s1 - 1;
+
+    F f;
+    f.init(M, nb, RowAddr(M, m0 + j), h);
+    const uint16_t * xb = L.xb + (uint64_t) sl * N * K;
+    XDma<W, BN> xt;
+    xt.init(N, K, n0, wave, lane);
+    const int abase = j * XR; // + 32 q XR + 8 chunk(h, t): immediate offsets
+
+    f32x16 acc[NF];
+#pragma unroll
+    for (int q = 0; q < NF; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[q][v] = 0.0f;
+
+    // one stage: the weights of stage s + 1 into nw and its x tile into the other LDS buffer
+    // (read by every wave before the last barrier) while the MFMAs run over buffer s % 2
+    auto stage = [&](auto dtag, int s, const Raw & cw, Raw & nw) __attribute__((always_inline)) {
+        constexpr int D = decltype(dtag)::value;
+        const int sn = min(s + 1, lim);
+        if constexpr ((DT == Q4_K || DT == Q6_K) && (D & 1) == 0) nw = f.load_half2(w, sn, cw);
+        else nw = f.load(w, sn);
+        if (s + 1 < s1) xt.load(xb, (s + 1) * BK, lds_mm + ((D + 1) & 1) * (BN * XR));
+        const uint16_t * X = lds_mm + (D & 1) * (BN * XR) + abase;
+        const typename F::Sc sc = f.prep(cw, (s & ~3) | D);
+        f16x8 a[NF];
+#pragma unroll
+        for (int q = 0; q < NF; ++q) a[q] = *reinterpret_cast<const f16x8 *>(X + q * 32 * XR + 8 * F::chunk(h, 0));
+        f16x8 b = F::bop(cw, sc, 0);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            // issue priority falling through the stage: the waves of a SIMD that are behind win
+            // the arbitration, so they reach the stage barrier together
+            if (t == 0) __builtin_amdgcn_s_setprio(3);
+            if (t == 2) __builtin_amdgcn_s_setprio(2);
+            if (t == 4) __builtin_amdgcn_s_setprio(1);
+            if (t == 6) __builtin_amdgcn_s_setprio(0);
+            f16x8 bn;
+            if (t < 7) bn = F::bop(cw, sc, t + 1);
+#pragma unroll
+            for (int q = 0; q < NF; ++q) {
+                acc[q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[q], b, acc[q], 0, 0, 0);
+                if (t < 7) a[q] = *reinterpret_cast<const f16x8 *>(X + q * 32 * XR + 8 * F::chunk(h, t + 1));
+            }
+            if (t < 7) b = bn;
+        }
+        __syncthreads(); // (waits for this wave's loads: the next x tile is in LDS)
+    };
+    Raw ra{}, rb{};
+    ra = f.load(w, s0);
+    xt.load(xb, s0 * BK, lds_mm);
+    __syncthreads();
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    int s = s0;
+    for (; s + 3 < s1; s += 4) {
+        stage(I0{}, s, ra, rb);
+        stage(I1{}, s + 1, rb, ra);
+        stage(I2{}, s + 2, ra, rb);
+        stage(I3{}, s + 3, rb, ra);
+    }
+    if (s < s1) {
+        stage(I0{}, s, ra, rb);
+        if (s + 1 < s1) {
+            stage(I1{}, s + 1, rb, ra);
+            if (s + 2 < s1) stage(I2{}, s + 2, ra, rb);
+        }
+    }
+    // acc[q][v], lane (j, h): token n0 + 32q + 8 (v / 4) + 4h + v % 4, weight row m0 + j
+    const int64_t slices = L.a.ne12 * L.a.ne13;
+    float * y;
+    int64_t ys1;
+    if (L.split == 1) {
+        y = L.nmat > 1 ? L.ym[mj] : L.a.y + i2 * L.a.y_s2 + i3 * L.a.y_s3;
+        ys1 = L.nmat > 1 ? L.ys1m[mj] : L.a.y_s1;
+    } else {
+        const int64_t mt_all = L.mo[L.nmat];
+        y = L.part + ((uint64_t) split * slices + (uint64_t) sl) * N * mt_all + L.mo[mj];
+        ys1 = mt_all;
+    }
+    const float * xs = L.xs + (uint64_t) sl * N;
+    const int64_t m = m0 + j;
+#pragma unroll
+    for (int q = 0; q < NF; ++q) {
+        float u[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) u[v] = xs[min<int64_t>(n0 + 32 * q + 8 * (v >> 2) + 4 * h + (v & 3), N - 1)];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int64_t n = n0 + 32 * q + 8 * (v >> 2) + 4 * h + (v & 3);
+            // (outputs are not read again by this kernel: stores that bypass the caches)
+            if (n < N && m < M) __builtin_nontemporal_store(acc[q][v] * u[v], y + n * ys1 + m);
+        }
+    }
+}
+
 // y = sum of the split-K partials, in split order. blockIdx.x is the row (token n of slice sl),
 // blockIdx.y covers 1024 columns of it (all matrices' rows when several share x; column c is row
 // c - mo[j] of matrix j); VEC when every matrix's rows and y's row starts allow float4 accesses.
@@ -1111,6 +1287,7 @@ struct MmConfig {
     int split;
     int w;  // waves per work-group: 4, or 12 (one work-group per CU, see k_matmul)
     int kg; // K groups of a 12-wave work-group: 1 or 3
+    bool wide = false; // k_gemm_w: 128-token wave tiles (w = 12, kg = 1, bn = 128)
 };
 
 int env_int(const char * name, int dflt) {
@@ -1151,6 +1328,17 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
         c.bn = 64;
         c.rg = 1;
         c.split = 1;
+        // the wide form first (k_gemm_w): 384-row x 128-token tiles (at most an eighth of the
+        // token tiles padding) that fill the CUs; K a whole number of stages (its x tiles are
+        // loaded without a K tail)
+        static const int env_wide = env_int("SCRAPGPU_HIP_MM_WIDE", 1);
+        if (env_wide != 0 && free_choice && env_kg != 2 && env_kg != 3 && a.K % BK == 0 && a.N >= 128 &&
+            (a.N + 127) / 128 * 128 * 8 <= 9 * a.N && (a.M % 384 == 0 || a.M >= 8 * 384) && fill((a.M + 383) / 384 * ((a.N + 127) / 128) * slices)) {
+            c.kg = 1;
+            c.bn = 128;
+            c.wide = true;
+            return c;
+        }
         if (env_w == 12) { // forced: KG = 1, split from SCRAPGPU_HIP_MM_SPLIT
             c.kg = 1;
             if (env_split > 0) c.split = (int) std::max<int64_t>(1, std::min<int64_t>(std::min(env_split, 8), (stages + 3) / 4));
@@ -1183,6 +1371,7 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
 
 template <int DT>
 void * kernel_of(const MmConfig & c) {
+    if (c.wide) return (void *) k_gemm_w<DT>;
     if (c.w == 12) return c.kg == 3 ? (void *) k_matmul<DT, 64, 1, 12, 3> : c.kg == 2 ? (void *) k_matmul<DT, 64, 1, 12, 2> : (void *) k_matmul<DT, 64, 1, 12, 1>;
     if (c.rg == 1) return c.bn == 64 ? (void *) k_matmul<DT, 64, 1, 4, 1> : (void *) k_matmul<DT, 128, 1, 4, 1>;
     return c.bn == 64 ? (void *) k_matmul<DT, 64, 2, 4, 1> : (void *) k_matmul<DT, 128, 2, 4, 1>;
@@ -1232,9 +1421,19 @@ size_t matmul_scratch_bytes(const MatArgs & a, int cu_count) {
     return part_offset(a) + (split == 1 ? 0 : part_bytes(a, split));
 }
 
-bool matmul_same_x(const MatArgs & a, const MatArgs & b) {
+// the pre-pass writes Q4_K's single-fma form of x (high-nibble positions / 16, sub-block sums)
+// for the Q4_K kernels that use it, plain scaled x for every other kernel
+static bool q4k_x_form(const MatArgs & a, int cu_count) {
+    return a.dtype == Q4_K && !config_of(a, cu_count).wide;
+}
+
+bool matmul_reads_same_x(const MatArgs & a, const MatArgs & b) {
     return a.x == b.x && a.x_s1 == b.x_s1 && a.x_s2 == b.x_s2 && a.x_s3 == b.x_s3 && a.N == b.N && a.K == b.K && a.ne12 == b.ne12 &&
-           a.ne13 == b.ne13 && (a.dtype == Q4_K) == (b.dtype == Q4_K);
+           a.ne13 == b.ne13;
+}
+
+bool matmul_same_x(const MatArgs & a, const MatArgs & b, int cu_count) {
+    return matmul_reads_same_x(a, b) && q4k_x_form(a, cu_count) == q4k_x_form(b, cu_count);
 }
 
 hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name,
@@ -1244,7 +1443,7 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     // of all their rows for its shape choice and scratch
     MatArgs a = mats[0];
     for (int j = 1; j < nmat; ++j) {
-        if (mats[j].dtype != a.dtype || !matmul_same_x(mats[j], a) || mats[j].ne12 * mats[j].ne13 != 1 || a.ne12 * a.ne13 != 1) return hipErrorInvalidValue;
+        if (mats[j].dtype != a.dtype || !matmul_reads_same_x(mats[j], a) || mats[j].ne12 * mats[j].ne13 != 1 || a.ne12 * a.ne13 != 1) return hipErrorInvalidValue;
         a.M += mats[j].M;
     }
     uint16_t * xb = reinterpret_cast<uint16_t *>(scratch);
@@ -1255,9 +1454,10 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     const int64_t xsum_row = xsum_row_of(a);
     if (rows > 0x7fffffff) return hipErrorInvalidValue;
     const dim3 xg((unsigned) rows);
+    const MmConfig cfg = config_of(a, cu_count);
     if (x_ready) {
         // x converted by the previous product's pre-pass (matmul_same_x)
-    } else if (a.dtype == Q4_K) {
+    } else if (a.dtype == Q4_K && !cfg.wide) {
         if (vec)
             hipLaunchKernelGGL((k_x_to_f16<true, true>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
         else
@@ -1278,7 +1478,6 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     L.part = reinterpret_cast<float *>(scratch + part_offset(a));
     L.xsum = xsum;
     L.xsum_row = xsum_row;
-    const MmConfig cfg = config_of(a, cu_count);
     const int BN = cfg.bn;
     const int bmt = 32 * cfg.rg * (cfg.w / cfg.kg);
     // each matrix's rows tiled on their own
@@ -1303,7 +1502,7 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     L.tiles_n = (a.N + BN - 1) / BN;
     L.stages = (a.K + BK - 1) / BK;
     L.split = cfg.split;
-    const size_t lds = (size_t) cfg.kg * 2 * BN * BK * sizeof(uint16_t);
+    const size_t lds = (size_t) cfg.kg * 2 * BN * (cfg.wide ? XR : BK) * sizeof(uint16_t);
     const int64_t slices = a.ne12 * a.ne13;
     const dim3 grid((unsigned) (L.tiles_m * L.tiles_n * L.split), (unsigned) slices);
     void * args[] = {&L};
@@ -1316,7 +1515,8 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
         default: return hipErrorInvalidValue;
     }
     if ((e = allow_lds(fn, lds)) != hipSuccess) return e;
-    std::snprintf(last_form().form, sizeof(last_form().form), "gemm w=%d kg=%d bn=%d rg=%d split=%d", cfg.w, cfg.kg, BN, cfg.rg, L.split);
+    std::snprintf(last_form().form, sizeof(last_form().form), "gemm%s w=%d kg=%d bn=%d rg=%d split=%d", cfg.wide ? " wide" : "", cfg.w, cfg.kg, BN,
+                  cfg.rg, L.split);
     last_form().grid = (uint64_t) grid.x * grid.y;
     e = hipLaunchKernel(fn, grid, dim3((unsigned) (64 * cfg.w)), args, lds, stream);
     if (e != hipSuccess || L.split == 1) return e;

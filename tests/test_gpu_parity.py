@@ -310,6 +310,95 @@ def test_prefill_workgroup_per_cu_slices_broadcast_strides(hip, M, K):
         b.free()
 
 
+def wide_tokens(dev, row_tiles, pad=0):
+    """Tokens at which `row_tiles` 384-row x 128-token tiles fill the device's CUs in one round
+    (less `pad`: a part-empty last token tile)."""
+    cus = dev.info().compute_units
+    assert (cus * 128) % row_tiles == 0, cus
+    return cus * 128 // row_tiles - pad
+
+
+@pytest.mark.parametrize("dtype,M,pad", [(sg.Q4_0, 3072, 0), (sg.Q8_0, 3072, 40), (sg.Q4_K, 3072, 0), (sg.Q6_K, 3072, 0),
+                                         (sg.Q4_K, 6000, 40)],
+                         ids=["q4_0", "q8_0_token_tail", "q4_k", "q6_k", "q4_k_row_tail"])
+def test_prefill_wide_tiles(hip, dtype, M, pad):
+    """The wide GEMM (384-row x 128-token tiles, one per CU, x tiles loaded straight into LDS,
+    exact Q4_K dequantization): every dtype; a part-empty last token tile (tokens past N read the
+    last token, outputs dropped); M = 6000 ends in a partial row tile. The launch form is pinned."""
+    dev, st = hip
+    K = 512
+    N = wide_tokens(dev, (M + 383) // 384, pad)
+    q, _ = quantized(dtype, K, M, 900 + M)
+    x = O.normal(N * K, 901).reshape(N, K)
+    wb, wt = upload_weights(dev, st, dtype, q, K, M)
+    xb, yb = dev.alloc(x.nbytes), dev.alloc(4 * M * N)
+    xt, yt = sg.tdesc(sg.F32, (K, N), xb), sg.tdesc(sg.F32, (M, N), yb)
+    st.upload(xt, x)
+    op, keep = sg.mul_mat_op(wt, xt, yt)
+    st.execute(op)
+    st.sync()
+    form, grid = sg.last_launch()
+    assert form.startswith("gemm wide"), form
+    assert grid == (M + 383) // 384 * ((N + 127) // 128), (form, grid)
+    y = st.download(yt).reshape(N, M)
+    ref = O.mul_mat(dtype, q, K, M, x, threads=8)
+    e = nmse(y, ref)
+    assert e <= 5e-5, f"NMSE {e:.3e}"
+    for b in (wb, xb, yb):
+        b.free()
+
+
+def test_prefill_wide_q4k_large_scales(hip):
+    """The wide GEMM's exact Q4_K form on rows with scales (weights in the hundreds) and offsets
+    (means near -3000) far beyond the ordinary ones, mixed with ordinary rows."""
+    dev, st = hip
+    K, M = 512, 3072
+    N = wide_tokens(dev, 8)
+    w = O.normal(K * M, 79, 0.0, 0.02).reshape(M, K)
+    w[0:10] *= 1e4
+    w[20:30] += -3000.0
+    w[40:45, :256] *= 1e4
+    q = O.quantize(sg.Q4_K, w.reshape(-1))
+    x = O.normal(N * K, 80).reshape(N, K)
+    y = run_mul_mat(dev, st, sg.Q4_K, q, K, M, x)
+    assert sg.last_launch()[0].startswith("gemm wide")
+    ref = O.mul_mat(sg.Q4_K, q, K, M, x, threads=8)
+    assert np.all(np.isfinite(y))
+    for rows in (slice(0, 10), slice(20, 30), slice(40, 45), slice(50, M)):
+        e = nmse(y[:, rows], ref[:, rows])
+        assert e <= 5e-5, f"rows {rows}: NMSE {e:.3e}"
+
+
+def test_prefill_wide_multi_tiles_across_weights(hip):
+    """A prefill MUL_MAT_MULTI on the wide GEMM: 3 weights of 1024 rows (32-row multiples), the
+    384-row tiles running across their boundaries, each wave taking the weight its rows are in."""
+    dev, st = hip
+    dtype, K, Ms = sg.Q6_K, 512, (1024, 1024, 1024)
+    N = wide_tokens(dev, 8)
+    x = O.normal(N * K, 910).reshape(N, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    st.upload(xt, x)
+    bufs, wts, yts, refs = [], [], [], []
+    for i, M in enumerate(Ms):
+        q, _ = quantized(dtype, K, M, 920 + i)
+        b, t = upload_weights(dev, st, dtype, q, K, M)
+        yb = dev.alloc(4 * M * N)
+        bufs += [b, yb]
+        wts.append(t)
+        yts.append(sg.tdesc(sg.F32, (M, N), yb))
+        refs.append(O.mul_mat(dtype, q, K, M, x, threads=8))
+    op, keep = sg.multi_op(wts, xt, yts)
+    st.execute(op)
+    st.sync()
+    assert sg.last_launch()[0].startswith("gemm wide"), sg.last_launch()
+    for M, yt, ref in zip(Ms, yts, refs):
+        e = nmse(st.download(yt).reshape(N, M), ref)
+        assert e <= 5e-5, f"{M} rows: NMSE {e:.3e}"
+    for b in bufs + [xb]:
+        b.free()
+
+
 @pytest.mark.parametrize("dtype", [sg.Q4_0, sg.Q4_K], ids=lambda d: sg.NAMES[d])
 @pytest.mark.parametrize("N", [1, 4, 33])
 def test_slices_broadcast_and_strides(hip, dtype, N):
