@@ -952,20 +952,22 @@ struct XDma {
 // registers for the extra accumulators come from the exact Q4_K form (s (c + bias) + o per pair,
 // from plain x: no offset MFMA, no sub-block sums, no rare-scale branch), one set of A fragments
 // (each read again right after the MFMA that consumed it), x tiles loaded straight into LDS and
-// padded x rows (immediate LDS offsets). Measured on 12288 x 4096: 273 against 295 us at 2048
-// tokens, and gate+up (24576 rows) at 512 tokens 132 against 141 us. Splitting K over 2 groups of
-// 6 waves in the work-group (192-row tiles, for shapes these tiles do not fill) measured slower
-// than the 64-token form (70 against 65 us at 12288 x 4096 x 512), as did wave tiles of 64 rows x
-// 64 tokens (half the LDS reads per MFMA, twice the dequantization: 96 us). Split-K over
-// work-groups (partials + k_split_reduce) as in k_matmul.
-template <int DT>
+// padded x rows (immediate LDS offsets). KG = 1: 12 row waves, 384-row tiles; KG = 2: 6 row
+// waves x 2 groups that take half of K each (192-row tiles, for shapes the 384-row ones do not
+// fill), each group finishing half of the token fragments. Measured (quantized N(0, 0.02)
+// weights): 12288 x 4096 at 2048 tokens 219 against 272 us, gate+up (24576 rows) at 512 tokens
+// 118 against 145 us, 12288 x 4096 at 512 tokens (KG = 2) 70-76 against 79-82 us. Wave tiles of 64
+// rows x 64 tokens (half the LDS reads per MFMA, twice the dequantization) measured slower than
+// the 64-token form. Split-K over work-groups (partials + k_split_reduce) as in k_matmul.
+template <int DT, int KG>
 __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
-    constexpr int W = 12, NF = 4, BN = 32 * NF, BMT = 32 * W;
+    constexpr int W = 12, NF = 4, BN = 32 * NF, RW = W / KG, BMT = 32 * RW;
     using F = PFmt<DT>;
     using Raw = typename F::Raw;
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_mm[];
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // wave-uniform: scalar addressing
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // wave-uniform: scalar addressing
+    const int wave = wid % RW, kg = wid / RW;                         // row wave, K group
     const int j = lane & 31, h = lane >> 5;
     const int64_t tile = blockIdx.x / L.split;
     const int split = (int) (blockIdx.x % L.split);
@@ -981,17 +983,22 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
     const int64_t M = L.nmat > 1 ? L.Mm[mj] : L.a.M;
     const int64_t n0 = tn * BN;
     const int64_t m0 = L.packed ? grow - L.mo[mj] : (tm - L.mt[mj]) * BMT + 32 * wave;
-    // the split's stages (whole groups of 4, as in k_matmul)
+    // the stages of the split (whole groups of 4) or of the K group (KG = 2: every group walks
+    // 4 ceil(groups / 2) stages so that all waves meet the same barriers; a group's stages past K
+    // are inactive: their loads repeat a valid stage, their k-steps are skipped), as in k_matmul
     const int64_t groups = (L.stages + 3) / 4;
-    const int s0 = (int) (4 * (groups * split / L.split));
-    const int s1 = (int) min(4 * (groups * (split + 1) / L.split), L.stages);
+    const int gsz = (int) (4 * ((groups + KG - 1) / KG));
+    const int s0 = (int) (KG > 1 ? kg * gsz : 4 * (groups * split / L.split));
+    const int s1 = (int) (KG > 1 ? min<int64_t>(s0 + gsz, L.stages) : min(4 * (groups * (split + 1) / L.split), L.stages));
+    const int send = KG > 1 ? s0 + gsz : s1;
     const int lim = s1 - 1;
 
     F f;
     f.init(M, nb, RowAddr(M, m0 + j), h);
     const uint16_t * xb = L.xb + (uint64_t) sl * N * K;
-    XDma<W, BN> xt;
+    XDma<RW, BN> xt;
     xt.init(N, K, n0, wave, lane);
+    uint16_t * const lds_x = lds_mm + kg * (2 * BN * XR); // the K group's two x buffers
     const int abase = j * XR; // + 32 q XR + 8 chunk(h, t): immediate offsets
 
     f32x16 acc[NF];
@@ -1007,8 +1014,12 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
         const int sn = min(s + 1, lim);
         if constexpr ((DT == Q4_K || DT == Q6_K) && (D & 1) == 0) nw = f.load_half2(w, sn, cw);
         else nw = f.load(w, sn);
-        if (s + 1 < s1) xt.load(xb, (s + 1) * BK, lds_mm + ((D + 1) & 1) * (BN * XR));
-        const uint16_t * X = lds_mm + (D & 1) * (BN * XR) + abase;
+        if (s + 1 < s1) xt.load(xb, (s + 1) * BK, lds_x + ((D + 1) & 1) * (BN * XR));
+        const uint16_t * X = lds_x + (D & 1) * (BN * XR) + abase;
+        if (KG > 1 && s >= s1) { // an inactive stage (wave-uniform): only the barrier
+            __syncthreads();
+            return;
+        }
         const typename F::Sc sc = f.prep(cw, (s & ~3) | D);
         f16x8 a[NF];
 #pragma unroll
@@ -1034,21 +1045,21 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
         __syncthreads(); // (waits for this wave's loads: the next x tile is in LDS)
     };
     Raw ra{}, rb{};
-    ra = f.load(w, s0);
-    xt.load(xb, s0 * BK, lds_mm);
+    ra = f.load(w, min(s0, lim));
+    xt.load(xb, min(s0, lim) * BK, lds_x);
     __syncthreads();
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
     int s = s0;
-    for (; s + 3 < s1; s += 4) {
+    for (; s + 3 < send; s += 4) {
         stage(I0{}, s, ra, rb);
         stage(I1{}, s + 1, rb, ra);
         stage(I2{}, s + 2, ra, rb);
         stage(I3{}, s + 3, rb, ra);
     }
-    if (s < s1) {
+    if (s < send) { // (KG = 2: send - s0 is a multiple of 4, no tail)
         stage(I0{}, s, ra, rb);
         if (s + 1 < s1) {
             stage(I1{}, s + 1, rb, ra);
@@ -1056,31 +1067,61 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
         }
     }
     // acc[q][v], lane (j, h): token n0 + 32q + 8 (v / 4) + 4h + v % 4, weight row m0 + j
-    const int64_t slices = L.a.ne12 * L.a.ne13;
-    float * y;
-    int64_t ys1;
-    if (L.split == 1) {
-        y = L.nmat > 1 ? L.ym[mj] : L.a.y + i2 * L.a.y_s2 + i3 * L.a.y_s3;
-        ys1 = L.nmat > 1 ? L.ys1m[mj] : L.a.y_s1;
-    } else {
-        const int64_t mt_all = L.mo[L.nmat];
-        y = L.part + ((uint64_t) split * slices + (uint64_t) sl) * N * mt_all + L.mo[mj];
-        ys1 = mt_all;
-    }
-    const float * xs = L.xs + (uint64_t) sl * N;
-    const int64_t m = m0 + j;
-#pragma unroll
-    for (int q = 0; q < NF; ++q) {
-        float u[16];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) u[v] = xs[min<int64_t>(n0 + 32 * q + 8 * (v >> 2) + 4 * h + (v & 3), N - 1)];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int64_t n = n0 + 32 * q + 8 * (v >> 2) + 4 * h + (v & 3);
-            // (outputs are not read again by this kernel: stores that bypass the caches)
-            if (n < N && m < M) __builtin_nontemporal_store(acc[q][v] * u[v], y + n * ys1 + m);
+    auto store_out = [&](auto qb, auto qc) __attribute__((always_inline)) {
+        constexpr int QB = decltype(qb)::value, QC = decltype(qc)::value;
+        const int64_t slices = L.a.ne12 * L.a.ne13;
+        float * y;
+        int64_t ys1;
+        if (L.split == 1) {
+            y = L.nmat > 1 ? L.ym[mj] : L.a.y + i2 * L.a.y_s2 + i3 * L.a.y_s3;
+            ys1 = L.nmat > 1 ? L.ys1m[mj] : L.a.y_s1;
+        } else {
+            const int64_t mt_all = L.mo[L.nmat];
+            y = L.part + ((uint64_t) split * slices + (uint64_t) sl) * N * mt_all + L.mo[mj];
+            ys1 = mt_all;
         }
-    }
+        const float * xs = L.xs + (uint64_t) sl * N;
+        const int64_t m = m0 + j;
+#pragma unroll
+        for (int q = QB; q < QB + QC; ++q) {
+            float u[16];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) u[v] = xs[min<int64_t>(n0 + 32 * q + 8 * (v >> 2) + 4 * h + (v & 3), N - 1)];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t n = n0 + 32 * q + 8 * (v >> 2) + 4 * h + (v & 3);
+                // (outputs are not read again by this kernel: stores that bypass the caches)
+                if (n < N && m < M) __builtin_nontemporal_store(acc[q][v] * u[v], y + n * ys1 + m);
+            }
+        }
+    };
+    // KG = 2: each group finishes half of the token fragments, QB .. QB + QN: it hands the other
+    // half of its sums to the other group through LDS (the x buffers are free now) and adds the
+    // other group's half of its own (a + b = b + a exactly: no order to keep), so both groups store
+    constexpr int QN = NF / KG;
+    auto finish = [&](auto gtag) __attribute__((always_inline)) {
+        // (the group's fragments as a compile-time range: registers cannot be indexed at run time)
+        constexpr int G = decltype(gtag)::value, QB = G * QN;
+        if constexpr (KG > 1) {
+            constexpr int PER = QN * 16, QO = (1 - G) * QN; // QO: the other group's fragments
+            float * red = reinterpret_cast<float *>(lds_mm);
+            __syncthreads();
+            float * r = red + ((size_t) (G * RW + wave) * PER) * 64 + lane;
+#pragma unroll
+            for (int q = 0; q < QN; ++q)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) r[(q * 16 + v) * 64] = acc[QO + q][v];
+            __syncthreads();
+            const float * o = red + ((size_t) ((1 - G) * RW + wave) * PER) * 64 + lane;
+#pragma unroll
+            for (int q = 0; q < QN; ++q)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[QB + q][v] += o[(q * 16 + v) * 64];
+        }
+        store_out(std::integral_constant<int, QB>{}, std::integral_constant<int, QN>{});
+    };
+    if (KG == 1 || kg == 0) finish(std::integral_constant<int, 0>{});
+    else finish(std::integral_constant<int, 1>{});
 }
 
 // y = sum of the split-K partials, in split order. blockIdx.x is the row (token n of slice sl),
@@ -1287,7 +1328,7 @@ struct MmConfig {
     int split;
     int w;  // waves per work-group: 4, or 12 (one work-group per CU, see k_matmul)
     int kg; // K groups of a 12-wave work-group: 1 or 3
-    bool wide = false; // k_gemm_w: 128-token wave tiles (w = 12, kg = 1, bn = 128)
+    bool wide = false; // k_gemm_w: 128-token wave tiles (w = 12, kg 1 or 2, bn = 128)
 };
 
 int env_int(const char * name, int dflt) {
@@ -1328,16 +1369,24 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
         c.bn = 64;
         c.rg = 1;
         c.split = 1;
-        // the wide form first (k_gemm_w): 384-row x 128-token tiles (at most an eighth of the
-        // token tiles padding) that fill the CUs; K a whole number of stages (its x tiles are
-        // loaded without a K tail)
+        // the wide form first (k_gemm_w): 128-token tiles (at most an eighth of the token tiles
+        // padding) of 384 rows that fill the CUs, or of 192 rows with K in two equal runs of whole
+        // groups of 4 stages; K a whole number of stages (its x tiles are loaded without a K tail)
         static const int env_wide = env_int("SCRAPGPU_HIP_MM_WIDE", 1);
-        if (env_wide != 0 && free_choice && env_kg != 2 && env_kg != 3 && a.K % BK == 0 && a.N >= 128 &&
-            (a.N + 127) / 128 * 128 * 8 <= 9 * a.N && (a.M % 384 == 0 || a.M >= 8 * 384) && fill((a.M + 383) / 384 * ((a.N + 127) / 128) * slices)) {
-            c.kg = 1;
+        if (env_wide != 0 && free_choice && env_kg != 3 && a.K % BK == 0 && a.N >= 128 && (a.N + 127) / 128 * 128 * 8 <= 9 * a.N) {
+            const int64_t ntw = (a.N + 127) / 128 * slices;
             c.bn = 128;
             c.wide = true;
-            return c;
+            if (env_kg != 2 && (a.M % 384 == 0 || a.M >= 8 * 384) && fill((a.M + 383) / 384 * ntw)) {
+                c.kg = 1;
+                return c;
+            }
+            if (env_kg != 1 && (a.M % 192 == 0 || a.M >= 8 * 192) && fill((a.M + 191) / 192 * ntw) && stages >= 16 && (2 * gsz2 - stages) * 8 <= stages) {
+                c.kg = 2;
+                return c;
+            }
+            c.bn = 64;
+            c.wide = false;
         }
         if (env_w == 12) { // forced: KG = 1, split from SCRAPGPU_HIP_MM_SPLIT
             c.kg = 1;
@@ -1371,7 +1420,7 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
 
 template <int DT>
 void * kernel_of(const MmConfig & c) {
-    if (c.wide) return (void *) k_gemm_w<DT>;
+    if (c.wide) return c.kg == 2 ? (void *) k_gemm_w<DT, 2> : (void *) k_gemm_w<DT, 1>;
     if (c.w == 12) return c.kg == 3 ? (void *) k_matmul<DT, 64, 1, 12, 3> : c.kg == 2 ? (void *) k_matmul<DT, 64, 1, 12, 2> : (void *) k_matmul<DT, 64, 1, 12, 1>;
     if (c.rg == 1) return c.bn == 64 ? (void *) k_matmul<DT, 64, 1, 4, 1> : (void *) k_matmul<DT, 128, 1, 4, 1>;
     return c.bn == 64 ? (void *) k_matmul<DT, 64, 2, 4, 1> : (void *) k_matmul<DT, 128, 2, 4, 1>;
@@ -1502,7 +1551,9 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     L.tiles_n = (a.N + BN - 1) / BN;
     L.stages = (a.K + BK - 1) / BK;
     L.split = cfg.split;
-    const size_t lds = (size_t) cfg.kg * 2 * BN * (cfg.wide ? XR : BK) * sizeof(uint16_t);
+    // (the wide GEMM with 2 K groups hands half of its sums over through the x buffers at the end)
+    const size_t lds = cfg.wide ? std::max((size_t) cfg.kg * 2 * BN * XR * sizeof(uint16_t), (size_t) (cfg.kg > 1 ? 12 * 2 * 16 * 64 : 0) * sizeof(float))
+                                : (size_t) cfg.kg * 2 * BN * BK * sizeof(uint16_t);
     const int64_t slices = a.ne12 * a.ne13;
     const dim3 grid((unsigned) (L.tiles_m * L.tiles_n * L.split), (unsigned) slices);
     void * args[] = {&L};

@@ -338,8 +338,38 @@ def test_prefill_wide_tiles(hip, dtype, M, pad):
     st.execute(op)
     st.sync()
     form, grid = sg.last_launch()
-    assert form.startswith("gemm wide"), form
+    assert form.startswith("gemm wide w=12 kg=1"), form
     assert grid == (M + 383) // 384 * ((N + 127) // 128), (form, grid)
+    y = st.download(yt).reshape(N, M)
+    ref = O.mul_mat(dtype, q, K, M, x, threads=8)
+    e = nmse(y, ref)
+    assert e <= 5e-5, f"NMSE {e:.3e}"
+    for b in (wb, xb, yb):
+        b.free()
+
+
+@pytest.mark.parametrize("dtype,K,pad", [(sg.Q4_K, 2048, 0), (sg.Q8_0, 2048, 0), (sg.Q4_0, 2048, 40), (sg.Q6_K, 4608, 0)],
+                         ids=["q4_k", "q8_0", "q4_0_token_tail", "q6_k_uneven"])
+def test_prefill_wide_k_groups(hip, dtype, K, pad):
+    """The wide GEMM with 2 K groups of 6 row waves (192-row x 128-token tiles that fill the CUs
+    where the 384-row ones do not): each group sums half of K, hands half of its token fragments'
+    sums to the other group through LDS and stores the other half. K = 4608 (36 stages): groups
+    of 20 stages, the second one's last 4 inactive."""
+    dev, st = hip
+    M = 3072
+    N = wide_tokens(dev, M // 192, pad)
+    q, _ = quantized(dtype, K, M, 930 + K)
+    x = O.normal(N * K, 931).reshape(N, K)
+    wb, wt = upload_weights(dev, st, dtype, q, K, M)
+    xb, yb = dev.alloc(x.nbytes), dev.alloc(4 * M * N)
+    xt, yt = sg.tdesc(sg.F32, (K, N), xb), sg.tdesc(sg.F32, (M, N), yb)
+    st.upload(xt, x)
+    op, keep = sg.mul_mat_op(wt, xt, yt)
+    st.execute(op)
+    st.sync()
+    form, grid = sg.last_launch()
+    assert form.startswith("gemm wide w=12 kg=2"), form
+    assert grid == M // 192 * ((N + 127) // 128), (form, grid)
     y = st.download(yt).reshape(N, M)
     ref = O.mul_mat(dtype, q, K, M, x, threads=8)
     e = nmse(y, ref)
