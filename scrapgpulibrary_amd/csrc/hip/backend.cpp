@@ -77,6 +77,7 @@ struct Stream {
     uint8_t * scratch = nullptr; // prefill matmul: f16 activations, row factors and split-K partials (grown on demand)
     size_t scratch_size = 0;
     uint64_t scratch_gen = 0;    // process-unique; renewed on every re-allocation (keys recorded graphs)
+    uint32_t * arrive = nullptr; // the chunked decode matvec's arrival counts (sgk::kArriveMax, zero between launches)
 };
 
 std::atomic<uint64_t> g_scratch_gen{1};
@@ -92,6 +93,7 @@ struct Device {
     uint8_t * staging = nullptr;
     size_t staging_size = 0;
     uint8_t * static_scratch = nullptr; // this device's copy of `scratch` (below), or null
+    uint32_t * static_arrive = nullptr; // this device's copy of `arrive_counts` (below), or null
 };
 
 struct PlanNode {
@@ -162,6 +164,7 @@ std::atomic<bool> g_prof{false};
 // while a scrapgpu_hip_op_execute_static call runs on this thread: its device's static scratch
 // (the profiler stays off then: its events are allocations)
 thread_local uint8_t * t_static_scratch = nullptr;
+thread_local uint32_t * t_static_arrive = nullptr;
 std::mutex g_prof_mu;
 std::vector<ProfRecord> g_prof_pending;
 std::vector<ProfEntry> g_prof_table;
@@ -376,10 +379,20 @@ scrapgpu_status api_stream_create(scrapgpu_device_t * device, scrapgpu_stream_t 
     SG_HIP(use(d), "hipSetDevice");
     hipStream_t hs;
     SG_HIP(hipStreamCreateWithFlags(&hs, hipStreamNonBlocking), "hipStreamCreate");
+    // the chunked matvec's arrival counts: zeroed here, once (every launch leaves them at zero)
+    uint32_t * arrive = nullptr;
+    hipError_t e = hipMalloc(reinterpret_cast<void **>(&arrive), (size_t) sgk::kArriveMax * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(arrive, 0, (size_t) sgk::kArriveMax * sizeof(uint32_t));
+    if (e != hipSuccess) {
+        if (arrive) hipFree(arrive);
+        hipStreamDestroy(hs);
+        return hip_fail(e, "hipMalloc / hipMemset (stream arrival counts)");
+    }
     Stream * s = new Stream;
     s->hdr.backend = &kVtable;
     s->dev = d;
     s->s = hs;
+    s->arrive = arrive;
     s->scratch_gen = g_scratch_gen.fetch_add(1);
     *out = reinterpret_cast<scrapgpu_stream_t *>(s);
     return SCRAPGPU_STATUS_OK;
@@ -391,6 +404,7 @@ scrapgpu_status api_stream_free(scrapgpu_stream_t * stream) {
     use(s->dev);
     hipStreamSynchronize(s->s);
     if (s->scratch) hipFree(s->scratch);
+    if (s->arrive) hipFree(s->arrive);
     hipStreamDestroy(s->s);
     delete s;
     return SCRAPGPU_STATUS_OK;
@@ -412,6 +426,9 @@ scrapgpu_status api_stream_sync(scrapgpu_stream_t * stream) {
 // kernel). Every static call on one GPU shares it.
 constexpr size_t kStaticScratchBytes = (size_t) 32 << 20;
 static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+// ... and its arrival counts of the chunked decode matvec: zero at load, left at zero by every
+// launch (the stream's own counts play this part in scrapgpu_op_execute)
+static __device__ __align__(256) uint32_t arrive_counts[sgk::kArriveMax];
 
 namespace {
 
@@ -832,7 +849,8 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
             ProfScope prof(s->s);
             const char * name = nullptr;
             uint64_t grid = 0;
-            SG_HIP(sgk::launch_matvec(m, cnt, cus, s->s, &name, &grid, nullptr, scr), "matvec launch");
+            uint32_t * arrive = t_static_scratch != nullptr ? t_static_arrive : s->arrive;
+            SG_HIP(sgk::launch_matvec(m, cnt, cus, s->s, &name, &grid, nullptr, scr, arrive), "matvec launch");
             prof.done(name, bytes, flops);
         } else {
             uint8_t * scr = nullptr;
@@ -1391,6 +1409,8 @@ scrapgpu_status scrapgpu_hip_register(void) {
         // where the lookup failed)
         void * sp = nullptr;
         if (hipSetDevice(i) == hipSuccess && hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)) == hipSuccess) d->static_scratch = static_cast<uint8_t *>(sp);
+        void * ap = nullptr;
+        if (d->static_scratch != nullptr && hipGetSymbolAddress(&ap, HIP_SYMBOL(arrive_counts)) == hipSuccess) d->static_arrive = static_cast<uint32_t *>(ap);
         r.devices.push_back(std::move(d));
     }
     if (had_cur) hipSetDevice(cur); // (the static scratch lookups made each device current in turn)
@@ -1482,12 +1502,14 @@ scrapgpu_status scrapgpu_hip_op_execute_static(scrapgpu_stream_t * stream, const
     Stream * s = stream_of(stream);
     if (s == nullptr) return invalid("not a hip stream");
     if (desc == nullptr) return invalid("op desc is null");
-    if (s->dev->static_scratch == nullptr) {
+    if (s->dev->static_scratch == nullptr || s->dev->static_arrive == nullptr) {
         return set_err(SCRAPGPU_STATUS_BACKEND_ERROR, "the static scratch of this device could not be located (hipGetSymbolAddress failed at registration)");
     }
     t_static_scratch = s->dev->static_scratch;
+    t_static_arrive = s->dev->static_arrive;
     const scrapgpu_status st = exec_desc(s, desc);
     t_static_scratch = nullptr;
+    t_static_arrive = nullptr;
     return st;
 }
 

@@ -60,12 +60,18 @@ struct IdArgs {
 // mats[j].w / M / y / y_s1 per matrix, everything else from mats[0]). With `id` (N = 1): the
 // MUL_MAT_ID pairs above instead of the slices; nmat > 1 expert tensors then share the ids, x, the
 // expert stride w_s2 and the output strides y_s1 / y_s2.
-// Scratch the launch needs (0 for one column): for 2..8 columns of one slice, x converted once to
-// its int8 planes, and the partial sums of K chunks when K > 4096. launch_matvec takes that much
-// device memory as `scratch` (null: the form that needs none).
+// Scratch the launch needs: for 2..8 columns of one slice, x converted once to its int8 planes,
+// and the partial sums of K chunks when K > 4096. launch_matvec takes that much device memory as
+// `scratch` (null: the form that needs none).
+// One column with a long K (17..64 steps of 256) on one slice: K in chunks of 16 steps over
+// separate work-groups, whose partial sums take matvec_scratch_bytes of `scratch` and meet through
+// `arrive`: kArriveMax counters that must be zero before the first launch that uses them and are
+// left at zero by every launch (the last chunk of a row tile resets its count); launches that
+// share them must not overlap. Without scratch or counters the one-work-group-per-tile form runs.
+constexpr int64_t kArriveMax = 65536;
 size_t matvec_scratch_bytes(const MatArgs * mats, int nmat, const IdArgs * id = nullptr);
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
-                         uint64_t * grid_size, const IdArgs * id = nullptr, uint8_t * scratch = nullptr);
+                         uint64_t * grid_size, const IdArgs * id = nullptr, uint8_t * scratch = nullptr, uint32_t * arrive = nullptr);
 
 // prefill: f16 MFMA with fp32 accumulate, weights dequantized in registers (any N >= 1).
 // `scratch` (matmul_scratch_bytes(a, cu_count) bytes of device memory, owned by the stream)

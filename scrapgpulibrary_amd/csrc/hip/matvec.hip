@@ -89,7 +89,15 @@ struct MvArgs {
     const int32_t * ids;
     int64_t ids_s0, ids_s1, n_used, n_exp;
     int x_shared;
+    // chunked burst (k_mvb with CHUNK): blockIdx.y is the K chunk (kChunkSteps steps each); part:
+    // [chunk][tile * 16 + row] partial sums; arrive: chunks done per row tile, zero between
+    // launches (the last chunk of a tile resets its count)
+    int64_t nck;
+    float * part;
+    uint32_t * arrive;
 };
+
+constexpr int kChunkSteps = 16; // steps of K per work-group of the chunked burst (8 waves x 2)
 
 __device__ __forceinline__ float half_bits(uint32_t h) {
     return __half2float(__ushort_as_half((unsigned short) (h & 0xFFFFu)));
@@ -599,15 +607,23 @@ __device__ __forceinline__ void reduce_store(const MvArgs & A, const Where & wh,
 
 // Burst form (one column, <= SPW steps per wave, one tile of 16 * RG rows per work-group): the wave
 // first loads its x range, then issues every weight load, and only then converts x.
-template <int DT, int RG, int W, int SPW>
+// CHUNK (one slice, 16-row tiles, W x SPW = kChunkSteps): work-group (tile, c) takes chunk c of K,
+// so that a long K runs on several small work-groups instead of one large one per tile. The
+// chunks' partial sums meet as in k_mvc: agent-scope stores, an arrival count per tile, and the
+// last chunk to arrive adds them in chunk order and resets the count.
+template <int DT, int RG, int W, int SPW, bool CHUNK = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2 && RG == 1 ? 6 : SPW <= 2 && RG == 2 ? 5 : 4, 8))) void k_mvb(MvArgs A) {
+    static_assert(!CHUNK || (RG == 1 && W * SPW == kChunkSteps), "chunks of kChunkSteps on 16-row tiles");
     using F = Fmt<DT>;
     using Raw = typename F::Raw;
     extern __shared__ uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const Where wh = where_of(A);
+    const Where wh = CHUNK ? Where{0, 0, A.x} : where_of(A);
 
-    const int64_t s0 = A.nst * wave / W, s1 = A.nst * (wave + 1) / W;
+    // the work-group's steps: all of K, or chunk blockIdx.y (CHUNK)
+    const int64_t cb = CHUNK ? (int64_t) blockIdx.y * kChunkSteps : 0;
+    const int64_t cn = CHUNK ? min<int64_t>(kChunkSteps, A.nst - cb) : A.nst;
+    const int64_t s0 = cb + cn * wave / W, s1 = cb + cn * (wave + 1) / W;
     const int ns = (int) (s1 - s0);
 
     // x: lane l holds elements 8 (l % 4) .. +8 of segment l / 4 + 16 p of the wave's range (pass p)
@@ -662,7 +678,41 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2
     for (int s = 0; s < SPW; ++s) {
         if (s < ns) step_mfma<DT, RG, 1>(f, buf[s], al, s * kSegs, xw, acc);
     }
-    reduce_store<RG, 1, W>(A, wh, row, acc, red, tid);
+    if constexpr (!CHUNK) {
+        reduce_store<RG, 1, W>(A, wh, row, acc, red, tid);
+    } else {
+        // the waves' sums of the chunk (as reduce_store), then the chunks' through memory
+        const int r = lane & 15;
+        float v = acc[0][0];
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        if (lane < 16) red[wave * 16 + r] = v;
+        __syncthreads();
+        const int64_t tile = blockIdx.x;
+        if (tid < 16) {
+            float t = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < W; ++w2) t += red[w2 * 16 + tid];
+            // visible to every XCD before the tile's count moves (agent-scope stores write
+            // through the L2; then this wave waits for them)
+            __hip_atomic_store(A.part + (int64_t) blockIdx.y * A.tiles * 16 + tile * 16 + tid, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
+        }
+        uint32_t & last = *reinterpret_cast<uint32_t *>(zpad + 16);
+        if (tid == 0) last = __hip_atomic_fetch_add(A.arrive + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t) A.nck - 1;
+        __syncthreads();
+        // the last chunk of the tile to arrive adds all of them in chunk order (agent-scope loads:
+        // the other chunks' sums may come from other XCDs) and leaves the count at zero for the
+        // next launch
+        if (last && tid < 16) {
+            const int64_t m = row.m0 + tid;
+            float t = 0.0f;
+            for (int64_t c = 0; c < A.nck; ++c)
+                t += __hip_atomic_load(A.part + c * A.tiles * 16 + tile * 16 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (m < row.M) A.y[row.j][m] = t;
+            if (tid == 0) __hip_atomic_store(A.arrive + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
 // Streaming form: one work-group walks tiles blockIdx.x, blockIdx.x + gridDim.x, ... (16 rows
@@ -1445,7 +1495,32 @@ static bool mc_form(const MatArgs * mats, int nmat, const IdArgs * id) {
     return on && id == nullptr && mats[0].N >= 2 && mats[0].N <= 8 && mats[0].ne12 * mats[0].ne13 == 1;
 }
 
+// the chunked burst applies (one column, one slice, not MUL_MAT_ID, K of 17..64 steps, at most
+// kArriveMax 16-row tiles); it also needs x 16-byte aligned, checked at launch
+static bool chunk_form(const MatArgs * mats, int nmat, const IdArgs * id) {
+    static const bool on = [] {
+        const char * v = std::getenv("SCRAPGPU_HIP_MV_CHUNK");
+        return v == nullptr || v[0] != '0';
+    }();
+    if (!on || id != nullptr || mats[0].N != 1) return false;
+    const int64_t nst = (mats[0].K + kStep - 1) / kStep;
+    int64_t tiles = 0;
+    for (int j = 0; j < nmat; ++j) {
+        if (mats[j].ne12 * mats[j].ne13 != 1) return false;
+        tiles += (mats[j].M + 15) / 16;
+    }
+    return nst > kChunkSteps && nst <= 64 && tiles <= kArriveMax;
+}
+
+static size_t chunk_part_bytes(const MatArgs * mats, int nmat) {
+    const int64_t nst = (mats[0].K + kStep - 1) / kStep, nck = (nst + kChunkSteps - 1) / kChunkSteps;
+    int64_t tiles = 0;
+    for (int j = 0; j < nmat; ++j) tiles += (mats[j].M + 15) / 16;
+    return ((size_t) nck * (size_t) tiles * 16 * sizeof(float) + 255) / 256 * 256;
+}
+
 size_t matvec_scratch_bytes(const MatArgs * mats, int nmat, const IdArgs * id) {
+    if (nmat >= 1 && chunk_form(mats, nmat, id)) return chunk_part_bytes(mats, nmat);
     if (nmat < 1 || !mc_form(mats, nmat, id)) return 0;
     const int64_t nst = (mats[0].K + kStep - 1) / kStep, nchunks = (nst + kMcChunk - 1) / kMcChunk, nsegp = nchunks * kMcChunk * kSegs;
     int64_t tiles = 0;
@@ -1457,7 +1532,7 @@ size_t matvec_scratch_bytes(const MatArgs * mats, int nmat, const IdArgs * id) {
 }
 
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
-                         uint64_t * grid_size, const IdArgs * id, uint8_t * scratch) {
+                         uint64_t * grid_size, const IdArgs * id, uint8_t * scratch, uint32_t * arrive) {
     if (nmat < 1 || nmat > 3) return hipErrorInvalidValue;
     const MatArgs & a = mats[0];
     for (int j = 0; j < nmat; ++j) {
@@ -1515,6 +1590,31 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     // burst form (one column, K <= 64 steps): every wave's steps (<= 4) loaded at once, one tile
     // per work-group. 32- or 48-row tiles (two or three row groups sharing each x operand) for
     // large products, 16-row tiles otherwise (more work-groups). 2 steps per wave up to K = 32 steps, 3 up to 48 (16 waves), then 4.
+    L.nck = 1;
+    L.part = nullptr;
+    L.arrive = nullptr;
+    if (nc == 1 && L.xvec && scratch != nullptr && arrive != nullptr && chunk_form(mats, nmat, id) && rows >= (int64_t) 64 * cu_count &&
+        tuning("SCRAPGPU_HIP_MV_BURST", 1)) {
+        // a long K in chunks of kChunkSteps steps over 8-wave work-groups of 16 rows, once there
+        // are 4 row tiles per CU: the chunks' hand-over (partial-sum stores, the arrival count,
+        // the last chunk's loads) adds dependent memory round trips at the end of the launch,
+        // which cost more than smaller work-groups save below that (Q6_K 4096 x 12288: 11.8
+        // against 10.7 us; Q4_K 28672 x 8192: 30.7 against 32.1 us)
+        set_tiles(L, mats, nmat, 16);
+        L.nck = (nst + kChunkSteps - 1) / kChunkSteps;
+        L.part = reinterpret_cast<float *>(scratch);
+        L.arrive = arrive;
+        constexpr int W = 8, sp = 2;
+        const size_t lds = (size_t) W * sp * kSegs * (sizeof(XSeg) + sizeof(float4)) + (size_t) W * 16 * sizeof(float) + 32;
+        void * fn = dt == Q4_0 ? (void *) k_mvb<Q4_0, 1, W, sp, true> : dt == Q8_0 ? (void *) k_mvb<Q8_0, 1, W, sp, true>
+                  : dt == Q4_K ? (void *) k_mvb<Q4_K, 1, W, sp, true> : (void *) k_mvb<Q6_K, 1, W, sp, true>;
+        const uint64_t grid = (uint64_t) L.tiles * (uint64_t) L.nck;
+        if (grid_size) *grid_size = grid;
+        std::snprintf(last_form().form, sizeof(last_form().form), "burst-chunks rg=1 W=%d spw=%d chunks=%d", W, sp, (int) L.nck);
+        last_form().grid = grid;
+        void * args[] = {&L};
+        return hipLaunchKernel(fn, dim3((unsigned) L.tiles, (unsigned) L.nck), dim3((unsigned) (64 * W)), args, lds, stream);
+    }
     if (nc == 1 && L.xvec && nst <= 64 && tuning("SCRAPGPU_HIP_MV_BURST", 1)) {
         // (the 32-row Q8_0 / Q6_K forms need more registers than 5 waves per SIMD leave them)
         // 48-row tiles once they give every CU two work-groups (one round at 4 waves per SIMD)

@@ -189,12 +189,11 @@ def test_config5_q6_k_lm_head(hip, N):
 
 
 def test_config5_q4_k_70b_mlp(hip):
-    """the 70B-class Q4_K MLP matrix, W 28672 x 8192, at batch 1 (32 steps of K: the
-    48-row burst tiles at 2 steps per wave)."""
+    """the 70B-class Q4_K MLP matrix, W 28672 x 8192, at batch 1 (32 steps of K: two
+    chunks of 16 steps on 16-row tiles)."""
     K, M = 8192, 28672
     q, _, wt = weights(hip, sg.Q4_K, K, M, 800)
     x = O.normal(K, 80).reshape(1, K)
     (y,), (form, grid) = run(hip, [wt], x)
-    want = "burst rg=3" if M >= 96 * cus(hip) else "burst rg=2" if M >= 64 * cus(hip) else "burst rg=1"
-    assert form.startswith(want), form
+    assert form.startswith("burst-chunks rg=1 W=8 spw=2 chunks=2"), form
     check(sg.Q4_K, q, K, M, x, y, f"Q4_K {M}x{K} N=1 [{form}]")

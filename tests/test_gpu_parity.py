@@ -162,20 +162,58 @@ def test_matvec_decode_three_steps_per_wave(hip, dtype, K):
     check_matvec(y, ref, x, deq)
 
 
-@pytest.mark.parametrize("dtype", [sg.Q4_0, sg.Q4_K], ids=["q4_0", "q4_k"])
-def test_matvec_decode_long_k_many_rows(hip, dtype):
-    """N = 1, K = 12288 (48 steps) over 96 rows per CU: enough rows for 48-row tiles, which past 32
-    steps give way to 16-row tiles of 3 steps per wave (the launch must show 16-row tiles)."""
+@pytest.mark.parametrize("dtype,K", [(sg.Q4_0, 12288), (sg.Q4_K, 12288), (sg.Q6_K, 11008), (sg.Q8_0, 4352)],
+                         ids=["q4_0", "q4_k", "q6_k_partial_chunk", "q8_0_one_step_chunk"])
+def test_matvec_decode_long_k_chunks(hip, dtype, K):
+    """N = 1 with K past 16 steps and 4 row tiles per CU: K in chunks of 16 steps over 8-wave
+    work-groups of 16 rows, the
+    chunks' partial sums added by the last chunk of each row tile to arrive, which resets its
+    count. Three launches in a row (the counts must be back at zero after each), each against the
+    oracle and bit for bit equal to the first; K = 11008 ends in a chunk of 11 steps, K = 4352 in
+    a chunk of one step. The launch shape is pinned."""
     dev, st = hip
-    K, M = 12288, 96 * dev.info().compute_units
-    q0, d0 = quantized(dtype, K, 96, 950) # 96 rows, repeated (rows are independent)
-    q, deq = np.tile(q0, M // 96), np.tile(d0, (M // 96, 1))
+    M = 64 * dev.info().compute_units + 40 # 4 row tiles per CU (where chunks start), a partial last one
+    q0, d0 = quantized(dtype, K, 96, 950)   # 96 rows, repeated (rows are independent)
+    reps = -(-M // 96)
+    q, deq = np.tile(q0, reps)[: M * (q0.size // 96)], np.tile(d0, (reps, 1))[:M]
     x = O.normal(K, 951).reshape(1, K)
-    y = run_mul_mat(dev, st, dtype, q, K, M, x)
-    form, grid = sg.last_launch()
-    assert form == "burst rg=1 W=16 spw=3" and grid == M // 16, (form, grid)
     ref = O.mul_mat(dtype, q, K, M, x, threads=8)
-    check_matvec(y, ref, x, deq)
+    first = None
+    for _ in range(3):
+        y = run_mul_mat(dev, st, dtype, q, K, M, x)
+        form, grid = sg.last_launch()
+        nck = -(-(K // 256) // 16)
+        assert form == f"burst-chunks rg=1 W=8 spw=2 chunks={nck}" and grid == (M + 15) // 16 * nck, (form, grid)
+        check_matvec(y, ref, x, deq)
+        if first is None:
+            first = y
+        assert np.array_equal(y.view(np.uint32), first.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [sg.Q4_0, sg.Q4_K], ids=["q4_0", "q4_k"])
+def test_matvec_decode_long_k_slices(hip, dtype):
+    """N = 1, K = 12288 (48 steps) over 2 slices: no chunks (one slice only), 16-row tiles of 3
+    steps per wave on 16 waves (the launch must show them)."""
+    dev, st = hip
+    K, M, S = 12288, 320, 2
+    q0, d0 = quantized(dtype, K, M, 952)
+    q1, d1 = quantized(dtype, K, M, 953)
+    wb, wt = upload_weights(dev, st, dtype, np.concatenate([q0, q1]), K, M, slices=S)
+    x = O.normal(S * K, 954).reshape(S, 1, K)
+    xb, yb = dev.alloc(x.nbytes), dev.alloc(4 * M * S)
+    xt = sg.tdesc(sg.F32, (K, 1, S), xb)
+    yt = sg.tdesc(sg.F32, (M, 1, S), yb)
+    st.upload(xt, x)
+    op, keep = sg.mul_mat_op(wt, xt, yt)
+    st.execute(op)
+    st.sync()
+    form, grid = sg.last_launch()
+    assert form == "burst rg=1 W=16 spw=3" and grid == M // 16 * S, (form, grid)
+    y = st.download(yt).reshape(S, M)
+    for sl, (q, deq) in enumerate(((q0, d0), (q1, d1))):
+        check_matvec(y[sl:sl + 1], O.mul_mat(dtype, q, K, M, x[sl], threads=8), x[sl], deq)
+    for b in (wb, xb, yb):
+        b.free()
 
 
 @pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])

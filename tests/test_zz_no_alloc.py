@@ -34,15 +34,17 @@ def _run(dev, st, wt, x, M, static):
     return y
 
 
-@pytest.mark.parametrize("dtype", [sg.Q4_K, sg.Q6_K], ids=lambda d: sg.NAMES[d])
-def test_static_scratch_matches_op_execute(hip, dtype):
+@pytest.mark.parametrize("dtype,K", [(sg.Q4_K, 4096), (sg.Q6_K, 4096), (sg.Q4_K, 12288)], ids=["q4_k", "q6_k", "q4_k_long_k"])
+def test_static_scratch_matches_op_execute(hip, dtype, K):
+    """K = 12288 over 4 row tiles per CU: the decode column runs in K chunks, whose arrival counts
+    are the static ones."""
     dev, st = hip
-    K, M = 4096, 1536
+    M = 1536 if K == 4096 else 64 * dev.info().compute_units
     q, _ = quantized(dtype, K, M, 1500)
     wb, wt = upload_weights(dev, st, dtype, q, K, M)
     # prefill at 512 tokens (f16 x in the scratch), then 64 tokens (split-K partials as well), then
     # one decode column (no scratch): each against scrapgpu_op_execute and the oracle
-    for N in (512, 64, 1):
+    for N in ((512, 64, 1) if K == 4096 else (64, 1)):  # (512 tokens at K = 12288 need more than the static scratch)
         x = O.normal(N * K, 1501 + N).reshape(N, K)
         y_static = _run(dev, st, wt, x, M, True)
         form = sg.last_launch()[0]
