@@ -317,13 +317,15 @@ def test_prefill_q4k_large_scales_and_split_groups(hip, K, M, N):
         assert e <= 5e-5, f"rows {rows}: NMSE {e:.3e}"
 
 
-@pytest.mark.parametrize("M,K", [(768, 256), (256, 3072)], ids=["one_k_group", "three_k_groups"])
-def test_prefill_workgroup_per_cu_slices_broadcast_strides(hip, M, K):
-    """The 12-wave prefill kernels over 4 x slices with 2 weight slices (broadcast r2 = 2) and
-    padded x / y column strides: 384-row tiles (M = 768) and 3 K groups (K = 3072), each filling
-    the CUs with 4 slices x 2048 tokens."""
+@pytest.mark.parametrize("M,K,S,form", [(768, 256, 4, "gemm w=12 kg=1 bn=64"), (256, 3072, 4, "gemm w=12 kg=3"), (768, 256, 8, "gemm wide w=12 kg=1")],
+                         ids=["one_k_group", "three_k_groups", "wide"])
+def test_prefill_workgroup_per_cu_slices_broadcast_strides(hip, M, K, S, form):
+    """The 12-wave prefill kernels over S x slices with 2 weight slices (broadcast r2 = S / 2) and
+    padded x / y column strides: 384-row x 64-token tiles (M = 768, 4 slices), 3 K groups
+    (K = 3072), and 384-row x 128-token tiles of the wide GEMM (8 slices), each filling the CUs
+    with S slices x 2048 tokens (on a 256-CU part)."""
     dev, st = hip
-    dtype, N, S = sg.Q4_K, 2048, 4
+    dtype, N = sg.Q4_K, 2048
     q0, _ = quantized(dtype, K, M, 11)
     q1, _ = quantized(dtype, K, M, 12)
     wb, wt = upload_weights(dev, st, dtype, np.concatenate([q0, q1]), K, M, slices=2)
@@ -338,9 +340,11 @@ def test_prefill_workgroup_per_cu_slices_broadcast_strides(hip, M, K):
     op, keep = sg.mul_mat_op(wt, xt, yt, allow_broadcast=1)
     st.execute(op)
     st.sync()
+    if dev.info().compute_units == 256:
+        assert sg.last_launch()[0].startswith(form), sg.last_launch()
     y = st.read(yb, 0, 4 * ys1 * N * S).view(np.float32).reshape(S, N, ys1)
     for s in range(S):
-        ref = O.mul_mat(dtype, q0 if s // 2 == 0 else q1, K, M, x[s, :, :K].copy(), threads=8)
+        ref = O.mul_mat(dtype, q0 if s // (S // 2) == 0 else q1, K, M, x[s, :, :K].copy(), threads=8)
         e = nmse(y[s, :, :M], ref)
         assert e <= 5e-5, f"slice {s}: NMSE {e:.3e}"
         assert np.all(y[s, :, M:] == -7.0), "padding of dst was written"
@@ -435,6 +439,39 @@ def test_prefill_wide_q4k_large_scales(hip):
     for rows in (slice(0, 10), slice(20, 30), slice(40, 45), slice(50, M)):
         e = nmse(y[:, rows], ref[:, rows])
         assert e <= 5e-5, f"rows {rows}: NMSE {e:.3e}"
+
+
+def test_prefill_wide_multi_per_weight_tiles(hip):
+    """A prefill MUL_MAT_MULTI on the wide GEMM whose first weights are not whole 32-row groups
+    (1000 + 1000 + 1072 rows): each weight owns its own 384-row tiles, the last one of each
+    partial."""
+    dev, st = hip
+    dtype, K, Ms = sg.Q4_K, 512, (1000, 1000, 1072)
+    N = wide_tokens(dev, 8)
+    x = O.normal(N * K, 940).reshape(N, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    st.upload(xt, x)
+    bufs, wts, yts, refs = [], [], [], []
+    for i, M in enumerate(Ms):
+        q, _ = quantized(dtype, K, M, 941 + i)
+        b, t = upload_weights(dev, st, dtype, q, K, M)
+        yb = dev.alloc(4 * M * N)
+        bufs += [b, yb]
+        wts.append(t)
+        yts.append(sg.tdesc(sg.F32, (M, N), yb))
+        refs.append(O.mul_mat(dtype, q, K, M, x, threads=8))
+    op, keep = sg.multi_op(wts, xt, yts)
+    st.execute(op)
+    st.sync()
+    form, grid = sg.last_launch()
+    assert form.startswith("gemm wide"), form
+    assert grid == sum((M + 383) // 384 for M in Ms) * ((N + 127) // 128), (form, grid)
+    for M, yt, ref in zip(Ms, yts, refs):
+        e = nmse(st.download(yt).reshape(N, M), ref)
+        assert e <= 5e-5, f"{M} rows: NMSE {e:.3e}"
+    for b in bufs + [xb]:
+        b.free()
 
 
 def test_prefill_wide_multi_tiles_across_weights(hip):
