@@ -947,8 +947,9 @@ struct XDma {
 };
 
 // The wide GEMM: one 12-wave work-group per CU as in the 12-wave k_matmul, but each wave owns 32
-// weight rows x 128 tokens (4 token fragments), so every dequantized B fragment feeds 4 MFMAs
-// instead of 2 (a 384-row x 128-token tile). The dequantization VALU per MFMA halves; the
+// weight rows x 128 tokens (NF = 4 token fragments), so every dequantized B fragment feeds 4 MFMAs
+// instead of 2 (a 384-row x 128-token tile). NF = 2 (64 tokens) serves shapes with few tokens and
+// many rows, bound by their weight stream. The dequantization VALU per MFMA halves; the
 // registers for the extra accumulators come from the exact Q4_K form (s (c + bias) + o per pair,
 // from plain x: no offset MFMA, no sub-block sums, no rare-scale branch), one set of A fragments
 // (each read again right after the MFMA that consumed it), x tiles loaded straight into LDS and
@@ -959,9 +960,9 @@ struct XDma {
 // 118 against 145 us, 12288 x 4096 at 512 tokens (KG = 2) 70-76 against 79-82 us. Wave tiles of 64
 // rows x 64 tokens (half the LDS reads per MFMA, twice the dequantization) measured slower than
 // the 64-token form. Split-K over work-groups (partials + k_split_reduce) as in k_matmul.
-template <int DT, int KG>
+template <int DT, int KG, int NF = 4>
 __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
-    constexpr int W = 12, NF = 4, BN = 32 * NF, RW = W / KG, BMT = 32 * RW;
+    constexpr int W = 12, BN = 32 * NF, RW = W / KG, BMT = 32 * RW;
     using F = PFmt<DT>;
     using Raw = typename F::Raw;
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_mm[];
@@ -1328,7 +1329,7 @@ struct MmConfig {
     int split;
     int w;  // waves per work-group: 4, or 12 (one work-group per CU, see k_matmul)
     int kg; // K groups of a 12-wave work-group: 1 or 3
-    bool wide = false; // k_gemm_w: 128-token wave tiles (w = 12, kg 1 or 2, bn = 128)
+    bool wide = false; // k_gemm_w (w = 12): 128-token wave tiles (kg 1 or 2, bn = 128), or 64-token ones (kg = 1, bn = 64)
 };
 
 int env_int(const char * name, int dflt) {
@@ -1388,6 +1389,18 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
             c.bn = 64;
             c.wide = false;
         }
+        // ... or 384-row x 64-token wave tiles of it (64 tokens or fewer) where they give every CU
+        // a work-group at least: the shape is then bound by its
+        // weight stream, which the wide form reads from fewer, larger work-groups (the Q6_K LM
+        // head at 64 tokens: 163 against 191 us; with fewer tiles than CUs it lost, the 70B-class
+        // 28672x8192 at 64 tokens 92 against 77 us split over K)
+        if (env_wide != 0 && free_choice && env_kg != 2 && env_kg != 3 && a.K % BK == 0 && a.N <= 64 &&
+            (a.M % 384 == 0 || a.M >= 8 * 384) && (a.M + 383) / 384 * ((a.N + 63) / 64) * slices >= cu_count) {
+            c.kg = 1;
+            c.bn = 64;
+            c.wide = true;
+            return c;
+        }
         if (env_w == 12) { // forced: KG = 1, split from SCRAPGPU_HIP_MM_SPLIT
             c.kg = 1;
             if (env_split > 0) c.split = (int) std::max<int64_t>(1, std::min<int64_t>(std::min(env_split, 8), (stages + 3) / 4));
@@ -1420,7 +1433,7 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
 
 template <int DT>
 void * kernel_of(const MmConfig & c) {
-    if (c.wide) return c.kg == 2 ? (void *) k_gemm_w<DT, 2> : (void *) k_gemm_w<DT, 1>;
+    if (c.wide) return c.bn == 64 ? (void *) k_gemm_w<DT, 1, 2> : c.kg == 2 ? (void *) k_gemm_w<DT, 2> : (void *) k_gemm_w<DT, 1>;
     if (c.w == 12) return c.kg == 3 ? (void *) k_matmul<DT, 64, 1, 12, 3> : c.kg == 2 ? (void *) k_matmul<DT, 64, 1, 12, 2> : (void *) k_matmul<DT, 64, 1, 12, 1>;
     if (c.rg == 1) return c.bn == 64 ? (void *) k_matmul<DT, 64, 1, 4, 1> : (void *) k_matmul<DT, 128, 1, 4, 1>;
     return c.bn == 64 ? (void *) k_matmul<DT, 64, 2, 4, 1> : (void *) k_matmul<DT, 128, 2, 4, 1>;

@@ -420,6 +420,25 @@ def test_prefill_wide_k_groups(hip, dtype, K, pad):
         b.free()
 
 
+@pytest.mark.parametrize("dtype,N,extra", [(sg.Q6_K, 64, 0), (sg.Q8_0, 40, 0), (sg.Q4_K, 64, 100), (sg.Q4_0, 16, 0)],
+                         ids=["q6_k", "q8_0_token_tail", "q4_k_row_tail", "q4_0_16_tokens"])
+def test_prefill_wide_64_tokens(hip, dtype, N, extra):
+    """The wide GEMM with 64-token wave tiles (few tokens, rows enough for a 384-row tile per CU,
+    as in an LM head): a part-empty token tile (N = 40, 16) and a partial last row tile."""
+    dev, st = hip
+    K = 256
+    M = 384 * dev.info().compute_units + extra
+    q, _ = quantized(dtype, K, M, 960 + N)
+    x = O.normal(N * K, 961).reshape(N, K)
+    y = run_mul_mat(dev, st, dtype, q, K, M, x)
+    form, grid = sg.last_launch()
+    assert form.startswith("gemm wide w=12 kg=1 bn=64"), form
+    assert grid == (M + 383) // 384, (form, grid)
+    ref = O.mul_mat(dtype, q, K, M, x, threads=8)
+    e = nmse(y, ref)
+    assert e <= 5e-5, f"NMSE {e:.3e}"
+
+
 def test_prefill_wide_q4k_large_scales(hip):
     """The wide GEMM's exact Q4_K form on rows with scales (weights in the hundreds) and offsets
     (means near -3000) far beyond the ordinary ones, mixed with ordinary rows."""
