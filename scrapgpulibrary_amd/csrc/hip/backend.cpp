@@ -814,11 +814,12 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
             flops += 2.0 * (double) mats[j].M * (double) mats[j].K * (double) mats[j].N;
         }
         uint8_t * scr = nullptr;
-        const scrapgpu_status st = scratch_for(s, sgk::matmul_scratch_bytes(all, cus), &scr);
+        const bool lean = t_static_scratch != nullptr;
+        const scrapgpu_status st = scratch_for(s, sgk::matmul_scratch_bytes(all, cus, lean), &scr);
         if (st != SCRAPGPU_STATUS_OK) return st;
         ProfScope prof(s->s);
         const char * name = nullptr;
-        SG_HIP(sgk::launch_matmul_mfma(mats, n, scr, cus, s->s, &name), "matmul (MULTI) launch");
+        SG_HIP(sgk::launch_matmul_mfma(mats, n, scr, cus, s->s, &name, false, lean), "matmul (MULTI) launch");
         prof.done(name, bytes, flops);
         return SCRAPGPU_STATUS_OK;
     }
@@ -827,7 +828,7 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
         // prefill products of one MUL_MAT_MULTI: scratch for the largest first, so that products
         // reading the same x share one x pre-pass (the scratch stays in place between them)
         size_t need = 0;
-        for (int j = 0; j < n; ++j) need = std::max(need, sgk::matmul_scratch_bytes(mats[j], cus));
+        for (int j = 0; j < n; ++j) need = std::max(need, sgk::matmul_scratch_bytes(mats[j], cus, t_static_scratch != nullptr));
         uint8_t * scr = nullptr;
         const scrapgpu_status st = scratch_for(s, need, &scr);
         if (st != SCRAPGPU_STATUS_OK) return st;
@@ -854,12 +855,13 @@ scrapgpu_status run_products(Stream * s, const sgk::MatArgs * mats, int n) {
             prof.done(name, bytes, flops);
         } else {
             uint8_t * scr = nullptr;
-            const scrapgpu_status st = scratch_for(s, sgk::matmul_scratch_bytes(m[0], cus), &scr);
+            const bool lean = t_static_scratch != nullptr;
+            const scrapgpu_status st = scratch_for(s, sgk::matmul_scratch_bytes(m[0], cus, lean), &scr);
             if (st != SCRAPGPU_STATUS_OK) return st;
             ProfScope prof(s->s);
             const char * name = nullptr;
-            const bool x_ready = !fuse && gi > 0 && mats[gi - 1].N > mv_n && sgk::matmul_same_x(mats[gi - 1], m[0], cus);
-            SG_HIP(sgk::launch_matmul_mfma(m, 1, scr, cus, s->s, &name, x_ready), "matmul launch");
+            const bool x_ready = !fuse && gi > 0 && mats[gi - 1].N > mv_n && sgk::matmul_same_x(mats[gi - 1], m[0], cus, lean);
+            SG_HIP(sgk::launch_matmul_mfma(m, 1, scr, cus, s->s, &name, x_ready, lean), "matmul launch");
             prof.done(name, bytes, flops);
         }
     }

@@ -80,14 +80,16 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
 // nmat = 1, or 2..3 single-slice weights of one dtype that read the same x (matmul_reads_same_x): one
 // launch over all their row tiles (run end to end over all their rows when every weight but the
 // last has a whole number of a wave's 32 or 64 rows); matmul_scratch_bytes then takes mats[0] with M = the sum of the
-// matrices' M.
-size_t matmul_scratch_bytes(const MatArgs & a, int cu_count);
+// matrices' M. `lean`: only forms whose scratch is the x buffers and at most split-K partials (no
+// stream-K slots), for a caller whose scratch is a fixed static array; the same `lean` must be
+// passed to every call about one launch.
+size_t matmul_scratch_bytes(const MatArgs & a, int cu_count, bool lean = false);
 hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name,
-                              bool x_ready = false);
+                              bool x_ready = false, bool lean = false);
 // true when b's x pre-pass would write what a's did (same x and shape, and the same x form: the
 // Q4_K single-fma kernels read x in a form of their own): a product
 // launched right after a's on the same scratch may then pass x_ready and skip its own
-bool matmul_same_x(const MatArgs & a, const MatArgs & b, int cu_count);
+bool matmul_same_x(const MatArgs & a, const MatArgs & b, int cu_count, bool lean = false);
 // true when a and b read the same x with the same shape (what one fused launch over both needs)
 bool matmul_reads_same_x(const MatArgs & a, const MatArgs & b);
 

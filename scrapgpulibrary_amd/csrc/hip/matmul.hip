@@ -436,6 +436,7 @@ struct MmArgs {
     int64_t tiles_m, tiles_n;
     int64_t stages;      // stages of K (BK elements each)
     int split;           // work-groups along K per tile
+    int sk_g;            // stream-K (k_gemm_w<.., SK>): the work-groups sharing the tiles' stages
     // grouped MUL_MAT_ID (GA kernels): pair p = t * n_used + slot; pairs[] grouped by expert,
     // expert e's pairs at e_off[e] .. e_off[e + 1] and token tiles at t_start[e] .. t_start[e + 1];
     // x row of a pair: t * x_cols + (x_cols > 1 ? slot : 0); y of a pair: a.y + slot * a.y_s1 + t * a.y_s2
@@ -960,9 +961,10 @@ struct XDma {
 // 118 against 145 us, 12288 x 4096 at 512 tokens (KG = 2) 70-76 against 79-82 us. Wave tiles of 64
 // rows x 64 tokens (half the LDS reads per MFMA, twice the dequantization) measured slower than
 // the 64-token form. Split-K over work-groups (partials + k_split_reduce) as in k_matmul.
-template <int DT, int KG, int NF = 4>
+template <int DT, int KG, int NF = 4, bool SK = false>
 __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
     constexpr int W = 12, BN = 32 * NF, RW = W / KG, BMT = 32 * RW;
+    static_assert(!SK || KG == 1, "stream-K runs 12 row waves");
     using F = PFmt<DT>;
     using Raw = typename F::Raw;
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_mm[];
@@ -970,8 +972,14 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // wave-uniform: scalar addressing
     const int wave = wid % RW, kg = wid / RW;                         // row wave, K group
     const int j = lane & 31, h = lane >> 5;
-    const int64_t tile = blockIdx.x / L.split;
-    const int split = (int) (blockIdx.x % L.split);
+    // one piece of work: stages [p0, p1) of a tile. Split-K: the split's stages of tile
+    // blockIdx.x / split. Stream-K: work-group g takes units [g U / G, (g + 1) U / G) of the
+    // U = tiles x stages / 2 units of 2 stages (tile-major), at most two pieces since U / G is at
+    // most a tile's units; a piece that is
+    // not a whole tile stores its sums (x the rows' factors) into partial slot g + t, which
+    // k_sk_reduce adds in work-group order (g + t rises by at least one from piece to piece, so
+    // the slots are distinct)
+    auto piece = [&](const int64_t tile, const int split, const int p0, const int p1, const int64_t slot) __attribute__((always_inline)) {
     const int64_t tm = tile % L.tiles_m, tn = tile / L.tiles_m;
     const int64_t sl = blockIdx.y;
     const int64_t i2 = sl % L.a.ne12, i3 = sl / L.a.ne12;
@@ -989,8 +997,8 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
     // are inactive: their loads repeat a valid stage, their k-steps are skipped), as in k_matmul
     const int64_t groups = (L.stages + 3) / 4;
     const int gsz = (int) (4 * ((groups + KG - 1) / KG));
-    const int s0 = (int) (KG > 1 ? kg * gsz : 4 * (groups * split / L.split));
-    const int s1 = (int) (KG > 1 ? min<int64_t>(s0 + gsz, L.stages) : min(4 * (groups * (split + 1) / L.split), L.stages));
+    const int s0 = SK ? p0 : (int) (KG > 1 ? kg * gsz : 4 * (groups * split / L.split));
+    const int s1 = SK ? p1 : (int) (KG > 1 ? min<int64_t>(s0 + gsz, L.stages) : min(4 * (groups * (split + 1) / L.split), L.stages));
     const int send = KG > 1 ? s0 + gsz : s1;
     const int lim = s1 - 1;
 
@@ -1046,14 +1054,28 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
         __syncthreads(); // (waits for this wave's loads: the next x tile is in LDS)
     };
     Raw ra{}, rb{};
-    ra = f.load(w, min(s0, lim));
-    xt.load(xb, min(s0, lim) * BK, lds_x);
-    __syncthreads();
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
     int s = s0;
+    if constexpr (SK) {
+        // a piece starts at an even stage: stages 2 and 3 of a group of 4 run first when it
+        // starts inside one, tagged with their position in the unrolled group (LDS buffer,
+        // half-block parity)
+        ra = f.load(w, s0);
+        xt.load(xb, s0 * BK, lds_x);
+        __syncthreads();
+        if (s0 & 2) {
+            stage(I2{}, s, ra, rb);
+            if (s + 1 < s1) stage(I3{}, s + 1, rb, ra);
+            s += 2;
+        }
+    } else {
+        ra = f.load(w, min(s0, lim));
+        xt.load(xb, min(s0, lim) * BK, lds_x);
+        __syncthreads();
+    }
     for (; s + 3 < send; s += 4) {
         stage(I0{}, s, ra, rb);
         stage(I1{}, s + 1, rb, ra);
@@ -1073,7 +1095,11 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
         const int64_t slices = L.a.ne12 * L.a.ne13;
         float * y;
         int64_t ys1;
-        if (L.split == 1) {
+        int64_t m = m0 + j;
+        if (SK && slot >= 0) { // a partial slot: [BN tokens][BMT rows] of the tile
+            y = L.part + (uint64_t) slot * (BN * BMT) - n0 * BMT + 32 * wave + j - m;
+            ys1 = BMT;
+        } else if (L.split == 1) {
             y = L.nmat > 1 ? L.ym[mj] : L.a.y + i2 * L.a.y_s2 + i3 * L.a.y_s3;
             ys1 = L.nmat > 1 ? L.ys1m[mj] : L.a.y_s1;
         } else {
@@ -1082,7 +1108,6 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
             ys1 = mt_all;
         }
         const float * xs = L.xs + (uint64_t) sl * N;
-        const int64_t m = m0 + j;
 #pragma unroll
         for (int q = QB; q < QB + QC; ++q) {
             float u[16];
@@ -1123,6 +1148,21 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
     };
     if (KG == 1 || kg == 0) finish(std::integral_constant<int, 0>{});
     else finish(std::integral_constant<int, 1>{});
+    };
+    if constexpr (SK) {
+        // units of 2 stages (the stage count is even)
+        const int64_t S = L.stages / 2, U = L.tiles_m * L.tiles_n * S, G = gridDim.x, g = blockIdx.x;
+        int64_t lo = g * U / G;
+        const int64_t hi = (g + 1) * U / G;
+        while (lo < hi) {
+            const int64_t t = lo / S;
+            const int p0 = (int) (lo - t * S), p1 = (int) min<int64_t>(S, hi - t * S);
+            piece(t, 0, 2 * p0, 2 * p1, p0 == 0 && p1 == S ? -1 : g + t);
+            lo = (t + 1) * S;
+        }
+    } else {
+        piece(blockIdx.x / L.split, (int) (blockIdx.x % L.split), 0, 0, -1);
+    }
 }
 
 // y = sum of the split-K partials, in split order. blockIdx.x is the row (token n of slice sl),
@@ -1158,6 +1198,61 @@ __global__ __launch_bounds__(256) void k_split_reduce(MmArgs L) {
             for (int sp = 0; sp < L.split; ++sp) v += p[sp * plane + e];
             *out(e) = v;
         }
+    }
+}
+
+// stream-K: y = the sum of a tile's partial slots in work-group order, for the tiles that more
+// than one work-group shared (k_gemm_w<.., SK>). blockIdx.x is the tile, blockIdx.y covers 1024
+// of its 128 x 384 sums (4 consecutive rows of one token per thread); VEC when every matrix's rows
+// and y's rows allow float4 stores. One slice.
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_sk_reduce(MmArgs L) {
+    constexpr int BN = 128, BMT = 384, TE = BN * BMT;
+    const int64_t S = L.stages / 2, U = L.tiles_m * L.tiles_n * S, G = L.sk_g, t = blockIdx.x; // (units of 2 stages)
+    // the work-groups g with g U / G <= t S < (g + 1) U / G, and with (t + 1) S - 1 in their range
+    const int64_t ga = ((t * S + 1) * G + U - 1) / U - 1, gb = ((t + 1) * S * G + U - 1) / U - 1;
+    if (ga == gb) return; // a whole tile of one work-group: stored by it
+    const int e = (blockIdx.y * 256 + threadIdx.x) * 4;
+    if (e >= TE) return;
+    const int nl = e / BMT, ml = e - nl * BMT;
+    const int64_t tm = t % L.tiles_m, n = t / L.tiles_m * BN + nl;
+    if (n >= L.a.N) return;
+    int mj = 0;
+    int64_t m = tm * BMT + ml;
+    if (L.nmat > 1) {
+        if (L.packed) {
+            mj = min(L.nmat - 1, m >= L.mo[1] ? (m >= L.mo[2] ? 2 : 1) : 0);
+            m -= L.mo[mj];
+        } else {
+            mj = tm >= L.mt[1] ? (tm >= L.mt[2] ? 2 : 1) : 0;
+            m = (tm - L.mt[mj]) * BMT + ml;
+        }
+    }
+    const int64_t M = L.nmat > 1 ? L.Mm[mj] : L.a.M;
+    if (m >= M) return;
+    float * y = (L.nmat > 1 ? L.ym[mj] + n * L.ys1m[mj] : L.a.y + n * L.a.y_s1) + m;
+    const float * p = L.part + (uint64_t) (ga + t) * TE + e;
+    // up to 8 slots loaded together, then added in order
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int64_t g0 = 0; g0 <= gb - ga; g0 += 8) {
+        float4 u[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (g0 + i <= gb - ga) u[i] = *reinterpret_cast<const float4 *>(p + (uint64_t) (g0 + i) * TE);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (g0 + i <= gb - ga) {
+                v.x += u[i].x;
+                v.y += u[i].y;
+                v.z += u[i].z;
+                v.w += u[i].w;
+            }
+    }
+    if (VEC) {
+        *reinterpret_cast<float4 *>(y) = v;
+    } else {
+        const float r[4] = {v.x, v.y, v.z, v.w};
+        for (int i = 0; i < 4 && m + i < M; ++i) y[i] = r[i];
     }
 }
 
@@ -1330,6 +1425,7 @@ struct MmConfig {
     int w;  // waves per work-group: 4, or 12 (one work-group per CU, see k_matmul)
     int kg; // K groups of a 12-wave work-group: 1 or 3
     bool wide = false; // k_gemm_w (w = 12): 128-token wave tiles (kg 1 or 2, bn = 128), or 64-token ones (kg = 1, bn = 64)
+    bool sk = false;   // the wide form's stream-K (kg = 1, bn = 128): cu_count work-groups share all tiles' stages
 };
 
 int env_int(const char * name, int dflt) {
@@ -1337,7 +1433,7 @@ int env_int(const char * name, int dflt) {
     return v != nullptr && *v ? std::atoi(v) : dflt;
 }
 
-MmConfig config_of(const MatArgs & a, int cu_count) {
+MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
     static const int env_bn = env_int("SCRAPGPU_HIP_MM_BN", 0), env_rg = env_int("SCRAPGPU_HIP_MM_RG", 0);
     static const int env_split = env_int("SCRAPGPU_HIP_MM_SPLIT", 0);
     const int64_t slices = a.ne12 * a.ne13;
@@ -1380,6 +1476,26 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
             c.wide = true;
             if (env_kg != 2 && (a.M % 384 == 0 || a.M >= 8 * 384) && fill((a.M + 383) / 384 * ntw)) {
                 c.kg = 1;
+                return c;
+            }
+            static const int env_ws = env_int("SCRAPGPU_HIP_MM_WSPLIT", 0);
+            if (env_ws > 1) {
+                c.kg = env_kg == 2 ? 2 : 1;
+                if (c.kg == 1) c.split = env_ws;
+                return c;
+            }
+            // stream-K: fewer 384-row tiles than CUs, one slice, and every work-group gets at least
+            // SCRAPGPU_HIP_MM_SK (default 32) stages. Its partial slots take (CUs + tiles) x 192 KiB
+            // of scratch, which the static scratch does not hold (lean). (4096x12288 at 2048 tokens:
+            // 213 + 23 (reduce) us against 290 for the 64-token form; at 512 tokens, 16.5 stages per
+            // work-group, 69 + 16 against 78: the GEMM is bound by its loads there, 60 KiB per
+            // 12.6 MFLOP stage, and the partial sums cost more than the even split saves)
+            static const int env_sk = env_int("SCRAPGPU_HIP_MM_SK", 32);
+            const int64_t tw = (a.M + 383) / 384 * ntw;
+            if (env_sk > 0 && !lean && env_kg != 2 && slices == 1 && stages % 2 == 0 && (a.M % 384 == 0 || a.M >= 8 * 384) && tw < cu_count &&
+                tw * stages >= (int64_t) env_sk * cu_count) {
+                c.kg = 1;
+                c.sk = true;
                 return c;
             }
             if (env_kg != 1 && (a.M % 192 == 0 || a.M >= 8 * 192) && fill((a.M + 191) / 192 * ntw) && stages >= 16 && (2 * gsz2 - stages) * 8 <= stages) {
@@ -1433,6 +1549,7 @@ MmConfig config_of(const MatArgs & a, int cu_count) {
 
 template <int DT>
 void * kernel_of(const MmConfig & c) {
+    if (c.sk) return (void *) k_gemm_w<DT, 1, 4, true>;
     if (c.wide) return c.bn == 64 ? (void *) k_gemm_w<DT, 1, 2> : c.kg == 2 ? (void *) k_gemm_w<DT, 2> : (void *) k_gemm_w<DT, 1>;
     if (c.w == 12) return c.kg == 3 ? (void *) k_matmul<DT, 64, 1, 12, 3> : c.kg == 2 ? (void *) k_matmul<DT, 64, 1, 12, 2> : (void *) k_matmul<DT, 64, 1, 12, 1>;
     if (c.rg == 1) return c.bn == 64 ? (void *) k_matmul<DT, 64, 1, 4, 1> : (void *) k_matmul<DT, 128, 1, 4, 1>;
@@ -1478,15 +1595,26 @@ static hipError_t allow_lds(void * fn, size_t lds) {
     return hipSuccess;
 }
 
-size_t matmul_scratch_bytes(const MatArgs & a, int cu_count) {
-    const int split = config_of(a, cu_count).split;
-    return part_offset(a) + (split == 1 ? 0 : part_bytes(a, split));
+// stream-K partial slots: one per piece, at most cu_count + tiles - 1, each 128 x 384 floats. The
+// row tiles of 2..3 weights tiled one by one are at most 2 more than those of all their rows
+static int64_t sk_max_tiles(const MatArgs & a) {
+    return ((a.M + 383) / 384 + 2) * ((a.N + 127) / 128);
+}
+
+static size_t sk_part_bytes(const MatArgs & a, int cu_count) {
+    return (size_t) (cu_count + sk_max_tiles(a) - 1) * 128 * 384 * sizeof(float);
+}
+
+size_t matmul_scratch_bytes(const MatArgs & a, int cu_count, bool lean) {
+    const MmConfig c = config_of(a, cu_count, lean);
+    if (c.sk) return part_offset(a) + sk_part_bytes(a, cu_count);
+    return part_offset(a) + (c.split == 1 ? 0 : part_bytes(a, c.split));
 }
 
 // the pre-pass writes Q4_K's single-fma form of x (high-nibble positions / 16, sub-block sums)
 // for the Q4_K kernels that use it, plain scaled x for every other kernel
-static bool q4k_x_form(const MatArgs & a, int cu_count) {
-    return a.dtype == Q4_K && !config_of(a, cu_count).wide;
+static bool q4k_x_form(const MatArgs & a, int cu_count, bool lean) {
+    return a.dtype == Q4_K && !config_of(a, cu_count, lean).wide;
 }
 
 bool matmul_reads_same_x(const MatArgs & a, const MatArgs & b) {
@@ -1494,12 +1622,12 @@ bool matmul_reads_same_x(const MatArgs & a, const MatArgs & b) {
            a.ne13 == b.ne13;
 }
 
-bool matmul_same_x(const MatArgs & a, const MatArgs & b, int cu_count) {
-    return matmul_reads_same_x(a, b) && q4k_x_form(a, cu_count) == q4k_x_form(b, cu_count);
+bool matmul_same_x(const MatArgs & a, const MatArgs & b, int cu_count, bool lean) {
+    return matmul_reads_same_x(a, b) && q4k_x_form(a, cu_count, lean) == q4k_x_form(b, cu_count, lean);
 }
 
 hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name,
-                              bool x_ready) {
+                              bool x_ready, bool lean) {
     if (nmat < 1 || nmat > 3) return hipErrorInvalidValue;
     // several weights: one slice each, one dtype, the same x; the launch sees them as one matrix
     // of all their rows for its shape choice and scratch
@@ -1516,7 +1644,7 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     const int64_t xsum_row = xsum_row_of(a);
     if (rows > 0x7fffffff) return hipErrorInvalidValue;
     const dim3 xg((unsigned) rows);
-    const MmConfig cfg = config_of(a, cu_count);
+    const MmConfig cfg = config_of(a, cu_count, lean);
     if (x_ready) {
         // x converted by the previous product's pre-pass (matmul_same_x)
     } else if (a.dtype == Q4_K && !cfg.wide) {
@@ -1568,7 +1696,9 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     const size_t lds = cfg.wide ? std::max((size_t) cfg.kg * 2 * BN * XR * sizeof(uint16_t), (size_t) (cfg.kg > 1 ? 12 * 2 * 16 * 64 : 0) * sizeof(float))
                                 : (size_t) cfg.kg * 2 * BN * BK * sizeof(uint16_t);
     const int64_t slices = a.ne12 * a.ne13;
-    const dim3 grid((unsigned) (L.tiles_m * L.tiles_n * L.split), (unsigned) slices);
+    L.sk_g = cfg.sk ? cu_count : 0;
+    if (cfg.sk && L.tiles_m * L.tiles_n > sk_max_tiles(a)) return hipErrorInvalidValue; // (more slots than the scratch holds)
+    const dim3 grid(cfg.sk ? (unsigned) cu_count : (unsigned) (L.tiles_m * L.tiles_n * L.split), (unsigned) slices);
     void * args[] = {&L};
     void * fn = nullptr;
     switch (a.dtype) {
@@ -1579,13 +1709,24 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
         default: return hipErrorInvalidValue;
     }
     if ((e = allow_lds(fn, lds)) != hipSuccess) return e;
-    std::snprintf(last_form().form, sizeof(last_form().form), "gemm%s w=%d kg=%d bn=%d rg=%d split=%d", cfg.wide ? " wide" : "", cfg.w, cfg.kg, BN,
-                  cfg.rg, L.split);
+    if (cfg.sk)
+        std::snprintf(last_form().form, sizeof(last_form().form), "gemm wide stream-k w=12 kg=1 bn=128 rg=1 wgs=%d", cu_count);
+    else
+        std::snprintf(last_form().form, sizeof(last_form().form), "gemm%s w=%d kg=%d bn=%d rg=%d split=%d", cfg.wide ? " wide" : "", cfg.w, cfg.kg, BN,
+                      cfg.rg, L.split);
     last_form().grid = (uint64_t) grid.x * grid.y;
     e = hipLaunchKernel(fn, grid, dim3((unsigned) (64 * cfg.w)), args, lds, stream);
-    if (e != hipSuccess || L.split == 1) return e;
+    if (e != hipSuccess || (L.split == 1 && !cfg.sk)) return e;
     bool yvec = a.y_s2 % 4 == 0 && a.y_s3 % 4 == 0;
     for (int j = 0; j < nmat; ++j) yvec = yvec && (reinterpret_cast<uintptr_t>(mats[j].y) & 15) == 0 && mats[j].M % 4 == 0 && mats[j].y_s1 % 4 == 0;
+    if (cfg.sk) {
+        const dim3 rg((unsigned) (L.tiles_m * L.tiles_n), (unsigned) (128 * 384 / 1024));
+        if (yvec)
+            hipLaunchKernelGGL(k_sk_reduce<true>, rg, dim3(256), 0, stream, L);
+        else
+            hipLaunchKernelGGL(k_sk_reduce<false>, rg, dim3(256), 0, stream, L);
+        return hipGetLastError();
+    }
     const dim3 rg((unsigned) rows, (unsigned) ((a.M + 1023) / 1024));
     if (yvec)
         hipLaunchKernelGGL(k_split_reduce<true>, rg, dim3(256), 0, stream, L);

@@ -174,6 +174,8 @@ def test_config4_q4_k_prefill(hip, K, M, N):
     x = O.normal(N * K, 60 + N).reshape(N, K)
     (y,), (form, grid) = run(hip, [wt], x)
     assert form.startswith("gemm"), form
+    if M == 4096 and N == 2048 and hip[0].info().compute_units == 256:
+        assert form.startswith("gemm wide stream-k"), form  # (176 tiles, 66 stages per CU)
     check(sg.Q4_K, q, K, M, x, y, f"Q4_K {M}x{K} N={N} [{form}]")
 
 

@@ -493,6 +493,65 @@ def test_prefill_wide_multi_per_weight_tiles(hip):
         b.free()
 
 
+def sk_tokens(dev, row_tiles, stages, pad=0, extra=0):
+    """Tokens at which `row_tiles` 384-row x 128-token tiles are fewer than the CUs but hold at
+    least 32 stages of K per CU (the wide GEMM's stream-K form), plus `extra` token tiles, less
+    `pad`."""
+    cus = dev.info().compute_units
+    ntw = -(-32 * cus // (row_tiles * stages)) + extra
+    assert row_tiles * ntw < cus, (row_tiles, ntw, cus)
+    return 128 * ntw - pad
+
+
+def _sk_run(dev, st, dtype, K, Ms, N, seed):
+    x = O.normal(N * K, seed).reshape(N, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    st.upload(xt, x)
+    bufs, wts, yts, refs = [xb], [], [], []
+    for i, M in enumerate(Ms):
+        q, _ = quantized(dtype, K, M, seed + 1 + i)
+        b, t = upload_weights(dev, st, dtype, q, K, M)
+        yb = dev.alloc(4 * M * N)
+        st.write(yb, 0, np.full(M * N, np.nan, np.float32))
+        bufs += [b, yb]
+        wts.append(t)
+        yts.append(sg.tdesc(sg.F32, (M, N), yb))
+        refs.append(O.mul_mat(dtype, q, K, M, x, threads=8))
+    op, keep = sg.multi_op(wts, xt, yts) if len(Ms) > 1 else sg.mul_mat_op(wts[0], xt, yts[0])
+    ys = []
+    for rep in range(2):  # (the second launch finds the first one's partial slots in the scratch)
+        st.execute(op)
+        st.sync()
+        ys.append([st.download(yt).reshape(N, M).copy() for M, yt in zip(Ms, yts)])
+    form, grid = sg.last_launch()
+    for b in bufs:
+        b.free()
+    return ys, refs, form, grid
+
+
+@pytest.mark.parametrize("dtype,K,Ms,pad", [(sg.Q6_K, 12288, (3102,), 60), (sg.Q8_0, 8192, (3840,), 100),
+                                            (sg.Q4_K, 8192, (1000, 1000, 1072), 100), (sg.Q4_0, 8192, (1024, 1024, 1024), 0)],
+                         ids=["q6_k_row_tail_scalar_y", "q8_0_token_tail", "q4_k_multi_per_weight_tiles", "q4_0_multi_packed"])
+def test_prefill_wide_stream_k(hip, dtype, K, Ms, pad):
+    """The wide GEMM's stream-K form: fewer 384-row tiles than CUs, each CU an equal run of 2-stage
+    units over all tiles (a tile shared by several CUs is added from its partial slots in CU order
+    by a reduce pass). A row tail with rows not a multiple of 4 (the reduce's scalar stores), a
+    part-empty token tile, a MUL_MAT_MULTI whose weights own their row tiles (more tiles than all
+    rows together need) and one run end to end; two launches bit-identical."""
+    dev, st = hip
+    M = sum(Ms)
+    # (3072 rows: one token tile more than the minimum, where 192-row tiles would fill the CUs)
+    N = sk_tokens(dev, (M + 383) // 384, K // 128, pad, extra=1 if M == 3072 else 0)
+    ys, refs, form, grid = _sk_run(dev, st, dtype, K, Ms, N, 960 + len(Ms))
+    assert form.startswith("gemm wide stream-k"), form
+    assert grid == dev.info().compute_units, (form, grid)
+    for M, a, b, ref in zip(Ms, ys[0], ys[1], refs):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{M} rows: launches differ"
+        e = nmse(a, ref)
+        assert e <= 5e-5, f"{sg.NAMES[dtype]} {M}x{K} N={N}: NMSE {e:.3e} [{form}]"
+
+
 def test_prefill_wide_multi_tiles_across_weights(hip):
     """A prefill MUL_MAT_MULTI on the wide GEMM: 3 weights of 1024 rows (32-row multiples), the
     384-row tiles running across their boundaries, each wave taking the weight its rows are in."""
