@@ -1478,6 +1478,10 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
                 c.kg = 1;
                 return c;
             }
+            if (env_kg != 1 && (a.M % 192 == 0 || a.M >= 8 * 192) && fill((a.M + 191) / 192 * ntw) && stages >= 16 && (2 * gsz2 - stages) * 8 <= stages) {
+                c.kg = 2;
+                return c;
+            }
             static const int env_ws = env_int("SCRAPGPU_HIP_MM_WSPLIT", 0);
             if (env_ws > 1) {
                 c.kg = env_kg == 2 ? 2 : 1;
@@ -1498,10 +1502,18 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
                 c.sk = true;
                 return c;
             }
-            if (env_kg != 1 && (a.M % 192 == 0 || a.M >= 8 * 192) && fill((a.M + 191) / 192 * ntw) && stages >= 16 && (2 * gsz2 - stages) * 8 <= stages) {
-                c.kg = 2;
-                return c;
-            }
+            // ... else K split over work-groups of 384-row tiles when that occupies 3/4 of the CUs
+            // or more in one round with >= 16 stages per split (the largest such split; partials
+            // added by k_split_reduce). (4096x12288 at 512 tokens: 5 splits, 88 against 95 us per
+            // op with the 64-token form's 3 K groups; 6144x4096 at 2 splits on half the CUs lost,
+            // 60 against 51)
+            if (env_kg != 2 && slices == 1 && (a.M % 384 == 0 || a.M >= 8 * 384))
+                for (int sp = 8; sp >= 2; --sp)
+                    if (tw * sp <= cu_count && 4 * tw * sp >= 3 * cu_count && stages / sp >= 16) {
+                        c.kg = 1;
+                        c.split = sp;
+                        return c;
+                    }
             c.bn = 64;
             c.wide = false;
         }
