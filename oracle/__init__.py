@@ -19,11 +19,12 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libscrapgpu_ref.so")
 
-F32, I32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 16, 17, 32, 33
+F32, F16, I32, BF16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 5, 16, 17, 32, 33
 QTYPES = (Q4_0, Q8_0, Q4_K, Q6_K)
-NAMES = {F32: "f32", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
-BLOCK = {F32: 1, Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
-TYPE_SIZE = {F32: 4, Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}
+FTYPES = (F32, F16, BF16)
+NAMES = {F32: "f32", F16: "f16", BF16: "bf16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+BLOCK = {F32: 1, F16: 1, BF16: 1, Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
+TYPE_SIZE = {F32: 4, F16: 2, BF16: 2, Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}
 
 
 def build(ref: bool = False) -> None:
@@ -70,6 +71,19 @@ def _p(a: np.ndarray) -> int:
 
 def row_bytes(dtype: int, K: int) -> int:
     return K // BLOCK[dtype] * TYPE_SIZE[dtype]
+
+
+def float_to_bf16(x: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns of float32 x, rounded to nearest even (NaNs kept quiet), as the
+    reference's st_bf16 (src/core/ref/ops.cpp:43-52)."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (b & 0x7FFFFFFF) > 0x7F800000
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) & 0xFFFF
+    return np.where(nan, (b >> 16) | 0x40, r).astype(np.uint16)
+
+
+def bf16_to_float(h: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
 def half_to_float(h: np.ndarray) -> np.ndarray:
@@ -136,10 +150,11 @@ def _tensor(dtype: int, arr: np.ndarray, ne, nb) -> SgoTensor:
 
 def mul_mat(dtype: int, w: np.ndarray, K: int, M: int, x: np.ndarray, threads: int = 1) -> np.ndarray:
     """y[n, m] = sum_k W[m, k] x[n, k] for one contiguous slice: w holds M rows of natural blocks
-    (or float32 [M, K] for F32), x is float32 [N, K]. Returns float32 [N, M]."""
+    (float rows: float32 [M, K] for F32, the uint16 bit patterns [M, K] for F16 and BF16), x is
+    float32 [N, K]. Returns float32 [N, M]."""
     x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, K)
     N = x.shape[0]
-    rb = row_bytes(dtype, K) if dtype != F32 else 4 * K
+    rb = row_bytes(dtype, K)
     w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
     assert w.size == rb * M, (w.size, rb, M)
     y = np.zeros((N, M), np.float32)
@@ -160,7 +175,7 @@ def mul_mat_id(dtype: int, w: np.ndarray, K: int, M: int, E: int, x: np.ndarray,
     T, nu = ids.shape
     x = np.ascontiguousarray(x, dtype=np.float32).reshape(T, -1, K)
     n1 = x.shape[1]
-    rb = row_bytes(dtype, K) if dtype != F32 else 4 * K
+    rb = row_bytes(dtype, K)
     w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
     assert w.size == rb * M * E
     y = np.zeros((T, nu, M), np.float32)
@@ -178,7 +193,7 @@ def get_rows(dtype: int, w: np.ndarray, K: int, R: int, ids: np.ndarray) -> np.n
     """GET_ROWS of one slice: w holds R rows of natural blocks, ids int32 [n]. Returns float32 [n, K]."""
     ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
     n = ids.size
-    rb = row_bytes(dtype, K) if dtype != F32 else 4 * K
+    rb = row_bytes(dtype, K)
     w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
     y = np.zeros((n, K), np.float32)
     tw = _tensor(dtype, w, (K, R, 1, 1), (TYPE_SIZE[dtype], rb, rb * R, rb * R))
@@ -296,7 +311,7 @@ def ref_mul_mat(dtype: int, w: np.ndarray, K: int, M: int, x: np.ndarray) -> np.
     x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, K)
     N = x.shape[0]
     w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
-    rb = row_bytes(dtype, K) if dtype != F32 else 4 * K
+    rb = row_bytes(dtype, K)
     y = np.zeros((N, M), np.float32)
     ins = (_RefTensorDesc * 2)()
     outs = (_RefTensorDesc * 1)()
@@ -347,7 +362,7 @@ def ref_mul_mat_id(dtype: int, w: np.ndarray, K: int, M: int, E: int, x: np.ndar
     T, nu = ids.shape
     x = np.ascontiguousarray(x, dtype=np.float32).reshape(T, -1, K)
     n1 = x.shape[1]
-    rb = row_bytes(dtype, K) if dtype != F32 else 4 * K
+    rb = row_bytes(dtype, K)
     w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
     y = np.zeros((T, nu, M), np.float32)
     ins = (_RefTensorDesc * 3)()
@@ -368,7 +383,7 @@ def ref_get_rows(dtype: int, w: np.ndarray, K: int, R: int, ids: np.ndarray):
     """scrapgpu_ref_execute(GET_ROWS) of the reference on one slice. Returns (status, y [n, K])."""
     ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
     n = ids.size
-    rb = row_bytes(dtype, K) if dtype != F32 else 4 * K
+    rb = row_bytes(dtype, K)
     w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
     y = np.zeros((n, K), np.float32)
     ins = (_RefTensorDesc * 2)()

@@ -115,7 +115,9 @@ void sgo_float_to_half_n(const float * src, uint16_t * dst, int64_t n) {
 
 size_t sgo_block_size(int32_t dtype) {
     switch (dtype) {
-        case SGO_F32: return 1;
+        case SGO_F32:
+        case SGO_F16:
+        case SGO_BF16: return 1;
         case SGO_Q4_0:
         case SGO_Q8_0: return 32;
         case SGO_Q4_K:
@@ -127,6 +129,8 @@ size_t sgo_block_size(int32_t dtype) {
 size_t sgo_type_size(int32_t dtype) {
     switch (dtype) {
         case SGO_F32: return 4;
+        case SGO_F16:
+        case SGO_BF16: return 2;
         case SGO_Q4_0: return 18;
         case SGO_Q8_0: return 34;
         case SGO_Q4_K: return 144;
@@ -536,9 +540,22 @@ static int64_t dim(const sgo_tensor * t, int i) {
     return t->ne[i] > 0 ? t->ne[i] : 1;
 }
 
+/* a row of src0 as floats (ops.cpp:258-269 with load_float, ops.cpp:32-41,78-93): F16 through
+ * half_to_float, BF16 as the high half of an f32, quantized rows dequantized */
 static void load_row(const sgo_tensor * w, const uint8_t * p, int64_t K, float * row) {
     if (w->dtype == SGO_F32) {
         memcpy(row, p, (size_t) K * 4);
+    } else if (w->dtype == SGO_F16 || w->dtype == SGO_BF16) {
+        for (int64_t k = 0; k < K; ++k) {
+            uint16_t h;
+            memcpy(&h, p + 2 * k, 2);
+            if (w->dtype == SGO_F16) {
+                row[k] = sgo_half_to_float(h);
+            } else {
+                const uint32_t bits = (uint32_t) h << 16;
+                memcpy(&row[k], &bits, 4);
+            }
+        }
     } else {
         sgo_dequantize(w->dtype, p, row, K);
     }
@@ -627,7 +644,7 @@ static void * mm_run(void * arg) {
 static int mm_check(const sgo_tensor * w, const sgo_tensor * x, const sgo_tensor * y, int allow_broadcast, int64_t * r2, int64_t * r3) {
     if (w == NULL || x == NULL || y == NULL || w->data == NULL || x->data == NULL || y->data == NULL) return SGO_INVALID;
     if (x->dtype != SGO_F32 || y->dtype != SGO_F32) return SGO_UNSUPPORTED;
-    if (w->dtype != SGO_F32 && !is_quant(w->dtype)) return SGO_UNSUPPORTED;
+    if (w->dtype != SGO_F32 && w->dtype != SGO_F16 && w->dtype != SGO_BF16 && !is_quant(w->dtype)) return SGO_UNSUPPORTED;
     if (w->nb[0] != sgo_type_size(w->dtype)) return SGO_UNSUPPORTED;
     if (is_quant(w->dtype) && dim(w, 0) % (int64_t) sgo_block_size(w->dtype) != 0) return SGO_UNSUPPORTED;
     if (dim(w, 0) != dim(x, 0)) return SGO_INVALID;
@@ -688,7 +705,7 @@ static int ids_i32(const sgo_tensor * ids, int64_t i, int64_t t, int32_t * e) {
 int sgo_mul_mat_id(const sgo_tensor * w, const sgo_tensor * x, const sgo_tensor * ids, sgo_tensor * y) {
     if (w == NULL || x == NULL || ids == NULL || y == NULL || w->data == NULL || x->data == NULL || ids->data == NULL || y->data == NULL) return SGO_INVALID;
     if (x->dtype != SGO_F32 || y->dtype != SGO_F32 || ids->dtype != SGO_I32) return SGO_UNSUPPORTED;
-    if (w->dtype != SGO_F32 && !is_quant(w->dtype)) return SGO_UNSUPPORTED;
+    if (w->dtype != SGO_F32 && w->dtype != SGO_F16 && !is_quant(w->dtype)) return SGO_UNSUPPORTED;
     if (w->nb[0] != sgo_type_size(w->dtype)) return SGO_UNSUPPORTED;
     if (dim(w, 3) != 1 || dim(x, 3) != 1 || dim(ids, 2) != 1 || dim(ids, 3) != 1) return SGO_INVALID;
     if (dim(w, 0) != dim(x, 0) || (dim(x, 1) != 1 && dim(x, 1) != dim(ids, 0)) || dim(x, 2) != dim(ids, 1) ||
@@ -730,7 +747,7 @@ int sgo_mul_mat_id(const sgo_tensor * w, const sgo_tensor * x, const sgo_tensor 
 int sgo_get_rows(const sgo_tensor * w, const sgo_tensor * ids, sgo_tensor * y) {
     if (w == NULL || ids == NULL || y == NULL || w->data == NULL || ids->data == NULL || y->data == NULL) return SGO_INVALID;
     if (ids->dtype != SGO_I32 || y->dtype != SGO_F32) return SGO_UNSUPPORTED;
-    if (w->dtype != SGO_F32 && !is_quant(w->dtype)) return SGO_UNSUPPORTED;
+    if (w->dtype != SGO_F32 && w->dtype != SGO_F16 && !is_quant(w->dtype)) return SGO_UNSUPPORTED;
     if (w->nb[0] != sgo_type_size(w->dtype)) return SGO_UNSUPPORTED;
     if (dim(ids, 3) != 1 || dim(ids, 1) > dim(w, 2) || dim(ids, 2) > dim(w, 3) || dim(y, 0) != dim(w, 0) || dim(y, 1) != dim(ids, 0) ||
         dim(y, 2) != dim(ids, 1) || dim(y, 3) != dim(ids, 2)) {

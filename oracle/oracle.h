@@ -1,13 +1,15 @@
 /* CPU oracle for the quantized MUL_MAT path -- TEST INFRASTRUCTURE ONLY.
  *
  * A plain-C restatement of the reference's CPU implementation (src/core/ref/f16.cpp,
- * src/core/ref/quant.cpp, src/core/ref/ops.cpp:258-269,690-721,802-1024) and of the R32 host pack/unpack
+ * src/core/ref/quant.cpp, src/core/ref/ops.cpp:32-41,78-93,258-269,690-721,802-1024) and of the R32 host pack/unpack
  * (src/backends/opencl11/r32.h:35-90, src/tensor/tensor.cpp:5-19). It is the checker of the GPU
  * path and the CPU baseline that bench.py times; only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py load it. The product library never links or calls it.
  *
  * Status codes follow scrapgpu_status: 0 OK, 1 UNSUPPORTED, 2 INVALID_ARGUMENT. dtype values are
- * the scrapgpu_dtype enum values (F32 = 0, Q4_0 = 16, Q8_0 = 17, Q4_K = 32, Q6_K = 33).
+ * the scrapgpu_dtype enum values (F32 = 0, F16 = 1, BF16 = 5, Q4_0 = 16, Q8_0 = 17, Q4_K = 32,
+ * Q6_K = 33). Float weights (F32, F16, BF16; MUL_MAT_ID and GET_ROWS: F32, F16) are read as the
+ * reference's load_float reads them.
  *
  * Pinning (what checks each function; see tests/test_oracle.py):
  *   half<->float         exhaustive half->float vs numpy; float->half RNE vs numpy on all
@@ -16,9 +18,9 @@
  *                        produced by the reference compiled from source (tests/golden/)
  *   quantize_*           golden vectors from the compiled reference + round-trip bounds
  *                        (ref_quant_tests.cpp:112-158) + the cpu_bench checksums
- *   mul_mat              golden vectors, the increasing-K cancellation case
- *                        (ref_ops_tests.cpp:754-771), fp64 brute force on small shapes, cpu_bench
- *                        checksums (tools/cpu_bench.cpp)
+ *   mul_mat              golden vectors (every weight dtype, float ones included), the
+ *                        increasing-K cancellation case (ref_ops_tests.cpp:754-771), fp64 brute
+ *                        force on small shapes, cpu_bench checksums (tools/cpu_bench.cpp)
  *   r32 pack/unpack      hand-checked layouts (r32_tests.cpp:104-181), pack/unpack identity,
  *                        golden vectors from the reference pack
  *   mul_mat_id           golden vectors from the compiled reference (scrapgpu_ref_execute), and
@@ -38,7 +40,9 @@ extern "C" {
 
 enum {
     SGO_F32 = 0,
+    SGO_F16 = 1,
     SGO_I32 = 2,
+    SGO_BF16 = 5,
     SGO_Q4_0 = 16,
     SGO_Q8_0 = 17,
     SGO_Q4_K = 32,

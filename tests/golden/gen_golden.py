@@ -107,7 +107,50 @@ def moe_getrows():
         out[f"{name}_gr_y"] = g
     np.savez_compressed(os.path.join(OUT, "mul_mat_id_get_rows.npz"), **out)
     print("wrote", len(out), "arrays")
+    float_weights()
+
+
+def float_weights():
+    """MUL_MAT with F32 / F16 / BF16 weights (the scalar N < 4 path, the F32 4-row panel with a
+    ragged last panel, the column panels), and MUL_MAT_ID / GET_ROWS with F16 weights, through
+    scrapgpu_ref_execute. Weights include values outside F16's normal range (subnormal, large)."""
+    rng = np.random.default_rng(20261203)
+    out = {}
+    K = 72
+    for dt in O.FTYPES:
+        name = O.NAMES[dt]
+        for M, N in ((24, 1), (23, 3), (37, 7), (37, 17)):
+            wf = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+            wf[0, :4] = (3e-6, -2e-7, 900.0, -1500.0)
+            w = wf if dt == O.F32 else O.float_to_half(wf) if dt == O.F16 else O.float_to_bf16(wf)
+            xx = rng.standard_normal((N, K)).astype(np.float32)
+            out[f"{name}_mm_K{K}_M{M}_N{N}_w"] = w
+            out[f"{name}_mm_K{K}_M{M}_N{N}_x"] = xx
+            out[f"{name}_mm_K{K}_M{M}_N{N}_y"] = O.ref_mul_mat(dt, w, K, M, xx)
+    M, E, T, nu = 40, 5, 3, 2
+    w = O.float_to_half((rng.standard_normal(K * M * E) * 0.02).astype(np.float32))
+    ids = rng.integers(0, E, (T, nu)).astype(np.int32)
+    out["f16_mid_w"] = w
+    out["f16_mid_ids"] = ids
+    x = rng.standard_normal((T, nu, K)).astype(np.float32)
+    st, y = O.ref_mul_mat_id(O.F16, w, K, M, E, x, ids)
+    assert st == 0, st
+    out["f16_mid_x"] = x
+    out["f16_mid_y"] = y
+    R = 37
+    wr = O.float_to_half(rng.standard_normal(K * R).astype(np.float32))
+    rid = np.array([0, R - 1, 5, 5, 12, 30], np.int32)
+    st, g = O.ref_get_rows(O.F16, wr, K, R, rid)
+    assert st == 0, st
+    out["f16_gr_w"] = wr
+    out["f16_gr_ids"] = rid
+    out["f16_gr_y"] = g
+    np.savez_compressed(os.path.join(OUT, "float_weights.npz"), **out)
+    print("wrote", len(out), "arrays")
 
 
 if __name__ == "__main__":
-    main()
+    if len(sys.argv) > 1 and sys.argv[1] == "float":
+        float_weights()
+    else:
+        main()

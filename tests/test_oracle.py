@@ -111,6 +111,67 @@ def test_golden_get_rows(gold_id, dt):
         O.get_rows(dt, w, K, R, np.array([R], np.int32))
 
 
+# float weights (F32 / F16 / BF16): golden vectors of the reference, and independent checks: the
+# conversion against numpy's (F16) and the exact high-half rule (BF16), the product against an fp64
+# dot of the converted weights
+
+GOLD_F = os.path.join(os.path.dirname(__file__), "golden", "float_weights.npz")
+
+
+@pytest.fixture(scope="module")
+def gold_f():
+    return np.load(GOLD_F)
+
+
+def _as_float(dt, w):
+    if dt == O.F32:
+        return np.asarray(w, np.float32)
+    if dt == O.F16:
+        return np.asarray(w, np.uint16).view(np.float16).astype(np.float32)
+    return O.bf16_to_float(w)
+
+
+@pytest.mark.parametrize("dt", O.FTYPES, ids=lambda d: O.NAMES[d])
+def test_golden_float_mul_mat(gold_f, dt):
+    n = O.NAMES[dt]
+    K = 72
+    for M, N in ((24, 1), (23, 3), (37, 7), (37, 17)):
+        k = f"{n}_mm_K{K}_M{M}_N{N}"
+        w, x, y = gold_f[k + "_w"], gold_f[k + "_x"], gold_f[k + "_y"]
+        got = O.mul_mat(dt, w, K, M, x)
+        assert np.array_equal(got.view(np.uint32), y.view(np.uint32)), k
+        wf = _as_float(dt, w).reshape(M, K).astype(np.float64)
+        ref = x.astype(np.float64) @ wf.T
+        bound = 2.0 * K * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(wf).T) + 1e-30
+        assert np.all(np.abs(got - ref) <= bound), k
+
+
+def test_float_weights_conversion():
+    """bf16: the high half of the f32 bits, rounding to nearest even with ties; f16 rows through the
+    oracle's half_to_float equal numpy's float16."""
+    v = np.array([1.0, -2.5, 1.00390625, 1.005859375, 3e-39, 65504.0, np.inf, -0.0], np.float32)
+    b = O.float_to_bf16(v)
+    assert b.tolist() == [0x3F80, 0xC020, 0x3F80, 0x3F81, 0x0021, 0x4780, 0x7F80, 0x8000]
+    w = np.arange(-300, 300, dtype=np.float32) * 0.37
+    hb = w.astype(np.float16).view(np.uint16)
+    one = np.ones((1, w.size), np.float32)
+    y = O.mul_mat(O.F16, hb, w.size, 1, one)
+    # (the increasing-k float sum: cumsum adds in order, np.sum would pair)
+    assert y[0, 0] == np.cumsum(w.astype(np.float16).astype(np.float32), dtype=np.float32)[-1]
+
+
+def test_golden_float_mul_mat_id_get_rows(gold_f):
+    K, M, E = 72, 40, 5
+    w, ids, x, y = gold_f["f16_mid_w"], gold_f["f16_mid_ids"], gold_f["f16_mid_x"], gold_f["f16_mid_y"]
+    got = O.mul_mat_id(O.F16, w, K, M, E, x, ids)
+    assert np.array_equal(got.view(np.uint32), y.view(np.uint32))
+    R = 37
+    wr, rid, g = gold_f["f16_gr_w"], gold_f["f16_gr_ids"], gold_f["f16_gr_y"]
+    got = O.get_rows(O.F16, wr, K, R, rid)
+    assert np.array_equal(got.view(np.uint32), g.view(np.uint32))
+    assert np.array_equal(got, wr.reshape(R, K).view(np.float16).astype(np.float32)[rid])
+
+
 # ---------------------------------------------------------------------------------------------
 # the reference's known-answer tests
 # ---------------------------------------------------------------------------------------------
