@@ -30,6 +30,7 @@ SOURCES = [
     ("core/tensor.cpp", []),
     ("hip/backend.cpp", ["-x", "hip"] + DEVICE),
     ("hip/matvec.hip", DEVICE),
+    ("hip/matvec_float.hip", DEVICE),
     ("hip/matmul.hip", DEVICE),
     # bit-exact conversions: one IEEE operation per source operation
     ("hip/quant.hip", DEVICE + ["-ffp-contract=off"]),

@@ -560,13 +560,24 @@ scrapgpu_status api_tensor_download(scrapgpu_stream_t * stream, const scrapgpu_t
 // the support rule of one product W x -> y; fills `a` (pointers left null) when supported
 scrapgpu_status mul_mat_rule(const scrapgpu_tensor_desc & w, const scrapgpu_tensor_desc & x, const scrapgpu_tensor_desc & y, int allow_broadcast,
                              sgk::MatArgs * a, const char ** reason) {
-    if (!sg::is_quant(w.dtype)) {
-        return unsupported("the hip backend implements MUL_MAT for Q4_0 / Q8_0 / Q4_K / Q6_K weights only", reason);
+    const bool fw = w.dtype == SCRAPGPU_DTYPE_F32 || w.dtype == SCRAPGPU_DTYPE_F16 || w.dtype == SCRAPGPU_DTYPE_BF16;
+    if (!sg::is_quant(w.dtype) && !fw) {
+        return unsupported("the hip backend implements MUL_MAT for Q4_0 / Q8_0 / Q4_K / Q6_K, F32, F16 and BF16 weights", reason);
     }
-    if (w.layout != SCRAPGPU_LAYOUT_R32) {
-        return unsupported("quantized weights run from the R32 layout only: upload them with layout R32 (the upload repacks natural blocks)", reason);
+    if (fw) {
+        // float weights (the reference's exec_mul_mat reads them with load_float): natural rows
+        if (w.layout != SCRAPGPU_LAYOUT_NATURAL) return unsupported("float weights run from the natural layout", reason);
+        if (w.nb[0] != sg::type_size(w.dtype)) return unsupported("MUL_MAT needs contiguous rows of src0 (nb0 == element size)", reason);
+        if (sg::dim1(w.ne[0]) % 8 != 0) return unsupported("float weights: the hip kernels read rows in runs of 8 elements, so K must be a multiple of 8", reason);
+        if (w.nb[1] % 16 != 0 || w.nb[2] % 16 != 0 || w.nb[3] % 16 != 0 || w.offset % 16 != 0) {
+            return unsupported("float weights: rows and slices must start on 16-byte boundaries", reason);
+        }
+    } else {
+        if (w.layout != SCRAPGPU_LAYOUT_R32) {
+            return unsupported("quantized weights run from the R32 layout only: upload them with layout R32 (the upload repacks natural blocks)", reason);
+        }
+        if (!sg::r32_eligible(w)) return unsupported("src0 is not R32-eligible (contiguous, whole blocks per row, 16-byte slice strides)", reason);
     }
-    if (!sg::r32_eligible(w)) return unsupported("src0 is not R32-eligible (contiguous, whole blocks per row, 16-byte slice strides)", reason);
     if (x.dtype != SCRAPGPU_DTYPE_F32 || y.dtype != SCRAPGPU_DTYPE_F32 || x.layout != SCRAPGPU_LAYOUT_NATURAL || y.layout != SCRAPGPU_LAYOUT_NATURAL) {
         return unsupported("MUL_MAT expects an F32 natural-layout src1 and destination", reason);
     }
@@ -593,9 +604,10 @@ scrapgpu_status mul_mat_rule(const scrapgpu_tensor_desc & w, const scrapgpu_tens
     }
     if (x2 * x3 > 65535) return unsupported("MUL_MAT: more than 65535 slices", reason);
     // the kernels address one slice of weights, and one slice of x in f16, with 32-bit offsets
-    if (sg::sat_mul(sg::row_size(w.dtype, K), (uint64_t) M) >= ((uint64_t) 1 << 32)) {
+    if (sg::sat_mul(fw ? std::max<uint64_t>(w.nb[1], sg::row_size(w.dtype, K)) : sg::row_size(w.dtype, K), (uint64_t) M) >= ((uint64_t) 1 << 32)) {
         return unsupported("MUL_MAT: one slice of src0 must be smaller than 4 GiB", reason);
     }
+    if (fw && sg::dim1(x.ne[1]) > 8) return unsupported("float weights: the hip backend runs them for up to 8 columns of src1", reason);
     if (sg::sat_mul((uint64_t) K, (uint64_t) sg::dim1(x.ne[1])) >= ((uint64_t) 1 << 31)) {
         return unsupported("MUL_MAT: one slice of src1 must hold fewer than 2^31 elements", reason);
     }
@@ -603,7 +615,7 @@ scrapgpu_status mul_mat_rule(const scrapgpu_tensor_desc & w, const scrapgpu_tens
         a->dtype = w.dtype;
         a->M = M;
         a->K = K;
-        a->nb = K / (int64_t) sg::block_size(w.dtype);
+        a->nb = fw ? (int64_t) w.nb[1] : K / (int64_t) sg::block_size(w.dtype); // (float weights: the row stride in bytes)
         a->w_s2 = w.nb[2];
         a->w_s3 = w.nb[3];
         a->x_s1 = (int64_t) (x.nb[1] / 4);

@@ -8,7 +8,7 @@
 
 namespace sgk {
 
-enum : int { F32 = 0, Q4_0 = 16, Q8_0 = 17, Q4_K = 32, Q6_K = 33 };
+enum : int { F32 = 0, F16 = 1, BF16 = 5, Q4_0 = 16, Q8_0 = 17, Q4_K = 32, Q6_K = 33 };
 
 // The form the calling thread's last matvec / matmul launch chose ("burst rg=3 W=4 spw=2", ...)
 // and its work-group count: a diagnostic that lets tests pin the kernel a shape selects.
@@ -27,9 +27,10 @@ struct Areas {
 };
 Areas areas_of(int dtype);
 
-// Quantized matrix product y[n, m] = sum_k W[m, k] x[n, k] over R32 weights.
-// W: slices of M rows, nb blocks each; slice (i2/r2, i3/r3) starts at w + i2w * w_s2 + i3w * w_s3
-// (bytes). x / y: float element strides (s1 between columns, s2 / s3 between slices).
+// Matrix product y[n, m] = sum_k W[m, k] x[n, k] over R32 quantized weights or natural-layout
+// float weights (F32 / F16 / BF16). W: slices of M rows, nb blocks each (quantized) or rows nb
+// bytes apart (float); slice (i2/r2, i3/r3) starts at w + i2w * w_s2 + i3w * w_s3 (bytes). x / y:
+// float element strides (s1 between columns, s2 / s3 between slices).
 struct MatArgs {
     int dtype;
     const uint8_t * w;
@@ -69,6 +70,10 @@ struct IdArgs {
 // left at zero by every launch (the last chunk of a row tile resets its count); launches that
 // share them must not overlap. Without scratch or counters the one-work-group-per-tile form runs.
 constexpr int64_t kArriveMax = 65536;
+bool is_float_weight(int dtype);
+// float weights, 1 <= N <= 8 (launch_matvec calls it for them): exact f32 products, K a multiple of
+// 8, rows and slices 16-byte aligned; no scratch
+hipError_t launch_matvec_float(const MatArgs * mats, int nmat, hipStream_t stream, const char ** kernel_name, uint64_t * grid_size);
 size_t matvec_scratch_bytes(const MatArgs * mats, int nmat, const IdArgs * id = nullptr);
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
                          uint64_t * grid_size, const IdArgs * id = nullptr, uint8_t * scratch = nullptr, uint32_t * arrive = nullptr);

@@ -1520,6 +1520,7 @@ static size_t chunk_part_bytes(const MatArgs * mats, int nmat) {
 }
 
 size_t matvec_scratch_bytes(const MatArgs * mats, int nmat, const IdArgs * id) {
+    if (nmat >= 1 && is_float_weight(mats[0].dtype)) return 0;
     if (nmat >= 1 && chunk_form(mats, nmat, id)) return chunk_part_bytes(mats, nmat);
     if (nmat < 1 || !mc_form(mats, nmat, id)) return 0;
     const int64_t nst = (mats[0].K + kStep - 1) / kStep, nchunks = (nst + kMcChunk - 1) / kMcChunk, nsegp = nchunks * kMcChunk * kSegs;
@@ -1535,6 +1536,7 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
                          uint64_t * grid_size, const IdArgs * id, uint8_t * scratch, uint32_t * arrive) {
     if (nmat < 1 || nmat > 3) return hipErrorInvalidValue;
     const MatArgs & a = mats[0];
+    if (is_float_weight(a.dtype)) return id == nullptr ? launch_matvec_float(mats, nmat, stream, kernel_name, grid_size) : hipErrorInvalidValue;
     for (int j = 0; j < nmat; ++j) {
         if (mats[j].dtype != a.dtype || mats[j].K != a.K || mats[j].N != a.N || (nmat > 1 && mats[j].ne12 * mats[j].ne13 != 1)) {
             return hipErrorInvalidValue;

@@ -1,0 +1,180 @@
+"""MUL_MAT with float weights (F32 / F16 / BF16 rows in the natural layout) through the C-ABI,
+against the oracle (the reference's exec_mul_mat restated, pinned by its golden vectors) and the
+reference's golden vectors themselves. 1..8 columns run exact f32 products (the decode gate:
+NMSE <= 1e-7 and max-abs <= 1e-4 ||x||_2 max|w|)."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+import scrapgpulibrary_amd as sg
+from tests.gpu_util import check_matvec, nmse
+
+pytestmark = pytest.mark.gpu
+
+FT = (sg.F32, sg.F16, sg.BF16)
+IDS = {sg.F32: "f32", sg.F16: "f16", sg.BF16: "bf16"}
+
+
+def float_weights(dtype, M, K, seed, std=0.02):
+    """(bytes as stored, the weights as f32) of M rows of K."""
+    w = O.normal(M * K, seed, 0.0, std).reshape(M, K)
+    if dtype == sg.F32:
+        return w, w
+    if dtype == sg.F16:
+        h = w.astype(np.float16)
+        return h.view(np.uint16), h.astype(np.float32)
+    b = O.float_to_bf16(w)
+    return b, O.bf16_to_float(b).reshape(M, K)
+
+
+def run(dev, st, dtype, wbytes, K, M, x, row_stride=None, x_offset=0, check_form=True):
+    """y [N, M] = W x, W uploaded with rows `row_stride` bytes apart (default: packed)."""
+    N = x.shape[0]
+    esz = sg.TYPE_SIZE[dtype]
+    rs = row_stride or K * esz
+    img = np.zeros((M, rs), np.uint8)
+    img[:, :K * esz] = np.ascontiguousarray(wbytes).view(np.uint8).reshape(M, K * esz)
+    wb = dev.alloc(img.nbytes)
+    st.write(wb, 0, img)
+    wt = sg.tdesc(dtype, (K, M), wb, nb=[esz, rs, rs * M, rs * M])
+    xb = dev.alloc(x.nbytes + x_offset)
+    xt = sg.tdesc(sg.F32, (K, N), xb, offset=x_offset)
+    st.write(xb, x_offset, np.ascontiguousarray(x, np.float32))
+    yb = dev.alloc(4 * M * N)
+    yt = sg.tdesc(sg.F32, (M, N), yb)
+    op, keep = sg.mul_mat_op(wt, xt, yt)
+    st.execute(op)
+    st.sync()
+    form, grid = sg.last_launch()
+    if check_form:
+        ncp = 1 if N == 1 else 2 if N == 2 else 4 if N <= 4 else 8
+        assert form == f"float rows=8 nc={ncp}", form
+        assert grid == (M + 7) // 8, (form, grid)
+    y = st.download(yt).reshape(N, M).copy()
+    for b in (wb, xb, yb):
+        b.free()
+    return y
+
+
+@pytest.mark.parametrize("dtype", FT, ids=lambda d: IDS[d])
+@pytest.mark.parametrize("K,M,N", [(4096, 1000, 1), (4096, 256, 2), (520, 77, 3), (4096, 512, 4), (1536, 333, 5), (12288, 264, 8)])
+def test_float_decode(hip, dtype, K, M, N):
+    """Every dtype at 1..8 columns: a row tail (M not a multiple of 8), K not a multiple of the
+    512-element step (520, 1536 over 4 waves), a long K."""
+    dev, st = hip
+    wbytes, wf = float_weights(dtype, M, K, 7000 + K + M)
+    x = O.normal(N * K, 7001 + N).reshape(N, K)
+    y = run(dev, st, dtype, wbytes, K, M, x)
+    ref = O.mul_mat(dtype, wbytes, K, M, x, threads=8)
+    e = check_matvec(y, ref, x, wf)
+    assert e <= 1e-10, f"NMSE {e:.3e}"
+
+
+@pytest.mark.parametrize("dtype", FT, ids=lambda d: IDS[d])
+def test_float_golden(hip, dtype):
+    """The reference's own outputs (tests/golden/float_weights.npz, scrapgpu_ref_execute) at 1, 3 and
+    7 columns, with weights outside F16's normal range (subnormal, hundreds)."""
+    dev, st = hip
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "float_weights.npz"))
+    n = IDS[dtype]
+    for M, N in ((24, 1), (23, 3), (37, 7)):
+        k = f"{n}_mm_K72_M{M}_N{N}"
+        w, x, yref = g[k + "_w"], g[k + "_x"], g[k + "_y"]
+        y = run(dev, st, dtype, w, 72, M, x)
+        assert np.allclose(y, yref, rtol=1e-5, atol=1e-5 * float(np.max(np.abs(yref)))), k
+        assert nmse(y, yref) <= 1e-12, k
+
+
+@pytest.mark.parametrize("dtype", FT, ids=lambda d: IDS[d])
+def test_float_padded_rows_and_unaligned_x(hip, dtype):
+    """Rows 48 bytes longer than K elements (the row stride is honoured), x 4 bytes past a 16-byte
+    boundary (the scalar x loads)."""
+    dev, st = hip
+    K, M, N = 1024, 100, 3
+    wbytes, wf = float_weights(dtype, M, K, 7100)
+    x = O.normal(N * K, 7101).reshape(N, K)
+    rs = K * sg.TYPE_SIZE[dtype] + 48
+    y = run(dev, st, dtype, wbytes, K, M, x, row_stride=rs, x_offset=4)
+    ref = O.mul_mat(dtype, wbytes, K, M, x, threads=8)
+    check_matvec(y, ref, x, wf)
+
+
+def test_float_slices_broadcast(hip):
+    """F16 weights of 2 slices under x of 4 slices (allow_broadcast): slice i of x uses weight slice
+    i // 2."""
+    dev, st = hip
+    K, M, N, S, SW = 512, 40, 2, 4, 2
+    ws = [float_weights(sg.F16, M, K, 7200 + i) for i in range(SW)]
+    img = np.concatenate([w[0].reshape(-1) for w in ws]).view(np.uint8)
+    wb = dev.alloc(img.nbytes)
+    st.write(wb, 0, img)
+    rb = 2 * K
+    wt = sg.tdesc(sg.F16, (K, M, SW), wb, nb=[2, rb, rb * M, rb * M * SW])
+    x = O.normal(S * N * K, 7201).reshape(S, N, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N, S), xb)
+    st.write(xb, 0, x)
+    yb = dev.alloc(4 * M * N * S)
+    yt = sg.tdesc(sg.F32, (M, N, S), yb)
+    op, keep = sg.mul_mat_op(wt, xt, yt, allow_broadcast=1)
+    st.execute(op)
+    st.sync()
+    y = st.download(yt).reshape(S, N, M)
+    for i in range(S):
+        wbytes, wf = ws[i // (S // SW)]
+        ref = O.mul_mat(sg.F16, wbytes, K, M, x[i])
+        check_matvec(y[i], ref, x[i], wf)
+    for b in (wb, xb, yb):
+        b.free()
+
+
+@pytest.mark.parametrize("dtype", FT, ids=lambda d: IDS[d])
+def test_float_multi(hip, dtype):
+    """MUL_MAT_MULTI of three float weights sharing x (q / k / v shapes at 2 columns): one launch
+    over all their rows."""
+    dev, st = hip
+    K, N, Ms = 2048, 2, (512, 128, 136)
+    x = O.normal(N * K, 7300).reshape(N, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    st.write(xb, 0, x)
+    bufs, wts, yts, refs = [xb], [], [], []
+    for i, M in enumerate(Ms):
+        wbytes, wf = float_weights(dtype, M, K, 7301 + i)
+        wb = dev.alloc(wbytes.nbytes)
+        st.write(wb, 0, np.ascontiguousarray(wbytes).view(np.uint8).reshape(-1))
+        wts.append(sg.tdesc(dtype, (K, M), wb))
+        yb = dev.alloc(4 * M * N)
+        yts.append(sg.tdesc(sg.F32, (M, N), yb))
+        bufs += [wb, yb]
+        refs.append((O.mul_mat(dtype, wbytes, K, M, x), wf))
+    op, keep = sg.multi_op(wts, xt, yts)
+    st.execute(op)
+    st.sync()
+    form, grid = sg.last_launch()
+    assert form == "float rows=8 nc=2" and grid == sum((M + 7) // 8 for M in Ms), (form, grid)
+    for M, yt, (ref, wf) in zip(Ms, yts, refs):
+        check_matvec(st.download(yt).reshape(N, M), ref, x, wf)
+    for b in bufs:
+        b.free()
+
+
+def test_float_support_rules(hip):
+    dev, st = hip
+    K, M = 1024, 16
+    wb, xb, yb = dev.alloc(4 * K * M), dev.alloc(4 * K * 16), dev.alloc(4 * M * 16)
+    x, y = sg.tdesc(sg.F32, (K, 1), xb), sg.tdesc(sg.F32, (M, 1), yb)
+    ok = sg.tdesc(sg.F16, (K, M), wb)
+    assert dev.supported(sg.mul_mat_op(ok, x, y)[0])[0] == sg.OK
+    k_odd = sg.tdesc(sg.F16, (K - 4, M), wb)
+    stt, reason = dev.supported(sg.mul_mat_op(k_odd, sg.tdesc(sg.F32, (K - 4, 1), xb), y)[0])
+    assert stt == sg.UNSUPPORTED and "multiple of 8" in reason
+    unaligned = sg.tdesc(sg.F16, (K, M), wb, nb=[2, 2 * K + 8, (2 * K + 8) * M, (2 * K + 8) * M])
+    stt, reason = dev.supported(sg.mul_mat_op(unaligned, x, y)[0])
+    assert stt == sg.UNSUPPORTED and "16-byte" in reason
+    i32 = sg.tdesc(sg.I32, (K, M), wb)  # not a MUL_MAT src0 dtype at all (the core's op rule)
+    assert dev.supported(sg.mul_mat_op(i32, x, y)[0])[0] == sg.INVALID_ARGUMENT
+    for b in (wb, xb, yb):
+        b.free()

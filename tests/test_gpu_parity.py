@@ -635,7 +635,11 @@ def test_support_rules(hip):
     assert stt == sg.UNSUPPORTED and "R32" in reason
     f32w = sg.tdesc(sg.F32, (K, M), wb)
     op, keep = sg.mul_mat_op(f32w, x, y)
-    assert dev.supported(op)[0] == sg.UNSUPPORTED
+    assert dev.supported(op)[0] == sg.OK  # float weights run from the natural layout
+    f32r = sg.tdesc(sg.F32, (K, M), wb, layout=sg.R32)
+    op, keep = sg.mul_mat_op(f32r, x, y)
+    stt, reason = dev.supported(op)
+    assert stt == sg.UNSUPPORTED and "natural" in reason
     r32 = sg.tdesc(sg.Q4_K, (K, M), wb, layout=sg.R32)
     op, keep = sg.mul_mat_op(r32, x, y)
     assert dev.supported(op)[0] == sg.OK
