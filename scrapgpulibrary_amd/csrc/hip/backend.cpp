@@ -607,7 +607,6 @@ scrapgpu_status mul_mat_rule(const scrapgpu_tensor_desc & w, const scrapgpu_tens
     if (sg::sat_mul(fw ? std::max<uint64_t>(w.nb[1], sg::row_size(w.dtype, K)) : sg::row_size(w.dtype, K), (uint64_t) M) >= ((uint64_t) 1 << 32)) {
         return unsupported("MUL_MAT: one slice of src0 must be smaller than 4 GiB", reason);
     }
-    if (fw && sg::dim1(x.ne[1]) > 8) return unsupported("float weights: the hip backend runs them for up to 8 columns of src1", reason);
     if (sg::sat_mul((uint64_t) K, (uint64_t) sg::dim1(x.ne[1])) >= ((uint64_t) 1 << 31)) {
         return unsupported("MUL_MAT: one slice of src1 must hold fewer than 2^31 elements", reason);
     }

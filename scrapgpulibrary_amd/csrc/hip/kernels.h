@@ -71,8 +71,9 @@ struct IdArgs {
 // share them must not overlap. Without scratch or counters the one-work-group-per-tile form runs.
 constexpr int64_t kArriveMax = 65536;
 bool is_float_weight(int dtype);
-// float weights, 1 <= N <= 8 (launch_matvec calls it for them): exact f32 products, K a multiple of
-// 8, rows and slices 16-byte aligned; no scratch
+// float weights (launch_matvec calls it for them, launch_matmul_mfma for F32 and for K not a
+// multiple of 128): exact f32 products, K a multiple of 8, rows and slices 16-byte aligned; one
+// launch per group of 8 columns; no scratch
 hipError_t launch_matvec_float(const MatArgs * mats, int nmat, hipStream_t stream, const char ** kernel_name, uint64_t * grid_size);
 size_t matvec_scratch_bytes(const MatArgs * mats, int nmat, const IdArgs * id = nullptr);
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,

@@ -46,6 +46,8 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float half_bits(uint32_t h) {
     return __half2float(__ushort_as_half((unsigned short) (h & 0xFFFFu)));
@@ -426,6 +428,52 @@ template <> struct PFmt<Q4_0> {
     }
 };
 
+// F16 / BF16 rows in the natural layout (float weights, K a multiple of the 128-element stage):
+// stage s = elements 128 s .. + 127 of the row; k-half h takes elements 64 h .. + 63 (eight
+// 16-byte chunks, contiguous), k-step t its chunk t. The pairs are reordered to the x tile's
+// element order 0 2 1 3 of each group of 4. BF16 feeds the bf16 MFMA (x then in bf16, see
+// k_x_to_f16), F16 the f16 one; neither needs scales.
+template <int DT> struct PFmtFloat {
+    struct Raw {
+        uint4 q[8];
+    };
+    struct Sc {};
+    uint32_t ro;
+    int h;
+    // (nb: the row stride in bytes for float weights)
+    __device__ void init(int64_t, int64_t nb, const RowAddr & ra, int h_) {
+        h = h_;
+        ro = (uint32_t) ((ra.g0 + ra.lr) * nb) + 128 * (uint32_t) h_;
+    }
+    __device__ Raw load(const uint8_t * w, int s) const {
+        const uint8_t * p = w + (ro + (uint32_t) s * 256);
+        Raw r;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r.q[i] = load16(p + 16 * i);
+        return r;
+    }
+    __device__ Raw load_half2(const uint8_t * w, int s, const Raw &) const { return load(w, s); }
+    __device__ Sc prep(const Raw &, int) const { return Sc{}; }
+    __device__ static f16x8 bop(const Raw & r, const Sc &, int t) {
+        const uint4 & q = r.q[t];
+        const uint4 o = make_uint4((q.x & 0xFFFFu) | (q.y << 16), (q.x >> 16) | (q.y & 0xFFFF0000u), (q.z & 0xFFFFu) | (q.w << 16),
+                                   (q.z >> 16) | (q.w & 0xFFFF0000u));
+        return __builtin_bit_cast(f16x8, o);
+    }
+    __device__ static int chunk(int h, int t) {
+        return 8 * h + t;
+    }
+};
+template <> struct PFmt<F16> : PFmtFloat<F16> {};
+template <> struct PFmt<BF16> : PFmtFloat<BF16> {};
+
+// the GEMM's matrix instruction: f16 operands, or bf16 ones (BF16 weights) carried in f16x8
+template <int DT>
+__device__ __forceinline__ f32x16 mma32(const f16x8 & a, const f16x8 & b, const f32x16 & c) {
+    if constexpr (DT == BF16) return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
 struct MmArgs {
     MatArgs a;
     const uint16_t * xb; // f16 activations [slices][N][K], each row scaled (k_x_to_f16)
@@ -560,7 +608,9 @@ __device__ __forceinline__ f16x8 bop_of(const typename F::Raw & r, const typenam
 
 // work-groups of W waves per CU that the register file (and, at BN = 128, the LDS) holds
 constexpr int occupancy_of(int dt, int bn, int rg, int w = 4) {
-    return w == 12 ? 1 : bn == 32 ? 3 : bn == 64 && rg == 1 ? (dt == Q6_K ? 2 : 3) : bn == 128 && rg == 2 ? 1 : 2;
+    // (float weights: 32 registers per stage of a row's raw data, held for two stages)
+    return dt == F16 || dt == BF16 ? (w == 12 || bn > 64 || rg > 1 ? 1 : 2)
+         : w == 12 ? 1 : bn == 32 ? 3 : bn == 64 && rg == 1 ? (dt == Q6_K ? 2 : 3) : bn == 128 && rg == 2 ? 1 : 2;
 }
 
 // W = 4: a work-group per SIMD quad, several per CU. W = 12: the CU's whole complement of 3 waves
@@ -767,7 +817,7 @@ __global__ __launch_bounds__(64 * W, occupancy_of(DT, BN, RG, W)) void k_matmul(
                 // GA: a tile of at most 32 pairs leaves the second token fragment to padding
                 if (GA && q > 0 && half_tile) continue;
 #pragma unroll
-                for (int i = 0; i < RG; ++i) acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c][q], b[c][i], acc[i][q], 0, 0, 0);
+                for (int i = 0; i < RG; ++i) acc[i][q] = mma32<DT>(a[c][q], b[c][i], acc[i][q]);
             }
             if (t < 7) {
 #pragma unroll
@@ -1266,7 +1316,7 @@ __global__ __launch_bounds__(256) void k_sk_reduce(MmArgs L) {
 // are stored divided by 16 more, and xsum gets the row's 32-element sub-block sums (of the scaled
 // x, times 1/32 so that they fit f16), 16 per 512 elements in the order the matmul's lanes hold
 // the sub-blocks: position 8 h + e <- sub-block 4 (e / 2) + 2 h + e % 2; missing ones are zero.
-template <bool VEC, bool Q4K>
+template <bool VEC, bool Q4K, bool BF = false>
 __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, float * xs, uint16_t * xsum, int64_t xsum_row) {
     constexpr int kCached = 6; // K <= 12288 is read once
     const int64_t row = blockIdx.x, sl = row / a.N, n = row - sl * a.N;
@@ -1305,10 +1355,17 @@ __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, floa
                 for (int e = 0; e < 8; ++e) s[e] *= 0.0625f;
             }
         }
-        const f16x2 p0 = __builtin_convertvector((f32x2{s[0], s[2]}), f16x2), p1 = __builtin_convertvector((f32x2{s[1], s[3]}), f16x2);
-        const f16x2 p2 = __builtin_convertvector((f32x2{s[4], s[6]}), f16x2), p3 = __builtin_convertvector((f32x2{s[5], s[7]}), f16x2);
-        *reinterpret_cast<uint4 *>(op + k) = make_uint4(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
-                                                        __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3));
+        if constexpr (BF) { // (BF16 weights: x in bf16, rounded to nearest even)
+            const bf16x2 p0 = __builtin_convertvector((f32x2{s[0], s[2]}), bf16x2), p1 = __builtin_convertvector((f32x2{s[1], s[3]}), bf16x2);
+            const bf16x2 p2 = __builtin_convertvector((f32x2{s[4], s[6]}), bf16x2), p3 = __builtin_convertvector((f32x2{s[5], s[7]}), bf16x2);
+            *reinterpret_cast<uint4 *>(op + k) = make_uint4(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                                                            __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3));
+        } else {
+            const f16x2 p0 = __builtin_convertvector((f32x2{s[0], s[2]}), f16x2), p1 = __builtin_convertvector((f32x2{s[1], s[3]}), f16x2);
+            const f16x2 p2 = __builtin_convertvector((f32x2{s[4], s[6]}), f16x2), p3 = __builtin_convertvector((f32x2{s[5], s[7]}), f16x2);
+            *reinterpret_cast<uint4 *>(op + k) = make_uint4(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                                                            __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3));
+        }
     };
     const int64_t k0 = (int64_t) threadIdx.x * 8; // K is a multiple of 32: a group of 8 is whole
     float cache[kCached][8];
@@ -1440,6 +1497,20 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
     const int64_t stages = (a.K + BK - 1) / BK;
     static const int env_w = env_int("SCRAPGPU_HIP_MM_W", 0);
     MmConfig c;
+    if (a.dtype == F16 || a.dtype == BF16) {
+        // 4-wave work-groups, 128-token tiles from 128 tokens on (each 2-byte weight fetched half as
+        // often: 12288x4096 at 512 tokens 119 against 137 us, at 256 tokens 81 against 92), K split
+        // while the tiles leave work-group slots empty, every split >= 8 stages
+        c.w = 4;
+        c.kg = 1;
+        c.rg = 1;
+        const int64_t tm = (a.M + 127) / 128;
+        c.bn = env_bn == 64 || env_bn == 128 ? env_bn : a.N >= 128 ? 128 : 64;
+        const int64_t tiles = tm * ((a.N + c.bn - 1) / c.bn) * slices, want = (int64_t) cu_count * occupancy_of(a.dtype, c.bn, 1);
+        c.split = 1;
+        while (tiles * c.split < want && stages / (c.split + 1) >= 8 && c.split < 8) ++c.split;
+        return c;
+    }
     // 12-wave work-groups, one per CU, in this order of preference:
     //  1. KG = 1: 384-row tiles of 64 tokens that fill the CUs in whole rounds (or in enough
     //     rounds that the last one matters little), the last row tile mostly inside M;
@@ -1568,6 +1639,13 @@ void * kernel_of(const MmConfig & c) {
     return c.bn == 64 ? (void *) k_matmul<DT, 64, 2, 4, 1> : (void *) k_matmul<DT, 128, 2, 4, 1>;
 }
 
+// float weights: the 4-wave 64-token kernel only (their raw rows take the registers the wider
+// forms need)
+template <int DT>
+void * kernel_of_float(const MmConfig & c) {
+    return c.bn == 64 ? (void *) k_matmul<DT, 64, 1, 4, 1> : (void *) k_matmul<DT, 128, 1, 4, 1>;
+}
+
 // scratch: x as f16 [slices][N][K] | row factors [slices][N] | Q4_K sub-block sums
 // [slices][N][xsum_row] | split-K partials
 size_t xs_offset(const MatArgs & a) {
@@ -1629,13 +1707,20 @@ static bool q4k_x_form(const MatArgs & a, int cu_count, bool lean) {
     return a.dtype == Q4_K && !config_of(a, cu_count, lean).wide;
 }
 
+// float weights on the GEMM: F16 / BF16 with K a whole number of 128-element stages (x rows in bf16
+// for BF16); the rest (F32, other K) runs the exact float matvec over groups of 8 columns
+static bool float_gemm(const MatArgs & a) {
+    return (a.dtype == F16 || a.dtype == BF16) && a.K % BK == 0;
+}
+
 bool matmul_reads_same_x(const MatArgs & a, const MatArgs & b) {
     return a.x == b.x && a.x_s1 == b.x_s1 && a.x_s2 == b.x_s2 && a.x_s3 == b.x_s3 && a.N == b.N && a.K == b.K && a.ne12 == b.ne12 &&
            a.ne13 == b.ne13;
 }
 
 bool matmul_same_x(const MatArgs & a, const MatArgs & b, int cu_count, bool lean) {
-    return matmul_reads_same_x(a, b) && q4k_x_form(a, cu_count, lean) == q4k_x_form(b, cu_count, lean);
+    return matmul_reads_same_x(a, b) && q4k_x_form(a, cu_count, lean) == q4k_x_form(b, cu_count, lean) && (a.dtype == BF16) == (b.dtype == BF16) &&
+           !(is_float_weight(a.dtype) && !float_gemm(a)) && !(is_float_weight(b.dtype) && !float_gemm(b));
 }
 
 hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name,
@@ -1648,6 +1733,7 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
         if (mats[j].dtype != a.dtype || !matmul_reads_same_x(mats[j], a) || mats[j].ne12 * mats[j].ne13 != 1 || a.ne12 * a.ne13 != 1) return hipErrorInvalidValue;
         a.M += mats[j].M;
     }
+    if (is_float_weight(a.dtype) && !float_gemm(a)) return launch_matvec_float(mats, nmat, stream, kernel_name, nullptr);
     uint16_t * xb = reinterpret_cast<uint16_t *>(scratch);
     const int64_t rows = a.N * a.ne12 * a.ne13;
     float * xs = reinterpret_cast<float *>(scratch + xs_offset(a));
@@ -1664,6 +1750,11 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
             hipLaunchKernelGGL((k_x_to_f16<true, true>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
         else
             hipLaunchKernelGGL((k_x_to_f16<false, true>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
+    } else if (a.dtype == BF16) {
+        if (vec)
+            hipLaunchKernelGGL((k_x_to_f16<true, false, true>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
+        else
+            hipLaunchKernelGGL((k_x_to_f16<false, false, true>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
     } else {
         if (vec)
             hipLaunchKernelGGL((k_x_to_f16<true, false>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
@@ -1718,6 +1809,8 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
         case Q8_0: fn = kernel_of<Q8_0>(cfg); if (kernel_name) *kernel_name = "matmul_mfma_q8_0"; break;
         case Q4_K: fn = kernel_of<Q4_K>(cfg); if (kernel_name) *kernel_name = "matmul_mfma_q4_k"; break;
         case Q6_K: fn = kernel_of<Q6_K>(cfg); if (kernel_name) *kernel_name = "matmul_mfma_q6_k"; break;
+        case F16: fn = kernel_of_float<F16>(cfg); if (kernel_name) *kernel_name = "matmul_mfma_f16"; break;
+        case BF16: fn = kernel_of_float<BF16>(cfg); if (kernel_name) *kernel_name = "matmul_mfma_bf16"; break;
         default: return hipErrorInvalidValue;
     }
     if ((e = allow_lds(fn, lds)) != hipSuccess) return e;

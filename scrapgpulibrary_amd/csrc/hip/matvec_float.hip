@@ -210,8 +210,25 @@ bool is_float_weight(int dtype) {
 
 hipError_t launch_matvec_float(const MatArgs * mats, int nmat, hipStream_t stream, const char ** kernel_name, uint64_t * grid_size) {
     if (nmat < 1 || nmat > 3) return hipErrorInvalidValue;
+    if (mats[0].N > 8) {
+        // more columns (F32 weights, or K not a whole number of GEMM stages): one launch per group
+        // of 8 columns, each the exact product above
+        for (int64_t c0 = 0; c0 < mats[0].N; c0 += 8) {
+            MatArgs g[3];
+            for (int j = 0; j < nmat; ++j) {
+                g[j] = mats[j];
+                g[j].N = std::min<int64_t>(8, mats[j].N - c0);
+                g[j].x = mats[j].x + c0 * mats[j].x_s1;
+                g[j].y = mats[j].y + c0 * mats[j].y_s1;
+            }
+            const hipError_t e = launch_matvec_float(g, nmat, stream, kernel_name, grid_size);
+            if (e != hipSuccess) return e;
+        }
+        std::snprintf(last_form().form, sizeof(last_form().form), "float rows=8 column-groups=%d", (int) ((mats[0].N + 7) / 8));
+        return hipSuccess;
+    }
     const MatArgs & a = mats[0];
-    if (!is_float_weight(a.dtype) || a.N < 1 || a.N > 8 || a.K < 8 || a.K % 8 != 0) return hipErrorInvalidValue;
+    if (!is_float_weight(a.dtype) || a.N < 1 || a.K < 8 || a.K % 8 != 0) return hipErrorInvalidValue;
     MvfArgs A;
     std::memset(&A, 0, sizeof(A));
     A.a = a;

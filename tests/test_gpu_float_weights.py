@@ -178,3 +178,70 @@ def test_float_support_rules(hip):
     assert dev.supported(sg.mul_mat_op(i32, x, y)[0])[0] == sg.INVALID_ARGUMENT
     for b in (wb, xb, yb):
         b.free()
+
+
+# ---- more than 8 columns ------------------------------------------------------------------------
+# F16 / BF16 with K a multiple of 128: the MFMA GEMM (f16 operands for F16, the weights exact; bf16
+# operands for BF16, x rounded to bf16): the prefill gate NMSE <= 5e-5, and tighter bounds that a
+# lost bit of either operand would break. F32 and other K: the exact matvec per group of 8 columns.
+
+PREFILL_NMSE = {sg.F16: 1e-6, sg.BF16: 2e-5}
+
+
+@pytest.mark.parametrize("dtype", (sg.F16, sg.BF16), ids=lambda d: IDS[d])
+@pytest.mark.parametrize("K,M,N", [(4096, 1000, 64), (2048, 384, 200), (512, 4096, 512), (1024, 8192, 9)])
+def test_float_prefill_gemm(hip, dtype, K, M, N):
+    dev, st = hip
+    wbytes, wf = float_weights(dtype, M, K, 7400 + K + N)
+    x = O.normal(N * K, 7401 + N).reshape(N, K)
+    x[:, ::37] *= 100.0  # outlier channels: the per-row scaling of x keeps them in range
+    y = run(dev, st, dtype, wbytes, K, M, x, check_form=False)
+    form, _ = sg.last_launch()
+    assert form.startswith("gemm w=4 kg=1"), form
+    ref = O.mul_mat(dtype, wbytes, K, M, x, threads=8)
+    e = nmse(y, ref)
+    assert e <= PREFILL_NMSE[dtype], f"{IDS[dtype]} {M}x{K} N={N}: NMSE {e:.3e} [{form}]"
+
+
+@pytest.mark.parametrize("dtype,K,N", [(sg.F32, 1024, 20), (sg.F16, 520, 17), (sg.BF16, 72, 33)], ids=["f32", "f16_k520", "bf16_k72"])
+def test_float_prefill_column_groups(hip, dtype, K, N):
+    """F32 weights and K not a multiple of 128: exact products, 8 columns per launch."""
+    dev, st = hip
+    M = 300
+    wbytes, wf = float_weights(dtype, M, K, 7500 + K)
+    x = O.normal(N * K, 7501).reshape(N, K)
+    y = run(dev, st, dtype, wbytes, K, M, x, check_form=False)
+    assert sg.last_launch()[0] == f"float rows=8 column-groups={(N + 7) // 8}"
+    ref = O.mul_mat(dtype, wbytes, K, M, x, threads=8)
+    check_matvec(y, ref, x, wf)
+
+
+@pytest.mark.parametrize("dtype", (sg.F16, sg.BF16), ids=lambda d: IDS[d])
+def test_float_prefill_multi(hip, dtype):
+    """A prefill MUL_MAT_MULTI of three float weights (q / k / v shapes): one GEMM over all rows."""
+    dev, st = hip
+    K, N, Ms = 1024, 96, (512, 128, 136)
+    x = O.normal(N * K, 7600).reshape(N, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    st.write(xb, 0, x)
+    bufs, wts, yts, refs = [xb], [], [], []
+    for i, M in enumerate(Ms):
+        wbytes, wf = float_weights(dtype, M, K, 7601 + i)
+        wb = dev.alloc(wbytes.nbytes)
+        st.write(wb, 0, np.ascontiguousarray(wbytes).view(np.uint8).reshape(-1))
+        wts.append(sg.tdesc(dtype, (K, M), wb))
+        yb = dev.alloc(4 * M * N)
+        yts.append(sg.tdesc(sg.F32, (M, N), yb))
+        bufs += [wb, yb]
+        refs.append(O.mul_mat(dtype, wbytes, K, M, x, threads=8))
+    op, keep = sg.multi_op(wts, xt, yts)
+    st.execute(op)
+    st.sync()
+    form, _ = sg.last_launch()
+    assert form.startswith("gemm w=4 kg=1"), form
+    for M, yt, ref in zip(Ms, yts, refs):
+        e = nmse(st.download(yt).reshape(N, M), ref)
+        assert e <= PREFILL_NMSE[dtype], f"{M} rows: NMSE {e:.3e}"
+    for b in bufs:
+        b.free()
