@@ -637,11 +637,20 @@ scrapgpu_status mul_mat_rule(const scrapgpu_tensor_desc & w, const scrapgpu_tens
 // Fills `a` / `id` (pointers left null) when supported. One (slot, token) pair per matvec slice.
 scrapgpu_status mul_mat_id_rule(const scrapgpu_tensor_desc & w, const scrapgpu_tensor_desc & x, const scrapgpu_tensor_desc & ids,
                                 const scrapgpu_tensor_desc & y, sgk::MatArgs * a, sgk::IdArgs * id, const char ** reason) {
-    if (!sg::is_quant(w.dtype)) return unsupported("the hip backend implements MUL_MAT_ID for Q4_0 / Q8_0 / Q4_K / Q6_K experts only", reason);
-    if (w.layout != SCRAPGPU_LAYOUT_R32) {
-        return unsupported("quantized experts must use the R32 layout (scrapgpu_tensor_upload packs them on the way)", reason);
+    const bool fw = w.dtype == SCRAPGPU_DTYPE_F32 || w.dtype == SCRAPGPU_DTYPE_F16;
+    if (!sg::is_quant(w.dtype) && !fw) return unsupported("the hip backend implements MUL_MAT_ID for Q4_0 / Q8_0 / Q4_K / Q6_K, F32 and F16 experts", reason);
+    if (fw) {
+        // (reference ops.cpp:986-1024 reads F32 / F16 experts with load_float): natural rows
+        if (w.layout != SCRAPGPU_LAYOUT_NATURAL) return unsupported("float experts run from the natural layout", reason);
+        if (w.nb[0] != sg::type_size(w.dtype)) return unsupported("MUL_MAT_ID needs contiguous rows of src0 (nb0 == element size)", reason);
+        if (sg::dim1(w.ne[0]) % 8 != 0) return unsupported("float experts: the hip kernels read rows in runs of 8 elements, so K must be a multiple of 8", reason);
+        if (w.nb[1] % 16 != 0 || w.nb[2] % 16 != 0 || w.offset % 16 != 0) return unsupported("float experts: rows and experts must start on 16-byte boundaries", reason);
+    } else {
+        if (w.layout != SCRAPGPU_LAYOUT_R32) {
+            return unsupported("quantized experts must use the R32 layout (scrapgpu_tensor_upload packs them on the way)", reason);
+        }
+        if (!sg::r32_eligible(w)) return unsupported("src0 is not R32-eligible (contiguous, whole blocks per row, 16-byte slice strides)", reason);
     }
-    if (!sg::r32_eligible(w)) return unsupported("src0 is not R32-eligible (contiguous, whole blocks per row, 16-byte slice strides)", reason);
     if (x.dtype != SCRAPGPU_DTYPE_F32 || y.dtype != SCRAPGPU_DTYPE_F32 || x.layout != SCRAPGPU_LAYOUT_NATURAL || y.layout != SCRAPGPU_LAYOUT_NATURAL) {
         return unsupported("MUL_MAT_ID expects an F32 natural-layout src1 and destination", reason);
     }
@@ -660,7 +669,7 @@ scrapgpu_status mul_mat_id_rule(const scrapgpu_tensor_desc & w, const scrapgpu_t
         return invalid("MUL_MAT_ID: src1, ids and dst shapes are inconsistent with src0 and n_used");
     }
     if (nu * T > 65535) return unsupported("MUL_MAT_ID: more than 65535 (slot, token) pairs", reason);
-    if (sg::sat_mul(sg::row_size(w.dtype, K), (uint64_t) M) >= ((uint64_t) 1 << 32)) {
+    if (sg::sat_mul(fw ? std::max<uint64_t>(w.nb[1], sg::row_size(w.dtype, K)) : sg::row_size(w.dtype, K), (uint64_t) M) >= ((uint64_t) 1 << 32)) {
         return unsupported("MUL_MAT_ID: one expert must be smaller than 4 GiB", reason);
     }
     if (a) {
@@ -668,7 +677,7 @@ scrapgpu_status mul_mat_id_rule(const scrapgpu_tensor_desc & w, const scrapgpu_t
         a->dtype = w.dtype;
         a->M = M;
         a->K = K;
-        a->nb = K / (int64_t) sg::block_size(w.dtype);
+        a->nb = fw ? (int64_t) w.nb[1] : K / (int64_t) sg::block_size(w.dtype); // (float experts: the row stride in bytes)
         a->w_s2 = w.nb[2];
         a->x_s1 = (int64_t) (x.nb[1] / 4);
         a->x_s2 = (int64_t) (x.nb[2] / 4);
@@ -697,11 +706,22 @@ scrapgpu_status mul_mat_id_rule(const scrapgpu_tensor_desc & w, const scrapgpu_t
 // [K, n0, n1, n2]. Fills `g` (pointers left null) when supported.
 scrapgpu_status get_rows_rule(const scrapgpu_tensor_desc & w, const scrapgpu_tensor_desc & ids, const scrapgpu_tensor_desc & y,
                               sgk::GetRowsLaunch * g, const char ** reason) {
-    if (!sg::is_quant(w.dtype)) return unsupported("the hip backend implements GET_ROWS for Q4_0 / Q8_0 / Q4_K / Q6_K rows only", reason);
-    if (w.layout != SCRAPGPU_LAYOUT_R32) {
-        return unsupported("quantized GET_ROWS sources must use the R32 layout (scrapgpu_tensor_upload packs them on the way)", reason);
+    const bool fw = w.dtype == SCRAPGPU_DTYPE_F32 || w.dtype == SCRAPGPU_DTYPE_F16;
+    if (!sg::is_quant(w.dtype) && !fw) return unsupported("the hip backend implements GET_ROWS for Q4_0 / Q8_0 / Q4_K / Q6_K, F32 and F16 rows", reason);
+    if (fw) {
+        // (reference ops.cpp:690-721 reads F32 / F16 rows with load_float)
+        if (w.layout != SCRAPGPU_LAYOUT_NATURAL) return unsupported("F32 / F16 GET_ROWS sources use the natural layout", reason);
+        if (w.nb[0] != sg::type_size(w.dtype)) return unsupported("GET_ROWS needs contiguous rows (nb0 == element size)", reason);
+        for (int i = 1; i < 4; ++i) {
+            if (w.nb[i] % w.nb[0] != 0) return unsupported("GET_ROWS: src0 strides must be whole elements", reason);
+        }
+        if (w.offset % w.nb[0] != 0) return unsupported("GET_ROWS: the src0 offset must be a whole element", reason);
+    } else {
+        if (w.layout != SCRAPGPU_LAYOUT_R32) {
+            return unsupported("quantized GET_ROWS sources must use the R32 layout (scrapgpu_tensor_upload packs them on the way)", reason);
+        }
+        if (!sg::r32_eligible(w)) return unsupported("src0 is not R32-eligible (contiguous, whole blocks per row, 16-byte slice strides)", reason);
     }
-    if (!sg::r32_eligible(w)) return unsupported("src0 is not R32-eligible (contiguous, whole blocks per row, 16-byte slice strides)", reason);
     if (ids.dtype != SCRAPGPU_DTYPE_I32 || ids.layout != SCRAPGPU_LAYOUT_NATURAL || y.dtype != SCRAPGPU_DTYPE_F32 || y.layout != SCRAPGPU_LAYOUT_NATURAL) {
         return unsupported("GET_ROWS expects I32 indices and an F32 natural-layout destination", reason);
     }
@@ -719,6 +739,7 @@ scrapgpu_status get_rows_rule(const scrapgpu_tensor_desc & w, const scrapgpu_ten
     if (g) {
         std::memset(g, 0, sizeof(*g));
         g->dtype = w.dtype;
+        g->w_s1 = w.nb[1];
         g->w_s2 = w.nb[2];
         g->w_s3 = w.nb[3];
         g->i_s0 = (int64_t) (ids.nb[0] / 4);
@@ -776,6 +797,9 @@ scrapgpu_status api_op_supported(scrapgpu_device_t * device, const scrapgpu_op_d
 }
 
 double weight_bytes(const sgk::MatArgs & a) {
+    if (sgk::is_float_weight(a.dtype)) {
+        return (double) a.M * (double) a.K * (a.dtype == sgk::F32 ? 4.0 : 2.0) * (double) ((a.ne12 / a.r2) * (a.ne13 / a.r3));
+    }
     const int64_t bs = a.dtype == sgk::Q4_K || a.dtype == sgk::Q6_K ? 256 : 32;
     const double ts = a.dtype == sgk::Q4_0 ? 18 : a.dtype == sgk::Q8_0 ? 34 : a.dtype == sgk::Q4_K ? 144 : 210;
     return (double) a.M * (double) (a.K / bs) * ts * (double) ((a.ne12 / a.r2) * (a.ne13 / a.r3));
@@ -788,7 +812,7 @@ double weight_bytes(const sgk::MatArgs & a) {
 // fast), within the routing kernel's limits
 bool mul_mat_id_grouped(const sgk::MatArgs & a, const sgk::IdArgs & id) {
     const int64_t rows = (id.x_shared ? 1 : id.n_used) * id.n_tok;
-    return id.n_tok > 8 && id.n_used * id.n_tok >= 4 * id.n_exp && id.n_exp <= 1024 && rows * a.K < ((int64_t) 1 << 31);
+    return !sgk::is_float_weight(a.dtype) && id.n_tok > 8 && id.n_used * id.n_tok >= 4 * id.n_exp && id.n_exp <= 1024 && rows * a.K < ((int64_t) 1 << 31);
 }
 
 // the largest column count that takes the decode matvec (above it: the f16 MFMA GEMM). 8 keeps

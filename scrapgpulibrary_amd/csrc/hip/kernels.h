@@ -74,7 +74,9 @@ bool is_float_weight(int dtype);
 // float weights (launch_matvec calls it for them, launch_matmul_mfma for F32 and for K not a
 // multiple of 128): exact f32 products, K a multiple of 8, rows and slices 16-byte aligned; one
 // launch per group of 8 columns; no scratch
-hipError_t launch_matvec_float(const MatArgs * mats, int nmat, hipStream_t stream, const char ** kernel_name, uint64_t * grid_size);
+// With `id` (N = 1): the MUL_MAT_ID pairs as launch_matvec takes them.
+hipError_t launch_matvec_float(const MatArgs * mats, int nmat, hipStream_t stream, const char ** kernel_name, uint64_t * grid_size,
+                               const IdArgs * id = nullptr);
 size_t matvec_scratch_bytes(const MatArgs * mats, int nmat, const IdArgs * id = nullptr);
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
                          uint64_t * grid_size, const IdArgs * id = nullptr, uint8_t * scratch = nullptr, uint32_t * arrive = nullptr);
@@ -111,9 +113,9 @@ hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t 
 // GET_ROWS on R32 weights: dst[:, a, b, c] = dequantized row ids[a, b, c] of slice (b, c) of src0
 // (bit-exact with the dequantizer; out-of-range indices read the nearest row).
 struct GetRowsLaunch {
-    int dtype;
+    int dtype;            // quantized (R32) or F32 / F16 (natural rows w_s1 bytes apart)
     const uint8_t * w;
-    uint64_t w_s2, w_s3;
+    uint64_t w_s1, w_s2, w_s3;
     const int32_t * ids;
     int64_t i_s0, i_s1, i_s2; // element strides
     float * y;

@@ -1536,7 +1536,7 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
                          uint64_t * grid_size, const IdArgs * id, uint8_t * scratch, uint32_t * arrive) {
     if (nmat < 1 || nmat > 3) return hipErrorInvalidValue;
     const MatArgs & a = mats[0];
-    if (is_float_weight(a.dtype)) return id == nullptr ? launch_matvec_float(mats, nmat, stream, kernel_name, grid_size) : hipErrorInvalidValue;
+    if (is_float_weight(a.dtype)) return launch_matvec_float(mats, nmat, stream, kernel_name, grid_size, id);
     for (int j = 0; j < nmat; ++j) {
         if (mats[j].dtype != a.dtype || mats[j].K != a.K || mats[j].N != a.N || (nmat > 1 && mats[j].ne12 * mats[j].ne13 != 1)) {
             return hipErrorInvalidValue;

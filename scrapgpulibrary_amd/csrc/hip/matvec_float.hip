@@ -41,6 +41,8 @@ struct MvfArgs {
     int64_t Mm[3];
     float * ym[3];
     int64_t ys1m[3];
+    IdArgs id;     // MUL_MAT_ID (has_id): blockIdx.y is the pair t * n_used + i
+    int has_id;
 };
 
 // 8 consecutive weights of one row as f32 (p 16-byte aligned)
@@ -121,6 +123,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, NC >= 4 
     const int64_t i2 = sl % a.ne12, i3 = sl / a.ne12;
     const uint8_t * w = A.nmat > 1 ? A.wm[j] : a.w + (uint64_t) (i2 / a.r2) * a.w_s2 + (uint64_t) (i3 / a.r3) * a.w_s3;
     const float * x = a.x + i2 * a.x_s2 + i3 * a.x_s3;
+    float * yb = A.nmat > 1 ? A.ym[j] : a.y + i2 * a.y_s2 + i3 * a.y_s3;
+    if (A.has_id) {
+        // the pair's expert (read on the device, clamped into range), x column and y column
+        const int64_t t = sl / A.id.n_used, i = sl - t * A.id.n_used;
+        int64_t e = A.id.ids[i * A.id.s0 + t * A.id.s1];
+        e = e < 0 ? 0 : (e >= A.id.n_exp ? A.id.n_exp - 1 : e);
+        w = (A.nmat > 1 ? A.wm[j] : a.w) + (uint64_t) e * a.w_s2;
+        x = a.x + (A.id.x_shared ? 0 : i) * a.x_s1 + t * a.x_s2;
+        yb = (A.nmat > 1 ? A.ym[j] : a.y) + i * a.y_s1 + t * a.y_s2;
+    }
     const int64_t K = a.K, N = a.N;
     constexpr int esz = WT == F32 ? 4 : 2;
     const uint8_t * row[kRows];
@@ -185,9 +197,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, NC >= 4 
         const int r = t / NC, c = t % NC;
         const float sum = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
         if (m0 + r < M && c < N) {
-            float * y = A.nmat > 1 ? A.ym[j] : a.y + i2 * a.y_s2 + i3 * a.y_s3;
             const int64_t ys1 = A.nmat > 1 ? A.ys1m[j] : a.y_s1;
-            y[c * ys1 + m0 + r] = sum;
+            yb[c * ys1 + m0 + r] = sum; // (MUL_MAT_ID: one column)
         }
     }
 }
@@ -208,9 +219,11 @@ bool is_float_weight(int dtype) {
     return dtype == F32 || dtype == F16 || dtype == BF16;
 }
 
-hipError_t launch_matvec_float(const MatArgs * mats, int nmat, hipStream_t stream, const char ** kernel_name, uint64_t * grid_size) {
+hipError_t launch_matvec_float(const MatArgs * mats, int nmat, hipStream_t stream, const char ** kernel_name, uint64_t * grid_size,
+                               const IdArgs * id) {
     if (nmat < 1 || nmat > 3) return hipErrorInvalidValue;
-    if (mats[0].N > 8) {
+    if (id != nullptr && (mats[0].N != 1 || id->ids == nullptr || id->n_used < 1 || id->n_tok < 1 || id->n_exp < 1)) return hipErrorInvalidValue;
+    if (mats[0].N > 8 && id == nullptr) {
         // more columns (F32 weights, or K not a whole number of GEMM stages): one launch per group
         // of 8 columns, each the exact product above
         for (int64_t c0 = 0; c0 < mats[0].N; c0 += 8) {
@@ -236,7 +249,7 @@ hipError_t launch_matvec_float(const MatArgs * mats, int nmat, hipStream_t strea
     A.mt[0] = 0;
     for (int j = 0; j < 3; ++j) {
         const bool has = j < nmat;
-        if (has && (mats[j].dtype != a.dtype || mats[j].K != a.K || mats[j].N != a.N || (nmat > 1 && mats[j].ne12 * mats[j].ne13 != 1))) {
+        if (has && (mats[j].dtype != a.dtype || mats[j].K != a.K || mats[j].N != a.N || (nmat > 1 && id == nullptr && mats[j].ne12 * mats[j].ne13 != 1))) {
             return hipErrorInvalidValue;
         }
         A.wm[j] = has ? mats[j].w : nullptr;
@@ -245,7 +258,11 @@ hipError_t launch_matvec_float(const MatArgs * mats, int nmat, hipStream_t strea
         A.ys1m[j] = has ? mats[j].y_s1 : 0;
         A.mt[j + 1] = A.mt[j] + (has ? (mats[j].M + kRows - 1) / kRows : 0);
     }
-    const int64_t slices = a.ne12 * a.ne13;
+    if (id != nullptr) {
+        A.id = *id;
+        A.has_id = 1;
+    }
+    const int64_t slices = id != nullptr ? id->n_used * id->n_tok : a.ne12 * a.ne13;
     if (A.mt[nmat] > 0x7fffffff || slices > 65535) return hipErrorInvalidValue;
     const int nc = (int) a.N;
     const bool xv = (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && a.x_s1 % 4 == 0 && a.x_s2 % 4 == 0 && a.x_s3 % 4 == 0;

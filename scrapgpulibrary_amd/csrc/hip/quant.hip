@@ -508,6 +508,22 @@ __global__ __launch_bounds__(256) void k_get_rows(GetRowsArgs a) {
     }
 }
 
+// GET_ROWS on F32 / F16 rows (natural layout, rows w_s1 bytes apart): one work-group per output
+// row, each element widened exactly to f32 (the reference's load_float)
+template <int DT>
+__global__ __launch_bounds__(256) void k_get_rows_float(GetRowsArgs a, uint64_t w_s1) {
+    const int64_t row = blockIdx.x;
+    const int64_t c = row / (a.n0 * a.n1), rem = row - c * a.n0 * a.n1, bi = rem / a.n0, ai = rem - bi * a.n0;
+    int64_t r = a.ids[ai * a.i_s0 + bi * a.i_s1 + c * a.i_s2];
+    r = r < 0 ? 0 : (r >= a.M ? a.M - 1 : r); // out-of-range rows read the nearest row
+    const uint8_t * src = a.w + (uint64_t) bi * a.w_s2 + (uint64_t) c * a.w_s3 + (uint64_t) r * w_s1;
+    float * y = a.y + ai * a.y_s1 + bi * a.y_s2 + c * a.y_s3;
+    for (int64_t e = threadIdx.x; e < a.K; e += blockDim.x) {
+        if constexpr (DT == F32) y[e] = reinterpret_cast<const float *>(src)[e];
+        else y[e] = __half2float(__ushort_as_half(reinterpret_cast<const unsigned short *>(src)[e]));
+    }
+}
+
 unsigned grid_for(int64_t n, int threads) {
     const int64_t g = (n + threads - 1) / threads;
     return (unsigned) (g < 65536 * 8 ? (g < 1 ? 1 : g) : 65536 * 8);
@@ -565,11 +581,18 @@ hipError_t launch_get_rows(const GetRowsLaunch & g, hipStream_t stream) {
     a.y_s3 = g.y_s3;
     a.K = g.K;
     a.M = g.M;
-    a.nb = g.K / block_elems(g.dtype);
     a.n0 = g.n0;
     a.n1 = g.n1;
-    a.ar = areas_of(g.dtype);
     const dim3 grid((unsigned) rows), block(256);
+    if (g.dtype == F32 || g.dtype == F16) {
+        a.nb = 0;
+        a.ar = Areas{};
+        if (g.dtype == F32) hipLaunchKernelGGL(k_get_rows_float<F32>, grid, block, 0, stream, a, g.w_s1);
+        else hipLaunchKernelGGL(k_get_rows_float<F16>, grid, block, 0, stream, a, g.w_s1);
+        return hipGetLastError();
+    }
+    a.nb = g.K / block_elems(g.dtype);
+    a.ar = areas_of(g.dtype);
     switch (g.dtype) {
         case Q4_0: hipLaunchKernelGGL(k_get_rows<Q4_0>, grid, block, 0, stream, a); break;
         case Q8_0: hipLaunchKernelGGL(k_get_rows<Q8_0>, grid, block, 0, stream, a); break;

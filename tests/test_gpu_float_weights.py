@@ -245,3 +245,95 @@ def test_float_prefill_multi(hip, dtype):
         assert e <= PREFILL_NMSE[dtype], f"{M} rows: NMSE {e:.3e}"
     for b in bufs:
         b.free()
+
+
+# ---- GET_ROWS -----------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", (sg.F32, sg.F16), ids=lambda d: IDS[d])
+def test_float_get_rows(hip, dtype):
+    """GET_ROWS on F32 / F16 rows: the reference's golden rows (F16), and the oracle's rows for
+    repeated, first and last indices; an index past the rows reads the last one (the GPU rule)."""
+    dev, st = hip
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "float_weights.npz"))
+    K, R = 72, 37
+    if dtype == sg.F16:
+        wbytes, rid, yref = g["f16_gr_w"], g["f16_gr_ids"], g["f16_gr_y"]
+    else:
+        wbytes = O.normal(K * R, 7700).reshape(R, K)
+        rid = np.array([0, R - 1, 5, 5, 12, 30], np.int32)
+        yref = O.get_rows(dtype, wbytes, K, R, rid)
+    rid_dev = np.concatenate([rid, np.array([R + 5], np.int32)])
+    wb = dev.alloc(np.ascontiguousarray(wbytes).nbytes)
+    st.write(wb, 0, np.ascontiguousarray(wbytes).view(np.uint8).reshape(-1))
+    ib, yb = dev.alloc(4 * rid_dev.size), dev.alloc(4 * K * rid_dev.size)
+    st.write(ib, 0, rid_dev)
+    wt = sg.tdesc(dtype, (K, R), wb)
+    it = sg.tdesc(sg.I32, (rid_dev.size,), ib)
+    yt = sg.tdesc(sg.F32, (K, rid_dev.size), yb)
+    op, keep = sg.get_rows_op(wt, it, yt)
+    st.execute(op)
+    st.sync()
+    y = st.download(yt).reshape(rid_dev.size, K)
+    assert np.array_equal(y[:-1].view(np.uint32), np.asarray(yref).view(np.uint32))
+    assert np.array_equal(y[-1].view(np.uint32), y[1].view(np.uint32))
+    for b in (wb, ib, yb):
+        b.free()
+
+
+# ---- MUL_MAT_ID ---------------------------------------------------------------------------------
+
+def run_mid(dev, st, dtype, wbytes, K, M, E, x, ids):
+    T, nu = ids.shape
+    n1 = x.shape[1]
+    w = np.ascontiguousarray(wbytes).view(np.uint8).reshape(-1)
+    wb = dev.alloc(w.nbytes)
+    st.write(wb, 0, w)
+    wt = sg.tdesc(dtype, (K, M, E), wb)
+    xb, ib, yb = dev.alloc(x.nbytes), dev.alloc(ids.nbytes), dev.alloc(4 * M * nu * T)
+    st.write(xb, 0, np.ascontiguousarray(x, np.float32))
+    st.write(ib, 0, np.ascontiguousarray(ids, np.int32))
+    xt, it, yt = sg.tdesc(sg.F32, (K, n1, T), xb), sg.tdesc(sg.I32, (nu, T), ib), sg.tdesc(sg.F32, (M, nu, T), yb)
+    op, keep = sg.mul_mat_id_op(wt, xt, it, yt, nu)
+    st.execute(op)
+    st.sync()
+    form, grid = sg.last_launch()
+    y = st.download(yt).reshape(T, nu, M).copy()
+    for b in (wb, xb, ib, yb):
+        b.free()
+    return y, form, grid
+
+
+def test_float_mul_mat_id_golden(hip):
+    """F16 experts: the reference's golden MUL_MAT_ID (scrapgpu_ref_execute)."""
+    dev, st = hip
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "float_weights.npz"))
+    K, M, E = 72, 40, 5
+    y, form, grid = run_mid(dev, st, sg.F16, g["f16_mid_w"], K, M, E, g["f16_mid_x"], g["f16_mid_ids"])
+    T, nu = g["f16_mid_ids"].shape
+    assert form == "float rows=8 nc=1" and grid == (M + 7) // 8 * T * nu, (form, grid)
+    assert nmse(y, g["f16_mid_y"]) <= 1e-12
+
+
+@pytest.mark.parametrize("dtype", (sg.F32, sg.F16), ids=lambda d: IDS[d])
+@pytest.mark.parametrize("shared", [True, False], ids=["x_shared", "x_per_slot"])
+def test_float_mul_mat_id(hip, dtype, shared):
+    """8 experts of 200 x 1024 at 2 slots over 20 tokens (many tokens stay on the per-pair matvec for
+    float experts), against the oracle per pair; an id out of range reads the nearest expert."""
+    dev, st = hip
+    K, M, E, T, nu = 1024, 200, 8, 20, 2
+    parts = [float_weights(dtype, M, K, 7800 + e) for e in range(E)]
+    wbytes = np.concatenate([p[0].reshape(-1) for p in parts])
+    ids = np.random.default_rng(7801).integers(0, E, (T, nu)).astype(np.int32)
+    x = O.normal(T * (1 if shared else nu) * K, 7802).reshape(T, 1 if shared else nu, K)
+    ref = O.mul_mat_id(dtype, wbytes, K, M, E, x, ids)
+    ids_dev = ids.copy()
+    ids_dev[3, 1] = E + 4  # clamped to E - 1 on the device
+    y, form, _ = run_mid(dev, st, dtype, wbytes, K, M, E, x, ids_dev)
+    assert form == "float rows=8 nc=1", form
+    ids_c = np.minimum(ids_dev, E - 1)
+    ref_c = O.mul_mat_id(dtype, wbytes, K, M, E, x, ids_c)
+    for t in range(T):
+        for i in range(nu):
+            xc = x[t, i if not shared else 0][None, :]
+            check_matvec(y[t, i][None, :], ref_c[t, i][None, :], xc, parts[ids_c[t, i]][1])
+    assert np.array_equal(ref_c[0], ref[0])
