@@ -595,6 +595,47 @@ def traffic_of(kernel):
     return None if k is None else k.get("hbm_bytes_per_launch")
 
 
+def bench_float(dev, st):
+    """Float weights (natural layout, no quantization): an F16 12288x4096 decode product at one
+    column (GB/s, 4 weight copies cycled so that they stream from HBM) and F16 / BF16 prefill at 512
+    tokens (TFLOP/s)."""
+    K, M = 4096, 12288
+    w = (np.random.default_rng(9000).standard_normal(M * K, dtype=np.float32) * 0.02).reshape(M, K)
+    out = {}
+    for name, dt, bits in (("f16", sg.F16, w.astype(np.float16).view(np.uint16)),
+                           ("bf16", sg.BF16, (w.view(np.uint32) >> 16).astype(np.uint16))):
+        copies = 4 if name == "f16" else 1
+        bufs = []
+        for _ in range(copies):
+            b = dev.alloc(bits.nbytes)
+            st.write(b, 0, bits.view(np.uint8).reshape(-1))
+            bufs.append(b)
+        for N in ((1, 512) if name == "f16" else (512,)):
+            xb, yb = dev.alloc(4 * K * N), dev.alloc(4 * M * N)
+            xt, yt = sg.tdesc(sg.F32, (K, N), xb), sg.tdesc(sg.F32, (M, N), yb)
+            st.fill_normal(xt, seed=9001)
+            keep = [sg.mul_mat_op(sg.tdesc(dt, (K, M), b), xt, yt) for b in bufs]
+            st.execute(keep[0][0])
+            st.sync()
+            form = sg.last_launch()[0]
+            ms = time_plan(dev, st, [op for op, _ in keep], 10)
+            line = {"kernel": form, "us": round(ms * 1e3, 2)}
+            if N == 1:
+                line["GBps"] = round(bits.nbytes / (ms * 1e-3) / 1e9, 1)
+                line["hbm_frac"] = round(bits.nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+            else:
+                tf = 2.0 * M * K * N / (ms * 1e-3) / 1e12
+                line["TFLOPs"] = round(tf, 1)
+                line["mfma_frac"] = round(tf / F16_PEAK_TFLOPS, 4)
+            out[f"{name}_{M}x{K}_N{N}"] = line
+            xb.free()
+            yb.free()
+        for b in bufs:
+            b.free()
+    log("float weights done")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -607,6 +648,7 @@ def main():
     ap.add_argument("--no-moe", action="store_true", help="skip the MUL_MAT_ID (MoE decode and prefill) lines")
     ap.add_argument("--no-get-rows", action="store_true", help="skip the GET_ROWS line")
     ap.add_argument("--no-configs", action="store_true", help="skip the lines of BASELINE.json's other workloads")
+    ap.add_argument("--no-float", action="store_true", help="skip the float-weight (F16 / BF16) lines")
     ap.add_argument("--config-cpu-seconds", type=float, default=2.0, help="CPU reference budget per config line (at least one call)")
     ap.add_argument("--no-fuse", action="store_true", help="one MUL_MAT per weight instead of MUL_MAT_MULTI for q/k/v and gate/up")
     args = ap.parse_args()
@@ -648,6 +690,7 @@ def main():
     get_rows = None if args.no_get_rows else bench_get_rows(dev, st, 512, 5)
     cpu = None if args.no_cpu else cpu_baseline(dev, st, model, args.cpu_seconds)
     configs = None if args.no_configs else bench_configs(dev, st, 0.0 if args.no_cpu else args.config_cpu_seconds)
+    float_w = None if args.no_float else bench_float(dev, st)
 
     result = {
         "metric": "Q4_K matvec weight GB/s (% HBM peak) at bs=1; prefill TFLOP/s at M=512",
@@ -678,6 +721,7 @@ def main():
         "get_rows": get_rows,
         "cpu_baseline": cpu,
         "configs": configs,
+        "float_weights": float_w,
     }
     print(json.dumps(result), flush=True)
 
