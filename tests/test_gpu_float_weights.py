@@ -337,3 +337,49 @@ def test_float_mul_mat_id(hip, dtype, shared):
             xc = x[t, i if not shared else 0][None, :]
             check_matvec(y[t, i][None, :], ref_c[t, i][None, :], xc, parts[ids_c[t, i]][1])
     assert np.array_equal(ref_c[0], ref[0])
+
+
+def test_float_plan_replays(hip):
+    """Float-weight products recorded in a plan (a HIP graph) and replayed with new x each time: an
+    F16 decode column, a BF16 4-column product and an F16 prefill GEMM match the oracle on every
+    replay."""
+    import ctypes as C
+
+    dev, st = hip
+    L = sg.lib()
+    K = 1024
+    items = []
+    for dtype, M, N, seed in ((sg.F16, 200, 1, 7900), (sg.BF16, 96, 4, 7901), (sg.F16, 384, 128, 7902)):
+        wbytes, wf = float_weights(dtype, M, K, seed)
+        wb = dev.alloc(wbytes.nbytes)
+        st.write(wb, 0, np.ascontiguousarray(wbytes).view(np.uint8).reshape(-1))
+        xb, yb = dev.alloc(4 * K * N), dev.alloc(4 * M * N)
+        xt, yt = sg.tdesc(sg.F32, (K, N), xb), sg.tdesc(sg.F32, (M, N), yb)
+        op, keep = sg.mul_mat_op(sg.tdesc(dtype, (K, M), wb), xt, yt)
+        items.append(dict(dtype=dtype, M=M, N=N, w=wbytes, wf=wf, bufs=(wb, xb, yb), xt=xt, yt=yt, op=op, keep=keep))
+    nodes = (sg.PlanNode * len(items))(*[sg.PlanNode(C.sizeof(sg.PlanNode), it["op"], 0) for it in items])
+    pdesc = sg.PlanDesc(C.sizeof(sg.PlanDesc), nodes, len(items))
+    plan = C.c_void_p()
+    sg.check(L.scrapgpu_plan_build(dev.handle, C.byref(pdesc), C.byref(plan)), "plan_build")
+    try:
+        for rep in range(3):
+            xs = []
+            for i, it in enumerate(items):
+                x = O.normal(it["N"] * K, 7950 + 10 * rep + i).reshape(it["N"], K)
+                st.upload(it["xt"], x)
+                xs.append(x)
+            st.sync()
+            sg.check(L.scrapgpu_plan_execute(st.handle, plan), "plan_execute")
+            st.sync()
+            for it, x in zip(items, xs):
+                y = st.download(it["yt"]).reshape(it["N"], it["M"])
+                ref = O.mul_mat(it["dtype"], it["w"], K, it["M"], x)
+                if it["N"] > 8:
+                    assert nmse(y, ref) <= PREFILL_NMSE[it["dtype"]], f"replay {rep}"
+                else:
+                    check_matvec(y, ref, x, it["wf"])
+    finally:
+        sg.check(L.scrapgpu_plan_free(plan), "plan_free")
+        for it in items:
+            for b in it["bufs"]:
+                b.free()
