@@ -68,3 +68,23 @@ def test_static_scratch_refuses_large_ops(hip):
     assert b"static scratch" in sg.lib().scrapgpu_last_error()
     for b in (wb, xb, yb):
         b.free()
+
+
+def test_static_scratch_float_weights(hip):
+    """F16 weights: the 64-column GEMM (x in the static scratch) and the one-column matvec (no
+    scratch) equal scrapgpu_op_execute bit for bit, on two calls in a row."""
+    dev, st = hip
+    K, M = 2048, 512
+    w = O.normal(M * K, 1510, 0.0, 0.02).astype(np.float16).view(np.uint16)
+    wb = dev.alloc(w.nbytes)
+    st.write(wb, 0, w.view(np.uint8).reshape(-1))
+    wt = sg.tdesc(sg.F16, (K, M), wb)
+    for N in (64, 1):
+        x = O.normal(N * K, 1511 + N).reshape(N, K)
+        y_static = _run(dev, st, wt, x, M, True)
+        y_plain = _run(dev, st, wt, x, M, False)
+        assert np.array_equal(y_static.view(np.uint32), y_plain.view(np.uint32)), f"N={N}: outputs differ"
+        ref = O.mul_mat(sg.F16, w, K, M, x, threads=8)
+        e = float(np.sum((y_static.astype(np.float64) - ref) ** 2) / np.sum(ref.astype(np.float64) ** 2))
+        assert e <= (1e-10 if N == 1 else 1e-6), f"N={N}: NMSE {e:.3e}"
+    wb.free()
