@@ -1573,14 +1573,16 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
                 c.sk = true;
                 return c;
             }
-            // ... else K split over work-groups of 384-row tiles when that occupies 3/4 of the CUs
-            // or more in one round with >= 16 stages per split (the largest such split; partials
-            // added by k_split_reduce). (4096x12288 at 512 tokens: 5 splits, 88 against 95 us per
-            // op with the 64-token form's 3 K groups; 6144x4096 at 2 splits on half the CUs lost,
-            // 60 against 51)
+            // ... else K split over work-groups of 384-row tiles when that occupies 2/3 of the CUs
+            // or more in one round with >= 16 stages per split (the fewest such splits: the GEMM is
+            // bound by its loads there, so more work-groups gain little and every split adds
+            // partial sums for k_split_reduce). (4096x12288 at 512 tokens, 44 tiles: 3 / 4 / 5 / 6
+            // splits 99 / 88 / 89 / 111 us per op, Q8_0 11008x4096 102 / 92 / 95 / 112, against 95
+            // and 92 for the 64-token form's 3 K groups; 6144x4096 at 2 splits on half the CUs
+            // lost, 60 against 51)
             if (env_kg != 2 && slices == 1 && (a.M % 384 == 0 || a.M >= 8 * 384))
-                for (int sp = 8; sp >= 2; --sp)
-                    if (tw * sp <= cu_count && 4 * tw * sp >= 3 * cu_count && stages / sp >= 16) {
+                for (int sp = 2; sp <= 8; ++sp)
+                    if (tw * sp <= cu_count && 3 * tw * sp >= 2 * cu_count && stages / sp >= 16) {
                         c.kg = 1;
                         c.split = sp;
                         return c;
