@@ -103,12 +103,17 @@ __device__ __forceinline__ float half_bits(uint32_t h) {
     return __half2float(__ushort_as_half((unsigned short) (h & 0xFFFFu)));
 }
 
+// weight loads are non-temporal: every weight byte is read once per product, so it should not
+// displace what the caches hold for the next launches (x, y, the counts). Measured on the Qwen3-8B
+// decode token: 1.237 -> 1.153 ms (3.54 -> 3.79 TB/s; gate+up 12.9 -> 11.4 us, q+k+v 6.1 -> 5.3)
+typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 load16(const uint8_t * p) {
-    return *reinterpret_cast<const uint4 *>(p);
+    const u32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 __device__ __forceinline__ uint32_t load_half(const uint8_t * p) {
-    return *reinterpret_cast<const uint16_t *>(p);
+    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
 }
 
 __device__ __forceinline__ v4i as_v4i(uint4 q) {

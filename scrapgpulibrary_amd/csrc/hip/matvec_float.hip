@@ -45,21 +45,29 @@ struct MvfArgs {
     int has_id;
 };
 
+// 16 bytes of weights, non-temporal (read once per product, as in the quantized matvec)
+typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld16_nt(const uint8_t * p) {
+    const u32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // 8 consecutive weights of one row as f32 (p 16-byte aligned)
 template <int WT> struct WLoad;
 template <> struct WLoad<F32> {
-    float4 u, v;
+    uint4 u, v;
     __device__ void load(const uint8_t * p) {
-        u = *reinterpret_cast<const float4 *>(p);
-        v = *reinterpret_cast<const float4 *>(p + 16);
+        u = ld16_nt(p);
+        v = ld16_nt(p + 16);
     }
     __device__ void to_f32(float * o) const {
-        o[0] = u.x, o[1] = u.y, o[2] = u.z, o[3] = u.w, o[4] = v.x, o[5] = v.y, o[6] = v.z, o[7] = v.w;
+        o[0] = __uint_as_float(u.x), o[1] = __uint_as_float(u.y), o[2] = __uint_as_float(u.z), o[3] = __uint_as_float(u.w);
+        o[4] = __uint_as_float(v.x), o[5] = __uint_as_float(v.y), o[6] = __uint_as_float(v.z), o[7] = __uint_as_float(v.w);
     }
 };
 template <> struct WLoad<F16> {
     uint4 q;
-    __device__ void load(const uint8_t * p) { q = *reinterpret_cast<const uint4 *>(p); }
+    __device__ void load(const uint8_t * p) { q = ld16_nt(p); }
     __device__ void to_f32(float * o) const {
         const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
@@ -71,7 +79,7 @@ template <> struct WLoad<F16> {
 };
 template <> struct WLoad<BF16> {
     uint4 q;
-    __device__ void load(const uint8_t * p) { q = *reinterpret_cast<const uint4 *>(p); }
+    __device__ void load(const uint8_t * p) { q = ld16_nt(p); }
     __device__ void to_f32(float * o) const {
         const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
