@@ -1600,7 +1600,8 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     L.nck = 1;
     L.part = nullptr;
     L.arrive = nullptr;
-    if (nc == 1 && L.xvec && scratch != nullptr && arrive != nullptr && chunk_form(mats, nmat, id) && rows >= (int64_t) 64 * cu_count &&
+    if (nc == 1 && L.xvec && scratch != nullptr && arrive != nullptr && chunk_form(mats, nmat, id) &&
+        rows >= (int64_t) tuning("SCRAPGPU_HIP_MV_CHUNK_ROWS", 64) * cu_count &&
         tuning("SCRAPGPU_HIP_MV_BURST", 1)) {
         // a long K in chunks of kChunkSteps steps over 8-wave work-groups of 16 rows, once there
         // are 4 row tiles per CU: the chunks' hand-over (partial-sum stores, the arrival count,
@@ -1624,10 +1625,12 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     }
     if (nc == 1 && L.xvec && nst <= 64 && tuning("SCRAPGPU_HIP_MV_BURST", 1)) {
         // (the 32-row Q8_0 / Q6_K forms need more registers than 5 waves per SIMD leave them)
-        // 48-row tiles once they give every CU two work-groups (one round at 4 waves per SIMD)
+        // 48-row tiles once they give every CU two work-groups (one round at 4 waves per SIMD),
+        // 32-row ones from 24 rows per CU (with the non-temporal weight loads the Q4_K q/k/v
+        // launch, 6144 rows, 5.06 against 5.28 us on 16-row tiles; o at 4096 rows stays on 16)
         const bool q4 = dt == Q4_K || dt == Q4_0;
         // (past 32 steps of K, 16-row tiles: the 32- and 48-row forms spill at 3-4 steps per wave)
-        int rg = q4 && rows * slices >= (int64_t) 96 * cu_count ? 3 : q4 && rows * slices >= (int64_t) 64 * cu_count ? 2 : 1;
+        int rg = q4 && rows * slices >= (int64_t) 96 * cu_count ? 3 : q4 && rows * slices >= (int64_t) tuning("SCRAPGPU_HIP_MV_RG2_ROWS", 24) * cu_count ? 2 : 1;
         if (const int fr = tuning("SCRAPGPU_HIP_MV_RG", 0)) rg = fr >= 3 ? 3 : fr >= 2 ? 2 : 1;
         if (nst > 32) rg = 1; // (also over the override)
         // 3 steps per wave for 33..48 steps (16 waves: no wave loads a step it does not use)

@@ -153,7 +153,7 @@ def test_burst_multi_row_tiles_ragged(hip, dtype, rg):
     M = (32 if rg == 2 else 48) * cus(hip) + 40  # rows * 1 slice >= 32 rg CUs, last R32 group of 8 rows
     q, _, wt = weights(hip, dtype, K, M, 400 + rg)
     x = O.normal(K, 41).reshape(1, K)
-    # alone: M rows select rg = 2 for M >= 64 CUs only; 2 M rows as MULTI select rg
+    # alone and as MULTI the row count per CU selects the tile height (32 rows from 24 per CU, 48 from 96)
     (y,), (form, grid) = run(hip, [wt], x)
     assert form.startswith("burst"), form
     check(dtype, q, K, M, x, y, f"{sg.NAMES[dtype]} {M}x{K} [{form}]")
