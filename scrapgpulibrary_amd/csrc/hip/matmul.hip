@@ -429,8 +429,9 @@ template <> struct PFmt<Q4_0> {
 };
 
 // F16 / BF16 rows in the natural layout (float weights, K a multiple of the 128-element stage):
-// stage s = elements 128 s .. + 127 of the row; k-half h takes elements 64 h .. + 63 (eight
-// 16-byte chunks, contiguous), k-step t its chunk t. The pairs are reordered to the x tile's
+// stage s = elements 128 s .. + 127 of the row; k-step t takes elements 16 t .. + 15, k-half h
+// the 16-byte chunk 2 t + h of them: the two lanes of a row read 32 contiguous bytes per load, so a
+// wave's load touches 32 cache lines instead of 64 (as 8 chunks per lane, contiguous). The pairs are reordered to the x tile's
 // element order 0 2 1 3 of each group of 4. BF16 feeds the bf16 MFMA (x then in bf16, see
 // k_x_to_f16), F16 the f16 one; neither needs scales.
 template <int DT> struct PFmtFloat {
@@ -443,13 +444,13 @@ template <int DT> struct PFmtFloat {
     // (nb: the row stride in bytes for float weights)
     __device__ void init(int64_t, int64_t nb, const RowAddr & ra, int h_) {
         h = h_;
-        ro = (uint32_t) ((ra.g0 + ra.lr) * nb) + 128 * (uint32_t) h_;
+        ro = (uint32_t) ((ra.g0 + ra.lr) * nb) + 16 * (uint32_t) h_;
     }
     __device__ Raw load(const uint8_t * w, int s) const {
         const uint8_t * p = w + (ro + (uint32_t) s * 256);
         Raw r;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) r.q[i] = load16(p + 16 * i);
+        for (int i = 0; i < 8; ++i) r.q[i] = load16(p + 32 * i);
         return r;
     }
     __device__ Raw load_half2(const uint8_t * w, int s, const Raw &) const { return load(w, s); }
@@ -461,7 +462,7 @@ template <int DT> struct PFmtFloat {
         return __builtin_bit_cast(f16x8, o);
     }
     __device__ static int chunk(int h, int t) {
-        return 8 * h + t;
+        return 2 * t + h;
     }
 };
 template <> struct PFmt<F16> : PFmtFloat<F16> {};
@@ -1096,7 +1097,7 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
             if (t < 7) bn = F::bop(cw, sc, t + 1);
 #pragma unroll
             for (int q = 0; q < NF; ++q) {
-                acc[q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[q], b, acc[q], 0, 0, 0);
+                acc[q] = mma32<DT>(a[q], b, acc[q]);
                 if (t < 7) a[q] = *reinterpret_cast<const f16x8 *>(X + q * 32 * XR + 8 * F::chunk(h, t + 1));
             }
             if (t < 7) b = bn;
@@ -1498,17 +1499,49 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
     static const int env_w = env_int("SCRAPGPU_HIP_MM_W", 0);
     MmConfig c;
     if (a.dtype == F16 || a.dtype == BF16) {
-        // 4-wave work-groups, 128-token tiles from 128 tokens on (each 2-byte weight fetched half as
-        // often: 12288x4096 at 512 tokens 119 against 137 us, at 256 tokens 81 against 92), K split
-        // while the tiles leave work-group slots empty, every split >= 8 stages
+        // the wide GEMM (k_gemm_w, 384-row x 128-token tiles; its 2-K-group form spills with the
+        // float rows' raw data) where its tiles fill the CUs, or with K split so that they occupy
+        // 2/3 of them or more in one round, >= 16 stages per split
+        static const int env_wide = env_int("SCRAPGPU_HIP_MM_WIDE", 1);
+        if (env_wide != 0 && env_w == 0 && env_bn == 0 && env_split <= 1 && a.K % BK == 0 && a.N >= 128 &&
+            (a.N + 127) / 128 * 128 * 8 <= 9 * a.N && (a.M % 384 == 0 || a.M >= 8 * 384)) {
+            const int64_t tw = (a.M + 383) / 384 * ((a.N + 127) / 128) * slices;
+            c.w = 12;
+            c.kg = 1;
+            c.rg = 1;
+            c.bn = 128;
+            c.wide = true;
+            c.split = 1;
+            if (tw % cu_count == 0 || tw >= 4 * (int64_t) cu_count) return c;
+            if (slices == 1) // (at most 2 splits: 3 and 4 measured slower than the 4-wave form)
+                for (int sp = 2; sp <= 2; ++sp)
+                    if (tw * sp <= cu_count && 3 * tw * sp >= 2 * cu_count && stages / sp >= 16) {
+                        c.split = sp;
+                        return c;
+                    }
+            c.wide = false;
+        }
+        // else 4-wave work-groups, 128-token tiles from 128 tokens on (each 2-byte weight fetched
+        // half as often: 12288x4096 at 512 tokens 119 against 137 us, at 256 tokens 81 against 92)
         c.w = 4;
         c.kg = 1;
         c.rg = 1;
         const int64_t tm = (a.M + 127) / 128;
         c.bn = env_bn == 64 || env_bn == 128 ? env_bn : a.N >= 128 ? 128 : 64;
-        const int64_t tiles = tm * ((a.N + c.bn - 1) / c.bn) * slices, want = (int64_t) cu_count * occupancy_of(a.dtype, c.bn, 1);
+        const int64_t tiles = tm * ((a.N + c.bn - 1) / c.bn) * slices;
+        // the split with the least estimated time: rounds of cu_count work-groups x (stages per
+        // split + 4, a work-group's fixed cost in stages), the fewer splits on a tie, every split
+        // >= 8 stages (F16, 128-token tiles, measured on 256 CUs: 12288x4096 at 128 tokens, 96
+        // tiles, 55.7 / 64.6 / 56.3 / 62.4 us at 2 / 3 / 4 / 8 splits; 4096x4096, 32 tiles, 31 us
+        // at 8 against 36 at 4; 12288x4096 at 256 tokens 78 us unsplit against 80-87 split)
         c.split = 1;
-        while (tiles * c.split < want && stages / (c.split + 1) >= 8 && c.split < 8) ++c.split;
+        if (env_split > 0) {
+            c.split = (int) std::max<int64_t>(1, std::min<int64_t>(std::min(env_split, 8), (stages + 3) / 4));
+            return c;
+        }
+        auto cost = [&](int sp) { return (tiles * sp + cu_count - 1) / cu_count * ((stages + sp - 1) / sp + 4); };
+        for (int sp = 2; sp <= 8 && stages / sp >= 8; ++sp)
+            if (cost(sp) < cost(c.split)) c.split = sp;
         return c;
     }
     // 12-wave work-groups, one per CU, in this order of preference:
@@ -1641,10 +1674,11 @@ void * kernel_of(const MmConfig & c) {
     return c.bn == 64 ? (void *) k_matmul<DT, 64, 2, 4, 1> : (void *) k_matmul<DT, 128, 2, 4, 1>;
 }
 
-// float weights: the 4-wave 64-token kernel only (their raw rows take the registers the wider
-// forms need)
+// float weights: the wide GEMM's 12-row-wave form (K split or not), else the 4-wave kernel (their
+// raw rows take the registers that its 12-wave and 2-K-group forms need)
 template <int DT>
 void * kernel_of_float(const MmConfig & c) {
+    if (c.wide) return c.kg == 2 ? (void *) k_gemm_w<DT, 2> : (void *) k_gemm_w<DT, 1>;
     return c.bn == 64 ? (void *) k_matmul<DT, 64, 1, 4, 1> : (void *) k_matmul<DT, 128, 1, 4, 1>;
 }
 

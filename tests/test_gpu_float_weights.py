@@ -203,6 +203,28 @@ def test_float_prefill_gemm(hip, dtype, K, M, N):
     assert e <= PREFILL_NMSE[dtype], f"{IDS[dtype]} {M}x{K} N={N}: NMSE {e:.3e} [{form}]"
 
 
+@pytest.mark.parametrize("dtype", (sg.F16, sg.BF16), ids=lambda d: IDS[d])
+@pytest.mark.parametrize("K,M,N,split", [(1024, 24536, 500, 1), (4096, 12288, 380, 2)], ids=["fill", "k_split"])
+def test_float_prefill_wide_gemm(hip, dtype, K, M, N, split):
+    """F16 / BF16 on the wide GEMM (384-row x 128-token tiles, one 12-wave work-group per CU): a
+    ragged shape whose tiles fill the CUs (the last row tile and token tile part empty), and one
+    with K split over 2 work-groups per tile (96 tiles, the last token tile part empty; partials
+    added by the split reduce)."""
+    dev, st = hip
+    wbytes, wf = float_weights(dtype, M, K, 7700 + K + N)
+    x = O.normal(N * K, 7701 + N).reshape(N, K)
+    x[:, ::41] *= 100.0
+    y = run(dev, st, dtype, wbytes, K, M, x, check_form=False)
+    form, _ = sg.last_launch()
+    if dev.info().compute_units == 256:
+        assert form.startswith(f"gemm wide w=12 kg=1 bn=128 rg=1 split={split}"), form
+    else:
+        assert form.startswith("gemm"), form
+    ref = O.mul_mat(dtype, wbytes, K, M, x, threads=8)
+    e = nmse(y, ref)
+    assert e <= PREFILL_NMSE[dtype], f"{IDS[dtype]} {M}x{K} N={N}: NMSE {e:.3e} [{form}]"
+
+
 @pytest.mark.parametrize("dtype,K,N", [(sg.F32, 1024, 20), (sg.F16, 520, 17), (sg.BF16, 72, 33)], ids=["f32", "f16_k520", "bf16_k72"])
 def test_float_prefill_column_groups(hip, dtype, K, N):
     """F32 weights and K not a multiple of 128: exact products, 8 columns per launch."""
