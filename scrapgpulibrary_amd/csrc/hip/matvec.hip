@@ -90,7 +90,7 @@ struct MvArgs {
     int64_t ids_s0, ids_s1, n_used, n_exp;
     int x_shared;
     // chunked burst (k_mvb with CHUNK): blockIdx.y is the K chunk (kChunkSteps steps each); part:
-    // [chunk][tile * 16 + row] partial sums; arrive: chunks done per row tile, zero between
+    // [chunk][tile * 16 RG + row] partial sums; arrive: chunks done per row tile, zero between
     // launches (the last chunk of a tile resets its count)
     int64_t nck;
     float * part;
@@ -612,13 +612,13 @@ __device__ __forceinline__ void reduce_store(const MvArgs & A, const Where & wh,
 
 // Burst form (one column, <= SPW steps per wave, one tile of 16 * RG rows per work-group): the wave
 // first loads its x range, then issues every weight load, and only then converts x.
-// CHUNK (one slice, 16-row tiles, W x SPW = kChunkSteps): work-group (tile, c) takes chunk c of K,
+// CHUNK (one slice, W x SPW = kChunkSteps): work-group (tile, c) takes chunk c of K,
 // so that a long K runs on several small work-groups instead of one large one per tile. The
 // chunks' partial sums meet as in k_mvc: agent-scope stores, an arrival count per tile, and the
 // last chunk to arrive adds them in chunk order and resets the count.
 template <int DT, int RG, int W, int SPW, bool CHUNK = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2 && RG == 1 ? 6 : SPW <= 2 && RG == 2 ? 5 : 4, 8))) void k_mvb(MvArgs A) {
-    static_assert(!CHUNK || (RG == 1 && W * SPW == kChunkSteps), "chunks of kChunkSteps on 16-row tiles");
+    static_assert(!CHUNK || W * SPW == kChunkSteps, "chunks of kChunkSteps steps");
     using F = Fmt<DT>;
     using Raw = typename F::Raw;
     extern __shared__ uint8_t lds[];
@@ -687,20 +687,24 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2
         reduce_store<RG, 1, W>(A, wh, row, acc, red, tid);
     } else {
         // the waves' sums of the chunk (as reduce_store), then the chunks' through memory
+        constexpr int R = 16 * RG;
         const int r = lane & 15;
-        float v = acc[0][0];
-        v += __shfl_xor(v, 16);
-        v += __shfl_xor(v, 32);
-        if (lane < 16) red[wave * 16 + r] = v;
+#pragma unroll
+        for (int i = 0; i < RG; ++i) {
+            float v = acc[i][0];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            if (lane < 16) red[wave * R + 16 * i + r] = v;
+        }
         __syncthreads();
         const int64_t tile = blockIdx.x;
-        if (tid < 16) {
+        if (tid < R) {
             float t = 0.0f;
 #pragma unroll
-            for (int w2 = 0; w2 < W; ++w2) t += red[w2 * 16 + tid];
+            for (int w2 = 0; w2 < W; ++w2) t += red[w2 * R + tid];
             // visible to every XCD before the tile's count moves (agent-scope stores write
             // through the L2; then this wave waits for them)
-            __hip_atomic_store(A.part + (int64_t) blockIdx.y * A.tiles * 16 + tile * 16 + tid, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(A.part + ((int64_t) blockIdx.y * A.tiles + tile) * R + tid, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
         }
         uint32_t & last = *reinterpret_cast<uint32_t *>(zpad + 16);
@@ -709,11 +713,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2
         // the last chunk of the tile to arrive adds all of them in chunk order (agent-scope loads:
         // the other chunks' sums may come from other XCDs) and leaves the count at zero for the
         // next launch
-        if (last && tid < 16) {
+        if (last && tid < R) {
             const int64_t m = row.m0 + tid;
             float t = 0.0f;
             for (int64_t c = 0; c < A.nck; ++c)
-                t += __hip_atomic_load(A.part + c * A.tiles * 16 + tile * 16 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                t += __hip_atomic_load(A.part + (c * A.tiles + tile) * R + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (m < row.M) A.y[row.j][m] = t;
             if (tid == 0) __hip_atomic_store(A.arrive + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -1520,7 +1524,8 @@ static bool chunk_form(const MatArgs * mats, int nmat, const IdArgs * id) {
 static size_t chunk_part_bytes(const MatArgs * mats, int nmat) {
     const int64_t nst = (mats[0].K + kStep - 1) / kStep, nck = (nst + kChunkSteps - 1) / kChunkSteps;
     int64_t tiles = 0;
-    for (int j = 0; j < nmat; ++j) tiles += (mats[j].M + 15) / 16;
+    // (rows of each matrix rounded up to its 16-, 32- or 48-row tiles: at most 32 past 16-row ones)
+    for (int j = 0; j < nmat; ++j) tiles += (mats[j].M + 15) / 16 + 2;
     return ((size_t) nck * (size_t) tiles * 16 * sizeof(float) + 255) / 256 * 256;
 }
 
@@ -1608,17 +1613,22 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         // the last chunk's loads) adds dependent memory round trips at the end of the launch,
         // which cost more than smaller work-groups save below that (Q6_K 4096 x 12288: 11.8
         // against 10.7 us; Q4_K 28672 x 8192: 30.7 against 32.1 us)
-        set_tiles(L, mats, nmat, 16);
+        // (Q4 products: 48-row tiles, three row groups sharing each x operand, from 96 rows per CU)
+        const bool q4 = dt == Q4_K || dt == Q4_0;
+        int rg = q4 && rows >= (int64_t) 96 * cu_count ? 3 : 1;
+        if (const int fr = tuning("SCRAPGPU_HIP_MV_CHUNK_RG", 0)) rg = q4 && fr >= 3 ? 3 : q4 && fr == 2 ? 2 : 1;
+        set_tiles(L, mats, nmat, 16 * rg);
         L.nck = (nst + kChunkSteps - 1) / kChunkSteps;
         L.part = reinterpret_cast<float *>(scratch);
         L.arrive = arrive;
         constexpr int W = 8, sp = 2;
-        const size_t lds = (size_t) W * sp * kSegs * (sizeof(XSeg) + sizeof(float4)) + (size_t) W * 16 * sizeof(float) + 32;
-        void * fn = dt == Q4_0 ? (void *) k_mvb<Q4_0, 1, W, sp, true> : dt == Q8_0 ? (void *) k_mvb<Q8_0, 1, W, sp, true>
-                  : dt == Q4_K ? (void *) k_mvb<Q4_K, 1, W, sp, true> : (void *) k_mvb<Q6_K, 1, W, sp, true>;
+        const size_t lds = (size_t) W * sp * kSegs * (sizeof(XSeg) + sizeof(float4)) + (size_t) W * 16 * rg * sizeof(float) + 32;
+        void * fn = dt == Q8_0 ? (void *) k_mvb<Q8_0, 1, W, sp, true> : dt == Q6_K ? (void *) k_mvb<Q6_K, 1, W, sp, true>
+                  : dt == Q4_0 ? (rg == 3 ? (void *) k_mvb<Q4_0, 3, W, sp, true> : rg == 2 ? (void *) k_mvb<Q4_0, 2, W, sp, true> : (void *) k_mvb<Q4_0, 1, W, sp, true>)
+                               : (rg == 3 ? (void *) k_mvb<Q4_K, 3, W, sp, true> : rg == 2 ? (void *) k_mvb<Q4_K, 2, W, sp, true> : (void *) k_mvb<Q4_K, 1, W, sp, true>);
         const uint64_t grid = (uint64_t) L.tiles * (uint64_t) L.nck;
         if (grid_size) *grid_size = grid;
-        std::snprintf(last_form().form, sizeof(last_form().form), "burst-chunks rg=1 W=%d spw=%d chunks=%d", W, sp, (int) L.nck);
+        std::snprintf(last_form().form, sizeof(last_form().form), "burst-chunks rg=%d W=%d spw=%d chunks=%d", rg, W, sp, (int) L.nck);
         last_form().grid = grid;
         void * args[] = {&L};
         return hipLaunchKernel(fn, dim3((unsigned) L.tiles, (unsigned) L.nck), dim3((unsigned) (64 * W)), args, lds, stream);

@@ -194,10 +194,11 @@ def test_config5_q6_k_lm_head(hip, N):
 
 def test_config5_q4_k_70b_mlp(hip):
     """the 70B-class Q4_K MLP matrix, W 28672 x 8192, at batch 1 (32 steps of K: two
-    chunks of 16 steps on 16-row tiles)."""
+    chunks of 16 steps on 48-row tiles, 16-row ones below 96 rows per CU)."""
     K, M = 8192, 28672
     q, _, wt = weights(hip, sg.Q4_K, K, M, 800)
     x = O.normal(K, 80).reshape(1, K)
     (y,), (form, grid) = run(hip, [wt], x)
-    assert form.startswith("burst-chunks rg=1 W=8 spw=2 chunks=2"), form
+    rg = 3 if M >= 96 * cus(hip) else 1
+    assert form.startswith(f"burst-chunks rg={rg} W=8 spw=2 chunks=2"), form
     check(sg.Q4_K, q, K, M, x, y, f"Q4_K {M}x{K} N=1 [{form}]")

@@ -162,17 +162,21 @@ def test_matvec_decode_three_steps_per_wave(hip, dtype, K):
     check_matvec(y, ref, x, deq)
 
 
-@pytest.mark.parametrize("dtype,K", [(sg.Q4_0, 12288), (sg.Q4_K, 12288), (sg.Q6_K, 11008), (sg.Q8_0, 4352)],
-                         ids=["q4_0", "q4_k", "q6_k_partial_chunk", "q8_0_one_step_chunk"])
-def test_matvec_decode_long_k_chunks(hip, dtype, K):
+@pytest.mark.parametrize("dtype,K,rpc", [(sg.Q4_0, 12288, 64), (sg.Q4_K, 12288, 64), (sg.Q6_K, 11008, 64), (sg.Q8_0, 4352, 64),
+                                         (sg.Q4_0, 8192, 96), (sg.Q4_K, 12288, 96), (sg.Q6_K, 8192, 96)],
+                         ids=["q4_0", "q4_k", "q6_k_partial_chunk", "q8_0_one_step_chunk", "q4_0_48_row_tiles", "q4_k_48_row_tiles",
+                              "q6_k_many_rows"])
+def test_matvec_decode_long_k_chunks(hip, dtype, K, rpc):
     """N = 1 with K past 16 steps and 4 row tiles per CU: K in chunks of 16 steps over 8-wave
-    work-groups of 16 rows, the
+    work-groups of 16 rows (48 rows for Q4_0 / Q4_K from 96 rows per CU), the
     chunks' partial sums added by the last chunk of each row tile to arrive, which resets its
     count. Three launches in a row (the counts must be back at zero after each), each against the
     oracle and bit for bit equal to the first; K = 11008 ends in a chunk of 11 steps, K = 4352 in
-    a chunk of one step. The launch shape is pinned."""
+    a chunk of one step; the row count leaves a partial last tile and a last R32 group of 8 rows.
+    The launch shape is pinned."""
     dev, st = hip
-    M = 64 * dev.info().compute_units + 40 # 4 row tiles per CU (where chunks start), a partial last one
+    M = rpc * dev.info().compute_units + 40 # 4 (or 6) row tiles per CU (where chunks start), a partial last one
+    rg = 3 if rpc >= 96 and dtype in (sg.Q4_0, sg.Q4_K) else 1
     q0, d0 = quantized(dtype, K, 96, 950)   # 96 rows, repeated (rows are independent)
     reps = -(-M // 96)
     q, deq = np.tile(q0, reps)[: M * (q0.size // 96)], np.tile(d0, (reps, 1))[:M]
@@ -183,11 +187,45 @@ def test_matvec_decode_long_k_chunks(hip, dtype, K):
         y = run_mul_mat(dev, st, dtype, q, K, M, x)
         form, grid = sg.last_launch()
         nck = -(-(K // 256) // 16)
-        assert form == f"burst-chunks rg=1 W=8 spw=2 chunks={nck}" and grid == (M + 15) // 16 * nck, (form, grid)
+        assert form == f"burst-chunks rg={rg} W=8 spw=2 chunks={nck}" and grid == -(-M // (16 * rg)) * nck, (form, grid)
         check_matvec(y, ref, x, deq)
         if first is None:
             first = y
         assert np.array_equal(y.view(np.uint32), first.view(np.uint32))
+
+
+def test_matvec_decode_long_k_chunks_multi(hip):
+    """The chunked burst on 48-row tiles over a MUL_MAT_MULTI of two Q4_K weights (K = 8192, 32
+    steps: 2 chunks) whose first weight ends inside a tile: each weight against the oracle, on two
+    launches in a row."""
+    dev, st = hip
+    cus = dev.info().compute_units
+    K, Ms = 8192, (48 * cus + 20, 48 * cus + 8)
+    x = O.normal(K, 960).reshape(1, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, 1), xb)
+    st.upload(xt, x)
+    bufs, wts, yts, refs = [xb], [], [], []
+    for i, M in enumerate(Ms):
+        q0, d0 = quantized(sg.Q4_K, K, 96, 961 + i)
+        reps = -(-M // 96)
+        q, deq = np.tile(q0, reps)[: M * (q0.size // 96)], np.tile(d0, (reps, 1))[:M]
+        wb, wt = upload_weights(dev, st, sg.Q4_K, q, K, M)
+        yb = dev.alloc(4 * M)
+        bufs += [wb, yb]
+        wts.append(wt)
+        yts.append(sg.tdesc(sg.F32, (M, 1), yb))
+        refs.append((O.mul_mat(sg.Q4_K, q, K, M, x, threads=8), deq))
+    op, keep = sg.multi_op(wts, xt, yts)
+    for _ in range(2):
+        st.execute(op)
+        st.sync()
+        form, grid = sg.last_launch()
+        assert form == "burst-chunks rg=3 W=8 spw=2 chunks=2" and grid == sum(-(-M // 48) for M in Ms) * 2, (form, grid)
+        for yt, (ref, deq) in zip(yts, refs):
+            check_matvec(st.download(yt).reshape(1, -1), ref, x, deq)
+    for b in bufs:
+        b.free()
 
 
 @pytest.mark.parametrize("dtype", [sg.Q4_0, sg.Q4_K], ids=["q4_0", "q4_k"])
