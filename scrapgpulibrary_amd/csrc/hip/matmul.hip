@@ -1175,7 +1175,33 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
     // KG = 2: each group finishes half of the token fragments, QB .. QB + QN: it hands the other
     // half of its sums to the other group through LDS (the x buffers are free now) and adds the
     // other group's half of its own (a + b = b + a exactly: no order to keep), so both groups store
-    constexpr int QN = NF / KG;
+    // KG = 3: groups 1 and 2 hand all their sums to group 0 through LDS, which adds them in group
+    // order and stores every fragment
+    constexpr int QN = KG == 3 ? NF : NF / KG;
+    auto finish3 = [&]() __attribute__((always_inline)) {
+        constexpr int PER = NF * 16;
+        float * red = reinterpret_cast<float *>(lds_mm);
+        __syncthreads();
+        if (kg > 0) {
+            float * r = red + ((size_t) ((kg - 1) * RW + wave) * PER) * 64 + lane;
+#pragma unroll
+            for (int q = 0; q < NF; ++q)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) r[(q * 16 + v) * 64] = acc[q][v];
+        }
+        __syncthreads();
+        if (kg == 0) {
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const float * o = red + ((size_t) (g * RW + wave) * PER) * 64 + lane;
+#pragma unroll
+                for (int q = 0; q < NF; ++q)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[q][v] += o[(q * 16 + v) * 64];
+            }
+            store_out(std::integral_constant<int, 0>{}, std::integral_constant<int, NF>{});
+        }
+    };
     auto finish = [&](auto gtag) __attribute__((always_inline)) {
         // (the group's fragments as a compile-time range: registers cannot be indexed at run time)
         constexpr int G = decltype(gtag)::value, QB = G * QN;
@@ -1197,7 +1223,8 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
         }
         store_out(std::integral_constant<int, QB>{}, std::integral_constant<int, QN>{});
     };
-    if (KG == 1 || kg == 0) finish(std::integral_constant<int, 0>{});
+    if constexpr (KG == 3) finish3();
+    else if (KG == 1 || kg == 0) finish(std::integral_constant<int, 0>{});
     else finish(std::integral_constant<int, 1>{});
     };
     if constexpr (SK) {
@@ -1642,8 +1669,22 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
         }
         if (free_choice) {
             if (s12 == 1 && env_kg != 2 && env_kg != 3) { c.kg = 1; return c; }
-            if (fits2 && env_kg != 1 && env_kg != 3) { c.kg = 2; return c; }
-            if (fits3 && env_kg != 1 && env_kg != 2) { c.kg = 3; return c; }
+            if (fits2 && env_kg != 1 && env_kg != 3) {
+                // the same 192-row x 64-token tiles on the wide GEMM's 2-K-group form where K is a
+                // whole number of stages (x tiles straight into LDS, the exact Q4_K form):
+                // 6144x4096 at 512 tokens 46.0-46.5 against 50.9-51.9 us, 12288x4096 at 256 tokens
+                // 45.1-45.3 against 50.2
+                c.kg = 2;
+                if (env_wide != 0 && a.K % BK == 0) c.wide = true;
+                return c;
+            }
+            if (fits3 && env_kg != 1 && env_kg != 2) {
+                // (on the wide GEMM's 3-K-group form where K is a whole number of stages: 4096x4096
+                // at 512 tokens 38.1-41.3 against 41.4-41.9 us)
+                c.kg = 3;
+                if (env_wide != 0 && a.K % BK == 0) c.wide = true;
+                return c;
+            }
             if (s12 > 1 && env_kg != 2 && env_kg != 3) { c.kg = 1; c.split = s12; return c; }
         }
     }
@@ -1668,7 +1709,7 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
 template <int DT>
 void * kernel_of(const MmConfig & c) {
     if (c.sk) return (void *) k_gemm_w<DT, 1, 4, true>;
-    if (c.wide) return c.bn == 64 ? (void *) k_gemm_w<DT, 1, 2> : c.kg == 2 ? (void *) k_gemm_w<DT, 2> : (void *) k_gemm_w<DT, 1>;
+    if (c.wide) return c.bn == 64 ? (c.kg == 3 ? (void *) k_gemm_w<DT, 3, 2> : c.kg == 2 ? (void *) k_gemm_w<DT, 2, 2> : (void *) k_gemm_w<DT, 1, 2>) : c.kg == 2 ? (void *) k_gemm_w<DT, 2> : (void *) k_gemm_w<DT, 1>;
     if (c.w == 12) return c.kg == 3 ? (void *) k_matmul<DT, 64, 1, 12, 3> : c.kg == 2 ? (void *) k_matmul<DT, 64, 1, 12, 2> : (void *) k_matmul<DT, 64, 1, 12, 1>;
     if (c.rg == 1) return c.bn == 64 ? (void *) k_matmul<DT, 64, 1, 4, 1> : (void *) k_matmul<DT, 128, 1, 4, 1>;
     return c.bn == 64 ? (void *) k_matmul<DT, 64, 2, 4, 1> : (void *) k_matmul<DT, 128, 2, 4, 1>;

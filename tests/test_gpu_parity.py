@@ -302,14 +302,19 @@ def test_prefill_one_workgroup_per_cu(hip, dtype, M, N, K):
                          ids=["q4_k_kgroups2", "q6_k_kgroups2", "q4_0_kgroups2", "q8_0_kgroups2_ktail", "q4_k_split", "q8_0_split_ktail"])
 def test_prefill_workgroup_per_cu_few_tiles(hip, dtype, M, N, K):
     """Too few 384-row x 64-token tiles to fill the CUs (128). K = 2048 (16 stages): 2 K groups of
-    6 row waves on 192-row tiles (256), added in LDS. K = 2304 / 2080 (18 / 17 stages, not two
-    equal runs of whole groups of 4): K split in 2 over 12-wave work-groups, partials added in split
-    order; Q8_0 with K = 2080 splits 17 stages into 8 + 9, the last one partial (K = 2016: 16
-    stages on 2 K groups, the last one partial)."""
+    6 row waves on 192-row tiles (256), added in LDS, on the wide GEMM's 64-token form. K = 2304 /
+    2080 (18 / 17 stages, not two equal runs of whole groups of 4): K split in 2 over 12-wave
+    work-groups, partials added in split order; Q8_0 with K = 2080 splits 17 stages into 8 + 9, the
+    last one partial (K = 2016: 16 stages on the 64-token kernel's 2 K groups, the last one
+    partial). The form is pinned on a 256-CU part."""
     dev, st = hip
     q, _ = quantized(dtype, K, M, 700 + M)
     x = O.normal(N * K, 701).reshape(N, K)
     y = run_mul_mat(dev, st, dtype, q, K, M, x)
+    if dev.info().compute_units == 256:
+        want = ("gemm wide w=12 kg=2 bn=64" if K == 2048 else "gemm w=12 kg=2 bn=64" if K == 2016
+                else "gemm w=12 kg=1 bn=64 rg=1 split=2")
+        assert sg.last_launch()[0].startswith(want), sg.last_launch()
     ref = O.mul_mat(dtype, q, K, M, x, threads=8)
     e = nmse(y, ref)
     assert e <= 5e-5, f"NMSE {e:.3e}"
@@ -321,13 +326,17 @@ def test_prefill_workgroup_per_cu_few_tiles(hip, dtype, M, N, K):
                          ids=["q4_0", "q4_k", "q6_k", "q8_0_partial_rows_ktail", "q4_k_uneven", "q6_k_uneven", "q8_0_uneven_ktail"])
 def test_prefill_k_groups(hip, dtype, M, N, K):
     """Shapes whose 128-row tiles fill the CUs: one 12-wave work-group per CU, 3 K groups added in
-    LDS. K = 3072 splits into 3 equal runs; K = 4096 (32 stages) into 12 + 12 + 8 with 4 inactive
-    stages in the last group. Q8_0 with K = 3040 / 4064 ends in a partial stage and M = 200 in a
-    partial row tile."""
+    LDS in group order (the wide GEMM's 64-token form where K is a whole number of 128-element
+    stages, the 64-token kernel otherwise). K = 3072 splits into 3 equal runs; K = 4096 (32 stages)
+    into 12 + 12 + 8 with 4 inactive stages in the last group. Q8_0 with K = 3040 / 4064 ends in a
+    partial stage and M = 200 in a partial row tile. The form is pinned on a 256-CU part."""
     dev, st = hip
     q, _ = quantized(dtype, K, M, 600 + M)
     x = O.normal(N * K, 601).reshape(N, K)
     y = run_mul_mat(dev, st, dtype, q, K, M, x)
+    if dev.info().compute_units == 256:
+        want = "gemm wide w=12 kg=3 bn=64" if K % 128 == 0 else "gemm w=12 kg=3 bn=64"
+        assert sg.last_launch()[0].startswith(want), sg.last_launch()
     ref = O.mul_mat(dtype, q, K, M, x, threads=8)
     e = nmse(y, ref)
     assert e <= 5e-5, f"NMSE {e:.3e}"
@@ -355,12 +364,12 @@ def test_prefill_q4k_large_scales_and_split_groups(hip, K, M, N):
         assert e <= 5e-5, f"rows {rows}: NMSE {e:.3e}"
 
 
-@pytest.mark.parametrize("M,K,S,form", [(768, 256, 4, "gemm w=12 kg=1 bn=64"), (256, 3072, 4, "gemm w=12 kg=3"), (768, 256, 8, "gemm wide w=12 kg=1")],
+@pytest.mark.parametrize("M,K,S,form", [(768, 256, 4, "gemm w=12 kg=1 bn=64"), (256, 3072, 4, "gemm wide w=12 kg=3 bn=64"), (768, 256, 8, "gemm wide w=12 kg=1")],
                          ids=["one_k_group", "three_k_groups", "wide"])
 def test_prefill_workgroup_per_cu_slices_broadcast_strides(hip, M, K, S, form):
     """The 12-wave prefill kernels over S x slices with 2 weight slices (broadcast r2 = S / 2) and
-    padded x / y column strides: 384-row x 64-token tiles (M = 768, 4 slices), 3 K groups
-    (K = 3072), and 384-row x 128-token tiles of the wide GEMM (8 slices), each filling the CUs
+    padded x / y column strides: 384-row x 64-token tiles (M = 768, 4 slices), 3 K groups of the
+    wide GEMM's 64-token form (K = 3072), and its 384-row x 128-token tiles (8 slices), each filling the CUs
     with S slices x 2048 tokens (on a 256-CU part)."""
     dev, st = hip
     dtype, N = sg.Q4_K, 2048
