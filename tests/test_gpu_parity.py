@@ -304,7 +304,8 @@ def test_prefill_workgroup_per_cu_few_tiles(hip, dtype, M, N, K):
     """Too few 384-row x 64-token tiles to fill the CUs (128). K = 2048 (16 stages): 2 K groups of
     6 row waves on 192-row tiles (256), added in LDS, on the wide GEMM's 64-token form. K = 2304 /
     2080 (18 / 17 stages, not two equal runs of whole groups of 4): K split in 2 over 12-wave
-    work-groups, partials added in split order; Q8_0 with K = 2080 splits 17 stages into 8 + 9, the
+    work-groups (the wide GEMM's for K = 2304, the 64-token kernel's for the K tail), partials
+    added in split order; Q8_0 with K = 2080 splits 17 stages into 8 + 9, the
     last one partial (K = 2016: 16 stages on the 64-token kernel's 2 K groups, the last one
     partial). The form is pinned on a 256-CU part."""
     dev, st = hip
@@ -313,7 +314,7 @@ def test_prefill_workgroup_per_cu_few_tiles(hip, dtype, M, N, K):
     y = run_mul_mat(dev, st, dtype, q, K, M, x)
     if dev.info().compute_units == 256:
         want = ("gemm wide w=12 kg=2 bn=64" if K == 2048 else "gemm w=12 kg=2 bn=64" if K == 2016
-                else "gemm w=12 kg=1 bn=64 rg=1 split=2")
+                else "gemm wide w=12 kg=1 bn=64 rg=1 split=2" if K == 2304 else "gemm w=12 kg=1 bn=64 rg=1 split=2")
         assert sg.last_launch()[0].startswith(want), sg.last_launch()
     ref = O.mul_mat(dtype, q, K, M, x, threads=8)
     e = nmse(y, ref)
@@ -364,12 +365,12 @@ def test_prefill_q4k_large_scales_and_split_groups(hip, K, M, N):
         assert e <= 5e-5, f"rows {rows}: NMSE {e:.3e}"
 
 
-@pytest.mark.parametrize("M,K,S,form", [(768, 256, 4, "gemm w=12 kg=1 bn=64"), (256, 3072, 4, "gemm wide w=12 kg=3 bn=64"), (768, 256, 8, "gemm wide w=12 kg=1")],
+@pytest.mark.parametrize("M,K,S,form", [(768, 256, 4, "gemm wide w=12 kg=1 bn=64"), (256, 3072, 4, "gemm wide w=12 kg=3 bn=64"), (768, 256, 8, "gemm wide w=12 kg=1 bn=128")],
                          ids=["one_k_group", "three_k_groups", "wide"])
 def test_prefill_workgroup_per_cu_slices_broadcast_strides(hip, M, K, S, form):
     """The 12-wave prefill kernels over S x slices with 2 weight slices (broadcast r2 = S / 2) and
-    padded x / y column strides: 384-row x 64-token tiles (M = 768, 4 slices), 3 K groups of the
-    wide GEMM's 64-token form (K = 3072), and its 384-row x 128-token tiles (8 slices), each filling the CUs
+    padded x / y column strides, all on the wide GEMM: 384-row x 64-token tiles (M = 768, 4
+    slices), its 64-token form's 3 K groups (K = 3072), and 384-row x 128-token tiles (8 slices), each filling the CUs
     with S slices x 2048 tokens (on a 256-CU part)."""
     dev, st = hip
     dtype, N = sg.Q4_K, 2048
