@@ -1662,9 +1662,10 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
             c.wide = true;
             return c;
         }
-        if (env_w == 12) { // forced: KG = 1, split from SCRAPGPU_HIP_MM_SPLIT
+        if (env_w == 12) { // forced: KG = 1, split from SCRAPGPU_HIP_MM_SPLIT (the wide GEMM's form where K allows)
             c.kg = 1;
             if (env_split > 0) c.split = (int) std::max<int64_t>(1, std::min<int64_t>(std::min(env_split, 8), (stages + 3) / 4));
+            if (env_wide != 0 && a.K % BK == 0) c.wide = true;
             return c;
         }
         if (free_choice) {
