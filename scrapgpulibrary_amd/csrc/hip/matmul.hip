@@ -986,6 +986,16 @@ struct XDma {
             off[i] = 2 * ((uint32_t) (min<int64_t>(n0 + n, N - 1) * K) + 8 * c);
         }
     }
+    // GA: the tile's tokens are the x rows rows[0 .. BN) (gathered pairs, repeated past the count)
+    __device__ void init_rows(const int32_t * rows, int64_t K, int wv_, int lane) {
+        wv = wv_;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int ins = min(wv + LW * i, INS - 1);
+            const int slot = ins * 64 + lane, n = slot / 17, c = min(slot - 17 * n, 15);
+            off[i] = 2 * ((uint32_t) rows[n] * (uint32_t) K + 8 * c);
+        }
+    }
     // the stage starting at element k0 into the LDS tile X
     __device__ void load(const uint16_t * xb, int k0, uint16_t * X) const {
         const uint8_t * base = reinterpret_cast<const uint8_t *>(xb) + 2 * (uint32_t) k0;
@@ -1012,10 +1022,11 @@ struct XDma {
 // 118 against 145 us, 12288 x 4096 at 512 tokens (KG = 2) 70-76 against 79-82 us. Wave tiles of 64
 // rows x 64 tokens (half the LDS reads per MFMA, twice the dequantization) measured slower than
 // the 64-token form. Split-K over work-groups (partials + k_split_reduce) as in k_matmul.
-template <int DT, int KG, int NF = 4, bool SK = false>
+template <int DT, int KG, int NF = 4, bool SK = false, bool GA = false>
 __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
     constexpr int W = 12, BN = 32 * NF, RW = W / KG, BMT = 32 * RW;
     static_assert(!SK || KG == 1, "stream-K runs 12 row waves");
+    static_assert(!GA || (KG == 1 && !SK && NF == 2), "grouped MUL_MAT_ID: 384-row x 64-token tiles, no split");
     using F = PFmt<DT>;
     using Raw = typename F::Raw;
     extern __shared__ __attribute__((aligned(16))) uint16_t lds_mm[];
@@ -1039,10 +1050,42 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
                  : L.packed    ? min(L.nmat - 1, grow >= L.mo[1] ? (grow >= L.mo[2] ? 2 : 1) : 0)
                                : (tm >= L.mt[1] ? (tm >= L.mt[2] ? 2 : 1) : 0);
     const uint8_t * w = L.nmat > 1 ? L.wm[mj] : L.a.w + (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
-    const int64_t K = L.a.K, nb = L.a.nb, N = L.a.N;
+    const int64_t K = L.a.K, nb = L.a.nb;
+    int64_t N = L.a.N;
     const int64_t M = L.nmat > 1 ? L.Mm[mj] : L.a.M;
-    const int64_t n0 = tn * BN;
+    int64_t n0 = tn * BN;
     const int64_t m0 = L.packed ? grow - L.mo[mj] : (tm - L.mt[mj]) * BMT + 32 * wave;
+    // GA (grouped MUL_MAT_ID, as in k_matmul): token tile tn belongs to one expert, whose weights
+    // the work-group reads; its tokens are gathered x rows and its outputs scattered through a
+    // table in LDS after the x buffers
+    int32_t * ga_rows = reinterpret_cast<int32_t *>(lds_mm + 2 * BN * XR); // x row of tile token n
+    int64_t * ga_y = reinterpret_cast<int64_t *>(ga_rows + BN);           // its y element offset
+    int32_t ga_cnt = BN;                                                  // the tile's pairs
+    bool half_tile = false; // at most 32 pairs: the second token fragment is padding (wave-uniform)
+    if constexpr (GA) {
+        // the expert owning token tile tn: the last e with t_start[e] <= tn (an empty expert
+        // shares its start with the next one)
+        if (tn >= L.t_start[L.n_exp]) return; // past this call's tiles (the whole work-group)
+        int lo = 0, hi = L.n_exp - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (L.t_start[mid] <= tn) lo = mid;
+            else hi = mid - 1;
+        }
+        const int32_t pb = L.e_off[lo] + (int32_t) (tn - L.t_start[lo]) * BN;
+        ga_cnt = min(BN, L.e_off[lo + 1] - pb);
+        half_tile = ga_cnt <= 32;
+        w = L.a.w + (uint64_t) lo * L.a.w_s2;
+        if (threadIdx.x < BN) {
+            const int32_t pr = L.pairs[pb + min((int) threadIdx.x, ga_cnt - 1)]; // tokens past the count repeat the last pair
+            const int32_t t = pr / L.n_used, slot = pr - t * L.n_used;
+            ga_rows[threadIdx.x] = t * L.x_cols + (L.x_cols > 1 ? slot : 0);
+            ga_y[threadIdx.x] = (int64_t) slot * L.a.y_s1 + (int64_t) t * L.a.y_s2;
+        }
+        __syncthreads();
+        N = BN;
+        n0 = 0;
+    }
     // the stages of the split (whole groups of 4) or of the K group (KG = 2: every group walks
     // 4 ceil(groups / 2) stages so that all waves meet the same barriers; a group's stages past K
     // are inactive: their loads repeat a valid stage, their k-steps are skipped), as in k_matmul
@@ -1057,7 +1100,8 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
     f.init(M, nb, RowAddr(M, m0 + j), h);
     const uint16_t * xb = L.xb + (uint64_t) sl * N * K;
     XDma<RW, BN> xt;
-    xt.init(N, K, n0, wave, lane);
+    if constexpr (GA) xt.init_rows(ga_rows, K, wave, lane);
+    else xt.init(N, K, n0, wave, lane);
     uint16_t * const lds_x = lds_mm + kg * (2 * BN * XR); // the K group's two x buffers
     const int abase = j * XR; // + 32 q XR + 8 chunk(h, t): immediate offsets
 
@@ -1097,7 +1141,7 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
             if (t < 7) bn = F::bop(cw, sc, t + 1);
 #pragma unroll
             for (int q = 0; q < NF; ++q) {
-                acc[q] = mma32<DT>(a[q], b, acc[q]);
+                if (!(GA && q > 0 && half_tile)) acc[q] = mma32<DT>(a[q], b, acc[q]);
                 if (t < 7) a[q] = *reinterpret_cast<const f16x8 *>(X + q * 32 * XR + 8 * F::chunk(h, t + 1));
             }
             if (t < 7) b = bn;
@@ -1143,6 +1187,22 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
     // acc[q][v], lane (j, h): token n0 + 32q + 8 (v / 4) + 4h + v % 4, weight row m0 + j
     auto store_out = [&](auto qb, auto qc) __attribute__((always_inline)) {
         constexpr int QB = decltype(qb)::value, QC = decltype(qc)::value;
+        if constexpr (GA) {
+            // scatter: token n of the tile is pair ga_y[n] (the pairs past ga_cnt are not stored)
+            const int64_t m = m0 + j;
+#pragma unroll
+            for (int q = QB; q < QB + QC; ++q) {
+                float u[16];
+#pragma unroll
+                for (int v = 0; v < 16; ++v) u[v] = L.xs[ga_rows[32 * q + 8 * (v >> 2) + 4 * h + (v & 3)]];
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int n = 32 * q + 8 * (v >> 2) + 4 * h + (v & 3);
+                    if (n < ga_cnt && m < M) L.a.y[ga_y[n] + m] = acc[q][v] * u[v];
+                }
+            }
+            return;
+        }
         const int64_t slices = L.a.ne12 * L.a.ne13;
         float * y;
         int64_t ys1;
@@ -1984,7 +2044,13 @@ hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t 
     const int64_t xsum_row = xsum_row_of(px);
     const bool vec = (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && a.x_s1 % 4 == 0 && a.x_s2 % 4 == 0;
     const dim3 xg((unsigned) rows);
-    if (a.dtype == Q4_K) {
+    const int bn = ga_bn(id);
+    const int waves = ga_waves(a, id, cu_count);
+    // 384-row x 64-token tiles on the wide GEMM where K is a whole number of stages (x tiles
+    // straight into LDS, the exact Q4_K form from plain x)
+    static const int env_wide = env_int("SCRAPGPU_HIP_MM_WIDE", 1);
+    const bool wide = env_wide != 0 && waves == 12 && bn == 64 && a.K % BK == 0;
+    if (a.dtype == Q4_K && !wide) {
         if (vec)
             hipLaunchKernelGGL((k_x_to_f16<true, true>), xg, dim3(256), 0, stream, px, xb, xs, xsum, xsum_row);
         else
@@ -1997,7 +2063,6 @@ hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t 
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int bn = ga_bn(id);
     int32_t * e_off = reinterpret_cast<int32_t *>(scratch + part_offset(px));
     int32_t * t_start = e_off + id.n_exp + 1;
     int32_t * pairs = t_start + id.n_exp + 1;
@@ -2023,7 +2088,6 @@ hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t 
     L.nmat = 1;
     L.mo[1] = L.mo[2] = L.mo[3] = a.M;
     L.stages = (a.K + BK - 1) / BK;
-    const int waves = ga_waves(a, id, cu_count);
     L.tiles_m = (a.M + 32 * waves - 1) / (32 * waves);
     L.mt[1] = L.mt[2] = L.mt[3] = L.tiles_m;
     L.tiles_n = (id.n_used * id.n_tok + bn - 1) / bn + id.n_exp; // at least the tiles the routing makes
@@ -2033,18 +2097,20 @@ hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t 
     L.n_used = (int32_t) id.n_used;
     L.n_exp = (int32_t) id.n_exp;
     L.x_cols = (int32_t) px.N;
-    const size_t lds = (size_t) 2 * bn * BK * sizeof(uint16_t) + (size_t) bn * (sizeof(int32_t) + sizeof(int64_t));
+    const size_t lds = (size_t) 2 * bn * (wide ? XR : BK) * sizeof(uint16_t) + (size_t) bn * (sizeof(int32_t) + sizeof(int64_t));
     void * fn = nullptr;
     switch (a.dtype) {
-        case Q4_0: fn = ga_kernel<Q4_0>(bn, waves); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q4_0"; break;
-        case Q8_0: fn = ga_kernel<Q8_0>(bn, waves); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q8_0"; break;
-        case Q4_K: fn = ga_kernel<Q4_K>(bn, waves); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q4_k"; break;
-        case Q6_K: fn = ga_kernel<Q6_K>(bn, waves); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q6_k"; break;
+        case Q4_0: fn = wide ? (void *) k_gemm_w<Q4_0, 1, 2, false, true> : ga_kernel<Q4_0>(bn, waves); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q4_0"; break;
+        case Q8_0: fn = wide ? (void *) k_gemm_w<Q8_0, 1, 2, false, true> : ga_kernel<Q8_0>(bn, waves); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q8_0"; break;
+        case Q4_K: fn = wide ? (void *) k_gemm_w<Q4_K, 1, 2, false, true> : ga_kernel<Q4_K>(bn, waves); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q4_k"; break;
+        case Q6_K: fn = wide ? (void *) k_gemm_w<Q6_K, 1, 2, false, true> : ga_kernel<Q6_K>(bn, waves); if (kernel_name) *kernel_name = "mul_mat_id_mfma_q6_k"; break;
         default: return hipErrorInvalidValue;
     }
     const int64_t grid = L.tiles_m * L.tiles_n;
     if (grid >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
     if ((e = allow_lds(fn, lds)) != hipSuccess) return e;
+    std::snprintf(last_form().form, sizeof(last_form().form), "grouped%s w=%d bn=%d", wide ? " wide" : "", waves, bn);
+    last_form().grid = (uint64_t) grid;
     void * args[] = {&L};
     return hipLaunchKernel(fn, dim3((unsigned) grid), dim3((unsigned) (64 * waves)), args, lds, stream);
 }

@@ -210,6 +210,24 @@ def test_mul_mat_id_grouped_cases(hip, case):
     check_grouped(y, O.mul_mat_id(dtype, w, K, M, E, x, np.clip(ids, 0, E - 1)))
 
 
+@pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
+@pytest.mark.parametrize("shared", [True, False], ids=["x_shared", "x_per_slot"])
+def test_mul_mat_id_grouped_wide(hip, dtype, shared):
+    """The grouped MUL_MAT_ID on the wide GEMM's 384-row x 64-token tiles (12 waves, 16 pairs per
+    expert on average, K a whole number of 128-element stages): 392 rows (a last row tile of 8),
+    tiles of up to 32 pairs that skip their second token fragment. The form is pinned."""
+    dev, st = hip
+    K, M, E, T, nu = 512, 392, 64, 128, 8
+    w = O.quantize(dtype, O.normal(K * M * E, 81, 0.0, 0.02))
+    rng = np.random.default_rng(82)
+    ids = np.stack([rng.permutation(E)[:nu] for _ in range(T)]).astype(np.int32)
+    x = O.normal(T * (1 if shared else nu) * K, 83).reshape(T, 1 if shared else nu, K)
+    y = run_mul_mat_id(dev, st, dtype, w, K, M, E, x, ids)
+    if dev.info().compute_units == 256:
+        assert sg.last_launch()[0] == "grouped wide w=12 bn=64", sg.last_launch()
+    check_grouped(y, O.mul_mat_id(dtype, w, K, M, E, x, ids))
+
+
 def test_mul_mat_id_grouped_plan_reads_ids_on_device(hip):
     """A recorded plan (HIP graph) of a grouped MUL_MAT_ID replayed after the ids changed in device
     memory: the routing runs on the device each replay."""
