@@ -636,20 +636,6 @@ def bench_float(dev, st):
     return out
 
 
-def calibrate(dev, st):
-    """Five device-to-device copies of 256 MiB through scrapgpu_buffer_copy (the runtime's copy
-    kernel): the reference reading of FETCH_SIZE and WRITE_SIZE for rocprofv3 --pmc (each launch
-    reads and writes exactly 256 MiB)."""
-    n = 256 << 20
-    a, b = dev.alloc(n), dev.alloc(n)
-    for _ in range(5):
-        sg.check(sg.lib().scrapgpu_buffer_copy(st.handle, b.handle, 0, a.handle, 0, n, 0), "buffer_copy")
-    st.sync()
-    a.free()
-    b.free()
-    print(json.dumps({"calibration": "scrapgpu_buffer_copy", "bytes_per_launch": n, "launches": 5}))
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -663,7 +649,6 @@ def main():
     ap.add_argument("--no-get-rows", action="store_true", help="skip the GET_ROWS line")
     ap.add_argument("--no-configs", action="store_true", help="skip the lines of BASELINE.json's other workloads")
     ap.add_argument("--no-float", action="store_true", help="skip the float-weight (F16 / BF16) lines")
-    ap.add_argument("--calibrate", action="store_true", help="only run the 256 MiB copies that calibrate the PMC byte counters")
     ap.add_argument("--config-cpu-seconds", type=float, default=2.0, help="CPU reference budget per config line (at least one call)")
     ap.add_argument("--no-fuse", action="store_true", help="one MUL_MAT per weight instead of MUL_MAT_MULTI for q/k/v and gate/up")
     args = ap.parse_args()
@@ -674,9 +659,6 @@ def main():
 
     dev = sg.Device(0)
     st = dev.stream()
-    if args.calibrate:
-        calibrate(dev, st)
-        return
     info = dev.info()
     log("device:", info.name.decode(), info.compute_units, "CUs")
     model = Model(dev, st, args.layers, fuse=not args.no_fuse)
