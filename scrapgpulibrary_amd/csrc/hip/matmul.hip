@@ -1017,7 +1017,11 @@ struct XDma {
 // (each read again right after the MFMA that consumed it), x tiles loaded straight into LDS and
 // padded x rows (immediate LDS offsets). KG = 1: 12 row waves, 384-row tiles; KG = 2: 6 row
 // waves x 2 groups that take half of K each (192-row tiles, for shapes the 384-row ones do not
-// fill), each group finishing half of the token fragments. Measured (quantized N(0, 0.02)
+// fill), each group finishing half of the token fragments; KG = 3 (64-token tiles): 4 row waves x
+// 3 groups (128-row tiles), groups 1 and 2 handing their sums to group 0, which adds them in group
+// order and stores. The 64-token forms also take the 64-token kernel's tile shapes wherever K is a
+// whole number of stages, and GA runs the grouped MUL_MAT_ID (gathered x rows, scattered
+// outputs). Measured (quantized N(0, 0.02)
 // weights): 12288 x 4096 at 2048 tokens 219 against 272 us, gate+up (24576 rows) at 512 tokens
 // 118 against 145 us, 12288 x 4096 at 512 tokens (KG = 2) 70-76 against 79-82 us. Wave tiles of 64
 // rows x 64 tokens (half the LDS reads per MFMA, twice the dequantization) measured slower than
