@@ -56,6 +56,28 @@ def test_static_scratch_matches_op_execute(hip, dtype, K):
     wb.free()
 
 
+def test_static_scratch_wide_64_token_forms(hip):
+    """The wide GEMM's 64-token forms through the static scratch: 6144x4096 at 512 tokens (192-row
+    tiles, 2 K groups) and then at 256 tokens (384-row tiles, K split over work-groups, partial
+    sums in the static scratch), each bit for bit equal to scrapgpu_op_execute's output."""
+    dev, st = hip
+    K, M = 4096, 6144
+    q, _ = quantized(sg.Q4_K, K, M, 1520)
+    wb, wt = upload_weights(dev, st, sg.Q4_K, q, K, M)
+    for N in (512, 256):
+        x = O.normal(N * K, 1521 + N).reshape(N, K)
+        y_static = _run(dev, st, wt, x, M, True)
+        form = sg.last_launch()[0]
+        if dev.info().compute_units == 256:
+            assert form.startswith("gemm wide w=12 kg=2 bn=64" if N == 512 else "gemm wide w=12 kg=1 bn=64 rg=1 split=4"), form
+        y_plain = _run(dev, st, wt, x, M, False)
+        assert np.array_equal(y_static.view(np.uint32), y_plain.view(np.uint32)), f"N={N} [{form}]: outputs differ"
+        ref = O.mul_mat(sg.Q4_K, q, K, M, x, threads=8)
+        e = float(np.sum((y_static.astype(np.float64) - ref) ** 2) / np.sum(ref.astype(np.float64) ** 2))
+        assert e <= 5e-5, f"N={N}: NMSE {e:.3e}"
+    wb.free()
+
+
 def test_static_scratch_refuses_large_ops(hip):
     dev, st = hip
     K, M, N = 12288, 256, 2048  # 2 N K = 48 MiB of f16 activations > 32 MiB
