@@ -703,7 +703,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "decode: q4_k/q6_k weight codes x int8 two-plane x (x ~ s*a + s/253*b per 32 elements) on i8 MFMA, int32 sums scaled and accumulated in f32; prefill: f16 MFMA, f32 accumulate",
+        "dtype": "decode: q4_k/q6_k weight codes x int8 three-plane x (x = f*(253*a + b + c/253) per 32 elements, |err| <= 1.03*2^-24*max|x_seg|; non-finite segments in fp32) on i8 MFMA, int32 sums scaled and accumulated in f32; prefill: f16 MFMA, f32 accumulate",
         "data": "synthetic: weights ~N(0,0.02) quantized on device (bit-identical to the reference quantizer), x ~N(0,1)",
         "config": {"workload": f"Qwen3-8B Q4_K_M decode token: {args.layers} layers x 7 matvecs (q,k,v,o,gate,up in Q4_K; down in Q6_K), bs=1"
                                + ("; q/k/v and gate/up as MUL_MAT_MULTI" if not args.no_fuse else ""),

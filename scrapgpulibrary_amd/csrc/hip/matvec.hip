@@ -17,24 +17,26 @@
 // codes (nibbles, 6-bit values, bytes) are unpacked to int8 in registers. One
 // v_mfma_i32_16x16x64_i8 then takes the 16 rows' codes as its B operand (lane (r, p) supplies 16
 // codes of row r: column r, k-group p) and x as its A operand. A decode product has only one x
-// column, so the 16 rows of A are used to keep apart what must be scaled separately: row 4c + k
-// of A holds, for k-group c only, plane k % 2 of x over the scale group that lane group c needs
-// (k / 2 selects one of two scale groups), and zeros elsewhere. After the 4 MFMAs of a step, lane
-// (r, p) finds in its 4 accumulator registers (rows 4p .. 4p + 3 of D, column r) exactly the 2 x 2
-// integer sums its part needs, and applies the block scales once per scale group. Per 64 weights a
-// lane spends ~30 VALU operations (unpack + scales) instead of ~110 with VALU dot products, which
-// leaves the VALU idle enough to overlap the HBM stream.
+// column, so the 16 rows of A are used to keep apart what must be scaled separately: rows 4w ..
+// 4w + 2 of A (a "window") hold the three planes of x over one scale group, for the lanes whose
+// k-group lies in that group, and zeros elsewhere (row 4w + 3 is zero). Lane (r, p) receives rows
+// 4p .. 4p + 3 of D, so window p of each accumulator set is what lane part p scales: each format
+// maps its MFMAs to accumulator sets so that every (set, window) holds exactly one scale group.
+// Per 64 weights a lane spends ~30 VALU operations (unpack + scales) instead of ~110 with VALU dot
+// products, which leaves the VALU idle enough to overlap the HBM stream.
 //
-// x conversion. Every 32-element segment of x is stored as two int8 planes a, b and a scale s
-// (s = max|x| / 127): x ~= s * a + (s / 253) * b, plus the plain sums of its two 16-element
-// halves:
-//   sum_i q_i x_i ~= (s / 253) * (253 * sum q a + sum q b)
+// x conversion. Every 32-element segment of x is stored as three int8 planes a, b, c and a unit f
+// (f = max|x| / (127 * 253)): x = f * (253 * a + b + c / 253) + e, plus the plain sums of its two
+// 16-element halves:
+//   sum_i q_i x_i ~= f * ((253 * sum q a + sum q b) + (sum q c) / 253)
 // with each format's constant offset applied once per scale group through the segment sums:
 //   Q4_0: d * (sum q x - 8 sum x)            Q8_0: d * sum q x      (q = stored byte xor 0x80)
 //   Q4_K: d*sc * sum q x - dmin*m * sum x    Q6_K: d*sc * (sum q x - 32 sum x)
-// The two planes carry ~15 significant bits of each x relative to its segment's largest |x|, so
-// the product differs from the fp32 reference by ~1e-5 of max|x| per term, well inside the
-// NMSE <= 1e-7 bound of the decode path.
+// |e| <= f / 506 = max|x_seg| / 16 257 146 (1.03 * 2^-24 of the segment's largest element), so each
+// product carries x at the precision of an fp32 element of that magnitude. A segment with an Inf
+// or NaN, or whose largest |x| is below 2^-90, is not converted: its planes and sums are zero and
+// its products are formed in plain fp32 from the dequantized weights (seg_exact), so non-finite
+// inputs give the reference's +-Inf / NaN pattern.
 //
 // Two forms:
 //  * burst (N = 1, K <= 64 steps): one tile per work-group, at most 4 steps per wave; the wave
@@ -136,18 +138,24 @@ __device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// 253 * (sum over plane a) + (sum over plane b), as float
-__device__ __forceinline__ float planes(int da, int db) {
-    return (float) (da * 253 + db);
+// (253 * A + B) + C / 253 over the three planes' integer sums, as float: 253 A + B is exact in
+// float for every format (|A| <= 127 * 128 * 32), C enters with one rounding
+__device__ __forceinline__ float planes(int da, int db, int dc) {
+    return fmaf((float) dc, 1.0f / 253.0f, (float) (da * 253 + db));
+}
+__device__ __forceinline__ float planes(const v4i & D) {
+    return planes(D.x, D.y, D.z);
 }
 
-// one x segment in LDS: plane a (32 int8), plane b (32 int8)
+// one x segment in LDS: planes a, b, c (32 int8 each; plane k at byte 32 k, half h at + 16 h)
 struct XSeg {
-    uint4 a0, a1, b0, b1;
+    uint4 a0, a1, b0, b1, c0, c1;
 };
+constexpr int kSegBytes = (int) sizeof(XSeg);
 
 // The converted x of one wave's chunk, per column n: xs[n * nseg + g] (planes) and
-// xf[n * nseg + g] = {s / 253, sum of elements 0..15, sum of elements 16..31, sum of all 32}.
+// xf[n * nseg + g] = {f, sum of elements 0..15, sum of elements 16..31, sum of all 32}; f = -0.0
+// flags a segment left to seg_exact.
 // zpad: 16 zero bytes, the A operand of lanes that carry no x.
 struct XView {
     const XSeg * xs;
@@ -156,24 +164,32 @@ struct XView {
     int nseg;
 };
 
+__device__ __forceinline__ bool seg_flagged(const float4 & f) {
+    return __float_as_uint(f.x) == 0x80000000u;
+}
+
 // ---- per format ----------------------------------------------------------------------------------
 // init() resolves the lane's row in every R32 area once (Q4_K, Q8_0, Q4_0: as 32-bit byte offsets
 // from the matrix slice's base w, which is uniform across the work-group and so stays in scalar
 // registers; a slice is < 4 GiB, checked on the host); load(step) fetches what the lane needs of
 // one step, branch-free; bop(raw, t) is the lane's B operand (16 int8 codes) for MFMA t = 0..3 of the step;
 // aoff(t, c, k, g) is the byte offset, inside the step's XSeg run, of the 16 x bytes that lane
-// (row 4c + k of A, k-group g) supplies to MFMA t, or -1 for zeros; flush() scales the integer
-// sums of lane part p into the row sum.
+// (row 4c + k of A: window c, plane k; k-group g) supplies to MFMA t, or -1 for zeros; set(t) is
+// the accumulator set MFMA t adds into; flush() scales the integer sums of lane part p (window p of
+// each set) into the row sum.
 
 template <int DT> struct Fmt;
 
 // Q4_K: a step is one block; part p takes chunk p (64 elements: units 2p, 2p + 1 of the 128
 // nibble bytes): sub-block 2p (low nibbles), 2p + 1 (high). MFMA t takes elements 64p + 16t .. +15
-// (t = 0, 1: low nibbles of units 2p, 2p + 1; t = 2, 3: high nibbles). A row 4c + k: plane k % 2
-// of sub-block 2c + k / 2.
+// (t = 0, 1: low nibbles of units 2p, 2p + 1; t = 2, 3: high nibbles). Set t / 2, window c:
+// sub-block 2c + t / 2.
 template <>
 struct Fmt<Q4_K> {
-    static constexpr int ND = 1; // accumulator sets per step
+    static constexpr int ND = 2; // accumulator sets per step
+    __device__ static constexpr int set(int t) {
+        return t >> 1;
+    }
     struct Raw {
         uint4 q0, q1, hd;
     };
@@ -199,8 +215,8 @@ struct Fmt<Q4_K> {
         return t == 0 ? lo4(r.q0) : t == 1 ? lo4(r.q1) : t == 2 ? hi4(r.q0) : hi4(r.q1);
     }
     __device__ static int aoff(int t, int c, int k, int g) {
-        if (c != g || (k >> 1) != (t >> 1)) return -1;
-        return (2 * g + (t >> 1)) * 64 + (k & 1) * 32 + (t & 1) * 16;
+        if (c != g || k == 3) return -1;
+        return (2 * g + (t >> 1)) * kSegBytes + k * 32 + (t & 1) * 16;
     }
     __device__ float flush(const Raw & r, const v4i * D, const float4 * xf) const {
         const float d = half_bits(r.hd.x), dmin = half_bits(r.hd.x >> 16);
@@ -221,20 +237,23 @@ struct Fmt<Q4_K> {
             m1 = (float) (((t1 >> 4) & 0x0Fu) | (((s1 >> sh1) >> 2) & 0x30u));
         }
         const float4 f0 = xf[2 * p], f1 = xf[2 * p + 1];
-        float a = (d * sc0) * f0.x * planes(D[0].x, D[0].y);
+        float a = (d * sc0) * f0.x * planes(D[0]);
         a = fmaf(-dmin * m0, f0.w, a);
-        a = fmaf((d * sc1) * f1.x, planes(D[0].z, D[0].w), a);
+        a = fmaf((d * sc1) * f1.x, planes(D[1]), a);
         return fmaf(-dmin * m1, f1.w, a);
     }
 };
 
 // Q6_K: a step is one block; part p takes task p = (h, hf): the 64 elements 128h + 32t + 16hf + i
 // (t, i < 4, 16) built from ql units 4h + hf, 4h + 2 + hf and qh unit 8 + 2h + hf; MFMA t takes
-// the 16 of run t, which has its own signed 8-bit scale. Two accumulator sets (t = 0, 1 and
-// t = 2, 3); A row 4c + k of set u: plane k % 2 of run 2u + k / 2 of task c.
+// the 16 of run t, which has its own signed 8-bit scale. One accumulator set per MFMA; window c
+// of set t: run t of task c.
 template <>
 struct Fmt<Q6_K> {
-    static constexpr int ND = 2;
+    static constexpr int ND = 4;
+    __device__ static constexpr int set(int t) {
+        return t;
+    }
     struct Raw {
         uint4 qa, qc, qh, sc;
         uint32_t d;
@@ -277,9 +296,9 @@ struct Fmt<Q6_K> {
                                  ((ql.w >> ls) & 0x0F0F0F0Fu) | (((r.qh.w >> hs) << 4) & 0x30303030u)));
     }
     __device__ static int aoff(int t, int c, int k, int g) {
-        if (c != g || (k >> 1) != (t & 1)) return -1;
+        if (c != g || k == 3) return -1;
         const int h = g >> 1, hf = g & 1;
-        return (4 * h + t) * 64 + (k & 1) * 32 + hf * 16;
+        return (4 * h + t) * kSegBytes + k * 32 + hf * 16;
     }
     __device__ float flush(const Raw & r, const v4i * D, const float4 * xf) const {
         const int h = p >> 1, hf = p & 1;
@@ -291,22 +310,24 @@ struct Fmt<Q6_K> {
         for (int t = 0; t < 4; ++t) {
             const uint32_t sw = t < 2 ? sw0 : sw1;
             const float ds = d * ((float) ((sw >> (8 * (2 * (t & 1) + hf))) & 0xFFu) - 128.0f);
-            const v4i & Dt = D[t >> 1];
-            const int ia = (t & 1) ? Dt.z : Dt.x, ib = (t & 1) ? Dt.w : Dt.y;
             const float4 f = xf[4 * h + t];
             const float s16 = hf ? f.z : f.y;
-            a = fmaf(ds, fmaf(f.x, planes(ia, ib), -32.0f * s16), a);
+            a = fmaf(ds, fmaf(f.x, planes(D[t]), -32.0f * s16), a);
         }
         return a;
     }
 };
 
-// Q8_0: a step is 8 blocks of 32; MFMA t takes blocks 2t, 2t + 1 (part p: half p % 2 of block
-// 2t + p / 2); part p scales blocks 2p, 2p + 1. A row 4c + k: plane k % 2 of block 2c + k / 2.
-// Blocks past the end of the row (K % 256 != 0) load block 0 and contribute with d = 0.
+// Q8_0: a step is 8 blocks of 32; MFMA t takes blocks 2t, 2t + 1 (part g: half g % 2 of block
+// 2t + g / 2). Set t / 2, window 2 (t % 2) + g / 2 holds block 2t + g / 2, so part p scales blocks
+// p (set 0) and p + 4 (set 1). Blocks past the end of the row (K % 256 != 0) load block 0 and
+// contribute with d = 0.
 template <>
 struct Fmt<Q8_0> {
-    static constexpr int ND = 1;
+    static constexpr int ND = 2;
+    __device__ static constexpr int set(int t) {
+        return t >> 1;
+    }
     struct Raw {
         uint4 u[4];
         uint32_t d0, d1;
@@ -330,7 +351,7 @@ struct Fmt<Q8_0> {
             b = b < nb ? b : 0;
             r.u[t] = load16(w + (__umul24(2 * b, u) + qo));
         }
-        const uint32_t b0 = (uint32_t) step * 8 + 2 * p, b1 = b0 + 1;
+        const uint32_t b0 = (uint32_t) step * 8 + p, b1 = b0 + 4;
         const uint32_t d0 = load_half(w + (__umul24(b0 < nb ? b0 : 0, u >> 3) + dof));
         const uint32_t d1 = load_half(w + (__umul24(b1 < nb ? b1 : 0, u >> 3) + dof));
         r.d0 = b0 < nb ? d0 : 0u;
@@ -342,21 +363,24 @@ struct Fmt<Q8_0> {
         return as_v4i(make_uint4(q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u));
     }
     __device__ static int aoff(int t, int c, int k, int g) {
-        if (c != t || (k >> 1) != (g >> 1)) return -1;
-        return (2 * t + (g >> 1)) * 64 + (k & 1) * 32 + (g & 1) * 16;
+        if (c != 2 * (t & 1) + (g >> 1) || k == 3) return -1;
+        return (2 * t + (g >> 1)) * kSegBytes + k * 32 + (g & 1) * 16;
     }
     __device__ float flush(const Raw & r, const v4i * D, const float4 * xf) const {
-        const float a = half_bits(r.d0) * xf[2 * p].x * planes(D[0].x, D[0].y);
-        return fmaf(half_bits(r.d1) * xf[2 * p + 1].x, planes(D[0].z, D[0].w), a);
+        const float a = half_bits(r.d0) * xf[p].x * planes(D[0]);
+        return fmaf(half_bits(r.d1) * xf[p + 4].x, planes(D[1]), a);
     }
 };
 
 // Q4_0: a step is 8 blocks of 32 (16 nibble bytes each: low nibbles = elements 0..15, high =
 // 16..31); part p takes blocks p and p + 4. MFMA t: blocks 0..3 (t < 2) or 4..7, half t % 2.
-// A row 4c + k: plane k % 2 of block c + 4 (k / 2).
+// Set t / 2, window c: block c + 4 (t / 2).
 template <>
 struct Fmt<Q4_0> {
-    static constexpr int ND = 1;
+    static constexpr int ND = 2;
+    __device__ static constexpr int set(int t) {
+        return t >> 1;
+    }
     struct Raw {
         uint4 qa, qb;
         uint32_t da, db;
@@ -390,13 +414,13 @@ struct Fmt<Q4_0> {
         return t == 0 ? lo4(r.qa) : t == 1 ? hi4(r.qa) : t == 2 ? lo4(r.qb) : hi4(r.qb);
     }
     __device__ static int aoff(int t, int c, int k, int g) {
-        if (c != g || (k >> 1) != (t >> 1)) return -1;
-        return (g + 4 * (t >> 1)) * 64 + (k & 1) * 32 + (t & 1) * 16;
+        if (c != g || k == 3) return -1;
+        return (g + 4 * (t >> 1)) * kSegBytes + k * 32 + (t & 1) * 16;
     }
     __device__ float flush(const Raw & r, const v4i * D, const float4 * xf) const {
         const float4 fa = xf[p], fb = xf[p + 4];
-        const float a = half_bits(r.da) * fmaf(fa.x, planes(D[0].x, D[0].y), -8.0f * fa.w);
-        return fmaf(half_bits(r.db), fmaf(fb.x, planes(D[0].z, D[0].w), -8.0f * fb.w), a);
+        const float a = half_bits(r.da) * fmaf(fa.x, planes(D[0]), -8.0f * fa.w);
+        return fmaf(half_bits(r.db), fmaf(fb.x, planes(D[1]), -8.0f * fb.w), a);
     }
 };
 
@@ -435,7 +459,7 @@ __device__ __forceinline__ void step_mfma(const Fmt<DT> (&f)[RG], const typename
             for (int u = 0; u < ND; ++u) D[u] = v4i{0, 0, 0, 0};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const int u = ND == 1 ? 0 : (t >> 1);
+                const int u = Fmt<DT>::set(t);
                 D[u] = mfma(Aop[t], Fmt<DT>::bop(raw[i], t), D[u]);
             }
             acc[i][n] += f[i].flush(raw[i], D, xf);
@@ -446,55 +470,81 @@ __device__ __forceinline__ void step_mfma(const Fmt<DT> (&f)[RG], const typename
 // ---- x conversion ----------------------------------------------------------------------------------
 
 // Segment g (of nseg) of a wave's range, elements 8q .. 8q + 7 held by this lane in v (lanes
-// 4k .. 4k + 3 hold one segment): two int8 planes, the plane scale and the plain sums. Rounding
-// to integers: adding 1.5 * 2^23 leaves the nearest integer in the low mantissa bits.
-__device__ __forceinline__ void convert_seg(const float (&v)[8], int g, int nseg, int q, XSeg * xs, float4 * xf) {
+// 4k .. 4k + 3 hold one segment): three int8 planes, the unit f and the plain sums. Rounding to
+// integers: adding 1.5 * 2^23 leaves the nearest integer in the low mantissa bits. Each residual is
+// one fma over an exact product (253 a and b are integers below 2^24), so x - f (253 a + b + c / 253)
+// is only the last plane's rounding. Returns true for a segment flagged for seg_exact (non-finite,
+// or largest |x| below 2^-90), whose planes and sums are zero and whose f is -0.0.
+__device__ __forceinline__ bool convert_seg(const float (&v)[8], int g, int nseg, int q, XSeg * xs, float4 * xf) {
     constexpr float kMagic = 12582912.0f; // 1.5 * 2^23
-    float amax = 0.0f, sum = 0.0f;
+    float amax = 0.0f;
+    int nonfinite = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        amax = fmaxf(amax, fabsf(v[i]));
-        sum += v[i];
+        const float a = fabsf(v[i]);
+        nonfinite |= !(a <= 3.40282347e38f); // Inf or NaN
+        amax = fmaxf(amax, a);
     }
     amax = fmaxf(amax, __shfl_xor(amax, 1));
     amax = fmaxf(amax, __shfl_xor(amax, 2));
+    nonfinite |= __shfl_xor(nonfinite, 1);
+    nonfinite |= __shfl_xor(nonfinite, 2);
+    const bool special = nonfinite || (amax > 0.0f && amax < 0x1p-90f);
+    float t[8], sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        t[i] = special ? 0.0f : v[i];
+        sum += t[i];
+    }
     const float s16 = sum + __shfl_xor(sum, 1);
     const float s32 = s16 + __shfl_xor(s16, 2);
     const float s16o = __shfl_xor(s16, 2);
-    const float sc = amax * (1.0f / 127.0f);
-    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
-    const float invb = 253.0f * inv;
-    uint32_t pa[2], pb[2];
+    const float f = special ? 0.0f : amax * (1.0f / 32131.0f); // 127 * 253
+    const bool live = f > 0.0f && !special;
+    // reciprocals need not be exact: |a| <= 127 holds within a few ulps, and a rounding off by one
+    // near a tie leaves |b| <= 126.5 + tiny, |c| likewise
+    const float ia = live ? __builtin_amdgcn_rcpf(253.0f * f) : 0.0f;
+    const float ib = live ? __builtin_amdgcn_rcpf(f) : 0.0f;
+    const float ic = 253.0f * ib;
+    uint32_t pk[3][2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        uint32_t ba[4], bb[4];
+        uint32_t ba[4], bb[4], bc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float t = v[4 * h + i];
-            const float fa = fmaf(t, inv, kMagic);                          // |a| <= 127
-            const float fb = fmaf(fmaf(kMagic - fa, sc, t), invb, kMagic); // |b| <= 127 (253 < 254)
+            const float x = t[4 * h + i];
+            const float fa = fmaf(x, ia, kMagic);
+            const float r1 = fmaf((kMagic - fa) * 253.0f, f, x); // x - 253 a f
+            const float fb = fmaf(r1, ib, kMagic);
+            const float r2 = fmaf(kMagic - fb, f, r1); // r1 - b f
+            const float fc = fmaf(r2, ic, kMagic);
             ba[i] = __float_as_uint(fa);
             bb[i] = __float_as_uint(fb);
+            bc[i] = __float_as_uint(fc);
         }
         // byte i of the result = byte 0 of word i
-        pa[h] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(ba[3], ba[2], 0x0c0c0400u), __builtin_amdgcn_perm(ba[1], ba[0], 0x0c0c0400u),
-                                      0x05040100u);
-        pb[h] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(bb[3], bb[2], 0x0c0c0400u), __builtin_amdgcn_perm(bb[1], bb[0], 0x0c0c0400u),
-                                      0x05040100u);
+        pk[0][h] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(ba[3], ba[2], 0x0c0c0400u), __builtin_amdgcn_perm(ba[1], ba[0], 0x0c0c0400u),
+                                         0x05040100u);
+        pk[1][h] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(bb[3], bb[2], 0x0c0c0400u), __builtin_amdgcn_perm(bb[1], bb[0], 0x0c0c0400u),
+                                         0x05040100u);
+        pk[2][h] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(bc[3], bc[2], 0x0c0c0400u), __builtin_amdgcn_perm(bc[1], bc[0], 0x0c0c0400u),
+                                         0x05040100u);
     }
     if (g < nseg) {
         uint8_t * sp = reinterpret_cast<uint8_t *>(xs + g);
-        *reinterpret_cast<uint2 *>(sp + 8 * q) = make_uint2(pa[0], pa[1]);
-        *reinterpret_cast<uint2 *>(sp + 32 + 8 * q) = make_uint2(pb[0], pb[1]);
-        if (q == 0) xf[g] = make_float4(sc * (1.0f / 253.0f), s16, s16o, s32);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) *reinterpret_cast<uint2 *>(sp + 32 * k + 8 * q) = make_uint2(pk[k][0], pk[k][1]);
+        if (q == 0) xf[g] = special ? make_float4(-0.0f, 0.0f, 0.0f, 0.0f) : make_float4(f, s16, s16o, s32);
     }
+    return special && g < nseg;
 }
 
 // The wave's chunk of nseg segments starting at element e0, for NC columns. Lane l converts
 // elements 8 (l % 4) .. +8 of segment l / 4 (16 segments per pass); elements past K are zero.
 template <int NC>
-__device__ void convert_x(const MvArgs & A, const float * x, int64_t e0, int nseg, int lane, XSeg * xs, float4 * xf) {
+__device__ bool convert_x(const MvArgs & A, const float * x, int64_t e0, int nseg, int lane, XSeg * xs, float4 * xf) {
     const int q = lane & 3;
+    bool special = false;
     for (int base = 0; base < nseg; base += 16) {
         const int g = base + (lane >> 2);
         const int64_t e = e0 + 32 * (int64_t) g + 8 * q;
@@ -516,9 +566,10 @@ __device__ void convert_x(const MvArgs & A, const float * x, int64_t e0, int nse
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[i] = 0.0f;
             }
-            convert_seg(v, g, nseg, q, xs + n * nseg, xf + n * nseg);
+            special |= convert_seg(v, g, nseg, q, xs + n * nseg, xf + n * nseg);
         }
     }
+    return __ballot(special) != 0; // wave-uniform: some segment needs seg_exact
 }
 
 // the slice a work-group works on
@@ -583,8 +634,13 @@ __device__ __forceinline__ Row row_of(const MvArgs & A, int64_t tile, uint64_t w
 
 // Adds the parts of each row (lanes r, r + 16, r + 32, r + 48) and then the waves in order; lanes
 // tid < 16 * RG * NC write y. red: [W][NC][16 * RG] floats.
-template <int RG, int NC, int W>
-__device__ __forceinline__ void reduce_store(const MvArgs & A, const Where & wh, const Row & row, float (&acc)[RG][NC], float * red, int tid) {
+// fix() runs after this wave's sums are in red (the exact sums of flagged x segments go there)
+struct NoFix {
+    __device__ void operator()() const {}
+};
+template <int RG, int NC, int W, class Fix = NoFix>
+__device__ __forceinline__ void reduce_store(const MvArgs & A, const Where & wh, const Row & row, float (&acc)[RG][NC], float * red, int tid,
+                                             const Fix & fix = Fix()) {
     constexpr int R = 16 * RG;
     const int lane = tid & 63, wave = tid >> 6, r = lane & 15;
 #pragma unroll
@@ -597,6 +653,7 @@ __device__ __forceinline__ void reduce_store(const MvArgs & A, const Where & wh,
             if (lane < 16) red[(wave * NC + n) * R + 16 * i + r] = v;
         }
     }
+    fix();
     __syncthreads();
     if (tid < NC * R) {
         const int n = tid / R, rr = tid % R;
@@ -606,6 +663,161 @@ __device__ __forceinline__ void reduce_store(const MvArgs & A, const Where & wh,
 #pragma unroll
             for (int w2 = 0; w2 < W; ++w2) v += red[(w2 * NC + n) * R + rr];
             A.y[row.j][wh.y_off + n * A.ys1[row.j] + m] = v;
+        }
+    }
+}
+
+// ---- exact fp32 products over flagged x segments ---------------------------------------------------
+//
+// A segment that convert_seg flags (an Inf or NaN in it, or its largest |x| below 2^-90) has zero
+// planes and sums; its products are formed here in fp32 instead, w[m, k] * x[k] with the weight
+// dequantized by the reference's element formulas (src/core/ref/quant.cpp:30-108), so that +-Inf,
+// Inf * 0 = NaN and NaN reach y as in the reference's fp32 dot product (ops.cpp:968-980). Only
+// waves whose x holds such a segment take this path (a wave-uniform branch).
+
+// one row of an R32 slice
+struct R32Row {
+    const uint8_t * w; // the slice
+    int64_t M, nb, g0;
+    int rs, lane;
+};
+
+__device__ __forceinline__ R32Row r32_row(const uint8_t * w, int64_t M, int64_t nb, int64_t m) {
+    m = min(m, M - 1);
+    const int64_t g0 = m & ~(int64_t) 31;
+    return R32Row{w, M, nb, g0, (int) min<int64_t>(32, M - g0), (int) (m - g0)};
+}
+
+// natural byte j of block b of the row: area k of the slice starts at M nb (bytes per block of
+// the earlier areas); in an area of L bytes per block, 16-byte unit u of block b of the row sits at
+// g0 nb L + ((b L / 16 + u) rs + lane) 16, and a 2-byte area holds halves at g0 nb 2 + (b rs + lane)
+// 2; the area's xor mask is undone
+template <int DT>
+__device__ uint32_t nat_byte(const R32Row & r, int64_t b, int j) {
+    int before, src, len;
+    uint32_t xr = 0;
+    if constexpr (DT == Q4_0) {
+        if (j >= 2) { before = 0; src = 2; len = 16; } else { before = 16; src = 0; len = 2; }
+    } else if constexpr (DT == Q8_0) {
+        if (j >= 2) { before = 0; src = 2; len = 32; xr = 0x80; } else { before = 32; src = 0; len = 2; }
+    } else if constexpr (DT == Q4_K) {
+        if (j >= 16) { before = 0; src = 16; len = 128; } else { before = 128; src = 0; len = 16; }
+    } else {
+        if (j < 192) { before = 0; src = 0; len = 192; }
+        else if (j < 208) { before = 192; src = 192; len = 16; xr = 0x80; }
+        else { before = 208; src = 208; len = 2; }
+    }
+    const uint8_t * area = r.w + (uint64_t) r.M * (uint64_t) r.nb * (uint64_t) before;
+    const int o = j - src;
+    const uint8_t * q = len == 2 ? area + (uint64_t) r.g0 * r.nb * 2 + ((uint64_t) b * r.rs + r.lane) * 2 + o
+                                 : area + (uint64_t) r.g0 * r.nb * len + (((uint64_t) b * (len / 16) + o / 16) * r.rs + r.lane) * 16 + o % 16;
+    return (uint32_t) *q ^ xr;
+}
+
+// weight [m, k] (the reference's dequantize_row_* element formulas)
+template <int DT>
+__device__ float weight_at(const R32Row & r, int64_t k) {
+    constexpr int BS = DT == Q4_K || DT == Q6_K ? 256 : 32;
+    const int64_t b = k / BS;
+    const int i = (int) (k - b * BS);
+    auto byte = [&](int j) { return nat_byte<DT>(r, b, j); };
+    auto half = [&](int j) { return half_bits(byte(j) | (byte(j + 1) << 8)); };
+    if constexpr (DT == Q4_0) {
+        const uint32_t q = byte(2 + (i & 15));
+        return (float) ((int) (i < 16 ? (q & 15u) : (q >> 4)) - 8) * half(0);
+    } else if constexpr (DT == Q8_0) {
+        return (float) (int8_t) byte(2 + i) * half(0);
+    } else if constexpr (DT == Q4_K) {
+        const int c = i / 64, l = i % 32, hi = (i % 64) >= 32, j = 2 * c + hi;
+        uint32_t sc, mn;
+        if (j < 4) {
+            sc = byte(4 + j) & 63u;
+            mn = byte(8 + j) & 63u;
+        } else {
+            sc = (byte(8 + j) & 15u) | ((byte(j) >> 6) << 4);
+            mn = (byte(8 + j) >> 4) | ((byte(4 + j) >> 6) << 4);
+        }
+        const float d1 = half(0) * (float) sc, m1 = half(2) * (float) mn;
+        const uint32_t q = byte(16 + 32 * c + l);
+        return d1 * (float) (hi ? (q >> 4) : (q & 15u)) - m1;
+    } else {
+        const int h = i / 128, rr = (i % 128) / 32, l = i % 32;
+        const uint32_t qh = byte(128 + 32 * h + l);
+        const uint32_t lowq = byte(64 * h + l + ((rr & 1) ? 32 : 0));
+        const int nib = (int) (rr < 2 ? (lowq & 15u) : (lowq >> 4));
+        const int v = (nib | (int) (((qh >> (2 * rr)) & 3u) << 4)) - 32;
+        const int sc = (int) (int8_t) byte(192 + 8 * h + 2 * rr + l / 16);
+        return half(208) * (float) sc * (float) v;
+    }
+}
+
+// the fp32 dot product of one row with x over the 32-element segment at k0: lane part p takes
+// elements k0 + p + 4 i, then the four parts' sums are added, so every lane of the row returns
+// the segment's sum
+template <int DT>
+__device__ __noinline__ float seg_exact(R32Row r, const float * x, int64_t k0, int p) {
+    float s = 0.0f;
+#pragma unroll 1
+    for (int i = 0; i < 8; ++i) {
+        const int64_t k = k0 + p + 4 * i;
+        s += weight_at<DT>(r, k) * x[k];
+    }
+    s += __shfl_xor(s, 16);
+    s += __shfl_xor(s, 32);
+    return s;
+}
+
+// the flag of segment g of a view, the same on every lane (scalar: the branches on it stay uniform)
+__device__ __forceinline__ bool flagged_at(const float4 * xf, int g) {
+    return __builtin_amdgcn_readfirstlane(__float_as_uint(xf[g].x)) == 0x80000000u;
+}
+
+// one column, the single-column lane mapping (k_mvb): red[16 i + r] (this wave's row sums, lanes
+// r < 16) += the exact sums of the flagged segments 0 .. nseg - 1 of the view (segment g starts
+// at element k0 + 32 g) for rows m0 + 16 i + r of the slice w. Runs after the MFMA sums are
+// stored, so that no accumulator is live; not inlined, and given only uniform values, so that
+// it costs the main path no registers.
+template <int DT, int RG>
+__device__ __noinline__ void exact_red(const uint8_t * w, int64_t M, int64_t nb, int64_t m0, const float * x, const float4 * xf, int nseg,
+                                       int64_t k0, float * red) {
+    const int lane = threadIdx.x & 63;
+    for (int g = 0; g < nseg; ++g) {
+        if (!flagged_at(xf, g)) continue;
+#pragma unroll
+        for (int i = 0; i < RG; ++i) {
+            const float e = seg_exact<DT>(r32_row(w, M, nb, m0 + (lane & 15) + 16 * i), x, k0 + 32 * (int64_t) g, lane >> 4);
+            if (lane < 16) red[16 * i + lane] += e;
+        }
+    }
+}
+
+// the same for one column of k_mvc (16 rows at m0), the flagged segments given as bit g * bs of
+// fmask
+template <int DT>
+__device__ __noinline__ void exact_red_n(const uint8_t * w, int64_t M, int64_t nb, int64_t m0, const float * x, uint64_t fmask, int bs, int nseg,
+                                         int64_t k0, float * red) {
+    const int lane = threadIdx.x & 63;
+    for (int g = 0; g < nseg; ++g) {
+        if (!((fmask >> (g * bs)) & 1u)) continue;
+        const float e = seg_exact<DT>(r32_row(w, M, nb, m0 + (lane & 15)), x, k0 + 32 * (int64_t) g, lane >> 4);
+        if (lane < 16) red[lane] += e;
+    }
+}
+
+// single-column lane mapping (k_mvs): acc[i][n] of lane part 0 += the exact sums of the
+// flagged segments sg .. sg + cnt - 1 of the view (segment sg + g starts at element k0 + 32 g)
+template <int DT, int RG, int NC>
+__device__ void exact_segments(const MvArgs & A, const Where & wh, const Row & row, int r, int part, const XView & xv, int sg, int cnt,
+                               int64_t k0, float (&acc)[RG][NC]) {
+    const uint8_t * w = A.w[row.j] + wh.w_off;
+    for (int n = 0; n < NC; ++n) {
+        for (int g = 0; g < cnt; ++g) {
+            if (!flagged_at(xv.xf + n * xv.nseg, sg + g)) continue;
+#pragma unroll
+            for (int i = 0; i < RG; ++i) {
+                const float e = seg_exact<DT>(r32_row(w, row.M, A.nb, row.m0 + r + 16 * i), wh.x + n * A.x_s1, k0 + 32 * (int64_t) g, part);
+                if (part == 0) acc[i][n] += e;
+            }
         }
     }
 }
@@ -669,8 +881,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2
                                             (size_t) W * SPW * kSegs);
     uint8_t * zpad = reinterpret_cast<uint8_t *>(red + W * 16 * RG);
     if (lane < 4) reinterpret_cast<uint32_t *>(zpad)[lane] = 0u;
+    bool sp = false;
 #pragma unroll
-    for (int p = 0; p < XP; ++p) convert_seg(xv[p], 16 * p + (lane >> 2), nseg, lane & 3, xs, xf);
+    for (int p = 0; p < XP; ++p) sp |= convert_seg(xv[p], 16 * p + (lane >> 2), nseg, lane & 3, xs, xf);
+    const bool special = __ballot(sp) != 0;
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
 
@@ -684,7 +898,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2
         if (s < ns) step_mfma<DT, RG, 1>(f, buf[s], al, s * kSegs, xw, acc);
     }
     if constexpr (!CHUNK) {
-        reduce_store<RG, 1, W>(A, wh, row, acc, red, tid);
+        reduce_store<RG, 1, W>(A, wh, row, acc, red, tid, [&] {
+            if (special) exact_red<DT, RG>(A.w[row.j] + wh.w_off, row.M, A.nb, row.m0, wh.x, xf, nseg, s0 * kStep, red + wave * 16 * RG);
+        });
     } else {
         // the waves' sums of the chunk (as reduce_store), then the chunks' through memory
         constexpr int R = 16 * RG;
@@ -696,6 +912,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2
             v += __shfl_xor(v, 32);
             if (lane < 16) red[wave * R + 16 * i + r] = v;
         }
+        if (special) exact_red<DT, RG>(A.w[row.j] + wh.w_off, row.M, A.nb, row.m0, wh.x, xf, nseg, s0 * kStep, red + wave * R);
         __syncthreads();
         const int64_t tile = blockIdx.x;
         if (tid < R) {
@@ -754,7 +971,8 @@ __global__ __launch_bounds__(64 * W) void k_mvs(MvArgs A) {
     Row row = row_of<DT, 1>(A, tile, wh.w_off, r, part, f);
     Raw cur[1];
     if (ns > 0) cur[0] = f[0].load(s0);
-    if (once && ns > 0) convert_x<NC>(A, wh.x, s0 * kStep, ns * kSegs, lane, xs, xf);
+    bool special = false; // the current x chunk holds a segment for exact_segments
+    if (once && ns > 0) special = convert_x<NC>(A, wh.x, s0 * kStep, ns * kSegs, lane, xs, xf);
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
 
@@ -772,7 +990,7 @@ __global__ __launch_bounds__(64 * W) void k_mvs(MvArgs A) {
                 // a new x chunk: steps [k, k + cs) of this wave
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
-                convert_x<NC>(A, wh.x, (s0 + k) * kStep, min(cs, ns - k) * kSegs, lane, xs, xf);
+                special = convert_x<NC>(A, wh.x, (s0 + k) * kStep, min(cs, ns - k) * kSegs, lane, xs, xf);
                 __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
                 __builtin_amdgcn_wave_barrier();
             }
@@ -784,6 +1002,7 @@ __global__ __launch_bounds__(64 * W) void k_mvs(MvArgs A) {
             }
             const XView xv{xs, xf, zpad, min(cs, ns - (k / cs) * cs) * kSegs};
             step_mfma<DT, 1, NC>(f, cur, al, (k % cs) * kSegs, xv, acc);
+            if (special) exact_segments<DT, 1, NC>(A, wh, row, r, part, xv, (k % cs) * kSegs, kSegs, (s0 + k) * kStep, acc);
             cur[0] = nxt[0];
         }
         reduce_store<1, NC, W>(A, wh, row, acc, red + (it & 1) * (W * NC * 16), tid);
@@ -798,14 +1017,14 @@ __global__ __launch_bounds__(64 * W) void k_mvs(MvArgs A) {
 // For N = 2..8 the columns go into the rows of the MFMA's A operand, so each weight code is
 // unpacked once for all of them. This needs every MFMA to span few scale groups: the lane parts
 // are mapped so that parts {0, 1} of an MFMA lie in one scale group and parts {2, 3} in one other
-// (G = 2: Q4_0, Q8_0, Q4_K), or each part in its own 16-element group (G = 4: Q6_K). A row i of A
-// is (column, group, plane): rows 4c .. 4c + 3 = column c of the set, groups 0 / 1, planes a / b
-// (G = 2, 4 columns per MFMA set), or rows 8c .. 8c + 7 (G = 4, 2 columns per set). A row holds
-// its column's x plane only at the k positions of its group (zeros elsewhere), so row (c, g, .)
-// of D is column c's integer dot product over group g alone. Lane (r, p) receives rows
-// 4p .. 4p + 3 of D: for G = 2 all of column p's pairs (both groups, both planes); for G = 4 two
-// groups of column p / 2. It scales them with the groups' block scales and x-segment factors and
-// accumulates column p (or p / 2) of weight row r.
+// (G = 2: Q4_0, Q8_0, Q4_K), or each part in its own 16-element group (G = 4: Q6_K). Rows 4w ..
+// 4w + 2 of A (window w) hold the three x planes of one (column, group): G = 2: window 2c + g =
+// column c of the set (2 columns per MFMA set), group g; G = 4: window g of the set's one column.
+// A window holds its column's planes only at the k positions of its group (zeros elsewhere), so
+// window w of D is that column's integer dot product over that group alone. Lane (r, p) receives
+// window p of D, scales it with its group's block scale and x-segment factor, and accumulates it
+// for its column; the parts of one column are added at the end (parts p and p ^ 1 for G = 2, all
+// four for G = 4).
 //
 // Per format, for MFMA t = 0..3 of a step and lane part p: the segment (32 elements of the step)
 // and 16-byte half that part p supplies, the group it belongs to, and the flush of the lane's D.
@@ -846,10 +1065,17 @@ struct FmtN<Q4_K> {
     __device__ static int seg(int t, int g) {
         return 4 * (t >> 1) + (t & 1) + 2 * g;
     }
-    // scale and min of sub-block s (get_scale_min_k4)
-    __device__ static void scale_min(const Raw & r, int s, float & sc, float & m) {
+    // the factors of the lane's window group (p % 2) in MFMA t: d * sc, -dmin * m
+    // (get_scale_min_k4 of sub-block seg(t, p % 2))
+    struct Sc {
+        float k, o;
+    };
+    __device__ Sc scales(const Raw & r, int t, const uint32_t (&)[2]) const {
+        const float d = half_bits(r.hd.x), dmin = half_bits(r.hd.x >> 16);
+        const int s = seg(t, p & 1);
         const uint32_t s0 = r.hd.y, s1 = r.hd.z, s2 = r.hd.w;
         const int sh = 8 * (s & 3);
+        float sc, m;
         if (s < 4) {
             sc = (float) ((s0 >> sh) & 63u);
             m = (float) ((s1 >> sh) & 63u);
@@ -858,36 +1084,17 @@ struct FmtN<Q4_K> {
             sc = (float) ((t0 & 0x0Fu) | (((s0 >> sh) >> 2) & 0x30u));
             m = (float) (((t0 >> 4) & 0x0Fu) | (((s1 >> sh) >> 2) & 0x30u));
         }
+        return Sc{d * sc, -dmin * m};
     }
-    // the factors of MFMA t's two groups (the same for every column set): d * sc, -dmin * m
-    struct Sc {
-        float k[2], o[2];
-    };
-    __device__ Sc scales(const Raw & r, int t, const uint32_t (&)[2]) const {
-        const float d = half_bits(r.hd.x), dmin = half_bits(r.hd.x >> 16);
-        Sc c;
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            float sc, m;
-            scale_min(r, seg(t, g), sc, m);
-            c.k[g] = d * sc;
-            c.o[g] = -dmin * m;
-        }
-        return c;
-    }
-    // D rows (group g, plane): the lane's column over MFMA t's two groups
-    __device__ static float apply(const Sc & c, int t, const v4i & D, const float4 * xf) {
-        const float4 f0 = xf[seg(t, 0)], f1 = xf[seg(t, 1)];
-        float a = c.k[0] * f0.x * planes(D.x, D.y);
-        a = fmaf(c.o[0], f0.w, a);
-        a = fmaf(c.k[1] * f1.x, planes(D.z, D.w), a);
-        return fmaf(c.o[1], f1.w, a);
+    __device__ float apply(const Sc & c, int t, const v4i & D, const float4 * xf) const {
+        const float4 f = xf[seg(t, p & 1)];
+        return fmaf(c.k * f.x, planes(D), c.o * f.w);
     }
 };
 
 // Q4_0: MFMA t, group g is block 2t + g; part p supplies nibble half p % 2 (elements 16 (p % 2)
-// .. +15) of block 2t + p / 2. Part p loads those 4 blocks' units and scales; the scales of the
-// other group's blocks come from lane + 32 (part p ^ 2).
+// .. +15) of block 2t + p / 2. Part p loads those 4 blocks' units and scales; the scale of its
+// window's group p % 2 is its own (p / 2 == p % 2) or comes from lane + 32 (part p ^ 2).
 template <>
 struct FmtN<Q4_0> {
     static constexpr int G = 2;
@@ -932,22 +1139,20 @@ struct FmtN<Q4_0> {
     __device__ static int seg(int t, int g) {
         return 2 * t + g;
     }
-    // the scales of MFMA t's two blocks: the lane's own group p / 2, the other from part p ^ 2
     struct Sc {
-        float k[2];
+        float k;
     };
     __device__ Sc scales(const Raw & r, int t, const uint32_t (&other)[2]) const {
         const uint32_t mine = r.d[t >> 1] >> (16 * (t & 1)), theirs = other[t >> 1] >> (16 * (t & 1));
-        return Sc{{half_bits((p >> 1) ? theirs : mine), half_bits((p >> 1) ? mine : theirs)}};
+        return Sc{half_bits((p >> 1) == (p & 1) ? mine : theirs)};
     }
-    __device__ static float apply(const Sc & c, int t, const v4i & D, const float4 * xf) {
-        const float a = c.k[0] * xf[seg(t, 0)].x * planes(D.x, D.y);
-        return fmaf(c.k[1] * xf[seg(t, 1)].x, planes(D.z, D.w), a);
+    __device__ float apply(const Sc & c, int t, const v4i & D, const float4 * xf) const {
+        return c.k * xf[seg(t, p & 1)].x * planes(D);
     }
 };
 
-// Q8_0: MFMA t, group g is block 2t + g; part p supplies half p % 2 of block 2t + p / 2 (the
-// single-column mapping). Scales as for Q4_0.
+// Q8_0: MFMA t, group g is block 2t + g; part p supplies half p % 2 of block 2t + p / 2. Scales
+// as for Q4_0.
 template <>
 struct FmtN<Q8_0> {
     static constexpr int G = 2;
@@ -990,21 +1195,20 @@ struct FmtN<Q8_0> {
         return 2 * t + g;
     }
     struct Sc {
-        float k[2];
+        float k;
     };
     __device__ Sc scales(const Raw & r, int t, const uint32_t (&other)[2]) const {
         const uint32_t mine = r.d[t >> 1] >> (16 * (t & 1)), theirs = other[t >> 1] >> (16 * (t & 1));
-        return Sc{{half_bits((p >> 1) ? theirs : mine), half_bits((p >> 1) ? mine : theirs)}};
+        return Sc{half_bits((p >> 1) == (p & 1) ? mine : theirs)};
     }
-    __device__ static float apply(const Sc & c, int t, const v4i & D, const float4 * xf) {
-        const float a = c.k[0] * xf[seg(t, 0)].x * planes(D.x, D.y);
-        return fmaf(c.k[1] * xf[seg(t, 1)].x, planes(D.z, D.w), a);
+    __device__ float apply(const Sc & c, int t, const v4i & D, const float4 * xf) const {
+        return c.k * xf[seg(t, p & 1)].x * planes(D);
     }
 };
 
 // Q6_K: the single-column mapping (part p = task (h, hf) = (p / 2, p % 2): elements
-// 128 h + 32 t + 16 hf + i in MFMA t), each part its own 16-element group (G = 4). Lane (r, p)
-// flushes groups 2 (p % 2) and 2 (p % 2) + 1 of column p / 2 of its set.
+// 128 h + 32 t + 16 hf + i in MFMA t), each part its own 16-element group (G = 4), which is also
+// its window.
 template <>
 struct FmtN<Q6_K> : Fmt<Q6_K> {
     static constexpr int G = 4;
@@ -1017,41 +1221,33 @@ struct FmtN<Q6_K> : Fmt<Q6_K> {
         return as_v4i(make_uint4(((uint32_t) b.x + 0x60606060u) ^ 0x80808080u, ((uint32_t) b.y + 0x60606060u) ^ 0x80808080u,
                                  ((uint32_t) b.z + 0x60606060u) ^ 0x80808080u, ((uint32_t) b.w + 0x60606060u) ^ 0x80808080u));
     }
-    // d * scale of the lane's groups 2 (p % 2) + k in MFMA t (scale index 8 h + 2 t + hf, stored
-    // xor 0x80)
+    // d * scale of the lane's group p in MFMA t (scale index 8 h + 2 t + hf, stored xor 0x80)
     struct Sc {
-        float k[2];
+        float k;
     };
     __device__ Sc scales(const Raw & r, int t, const uint32_t (&)[2]) const {
-        const float d = half_bits(r.d);
-        Sc c;
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int g = 2 * (p & 1) + k, h = g >> 1, hf = g & 1;
-            const uint32_t sw = h ? (t < 2 ? r.sc.z : r.sc.w) : (t < 2 ? r.sc.x : r.sc.y);
-            c.k[k] = d * ((float) ((sw >> (8 * (2 * (t & 1) + hf))) & 0xFFu) - 128.0f);
-        }
-        return c;
+        const int h = p >> 1, hf = p & 1;
+        const uint32_t sw = h ? (t < 2 ? r.sc.z : r.sc.w) : (t < 2 ? r.sc.x : r.sc.y);
+        return Sc{half_bits(r.d) * ((float) ((sw >> (8 * (2 * (t & 1) + hf))) & 0xFFu) - 128.0f)};
     }
     __device__ float apply(const Sc & c, int t, const v4i & D, const float4 * xf) const {
-        const int g0 = 2 * (p & 1);
-        const float a = c.k[0] * xf[seg(t, g0)].x * planes(D.x, D.y);
-        return fmaf(c.k[1] * xf[seg(t, g0 + 1)].x, planes(D.z, D.w), a);
+        return c.k * xf[seg(t, p)].x * planes(D);
     }
 };
 
 // The lane's A operand for MFMA t of set s: byte offset inside its column's XSeg run of the step,
-// the column, or -1 (zeros). Row i = l % 16, part p = l / 16.
+// the column, or -1 (zeros). Row i = l % 16 = 4 w + k (window w, plane k), part p = l / 16.
 template <int DT, int NC>
 struct ALaneN {
     static constexpr int G = FmtN<DT>::G;
-    static constexpr int CPS = 16 / (2 * G); // columns per MFMA set
+    static constexpr int CPS = G == 2 ? 2 : 1; // columns per MFMA set
     static constexpr int NS = (NC + CPS - 1) / CPS;
     int off[NS][4];
     int col[NS];
     __device__ explicit ALaneN(int lane) {
         const int i = lane & 15, p = lane >> 4;
-        const int c = i / (2 * G), g = (i >> 1) % G, plane = i & 1;
+        const int w = i >> 2, k = i & 3;
+        const int c = G == 2 ? w >> 1 : 0, g = G == 2 ? (w & 1) : w;
         const int pg = G == 2 ? p >> 1 : p; // the group of part p
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
@@ -1059,18 +1255,22 @@ struct ALaneN {
             col[s] = n;
 #pragma unroll
             for (int t = 0; t < 4; ++t)
-                off[s][t] = (g == pg && n < NC) ? FmtN<DT>::seg(t, pg) * 64 + plane * 32 + (p & 1) * 16 : -1;
+                off[s][t] = (k < 3 && g == pg && n < NC) ? FmtN<DT>::seg(t, pg) * kSegBytes + k * 32 + (p & 1) * 16 : -1;
         }
     }
 };
 
-// one step of NC columns: acc[s] is the lane's column of set s (column s * CPS + p, or
-// s * CPS + p / 2 for G = 4)
+// the column whose partial lane part p holds in set s
+template <int DT, int NC>
+__device__ __forceinline__ int lane_col(int s, int p) {
+    return s * ALaneN<DT, NC>::CPS + (FmtN<DT>::G == 2 ? p >> 1 : 0);
+}
+
+// one step of NC columns: acc[s] is the lane's partial of column lane_col(s, p)
 // (sets S0 .. S1 only; column n's x sits in slot n - c0 of the view)
 template <int DT, int NC, int S0 = 0, int S1 = ALaneN<DT, NC>::NS>
 __device__ __forceinline__ void step_mfma_n(const FmtN<DT> & f, const typename FmtN<DT>::Raw & raw, const ALaneN<DT, NC> & al, int sg0,
                                             const XView & xv, float (&acc)[ALaneN<DT, NC>::NS], int lane, int c0 = 0) {
-    constexpr int G = FmtN<DT>::G, CPS = ALaneN<DT, NC>::CPS, NS = ALaneN<DT, NC>::NS;
     const int p = lane >> 4;
     uint32_t other[2] = {0u, 0u};
     if constexpr (DT == Q4_0 || DT == Q8_0) {
@@ -1088,9 +1288,37 @@ __device__ __forceinline__ void step_mfma_n(const FmtN<DT> & f, const typename F
             const uint8_t * pa = al.off[s][t] >= 0 ? base + al.off[s][t] : xv.zpad;
             const v4i A = *reinterpret_cast<const v4i *>(pa);
             const v4i D = mfma(A, B, v4i{0, 0, 0, 0});
-            // the lane's column of this set
-            const int nl = s * CPS + (G == 2 ? p : p >> 1);
+            const int nl = lane_col<DT, NC>(s, p);
             if (nl < NC) acc[s] += f.apply(sc, t, D, xv.xf + (nl - c0) * xv.nseg + sg0);
+        }
+    }
+}
+
+// the parts of one column: G = 2: parts p and p ^ 1; G = 4: all four. True on the lane that
+// stores the column's sum (window 0 of it)
+template <int DT>
+__device__ __forceinline__ bool add_parts(float & v, int p) {
+    v += __shfl_xor(v, 16);
+    if constexpr (FmtN<DT>::G == 4) v += __shfl_xor(v, 32);
+    return FmtN<DT>::G == 2 ? (p & 1) == 0 : p == 0;
+}
+
+// columns-in-rows lane mapping (k_mvn, k_mvc): for the columns c0 .. c1 - 1 held in slots
+// n - c0 of the view, the exact sums of the flagged segments sg .. sg + cnt - 1 (segment sg + g
+// starts at element k0 + 32 g; column n's x at x + n x_s1) go into the partial of the lane that
+// stores column n
+template <int DT, int NC>
+__device__ void exact_segments_n(const R32Row & row, const float * x, int64_t x_s1, const XView & xv, int sg, int cnt, int64_t k0, int c0, int c1,
+                                 float (&acc)[ALaneN<DT, NC>::NS], int p) {
+    constexpr int CPS = ALaneN<DT, NC>::CPS;
+#pragma unroll
+    for (int n = 0; n < NC; ++n) {
+        if (n < c0 || n >= c1) continue;
+        for (int g = 0; g < cnt; ++g) {
+            if (!flagged_at(xv.xf + (n - c0) * xv.nseg, sg + g)) continue;
+            const float e = seg_exact<DT>(row, x + n * x_s1, k0 + 32 * (int64_t) g, p);
+            const bool mine = FmtN<DT>::G == 2 ? p == 2 * (n % CPS) : p == 0;
+            if (mine) acc[n / CPS] += e;
         }
     }
 }
@@ -1132,7 +1360,8 @@ __global__ __launch_bounds__(64 * W) void k_mvn(MvArgs A) {
     }
     Raw cur;
     if (ns > 0) cur = f.load(s0);
-    if (once && ns > 0) convert_x<NC>(A, wh.x, s0 * kStep, ns * kSegs, lane, xs, xf);
+    bool special = false; // the current x chunk holds a segment for exact_segments_n
+    if (once && ns > 0) special = convert_x<NC>(A, wh.x, s0 * kStep, ns * kSegs, lane, xs, xf);
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
 
@@ -1153,7 +1382,7 @@ __global__ __launch_bounds__(64 * W) void k_mvn(MvArgs A) {
             if (!once && k % cs == 0) {
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
-                convert_x<NC>(A, wh.x, (s0 + k) * kStep, min(cs, ns - k) * kSegs, lane, xs, xf);
+                special = convert_x<NC>(A, wh.x, (s0 + k) * kStep, min(cs, ns - k) * kSegs, lane, xs, xf);
                 __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
                 __builtin_amdgcn_wave_barrier();
             }
@@ -1165,17 +1394,19 @@ __global__ __launch_bounds__(64 * W) void k_mvn(MvArgs A) {
             }
             const XView xv{xs, xf, zpad, min(cs, ns - (k / cs) * cs) * kSegs};
             step_mfma_n<DT, NC>(f, cur, al, (k % cs) * kSegs, xv, acc, lane);
+            if (special)
+                exact_segments_n<DT, NC>(r32_row(A.w[row.j] + wh.w_off, row.M, A.nb, row.m0 + r), wh.x, A.x_s1, xv, (k % cs) * kSegs, kSegs,
+                                         (s0 + k) * kStep, 0, NC, acc, part);
             cur = nxt;
         }
-        // the parts of a row: none to add for G = 2 (lane (r, p) holds column p of each set);
-        // for G = 4 parts 2c and 2c + 1 hold the two halves of column c's groups
+        // the parts of a column (add_parts), then the waves through LDS
         float * rb = red + (it & 1) * (W * NC * 16);
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             float v = acc[s];
-            if constexpr (G == 4) v += __shfl_xor(v, 16);
-            const int n = s * CPS + (G == 2 ? part : part >> 1);
-            if (n < NC && (G == 2 || (part & 1) == 0)) rb[(wave * NC + n) * 16 + r] = v;
+            const bool st = add_parts<DT>(v, part);
+            const int n = lane_col<DT, NC>(s, part);
+            if (n < NC && st) rb[(wave * NC + n) * 16 + r] = v;
         }
         __syncthreads();
         if (tid < NC * 16) {
@@ -1256,7 +1487,7 @@ __global__ __launch_bounds__(64) void k_x_planes(const float * x, int64_t x_s1, 
 // issuing its weight loads), which saves the pre-pass launch where the columns are few
 // 4 waves per SIMD (two work-groups per CU) where that fits without spilling
 constexpr int mc_waves(int dt, int nc) {
-    return (dt == Q4_K && nc == 8) || (dt == Q6_K && nc == 7) ? 3 : 4;
+    return (dt == Q4_K && nc >= 7) || (dt == Q6_K && nc >= 5) ? 3 : 4;
 }
 
 template <int DT, int NC, bool PRE>
@@ -1264,7 +1495,7 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(mc_wa
     using F = FmtN<DT>;
     using Raw = typename F::Raw;
     using AL = ALaneN<DT, NC>;
-    constexpr int G = F::G, CPS = AL::CPS, NS = AL::NS, W = kMcW, SPW = kMcSpw, SEGS = SPW * kSegs;
+    constexpr int CPS = AL::CPS, NS = AL::NS, W = kMcW, SPW = kMcSpw, SEGS = SPW * kSegs;
     extern __shared__ uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, part = lane >> 4;
@@ -1277,7 +1508,7 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(mc_wa
     // (plain scalars: arrays of vector types end up in scratch memory). x of the first pass of
     // columns now, ahead of the weights; the second pass's (NC > 4) once the first is in LDS
     constexpr int PC = NC < 4 ? NC : 4, NP = (NC + 3) / 4;
-    uint32_t xq[PC][4];
+    uint32_t xq[PC][6]; // the 16 segments' 1536 plane bytes: 16 per lane, then 8 per lane
     float xfq[PC][4];
     float xe[PC][8];
     const int64_t e = sb * kStep + 32 * (lane >> 2) + 8 * (lane & 3); // !PRE: lane's 8 elements
@@ -1287,9 +1518,11 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(mc_wa
         for (int k = 0; k < PC; ++k) {
             const int n = c0 + k < NC ? c0 + k : c0; // (a column past NC re-reads the pass's first)
             if constexpr (PRE) {
-                const uint4 q = reinterpret_cast<const uint4 *>(A.planes + n * A.nsegp + sb * kSegs)[lane];
+                const uint8_t * pb = reinterpret_cast<const uint8_t *>(A.planes + n * A.nsegp + sb * kSegs);
+                const uint4 q = reinterpret_cast<const uint4 *>(pb)[lane];
+                const uint2 q2 = reinterpret_cast<const uint2 *>(pb + 1024)[lane];
                 const float4 fq = A.fac[n * A.nsegp + sb * kSegs + (lane & 15)];
-                xq[k][0] = q.x; xq[k][1] = q.y; xq[k][2] = q.z; xq[k][3] = q.w;
+                xq[k][0] = q.x; xq[k][1] = q.y; xq[k][2] = q.z; xq[k][3] = q.w; xq[k][4] = q2.x; xq[k][5] = q2.y;
                 xfq[k][0] = fq.x; xfq[k][1] = fq.y; xfq[k][2] = fq.z; xfq[k][3] = fq.w;
             } else {
                 // branch-free: past K (or past the wave's steps) re-read element 0 and drop it
@@ -1329,6 +1562,10 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(mc_wa
     float acc[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) acc[s] = 0.0f;
+    // flagged x segments of column n: bit g (PRE) or 4 g of fmask[n] (scalar)
+    uint64_t fmask[NC];
+#pragma unroll
+    for (int n = 0; n < NC; ++n) fmask[n] = 0;
 #pragma unroll
     for (int q = 0; q < NP; ++q) {
         if (q > 0) {
@@ -1339,10 +1576,13 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(mc_wa
         for (int k = 0; k < PC; ++k) {
             if (4 * q + k < NC) {
                 if constexpr (PRE) {
-                    reinterpret_cast<uint4 *>(xs + k * SEGS)[lane] = make_uint4(xq[k][0], xq[k][1], xq[k][2], xq[k][3]);
+                    uint8_t * xb = reinterpret_cast<uint8_t *>(xs + k * SEGS);
+                    reinterpret_cast<uint4 *>(xb)[lane] = make_uint4(xq[k][0], xq[k][1], xq[k][2], xq[k][3]);
+                    reinterpret_cast<uint2 *>(xb + 1024)[lane] = make_uint2(xq[k][4], xq[k][5]);
                     if (lane < 16) xf[k * SEGS + lane] = make_float4(xfq[k][0], xfq[k][1], xfq[k][2], xfq[k][3]);
+                    fmask[4 * q + k] = __ballot(lane < 16 && __float_as_uint(xfq[k][0]) == 0x80000000u);
                 } else {
-                    convert_seg(xe[k], lane >> 2, SEGS, lane & 3, xs + k * SEGS, xf + k * SEGS);
+                    fmask[4 * q + k] = __ballot(convert_seg(xe[k], lane >> 2, SEGS, lane & 3, xs + k * SEGS, xf + k * SEGS));
                 }
             }
         }
@@ -1361,9 +1601,14 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(mc_wa
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         float v = acc[s];
-        if constexpr (G == 4) v += __shfl_xor(v, 16);
-        const int n = s * CPS + (G == 2 ? part : part >> 1);
-        if (n < NC && (G == 2 || (part & 1) == 0)) red[(wave * NC + n) * 16 + r] = v;
+        const bool st = add_parts<DT>(v, part);
+        const int n = lane_col<DT, NC>(s, part);
+        if (n < NC && st) red[(wave * NC + n) * 16 + r] = v;
+    }
+    // the exact sums of flagged x segments (with no accumulator live any more)
+    for (int n = 0; n < NC; ++n) {
+        if (fmask[n] != 0)
+            exact_red_n<DT>(A.w[j], M, A.nb, m0, A.x + n * A.x_s1, fmask[n], PRE ? 1 : 4, ns * kSegs, sb * kStep, red + (wave * NC + n) * 16);
     }
     __syncthreads();
     if (tid < NC * 16) {
