@@ -49,12 +49,16 @@ SCRAPGPU_API scrapgpu_status scrapgpu_hip_profile_read(size_t index, const char 
 /* scrapgpu_op_execute for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference.
  * It runs the same kernels as scrapgpu_op_execute, but the scratch those kernels need (the prefill
- * GEMM's f16 activations and split-K partial sums, the grouped MUL_MAT_ID's routing tables) comes
- * from a static array of 32 MiB per GPU that the library holds until the process ends, instead of
- * the stream's scratch, which scrapgpu_op_execute grows with hipMalloc; it calls no hipMalloc or
- * hipFree, and the event profiler stays off during the call. An op that needs more than 32 MiB of
- * scratch is refused with SCRAPGPU_STATUS_UNSUPPORTED and a reason (decode matvecs need none;
- * prefill needs about 2 * N * K bytes plus, for split-K shapes, 4 * splits * N * M bytes).
+ * GEMM's f16 activations and split-K partial sums, the grouped MUL_MAT_ID's routing tables, the
+ * decode matvec's x planes and K-chunk partial sums) comes from a static array of 32 MiB per GPU
+ * that the library holds until the process ends, instead of the stream's scratch, which
+ * scrapgpu_op_execute grows with hipMalloc; it calls no hipMalloc or hipFree, and the event
+ * profiler stays off during the call. One exception to "the same kernels": a prefill shape that
+ * scrapgpu_op_execute runs in the stream-K form (fewer 384-row tiles than CUs and a long K) runs
+ * another GEMM form here, whose output differs in rounding (both within the prefill tolerance),
+ * because stream-K's partial slots do not fit the static array. An op that needs more than 32 MiB
+ * of scratch is refused with SCRAPGPU_STATUS_UNSUPPORTED and a reason (decode matvecs need at most
+ * a few MiB; prefill needs about 2 * N * K bytes plus, for split-K shapes, 4 * splits * N * M bytes).
  * Every call on one GPU shares that GPU's array: calls whose work overlaps on one GPU (two
  * streams, two threads) race on it; serialize them. */
 SCRAPGPU_API scrapgpu_status scrapgpu_hip_op_execute_static(scrapgpu_stream_t * stream, const scrapgpu_op_desc * desc);

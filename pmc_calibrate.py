@@ -6,7 +6,7 @@ reading per launch divided by the size is the factor that turns a kernel's readi
 (and the three sizes show whether it depends on the size). Run under the profiler, one counter per
 run:
 
-    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -o fetch -- python3 -m scrapgpulibrary_amd.pmc_calibrate
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir> -o fetch -- python3 pmc_calibrate.py
 """
 import json
 

@@ -11,9 +11,10 @@
 
 namespace sgcore {
 
-// The registered table that owns `obj` (null `obj` or a foreign header: nullptr, with the last
-// error set to "<call>: <what> is not an object of a registered backend"). The returned table
-// stays valid until scrapgpu_unregister_all_backends.
+// The table that owns `obj`: the registered copy of its header's table, or (a table no longer or
+// never registered) a padded copy of the header's own table. Null `obj`, a null table or one
+// below the ABI 0.2 size: nullptr, with the last error set. The returned table stays valid until
+// the process ends.
 const scrapgpu_backend_vtable * owner_table(const void * obj, const char * call, const char * what);
 
 // Sets the last error and returns INVALID_ARGUMENT: "<call>: <what> is null".

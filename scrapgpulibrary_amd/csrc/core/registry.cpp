@@ -7,6 +7,13 @@
 // required argument is INVALID_ARGUMENT, an entry the backend left null is UNSUPPORTED with a
 // reason, and freeing a null object is a no-op. Registering a table that is already registered
 // replaces its entry instead of listing its devices twice.
+//
+// The core calls through padded copies of the tables. A copy is never freed before the process
+// ends, so a table pointer handed to a caller stays valid while another thread re-registers or
+// unregisters. An object whose header names a table that is not (or no longer) registered is
+// dispatched through a padded copy of that header's own table, as the reference dispatches through
+// the header (src/core/registry.cpp): its buffers, streams and plans can still be used and freed
+// after scrapgpu_unregister_all_backends.
 #include "dispatch.h"
 #include "scrapgpu/stream.h"
 
@@ -25,6 +32,8 @@ struct Registered {
     scrapgpu_backend_vtable table;          // the core's padded copy
 };
 
+constexpr size_t kMinTable = offsetof(scrapgpu_backend_vtable, plan_free) + sizeof(void (*)());
+
 class Registry {
   public:
     static Registry & get() {
@@ -33,19 +42,15 @@ class Registry {
     }
 
     void add(const scrapgpu_backend_vtable * vt) {
-        auto e = std::make_unique<Registered>();
-        e->origin = vt;
-        std::memset(&e->table, 0, sizeof(e->table));
-        std::memcpy(&e->table, vt, std::min(vt->struct_size, sizeof(e->table)));
-        e->table.struct_size = sizeof(e->table);
         std::lock_guard<std::mutex> hold(mu_);
+        Registered * e = copy_of(vt);
         for (auto & old : list_) {
             if (old->origin == vt) {
-                old = std::move(e);
+                old = e;
                 return;
             }
         }
-        list_.push_back(std::move(e));
+        list_.push_back(e);
     }
 
     void clear() {
@@ -53,32 +58,48 @@ class Registry {
         list_.clear();
     }
 
+    // the table to call for objects whose header names `origin`: its registered copy, else the
+    // latest copy made of it, else a new padded copy of it (null: not a usable table)
     const scrapgpu_backend_vtable * find(const scrapgpu_backend_vtable * origin) {
+        if (origin == nullptr) return nullptr;
         std::lock_guard<std::mutex> hold(mu_);
-        for (const auto & e : list_)
+        for (const Registered * e : list_)
             if (e->origin == origin) return &e->table;
-        return nullptr;
+        for (auto it = all_.rbegin(); it != all_.rend(); ++it)
+            if ((*it)->origin == origin) return &(*it)->table;
+        if (origin->struct_size < kMinTable || origin->name == nullptr) return nullptr;
+        return &copy_of(origin)->table;
     }
 
     // calls fn(table) for each registered table, in registration order, until it returns true
     template <typename Fn>
     void each(Fn && fn) {
         std::lock_guard<std::mutex> hold(mu_);
-        for (const auto & e : list_)
+        for (const Registered * e : list_)
             if (fn(e->table)) return;
     }
 
   private:
+    // a new padded copy of vt, kept until the process ends (mu_ held)
+    Registered * copy_of(const scrapgpu_backend_vtable * vt) {
+        auto e = std::make_unique<Registered>();
+        e->origin = vt;
+        std::memset(&e->table, 0, sizeof(e->table));
+        std::memcpy(&e->table, vt, std::min(vt->struct_size, sizeof(e->table)));
+        e->table.struct_size = sizeof(e->table);
+        all_.push_back(std::move(e));
+        return all_.back().get();
+    }
+
     std::mutex mu_;
-    std::vector<std::unique_ptr<Registered>> list_;
+    std::vector<std::unique_ptr<Registered>> all_; // every copy ever made
+    std::vector<Registered *> list_;               // the registered ones, in registration order
 };
 
 scrapgpu_status complain(scrapgpu_status st, const std::string & msg) {
     scrapgpu_set_last_error(msg.c_str());
     return st;
 }
-
-constexpr size_t kMinTable = offsetof(scrapgpu_backend_vtable, plan_free) + sizeof(void (*)());
 
 } // namespace
 
@@ -87,7 +108,7 @@ namespace sgcore {
 const scrapgpu_backend_vtable * owner_table(const void * obj, const char * call, const char * what) {
     const scrapgpu_backend_vtable * t = nullptr;
     if (obj != nullptr) t = Registry::get().find(static_cast<const scrapgpu_object_header *>(obj)->backend);
-    if (t == nullptr) complain(SCRAPGPU_STATUS_INVALID_ARGUMENT, std::string(call) + ": " + what + " is not an object of a registered backend");
+    if (t == nullptr) complain(SCRAPGPU_STATUS_INVALID_ARGUMENT, std::string(call) + ": " + what + " is not an object of a backend (no usable table in its header)");
     return t;
 }
 

@@ -1849,7 +1849,11 @@ static size_t sk_part_bytes(const MatArgs & a, int cu_count) {
     return (size_t) (cu_count + sk_max_tiles(a) - 1) * 128 * 384 * sizeof(float);
 }
 
+static bool float_gemm(const MatArgs & a);
+
 size_t matmul_scratch_bytes(const MatArgs & a, int cu_count, bool lean) {
+    // (float weights off the GEMM run the float matvec, which takes no scratch)
+    if (is_float_weight(a.dtype) && !float_gemm(a)) return 0;
     const MmConfig c = config_of(a, cu_count, lean);
     if (c.sk) return part_offset(a) + sk_part_bytes(a, cu_count);
     return part_offset(a) + (c.split == 1 ? 0 : part_bytes(a, c.split));

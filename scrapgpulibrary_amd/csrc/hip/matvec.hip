@@ -919,17 +919,21 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2
             float t = 0.0f;
 #pragma unroll
             for (int w2 = 0; w2 < W; ++w2) t += red[w2 * R + tid];
-            // visible to every XCD before the tile's count moves (agent-scope stores write
-            // through the L2; then this wave waits for them)
+            // agent-scope stores (written through the XCD's L2), waited for by this wave
             __hip_atomic_store(A.part + ((int64_t) blockIdx.y * A.tiles + tile) * R + tid, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
         }
+        // the count moves after this wave's write-through stores are acknowledged (vmcnt(0)
+        // above): every chunk's sums are in memory before its increment is visible, without the
+        // L2 write-back a release would add; the increment that completes the count is followed
+        // by an acquire fence below
         uint32_t & last = *reinterpret_cast<uint32_t *>(zpad + 16);
         if (tid == 0) last = __hip_atomic_fetch_add(A.arrive + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t) A.nck - 1;
         __syncthreads();
         // the last chunk of the tile to arrive adds all of them in chunk order (agent-scope loads:
         // the other chunks' sums may come from other XCDs) and leaves the count at zero for the
         // next launch
+        if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         if (last && tid < R) {
             const int64_t m = row.m0 + tid;
             float t = 0.0f;
@@ -1629,11 +1633,15 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(mc_wa
     __syncthreads();
     // (in the dynamic LDS after zpad: a static __shared__ would shift the dynamic block off its
     // 16-byte alignment)
+    // the count moves after every storing wave's write-through stores are acknowledged (their
+    // vmcnt(0), then the barrier), without the L2 write-back a release would add; the increment
+    // that completes the count is followed by an acquire fence below
     uint32_t & last = *reinterpret_cast<uint32_t *>(zpad + 16);
     if (tid == 0) last = __hip_atomic_fetch_add(A.arrive + rt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t) A.nchunks - 1;
     __syncthreads();
     // the last chunk of the row tile to finish adds all of them, in chunk order (agent-scope
     // loads: the other chunks' sums may come from other XCDs)
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (last && tid < NC * 16) {
         const int n = tid / 16, rr = tid % 16;
         if (m0 + rr < M) {

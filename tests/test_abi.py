@@ -274,7 +274,21 @@ def test_fake_backend_dispatch_and_short_vtable():
         assert L.scrapgpu_stream_create(dev, C.byref(st)) == sg.UNSUPPORTED
         assert L.scrapgpu_last_error()
         assert L.scrapgpu_buffer_free(buf) == sg.OK
-        # an object without a registered header is rejected
+        # objects outlive their backend's registration: after unregister_all they are dispatched
+        # through their header's own table (freeing them still reaches the backend), and a table
+        # registered again is called through its new copy
+        b1, b2 = C.c_void_p(), C.c_void_p()
+        assert L.scrapgpu_buffer_alloc(dev, 1, C.byref(b1)) == sg.OK
+        assert L.scrapgpu_buffer_alloc(dev, 2, C.byref(b2)) == sg.OK
+        L.scrapgpu_unregister_all_backends()
+        assert L.scrapgpu_get_device_count() == 0
+        assert L.scrapgpu_buffer_free(b1) == sg.OK
+        assert L.scrapgpu_register_backend(C.byref(vt)) == sg.OK
+        assert L.scrapgpu_register_backend(C.byref(vt)) == sg.OK  # re-registration: one entry
+        assert L.scrapgpu_get_device_count() == 1
+        assert L.scrapgpu_buffer_free(b2) == sg.OK
+        assert calls[-4:] == [("alloc", 1), ("alloc", 2), ("free",), ("free",)]
+        # an object without a usable header table is rejected
         stray = (C.c_void_p * 2)(None, None)
         assert L.scrapgpu_buffer_free(C.addressof(stray)) == sg.INVALID_ARGUMENT
         # incomplete vtables are refused

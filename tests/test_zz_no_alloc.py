@@ -78,6 +78,51 @@ def test_static_scratch_wide_64_token_forms(hip):
     wb.free()
 
 
+def test_static_scratch_stream_k_shape(hip):
+    """12288x5632 at 768 tokens: scrapgpu_op_execute runs it in the stream-K form (192 384-row
+    tiles, fewer than the CUs, 44 stages each); the static entry point runs another GEMM form (the
+    stream-K slots do not fit its array), so its output is checked against the oracle (NMSE) and
+    for being the same on two calls in a row, not for bit equality with the stream-K output."""
+    dev, st = hip
+    K, M, N = 5632, 12288, 768
+    q, _ = quantized(sg.Q4_K, K, M, 1530)
+    wb, wt = upload_weights(dev, st, sg.Q4_K, q, K, M)
+    x = O.normal(N * K, 1531).reshape(N, K)
+    y_plain = _run(dev, st, wt, x, M, False)
+    plain_form = sg.last_launch()[0]
+    y_static = _run(dev, st, wt, x, M, True)
+    static_form = sg.last_launch()[0]
+    y_again = _run(dev, st, wt, x, M, True)
+    if dev.info().compute_units == 256:
+        assert "stream-k" in plain_form, plain_form
+    assert "stream-k" not in static_form, static_form
+    assert np.array_equal(y_static.view(np.uint32), y_again.view(np.uint32))
+    ref = O.mul_mat(sg.Q4_K, q, K, M, x, threads=8)
+    for y, form in ((y_static, static_form), (y_plain, plain_form)):
+        e = float(np.sum((y.astype(np.float64) - ref) ** 2) / np.sum(ref.astype(np.float64) ** 2))
+        assert e <= 5e-5, f"[{form}]: NMSE {e:.3e}"
+    wb.free()
+
+
+def test_static_scratch_float_matvec_many_columns(hip):
+    """F32 weights at 4096 tokens run the exact float matvec (no scratch): the static entry point
+    runs them instead of refusing them for scratch they do not use."""
+    dev, st = hip
+    K, M, N = 4096, 64, 4096
+    w = O.normal(M * K, 1540, 0.0, 0.02).astype(np.float32)
+    wb = dev.alloc(w.nbytes)
+    st.write(wb, 0, w.view(np.uint8).reshape(-1))
+    wt = sg.tdesc(sg.F32, (K, M), wb)
+    x = O.normal(N * K, 1541).reshape(N, K)
+    y_static = _run(dev, st, wt, x, M, True)
+    y_plain = _run(dev, st, wt, x, M, False)
+    assert np.array_equal(y_static.view(np.uint32), y_plain.view(np.uint32))
+    ref = O.mul_mat(sg.F32, w, K, M, x, threads=8)
+    e = float(np.sum((y_static.astype(np.float64) - ref) ** 2) / np.sum(ref.astype(np.float64) ** 2))
+    assert e <= 1e-10, f"NMSE {e:.3e}"
+    wb.free()
+
+
 def test_static_scratch_refuses_large_ops(hip):
     dev, st = hip
     K, M, N = 12288, 256, 2048  # 2 N K = 48 MiB of f16 activations > 32 MiB
