@@ -12,7 +12,7 @@ import os
 import numpy as np
 
 PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG, "libscrapgpu_hip.so")
+LIB_PATH = os.environ.get("SCRAPGPU_HIP_LIB") or os.path.join(PKG, "libscrapgpu_hip.so")
 
 # status (include/scrapgpu/status.h)
 OK, UNSUPPORTED, INVALID_ARGUMENT, OUT_OF_MEMORY, BACKEND_ERROR, DEVICE_LOST = range(6)

@@ -141,7 +141,7 @@ __device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
 // (253 * A + B) + C / 253 over the three planes' integer sums, as float: 253 A + B is exact in
 // float for every format (|A| <= 127 * 128 * 32), C enters with one rounding
 __device__ __forceinline__ float planes(int da, int db, int dc) {
-    return fmaf((float) dc, 1.0f / 253.0f, (float) (da * 253 + db));
+    return fmaf((float) dc, 1.0f / 253.0f, (float) (__mul24(da, 253) + db)); // (|A| < 2^23: one v_mad_i32_i24)
 }
 __device__ __forceinline__ float planes(const v4i & D) {
     return planes(D.x, D.y, D.z);
@@ -475,7 +475,10 @@ __device__ __forceinline__ void step_mfma(const Fmt<DT> (&f)[RG], const typename
 // one fma over an exact product (253 a and b are integers below 2^24), so x - f (253 a + b + c / 253)
 // is only the last plane's rounding. Returns true for a segment flagged for seg_exact (non-finite,
 // or largest |x| below 2^-90), whose planes and sums are zero and whose f is -0.0.
-__device__ __forceinline__ bool convert_seg(const float (&v)[8], int g, int nseg, int q, XSeg * xs, float4 * xf) {
+// (SPLIT: the unit and the sum of all 32 go to fo[g] and so[g] instead of xf[g])
+template <bool SPLIT = false>
+__device__ __forceinline__ bool convert_seg(const float (&v)[8], int g, int nseg, int q, XSeg * xs, float4 * xf, float * fo = nullptr,
+                                            float * so = nullptr) {
     constexpr float kMagic = 12582912.0f; // 1.5 * 2^23
     float amax = 0.0f;
     int nonfinite = 0;
@@ -534,7 +537,14 @@ __device__ __forceinline__ bool convert_seg(const float (&v)[8], int g, int nseg
         uint8_t * sp = reinterpret_cast<uint8_t *>(xs + g);
 #pragma unroll
         for (int k = 0; k < 3; ++k) *reinterpret_cast<uint2 *>(sp + 32 * k + 8 * q) = make_uint2(pk[k][0], pk[k][1]);
-        if (q == 0) xf[g] = special ? make_float4(-0.0f, 0.0f, 0.0f, 0.0f) : make_float4(f, s16, s16o, s32);
+        if constexpr (SPLIT) {
+            if (q == 0) {
+                fo[g] = special ? -0.0f : f;
+                so[g] = special ? 0.0f : s32;
+            }
+        } else {
+            if (q == 0) xf[g] = special ? make_float4(-0.0f, 0.0f, 0.0f, 0.0f) : make_float4(f, s16, s16o, s32);
+        }
     }
     return special && g < nseg;
 }
@@ -924,16 +934,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2
             __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
         }
         // the count moves after this wave's write-through stores are acknowledged (vmcnt(0)
-        // above): every chunk's sums are in memory before its increment is visible, without the
-        // L2 write-back a release would add; the increment that completes the count is followed
-        // by an acquire fence below
+        // above): every chunk's sums are in memory before its increment is visible (the ordering
+        // a release would give, without its L2 write-back)
         uint32_t & last = *reinterpret_cast<uint32_t *>(zpad + 16);
         if (tid == 0) last = __hip_atomic_fetch_add(A.arrive + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t) A.nck - 1;
         __syncthreads();
-        // the last chunk of the tile to arrive adds all of them in chunk order (agent-scope loads:
-        // the other chunks' sums may come from other XCDs) and leaves the count at zero for the
-        // next launch
-        if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        // the last chunk of the tile to arrive adds all of them in chunk order and leaves the
+        // count at zero for the next launch. Its loads are agent-scope (coherent across XCDs by
+        // themselves, never served from a stale line of this XCD's L2) and issue only after the
+        // count's atomic returned (the barrier that publishes `last`)
         if (last && tid < R) {
             const int64_t m = row.m0 + tid;
             float t = 0.0f;
@@ -1634,14 +1643,12 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(mc_wa
     // (in the dynamic LDS after zpad: a static __shared__ would shift the dynamic block off its
     // 16-byte alignment)
     // the count moves after every storing wave's write-through stores are acknowledged (their
-    // vmcnt(0), then the barrier), without the L2 write-back a release would add; the increment
-    // that completes the count is followed by an acquire fence below
+    // vmcnt(0), then the barrier): the ordering a release would give, without its L2 write-back
     uint32_t & last = *reinterpret_cast<uint32_t *>(zpad + 16);
     if (tid == 0) last = __hip_atomic_fetch_add(A.arrive + rt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t) A.nchunks - 1;
     __syncthreads();
     // the last chunk of the row tile to finish adds all of them, in chunk order (agent-scope
     // loads: the other chunks' sums may come from other XCDs)
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (last && tid < NC * 16) {
         const int n = tid / 16, rr = tid % 16;
         if (m0 + rr < M) {
@@ -1650,6 +1657,432 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(mc_wa
                 v += __hip_atomic_load(A.part + (cc * NC + n) * A.prow + rt * 16 + rr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             A.y[j][n * A.ys1[j] + m0 + rr] = v;
         }
+    }
+}
+
+// ---- several columns on 32 x 32 x 32 MFMAs: k_mvw ------------------------------------------------
+//
+// v_mfma_i32_32x32x32_i8 takes the codes of a whole R32 group (32 rows: column j of B) over 32
+// consecutive elements of K (lane (j, h) supplies the 16 codes of k-half h, one 16-byte R32 unit
+// or the nibbles of one), and x in its 32 A rows: row 4c + k = plane k of column c (k < 3; row
+// 4c + 3 is zero). One MFMA covers one 32-element scale group of Q4_0 / Q8_0 / Q4_K for up to 8
+// columns, so no A row is zero-padded by group and every code is unpacked once for all columns.
+// Q6_K's groups are 16 elements: its A rows are (column c, group s, plane k) at 4 (2c + s) + k,
+// holding x only in k-half s, for 4 columns per MFMA. Lane (j, h) receives D rows 8 (i / 4) + 4h +
+// i % 4: column 2 (i / 4) + h's three planes (Q6_K: column i / 4's, group h), which it scales with
+// its row's group factor and the segment's x factor. A work-group owns one 32-row tile and one K
+// chunk of kMwW x kMwSpw steps; every wave issues all its loads at once (x first), and the waves'
+// sums meet in LDS in wave order; chunks meet as in k_mvc.
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16i mfma32(v4i a, v4i b) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, 0, 0, 0);
+}
+
+// Per format: init() resolves the lane's row (r < rs of the R32 group at g0) as 32-bit byte offsets
+// from the slice base; load(step) fetches the lane's bytes of one step; for MFMA q of the step
+// (Q = 8 per step), seg(q) is the x segment, bop(raw, q) the B operand (16 int8 codes of k-half
+// h), and fac(raw, q) the group's factors {scale, offset} (offset multiplies the segment's x sum).
+template <int DT> struct FmtW;
+
+// Q8_0: MFMA q = block q of the step; lane half h: unit 2q + h (bytes xor 0x80 stored)
+template <>
+struct FmtW<Q8_0> {
+    static constexpr bool OFF = false;
+    struct Raw {
+        uint4 u[8];
+        uint32_t d[4];
+    };
+    const uint8_t * w;
+    uint32_t qo, dof, u, nb;
+    __device__ void init(const uint8_t * w_, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int h) {
+        w = w_;
+        nb = (uint32_t) nb_;
+        u = (uint32_t) rs * 16;
+        qo = (uint32_t) (g0 * nb_ * 32 + lr * 16) + (uint32_t) h * u;
+        dof = (uint32_t) (M * nb_ * 32 + g0 * nb_ * 2 + lr * 2);
+    }
+    __device__ Raw load(int64_t step) const {
+        Raw r;
+        uint32_t dh[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            uint32_t b = (uint32_t) step * 8 + q;
+            const bool ok = b < nb;
+            b = ok ? b : 0;
+            r.u[q] = load16(w + (__umul24(2 * b, u) + qo));
+            const uint32_t d = load_half(w + (__umul24(b, u >> 3) + dof));
+            dh[q] = ok ? d : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.d[i] = dh[2 * i] | (dh[2 * i + 1] << 16);
+        return r;
+    }
+    __device__ static int seg(int q) {
+        return q;
+    }
+    __device__ static v4i bop(const Raw & r, int q) {
+        const uint4 v = r.u[q];
+        return as_v4i(make_uint4(v.x ^ 0x80808080u, v.y ^ 0x80808080u, v.z ^ 0x80808080u, v.w ^ 0x80808080u));
+    }
+    __device__ static float2 fac(const Raw & r, int q) {
+        return make_float2(half_bits(r.d[q >> 1] >> (16 * (q & 1))), 0.0f);
+    }
+};
+
+// Q4_0: MFMA q = block q; lane half h: the low (h = 0: elements 0..15) or high nibbles of the
+// block's one unit, minus 8
+template <>
+struct FmtW<Q4_0> {
+    static constexpr bool OFF = false;
+    struct Raw {
+        uint4 u[8];
+        uint32_t d[4];
+    };
+    const uint8_t * w;
+    uint32_t qo, dof, u, nb;
+    int h;
+    __device__ void init(const uint8_t * w_, int64_t M, int64_t nb_, int64_t g0, int rs, int lr, int h_) {
+        w = w_;
+        h = h_;
+        nb = (uint32_t) nb_;
+        u = (uint32_t) rs * 16;
+        qo = (uint32_t) (g0 * nb_ * 16 + lr * 16);
+        dof = (uint32_t) (M * nb_ * 16 + g0 * nb_ * 2 + lr * 2);
+    }
+    __device__ Raw load(int64_t step) const {
+        Raw r;
+        uint32_t dh[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            uint32_t b = (uint32_t) step * 8 + q;
+            const bool ok = b < nb;
+            b = ok ? b : 0;
+            r.u[q] = load16(w + (__umul24(b, u) + qo));
+            const uint32_t d = load_half(w + (__umul24(b, u >> 3) + dof));
+            dh[q] = ok ? d : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.d[i] = dh[2 * i] | (dh[2 * i + 1] << 16);
+        return r;
+    }
+    __device__ static int seg(int q) {
+        return q;
+    }
+    __device__ v4i bop(const Raw & r, int q) const {
+        const uint4 v = r.u[q];
+        const int sh = 4 * h;
+        return as_v4i(make_uint4((((v.x >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u, (((v.y >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u,
+                                 (((v.z >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u, (((v.w >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u));
+    }
+    __device__ static float2 fac(const Raw & r, int q) {
+        return make_float2(half_bits(r.d[q >> 1] >> (16 * (q & 1))), 0.0f);
+    }
+};
+
+// Q4_K: MFMA q = sub-block q of the block (the step); lane half h: unit 2 (q / 2) + h, low
+// nibbles for even q (sub-block 2c), high for odd (2c + 1); factors d * sc, -dmin * m
+template <>
+struct FmtW<Q4_K> {
+    static constexpr bool OFF = true;
+    struct Raw {
+        uint4 u[4], hd;
+    };
+    const uint8_t * w;
+    uint32_t qo, ho, u;
+    __device__ void init(const uint8_t * w_, int64_t M, int64_t nb, int64_t g0, int rs, int lr, int h) {
+        w = w_;
+        u = (uint32_t) rs * 16;
+        qo = (uint32_t) (g0 * nb * 128 + lr * 16) + (uint32_t) h * u;
+        ho = (uint32_t) (M * nb * 128 + g0 * nb * 16 + lr * 16);
+    }
+    __device__ Raw load(int64_t step) const {
+        Raw r;
+        const uint32_t q = __umul24((uint32_t) step * 8, u) + qo;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) r.u[c] = load16(w + q + (uint32_t) (2 * c) * u);
+        r.hd = load16(w + (__umul24((uint32_t) step, u) + ho));
+        return r;
+    }
+    __device__ static int seg(int q) {
+        return q;
+    }
+    __device__ static v4i bop(const Raw & r, int q) {
+        return (q & 1) ? hi4(r.u[q >> 1]) : lo4(r.u[q >> 1]);
+    }
+    __device__ static float2 fac(const Raw & r, int s) {
+        const float d = half_bits(r.hd.x), dmin = half_bits(r.hd.x >> 16);
+        const uint32_t s0 = r.hd.y, s1 = r.hd.z, s2 = r.hd.w;
+        const int sh = 8 * (s & 3);
+        float sc, m;
+        if (s < 4) {
+            sc = (float) ((s0 >> sh) & 63u);
+            m = (float) ((s1 >> sh) & 63u);
+        } else {
+            const uint32_t t0 = s2 >> sh;
+            sc = (float) ((t0 & 0x0Fu) | (((s0 >> sh) >> 2) & 0x30u));
+            m = (float) (((t0 >> 4) & 0x0Fu) | (((s1 >> sh) >> 2) & 0x30u));
+        }
+        return make_float2(d * sc, -dmin * m);
+    }
+};
+
+// Q6_K: MFMA q = (half-block hh = q / 4, run t = q % 4): elements 128 hh + 32 t + 16 h + i of
+// the block (segment 4 hh + t), lane half h = the 16-element group; codes from ql units
+// 4 hh + h (t = 0, 2) / 4 hh + 2 + h (t = 1, 3), low nibbles for t < 2, with bits 2t, 2t + 1 of
+// qh unit 8 + 2 hh + h on top, minus 32; factor d * scale[8 hh + 2t + h]
+template <>
+struct FmtW<Q6_K> {
+    static constexpr bool OFF = false;
+    struct Raw {
+        uint4 qa[2], qc[2], qh[2], sc;
+        uint32_t d;
+    };
+    const uint8_t * qb;
+    const uint8_t * sb;
+    const uint8_t * db;
+    uint32_t qblk, qunit, sblk, dblk;
+    int h;
+    __device__ void init(const uint8_t * w, int64_t M, int64_t nb, int64_t g0, int rs, int lr, int h_) {
+        h = h_;
+        qb = w + (uint64_t) g0 * nb * 192 + (uint64_t) lr * 16;
+        sb = w + (uint64_t) M * nb * 192 + (uint64_t) g0 * nb * 16 + (uint64_t) lr * 16;
+        db = w + (uint64_t) M * nb * 208 + (uint64_t) g0 * nb * 2 + (uint64_t) lr * 2;
+        qblk = (uint32_t) rs * 192;
+        qunit = (uint32_t) rs * 16;
+        sblk = (uint32_t) rs * 16;
+        dblk = (uint32_t) rs * 2;
+    }
+    __device__ Raw load(int64_t step) const {
+        Raw r;
+        const uint8_t * b = qb + (uint32_t) step * qblk;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            r.qa[hh] = load16(b + (uint32_t) (4 * hh + h) * qunit);
+            r.qc[hh] = load16(b + (uint32_t) (4 * hh + 2 + h) * qunit);
+            r.qh[hh] = load16(b + (uint32_t) (8 + 2 * hh + h) * qunit);
+        }
+        r.sc = load16(sb + (uint32_t) step * sblk);
+        r.d = load_half(db + (uint32_t) step * dblk);
+        return r;
+    }
+    __device__ static int seg(int q) {
+        return q;
+    }
+    __device__ static v4i bop(const Raw & r, int q) {
+        const int hh = q >> 2, t = q & 3;
+        const uint4 ql = (t & 1) ? r.qc[hh] : r.qa[hh];
+        const uint4 qh = r.qh[hh];
+        const int ls = t < 2 ? 0 : 4, hs = 2 * t;
+        return as_v4i(make_uint4(((((ql.x >> ls) & 0x0F0F0F0Fu) | (((qh.x >> hs) << 4) & 0x30303030u)) + 0x60606060u) ^ 0x80808080u,
+                                 ((((ql.y >> ls) & 0x0F0F0F0Fu) | (((qh.y >> hs) << 4) & 0x30303030u)) + 0x60606060u) ^ 0x80808080u,
+                                 ((((ql.z >> ls) & 0x0F0F0F0Fu) | (((qh.z >> hs) << 4) & 0x30303030u)) + 0x60606060u) ^ 0x80808080u,
+                                 ((((ql.w >> ls) & 0x0F0F0F0Fu) | (((qh.w >> hs) << 4) & 0x30303030u)) + 0x60606060u) ^ 0x80808080u));
+    }
+    __device__ float2 fac(const Raw & r, int q) const {
+        const int hh = q >> 2, t = q & 3;
+        // scale byte 8 hh + 2t + h (stored xor 0x80): word 2 hh + t / 2, byte 2 (t % 2) + h
+        const uint32_t sw = hh ? (t < 2 ? r.sc.z : r.sc.w) : (t < 2 ? r.sc.x : r.sc.y);
+        return make_float2(half_bits(r.d) * ((float) ((sw >> (8 * (2 * (t & 1) + h))) & 0xFFu) - 128.0f), 0.0f);
+    }
+};
+
+// columns per MFMA set: 8 (32-element groups), 4 (Q6_K)
+template <int DT>
+constexpr int mw_cps() {
+    return DT == Q6_K ? 4 : 8;
+}
+
+struct MwArgs {
+    const uint8_t * w[3];
+    int64_t M[3];
+    float * y[3];
+    int64_t ys1[3];
+    int64_t tstart[4]; // matrix j owns row tiles [tstart[j], tstart[j + 1])
+    int64_t nb, nst, K, nchunks;
+    const float * x;   // columns x_s1 floats apart, 16-byte aligned
+    int64_t x_s1;
+    float * part;      // nchunks > 1: [nchunks][NC][prow] partial sums
+    uint32_t * arrive; // nchunks > 1: chunks done per row tile, zero between launches
+    int64_t prow;      // tiles * rows per tile
+};
+
+// Work-group: RW x KW waves; wave (rw, kw) takes rows 32 rw .. + 31 of the tile and steps
+// 2 kw, 2 kw + 1 of the K chunk (2 KW steps); all of them share the chunk's x, converted once per
+// work-group into LDS by all its threads while the weight loads are in flight.
+template <int DT, int NC, int RW, int KW>
+__global__ __launch_bounds__(64 * RW * KW) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_mvw(MwArgs A) {
+    using F = FmtW<DT>;
+    using Raw = typename F::Raw;
+    constexpr int CPS = mw_cps<DT>(), NS = (NC + CPS - 1) / CPS, SPW = 2, CH = KW * SPW, SEGS = CH * kSegs, R = 32 * RW, T = 64 * RW * KW;
+    extern __shared__ uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rw = wave % RW, kw = wave / RW;
+    const int r = lane & 31, h = lane >> 5;
+    const int64_t rt = blockIdx.x;
+    const int c = (int) blockIdx.y;
+    const int64_t cb = (int64_t) c * CH;                      // the chunk's first step
+    const int64_t sb = cb + kw * SPW;                         // the wave's first step
+    const int ns = (int) max<int64_t>(0, min<int64_t>(SPW, A.nst - sb));
+
+    // x of the chunk: thread t converts elements 8 (t % 4) .. + 7 of segment (t / 4) % SEGS of
+    // column (t / 4) / SEGS (+ T / 4 / SEGS per pass); loads issued first, branch-free
+    constexpr int TASKS = NC * SEGS * 4, PASSES = (TASKS + T - 1) / T;
+    float xe[PASSES][8];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int task = p * T + tid, g = (task >> 2) % SEGS, n = (task >> 2) / SEGS;
+        const int64_t e = cb * kStep + 32 * g + 8 * (task & 3);
+        const bool ok = task < TASKS && e < A.K;
+        const float * xp = A.x + (ok ? n * A.x_s1 + e : 0);
+        const float4 u = *reinterpret_cast<const float4 *>(xp);
+        const float4 w = *reinterpret_cast<const float4 *>(xp + 4);
+        xe[p][0] = ok ? u.x : 0.0f; xe[p][1] = ok ? u.y : 0.0f; xe[p][2] = ok ? u.z : 0.0f; xe[p][3] = ok ? u.w : 0.0f;
+        xe[p][4] = ok ? w.x : 0.0f; xe[p][5] = ok ? w.y : 0.0f; xe[p][6] = ok ? w.z : 0.0f; xe[p][7] = ok ? w.w : 0.0f;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int j = rt >= A.tstart[1] ? (rt >= A.tstart[2] ? 2 : 1) : 0;
+    const int64_t M = A.M[j], m0 = (rt - A.tstart[j]) * R, mw = m0 + 32 * rw;
+    F f;
+    {
+        const int64_t m = min(mw + r, M - 1), g0 = m & ~(int64_t) 31;
+        f.init(A.w[j], M, A.nb, g0, (int) min<int64_t>(32, M - g0), (int) (m - g0), h);
+    }
+    Raw buf[SPW];
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) buf[s] = f.load(s < ns ? sb + s : (ns > 0 ? sb : 0));
+    __builtin_amdgcn_sched_barrier(0);
+
+    XSeg * xs = reinterpret_cast<XSeg *>(lds);                                  // [NC][SEGS]
+    float4 * xf = reinterpret_cast<float4 *>(xs + NC * SEGS);                   // [NC][SEGS]
+    float * red = reinterpret_cast<float *>(xf + NC * SEGS);                    // [KW][RW][NC][32]
+    uint8_t * zpad = reinterpret_cast<uint8_t *>(red + KW * RW * NC * 32);
+    if (tid < 4) reinterpret_cast<uint32_t *>(zpad)[tid] = 0u;
+    bool sp = false;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int task = p * T + tid, g = (task >> 2) % SEGS, n = task < TASKS ? (task >> 2) / SEGS : 0;
+        // (tasks past the last column convert zeros into a segment index past SEGS: not stored)
+        sp |= convert_seg(xe[p], task < TASKS ? g : SEGS, SEGS, task & 3, xs + n * SEGS, xf + n * SEGS);
+    }
+    const bool special = __syncthreads_or(sp); // (also: x and zpad are in LDS for every wave)
+
+    // the lane's A operand: row i = 4 blk + k (plane k < 3), k-half h
+    const int blk = r >> 2, k = r & 3;
+    int acol = -1; // the column of set 0 (set s adds s * CPS), -1: zeros
+    if (k < 3) {
+        if constexpr (DT == Q6_K) acol = ((blk & 1) == h) ? (blk >> 1) : -1;
+        else acol = blk;
+    }
+    const int aoff = k * 32 + h * 16;
+    float acc[NS][4];
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[s][i] = 0.0f;
+#pragma unroll
+    for (int st = 0; st < SPW; ++st) {
+        if (st < ns) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int sg = (kw * SPW + st) * kSegs + F::seg(q);
+                const v4i B = f.bop(buf[st], q);
+                const float2 fc = f.fac(buf[st], q);
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    const int n = acol + s * CPS;
+                    const uint8_t * pa = (acol >= 0 && n < NC) ? reinterpret_cast<const uint8_t *>(xs + n * SEGS + sg) + aoff : zpad;
+                    const v16i D = mfma32(*reinterpret_cast<const v4i *>(pa), B);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        // D rows 8 i + 4 h + (0..2): column 2 i + h (Q6_K: i, group h) of the set
+                        const int col = s * CPS + (DT == Q6_K ? i : 2 * i + h);
+                        if (col < NC) {
+                            const float4 xfv = xf[col * SEGS + sg];
+                            const float P = planes(D[4 * i], D[4 * i + 1], D[4 * i + 2]);
+                            if constexpr (F::OFF) acc[s][i] = fmaf(fc.x * xfv.x, P, fmaf(fc.y, xfv.w, acc[s][i]));
+                            else acc[s][i] = fmaf(fc.x * xfv.x, P, acc[s][i]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    // this wave's sums per (column, row)
+    float * rw_red = red + (kw * RW + rw) * NC * 32;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float v = acc[s][i];
+            if constexpr (DT == Q6_K) v += __shfl_xor(v, 32); // the row's two 16-element groups
+            const int col = s * CPS + (DT == Q6_K ? i : 2 * i + h);
+            if (col < NC && (DT != Q6_K || h == 0)) rw_red[col * 32 + r] = v;
+        }
+    }
+    // the exact sums of flagged x segments of the wave's steps (no accumulator live any more)
+    if (special) {
+        for (int n = 0; n < NC; ++n) {
+            const float * xn = A.x + n * A.x_s1;
+            uint64_t fm = 0;
+            for (int g = 0; g < ns * kSegs; ++g) fm |= (uint64_t) flagged_at(xf + n * SEGS, kw * SPW * kSegs + g) << g;
+            if (fm != 0) {
+                exact_red_n<DT>(A.w[j], M, A.nb, mw, xn, fm, 1, ns * kSegs, sb * kStep, rw_red + n * 32);
+                exact_red_n<DT>(A.w[j], M, A.nb, mw + 16, xn, fm, 1, ns * kSegs, sb * kStep, rw_red + n * 32 + 16);
+            }
+        }
+    }
+    __syncthreads();
+    // the K waves' sums in order, then y or the chunk's partial sums
+    for (int t = tid; t < NC * R; t += T) {
+        const int n = t / R, rr = t % R;
+        float v = 0.0f;
+#pragma unroll
+        for (int k2 = 0; k2 < KW; ++k2) v += red[((k2 * RW + rr / 32) * NC + n) * 32 + rr % 32];
+        if (A.nchunks == 1) {
+            if (m0 + rr < M) A.y[j][n * A.ys1[j] + m0 + rr] = v;
+        } else {
+            // agent-scope stores (written through the XCD's L2), waited for below
+            __hip_atomic_store(A.part + ((int64_t) c * NC + n) * A.prow + rt * R + rr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (A.nchunks == 1) return;
+    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this wave's partial-sum stores are done
+    __syncthreads();
+    // the count moves after every storing wave's write-through stores are acknowledged (the
+    // ordering of k_mvc); the last chunk of the tile adds all of them in chunk order and puts the
+    // count back to zero
+    uint32_t & last = *reinterpret_cast<uint32_t *>(zpad + 16);
+    if (tid == 0) last = __hip_atomic_fetch_add(A.arrive + rt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t) A.nchunks - 1;
+    __syncthreads();
+    if (!last) return;
+    for (int t = tid; t < NC * R; t += T) {
+        const int n = t / R, rr = t % R;
+        if (m0 + rr < M) {
+            float v = 0.0f;
+            for (int64_t cc = 0; cc < A.nchunks; ++cc)
+                v += __hip_atomic_load(A.part + (cc * NC + n) * A.prow + rt * R + rr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            A.y[j][n * A.ys1[j] + m0 + rr] = v;
+        }
+    }
+    if (tid == 0) __hip_atomic_store(A.arrive + rt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// waves per work-group: row waves x K waves (measured on the config shapes at N = 2, 4, 8 against
+// 2 x 4, 1 x 8 and 2 x 8: 4 x 2 the fastest or within 5% everywhere)
+constexpr int kMwRW = 4, kMwKW = 2;
+
+template <int DT>
+void * pick_mvw(int nc) {
+    switch (nc) {
+        case 2: return (void *) k_mvw<DT, 2, kMwRW, kMwKW>;
+        case 3: return (void *) k_mvw<DT, 3, kMwRW, kMwKW>;
+        case 4: return (void *) k_mvw<DT, 4, kMwRW, kMwKW>;
+        case 5: return (void *) k_mvw<DT, 5, kMwRW, kMwKW>;
+        case 6: return (void *) k_mvw<DT, 6, kMwRW, kMwKW>;
+        case 7: return (void *) k_mvw<DT, 7, kMwRW, kMwKW>;
+        default: return (void *) k_mvw<DT, 8, kMwRW, kMwKW>;
     }
 }
 
@@ -1787,12 +2220,19 @@ size_t matvec_scratch_bytes(const MatArgs * mats, int nmat, const IdArgs * id) {
     if (nmat >= 1 && chunk_form(mats, nmat, id)) return chunk_part_bytes(mats, nmat);
     if (nmat < 1 || !mc_form(mats, nmat, id)) return 0;
     const int64_t nst = (mats[0].K + kStep - 1) / kStep, nchunks = (nst + kMcChunk - 1) / kMcChunk, nsegp = nchunks * kMcChunk * kSegs;
-    int64_t tiles = 0;
-    for (int j = 0; j < nmat; ++j) tiles += (mats[j].M + 15) / 16;
+    int64_t tiles = 0, rows_w = 0;
+    for (int j = 0; j < nmat; ++j) {
+        tiles += (mats[j].M + 15) / 16;
+        rows_w += (mats[j].M + 32 * kMwRW - 1) / (32 * kMwRW) * (32 * kMwRW);
+    }
     const size_t nc = (size_t) mats[0].N;
+    // k_mvc: x planes and factors, K-chunk partial sums and counts
     size_t b = (nc * (size_t) nsegp * sizeof(XSeg) + 255) / 256 * 256 + (nc * (size_t) nsegp * sizeof(float4) + 255) / 256 * 256;
     if (nchunks > 1) b += ((size_t) nchunks * nc * (size_t) tiles * 16 * sizeof(float) + 255) / 256 * 256 + (size_t) tiles * sizeof(uint32_t);
-    return b;
+    // k_mvw: K-chunk partial sums
+    const int64_t wchunks = (nst + 2 * kMwKW - 1) / (2 * kMwKW);
+    const size_t bw = wchunks > 1 ? ((size_t) wchunks * nc * (size_t) rows_w * sizeof(float) + 255) / 256 * 256 : 0;
+    return std::max<size_t>(std::max<size_t>(b, bw), 256);
 }
 
 hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream_t stream, const char ** kernel_name,
@@ -1912,6 +2352,47 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         return hipLaunchKernel(fn, dim3((unsigned) L.tiles, (unsigned) slices), dim3((unsigned) (64 * W)), args, lds, stream);
     }
 
+    // several columns, one slice: k_mvw (128-row tiles x K chunks of 4 steps on 32x32x32 MFMAs, x
+    // converted in the kernel), which needs x 16-byte aligned and the stream's arrival counts; else
+    // (or SCRAPGPU_HIP_MV_MW=0) k_mvc
+    static const bool mw_on = tuning("SCRAPGPU_HIP_MV_MW", 1) != 0;
+    if (mw_on && scratch != nullptr && arrive != nullptr && L.xvec && mc_form(mats, nmat, id)) {
+        constexpr int R = 32 * kMwRW, CH = 2 * kMwKW;
+        MwArgs C;
+        std::memset(&C, 0, sizeof(C));
+        for (int j = 0; j < 3; ++j) {
+            const bool has = j < nmat;
+            C.w[j] = has ? mats[j].w : nullptr;
+            C.M[j] = has ? mats[j].M : 0;
+            C.y[j] = has ? mats[j].y : nullptr;
+            C.ys1[j] = has ? mats[j].y_s1 : 0;
+            C.tstart[j + 1] = has ? C.tstart[j] + (mats[j].M + R - 1) / R : INT64_MAX;
+        }
+        const int64_t tiles = C.tstart[nmat];
+        if (tiles > kArriveMax) return hipErrorInvalidValue;
+        C.nb = L.nb;
+        C.nst = nst;
+        C.K = a.K;
+        C.nchunks = (nst + CH - 1) / CH;
+        C.x = a.x;
+        C.x_s1 = a.x_s1;
+        C.part = reinterpret_cast<float *>(scratch);
+        C.arrive = arrive;
+        C.prow = tiles * R;
+        void * fn = dt == Q4_0 ? pick_mvw<Q4_0>(nc) : dt == Q8_0 ? pick_mvw<Q8_0>(nc) : dt == Q4_K ? pick_mvw<Q4_K>(nc) : pick_mvw<Q6_K>(nc);
+        const size_t lds = (size_t) nc * CH * kSegs * (sizeof(XSeg) + sizeof(float4)) + (size_t) kMwKW * kMwRW * nc * 32 * sizeof(float) + 32;
+        if (lds > 65536) {
+            static std::mutex mu;
+            std::lock_guard<std::mutex> lock(mu);
+            const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
+            if (e != hipSuccess) return e;
+        }
+        if (grid_size) *grid_size = (uint64_t) tiles * (uint64_t) C.nchunks;
+        std::snprintf(last_form().form, sizeof(last_form().form), "columns mfma32 nc=%d chunks=%d", nc, (int) C.nchunks);
+        last_form().grid = (uint64_t) tiles * (uint64_t) C.nchunks;
+        void * args[] = {&C};
+        return hipLaunchKernel(fn, dim3((unsigned) tiles, (unsigned) C.nchunks), dim3(64 * kMwRW * kMwKW), args, lds, stream);
+    }
     if (scratch != nullptr && mc_form(mats, nmat, id)) {
         // several columns: x pre-pass, then one work-group per 16 rows and K chunk
         McArgs C;
@@ -1936,7 +2417,7 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         C.fac = fac;
         C.prow = tiles * 16;
         C.part = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(fac) + ((size_t) nc * C.nsegp * sizeof(float4) + 255) / 256 * 256);
-        C.arrive = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(C.part) + ((size_t) C.nchunks * nc * (size_t) tiles * 16 * sizeof(float) + 255) / 256 * 256);
+        C.arrive = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(C.part) + ((size_t) C.nchunks * nc * (size_t) C.prow * sizeof(float) + 255) / 256 * 256);
         C.x = a.x;
         C.x_s1 = a.x_s1;
         C.K = a.K;

@@ -17,8 +17,9 @@ Segments with a non-finite element (or all elements below 2^-90) are summed in f
 instead of through the planes, so each output must have the oracle's class (NaN / +Inf / -Inf /
 finite), and the finite outputs its value within the decode gates. Every kernel form is reached:
 the one-column burst, its K-chunked form, the streaming form (K past 64 steps), the multi-column
-form with and without the x pre-pass and with several K chunks, the streaming multi-column form
-(several slices), and MUL_MAT_ID.
+form on 32x32x32 MFMAs (one K chunk and several), the 16x16x64 multi-column form with its x
+pre-pass (x not 16-byte aligned), the streaming multi-column form (several slices), and
+MUL_MAT_ID.
 """
 import os
 
@@ -164,14 +165,15 @@ def check_special(y, ref, x, deq):
     return int(np.sum(~np.isfinite(ref)))
 
 
-FORMS = {  # name: (K, M, N, slices, kernel form prefix)
-    "burst": (4096, 256, 1, 1, "burst rg="),
-    "burst_chunks": (12288, None, 1, 1, "burst-chunks"),
-    "stream": (16640, 96, 1, 1, "stream nc=1"),
-    "columns": (4096, 96, 2, 1, "columns nc=2 chunks=1"),
-    "columns_pre": (4096, 96, 8, 1, "columns nc=8 chunks=1 pre"),
-    "columns_chunks": (12288, 96, 5, 1, "columns nc=5 chunks=3 pre"),
-    "stream_columns": (4096, 64, 4, 2, "stream-columns nc=4"),
+FORMS = {  # name: (K, M, N, slices, kernel form prefix, x offset in floats)
+    "burst": (4096, 256, 1, 1, "burst rg=", 0),
+    "burst_chunks": (12288, None, 1, 1, "burst-chunks", 0),
+    "stream": (16640, 96, 1, 1, "stream nc=1", 0),
+    "columns_2": (4096, 96, 2, 1, "columns mfma32 nc=2 chunks=4", 0),
+    "columns_8": (4096, 200, 8, 1, "columns mfma32 nc=8 chunks=4", 0),
+    "columns_one_chunk": (768, 96, 5, 1, "columns mfma32 nc=5 chunks=1", 0),
+    "columns_unaligned_x": (12288, 96, 5, 1, "columns nc=5 chunks=3 pre", 1),
+    "stream_columns": (4096, 64, 4, 2, "stream-columns nc=4", 0),
 }
 
 
@@ -179,15 +181,15 @@ FORMS = {  # name: (K, M, N, slices, kernel form prefix)
 @pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
 def test_nonfinite_activations(hip, dtype, form):
     dev, st = hip
-    K, M, N, S, want = FORMS[form]
+    K, M, N, S, want, off = FORMS[form]
     if M is None:  # 4 row tiles per CU: the chunked burst
         M = 64 * dev.info().compute_units + 40
     q0, d0 = zero_cols(dtype, K, 96, 2400 + K % 97)
     reps = -(-M // 96)
     q, deq = np.tile(q0, reps)[: M * (q0.size // 96)], np.tile(d0, (reps, 1))[:M]
     wb, wt = upload_weights(dev, st, dtype, np.tile(q, S), K, M, slices=S)
-    xb, yb = dev.alloc(4 * K * N * S), dev.alloc(4 * M * N * S)
-    xt = sg.tdesc(sg.F32, (K, N, S), xb)
+    xb, yb = dev.alloc(4 * (K * N * S + off)), dev.alloc(4 * M * N * S)
+    xt = sg.tdesc(sg.F32, (K, N, S), xb, offset=4 * off)
     yt = sg.tdesc(sg.F32, (M, N, S), yb)
     op, keep = sg.mul_mat_op(wt, xt, yt)
     for r in (0, 3):  # (one column: patterns 0 and 3)
