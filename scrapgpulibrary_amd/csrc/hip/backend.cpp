@@ -76,7 +76,7 @@ struct Stream {
     hipStream_t s;
     uint8_t * scratch = nullptr; // prefill matmul: f16 activations, row factors and split-K partials (grown on demand)
     size_t scratch_size = 0;
-    uint64_t scratch_gen = 0;    // process-unique; renewed on every re-allocation (keys recorded graphs)
+    uint64_t scratch_gen = 0;    // process-unique: set at creation, renewed on every re-allocation (keys recorded graphs)
     uint32_t * arrive = nullptr; // the chunked decode matvec's arrival counts (sgk::kArriveMax, zero between launches)
 };
 
@@ -110,6 +110,9 @@ struct Plan {
     std::vector<Buffer *> buffers;
     // the launches of all nodes recorded once as a HIP graph and replayed (per stream: the
     // kernels use the recording stream's scratch)
+    // the captured graph is kept as long as its instantiation (a tracer that resolves a launch's
+    // nodes through the source graph finds it alive)
+    hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     Stream * exec_stream = nullptr;
     uint64_t exec_gen = 0;
@@ -1177,7 +1180,9 @@ scrapgpu_status api_plan_build(scrapgpu_device_t * device, const scrapgpu_plan_d
 
 void plan_drop_graph(Plan * p) {
     if (p->exec) hipGraphExecDestroy(p->exec);
+    if (p->graph) hipGraphDestroy(p->graph);
     p->exec = nullptr;
+    p->graph = nullptr;
     p->exec_stream = nullptr;
 }
 
@@ -1273,6 +1278,9 @@ scrapgpu_status api_plan_execute(scrapgpu_stream_t * stream, scrapgpu_plan_t * p
     scrapgpu_status st = plan_prepare(s, p);
     if (st != SCRAPGPU_STATUS_OK) return st;
     if (p->exec == nullptr || p->exec_stream != s || p->exec_gen != s->scratch_gen) {
+        // a graph recorded for another stream may still run there: wait for the device before
+        // destroying it (the same stream with new scratch was synchronized when it grew)
+        if (p->exec != nullptr && p->exec_stream != s) SG_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
         plan_drop_graph(p);
         SG_HIP(hipStreamBeginCapture(s->s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
         for (size_t i = 0; i < p->nodes.size(); i += (size_t) p->nodes[i].fuse + 1) {
@@ -1287,11 +1295,12 @@ scrapgpu_status api_plan_execute(scrapgpu_stream_t * stream, scrapgpu_plan_t * p
         }
         if (ec != hipSuccess) return hip_fail(ec, "hipStreamEndCapture");
         const hipError_t ei = hipGraphInstantiate(&p->exec, g, nullptr, nullptr, 0);
-        hipGraphDestroy(g);
         if (ei != hipSuccess) {
+            hipGraphDestroy(g);
             p->exec = nullptr;
             return hip_fail(ei, "hipGraphInstantiate");
         }
+        p->graph = g;
         p->exec_stream = s;
         p->exec_gen = s->scratch_gen;
     }
