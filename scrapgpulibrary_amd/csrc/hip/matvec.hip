@@ -1917,7 +1917,8 @@ __global__ __launch_bounds__(64 * RW * KW) __attribute__((amdgpu_waves_per_eu(4,
     using Raw = typename F::Raw;
     constexpr int CPS = mw_cps<DT>(), NS = (NC + CPS - 1) / CPS, SPW = 2, CH = KW * SPW, SEGS = CH * kSegs, R = 32 * RW, T = 64 * RW * KW;
     extern __shared__ uint8_t lds[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform: scalar control
     const int rw = wave % RW, kw = wave / RW;
     const int r = lane & 31, h = lane >> 5;
     const int64_t rt = blockIdx.x;
@@ -2070,7 +2071,7 @@ __global__ __launch_bounds__(64 * RW * KW) __attribute__((amdgpu_waves_per_eu(4,
 }
 
 // waves per work-group: row waves x K waves (measured on the config shapes at N = 2, 4, 8 against
-// 2 x 4, 1 x 8 and 2 x 8: 4 x 2 the fastest or within 5% everywhere)
+// 2 x 4, 1 x 8, 2 x 8, 2 x 2, 2 x 1 and 8 x 1: 4 x 2 the fastest or within 5% everywhere)
 constexpr int kMwRW = 4, kMwKW = 2;
 
 template <int DT>
