@@ -1307,6 +1307,136 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
     }
 }
 
+// The narrow GEMM (9..64 tokens): such a shape is bound by its weight stream, and the tiled forms
+// above spend it on barriers, split-K partial sums and their reduce pass. Here a work-group owns one
+// R32 group (32 weight rows) over all NF token fragments and the whole of K, its KW waves taking
+// consecutive runs of whole 2-stage units; the waves never meet until the end, where their sums
+// are added through LDS in wave order (deterministic) and stored with the rows' factors. A wave
+// reads its A fragments straight from the fragment-ordered x (k_x_to_f16<.., FRAG>): one 16-byte
+// load per lane is two 512-byte runs (the 32 tokens of the lane halves' chunks), kept in a ring 4
+// k-steps ahead of the MFMAs, and its weights one stage ahead, through the formats' exact
+// dequantization (the wide GEMM's). Grid: (R32 groups of all matrices, slices, token fragments /
+// NF): with few R32 groups, each group's fragments go to separate work-groups, gridDim.x apart
+// in dispatch order (a multiple of the 8 XCDs: the same XCD, whose L2 serves the second reader of
+// the weights).
+template <int DT, int NF, int KW, int RW = 1>
+__global__ __launch_bounds__(64 * KW * RW) void k_gemm_n(MmArgs L) {
+    using F = PFmt<DT>;
+    using Raw = typename F::Raw;
+    constexpr int RING = 4;
+    extern __shared__ __attribute__((aligned(16))) float lds_n[]; // [RW][KW / 2][NF * 16][64]
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rw = wv % RW, kw = wv / RW;
+    const int j = lane & 31, h = lane >> 5;
+    // the wave's R32 group (past the last one: the last one again, not stored)
+    const int64_t tm = min<int64_t>((int64_t) blockIdx.x * RW + rw, L.tiles_m - 1), sl = blockIdx.y;
+    const bool live = (int64_t) blockIdx.x * RW + rw < L.tiles_m;
+    const int64_t i2 = sl % L.a.ne12, i3 = sl / L.a.ne12;
+    const int mj = L.nmat == 1 ? 0 : (tm >= L.mt[1] ? (tm >= L.mt[2] ? 2 : 1) : 0);
+    const uint8_t * w = L.nmat > 1 ? L.wm[mj] : L.a.w + (uint64_t) (i2 / L.a.r2) * L.a.w_s2 + (uint64_t) (i3 / L.a.r3) * L.a.w_s3;
+    const int64_t nb = L.a.nb, N = L.a.N;
+    const int64_t M = L.nmat > 1 ? L.Mm[mj] : L.a.M;
+    const int64_t m0 = (tm - L.mt[mj]) * 32;
+    const int S = (int) L.stages, U = (S + 1) / 2; // units of 2 stages (the K-quants' blocks)
+    const int s0 = 2 * (U * kw / KW), s1 = min(2 * (U * (kw + 1) / KW), S), lim = max(s1 - 1, 0);
+
+    F f;
+    f.init(M, nb, RowAddr(M, m0 + j), h);
+    // x fragment (q, stage s, k-step t): 16 bytes at xq + (q S + s) 8192 + co[t]
+    const int tf = (int) ((N + 31) / 32);                // the slice's token fragments
+    const int qz = (int) blockIdx.z * NF;                // this work-group's first one
+    const uint8_t * xq = reinterpret_cast<const uint8_t *>(L.xb) + ((uint64_t) sl * tf + qz) * S * 8192;
+    uint32_t co[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) co[t] = (uint32_t) (F::chunk(h, t) * 32 + j) * 16;
+    auto xload = [&](int s, int t, int q) __attribute__((always_inline)) {
+        return *reinterpret_cast<const f16x8 *>(xq + ((uint32_t) (q * S + s) * 8192u + co[t]));
+    };
+
+    f32x16 acc[NF];
+#pragma unroll
+    for (int q = 0; q < NF; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[q][v] = 0.0f;
+
+    if (s0 < s1) { // (wave-uniform: K shorter than a unit per wave leaves some waves idle)
+        f16x8 ring[RING][NF];
+        // one stage: the weights of stage s + 1 into nw; k-step t's A fragments come from the ring,
+        // which takes k-step t + 4 (of this stage or the next) in their place
+        auto stage = [&](auto dtag, int s, const Raw & cw, Raw & nw) __attribute__((always_inline)) {
+            constexpr int D = decltype(dtag)::value;
+            const int sn = min(s + 1, lim);
+            if constexpr ((DT == Q4_K || DT == Q6_K) && D == 0) nw = f.load_half2(w, sn, cw);
+            else nw = f.load(w, sn);
+            // (the loads stay where they are issued: the scheduler would sink them to their use)
+            __builtin_amdgcn_sched_barrier(0);
+            const typename F::Sc sc = f.prep(cw, (s & ~1) | D);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const f16x8 b = F::bop(cw, sc, t);
+                f16x8 a[NF];
+#pragma unroll
+                for (int q = 0; q < NF; ++q) {
+                    a[q] = ring[t % RING][q];
+                    ring[t % RING][q] = t + RING < 8 ? xload(s, t + RING, q) : xload(sn, t + RING - 8, q);
+                }
+#pragma unroll
+                for (int q = 0; q < NF; ++q) acc[q] = mma32<DT>(a[q], b, acc[q]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        Raw ra = f.load(w, s0), rb;
+#pragma unroll
+        for (int t = 0; t < RING; ++t)
+#pragma unroll
+            for (int q = 0; q < NF; ++q) ring[t][q] = xload(s0, t, q);
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        // (no stage under a branch inside the loop: the compiler would then wait for every load in
+        // flight at the loop's head)
+        int s = s0;
+        for (; s + 1 < s1; s += 2) {
+            stage(I0{}, s, ra, rb);
+            stage(I1{}, s + 1, rb, ra);
+        }
+        if (s < s1) stage(I0{}, s, ra, rb); // (an odd stage count: Q4_0 / Q8_0 only)
+    }
+    // the waves' sums, pairwise in a fixed tree (deterministic): in round r waves r .. 2r - 1 hand
+    // theirs through LDS to waves 0 .. r - 1, which add them; wave 0 stores. acc[q][v], lane (j, h):
+    // token 32 q + 8 (v / 4) + 4 h + v % 4, weight row m0 + j
+    constexpr int PER = NF * 16 * 64;
+#pragma unroll
+    for (int r = KW / 2; r >= 1; r /= 2) {
+        if (kw >= r && kw < 2 * r) {
+#pragma unroll
+            for (int q = 0; q < NF; ++q)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) lds_n[(rw * (KW / 2) + kw - r) * PER + (q * 16 + v) * 64 + lane] = acc[q][v];
+        }
+        __syncthreads();
+        if (kw < r) {
+#pragma unroll
+            for (int q = 0; q < NF; ++q)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[q][v] += lds_n[(rw * (KW / 2) + kw) * PER + (q * 16 + v) * 64 + lane];
+        }
+        if (r > 1) __syncthreads();
+    }
+    if (kw != 0 || !live) return;
+    float * y = L.nmat > 1 ? L.ym[mj] : L.a.y + i2 * L.a.y_s2 + i3 * L.a.y_s3;
+    const int64_t ys1 = L.nmat > 1 ? L.ys1m[mj] : L.a.y_s1;
+    const float * xs = L.xs + (uint64_t) sl * N;
+    const int64_t m = m0 + j;
+#pragma unroll
+    for (int q = 0; q < NF; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int64_t n = 32 * (qz + q) + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (n < N && m < M) y[n * ys1 + m] = acc[q][v] * xs[n];
+        }
+}
+
 // y = sum of the split-K partials, in split order. blockIdx.x is the row (token n of slice sl),
 // blockIdx.y covers 1024 columns of it (all matrices' rows when several share x; column c is row
 // c - mo[j] of matrix j); VEC when every matrix's rows and y's row starts allow float4 accesses.
@@ -1408,13 +1538,19 @@ __global__ __launch_bounds__(256) void k_sk_reduce(MmArgs L) {
 // are stored divided by 16 more, and xsum gets the row's 32-element sub-block sums (of the scaled
 // x, times 1/32 so that they fit f16), 16 per 512 elements in the order the matmul's lanes hold
 // the sub-blocks: position 8 h + e <- sub-block 4 (e / 2) + 2 h + e % 2; missing ones are zero.
-template <bool VEC, bool Q4K, bool BF = false>
+// FRAG (K a multiple of the 128-element stage): the rows in the order the narrow GEMM reads them,
+// chunk c (8 elements) of stage s of token n at ((n / 32 * stages + s) * 16 + c) * 32 + n % 32 in
+// units of 16 bytes (per slice, tokens padded to a multiple of 32): the 32 tokens of one chunk
+// are 512 contiguous bytes.
+template <bool VEC, bool Q4K, bool BF = false, bool FRAG = false>
 __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, float * xs, uint16_t * xsum, int64_t xsum_row) {
     constexpr int kCached = 6; // K <= 12288 is read once
     const int64_t row = blockIdx.x, sl = row / a.N, n = row - sl * a.N;
     const int64_t i2 = sl % a.ne12, i3 = sl / a.ne12;
     const float * xp = a.x + i2 * a.x_s2 + i3 * a.x_s3 + n * a.x_s1;
     uint16_t * op = xb + row * a.K;
+    if constexpr (FRAG)
+        op = xb + ((sl * ((a.N + 31) / 32) + n / 32) * (a.K / BK) * kChunks * 32 + n % 32) * 8;
     auto load8 = [&](int64_t k, float * v) {
         if (VEC) {
             const float4 u = *reinterpret_cast<const float4 *>(xp + k);
@@ -1455,8 +1591,10 @@ __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, floa
         } else {
             const f16x2 p0 = __builtin_convertvector((f32x2{s[0], s[2]}), f16x2), p1 = __builtin_convertvector((f32x2{s[1], s[3]}), f16x2);
             const f16x2 p2 = __builtin_convertvector((f32x2{s[4], s[6]}), f16x2), p3 = __builtin_convertvector((f32x2{s[5], s[7]}), f16x2);
-            *reinterpret_cast<uint4 *>(op + k) = make_uint4(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
-                                                            __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3));
+            // (FRAG: chunk k / 8 of the row is chunk k / 8 % 16 of stage k / 128)
+            uint16_t * d = FRAG ? op + ((k >> 7) * kChunks * 32 + ((k >> 3) & 15) * 32) * 8 : op + k;
+            *reinterpret_cast<uint4 *>(d) = make_uint4(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                                                       __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3));
         }
     };
     const int64_t k0 = (int64_t) threadIdx.x * 8; // K is a multiple of 32: a group of 8 is whole
@@ -1564,6 +1702,11 @@ __global__ __launch_bounds__(1024) void k_moe_route(const int32_t * ids, int64_t
     for (int p = tid; p < P; p += 1024) pairs[atomicAdd(&cur[pe[p]], 1)] = p;
 }
 
+int env_int(const char * name, int dflt) {
+    const char * v = std::getenv(name);
+    return v != nullptr && *v ? std::atoi(v) : dflt;
+}
+
 // Tile shape and work-groups along K per tile. A work-group is 4 waves; each wave owns RG groups
 // of 32 weight rows (the tile is 128 RG rows) and BN tokens. Every A fragment read from LDS feeds
 // RG MFMAs. Splits along K are added while the tiles leave the CUs' work-group slots empty, each
@@ -1575,12 +1718,20 @@ struct MmConfig {
     int kg; // K groups of a 12-wave work-group: 1 or 3
     bool wide = false; // k_gemm_w (w = 12): 128-token wave tiles (kg 1 or 2, bn = 128), or 64-token ones (kg = 1, bn = 64)
     bool sk = false;   // the wide form's stream-K (kg = 1, bn = 128): cu_count work-groups share all tiles' stages
+    bool narrow = false; // k_gemm_n: 9..64 tokens, rw R32 groups per work-group, kw waves along K each
+    int kw = 8;
+    int nz = 1; // narrow: work-groups per R32 group, each with bn / nz tokens
+    int rw = 1; // narrow: R32 groups per work-group (kw waves each)
 };
 
-int env_int(const char * name, int dflt) {
-    const char * v = std::getenv(name);
-    return v != nullptr && *v ? std::atoi(v) : dflt;
+// the narrow GEMM's shapes: quantized weights, 9..64 tokens, one slice, K a whole number of
+// stages; x then goes to scratch in fragment order, its token rows padded to a multiple of 32
+bool narrow_shape(const MatArgs & a) {
+    static const int env = env_int("SCRAPGPU_HIP_MM_NARROW", 1);
+    return env != 0 && (a.dtype == Q4_0 || a.dtype == Q8_0 || a.dtype == Q4_K || a.dtype == Q6_K) && a.N > 8 && a.N <= 64 &&
+           a.ne12 * a.ne13 == 1 && a.K % BK == 0;
 }
+
 
 MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
     static const int env_bn = env_int("SCRAPGPU_HIP_MM_BN", 0), env_rg = env_int("SCRAPGPU_HIP_MM_RG", 0);
@@ -1589,6 +1740,35 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
     const int64_t stages = (a.K + BK - 1) / BK;
     static const int env_w = env_int("SCRAPGPU_HIP_MM_W", 0);
     MmConfig c;
+    if (narrow_shape(a) && env_w == 0 && env_bn == 0 && env_split == 0) {
+        static const int env_kw = env_int("SCRAPGPU_HIP_MM_KW", 0);
+        // R32 groups < CUs: one group per work-group (and 64 tokens as two work-groups of 32,
+        // 8 waves each; 32 tokens in 16 waves); up to 2x the CUs: two groups per work-group (the
+        // waves of a K run read the same x, the second mostly from L1). Measured on 256 CUs
+        // (op time with the x pre-pass, against the forms below): Q4_K 12288x4096 at 64 / 32 / 16
+        // tokens 26.8 / 19.9 / 18.9 against 31.4 / 27.6 / 26.5 us, 4096x12288 at 64 / 32 27.9 /
+        // 25.2 against 31.1 / 28.9, 4096x4096 at 64 16.2 against 23.2; more groups lost (gate+up
+        // 24576 rows 38-39 against 35.6, the Q6_K LM head 224-246 against 153)
+        static const int env_nz = env_int("SCRAPGPU_HIP_MM_NZ", 0);
+        static const int env_rw = env_int("SCRAPGPU_HIP_MM_RW", 0);
+        const int64_t groups = (a.M + 31) / 32;
+        if (groups <= 2 * (int64_t) cu_count || env_rw > 0) {
+            c.narrow = true;
+            c.kg = c.rg = c.split = 1;
+            c.bn = a.N <= 32 ? 32 : 64;
+            c.rw = env_rw == 1 || env_rw == 2 || env_rw == 4 ? env_rw : groups < cu_count ? 1 : 2;
+            c.nz = c.rw == 1 && c.bn == 64 && (env_nz == 2 || (env_nz == 0 && groups < cu_count)) ? 2 : 1;
+            if (c.rw == 1) {
+                c.kw = env_kw == 8 || env_kw == 16 ? env_kw : groups * c.nz >= cu_count ? 8 : 16;
+                if (c.kw == 16 && c.bn / c.nz == 64) c.kw = 8; // (64 tokens in 16 waves: more registers than 1024 threads allow)
+            } else {
+                if (c.rw == 4 && c.bn == 64) c.rw = 2; // (not built)
+                c.kw = c.bn == 64 || c.rw == 4 ? 4 : 8;
+            }
+            c.w = c.kw * c.rw;
+            return c;
+        }
+    }
     if (a.dtype == F16 || a.dtype == BF16) {
         // the wide GEMM (k_gemm_w, 384-row x 128-token tiles; its 2-K-group form spills with the
         // float rows' raw data) where its tiles fill the CUs, or with K split so that they occupy
@@ -1803,7 +1983,8 @@ void * kernel_of_float(const MmConfig & c) {
 // scratch: x as f16 [slices][N][K] | row factors [slices][N] | Q4_K sub-block sums
 // [slices][N][xsum_row] | split-K partials
 size_t xs_offset(const MatArgs & a) {
-    return ((size_t) a.N * (size_t) a.K * (size_t) (a.ne12 * a.ne13) * sizeof(uint16_t) + 255) / 256 * 256;
+    const size_t rows = narrow_shape(a) ? (size_t) (a.N + 31) / 32 * 32 : (size_t) a.N; // (fragment order: whole fragments)
+    return (rows * (size_t) a.K * (size_t) (a.ne12 * a.ne13) * sizeof(uint16_t) + 255) / 256 * 256;
 }
 
 int64_t xsum_row_of(const MatArgs & a) {
@@ -1851,6 +2032,54 @@ static size_t sk_part_bytes(const MatArgs & a, int cu_count) {
 
 static bool float_gemm(const MatArgs & a);
 
+template <int DT>
+static void * narrow_kernel(int nf, int kw, int rw) {
+    if (nf == 1) {
+        if (rw == 4) return (void *) k_gemm_n<DT, 1, 4, 4>;
+        if (rw == 2) return (void *) k_gemm_n<DT, 1, 8, 2>;
+        return kw == 16 ? (void *) k_gemm_n<DT, 1, 16> : (void *) k_gemm_n<DT, 1, 8>;
+    }
+    if (rw == 2) return (void *) k_gemm_n<DT, 2, 4, 2>;
+    return (void *) k_gemm_n<DT, 2, 8>; // (2 fragments in 16 waves would spill: not built)
+}
+
+// the narrow GEMM: one work-group per R32 group of each matrix (and slice)
+static hipError_t launch_narrow(MmArgs & L, const MatArgs * mats, int nmat, const MmConfig & cfg, hipStream_t stream, const char ** kernel_name) {
+    const MatArgs & a = L.a;
+    const int nf = cfg.bn / 32 / cfg.nz;
+    L.nmat = nmat;
+    L.mt[0] = L.mo[0] = 0;
+    for (int j = 0; j < 3; ++j) {
+        const bool has = j < nmat;
+        L.wm[j] = has ? mats[j].w : nullptr;
+        L.Mm[j] = has ? mats[j].M : 0;
+        L.ym[j] = has ? mats[j].y : nullptr;
+        L.ys1m[j] = has ? mats[j].y_s1 : 0;
+        L.mt[j + 1] = L.mt[j] + (has ? (mats[j].M + 31) / 32 : 0);
+        L.mo[j + 1] = L.mo[j] + (has ? mats[j].M : 0);
+    }
+    L.tiles_m = L.mt[nmat];
+    L.tiles_n = 1;
+    L.stages = a.K / BK;
+    L.split = 1;
+    void * fn = nullptr;
+    switch (a.dtype) {
+        case Q4_0: fn = narrow_kernel<Q4_0>(nf, cfg.kw, cfg.rw); if (kernel_name) *kernel_name = "matmul_mfma_q4_0"; break;
+        case Q8_0: fn = narrow_kernel<Q8_0>(nf, cfg.kw, cfg.rw); if (kernel_name) *kernel_name = "matmul_mfma_q8_0"; break;
+        case Q4_K: fn = narrow_kernel<Q4_K>(nf, cfg.kw, cfg.rw); if (kernel_name) *kernel_name = "matmul_mfma_q4_k"; break;
+        case Q6_K: fn = narrow_kernel<Q6_K>(nf, cfg.kw, cfg.rw); if (kernel_name) *kernel_name = "matmul_mfma_q6_k"; break;
+        default: return hipErrorInvalidValue;
+    }
+    const size_t lds = (size_t) cfg.rw * (cfg.kw / 2) * nf * 16 * 64 * sizeof(float);
+    hipError_t e = allow_lds(fn, lds);
+    if (e != hipSuccess) return e;
+    const dim3 grid((unsigned) ((L.tiles_m + cfg.rw - 1) / cfg.rw), (unsigned) (a.ne12 * a.ne13), (unsigned) cfg.nz);
+    std::snprintf(last_form().form, sizeof(last_form().form), "gemm narrow rw=%d kw=%d bn=%d nz=%d", cfg.rw, cfg.kw, cfg.bn, cfg.nz);
+    last_form().grid = (uint64_t) grid.x * grid.y;
+    void * args[] = {&L};
+    return hipLaunchKernel(fn, grid, dim3((unsigned) (64 * cfg.kw * cfg.rw)), args, lds, stream);
+}
+
 size_t matmul_scratch_bytes(const MatArgs & a, int cu_count, bool lean) {
     // (float weights off the GEMM run the float matvec, which takes no scratch)
     if (is_float_weight(a.dtype) && !float_gemm(a)) return 0;
@@ -1862,7 +2091,13 @@ size_t matmul_scratch_bytes(const MatArgs & a, int cu_count, bool lean) {
 // the pre-pass writes Q4_K's single-fma form of x (high-nibble positions / 16, sub-block sums)
 // for the Q4_K kernels that use it, plain scaled x for every other kernel
 static bool q4k_x_form(const MatArgs & a, int cu_count, bool lean) {
-    return a.dtype == Q4_K && !config_of(a, cu_count, lean).wide;
+    const MmConfig c = config_of(a, cu_count, lean);
+    return a.dtype == Q4_K && !c.wide && !c.narrow;
+}
+
+// x in the narrow GEMM's fragment order
+static bool frag_x_form(const MatArgs & a, int cu_count, bool lean) {
+    return !is_float_weight(a.dtype) && config_of(a, cu_count, lean).narrow;
 }
 
 // float weights on the GEMM: F16 / BF16 with K a whole number of 128-element stages (x rows in bf16
@@ -1877,7 +2112,8 @@ bool matmul_reads_same_x(const MatArgs & a, const MatArgs & b) {
 }
 
 bool matmul_same_x(const MatArgs & a, const MatArgs & b, int cu_count, bool lean) {
-    return matmul_reads_same_x(a, b) && q4k_x_form(a, cu_count, lean) == q4k_x_form(b, cu_count, lean) && (a.dtype == BF16) == (b.dtype == BF16) &&
+    return matmul_reads_same_x(a, b) && q4k_x_form(a, cu_count, lean) == q4k_x_form(b, cu_count, lean) &&
+           frag_x_form(a, cu_count, lean) == frag_x_form(b, cu_count, lean) && (a.dtype == BF16) == (b.dtype == BF16) &&
            !(is_float_weight(a.dtype) && !float_gemm(a)) && !(is_float_weight(b.dtype) && !float_gemm(b));
 }
 
@@ -1903,6 +2139,11 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     const MmConfig cfg = config_of(a, cu_count, lean);
     if (x_ready) {
         // x converted by the previous product's pre-pass (matmul_same_x)
+    } else if (cfg.narrow) {
+        if (vec)
+            hipLaunchKernelGGL((k_x_to_f16<true, false, false, true>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
+        else
+            hipLaunchKernelGGL((k_x_to_f16<false, false, false, true>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
     } else if (a.dtype == Q4_K && !cfg.wide) {
         if (vec)
             hipLaunchKernelGGL((k_x_to_f16<true, true>), xg, dim3(256), 0, stream, a, xb, xs, xsum, xsum_row);
@@ -1927,6 +2168,7 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     L.xb = xb;
     L.xs = xs;
     L.part = reinterpret_cast<float *>(scratch + part_offset(a));
+    if (cfg.narrow) return launch_narrow(L, mats, nmat, cfg, stream, kernel_name);
     L.xsum = xsum;
     L.xsum_row = xsum_row;
     const int BN = cfg.bn;

@@ -1,0 +1,106 @@
+"""The narrow GEMM (k_gemm_n: 9..64 tokens, one R32 group per work-group, K split over its waves
+and added in LDS): every quantized dtype against the oracle at the prefill gate (NMSE <= 5e-5, and
+per token row), on shapes that reach its edges -- a partial last R32 group, token counts on both
+sides of the 32-token fragment, a stage count below the waves (idle waves), an odd stage count
+(Q4_0 / Q8_0), both wave counts (8 and 16) -- plus MUL_MAT_MULTI over weights whose row counts are
+not multiples of 32, repeat launches (bit-identical), and a plan replay."""
+import numpy as np
+import pytest
+
+import oracle as O
+import scrapgpulibrary_amd as sg
+from tests.gpu_util import nmse, quantized, upload_weights
+
+pytestmark = pytest.mark.gpu
+
+QT = (sg.Q4_0, sg.Q8_0, sg.Q4_K, sg.Q6_K)
+
+# (K, M, N): M = 1000 and 333 end in a partial R32 group; 96 rows leave most CUs without a group
+# (16 waves, or 64 tokens as two work-groups); 12288 and 8990 rows are 1-2 groups per CU (two
+# groups per work-group; 8990 rows: an odd group count, the last work-group's second wave idle);
+# K = 256 is 2 stages for 8-16 waves; K = 384 an odd stage count
+SHAPES = [(4096, 1000, 9), (2048, 333, 17), (1536, 64, 32), (4096, 100, 33), (256, 40, 64), (12288, 96, 64),
+          (4096, 12288, 64), (2048, 8990, 30), (384, 200, 48)]
+
+
+def cases():
+    out = []
+    for dt in QT:
+        for K, M, N in SHAPES:
+            if K % sg.BLOCK[dt] == 0:
+                out.append((dt, K, M, N))
+    return out
+
+
+def run(hip, dt, q, K, M, x):
+    dev, st = hip
+    N = x.shape[0]
+    wb, wt = upload_weights(dev, st, dt, q, K, M)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    st.upload(xt, x)
+    yb = dev.alloc(4 * M * N)
+    yt = sg.tdesc(sg.F32, (M, N), yb)
+    op, keep = sg.mul_mat_op(wt, xt, yt)
+    ys = []
+    for _ in range(2):
+        st.execute(op)
+        st.sync()
+        ys.append(st.download(yt).reshape(N, M).copy())
+    form = sg.last_launch()[0]
+    for b in (wb, xb, yb):
+        b.free()
+    return ys, form
+
+
+def check(y, ref, what):
+    e = nmse(y, ref)
+    assert e <= 5e-5, f"{what}: NMSE {e:.3e}"
+    for n in range(y.shape[0]):
+        en = nmse(y[n], ref[n])
+        assert en <= 2e-4, f"{what}: token {n} NMSE {en:.3e}"
+
+
+@pytest.mark.parametrize("case", cases(), ids=lambda c: f"{O.NAMES[c[0]]}-K{c[1]}-M{c[2]}-N{c[3]}")
+def test_narrow(hip, case):
+    dt, K, M, N = case
+    q, _ = quantized(dt, K, M, 7 + K + M)
+    x = O.normal(N * K, 11 + N).reshape(N, K)
+    # heavy-tailed rows and an outlier channel: the per-row f16 scaling of x
+    x[0] *= 1000.0
+    x[-1] *= 1e-3
+    x[:, 5] *= 50.0
+    (y, y2), form = run(hip, dt, q, K, M, x)
+    assert form.startswith("gemm narrow"), form
+    assert np.array_equal(y, y2), "repeat launch differs"
+    ref = O.mul_mat(dt, q, K, M, x, threads=8)
+    check(y, ref, f"{O.NAMES[dt]} {M}x{K} N={N} [{form}]")
+
+
+@pytest.mark.parametrize("dt", QT, ids=lambda d: O.NAMES[d])
+def test_narrow_multi(hip, dt):
+    """MUL_MAT_MULTI: three weights (row counts 100, 257, 64) sharing x at 40 tokens, one launch."""
+    dev, st = hip
+    K, N, Ms = 2048, 40, (100, 257, 64)
+    x = O.normal(N * K, 5).reshape(N, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    st.write(xb, 0, x)
+    bufs, wts, yts, refs = [xb], [], [], []
+    for j, M in enumerate(Ms):
+        q, _ = quantized(dt, K, M, 60 + j)
+        wb, wt = upload_weights(dev, st, dt, q, K, M)
+        yb = dev.alloc(4 * M * N)
+        bufs += [wb, yb]
+        wts.append(wt)
+        yts.append(sg.tdesc(sg.F32, (M, N), yb))
+        refs.append(O.mul_mat(dt, q, K, M, x, threads=8))
+    op, keep = sg.multi_op(wts, xt, yts)
+    st.execute(op)
+    st.sync()
+    form = sg.last_launch()[0]
+    assert form.startswith("gemm narrow"), form
+    for M, yt, ref in zip(Ms, yts, refs):
+        check(st.download(yt).reshape(N, M), ref, f"{O.NAMES[dt]} {M} rows of {Ms} N={N} [{form}]")
+    for b in bufs:
+        b.free()
