@@ -1307,18 +1307,21 @@ __global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
     }
 }
 
-// The narrow GEMM (9..64 tokens): such a shape is bound by its weight stream, and the tiled forms
-// above spend it on barriers, split-K partial sums and their reduce pass. Here a work-group owns one
-// R32 group (32 weight rows) over all NF token fragments and the whole of K, its KW waves taking
-// consecutive runs of whole 2-stage units; the waves never meet until the end, where their sums
-// are added through LDS in wave order (deterministic) and stored with the rows' factors. A wave
-// reads its A fragments straight from the fragment-ordered x (k_x_to_f16<.., FRAG>): one 16-byte
-// load per lane is two 512-byte runs (the 32 tokens of the lane halves' chunks), kept in a ring 4
-// k-steps ahead of the MFMAs, and its weights one stage ahead, through the formats' exact
-// dequantization (the wide GEMM's). Grid: (R32 groups of all matrices, slices, token fragments /
-// NF): with few R32 groups, each group's fragments go to separate work-groups, gridDim.x apart
-// in dispatch order (a multiple of the 8 XCDs: the same XCD, whose L2 serves the second reader of
-// the weights).
+// The narrow GEMM (9..128 tokens, up to ~2 R32 groups per CU): the tiled forms above spend such a
+// shape on stage barriers, split-K partial sums and their reduce pass. Here a work-group owns RW
+// R32 groups (32 weight rows each) over NF token fragments and the whole of K, KW waves per group
+// taking consecutive runs of whole 2-stage units; the waves never meet until the end, where their
+// sums are added pairwise in a fixed tree through LDS (deterministic) and stored with the rows'
+// factors. A wave reads its A fragments straight from the fragment-ordered x (k_x_to_f16<..,
+// FRAG>): one 16-byte load per lane is two 512-byte runs (the 32 tokens of the lane halves'
+// chunks), kept in a ring 4 k-steps ahead of the MFMAs, and its weights one stage ahead, through
+// the formats' exact dequantization (the wide GEMM's). With RW = 2 the waves of one K run read the
+// same x at about the same time (the second mostly from L1). Grid: (work-groups of RW R32 groups
+// of all matrices, slices, token fragments / NF): with few R32 groups, each group's fragments go
+// to separate work-groups, gridDim.x apart in dispatch order (with the usual round-robin over the
+// 8 XCDs and gridDim.x a multiple of 8, the same XCD, whose L2 serves the second reader of the
+// weights). What bounds it: every wave reads 64 bytes of x per 18 bytes of Q4_K weights, so each
+// CU moves ~1 MB of x from L2 per 12288x4096 op at 64 tokens (~80 GB/s per CU measured).
 template <int DT, int NF, int KW, int RW = 1>
 __global__ __launch_bounds__(64 * KW * RW) void k_gemm_n(MmArgs L) {
     using F = PFmt<DT>;
@@ -1718,17 +1721,17 @@ struct MmConfig {
     int kg; // K groups of a 12-wave work-group: 1 or 3
     bool wide = false; // k_gemm_w (w = 12): 128-token wave tiles (kg 1 or 2, bn = 128), or 64-token ones (kg = 1, bn = 64)
     bool sk = false;   // the wide form's stream-K (kg = 1, bn = 128): cu_count work-groups share all tiles' stages
-    bool narrow = false; // k_gemm_n: 9..64 tokens, rw R32 groups per work-group, kw waves along K each
+    bool narrow = false; // k_gemm_n: 9..128 tokens, rw R32 groups per work-group, kw waves along K each
     int kw = 8;
     int nz = 1; // narrow: work-groups per R32 group, each with bn / nz tokens
     int rw = 1; // narrow: R32 groups per work-group (kw waves each)
 };
 
-// the narrow GEMM's shapes: quantized weights, 9..64 tokens, one slice, K a whole number of
+// the narrow GEMM's shapes: quantized weights, 9..128 tokens, one slice, K a whole number of
 // stages; x then goes to scratch in fragment order, its token rows padded to a multiple of 32
 bool narrow_shape(const MatArgs & a) {
     static const int env = env_int("SCRAPGPU_HIP_MM_NARROW", 1);
-    return env != 0 && (a.dtype == Q4_0 || a.dtype == Q8_0 || a.dtype == Q4_K || a.dtype == Q6_K) && a.N > 8 && a.N <= 64 &&
+    return env != 0 && (a.dtype == Q4_0 || a.dtype == Q8_0 || a.dtype == Q4_K || a.dtype == Q6_K) && a.N > 8 && a.N <= 128 &&
            a.ne12 * a.ne13 == 1 && a.K % BK == 0;
 }
 
@@ -1752,18 +1755,22 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
         static const int env_nz = env_int("SCRAPGPU_HIP_MM_NZ", 0);
         static const int env_rw = env_int("SCRAPGPU_HIP_MM_RW", 0);
         const int64_t groups = (a.M + 31) / 32;
-        if (groups <= 2 * (int64_t) cu_count || env_rw > 0) {
+        // (65..128 tokens: two work-groups of 64 per R32 group where the groups are fewer than the
+        // CUs: 4096x4096 22.4 against 32.2 us, 6144x4096 28.1 against 34.7, 4096x12288 38.9 against
+        // 41.4; 12288x4096 lost, 41.1 against 36.0)
+        if ((a.N <= 64 ? groups <= 2 * (int64_t) cu_count : groups < cu_count) || env_rw > 0) {
             c.narrow = true;
             c.kg = c.rg = c.split = 1;
-            c.bn = a.N <= 32 ? 32 : 64;
+            c.bn = a.N <= 32 ? 32 : a.N <= 64 ? 64 : 128;
             c.rw = env_rw == 1 || env_rw == 2 || env_rw == 4 ? env_rw : groups < cu_count ? 1 : 2;
             c.nz = c.rw == 1 && c.bn == 64 && (env_nz == 2 || (env_nz == 0 && groups < cu_count)) ? 2 : 1;
+            if (c.bn == 128) c.nz = env_nz == 4 && c.rw == 1 ? 4 : 2;
             if (c.rw == 1) {
                 c.kw = env_kw == 8 || env_kw == 16 ? env_kw : groups * c.nz >= cu_count ? 8 : 16;
                 if (c.kw == 16 && c.bn / c.nz == 64) c.kw = 8; // (64 tokens in 16 waves: more registers than 1024 threads allow)
             } else {
-                if (c.rw == 4 && c.bn == 64) c.rw = 2; // (not built)
-                c.kw = c.bn == 64 || c.rw == 4 ? 4 : 8;
+                if (c.rw == 4 && c.bn / c.nz == 64) c.rw = 2; // (not built)
+                c.kw = c.bn / c.nz == 64 || c.rw == 4 ? 4 : 8;
             }
             c.w = c.kw * c.rw;
             return c;

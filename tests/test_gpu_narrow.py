@@ -1,5 +1,5 @@
-"""The narrow GEMM (k_gemm_n: 9..64 tokens, one R32 group per work-group, K split over its waves
-and added in LDS): every quantized dtype against the oracle at the prefill gate (NMSE <= 5e-5, and
+"""The narrow GEMM (k_gemm_n: 9..128 tokens, one or two R32 groups per work-group, K split over
+its waves and added in LDS): every quantized dtype against the oracle at the prefill gate (NMSE <= 5e-5, and
 per token row), on shapes that reach its edges -- a partial last R32 group, token counts on both
 sides of the 32-token fragment, a stage count below the waves (idle waves), an odd stage count
 (Q4_0 / Q8_0), both wave counts (8 and 16) -- plus MUL_MAT_MULTI over weights whose row counts are
@@ -18,9 +18,10 @@ QT = (sg.Q4_0, sg.Q8_0, sg.Q4_K, sg.Q6_K)
 # (K, M, N): M = 1000 and 333 end in a partial R32 group; 96 rows leave most CUs without a group
 # (16 waves, or 64 tokens as two work-groups); 12288 and 8990 rows are 1-2 groups per CU (two
 # groups per work-group; 8990 rows: an odd group count, the last work-group's second wave idle);
-# K = 256 is 2 stages for 8-16 waves; K = 384 an odd stage count
+# K = 256 is 2 stages for 8-16 waves; K = 384 an odd stage count; 100 and 128 tokens run as two
+# work-groups of 64 per group
 SHAPES = [(4096, 1000, 9), (2048, 333, 17), (1536, 64, 32), (4096, 100, 33), (256, 40, 64), (12288, 96, 64),
-          (4096, 12288, 64), (2048, 8990, 30), (384, 200, 48)]
+          (4096, 12288, 64), (2048, 8990, 30), (384, 200, 48), (2048, 1000, 100), (1024, 64, 128)]
 
 
 def cases():
@@ -102,5 +103,45 @@ def test_narrow_multi(hip, dt):
     assert form.startswith("gemm narrow"), form
     for M, yt, ref in zip(Ms, yts, refs):
         check(st.download(yt).reshape(N, M), ref, f"{O.NAMES[dt]} {M} rows of {Ms} N={N} [{form}]")
+    for b in bufs:
+        b.free()
+
+
+def test_narrow_plan_replays_shared_x(hip):
+    """A plan of a Q4_K and a Q6_K product reading the same x at 48 tokens (the second reuses the
+    first's fragment-ordered x), replayed as a graph with new x each time, every replay against
+    the oracle."""
+    import ctypes as C
+
+    dev, st = hip
+    L = sg.lib()
+    K, N = 1024, 48
+    specs = [(sg.Q4_K, 300, 90), (sg.Q6_K, 200, 91)]
+    xb = dev.alloc(4 * K * N)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    bufs, items = [xb], []
+    for dt, M, seed in specs:
+        q, _ = quantized(dt, K, M, seed)
+        wb, wt = upload_weights(dev, st, dt, q, K, M)
+        yb = dev.alloc(4 * M * N)
+        yt = sg.tdesc(sg.F32, (M, N), yb)
+        op, keep = sg.mul_mat_op(wt, xt, yt)
+        bufs += [wb, yb]
+        items.append((dt, M, q, yt, op, keep))
+    nodes = (sg.PlanNode * 2)(*[sg.PlanNode(C.sizeof(sg.PlanNode), it[4], 0) for it in items])
+    pd = sg.PlanDesc(C.sizeof(sg.PlanDesc), nodes, 2)
+    plan = C.c_void_p()
+    sg.check(L.scrapgpu_plan_build(dev.handle, C.byref(pd), C.byref(plan)), "plan_build")
+    try:
+        for rep in range(3):
+            x = O.normal(N * K, 200 + rep).reshape(N, K)
+            st.upload(xt, x)
+            st.sync()
+            sg.check(L.scrapgpu_plan_execute(st.handle, plan), "plan_execute")
+            st.sync()
+            for dt, M, q, yt, _, _ in items:
+                check(st.download(yt).reshape(N, M), O.mul_mat(dt, q, K, M, x, threads=8), f"replay {rep} {O.NAMES[dt]}")
+    finally:
+        sg.check(L.scrapgpu_plan_free(plan), "plan_free")
     for b in bufs:
         b.free()
