@@ -33,12 +33,14 @@ def cases():
     return out
 
 
-def run(hip, dt, q, K, M, x):
+def run(hip, dt, q, K, M, x, off=0):
+    """(two launches' y, form); off: x starts `off` floats into its buffer (off % 4 != 0: not
+    16-byte aligned, the pre-pass's scalar path)."""
     dev, st = hip
     N = x.shape[0]
     wb, wt = upload_weights(dev, st, dt, q, K, M)
-    xb = dev.alloc(x.nbytes)
-    xt = sg.tdesc(sg.F32, (K, N), xb)
+    xb = dev.alloc(x.nbytes + 4 * off)
+    xt = sg.tdesc(sg.F32, (K, N), xb, offset=4 * off)
     st.upload(xt, x)
     yb = dev.alloc(4 * M * N)
     yt = sg.tdesc(sg.F32, (M, N), yb)
@@ -76,6 +78,17 @@ def test_narrow(hip, case):
     assert np.array_equal(y, y2), "repeat launch differs"
     ref = O.mul_mat(dt, q, K, M, x, threads=8)
     check(y, ref, f"{O.NAMES[dt]} {M}x{K} N={N} [{form}]")
+
+
+@pytest.mark.parametrize("dt", QT, ids=lambda d: O.NAMES[d])
+def test_narrow_unaligned_x(hip, dt):
+    """x one float past a 16-byte boundary: the pre-pass reads it element by element."""
+    K, M, N = 1024, 200, 40
+    q, _ = quantized(dt, K, M, 21)
+    x = O.normal(N * K, 22).reshape(N, K)
+    (y, _), form = run(hip, dt, q, K, M, x, off=1)
+    assert form.startswith("gemm narrow"), form
+    check(y, O.mul_mat(dt, q, K, M, x, threads=8), f"{O.NAMES[dt]} unaligned x [{form}]")
 
 
 @pytest.mark.parametrize("dt", QT, ids=lambda d: O.NAMES[d])
