@@ -42,8 +42,8 @@ def test_static_scratch_matches_op_execute(hip, dtype, K):
     M = 1536 if K == 4096 else 64 * dev.info().compute_units
     q, _ = quantized(dtype, K, M, 1500)
     wb, wt = upload_weights(dev, st, dtype, q, K, M)
-    # prefill at 512 tokens (f16 x in the scratch), then 64 tokens (split-K partials as well), then
-    # one decode column (no scratch): each against scrapgpu_op_execute and the oracle
+    # prefill at 512 tokens (f16 x in the scratch), then 64 tokens (the narrow GEMM: x in fragment
+    # order), then one decode column (no scratch): each against scrapgpu_op_execute and the oracle
     for N in ((512, 64, 1) if K == 4096 else (64, 1)):  # (512 tokens at K = 12288 need more than the static scratch)
         x = O.normal(N * K, 1501 + N).reshape(N, K)
         y_static = _run(dev, st, wt, x, M, True)
