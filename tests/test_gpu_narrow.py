@@ -158,3 +158,28 @@ def test_narrow_plan_replays_shared_x(hip):
         sg.check(L.scrapgpu_plan_free(plan), "plan_free")
     for b in bufs:
         b.free()
+
+
+@pytest.mark.parametrize("dt,K,M,N", [(sg.Q4_K, 4096, 12288, 64), (sg.Q6_K, 2048, 500, 100), (sg.Q8_0, 1024, 64, 20)],
+                         ids=["q4_k-2groups", "q6_k-100tok", "q8_0-idle-waves"])
+def test_narrow_new_x_each_launch(hip, dt, K, M, N):
+    """One op launched three times with new x (of growing magnitude) written before each: every
+    launch converts and reads its own x."""
+    dev, st = hip
+    q, _ = quantized(dt, K, M, 300 + N)
+    wb, wt = upload_weights(dev, st, dt, q, K, M)
+    xb = dev.alloc(4 * N * K)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    yb = dev.alloc(4 * M * N)
+    yt = sg.tdesc(sg.F32, (M, N), yb)
+    op, keep = sg.mul_mat_op(wt, xt, yt)
+    for rep in range(3):
+        x = O.normal(N * K, 310 + rep).reshape(N, K) * (10.0 ** (rep - 1))
+        st.upload(xt, x)
+        st.execute(op)
+        st.sync()
+        form = sg.last_launch()[0]
+        assert form.startswith("gemm narrow"), form
+        check(st.download(yt).reshape(N, M), O.mul_mat(dt, q, K, M, x, threads=8), f"launch {rep} [{form}]")
+    for b in (wb, xb, yb):
+        b.free()
