@@ -838,6 +838,22 @@ __device__ void exact_segments(const MvArgs & A, const Where & wh, const Row & r
 // so that a long K runs on several small work-groups instead of one large one per tile. The
 // chunks' partial sums meet as in k_mvc: agent-scope stores, an arrival count per tile, and the
 // last chunk to arrive adds them in chunk order and resets the count.
+// The sum over c = 0 .. n - 1 of p[c stride], added in order of c (the chunk hand-overs below):
+// agent-scope loads (coherent across XCDs by themselves), issued in batches of 8 before any is
+// added, so the last chunk pays one memory round trip per 8 chunks instead of one per chunk.
+__device__ __forceinline__ float ordered_sum(const float * p, int64_t stride, int64_t n) {
+    float t = 0.0f;
+    for (int64_t c0 = 0; c0 < n; c0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = c0 + i < n ? __hip_atomic_load(p + (c0 + i) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (c0 + i < n) t += v[i];
+    }
+    return t;
+}
+
 template <int DT, int RG, int W, int SPW, bool CHUNK = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2 && RG == 1 ? 6 : SPW <= 2 && RG == 2 ? 5 : 4, 8))) void k_mvb(MvArgs A) {
     static_assert(!CHUNK || W * SPW == kChunkSteps, "chunks of kChunkSteps steps");
@@ -877,8 +893,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2
     F f[RG];
     const Row row = row_of<DT, RG>(A, blockIdx.x, wh.w_off, lane & 15, lane >> 4, f);
     Raw buf[SPW][RG];
+    // step 0's loads go out before the x conversion, the others after it: a wave stalls issuing
+    // loads once the memory pipeline is full, and x converted behind all of them was the last
+    // thing a work-group waited for (the decode token 1.18 -> 1.12 ms on one box)
+    constexpr int S0 = 1;
 #pragma unroll
-    for (int s = 0; s < SPW; ++s) {
+    for (int s = 0; s < S0; ++s) {
         const int64_t ss = s < ns ? s0 + s : s0; // steps past the wave's range: reloaded, unused
 #pragma unroll
         for (int i = 0; i < RG; ++i) buf[s][i] = f[i].load(ss);
@@ -894,6 +914,14 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2
     bool sp = false;
 #pragma unroll
     for (int p = 0; p < XP; ++p) sp |= convert_seg(xv[p], 16 * p + (lane >> 2), nseg, lane & 3, xs, xf);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = S0; s < SPW; ++s) {
+        const int64_t ss = s < ns ? s0 + s : s0;
+#pragma unroll
+        for (int i = 0; i < RG; ++i) buf[s][i] = f[i].load(ss);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     const bool special = __ballot(sp) != 0;
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -945,9 +973,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2
         // count's atomic returned (the barrier that publishes `last`)
         if (last && tid < R) {
             const int64_t m = row.m0 + tid;
-            float t = 0.0f;
-            for (int64_t c = 0; c < A.nck; ++c)
-                t += __hip_atomic_load(A.part + (c * A.tiles + tile) * R + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float t = ordered_sum(A.part + tile * R + tid, A.tiles * R, A.nck);
             if (m < row.M) A.y[row.j][m] = t;
             if (tid == 0) __hip_atomic_store(A.arrive + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -1652,10 +1678,7 @@ __global__ __launch_bounds__(64 * kMcW) __attribute__((amdgpu_waves_per_eu(mc_wa
     if (last && tid < NC * 16) {
         const int n = tid / 16, rr = tid % 16;
         if (m0 + rr < M) {
-            float v = 0.0f;
-            for (int64_t cc = 0; cc < A.nchunks; ++cc)
-                v += __hip_atomic_load(A.part + (cc * NC + n) * A.prow + rt * 16 + rr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            A.y[j][n * A.ys1[j] + m0 + rr] = v;
+            A.y[j][n * A.ys1[j] + m0 + rr] = ordered_sum(A.part + n * A.prow + rt * 16 + rr, NC * A.prow, A.nchunks);
         }
     }
 }
@@ -1951,8 +1974,8 @@ __global__ __launch_bounds__(64 * RW * KW) __attribute__((amdgpu_waves_per_eu(4,
         f.init(A.w[j], M, A.nb, g0, (int) min<int64_t>(32, M - g0), (int) (m - g0), h);
     }
     Raw buf[SPW];
-#pragma unroll
-    for (int s = 0; s < SPW; ++s) buf[s] = f.load(s < ns ? sb + s : (ns > 0 ? sb : 0));
+    // (step 0's weights before the x conversion, step 1's after it, as in k_mvb)
+    buf[0] = f.load(ns > 0 ? sb : 0);
     __builtin_amdgcn_sched_barrier(0);
 
     XSeg * xs = reinterpret_cast<XSeg *>(lds);                                  // [NC][SEGS]
@@ -1967,6 +1990,10 @@ __global__ __launch_bounds__(64 * RW * KW) __attribute__((amdgpu_waves_per_eu(4,
         // (tasks past the last column convert zeros into a segment index past SEGS: not stored)
         sp |= convert_seg(xe[p], task < TASKS ? g : SEGS, SEGS, task & 3, xs + n * SEGS, xf + n * SEGS);
     }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 1; s < SPW; ++s) buf[s] = f.load(s < ns ? sb + s : (ns > 0 ? sb : 0));
+    __builtin_amdgcn_sched_barrier(0);
     const bool special = __syncthreads_or(sp); // (also: x and zpad are in LDS for every wave)
 
     // the lane's A operand: row i = 4 blk + k (plane k < 3), k-half h
@@ -2061,10 +2088,7 @@ __global__ __launch_bounds__(64 * RW * KW) __attribute__((amdgpu_waves_per_eu(4,
     for (int t = tid; t < NC * R; t += T) {
         const int n = t / R, rr = t % R;
         if (m0 + rr < M) {
-            float v = 0.0f;
-            for (int64_t cc = 0; cc < A.nchunks; ++cc)
-                v += __hip_atomic_load(A.part + (cc * NC + n) * A.prow + rt * R + rr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            A.y[j][n * A.ys1[j] + m0 + rr] = v;
+            A.y[j][n * A.ys1[j] + m0 + rr] = ordered_sum(A.part + n * A.prow + rt * R + rr, NC * A.prow, A.nchunks);
         }
     }
     if (tid == 0) __hip_atomic_store(A.arrive + rt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
