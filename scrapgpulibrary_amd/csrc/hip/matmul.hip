@@ -1021,14 +1021,16 @@ struct XDma {
 // 3 groups (128-row tiles), groups 1 and 2 handing their sums to group 0, which adds them in group
 // order and stores. The 64-token forms also take the 64-token kernel's tile shapes wherever K is a
 // whole number of stages, and GA runs the grouped MUL_MAT_ID (gathered x rows, scattered
-// outputs). Measured (quantized N(0, 0.02)
+// outputs). WV = 8 (KG = 1): 256-row tiles in 8-wave work-groups, one per CU (its LDS request
+// keeps a second one off the CU), for shapes whose 384-row tiles leave CUs idle. Measured (quantized N(0, 0.02)
 // weights): 12288 x 4096 at 2048 tokens 219 against 272 us, gate+up (24576 rows) at 512 tokens
 // 118 against 145 us, 12288 x 4096 at 512 tokens (KG = 2) 70-76 against 79-82 us. Wave tiles of 64
 // rows x 64 tokens (half the LDS reads per MFMA, twice the dequantization) measured slower than
 // the 64-token form. Split-K over work-groups (partials + k_split_reduce) as in k_matmul.
-template <int DT, int KG, int NF = 4, bool SK = false, bool GA = false>
-__global__ __launch_bounds__(768, 1) void k_gemm_w(MmArgs L) {
-    constexpr int W = 12, BN = 32 * NF, RW = W / KG, BMT = 32 * RW;
+template <int DT, int KG, int NF = 4, bool SK = false, bool GA = false, int WV = 12>
+__global__ __launch_bounds__(64 * WV, 1) void k_gemm_w(MmArgs L) {
+    constexpr int W = WV, BN = 32 * NF, RW = W / KG, BMT = 32 * RW;
+    static_assert(W % KG == 0, "whole row waves per K group");
     static_assert(!SK || KG == 1, "stream-K runs 12 row waves");
     static_assert(!GA || (KG == 1 && !SK && NF == 2), "grouped MUL_MAT_ID: 384-row x 64-token tiles, no split");
     using F = PFmt<DT>;
@@ -1717,9 +1719,9 @@ int env_int(const char * name, int dflt) {
 struct MmConfig {
     int bn, rg;
     int split;
-    int w;  // waves per work-group: 4, or 12 (one work-group per CU, see k_matmul)
+    int w;  // waves per work-group: 4, or 12 (one work-group per CU, see k_matmul), or 8 (the wide GEMM's 256-row tiles)
     int kg; // K groups of a 12-wave work-group: 1 or 3
-    bool wide = false; // k_gemm_w (w = 12): 128-token wave tiles (kg 1 or 2, bn = 128), or 64-token ones (kg = 1, bn = 64)
+    bool wide = false; // k_gemm_w (w = 12): 128-token wave tiles (kg 1 or 2, bn = 128), or 64-token ones (kg = 1, bn = 64); w = 8: 256-row x 128-token tiles
     bool sk = false;   // the wide form's stream-K (kg = 1, bn = 128): cu_count work-groups share all tiles' stages
     bool narrow = false; // k_gemm_n: 9..128 tokens, rw R32 groups per work-group, kw waves along K each
     int kw = 8;
@@ -1864,6 +1866,24 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
                 c.kg = 2;
                 return c;
             }
+            // 8-wave work-groups of 256-row x 128-token tiles, one per CU, with K split over sp of
+            // them, where that fills the CUs in one round (at least 15/16 of them) with >= 16
+            // stages per split: fewer waves per CU than the 12-wave forms, but every CU at work
+            // (4096x12288 at 512 tokens: 64 tiles x 4 splits, 75.6 against 85.3 us per op for 44
+            // 384-row tiles x 4 splits; Q6_K 78.2 against 87.5, Q8_0 4096x11008 77.1 against 86.4;
+            // at 2048 tokens 256 tiles unsplit, 232-237 against 257-262 for stream-K; at 1024
+            // tokens 128 x 2, 128.6 against 140.3)
+            static const int env_w8 = env_int("SCRAPGPU_HIP_MM_W8", 1);
+            if (env_w8 != 0 && env_kg != 2 && slices == 1 && (a.M % 256 == 0 || a.M >= 8 * 256)) {
+                const int64_t t8 = (a.M + 255) / 256 * ntw;
+                for (int sp = 1; sp <= 8; ++sp)
+                    if (t8 * sp <= cu_count && 16 * t8 * sp >= 15 * (int64_t) cu_count && stages / sp >= 16) {
+                        c.w = 8;
+                        c.kg = 1;
+                        c.split = sp;
+                        return c;
+                    }
+            }
             static const int env_ws = env_int("SCRAPGPU_HIP_MM_WSPLIT", 0);
             if (env_ws > 1) {
                 c.kg = env_kg == 2 ? 2 : 1;
@@ -1973,6 +1993,7 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
 template <int DT>
 void * kernel_of(const MmConfig & c) {
     if (c.sk) return (void *) k_gemm_w<DT, 1, 4, true>;
+    if (c.wide && c.w == 8) return (void *) k_gemm_w<DT, 1, 4, false, false, 8>;
     if (c.wide) return c.bn == 64 ? (c.kg == 3 ? (void *) k_gemm_w<DT, 3, 2> : c.kg == 2 ? (void *) k_gemm_w<DT, 2, 2> : (void *) k_gemm_w<DT, 1, 2>) : c.kg == 2 ? (void *) k_gemm_w<DT, 2> : (void *) k_gemm_w<DT, 1>;
     if (c.w == 12) return c.kg == 3 ? (void *) k_matmul<DT, 64, 1, 12, 3> : c.kg == 2 ? (void *) k_matmul<DT, 64, 1, 12, 2> : (void *) k_matmul<DT, 64, 1, 12, 1>;
     if (c.rg == 1) return c.bn == 64 ? (void *) k_matmul<DT, 64, 1, 4, 1> : (void *) k_matmul<DT, 128, 1, 4, 1>;
@@ -2203,8 +2224,9 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     L.stages = (a.K + BK - 1) / BK;
     L.split = cfg.split;
     // (the wide GEMM with 2 K groups hands half of its sums over through the x buffers at the end)
-    const size_t lds = cfg.wide ? std::max((size_t) cfg.kg * 2 * BN * XR * sizeof(uint16_t), (size_t) (cfg.kg > 1 ? 12 * 2 * 16 * 64 : 0) * sizeof(float))
-                                : (size_t) cfg.kg * 2 * BN * BK * sizeof(uint16_t);
+    size_t lds = cfg.wide ? std::max((size_t) cfg.kg * 2 * BN * XR * sizeof(uint16_t), (size_t) (cfg.kg > 1 ? 12 * 2 * 16 * 64 : 0) * sizeof(float))
+                          : (size_t) cfg.kg * 2 * BN * BK * sizeof(uint16_t);
+    if (cfg.wide && cfg.w == 8) lds = std::max(lds, (size_t) 81920); // (the 8-wave form: one work-group per CU)
     const int64_t slices = a.ne12 * a.ne13;
     L.sk_g = cfg.sk ? cu_count : 0;
     if (cfg.sk && L.tiles_m * L.tiles_n > sk_max_tiles(a)) return hipErrorInvalidValue; // (more slots than the scratch holds)

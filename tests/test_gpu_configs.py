@@ -175,9 +175,9 @@ def test_config4_q4_k_prefill(hip, K, M, N):
     (y,), (form, grid) = run(hip, [wt], x)
     assert form.startswith("gemm"), form
     if M == 4096 and N == 2048 and hip[0].info().compute_units == 256:
-        assert form.startswith("gemm wide stream-k"), form  # (176 tiles, 66 stages per CU)
+        assert form.startswith("gemm wide w=8 kg=1 bn=128 rg=1 split=1"), form  # (256 256-row tiles, one per CU)
     if M == 4096 and N == 512 and hip[0].info().compute_units == 256:
-        assert form.startswith("gemm wide w=12 kg=1 bn=128 rg=1 split=4"), form  # (44 tiles x 4 splits of K)
+        assert form.startswith("gemm wide w=8 kg=1 bn=128 rg=1 split=4"), form  # (64 256-row tiles x 4 splits of K)
     check(sg.Q4_K, q, K, M, x, y, f"Q4_K {M}x{K} N={N} [{form}]")
 
 

@@ -578,6 +578,25 @@ def _sk_run(dev, st, dtype, K, Ms, N, seed):
     return ys, refs, form, grid
 
 
+@pytest.mark.parametrize("dtype,K,Ms,N,split", [(sg.Q4_K, 2048, (3000,), 2504, 1), (sg.Q6_K, 8192, (4096,), 500, 4),
+                                              (sg.Q8_0, 4096, (2048, 2048), 1000, 2), (sg.Q4_0, 2048, (1000, 1000, 1048), 2500, 1)],
+                         ids=["q4_k_row_and_token_tails", "q6_k_k_split", "q8_0_multi_packed", "q4_0_multi_per_weight_tiles"])
+def test_prefill_wide_256_row_tiles(hip, dtype, K, Ms, N, split):
+    """The wide GEMM's 8-wave form: 256-row x 128-token tiles, one work-group per CU, K split over
+    `split` work-groups where that fills the CUs in one round (15/16 of them or more). A part-empty
+    last row tile and token tile, K split with the partials added by the split reduce, a
+    MUL_MAT_MULTI packed end to end and one whose weights own their row tiles; two launches
+    bit-identical, every output within the prefill NMSE of the oracle."""
+    dev, st = hip
+    ys, refs, form, grid = _sk_run(dev, st, dtype, K, Ms, N, 990 + N)
+    if dev.info().compute_units == 256:
+        assert form.startswith(f"gemm wide w=8 kg=1 bn=128 rg=1 split={split}"), form
+    for M, a, b, ref in zip(Ms, ys[0], ys[1], refs):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{M} rows: launches differ"
+        e = nmse(a, ref)
+        assert e <= 5e-5, f"{sg.NAMES[dtype]} {M}x{K} N={N}: NMSE {e:.3e} [{form}]"
+
+
 @pytest.mark.parametrize("dtype,K,Ms,pad", [(sg.Q6_K, 12288, (3102,), 60), (sg.Q8_0, 8192, (3840,), 100),
                                             (sg.Q4_K, 8192, (1000, 1000, 1072), 100), (sg.Q4_0, 8192, (1024, 1024, 1024), 0)],
                          ids=["q6_k_row_tail_scalar_y", "q8_0_token_tail", "q4_k_multi_per_weight_tiles", "q4_0_multi_packed"])
