@@ -2131,7 +2131,7 @@ void * pick_mvc(int nc, bool pre) {
 
 template <int DT, int RG>
 void * pick_burst_rg(int W, int spw) {
-    if (spw <= 2) return W >= 16 ? (void *) k_mvb<DT, RG, 16, 2> : W >= 8 ? (void *) k_mvb<DT, RG, 8, 2> : (void *) k_mvb<DT, RG, 4, 2>;
+    if (spw <= 2) return W >= 16 ? (void *) k_mvb<DT, RG, 16, 2> : W >= 8 ? (void *) k_mvb<DT, RG, 8, 2> : W >= 4 ? (void *) k_mvb<DT, RG, 4, 2> : (void *) k_mvb<DT, RG, 2, 2>;
     if constexpr (RG == 1) {
         if (spw == 3) return (void *) k_mvb<DT, 1, 16, 3>; // (W = 16 only; 16-row tiles only)
     }
@@ -2363,7 +2363,10 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         if (nst > 32) rg = 1; // (also over the override)
         // 3 steps per wave for 33..48 steps (16 waves: no wave loads a step it does not use)
         const int sp = nst <= 32 ? 2 : nst <= 48 && rg == 1 && tuning("SCRAPGPU_HIP_MV_SPW3", 1) ? 3 : 4;
-        int W = 4;
+        // (K of 4 steps or fewer: 2 waves, so that none is left without a step: the MoE experts'
+        // Q6_K down projection, K = 768, as 1024 2-wave work-groups: a 4-layer MoE token
+        // 53.7-55.2 -> 49.5-50.2 us)
+        int W = nst <= 2 * sp ? 2 : 4;
         while (W < 16 && (nst + W - 1) / W > sp) W *= 2;
         set_tiles(L, mats, nmat, 16 * rg);
         L.cs = sp;
