@@ -1760,13 +1760,29 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
         // (65..128 tokens: two work-groups of 64 per R32 group where the groups are fewer than the
         // CUs: 4096x4096 22.4 against 32.2 us, 6144x4096 28.1 against 34.7, 4096x12288 38.9 against
         // 41.4; 12288x4096 lost, 41.1 against 36.0)
-        if ((a.N <= 64 ? groups <= 2 * (int64_t) cu_count : groups < cu_count) || env_rw > 0) {
+        // 33..128 tokens where 3 R32 groups per work-group, the tokens in two halves (two
+        // work-groups per triple of groups, gridDim.x apart), fill the CUs in one round (15/16 of
+        // them or more): 12 waves, 4 along K per group. 12288x4096 at 64 tokens 26.0 -> 23.5 us
+        // against 2 groups per work-group (192 work-groups), Q6_K 28.1 -> 26.2, at 48 tokens 25.5 ->
+        // 23.7; at 128 tokens 35.1 against 35.7-36.0 for the wide GEMM's 64-token tiles
+        const int64_t t3 = (groups + 2) / 3 * 2;
+        const bool fill3 = a.N > 32 && t3 <= cu_count && 16 * t3 >= 15 * (int64_t) cu_count;
+        if ((a.N <= 64 ? groups <= 2 * (int64_t) cu_count : groups < cu_count) || (env_rw == 0 && fill3) || env_rw > 0) {
             c.narrow = true;
             c.kg = c.rg = c.split = 1;
             c.bn = a.N <= 32 ? 32 : a.N <= 64 ? 64 : 128;
-            c.rw = env_rw == 1 || env_rw == 2 || env_rw == 4 ? env_rw : groups < cu_count ? 1 : 2;
+            c.rw = env_rw == 1 || env_rw == 2 || env_rw == 3 || env_rw == 4 ? env_rw : fill3 ? 3 : groups < cu_count ? 1 : 2;
             c.nz = c.rw == 1 && c.bn == 64 && (env_nz == 2 || (env_nz == 0 && groups < cu_count)) ? 2 : 1;
             if (c.bn == 128) c.nz = env_nz == 4 && c.rw == 1 ? 4 : 2;
+            if (c.rw == 3) {
+                if (c.bn == 32) c.rw = 2; // (not built: 32 tokens would leave a third of the work-groups)
+                else {
+                    c.nz = 2;
+                    c.kw = 4;
+                    c.w = 12;
+                    return c;
+                }
+            }
             if (c.rw == 1) {
                 c.kw = env_kw == 8 || env_kw == 16 ? env_kw : groups * c.nz >= cu_count ? 8 : 16;
                 if (c.kw == 16 && c.bn / c.nz == 64) c.kw = 8; // (64 tokens in 16 waves: more registers than 1024 threads allow)
@@ -2064,10 +2080,12 @@ template <int DT>
 static void * narrow_kernel(int nf, int kw, int rw) {
     if (nf == 1) {
         if (rw == 4) return (void *) k_gemm_n<DT, 1, 4, 4>;
+        if (rw == 3) return (void *) k_gemm_n<DT, 1, 4, 3>;
         if (rw == 2) return (void *) k_gemm_n<DT, 1, 8, 2>;
         return kw == 16 ? (void *) k_gemm_n<DT, 1, 16> : (void *) k_gemm_n<DT, 1, 8>;
     }
     if (rw == 2) return (void *) k_gemm_n<DT, 2, 4, 2>;
+    if (rw == 3) return (void *) k_gemm_n<DT, 2, 4, 3>;
     return (void *) k_gemm_n<DT, 2, 8>; // (2 fragments in 16 waves would spill: not built)
 }
 

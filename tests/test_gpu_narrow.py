@@ -19,9 +19,11 @@ QT = (sg.Q4_0, sg.Q8_0, sg.Q4_K, sg.Q6_K)
 # (16 waves, or 64 tokens as two work-groups); 12288 and 8990 rows are 1-2 groups per CU (two
 # groups per work-group; 8990 rows: an odd group count, the last work-group's second wave idle);
 # K = 256 is 2 stages for 8-16 waves; K = 384 an odd stage count; 100 and 128 tokens run as two
-# work-groups of 64 per group
+# work-groups of 64 per group; 12288 / 12256 / 12224 rows at 33..128 tokens: 3 groups per
+# work-group with the tokens in two halves (the last triple 1 or 2 groups short at 12256 / 12224)
 SHAPES = [(4096, 1000, 9), (2048, 333, 17), (1536, 64, 32), (4096, 100, 33), (256, 40, 64), (12288, 96, 64),
-          (4096, 12288, 64), (2048, 8990, 30), (384, 200, 48), (2048, 1000, 100), (1024, 64, 128)]
+          (4096, 12288, 64), (2048, 8990, 30), (384, 200, 48), (2048, 1000, 100), (1024, 64, 128),
+          (4096, 12256, 100), (2048, 12224, 40)]
 
 
 def cases():
@@ -114,6 +116,37 @@ def test_narrow_multi(hip, dt):
     st.sync()
     form = sg.last_launch()[0]
     assert form.startswith("gemm narrow"), form
+    for M, yt, ref in zip(Ms, yts, refs):
+        check(st.download(yt).reshape(N, M), ref, f"{O.NAMES[dt]} {M} rows of {Ms} N={N} [{form}]")
+    for b in bufs:
+        b.free()
+
+
+@pytest.mark.parametrize("dt", QT, ids=lambda d: O.NAMES[d])
+def test_narrow_multi_three_groups(hip, dt):
+    """MUL_MAT_MULTI on the 3-groups-per-work-group form: 4096 + 4064 + 4128 rows (384 R32 groups
+    together, triples straddling the weights) at 64 tokens."""
+    dev, st = hip
+    K, N, Ms = 1024, 64, (4096, 4064, 4128)
+    x = O.normal(N * K, 15).reshape(N, K)
+    xb = dev.alloc(x.nbytes)
+    xt = sg.tdesc(sg.F32, (K, N), xb)
+    st.write(xb, 0, x)
+    bufs, wts, yts, refs = [xb], [], [], []
+    for j, M in enumerate(Ms):
+        q, _ = quantized(dt, K, M, 160 + j)
+        wb, wt = upload_weights(dev, st, dt, q, K, M)
+        yb = dev.alloc(4 * M * N)
+        bufs += [wb, yb]
+        wts.append(wt)
+        yts.append(sg.tdesc(sg.F32, (M, N), yb))
+        refs.append(O.mul_mat(dt, q, K, M, x, threads=8))
+    op, keep = sg.multi_op(wts, xt, yts)
+    st.execute(op)
+    st.sync()
+    form = sg.last_launch()[0]
+    if dev.info().compute_units == 256:
+        assert form.startswith("gemm narrow rw=3"), form
     for M, yt, ref in zip(Ms, yts, refs):
         check(st.download(yt).reshape(N, M), ref, f"{O.NAMES[dt]} {M} rows of {Ms} N={N} [{form}]")
     for b in bufs:
