@@ -832,12 +832,6 @@ __device__ void exact_segments(const MvArgs & A, const Where & wh, const Row & r
     }
 }
 
-// Burst form (one column, <= SPW steps per wave, one tile of 16 * RG rows per work-group): the wave
-// first loads its x range, then issues every weight load, and only then converts x.
-// CHUNK (one slice, W x SPW = kChunkSteps): work-group (tile, c) takes chunk c of K,
-// so that a long K runs on several small work-groups instead of one large one per tile. The
-// chunks' partial sums meet as in k_mvc: agent-scope stores, an arrival count per tile, and the
-// last chunk to arrive adds them in chunk order and resets the count.
 // The sum over c = 0 .. n - 1 of p[c stride], added in order of c (the chunk hand-overs below):
 // agent-scope loads (coherent across XCDs by themselves), issued in batches of 8 before any is
 // added, so the last chunk pays one memory round trip per 8 chunks instead of one per chunk.
@@ -854,6 +848,13 @@ __device__ __forceinline__ float ordered_sum(const float * p, int64_t stride, in
     return t;
 }
 
+// Burst form (one column, <= SPW steps per wave, one tile of 16 * RG rows per work-group): the wave
+// first loads its x range, then issues its first step's weight loads, converts x, and then issues
+// the loads of its other steps.
+// CHUNK (one slice, W x SPW = kChunkSteps): work-group (tile, c) takes chunk c of K,
+// so that a long K runs on several small work-groups instead of one large one per tile. The
+// chunks' partial sums meet as in k_mvc: agent-scope stores, an arrival count per tile, and the
+// last chunk to arrive adds them in chunk order and resets the count.
 template <int DT, int RG, int W, int SPW, bool CHUNK = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2 && RG == 1 ? 6 : SPW <= 2 && RG == 2 ? 5 : 4, 8))) void k_mvb(MvArgs A) {
     static_assert(!CHUNK || W * SPW == kChunkSteps, "chunks of kChunkSteps steps");
