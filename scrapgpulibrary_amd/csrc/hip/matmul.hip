@@ -1480,11 +1480,11 @@ __global__ __launch_bounds__(256) void k_split_reduce(MmArgs L) {
 
 // stream-K: y = the sum of a tile's partial slots in work-group order, for the tiles that more
 // than one work-group shared (k_gemm_w<.., SK>). blockIdx.x is the tile, blockIdx.y covers 1024
-// of its 128 x 384 sums (4 consecutive rows of one token per thread); VEC when every matrix's rows
+// of its BN x 384 sums (4 consecutive rows of one token per thread); VEC when every matrix's rows
 // and y's rows allow float4 stores. One slice.
-template <bool VEC>
+template <bool VEC, int BN = 128>
 __global__ __launch_bounds__(256) void k_sk_reduce(MmArgs L) {
-    constexpr int BN = 128, BMT = 384, TE = BN * BMT;
+    constexpr int BMT = 384, TE = BN * BMT;
     const int64_t S = L.stages / 2, U = L.tiles_m * L.tiles_n * S, G = L.sk_g, t = blockIdx.x; // (units of 2 stages)
     // the work-groups g with g U / G <= t S < (g + 1) U / G, and with (t + 1) S - 1 in their range
     const int64_t ga = ((t * S + 1) * G + U - 1) / U - 1, gb = ((t + 1) * S * G + U - 1) / U - 1;
@@ -1947,6 +1947,15 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
             c.kg = 1;
             c.bn = 64;
             c.wide = true;
+            // a second round of tiles at most a quarter full (and >= 16 stages per CU): stream-K
+            // over the CUs instead, each an equal run of 2-stage units, the shared tiles added by k_sk_reduce (100000x4096 Q4_K
+            // at 64 tokens, 261 tiles: 95.2-96.0 against 109.9-110.1 us; the Q6_K LM head's 396
+            // tiles, a second round 55% full, lost: 155 against 140-145)
+            const int64_t tw = (a.M + 383) / 384 * ((a.N + 63) / 64);
+            static const int env_sk64 = env_int("SCRAPGPU_HIP_MM_SK64", 1);
+            if (env_sk64 != 0 && !lean && slices == 1 && stages % 2 == 0 && tw > cu_count && tw < 2 * (int64_t) cu_count &&
+                4 * (tw - cu_count) <= cu_count && tw * stages >= 16 * (int64_t) cu_count)
+                c.sk = true;
             return c;
         }
         if (env_w == 12) { // forced: KG = 1, split from SCRAPGPU_HIP_MM_SPLIT (the wide GEMM's form where K allows)
@@ -2008,7 +2017,7 @@ MmConfig config_of(const MatArgs & a, int cu_count, bool lean) {
 
 template <int DT>
 void * kernel_of(const MmConfig & c) {
-    if (c.sk) return (void *) k_gemm_w<DT, 1, 4, true>;
+    if (c.sk) return c.bn == 64 ? (void *) k_gemm_w<DT, 1, 2, true> : (void *) k_gemm_w<DT, 1, 4, true>;
     if (c.wide && c.w == 8) return (void *) k_gemm_w<DT, 1, 4, false, false, 8>;
     if (c.wide) return c.bn == 64 ? (c.kg == 3 ? (void *) k_gemm_w<DT, 3, 2> : c.kg == 2 ? (void *) k_gemm_w<DT, 2, 2> : (void *) k_gemm_w<DT, 1, 2>) : c.kg == 2 ? (void *) k_gemm_w<DT, 2> : (void *) k_gemm_w<DT, 1>;
     if (c.w == 12) return c.kg == 3 ? (void *) k_matmul<DT, 64, 1, 12, 3> : c.kg == 2 ? (void *) k_matmul<DT, 64, 1, 12, 2> : (void *) k_matmul<DT, 64, 1, 12, 1>;
@@ -2064,14 +2073,14 @@ static hipError_t allow_lds(void * fn, size_t lds) {
     return hipSuccess;
 }
 
-// stream-K partial slots: one per piece, at most cu_count + tiles - 1, each 128 x 384 floats. The
+// stream-K partial slots: one per piece, at most cu_count + tiles - 1, each bn x 384 floats. The
 // row tiles of 2..3 weights tiled one by one are at most 2 more than those of all their rows
-static int64_t sk_max_tiles(const MatArgs & a) {
-    return ((a.M + 383) / 384 + 2) * ((a.N + 127) / 128);
+static int64_t sk_max_tiles(const MatArgs & a, int bn) {
+    return ((a.M + 383) / 384 + 2) * ((a.N + bn - 1) / bn);
 }
 
-static size_t sk_part_bytes(const MatArgs & a, int cu_count) {
-    return (size_t) (cu_count + sk_max_tiles(a) - 1) * 128 * 384 * sizeof(float);
+static size_t sk_part_bytes(const MatArgs & a, int cu_count, int bn) {
+    return (size_t) (cu_count + sk_max_tiles(a, bn) - 1) * bn * 384 * sizeof(float);
 }
 
 static bool float_gemm(const MatArgs & a);
@@ -2130,7 +2139,7 @@ size_t matmul_scratch_bytes(const MatArgs & a, int cu_count, bool lean) {
     // (float weights off the GEMM run the float matvec, which takes no scratch)
     if (is_float_weight(a.dtype) && !float_gemm(a)) return 0;
     const MmConfig c = config_of(a, cu_count, lean);
-    if (c.sk) return part_offset(a) + sk_part_bytes(a, cu_count);
+    if (c.sk) return part_offset(a) + sk_part_bytes(a, cu_count, c.bn);
     return part_offset(a) + (c.split == 1 ? 0 : part_bytes(a, c.split));
 }
 
@@ -2247,7 +2256,7 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     if (cfg.wide && cfg.w == 8) lds = std::max(lds, (size_t) 81920); // (the 8-wave form: one work-group per CU)
     const int64_t slices = a.ne12 * a.ne13;
     L.sk_g = cfg.sk ? cu_count : 0;
-    if (cfg.sk && L.tiles_m * L.tiles_n > sk_max_tiles(a)) return hipErrorInvalidValue; // (more slots than the scratch holds)
+    if (cfg.sk && L.tiles_m * L.tiles_n > sk_max_tiles(a, cfg.bn)) return hipErrorInvalidValue; // (more slots than the scratch holds)
     const dim3 grid(cfg.sk ? (unsigned) cu_count : (unsigned) (L.tiles_m * L.tiles_n * L.split), (unsigned) slices);
     void * args[] = {&L};
     void * fn = nullptr;
@@ -2262,7 +2271,7 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     }
     if ((e = allow_lds(fn, lds)) != hipSuccess) return e;
     if (cfg.sk)
-        std::snprintf(last_form().form, sizeof(last_form().form), "gemm wide stream-k w=12 kg=1 bn=128 rg=1 wgs=%d", cu_count);
+        std::snprintf(last_form().form, sizeof(last_form().form), "gemm wide stream-k w=12 kg=1 bn=%d rg=1 wgs=%d", BN, cu_count);
     else
         std::snprintf(last_form().form, sizeof(last_form().form), "gemm%s w=%d kg=%d bn=%d rg=%d split=%d", cfg.wide ? " wide" : "", cfg.w, cfg.kg, BN,
                       cfg.rg, L.split);
@@ -2272,11 +2281,18 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     bool yvec = a.y_s2 % 4 == 0 && a.y_s3 % 4 == 0;
     for (int j = 0; j < nmat; ++j) yvec = yvec && (reinterpret_cast<uintptr_t>(mats[j].y) & 15) == 0 && mats[j].M % 4 == 0 && mats[j].y_s1 % 4 == 0;
     if (cfg.sk) {
-        const dim3 rg((unsigned) (L.tiles_m * L.tiles_n), (unsigned) (128 * 384 / 1024));
-        if (yvec)
-            hipLaunchKernelGGL(k_sk_reduce<true>, rg, dim3(256), 0, stream, L);
-        else
-            hipLaunchKernelGGL(k_sk_reduce<false>, rg, dim3(256), 0, stream, L);
+        const dim3 rg((unsigned) (L.tiles_m * L.tiles_n), (unsigned) (BN * 384 / 1024));
+        if (BN == 64) {
+            if (yvec)
+                hipLaunchKernelGGL((k_sk_reduce<true, 64>), rg, dim3(256), 0, stream, L);
+            else
+                hipLaunchKernelGGL((k_sk_reduce<false, 64>), rg, dim3(256), 0, stream, L);
+        } else {
+            if (yvec)
+                hipLaunchKernelGGL(k_sk_reduce<true>, rg, dim3(256), 0, stream, L);
+            else
+                hipLaunchKernelGGL(k_sk_reduce<false>, rg, dim3(256), 0, stream, L);
+        }
         return hipGetLastError();
     }
     const dim3 rg((unsigned) rows, (unsigned) ((a.M + 1023) / 1024));

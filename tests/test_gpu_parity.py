@@ -597,6 +597,23 @@ def test_prefill_wide_256_row_tiles(hip, dtype, K, Ms, N, split):
         assert e <= 5e-5, f"{sg.NAMES[dtype]} {M}x{K} N={N}: NMSE {e:.3e} [{form}]"
 
 
+@pytest.mark.parametrize("dtype,K,Ms,N", [(sg.Q4_0, 2048, (98688,), 33), (sg.Q6_K, 2048, (49000, 49688), 64)],
+                         ids=["q4_0_257_tiles", "q6_k_multi_per_weight_tiles"])
+def test_prefill_wide_stream_k_64_tokens(hip, dtype, K, Ms, N):
+    """Stream-K on the wide GEMM's 64-token tiles: 257-258 tiles of 384 rows (a second round of
+    tiles at most a quarter full), so the CUs share all tiles' 2-stage units instead and the tiles
+    cut between CUs are added from their partial slots by the reduce pass; a part-empty token tile
+    and a MUL_MAT_MULTI whose weights own their row tiles; two launches bit-identical."""
+    dev, st = hip
+    ys, refs, form, grid = _sk_run(dev, st, dtype, K, Ms, N, 1200 + N)
+    if dev.info().compute_units == 256:
+        assert form.startswith("gemm wide stream-k w=12 kg=1 bn=64"), form
+    for M, a, b, ref in zip(Ms, ys[0], ys[1], refs):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{M} rows: launches differ"
+        e = nmse(a, ref)
+        assert e <= 5e-5, f"{sg.NAMES[dtype]} {M}x{K} N={N}: NMSE {e:.3e} [{form}]"
+
+
 @pytest.mark.parametrize("dtype,K,Ms,pad", [(sg.Q6_K, 12288, (3102,), 60), (sg.Q8_0, 8192, (3840,), 100),
                                             (sg.Q4_K, 8192, (1000, 1000, 1072), 100), (sg.Q4_0, 8192, (1024, 1024, 1024), 0)],
                          ids=["q6_k_row_tail_scalar_y", "q8_0_token_tail", "q4_k_multi_per_weight_tiles", "q4_0_multi_packed"])
