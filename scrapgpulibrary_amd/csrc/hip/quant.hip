@@ -454,13 +454,94 @@ struct GetRowsArgs {
     float * y;
     int64_t y_s1, y_s2, y_s3; // element strides of dst
     int64_t K, M, nb, n0, n1; // n0, n1: ids ne0, ne1 (rows = n0 * n1 * ne2)
-    Areas ar;
 };
 
 // the row's natural bytes are staged in LDS, kGetRowsBlocks blocks at a time: each R32 unit of the
 // row (16 bytes at ((b U + u) rs + lane) 16 of its area, or a 2-byte half at (b rs + lane) 2) is
-// one load; then every element is dequantized from LDS with the dequantizer's formula
+// one load, all of a pass issued before any is used; then every element is dequantized from LDS
+// with the dequantizer's formula
 constexpr int kGetRowsBlocks = 64;
+
+// one pass of GET_ROWS over blocks b0 .. b0 + nblk - 1 of one row: the slice, M nb (the bytes
+// per block of an area multiply it to give the area's start), g0 nb, rows in the group, the row's
+// place in it
+struct GrPass {
+    const uint8_t * slice;
+    uint64_t mnb, g0nb, rs, lane;
+    int64_t b0;
+    int nblk;
+};
+
+// area K of format DT's R32 layout (areas_of, as compile-time constants): at byte BEFORE x M nb
+// of the slice, LEN bytes per block, at natural offset SRC, stored xor XR; K past the format's
+// areas does nothing. load() fetches the thread's units of the pass into registers (16-byte
+// units: at most kGetRowsBlocks x 12 / 256 = 3 per thread; 2-byte halves: one), scatter() puts
+// their bytes at their natural places in LDS.
+template <int DT, int K>
+struct GrArea {
+    static constexpr int NA = DT == Q6_K ? 3 : 2;
+    static constexpr int SRC = K == 0 ? (DT == Q6_K ? 0 : DT == Q4_K ? 16 : 2) : K == 1 ? (DT == Q6_K ? 192 : 0) : 208;
+    static constexpr int LEN = K == 0 ? (DT == Q6_K ? 192 : DT == Q4_K ? 128 : DT == Q8_0 ? 32 : 16) : K == 1 ? (DT == Q6_K || DT == Q4_K ? 16 : 2) : 2;
+    static constexpr int BEFORE = K == 0 ? 0 : K == 1 ? (DT == Q6_K ? 192 : DT == Q4_K ? 128 : DT == Q8_0 ? 32 : 16) : 208;
+    static constexpr uint32_t XR = (K == 0 && DT == Q8_0) || (K == 1 && DT == Q6_K) ? 0x80u : 0u;
+    static constexpr int U = LEN / 16, NU = U > 0 ? (kGetRowsBlocks * U + 255) / 256 : 1;
+    uint4 v[NU];
+    uint32_t hv;
+    __device__ void load(const GrPass & p) {
+        if constexpr (K < NA) {
+            const uint8_t * area = p.slice + p.mnb * BEFORE;
+            if constexpr (LEN == 2) {
+                const int t = threadIdx.x;
+                hv = t < p.nblk ? (uint32_t) *reinterpret_cast<const uint16_t *>(area + p.g0nb * 2 + ((uint64_t) (p.b0 + t) * p.rs + p.lane) * 2) : 0u;
+            } else {
+#pragma unroll
+                for (int i = 0; i < NU; ++i) {
+                    const int t = threadIdx.x + 256 * i, bl = t / U, u = t - bl * U;
+                    if (t < p.nblk * U) v[i] = *reinterpret_cast<const uint4 *>(area + p.g0nb * LEN + (((uint64_t) (p.b0 + bl) * U + u) * p.rs + p.lane) * 16);
+                }
+            }
+        }
+    }
+    __device__ void scatter(const GrPass & p, uint8_t * nat, int bb) const {
+        if constexpr (K < NA) {
+            if constexpr (LEN == 2) {
+                const int t = threadIdx.x;
+                if (t < p.nblk) {
+                    nat[t * bb + SRC] = (uint8_t) (hv & 0xFFu);
+                    nat[t * bb + SRC + 1] = (uint8_t) (hv >> 8);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < NU; ++i) {
+                    const int t = threadIdx.x + 256 * i, bl = t / U, u = t - bl * U;
+                    if (t < p.nblk * U) {
+                        const uint32_t m = XR * 0x01010101u;
+                        const uint32_t w[4] = {v[i].x ^ m, v[i].y ^ m, v[i].z ^ m, v[i].w ^ m};
+                        uint8_t * d = nat + bl * bb + SRC + 16 * u; // natural offsets are not 4-aligned in general
+                        for (int q = 0; q < 16; ++q) d[q] = (uint8_t) (w[q >> 2] >> (8 * (q & 3)));
+                    }
+                }
+            }
+        }
+    }
+};
+
+// the kernel's compile-time areas against areas_of() (the layout the weights were packed in)
+template <int DT>
+bool gr_areas_match() {
+    const Areas ar = areas_of(DT);
+    const int src[3] = {GrArea<DT, 0>::SRC, GrArea<DT, 1>::SRC, GrArea<DT, 2>::SRC};
+    const int len[3] = {GrArea<DT, 0>::LEN, GrArea<DT, 1>::LEN, GrArea<DT, 2>::LEN};
+    const uint32_t xr[3] = {GrArea<DT, 0>::XR, GrArea<DT, 1>::XR, GrArea<DT, 2>::XR};
+    if (ar.na != GrArea<DT, 0>::NA) return false;
+    int before = 0;
+    for (int k = 0; k < ar.na; ++k) {
+        const int bk = k == 0 ? GrArea<DT, 0>::BEFORE : k == 1 ? GrArea<DT, 1>::BEFORE : GrArea<DT, 2>::BEFORE;
+        if (ar.src[k] != src[k] || ar.len[k] != len[k] || ar.xr[k] != xr[k] || bk != before) return false;
+        before += ar.len[k];
+    }
+    return true;
+}
 
 template <int DT>
 __global__ __launch_bounds__(256) void k_get_rows(GetRowsArgs a) {
@@ -477,31 +558,18 @@ __global__ __launch_bounds__(256) void k_get_rows(GetRowsArgs a) {
     float * y = a.y + ai * a.y_s1 + bi * a.y_s2 + c * a.y_s3;
     for (int64_t b0 = 0; b0 < a.nb; b0 += kGetRowsBlocks) {
         const int nblk = (int) min<int64_t>(kGetRowsBlocks, a.nb - b0);
-        uint64_t before = 0;
-        for (int k = 0; k < a.ar.na; ++k) {
-            const int src = a.ar.src[k], len = a.ar.len[k];
-            const uint8_t xr = a.ar.xr[k];
-            const uint8_t * area = slice + (uint64_t) a.M * (uint64_t) a.nb * before;
-            if (len == 2) {
-                for (int t = threadIdx.x; t < nblk; t += blockDim.x) {
-                    const uint8_t * p = area + (uint64_t) g0 * a.nb * 2 + ((uint64_t) (b0 + t) * rs + lane) * 2;
-                    nat[t * BB + src] = p[0];
-                    nat[t * BB + src + 1] = p[1];
-                }
-            } else {
-                const int U = len / 16;
-                for (int t = threadIdx.x; t < nblk * U; t += blockDim.x) {
-                    const int bl = t / U, u = t - bl * U;
-                    const uint4 v = *reinterpret_cast<const uint4 *>(area + (uint64_t) g0 * a.nb * len +
-                                                                        (((uint64_t) (b0 + bl) * U + u) * rs + lane) * 16);
-                    const uint32_t m = xr * 0x01010101u;
-                    const uint32_t w[4] = {v.x ^ m, v.y ^ m, v.z ^ m, v.w ^ m};
-                    uint8_t * d = nat + bl * BB + src + 16 * u; // natural offsets are not 4-aligned in general
-                    for (int q = 0; q < 16; ++q) d[q] = (uint8_t) (w[q >> 2] >> (8 * (q & 3)));
-                }
-            }
-            before += (uint64_t) len;
-        }
+        const GrPass p{slice, (uint64_t) a.M * (uint64_t) a.nb, (uint64_t) g0 * a.nb, (uint64_t) rs, (uint64_t) lane, b0, nblk};
+        // every load of the pass issued before the first is scattered into LDS: one memory round
+        // trip per pass, not one per area
+        GrArea<DT, 0> a0;
+        GrArea<DT, 1> a1;
+        GrArea<DT, 2> a2;
+        a0.load(p);
+        a1.load(p);
+        a2.load(p);
+        a0.scatter(p, nat, BB);
+        a1.scatter(p, nat, BB);
+        a2.scatter(p, nat, BB);
         __syncthreads();
         for (int e = threadIdx.x; e < nblk * BS; e += blockDim.x) y[b0 * BS + e] = deq_elem<DT>(nat + (e / BS) * BB, e % BS);
         __syncthreads();
@@ -586,13 +654,13 @@ hipError_t launch_get_rows(const GetRowsLaunch & g, hipStream_t stream) {
     const dim3 grid((unsigned) rows), block(256);
     if (g.dtype == F32 || g.dtype == F16) {
         a.nb = 0;
-        a.ar = Areas{};
         if (g.dtype == F32) hipLaunchKernelGGL(k_get_rows_float<F32>, grid, block, 0, stream, a, g.w_s1);
         else hipLaunchKernelGGL(k_get_rows_float<F16>, grid, block, 0, stream, a, g.w_s1);
         return hipGetLastError();
     }
     a.nb = g.K / block_elems(g.dtype);
-    a.ar = areas_of(g.dtype);
+    static const bool areas_ok = gr_areas_match<Q4_0>() && gr_areas_match<Q8_0>() && gr_areas_match<Q4_K>() && gr_areas_match<Q6_K>();
+    if (!areas_ok) return hipErrorInvalidValue;
     switch (g.dtype) {
         case Q4_0: hipLaunchKernelGGL(k_get_rows<Q4_0>, grid, block, 0, stream, a); break;
         case Q8_0: hipLaunchKernelGGL(k_get_rows<Q8_0>, grid, block, 0, stream, a); break;
