@@ -54,7 +54,8 @@ SCRAPGPU_API scrapgpu_status scrapgpu_hip_profile_read(size_t index, const char 
  * that the library holds until the process ends, instead of the stream's scratch, which
  * scrapgpu_op_execute grows with hipMalloc; it calls no hipMalloc or hipFree, and the event
  * profiler stays off during the call. One exception to "the same kernels": a prefill shape that
- * scrapgpu_op_execute runs in the stream-K form (fewer 384-row tiles than CUs and a long K) runs
+ * scrapgpu_op_execute runs in a stream-K form (its 384-row tiles fewer than the CUs, or a second
+ * round of them at most a quarter full, and a long K) runs
  * another GEMM form here, whose output differs in rounding (both within the prefill tolerance),
  * because stream-K's partial slots do not fit the static array. An op that needs more than 32 MiB
  * of scratch is refused with SCRAPGPU_STATUS_UNSUPPORTED and a reason (decode matvecs need at most
