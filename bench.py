@@ -254,7 +254,7 @@ def bench_prefill(dev, st, n_tokens, reps):
     return out
 
 
-MOE_E, MOE_USED, MOE_HIDDEN, MOE_FFN, MOE_LAYERS = 128, 8, 2048, 768, 4
+MOE_E, MOE_USED, MOE_HIDDEN, MOE_FFN, MOE_LAYERS = 128, 8, 2048, 768, 48
 
 
 def hip_events_ms(st, fn, reps):
@@ -285,8 +285,10 @@ def hip_events_ms(st, fn, reps):
 def bench_moe(dev, st, tokens):
     """MUL_MAT_ID: a Qwen3-30B-A3B-shaped MoE decode token, bs = 1: per layer the gate and up experts
     (Q4_K, 2048 -> 768) and the down experts (Q6_K, 768 -> 2048) of 128, 8 selected, as three
-    MUL_MAT_ID ops sharing the layer's ids; MOE_LAYERS layers (1.56 GB of experts, past the 256 MB
-    MALL); fresh random ids every token (read on the device by the recorded plan)."""
+    MUL_MAT_ID ops sharing the layer's ids; MOE_LAYERS layers, the model's 48 (18.8 GB of experts,
+    far past the 256 MB MALL; one plan replay per token, so its fixed launch cost is spread over the
+    token's 96 launches as in the model); fresh random ids every token (read on the device by the
+    recorded plan)."""
     rng = np.random.default_rng(17)
     bufs = []
     tmp = dev.alloc(4 * MOE_HIDDEN * MOE_FFN * MOE_E)

@@ -618,6 +618,26 @@ __device__ __forceinline__ Where where_of(const MvArgs & A) {
     return w;
 }
 
+// where_of for the burst form's MUL_MAT_ID instances (ids present) in two halves, so that the
+// pair's expert id is not a round trip ahead of its x loads: where_first() needs no memory read and issues the id load (a vector
+// load from one address: its wait counts in order, so the x loads issued after it stay in flight),
+// where_second() turns the id into the weight offset once the x loads are out.
+__device__ __forceinline__ Where where_first(const MvArgs & A, int32_t & eid) {
+    Where w;
+    const uint32_t pr = blockIdx.y, nu = (uint32_t) A.n_used;
+    const uint32_t t = pr / nu, i = pr - t * nu;
+    eid = __hip_atomic_load(A.ids + (int64_t) i * A.ids_s0 + (int64_t) t * A.ids_s1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    w.w_off = 0;
+    w.x = A.x + (A.x_shared ? 0 : (int64_t) i * A.x_s1) + (int64_t) t * A.x_s2;
+    w.y_off = (int64_t) i * A.ys1[0] + (int64_t) t * A.y_s2;
+    return w;
+}
+__device__ __forceinline__ void where_second(const MvArgs & A, int32_t eid, Where & w) {
+    int32_t e = __builtin_amdgcn_readfirstlane(eid);
+    e = e < 0 ? 0 : (e >= (int32_t) A.n_exp ? (int32_t) A.n_exp - 1 : e);
+    w.w_off = (uint64_t) e * A.w_s2;
+}
+
 // the lane's rows of a tile of 16 * RG rows: f[i] serves row m0 + r + 16 i (dead lanes of a
 // partial last tile read a real row and drop the result)
 struct Row {
@@ -855,14 +875,16 @@ __device__ __forceinline__ float ordered_sum(const float * p, int64_t stride, in
 // so that a long K runs on several small work-groups instead of one large one per tile. The
 // chunks' partial sums meet as in k_mvc: agent-scope stores, an arrival count per tile, and the
 // last chunk to arrive adds them in chunk order and resets the count.
-template <int DT, int RG, int W, int SPW, bool CHUNK = false>
+template <int DT, int RG, int W, int SPW, bool CHUNK = false, bool ID = false>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2 && RG == 1 ? 6 : SPW <= 2 && RG == 2 ? 5 : 4, 8))) void k_mvb(MvArgs A) {
     static_assert(!CHUNK || W * SPW == kChunkSteps, "chunks of kChunkSteps steps");
+    static_assert(!(CHUNK && ID), "MUL_MAT_ID pairs take whole K");
     using F = Fmt<DT>;
     using Raw = typename F::Raw;
     extern __shared__ uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const Where wh = CHUNK ? Where{0, 0, A.x} : where_of(A);
+    int32_t eid = 0;
+    Where wh = CHUNK ? Where{0, 0, A.x} : ID ? where_first(A, eid) : where_of(A);
 
     // the work-group's steps: all of K, or chunk blockIdx.y (CHUNK)
     const int64_t cb = CHUNK ? (int64_t) blockIdx.y * kChunkSteps : 0;
@@ -891,6 +913,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPW <= 2
 
     // the x loads stay ahead of the weight loads
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (ID) where_second(A, eid, wh);
     F f[RG];
     const Row row = row_of<DT, RG>(A, blockIdx.x, wh.w_off, lane & 15, lane >> 4, f);
     Raw buf[SPW][RG];
@@ -2144,6 +2167,19 @@ void * pick_burst(int W, int spw, int rg) {
     return rg == 3 ? pick_burst_rg<DT, 3>(W, spw) : rg == 2 ? pick_burst_rg<DT, 2>(W, spw) : pick_burst_rg<DT, 1>(W, spw);
 }
 
+// MUL_MAT_ID pairs with K of up to 32 steps: the instances that issue the expert id's load with
+// the x loads (others read it through where_of, one round trip ahead of them)
+template <int DT, int RG>
+void * pick_burst_id_rg(int W) {
+    return W >= 16 ? (void *) k_mvb<DT, RG, 16, 2, false, true> : W >= 8 ? (void *) k_mvb<DT, RG, 8, 2, false, true>
+         : W >= 4 ? (void *) k_mvb<DT, RG, 4, 2, false, true> : (void *) k_mvb<DT, RG, 2, 2, false, true>;
+}
+
+template <int DT>
+void * pick_burst_id(int W, int rg) {
+    return rg == 3 ? pick_burst_id_rg<DT, 3>(W) : rg == 2 ? pick_burst_id_rg<DT, 2>(W) : pick_burst_id_rg<DT, 1>(W);
+}
+
 // streaming variants: W = 8 for one column, 4 for several
 template <int DT>
 void * pick_stream(int nc) {
@@ -2372,8 +2408,12 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         set_tiles(L, mats, nmat, 16 * rg);
         L.cs = sp;
         const size_t lds = (size_t) W * sp * kSegs * (sizeof(XSeg) + sizeof(float4)) + (size_t) W * 16 * rg * sizeof(float) + 16;
+        static const bool id_early = tuning("SCRAPGPU_HIP_MV_ID_EARLY", 1) != 0;
         void * fn = dt == Q4_0 ? pick_burst<Q4_0>(W, sp, rg) : dt == Q8_0 ? pick_burst<Q8_0>(W, sp, rg)
                   : dt == Q4_K ? pick_burst<Q4_K>(W, sp, rg) : pick_burst<Q6_K>(W, sp, rg);
+        if (L.ids != nullptr && sp == 2 && id_early)
+            fn = dt == Q4_0 ? pick_burst_id<Q4_0>(W, rg) : dt == Q8_0 ? pick_burst_id<Q8_0>(W, rg)
+               : dt == Q4_K ? pick_burst_id<Q4_K>(W, rg) : pick_burst_id<Q6_K>(W, rg);
         if (grid_size) *grid_size = (uint64_t) L.tiles * (uint64_t) slices;
         std::snprintf(last_form().form, sizeof(last_form().form), "burst rg=%d W=%d spw=%d", rg, W, sp);
         last_form().grid = (uint64_t) L.tiles * (uint64_t) slices;
