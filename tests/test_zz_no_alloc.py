@@ -78,6 +78,28 @@ def test_static_scratch_wide_64_token_forms(hip):
     wb.free()
 
 
+def test_static_scratch_256_row_tiles(hip):
+    """The wide GEMM's 8-wave form (256-row x 128-token tiles, one work-group per CU) through the
+    static scratch: 4096x4096 at 2048 tokens (256 tiles, K whole), then 64 tokens (the narrow
+    GEMM), each bit for bit equal to scrapgpu_op_execute's output."""
+    dev, st = hip
+    K, M = 4096, 4096
+    q, _ = quantized(sg.Q4_K, K, M, 1525)
+    wb, wt = upload_weights(dev, st, sg.Q4_K, q, K, M)
+    for N in (2048, 64):
+        x = O.normal(N * K, 1526 + N).reshape(N, K)
+        y_static = _run(dev, st, wt, x, M, True)
+        form = sg.last_launch()[0]
+        if dev.info().compute_units == 256:
+            assert form.startswith("gemm wide w=8 kg=1 bn=128 rg=1 split=1" if N == 2048 else "gemm narrow"), form
+        y_plain = _run(dev, st, wt, x, M, False)
+        assert np.array_equal(y_static.view(np.uint32), y_plain.view(np.uint32)), f"N={N} [{form}]: outputs differ"
+        ref = O.mul_mat(sg.Q4_K, q, K, M, x, threads=8)
+        e = float(np.sum((y_static.astype(np.float64) - ref) ** 2) / np.sum(ref.astype(np.float64) ** 2))
+        assert e <= 5e-5, f"N={N}: NMSE {e:.3e}"
+    wb.free()
+
+
 def test_static_scratch_stream_k_shape(hip):
     """12288x5632 at 768 tokens: scrapgpu_op_execute runs it in the stream-K form (192 384-row
     tiles, fewer than the CUs, 44 stages each); the static entry point runs another GEMM form (the
