@@ -39,8 +39,7 @@ import scrapgpulibrary_amd as sg  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the dominant kernel, measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-# profiling run (the FETCH_SIZE and WRITE_SIZE commands are recorded in the file itself)
-# profiling run, see DESIGN.md
+# profiling runs (their commands are recorded in the file itself)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_matvec_decode_token.json")
 F16_PEAK_TFLOPS = 2500.0
 
