@@ -2253,7 +2253,9 @@ hipError_t launch_matmul_mfma(const MatArgs * mats, int nmat, uint8_t * scratch,
     // (the wide GEMM with 2 K groups hands half of its sums over through the x buffers at the end)
     size_t lds = cfg.wide ? std::max((size_t) cfg.kg * 2 * BN * XR * sizeof(uint16_t), (size_t) (cfg.kg > 1 ? 12 * 2 * 16 * 64 : 0) * sizeof(float))
                           : (size_t) cfg.kg * 2 * BN * BK * sizeof(uint16_t);
-    if (cfg.wide && cfg.w == 8) lds = std::max(lds, (size_t) 81920); // (the 8-wave form: one work-group per CU)
+    // (the 8-wave form: one work-group per CU, which more than half of the CU's 160 KiB of LDS
+    // ensures; its ~150 VGPRs per lane would also leave room for only one)
+    if (cfg.wide && cfg.w == 8) lds = std::max(lds, (size_t) 96 * 1024);
     const int64_t slices = a.ne12 * a.ne13;
     L.sk_g = cfg.sk ? cu_count : 0;
     if (cfg.sk && L.tiles_m * L.tiles_n > sk_max_tiles(a, cfg.bn)) return hipErrorInvalidValue; // (more slots than the scratch holds)
