@@ -1547,10 +1547,13 @@ __global__ __launch_bounds__(256) void k_sk_reduce(MmArgs L) {
 // chunk c (8 elements) of stage s of token n at ((n / 32 * stages + s) * 16 + c) * 32 + n % 32 in
 // units of 16 bytes (per slice, tokens padded to a multiple of 32): the 32 tokens of one chunk
 // are 512 contiguous bytes.
-template <bool VEC, bool Q4K, bool BF = false, bool FRAG = false>
-__global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, float * xs, uint16_t * xsum, int64_t xsum_row) {
+// (tid: the thread's index among the row's 256, wmax: 4 floats of LDS for the row's waves; a
+// thread group with live = false takes part in the barrier only)
+template <bool VEC, bool Q4K, bool BF, bool FRAG>
+__device__ __forceinline__ void x_row_to_f16(const MatArgs & a, uint16_t * xb, float * xs, uint16_t * xsum, int64_t xsum_row, int64_t row,
+                                             int tid, float * wmax, bool live) {
     constexpr int kCached = 6; // K <= 12288 is read once
-    const int64_t row = blockIdx.x, sl = row / a.N, n = row - sl * a.N;
+    const int64_t sl = row / a.N, n = row - sl * a.N;
     const int64_t i2 = sl % a.ne12, i3 = sl / a.ne12;
     const float * xp = a.x + i2 * a.x_s2 + i3 * a.x_s3 + n * a.x_s1;
     uint16_t * op = xb + row * a.K;
@@ -1578,7 +1581,7 @@ __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, floa
             // the 4 threads of a 32-element sub-block are lanes 4m .. 4m + 3 of one wave
             sum += __shfl_xor(sum, 1);
             sum += __shfl_xor(sum, 2);
-            if ((threadIdx.x & 3) == 0) {
+            if ((tid & 3) == 0 && live) {
                 const int64_t jb = k >> 5, jj = jb & 15;
                 const int64_t pos = (jb >> 4) * 16 + 8 * ((jj >> 1) & 1) + 2 * (jj >> 2) + (jj & 1);
                 xsum[row * xsum_row + pos] = __half_as_ushort(__float2half(sum * 0.03125f));
@@ -1588,6 +1591,7 @@ __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, floa
                 for (int e = 0; e < 8; ++e) s[e] *= 0.0625f;
             }
         }
+        if (!live) return;
         if constexpr (BF) { // (BF16 weights: x in bf16, rounded to nearest even)
             const bf16x2 p0 = __builtin_convertvector((f32x2{s[0], s[2]}), bf16x2), p1 = __builtin_convertvector((f32x2{s[1], s[3]}), bf16x2);
             const bf16x2 p2 = __builtin_convertvector((f32x2{s[4], s[6]}), bf16x2), p3 = __builtin_convertvector((f32x2{s[5], s[7]}), bf16x2);
@@ -1602,7 +1606,7 @@ __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, floa
                                                        __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3));
         }
     };
-    const int64_t k0 = (int64_t) threadIdx.x * 8; // K is a multiple of 32: a group of 8 is whole
+    const int64_t k0 = (int64_t) tid * 8; // K is a multiple of 32: a group of 8 is whole
     float cache[kCached][8];
     float mx = 0.0f;
 #pragma unroll
@@ -1622,8 +1626,7 @@ __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, floa
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    __shared__ float wmax[4];
-    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+    if ((tid & 63) == 0) wmax[tid >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
     int e2 = 0;
@@ -1632,7 +1635,7 @@ __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, floa
         frexpf(mx, &ex); // mx = f 2^ex, f in [0.5, 1)
         e2 = min(15 - ex, 120);
     }
-    if (threadIdx.x == 0) xs[row] = ldexpf(1.0f, -e2);
+    if (tid == 0 && live) xs[row] = ldexpf(1.0f, -e2);
 #pragma unroll
     for (int c = 0; c < kCached; ++c) {
         const int64_t k = k0 + (int64_t) c * 2048;
@@ -1644,36 +1647,49 @@ __global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, floa
         store8(k, v, e2);
     }
     if constexpr (Q4K) {
-        for (int64_t jb = a.K / 32 + threadIdx.x; jb < xsum_row; jb += 256) {
+        for (int64_t jb = a.K / 32 + tid; live && jb < xsum_row; jb += 256) {
             const int64_t jj = jb & 15;
             xsum[row * xsum_row + (jb >> 4) * 16 + 8 * ((jj >> 1) & 1) + 2 * (jj >> 2) + (jj & 1)] = 0;
         }
     }
 }
 
-// MUL_MAT_ID routing, one work-group of 1024 threads (E <= 1024 experts, P <= 65535 pairs): the
+template <bool VEC, bool Q4K, bool BF = false, bool FRAG = false>
+__global__ __launch_bounds__(256) void k_x_to_f16(MatArgs a, uint16_t * xb, float * xs, uint16_t * xsum, int64_t xsum_row) {
+    __shared__ float wmax[4];
+    x_row_to_f16<VEC, Q4K, BF, FRAG>(a, xb, xs, xsum, xsum_row, blockIdx.x, threadIdx.x, wmax, true);
+}
+
+// MUL_MAT_ID routing (E <= 1024 experts, P < 2^24 pairs), by one 1024-thread work-group: the
 // pairs p = t * n_used + slot grouped by expert (ids clamped to [0, E)); e_off[e] / t_start[e] =
-// the first pair / token tile (bn pairs) of expert e, [E] = the totals. The order of the pairs
-// inside an expert follows the LDS atomics; no output depends on it (each is one pair's own sum
-// over K). Each pair's expert is kept in LDS (dynamic, 2 bytes a pair) for the second pass.
-__global__ __launch_bounds__(1024) void k_moe_route(const int32_t * ids, int64_t s0, int64_t s1, int nu, int T, int E, int bn,
-                                                   int32_t * e_off, int32_t * t_start, int32_t * pairs) {
+// the first pair / token tile (bn pairs) of expert e, [E] = the totals. Counts with LDS atomics,
+// exclusive scans of the counts and of the tile counts (one expert per thread, wave scans), then
+// each pair placed at its expert's cursor (its id read again: it is in the L2 by then). The order
+// of the pairs inside an expert follows the LDS atomics; no output depends on it (each is one
+// pair's own sum over K).
+struct RouteArgs {
+    const int32_t * ids;
+    int64_t s0, s1;
+    int nu, T, E, bn;
+    int32_t * e_off;
+    int32_t * t_start;
+    int32_t * pairs;
+};
+
+__device__ __forceinline__ void moe_route(const RouteArgs & r) {
     __shared__ int32_t cnt[1024], cur[1024], wsum[2][16];
-    extern __shared__ uint16_t pe[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int P = r.nu * r.T;
+    auto expert = [&](int p) {
+        const int t = p / r.nu, slot = p - t * r.nu;
+        return min(max(r.ids[slot * r.s0 + t * r.s1], 0), r.E - 1);
+    };
     cnt[tid] = 0;
     __syncthreads();
-    const int P = nu * T;
-    for (int p = tid; p < P; p += 1024) {
-        const int t = p / nu, slot = p - t * nu;
-        const int e = min(max(ids[slot * s0 + t * s1], 0), E - 1);
-        pe[p] = (uint16_t) e;
-        atomicAdd(&cnt[e], 1);
-    }
+    for (int p = tid; p < P; p += 1024) atomicAdd(&cnt[expert(p)], 1);
     __syncthreads();
-    // exclusive scans of the counts and of the tile counts over the experts (one per thread)
-    const int c = tid < E ? cnt[tid] : 0;
-    const int tl = (c + bn - 1) / bn;
+    const int c = tid < r.E ? cnt[tid] : 0;
+    const int tl = (c + r.bn - 1) / r.bn;
     int a = c, b = tl;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -1688,23 +1704,39 @@ __global__ __launch_bounds__(1024) void k_moe_route(const int32_t * ids, int64_t
         wsum[1][wave] = b;
     }
     __syncthreads();
-    int pa = 0, pb = 0;
+    int ea = a - c, eb = b - tl; // exclusive prefixes
     for (int w2 = 0; w2 < wave; ++w2) {
-        pa += wsum[0][w2];
-        pb += wsum[1][w2];
+        ea += wsum[0][w2];
+        eb += wsum[1][w2];
     }
-    const int ea = pa + a - c, eb = pb + b - tl; // exclusive prefixes
-    if (tid < E) {
-        e_off[tid] = ea;
-        t_start[tid] = eb;
+    if (tid < r.E) {
+        r.e_off[tid] = ea;
+        r.t_start[tid] = eb;
         cur[tid] = ea;
     }
-    if (tid == E - 1) {
-        e_off[E] = ea + c;
-        t_start[E] = eb + tl;
+    if (tid == r.E - 1) {
+        r.e_off[r.E] = ea + c;
+        r.t_start[r.E] = eb + tl;
     }
     __syncthreads();
-    for (int p = tid; p < P; p += 1024) pairs[atomicAdd(&cur[pe[p]], 1)] = p;
+    for (int p = tid; p < P; p += 1024) r.pairs[atomicAdd(&cur[expert(p)], 1)] = p;
+}
+
+// the grouped MUL_MAT_ID's first launch: work-group 0 routes the pairs while the others convert
+// the x rows, 4 per work-group (k_x_to_f16's work, rows 4 (blockIdx.x - 1) + threadIdx.x / 256):
+// the routing's round trips run beside the conversion instead of in a launch of their own
+template <bool VEC, bool Q4K>
+__global__ __launch_bounds__(1024) void k_x_route(MatArgs a, uint16_t * xb, float * xs, uint16_t * xsum, int64_t xsum_row, int64_t rows,
+                                                  RouteArgs r) {
+    if (blockIdx.x == 0) {
+        moe_route(r);
+        return;
+    }
+    __shared__ float wmax[16];
+    const int q = threadIdx.x >> 8;
+    const int64_t row = 4 * ((int64_t) blockIdx.x - 1) + q;
+    const bool live = row < rows;
+    x_row_to_f16<VEC, Q4K, false, false>(a, xb, xs, xsum, xsum_row, live ? row : 0, threadIdx.x & 255, wmax + 4 * q, live);
 }
 
 int env_int(const char * name, int dflt) {
@@ -2358,37 +2390,31 @@ hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t 
     uint16_t * xsum = reinterpret_cast<uint16_t *>(scratch + xsum_offset(px));
     const int64_t xsum_row = xsum_row_of(px);
     const bool vec = (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && a.x_s1 % 4 == 0 && a.x_s2 % 4 == 0;
-    const dim3 xg((unsigned) rows);
     const int bn = ga_bn(id);
     const int waves = ga_waves(a, id, cu_count);
     // 384-row x 64-token tiles on the wide GEMM where K is a whole number of stages (x tiles
     // straight into LDS, the exact Q4_K form from plain x)
     static const int env_wide = env_int("SCRAPGPU_HIP_MM_WIDE", 1);
     const bool wide = env_wide != 0 && waves == 12 && bn == 64 && a.K % BK == 0;
-    if (a.dtype == Q4_K && !wide) {
-        if (vec)
-            hipLaunchKernelGGL((k_x_to_f16<true, true>), xg, dim3(256), 0, stream, px, xb, xs, xsum, xsum_row);
-        else
-            hipLaunchKernelGGL((k_x_to_f16<false, true>), xg, dim3(256), 0, stream, px, xb, xs, xsum, xsum_row);
-    } else {
-        if (vec)
-            hipLaunchKernelGGL((k_x_to_f16<true, false>), xg, dim3(256), 0, stream, px, xb, xs, xsum, xsum_row);
-        else
-            hipLaunchKernelGGL((k_x_to_f16<false, false>), xg, dim3(256), 0, stream, px, xb, xs, xsum, xsum_row);
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
     int32_t * e_off = reinterpret_cast<int32_t *>(scratch + part_offset(px));
     int32_t * t_start = e_off + id.n_exp + 1;
     int32_t * pairs = t_start + id.n_exp + 1;
-    const size_t route_lds = ((size_t) id.n_used * (size_t) id.n_tok * sizeof(uint16_t) + 15) / 16 * 16;
-    if (route_lds > 65536) { // the dynamic LDS beyond the 64 KiB default (16-bit experts of up to 65535 pairs)
-        static std::once_flag once;
-        std::call_once(once, [] { (void) hipFuncSetAttribute((const void *) k_moe_route, hipFuncAttributeMaxDynamicSharedMemorySize, 136 * 1024); });
+    const RouteArgs ra{id.ids, id.s0, id.s1, (int) id.n_used, (int) id.n_tok, (int) id.n_exp, bn, e_off, t_start, pairs};
+    // (work-group 0 routes the pairs, the others convert the x rows)
+    const dim3 xrg((unsigned) ((rows + 3) / 4 + 1));
+    if (a.dtype == Q4_K && !wide) {
+        if (vec)
+            hipLaunchKernelGGL((k_x_route<true, true>), xrg, dim3(1024), 0, stream, px, xb, xs, xsum, xsum_row, rows, ra);
+        else
+            hipLaunchKernelGGL((k_x_route<false, true>), xrg, dim3(1024), 0, stream, px, xb, xs, xsum, xsum_row, rows, ra);
+    } else {
+        if (vec)
+            hipLaunchKernelGGL((k_x_route<true, false>), xrg, dim3(1024), 0, stream, px, xb, xs, xsum, xsum_row, rows, ra);
+        else
+            hipLaunchKernelGGL((k_x_route<false, false>), xrg, dim3(1024), 0, stream, px, xb, xs, xsum, xsum_row, rows, ra);
     }
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), route_lds, stream, id.ids, id.s0, id.s1, (int) id.n_used, (int) id.n_tok, (int) id.n_exp, bn,
-                       e_off, t_start, pairs);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
     MmArgs L;
     std::memset(&L, 0, sizeof(L));
     L.a = a;
