@@ -387,6 +387,62 @@ def bench_moe_prefill(dev, st, n_tokens, reps):
             "experts_read": used, "weight_GBps": round(used * weight_bytes(sg.Q4_K, K, M) / (ms * 1e-3) / 1e9, 1)}
 
 
+def bench_moe_prefill_layer(dev, st, n_tokens, reps, order=("gate", "up", "down")):
+    """MUL_MAT_ID at prefill size over a whole MoE layer's experts: a plan of the Qwen3-30B-A3B
+    gate and up (Q4_K 2048->768, the same x and ids: one x pre-pass and routing for both) and down
+    (Q6_K 768->2048, x per slot) of 128 experts, 8 used, over n_tokens tokens with random distinct
+    ids per token; time per replay of the plan (a HIP graph)."""
+    E, U = MOE_E, MOE_USED
+    specs = {"gate": (sg.Q4_K, MOE_HIDDEN, MOE_FFN), "up": (sg.Q4_K, MOE_HIDDEN, MOE_FFN), "down": (sg.Q6_K, MOE_FFN, MOE_HIDDEN)}
+    bufs, keep, nodes = [], [], []
+    tmp = dev.alloc(4 * MOE_HIDDEN * MOE_FFN * E)
+    bufs.append(tmp)
+    bufs += [dev.alloc(4 * MOE_HIDDEN * n_tokens), dev.alloc(4 * MOE_FFN * U * n_tokens)]
+    xh = sg.tdesc(sg.F32, (MOE_HIDDEN, 1, n_tokens), bufs[-2])
+    xf = sg.tdesc(sg.F32, (MOE_FFN, U, n_tokens), bufs[-1])
+    st.fill_normal(xh, seed=41)
+    st.fill_normal(xf, seed=42)
+    rng = np.random.default_rng(43)
+    ids = np.stack([rng.permutation(E)[:U] for _ in range(n_tokens)]).astype(np.int32)
+    bufs.append(dev.alloc(ids.nbytes))
+    it = sg.tdesc(sg.I32, (U, n_tokens), bufs[-1])
+    st.upload(it, ids)
+    flops = 0.0
+    for i, name in enumerate(order):
+        dt, K, M = specs[name]
+        b = dev.alloc(weight_bytes(dt, K, M) * E)
+        bufs.append(b)
+        f = sg.tdesc(sg.F32, (K, M * E), tmp)
+        st.fill_normal(f, seed=300 + i, std=0.02)
+        st.quantize(f, sg.tdesc(dt, (K, M * E), b, layout=sg.R32))
+        bufs.append(dev.alloc(4 * M * U * n_tokens))
+        y = sg.tdesc(sg.F32, (M, U, n_tokens), bufs[-1])
+        op, k = sg.mul_mat_id_op(sg.tdesc(dt, (K, M, E), b, layout=sg.R32), xf if name == "down" else xh, it, y, U)
+        keep.append((op, k))
+        nodes.append(sg.PlanNode(C.sizeof(sg.PlanNode), op, 0))
+        flops += 2.0 * M * K * U * n_tokens
+    arr = (sg.PlanNode * len(nodes))(*nodes)
+    pdesc = sg.PlanDesc(C.sizeof(sg.PlanDesc), arr, len(nodes))
+    plan = C.c_void_p()
+    sg.check(sg.lib().scrapgpu_plan_build(dev.handle, C.byref(pdesc), C.byref(plan)), "plan_build")
+
+    def layer():
+        sg.check(sg.lib().scrapgpu_plan_execute(st.handle, plan), "plan_execute")
+
+    try:
+        layer()
+        st.sync()
+        ms = hip_events_ms(st, lambda: [layer() for _ in range(reps)], 3) / reps
+    finally:
+        sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
+        st.sync()
+        for b in bufs:
+            b.free()
+    return {"workload": f"Qwen3-30B-A3B MoE layer experts (gate, up Q4_K {MOE_HIDDEN}->{MOE_FFN}; down Q6_K {MOE_FFN}->{MOE_HIDDEN}) x {E}, "
+                        f"{U} used, {n_tokens} tokens, MUL_MAT_ID plan (device-grouped MFMA)",
+            "us": round(ms * 1e3, 2), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+
+
 def bench_get_rows(dev, st, n_rows, reps):
     """GET_ROWS: n_rows random rows of a Q6_K 151936 x 4096 table (the Qwen3 LM head / embedding
     shape, 510 MB, R32) dequantized to f32."""
@@ -694,6 +750,7 @@ def main():
     layer_pf = None if args.no_prefill else bench_layer_prefill(dev, st, model, 512, 5)
     moe = None if args.no_moe else bench_moe(dev, st, 20)
     moe_pf = None if args.no_moe else bench_moe_prefill(dev, st, 512, 10)
+    moe_pf_layer = None if args.no_moe else bench_moe_prefill_layer(dev, st, 512, 10)
     get_rows = None if args.no_get_rows else bench_get_rows(dev, st, 512, 5)
     cpu = None if args.no_cpu else cpu_baseline(dev, st, model, args.cpu_seconds)
     configs = None if args.no_configs else bench_configs(dev, st, 0.0 if args.no_cpu else args.config_cpu_seconds)
@@ -725,6 +782,7 @@ def main():
         "prefill_peak_frac": None if prefill is None else round(max(v["tflops"] for v in prefill.values()) / F16_PEAK_TFLOPS, 4),
         "moe_decode_mul_mat_id": moe,
         "moe_prefill_mul_mat_id": moe_pf,
+        "moe_prefill_layer_mul_mat_id": moe_pf_layer,
         "get_rows": get_rows,
         "cpu_baseline": cpu,
         "configs": configs,

@@ -1028,8 +1028,9 @@ bool outputs_apart(const PlanNode * group, int n, const PlanNode & b) {
 
 // consecutive MUL_MAT_ID nodes of a plan that may share one launch: the same x and ids, experts
 // of one dtype, K, count and stride, outputs of one layout apart from every tensor of the group
-// (outputs_apart), and the decode path (the grouped path runs one op per launch)
-bool id_fusable(const PlanNode * group, int n, const PlanNode & b) {
+// (outputs_apart), all on the decode path; or, all on the grouped path, one x pre-pass and
+// routing (mul_mat_id_same_x), after which each node runs its GEMM
+bool id_fusable(const PlanNode * group, int n, const PlanNode & b, int cu_count) {
     const PlanNode & a = group[0];
     if (a.op.op != SCRAPGPU_OP_MUL_MAT_ID || b.op.op != SCRAPGPU_OP_MUL_MAT_ID) return false;
     sgk::MatArgs ma, mb;
@@ -1038,8 +1039,15 @@ bool id_fusable(const PlanNode * group, int n, const PlanNode & b) {
         mul_mat_id_rule(b.op.inputs[0], b.op.inputs[1], b.op.inputs[2], b.op.outputs[0], &mb, &ib, nullptr) != SCRAPGPU_STATUS_OK) {
         return false;
     }
-    if (mul_mat_id_grouped(ma, ia) || mul_mat_id_grouped(mb, ib)) return false;
     if (!same_tensor(a.op.inputs[1], b.op.inputs[1]) || !same_tensor(a.op.inputs[2], b.op.inputs[2])) return false;
+    const bool ga = mul_mat_id_grouped(ma, ia), gb = mul_mat_id_grouped(mb, ib);
+    if (ga != gb) return false;
+    if (ga) {
+        // (x and ids are the same tensors: compare the x forms on the same pointers)
+        ma.x = mb.x = nullptr;
+        if (ma.dtype != mb.dtype || ia.n_exp != ib.n_exp || ia.n_used != ib.n_used || !sgk::mul_mat_id_same_x(ma, mb, ia, cu_count)) return false;
+        return outputs_apart(group, n, b);
+    }
     if (ma.dtype != mb.dtype || ma.K != mb.K || ma.w_s2 != mb.w_s2 || ia.n_exp != ib.n_exp || ia.n_used != ib.n_used) return false;
     if (ma.y_s1 != mb.y_s1 || ma.y_s2 != mb.y_s2) return false;
     return outputs_apart(group, n, b);
@@ -1098,6 +1106,22 @@ scrapgpu_status exec_node(Stream * s, const PlanNode * nodes) {
         const double pairs = (double) (idk.n_used * idk.n_tok);
         bytes += weight_bytes(mats[k]) * pairs;
         flops += 2.0 * (double) mats[k].M * (double) mats[k].K * pairs;
+    }
+    if (mul_mat_id_grouped(mats[0], id)) {
+        // one x pre-pass and routing (with the first node's GEMM), then each further node's GEMM
+        // on the same scratch
+        size_t need = 0;
+        for (int k = 0; k < n; ++k) need = std::max(need, sgk::mul_mat_id_scratch_bytes(mats[k], id));
+        uint8_t * scr = nullptr;
+        const scrapgpu_status st = scratch_for(s, need, &scr);
+        if (st != SCRAPGPU_STATUS_OK) return st;
+        for (int k = 0; k < n; ++k) {
+            ProfScope prof(s->s);
+            const char * name = nullptr;
+            SG_HIP(sgk::launch_mul_mat_id_mfma(mats[k], id, scr, (int) s->dev->cus, s->s, &name, k > 0), "grouped MUL_MAT_ID launch");
+            prof.done(name, weight_bytes(mats[k]) * (double) id.n_exp, 2.0 * (double) mats[k].M * (double) mats[k].K * (double) (id.n_used * id.n_tok));
+        }
+        return SCRAPGPU_STATUS_OK;
     }
     ProfScope prof(s->s);
     const char * name = nullptr;
@@ -1168,7 +1192,7 @@ scrapgpu_status api_plan_build(scrapgpu_device_t * device, const scrapgpu_plan_d
     for (size_t i = 0; i < p->nodes.size();) {
         int f = 0;
         while (f < 2 && i + f + 1 < p->nodes.size() &&
-               (id_fusable(&p->nodes[i], f + 1, p->nodes[i + f + 1]) || mm_fusable(&p->nodes[i], f + 1, p->nodes[i + f + 1]))) {
+               (id_fusable(&p->nodes[i], f + 1, p->nodes[i + f + 1], (int) d->cus) || mm_fusable(&p->nodes[i], f + 1, p->nodes[i + f + 1]))) {
             ++f;
         }
         p->nodes[i].fuse = f;

@@ -106,9 +106,15 @@ bool matmul_reads_same_x(const MatArgs & a, const MatArgs & b);
 // runs over (expert, 32- or 64-pair tile, 128- or 384-row tile) with gathered x rows and scattered
 // outputs; each expert's weights are read once per row tile instead of once per pair. `scratch`:
 // mul_mat_id_scratch_bytes(a, id) bytes (a as mul_mat_id_rule fills it; a.N = 1).
+// x_ready: the scratch already holds this x's pre-pass output and these ids' routing (the
+// previous launch on it was a grouped MUL_MAT_ID for which mul_mat_id_same_x(prev, a, id) held),
+// so only the GEMM is launched.
 size_t mul_mat_id_scratch_bytes(const MatArgs & a, const IdArgs & id);
 hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t * scratch, int cu_count, hipStream_t stream,
-                                  const char ** kernel_name);
+                                  const char ** kernel_name, bool x_ready = false);
+// true when grouped MUL_MAT_IDs a and b over the same x and ids (one IdArgs) write the same
+// pre-pass output and routing: the same x form and token tile, so b may run with x_ready after a
+bool mul_mat_id_same_x(const MatArgs & a, const MatArgs & b, const IdArgs & id, int cu_count);
 
 // GET_ROWS on R32 weights: dst[:, a, b, c] = dequantized row ids[a, b, c] of slice (b, c) of src0
 // (bit-exact with the dequantizer; out-of-range indices read the nearest row).

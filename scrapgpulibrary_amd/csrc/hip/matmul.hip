@@ -2381,7 +2381,19 @@ size_t mul_mat_id_scratch_bytes(const MatArgs & a, const IdArgs & id) {
     return part_offset(px) + (size_t) (2 * (id.n_exp + 1) + id.n_used * id.n_tok) * sizeof(int32_t);
 }
 
-hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name) {
+// the grouped path's x form: the wide GEMM (plain f16 x) or k_matmul (its single-fma Q4_K form)
+static bool ga_wide(const MatArgs & a, const IdArgs & id, int cu_count) {
+    static const int env_wide = env_int("SCRAPGPU_HIP_MM_WIDE", 1);
+    return env_wide != 0 && ga_waves(a, id, cu_count) == 12 && ga_bn(id) == 64 && a.K % BK == 0;
+}
+
+bool mul_mat_id_same_x(const MatArgs & a, const MatArgs & b, const IdArgs & id, int cu_count) {
+    const bool qa = a.dtype == Q4_K && !ga_wide(a, id, cu_count), qb = b.dtype == Q4_K && !ga_wide(b, id, cu_count);
+    return a.x == b.x && a.K == b.K && a.x_s1 == b.x_s1 && a.x_s2 == b.x_s2 && qa == qb;
+}
+
+hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t * scratch, int cu_count, hipStream_t stream, const char ** kernel_name,
+                                  bool x_ready) {
     const MatArgs px = ga_xargs(a, id);
     const int64_t rows = px.N * id.n_tok;
     if (id.n_exp < 1 || id.n_exp > 1024 || rows * a.K >= ((int64_t) 1 << 31) || id.n_used * id.n_tok >= ((int64_t) 1 << 24)) return hipErrorInvalidValue;
@@ -2394,15 +2406,16 @@ hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t 
     const int waves = ga_waves(a, id, cu_count);
     // 384-row x 64-token tiles on the wide GEMM where K is a whole number of stages (x tiles
     // straight into LDS, the exact Q4_K form from plain x)
-    static const int env_wide = env_int("SCRAPGPU_HIP_MM_WIDE", 1);
-    const bool wide = env_wide != 0 && waves == 12 && bn == 64 && a.K % BK == 0;
+    const bool wide = ga_wide(a, id, cu_count);
     int32_t * e_off = reinterpret_cast<int32_t *>(scratch + part_offset(px));
     int32_t * t_start = e_off + id.n_exp + 1;
     int32_t * pairs = t_start + id.n_exp + 1;
     const RouteArgs ra{id.ids, id.s0, id.s1, (int) id.n_used, (int) id.n_tok, (int) id.n_exp, bn, e_off, t_start, pairs};
     // (work-group 0 routes the pairs, the others convert the x rows)
     const dim3 xrg((unsigned) ((rows + 3) / 4 + 1));
-    if (a.dtype == Q4_K && !wide) {
+    if (x_ready) {
+        // x converted and the pairs routed by the previous grouped MUL_MAT_ID (mul_mat_id_same_x)
+    } else if (a.dtype == Q4_K && !wide) {
         if (vec)
             hipLaunchKernelGGL((k_x_route<true, true>), xrg, dim3(1024), 0, stream, px, xb, xs, xsum, xsum_row, rows, ra);
         else
@@ -2450,7 +2463,7 @@ hipError_t launch_mul_mat_id_mfma(const MatArgs & a, const IdArgs & id, uint8_t 
     const int64_t grid = L.tiles_m * L.tiles_n;
     if (grid >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
     if ((e = allow_lds(fn, lds)) != hipSuccess) return e;
-    std::snprintf(last_form().form, sizeof(last_form().form), "grouped%s w=%d bn=%d", wide ? " wide" : "", waves, bn);
+    std::snprintf(last_form().form, sizeof(last_form().form), "grouped%s w=%d bn=%d%s", wide ? " wide" : "", waves, bn, x_ready ? " shared-x" : "");
     last_form().grid = (uint64_t) grid;
     void * args[] = {&L};
     return hipLaunchKernel(fn, dim3((unsigned) grid), dim3((unsigned) (64 * waves)), args, lds, stream);

@@ -316,3 +316,66 @@ def test_mul_mat_id_plan_fuses_gate_up(hip):
         sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
     for b in bufs + list(ybs.values()) + [xhb, xfb, ib]:
         b.free()
+
+
+@pytest.mark.parametrize("form", ["tiled", "wide"])
+def test_mul_mat_id_grouped_plan_shares_routing(hip, form):
+    """A plan of a MoE layer at prefill size: down (its own x), then gate and up (the same x and
+    ids): up runs its GEMM on gate's x pre-pass and routing (the form says shared-x). On graph
+    replays with new ids, each output bit for bit equal to the op run alone and within the
+    prefill tolerance of the oracle. tiled: 4-wave 32-pair tiles with the Q4_K single-fma x form;
+    wide: the wide GEMM's 384-row x 64-pair tiles."""
+    dev, st = hip
+    if form == "tiled":
+        E, nu, T, H, F = 16, 4, 40, 512, 256
+    else:
+        E, nu, T, H, F = 64, 8, 128, 512, 512
+    rng = np.random.default_rng(97)
+    specs = [("down", sg.Q6_K, F, H), ("gate", sg.Q4_K, H, F), ("up", sg.Q4_K, H, F)]
+    ws, bufs, descs = {}, [], {}
+    for i, (name, dt, K, M) in enumerate(specs):
+        w = O.quantize(dt, O.normal(K * M * E, 98 + i, 0.0, 0.02))
+        b, t = upload_weights(dev, st, dt, w, K, M, slices=E)
+        ws[name] = w
+        descs[name] = t
+        bufs.append(b)
+    xh = O.normal(T * H, 101).reshape(T, 1, H)
+    xf = O.normal(T * nu * F, 102).reshape(T, nu, F)
+    xhb, xfb = dev.alloc(xh.nbytes), dev.alloc(xf.nbytes)
+    xht, xft = sg.tdesc(sg.F32, (H, 1, T), xhb), sg.tdesc(sg.F32, (F, nu, T), xfb)
+    st.upload(xht, xh)
+    st.upload(xft, xf)
+    ib = dev.alloc(4 * nu * T)
+    it = sg.tdesc(sg.I32, (nu, T), ib)
+    ybs = {name: dev.alloc(4 * M * nu * T) for name, _, _, M in specs}
+    yts = {name: sg.tdesc(sg.F32, (M, nu, T), ybs[name]) for name, _, _, M in specs}
+    ops = [sg.mul_mat_id_op(descs[name], xft if name == "down" else xht, it, yts[name], nu) for name, *_ in specs]
+    nodes = (sg.PlanNode * 3)(*[sg.PlanNode(C.sizeof(sg.PlanNode), op, 0) for op, _ in ops])
+    pdesc = sg.PlanDesc(C.sizeof(sg.PlanDesc), nodes, 3)
+    plan = C.c_void_p()
+    sg.check(sg.lib().scrapgpu_plan_build(dev.handle, C.byref(pdesc), C.byref(plan)), "plan_build")
+    try:
+        for rep in range(3):
+            ids = np.stack([rng.permutation(E)[:nu] for _ in range(T)]).astype(np.int32)
+            st.upload(it, ids)
+            eager = rep == 2
+            if eager:  # (the profiler runs a plan eagerly: the last launch's form is readable)
+                sg.lib().scrapgpu_hip_profile_reset()
+                sg.lib().scrapgpu_hip_profile_enable(1)
+            sg.check(sg.lib().scrapgpu_plan_execute(st.handle, plan), "plan_execute")
+            st.sync()
+            if eager:
+                sg.lib().scrapgpu_hip_profile_enable(0)
+                assert sg.last_launch()[0].endswith("shared-x"), sg.last_launch()
+            got = {name: st.download(yts[name]).reshape(T, nu, M).copy() for name, _, _, M in specs}
+            for (op, _), (name, dt, K, M) in zip(ops, specs):
+                st.execute(op)
+                st.sync()
+                alone = st.download(yts[name]).reshape(T, nu, M)
+                assert np.array_equal(got[name].view(np.uint32), alone.view(np.uint32)), f"rep {rep} {name}: plan and op differ"
+                x = xf if name == "down" else xh
+                check_grouped(got[name], O.mul_mat_id(dt, ws[name], K, M, E, x, ids))
+    finally:
+        sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
+    for b in bufs + list(ybs.values()) + [xhb, xfb, ib]:
+        b.free()
