@@ -2155,6 +2155,9 @@ void * pick_mvc(int nc, bool pre) {
 
 template <int DT, int RG>
 void * pick_burst_rg(int W, int spw) {
+    if (spw <= 2 && (W == 6 || W == 10 || W == 12 || W == 14)) {
+        return W == 6 ? (void *) k_mvb<DT, RG, 6, 2> : W == 10 ? (void *) k_mvb<DT, RG, 10, 2> : W == 12 ? (void *) k_mvb<DT, RG, 12, 2> : (void *) k_mvb<DT, RG, 14, 2>;
+    }
     if (spw <= 2) return W >= 16 ? (void *) k_mvb<DT, RG, 16, 2> : W >= 8 ? (void *) k_mvb<DT, RG, 8, 2> : W >= 4 ? (void *) k_mvb<DT, RG, 4, 2> : (void *) k_mvb<DT, RG, 2, 2>;
     if constexpr (RG == 1) {
         if (spw == 3) return (void *) k_mvb<DT, 1, 16, 3>; // (W = 16 only; 16-row tiles only)
@@ -2411,6 +2414,13 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         // 53.7-55.2 -> 49.5-50.2 us)
         int W = nst <= 2 * sp ? 2 : 4;
         while (W < 16 && (nst + W - 1) / W > sp) W *= 2;
+        // 2 steps per wave: an even number of waves, the fewest that cover K (at most 3 loads
+        // unused: 20 steps as 10 waves, not 16 with 12 of them reloading a step), whose count need
+        // not be a power of two. Against the power of two on one box: Q4_K 5120 x 5120 (20
+        // steps) 8.4-8.5 -> 6.6 us, 13824 x 5120 13.4 -> 11.2, Q8_0 5120 x 5120 11.1 -> 8.5,
+        // Q6_K 10.3 -> 8.3, Q4_K 4096 x 6144 (24 steps) 5.8 -> 5.2, 8192 x 7168 (28 steps) 8.6 ->
+        // 8.5. (MUL_MAT_ID pairs keep the power of two: the instances that read the id ahead.)
+        if (sp == 2 && nst > 8 && L.ids == nullptr && tuning("SCRAPGPU_HIP_MV_W2", 1)) W = (int) std::min<int64_t>(16, 2 * ((nst + 3) / 4));
         // Q4_0 / Q4_K / Q6_K with 33..48 steps: ceil(steps / 4) waves of 4 steps (9..12 waves, at most
         // 3 loads unused), against 16 waves of 3: the Q6_K down projection (48 steps) 9.9 -> 9.5-9.6
         // us and the token 1.074 -> 1.064 ms; 44-step Q4_0 8.4-8.5 -> 7.7, 40-step Q4_K 8.1-8.3 ->

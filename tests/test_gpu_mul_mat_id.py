@@ -379,3 +379,18 @@ def test_mul_mat_id_grouped_plan_shares_routing(hip, form):
         sg.check(sg.lib().scrapgpu_plan_free(plan), "plan_free")
     for b in bufs + list(ybs.values()) + [xhb, xfb, ib]:
         b.free()
+
+
+def test_mul_mat_id_decode_20_steps(hip):
+    """A decode MUL_MAT_ID with K of 20 steps: the pairs keep 16 waves of 2 steps (the instances
+    that read the expert id ahead of x), where a plain MUL_MAT of that K takes 10 waves."""
+    dev, st = hip
+    dtype, K, M, E, T, nu = sg.Q4_K, 5120, 96, 6, 1, 3
+    w = O.quantize(dtype, O.normal(K * M * E, 111, 0.0, 0.02))
+    rng = np.random.default_rng(112)
+    ids = np.stack([rng.permutation(E)[:nu] for _ in range(T)]).astype(np.int32)
+    x = O.normal(T * nu * K, 113).reshape(T, nu, K)
+    y = run_mul_mat_id(dev, st, dtype, w, K, M, E, x, ids)
+    assert sg.last_launch()[0] == "burst rg=1 W=16 spw=2", sg.last_launch()
+    deq = O.dequantize(dtype, w, K * M * E).reshape(E, M, K)
+    check_pairs(y, O.mul_mat_id(dtype, w, K, M, E, x, ids), x, deq, ids)

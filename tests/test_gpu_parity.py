@@ -258,6 +258,31 @@ def test_matvec_decode_long_k_slices(hip, dtype, K, want):
         b.free()
 
 
+@pytest.mark.parametrize("dtype,K,M,want", [(sg.Q4_K, 3072, 320, "burst rg=1 W=6 spw=2"), (sg.Q8_0, 4352, 320, "burst rg=1 W=10 spw=2"),
+                                            (sg.Q4_0, 5120, 320, "burst rg=1 W=10 spw=2"), (sg.Q6_K, 6144, 320, "burst rg=1 W=12 spw=2"),
+                                            (sg.Q4_K, 7168, 6144, "burst rg=2 W=14 spw=2"), (sg.Q4_0, 5120, 13824, "burst rg=2 W=10 spw=2")],
+                         ids=["q4_k_12", "q8_0_17", "q4_0_20", "q6_k_24", "q4_k_28_rg2", "q4_0_20_rg2"])
+def test_matvec_decode_even_wave_counts(hip, dtype, K, M, want):
+    """N = 1 with 9..32 steps of K: an even number of waves of 2 steps, the fewest that cover K
+    (6, 10, 12, 14: not a power of two; the last wave's loads past K discarded), on 16- and 32-row
+    tiles (the launch must show the form; from 64 rows per CU these K take the chunked form)."""
+    dev, st = hip
+    q, deq = quantized(dtype, K, M, 960 + K % 97)
+    x = O.normal(K, 961).reshape(1, K)
+    wb, wt = upload_weights(dev, st, dtype, q, K, M)
+    xb, yb = dev.alloc(x.nbytes), dev.alloc(4 * M)
+    xt, yt = sg.tdesc(sg.F32, (K, 1), xb), sg.tdesc(sg.F32, (M, 1), yb)
+    st.upload(xt, x)
+    op, keep = sg.mul_mat_op(wt, xt, yt)
+    st.execute(op)
+    st.sync()
+    if dev.info().compute_units == 256:
+        assert sg.last_launch()[0] == want, sg.last_launch()
+    check_matvec(st.download(yt).reshape(1, M), O.mul_mat(dtype, q, K, M, x, threads=8), x, deq)
+    for b in (wb, xb, yb):
+        b.free()
+
+
 @pytest.mark.parametrize("dtype", sg.QTYPES, ids=lambda d: sg.NAMES[d])
 def test_matvec_k_split_repeated(hip, dtype):
     """Few row groups + long K (N = 2, 64 steps): the streaming matvec, whose waves split K and
