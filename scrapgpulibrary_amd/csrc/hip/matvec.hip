@@ -2160,7 +2160,13 @@ void * pick_burst_rg(int W, int spw) {
     }
     if (spw <= 2) return W >= 16 ? (void *) k_mvb<DT, RG, 16, 2> : W >= 8 ? (void *) k_mvb<DT, RG, 8, 2> : W >= 4 ? (void *) k_mvb<DT, RG, 4, 2> : (void *) k_mvb<DT, RG, 2, 2>;
     if constexpr (RG == 1) {
-        if (spw == 3) return (void *) k_mvb<DT, 1, 16, 3>; // (W = 16 only; 16-row tiles only)
+        if constexpr (DT == Q8_0) { // (33..48 steps: as many waves of 3 steps as K needs)
+            if (spw == 3 && W < 16) {
+                return W == 11 ? (void *) k_mvb<DT, 1, 11, 3> : W == 12 ? (void *) k_mvb<DT, 1, 12, 3> : W == 13 ? (void *) k_mvb<DT, 1, 13, 3>
+                     : W == 14 ? (void *) k_mvb<DT, 1, 14, 3> : (void *) k_mvb<DT, 1, 15, 3>;
+            }
+        }
+        if (spw == 3) return (void *) k_mvb<DT, 1, 16, 3>; // (16-row tiles only)
         if constexpr (DT != Q8_0) { // (33..48 steps: as many waves of 4 steps as K needs)
             if (W == 12) return (void *) k_mvb<DT, 1, 12, 4>;
             if (W == 11) return (void *) k_mvb<DT, 1, 11, 4>;
@@ -2407,7 +2413,7 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         int rg = q4 && rows * slices >= (int64_t) 96 * cu_count ? 3 : q4 && rows * slices >= (int64_t) tuning("SCRAPGPU_HIP_MV_RG2_ROWS", 24) * cu_count ? 2 : 1;
         if (const int fr = tuning("SCRAPGPU_HIP_MV_RG", 0)) rg = fr >= 3 ? 3 : fr >= 2 ? 2 : 1;
         if (nst > 32) rg = 1; // (also over the override)
-        // 3 steps per wave for 33..48 steps (16 waves) in Q8_0 (below: the other formats)
+        // 3 steps per wave for 33..48 steps on 16 waves (below: as many waves as K needs)
         int sp = nst <= 32 ? 2 : nst <= 48 && rg == 1 && tuning("SCRAPGPU_HIP_MV_SPW3", 1) ? 3 : 4;
         // (K of 4 steps or fewer: 2 waves, so that none is left without a step: the MoE experts'
         // Q6_K down projection, K = 768, as 1024 2-wave work-groups: a 4-layer MoE token
@@ -2424,11 +2430,12 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         // Q4_0 / Q4_K / Q6_K with 33..48 steps: ceil(steps / 4) waves of 4 steps (9..12 waves, at most
         // 3 loads unused), against 16 waves of 3: the Q6_K down projection (48 steps) 9.9 -> 9.5-9.6
         // us and the token 1.074 -> 1.064 ms; 44-step Q4_0 8.4-8.5 -> 7.7, 40-step Q4_K 8.1-8.3 ->
-        // 7.25, 38-step Q6_K 9.9 -> 9.0 us. Q8_0 (its larger step registers) measured 11.1-11.2 ->
-        // 11.3-11.4 us on 4096 x 11008 and keeps 16 waves
-        if (nst > 32 && nst <= 48 && rg == 1 && dt != Q8_0 && tuning("SCRAPGPU_HIP_MV_W4", 1)) {
-            sp = 4;
-            W = (int) ((nst + 3) / 4);
+        // 7.25, 38-step Q6_K 9.9 -> 9.0 us. Q8_0 (its larger step registers: 4 steps measured 11.1-11.2
+        // -> 11.3-11.4 us on 4096 x 11008) takes ceil(steps / 3) waves of 3 steps: 4096 x 11008 (43
+        // steps, 15 waves) 11.15-11.22 -> 10.8, 4096 x 10240 (40 steps, 14 waves) 11.3 -> 10.7 us
+        if (nst > 32 && nst <= 48 && rg == 1 && tuning("SCRAPGPU_HIP_MV_W4", 1)) {
+            sp = dt == Q8_0 ? 3 : 4;
+            W = (int) ((nst + sp - 1) / sp);
         }
         set_tiles(L, mats, nmat, 16 * rg);
         L.cs = sp;

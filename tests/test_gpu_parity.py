@@ -230,12 +230,13 @@ def test_matvec_decode_long_k_chunks_multi(hip):
 
 @pytest.mark.parametrize("dtype,K,want", [(sg.Q4_0, 12288, "burst rg=1 W=12 spw=4"), (sg.Q4_K, 12288, "burst rg=1 W=12 spw=4"),
                                           (sg.Q4_0, 11264, "burst rg=1 W=11 spw=4"), (sg.Q4_K, 10240, "burst rg=1 W=10 spw=4"),
-                                          (sg.Q6_K, 8448, "burst rg=1 W=9 spw=4"), (sg.Q8_0, 11264, "burst rg=1 W=16 spw=3")],
-                         ids=["q4_0_48", "q4_k_48", "q4_0_44", "q4_k_40", "q6_k_33", "q8_0_44"])
+                                          (sg.Q6_K, 8448, "burst rg=1 W=9 spw=4"), (sg.Q8_0, 11264, "burst rg=1 W=15 spw=3"),
+                                          (sg.Q8_0, 12288, "burst rg=1 W=16 spw=3"), (sg.Q8_0, 8448, "burst rg=1 W=11 spw=3")],
+                         ids=["q4_0_48", "q4_k_48", "q4_0_44", "q4_k_40", "q6_k_33", "q8_0_44", "q8_0_48", "q8_0_33"])
 def test_matvec_decode_long_k_slices(hip, dtype, K, want):
-    """N = 1 over 2 slices with K of 33..48 steps: ceil(steps / 4) waves of 4 steps (the last
-    wave's loads past K discarded), or 16 waves of 3 steps for Q8_0; no chunks (one slice only),
-    16-row tiles (the launch must show the form)."""
+    """N = 1 over 2 slices with K of 33..48 steps: ceil(steps / 4) waves of 4 steps (Q8_0:
+    ceil(steps / 3) waves of 3; the last wave's loads past K discarded); no chunks (one slice
+    only), 16-row tiles (the launch must show the form)."""
     dev, st = hip
     M, S = 320, 2
     q0, d0 = quantized(dtype, K, M, 952)
