@@ -2155,6 +2155,9 @@ void * pick_mvc(int nc, bool pre) {
 
 template <int DT, int RG>
 void * pick_burst_rg(int W, int spw) {
+    if constexpr (RG == 1) { // (4-step waves on 16-row tiles: 3..8 waves, see the launcher)
+        if (spw == 4 && W < 8 && W != 4) return W == 3 ? (void *) k_mvb<DT, 1, 3, 4> : W == 5 ? (void *) k_mvb<DT, 1, 5, 4> : W == 6 ? (void *) k_mvb<DT, 1, 6, 4> : (void *) k_mvb<DT, 1, 7, 4>;
+    }
     if (spw <= 2 && (W == 6 || W == 10 || W == 12 || W == 14)) {
         return W == 6 ? (void *) k_mvb<DT, RG, 6, 2> : W == 10 ? (void *) k_mvb<DT, RG, 10, 2> : W == 12 ? (void *) k_mvb<DT, RG, 12, 2> : (void *) k_mvb<DT, RG, 14, 2>;
     }
@@ -2433,6 +2436,15 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         // 7.25, 38-step Q6_K 9.9 -> 9.0 us. Q8_0 (its larger step registers: 4 steps measured 11.1-11.2
         // -> 11.3-11.4 us on 4096 x 11008) takes ceil(steps / 3) waves of 3 steps: 4096 x 11008 (43
         // steps, 15 waves) 11.15-11.22 -> 10.8, 4096 x 10240 (40 steps, 14 waves) 11.3 -> 10.7 us
+        // 16-row tiles at 16 or more per CU (the LM head's 9496): 4-step waves, ceil(steps / 4) of
+        // them, against 2-step ones (A/B on two boxes): Q6_K 151936 x 4096 87.6 -> 84.1-85.0 and
+        // 93.9-95.7 -> 90.7-92.9 us, Q8_0 108 -> 105; at 4 tiles per CU (16384 rows) 11.8 -> 12.6-12.9,
+        // at 8 (32000 rows) 20.3-21.1 -> 21.2-21.3, at one (4096 x 4096) 3.98 -> 5.07, and on 32- and
+        // 48-row tiles (they spill) it loses
+        if (sp == 2 && rg == 1 && nst > 8 && L.ids == nullptr && rows * slices >= (int64_t) 256 * cu_count && tuning("SCRAPGPU_HIP_MV_S4", 1)) {
+            sp = 4;
+            W = (int) ((nst + 3) / 4);
+        }
         if (nst > 32 && nst <= 48 && rg == 1 && tuning("SCRAPGPU_HIP_MV_W4", 1)) {
             sp = dt == Q8_0 ? 3 : 4;
             W = (int) ((nst + sp - 1) / sp);

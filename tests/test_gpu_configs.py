@@ -183,12 +183,15 @@ def test_config4_q4_k_prefill(hip, K, M, N):
 
 @pytest.mark.parametrize("N", [1, 8, 64])
 def test_config5_q6_k_lm_head(hip, N):
-    """the Q6_K LM head, W 151936 x 4096, at batch 1, 8 and 64."""
+    """the Q6_K LM head, W 151936 x 4096, at batch 1, 8 and 64 (batch 1: 16-row tiles
+    of 4 waves of 4 steps, the form for 16 or more tiles per CU)."""
     K, M = 4096, 151936
     q, _, wt = weights(hip, sg.Q6_K, K, M, 700)
     x = O.normal(N * K, 70 + N).reshape(N, K)
     (y,), (form, grid) = run(hip, [wt], x)
     assert form.startswith("burst" if N == 1 else "columns" if N <= 8 else "gemm"), form
+    if N == 1 and cus(hip) == 256:
+        assert form == "burst rg=1 W=4 spw=4", form
     check(sg.Q6_K, q, K, M, x, y, f"Q6_K {M}x{K} N={N} [{form}]")
 
 
