@@ -2121,18 +2121,37 @@ __global__ __launch_bounds__(64 * RW * KW) __attribute__((amdgpu_waves_per_eu(4,
 // waves per work-group: row waves x K waves (measured on the config shapes at N = 2, 4, 8 against
 // 2 x 4, 1 x 8, 2 x 8, 2 x 2, 2 x 1 and 8 x 1: 4 x 2 the fastest or within 5% everywhere)
 constexpr int kMwRW = 4, kMwKW = 2;
+// K of 32 steps or more (down projections: few rows, long K): 2 row waves x 4 K waves, K chunks
+// of 8 steps (half the chunks to hand over). Measured against 4 x 2 (one box): Q8_0 4096 x 11008
+// at N = 2 / 4 / 8 15.2 / 15.2 / 18.0 -> 14.0 / 14.2 / 17.0 us, Q4_K 4096 x 12288 at N = 8 14.9 ->
+// 14.6, Q6_K 4096 x 12288 at N = 4 even; at 16 steps it lost (the Q6_K LM head at N = 8 148 -> 163,
+// gate+up 20.3-20.7 -> 21.4 us)
+int tuning(const char * name, int dflt);
+
+struct MwShape {
+    int rw, kw;
+};
+inline MwShape mw_shape(int64_t nst) {
+    static const bool on = tuning("SCRAPGPU_HIP_MV_MW_LONG", 1) != 0;
+    return on && nst >= 32 ? MwShape{2, 4} : MwShape{kMwRW, kMwKW};
+}
+
+template <int DT, int RW, int KW>
+void * pick_mvw_s(int nc) {
+    switch (nc) {
+        case 2: return (void *) k_mvw<DT, 2, RW, KW>;
+        case 3: return (void *) k_mvw<DT, 3, RW, KW>;
+        case 4: return (void *) k_mvw<DT, 4, RW, KW>;
+        case 5: return (void *) k_mvw<DT, 5, RW, KW>;
+        case 6: return (void *) k_mvw<DT, 6, RW, KW>;
+        case 7: return (void *) k_mvw<DT, 7, RW, KW>;
+        default: return (void *) k_mvw<DT, 8, RW, KW>;
+    }
+}
 
 template <int DT>
-void * pick_mvw(int nc) {
-    switch (nc) {
-        case 2: return (void *) k_mvw<DT, 2, kMwRW, kMwKW>;
-        case 3: return (void *) k_mvw<DT, 3, kMwRW, kMwKW>;
-        case 4: return (void *) k_mvw<DT, 4, kMwRW, kMwKW>;
-        case 5: return (void *) k_mvw<DT, 5, kMwRW, kMwKW>;
-        case 6: return (void *) k_mvw<DT, 6, kMwRW, kMwKW>;
-        case 7: return (void *) k_mvw<DT, 7, kMwRW, kMwKW>;
-        default: return (void *) k_mvw<DT, 8, kMwRW, kMwKW>;
-    }
+void * pick_mvw(int nc, MwShape sh) {
+    return sh.rw == 2 ? pick_mvw_s<DT, 2, 4>(nc) : pick_mvw_s<DT, kMwRW, kMwKW>(nc);
 }
 
 template <int DT, bool PRE>
@@ -2301,16 +2320,17 @@ size_t matvec_scratch_bytes(const MatArgs * mats, int nmat, const IdArgs * id) {
     if (nmat < 1 || !mc_form(mats, nmat, id)) return 0;
     const int64_t nst = (mats[0].K + kStep - 1) / kStep, nchunks = (nst + kMcChunk - 1) / kMcChunk, nsegp = nchunks * kMcChunk * kSegs;
     int64_t tiles = 0, rows_w = 0;
+    const MwShape mws = mw_shape(nst);
     for (int j = 0; j < nmat; ++j) {
         tiles += (mats[j].M + 15) / 16;
-        rows_w += (mats[j].M + 32 * kMwRW - 1) / (32 * kMwRW) * (32 * kMwRW);
+        rows_w += (mats[j].M + 32 * mws.rw - 1) / (32 * mws.rw) * (32 * mws.rw);
     }
     const size_t nc = (size_t) mats[0].N;
     // k_mvc: x planes and factors, K-chunk partial sums and counts
     size_t b = (nc * (size_t) nsegp * sizeof(XSeg) + 255) / 256 * 256 + (nc * (size_t) nsegp * sizeof(float4) + 255) / 256 * 256;
     if (nchunks > 1) b += ((size_t) nchunks * nc * (size_t) tiles * 16 * sizeof(float) + 255) / 256 * 256 + (size_t) tiles * sizeof(uint32_t);
     // k_mvw: K-chunk partial sums
-    const int64_t wchunks = (nst + 2 * kMwKW - 1) / (2 * kMwKW);
+    const int64_t wchunks = (nst + 2 * mws.kw - 1) / (2 * mws.kw);
     const size_t bw = wchunks > 1 ? ((size_t) wchunks * nc * (size_t) rows_w * sizeof(float) + 255) / 256 * 256 : 0;
     return std::max<size_t>(std::max<size_t>(b, bw), 256);
 }
@@ -2470,7 +2490,8 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
     // (or SCRAPGPU_HIP_MV_MW=0) k_mvc
     static const bool mw_on = tuning("SCRAPGPU_HIP_MV_MW", 1) != 0;
     if (mw_on && scratch != nullptr && arrive != nullptr && L.xvec && mc_form(mats, nmat, id)) {
-        constexpr int R = 32 * kMwRW, CH = 2 * kMwKW;
+        const MwShape mws = mw_shape(nst);
+        const int R = 32 * mws.rw, CH = 2 * mws.kw;
         MwArgs C;
         std::memset(&C, 0, sizeof(C));
         for (int j = 0; j < 3; ++j) {
@@ -2492,8 +2513,8 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         C.part = reinterpret_cast<float *>(scratch);
         C.arrive = arrive;
         C.prow = tiles * R;
-        void * fn = dt == Q4_0 ? pick_mvw<Q4_0>(nc) : dt == Q8_0 ? pick_mvw<Q8_0>(nc) : dt == Q4_K ? pick_mvw<Q4_K>(nc) : pick_mvw<Q6_K>(nc);
-        const size_t lds = (size_t) nc * CH * kSegs * (sizeof(XSeg) + sizeof(float4)) + (size_t) kMwKW * kMwRW * nc * 32 * sizeof(float) + 32;
+        void * fn = dt == Q4_0 ? pick_mvw<Q4_0>(nc, mws) : dt == Q8_0 ? pick_mvw<Q8_0>(nc, mws) : dt == Q4_K ? pick_mvw<Q4_K>(nc, mws) : pick_mvw<Q6_K>(nc, mws);
+        const size_t lds = (size_t) nc * CH * kSegs * (sizeof(XSeg) + sizeof(float4)) + (size_t) mws.kw * mws.rw * nc * 32 * sizeof(float) + 32;
         if (lds > 65536) {
             static std::mutex mu;
             std::lock_guard<std::mutex> lock(mu);
@@ -2504,7 +2525,7 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         std::snprintf(last_form().form, sizeof(last_form().form), "columns mfma32 nc=%d chunks=%d", nc, (int) C.nchunks);
         last_form().grid = (uint64_t) tiles * (uint64_t) C.nchunks;
         void * args[] = {&C};
-        return hipLaunchKernel(fn, dim3((unsigned) tiles, (unsigned) C.nchunks), dim3(64 * kMwRW * kMwKW), args, lds, stream);
+        return hipLaunchKernel(fn, dim3((unsigned) tiles, (unsigned) C.nchunks), dim3(64 * mws.rw * mws.kw), args, lds, stream);
     }
     if (scratch != nullptr && mc_form(mats, nmat, id)) {
         // several columns: x pre-pass, then one work-group per 16 rows and K chunk

@@ -172,6 +172,8 @@ FORMS = {  # name: (K, M, N, slices, kernel form prefix, x offset in floats)
     "columns_2": (4096, 96, 2, 1, "columns mfma32 nc=2 chunks=4", 0),
     "columns_8": (4096, 200, 8, 1, "columns mfma32 nc=8 chunks=4", 0),
     "columns_one_chunk": (768, 96, 5, 1, "columns mfma32 nc=5 chunks=1", 0),
+    "columns_long_k": (8192, 96, 4, 1, "columns mfma32 nc=4 chunks=4", 0),  # (32 steps: 2 x 4 waves, 8-step chunks)
+    "columns_long_k_8": (12288, 200, 8, 1, "columns mfma32 nc=8 chunks=6", 0),
     "columns_unaligned_x": (12288, 96, 5, 1, "columns nc=5 chunks=3 pre", 1),
     "stream_columns": (4096, 64, 4, 2, "stream-columns nc=4", 0),
 }
