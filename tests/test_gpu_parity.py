@@ -231,8 +231,10 @@ def test_matvec_decode_long_k_chunks_multi(hip):
 @pytest.mark.parametrize("dtype,K,want", [(sg.Q4_0, 12288, "burst rg=1 W=12 spw=4"), (sg.Q4_K, 12288, "burst rg=1 W=12 spw=4"),
                                           (sg.Q4_0, 11264, "burst rg=1 W=11 spw=4"), (sg.Q4_K, 10240, "burst rg=1 W=10 spw=4"),
                                           (sg.Q6_K, 8448, "burst rg=1 W=9 spw=4"), (sg.Q8_0, 11264, "burst rg=1 W=15 spw=3"),
-                                          (sg.Q8_0, 12288, "burst rg=1 W=16 spw=3"), (sg.Q8_0, 8448, "burst rg=1 W=11 spw=3")],
-                         ids=["q4_0_48", "q4_k_48", "q4_0_44", "q4_k_40", "q6_k_33", "q8_0_44", "q8_0_48", "q8_0_33"])
+                                          (sg.Q8_0, 12288, "burst rg=1 W=16 spw=3"), (sg.Q8_0, 8448, "burst rg=1 W=11 spw=3"),
+                                          (sg.Q4_0, 10016, "burst rg=1 W=10 spw=4"), (sg.Q8_0, 9248, "burst rg=1 W=13 spw=3")],
+                         ids=["q4_0_48", "q4_k_48", "q4_0_44", "q4_k_40", "q6_k_33", "q8_0_44", "q8_0_48", "q8_0_33", "q4_0_ragged_40",
+                              "q8_0_ragged_37"])
 def test_matvec_decode_long_k_slices(hip, dtype, K, want):
     """N = 1 over 2 slices with K of 33..48 steps: ceil(steps / 4) waves of 4 steps (Q8_0:
     ceil(steps / 3) waves of 3; the last wave's loads past K discarded); no chunks (one slice
