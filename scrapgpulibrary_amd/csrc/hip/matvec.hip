@@ -619,9 +619,10 @@ __device__ __forceinline__ Where where_of(const MvArgs & A) {
 }
 
 // where_of for the burst form's MUL_MAT_ID instances (ids present) in two halves, so that the
-// pair's expert id is not a round trip ahead of its x loads: where_first() needs no memory read and issues the id load (a vector
-// load from one address: its wait counts in order, so the x loads issued after it stay in flight),
-// where_second() turns the id into the weight offset once the x loads are out.
+// pair's expert id is not a round trip ahead of its x loads: where_first() needs no memory read
+// and issues the id load (a vector load from one address: its wait counts in order, so the x
+// loads issued after it stay in flight), where_second() turns the id into the weight offset once
+// the x loads are out.
 __device__ __forceinline__ Where where_first(const MvArgs & A, int32_t & eid) {
     Where w;
     const uint32_t pr = blockIdx.y, nu = (uint32_t) A.n_used;
@@ -2174,26 +2175,50 @@ void * pick_mvc(int nc, bool pre) {
 
 template <int DT, int RG>
 void * pick_burst_rg(int W, int spw) {
-    if constexpr (RG == 1) { // (4-step waves on 16-row tiles: 3..8 waves, see the launcher)
-        if (spw == 4 && W < 8 && W != 4) return W == 3 ? (void *) k_mvb<DT, 1, 3, 4> : W == 5 ? (void *) k_mvb<DT, 1, 5, 4> : W == 6 ? (void *) k_mvb<DT, 1, 6, 4> : (void *) k_mvb<DT, 1, 7, 4>;
-    }
-    if (spw <= 2 && (W == 6 || W == 10 || W == 12 || W == 14)) {
-        return W == 6 ? (void *) k_mvb<DT, RG, 6, 2> : W == 10 ? (void *) k_mvb<DT, RG, 10, 2> : W == 12 ? (void *) k_mvb<DT, RG, 12, 2> : (void *) k_mvb<DT, RG, 14, 2>;
-    }
-    if (spw <= 2) return W >= 16 ? (void *) k_mvb<DT, RG, 16, 2> : W >= 8 ? (void *) k_mvb<DT, RG, 8, 2> : W >= 4 ? (void *) k_mvb<DT, RG, 4, 2> : (void *) k_mvb<DT, RG, 2, 2>;
-    if constexpr (RG == 1) {
-        if constexpr (DT == Q8_0) { // (33..48 steps: as many waves of 3 steps as K needs)
-            if (spw == 3 && W < 16) {
-                return W == 11 ? (void *) k_mvb<DT, 1, 11, 3> : W == 12 ? (void *) k_mvb<DT, 1, 12, 3> : W == 13 ? (void *) k_mvb<DT, 1, 13, 3>
-                     : W == 14 ? (void *) k_mvb<DT, 1, 14, 3> : (void *) k_mvb<DT, 1, 15, 3>;
-            }
+    // the instances a launch can ask for: 2-step waves in any even count up to 16 (and 2, 4); on
+    // 16-row tiles also 4-step waves (3..12 of them, Q8_0 excepted past 8) and 3-step waves (Q8_0:
+    // 11..16; the other formats: 16) -- the launcher picks W and spw
+    if (spw <= 2) {
+        switch (W) {
+            case 2: return (void *) k_mvb<DT, RG, 2, 2>;
+            case 4: return (void *) k_mvb<DT, RG, 4, 2>;
+            case 6: return (void *) k_mvb<DT, RG, 6, 2>;
+            case 8: return (void *) k_mvb<DT, RG, 8, 2>;
+            case 10: return (void *) k_mvb<DT, RG, 10, 2>;
+            case 12: return (void *) k_mvb<DT, RG, 12, 2>;
+            case 14: return (void *) k_mvb<DT, RG, 14, 2>;
+            default: return (void *) k_mvb<DT, RG, 16, 2>;
         }
-        if (spw == 3) return (void *) k_mvb<DT, 1, 16, 3>; // (16-row tiles only)
-        if constexpr (DT != Q8_0) { // (33..48 steps: as many waves of 4 steps as K needs)
-            if (W == 12) return (void *) k_mvb<DT, 1, 12, 4>;
-            if (W == 11) return (void *) k_mvb<DT, 1, 11, 4>;
-            if (W == 10) return (void *) k_mvb<DT, 1, 10, 4>;
-            if (W == 9) return (void *) k_mvb<DT, 1, 9, 4>;
+    }
+    if constexpr (RG == 1) {
+        if (spw == 3) {
+            if constexpr (DT == Q8_0) {
+                switch (W) {
+                    case 11: return (void *) k_mvb<DT, 1, 11, 3>;
+                    case 12: return (void *) k_mvb<DT, 1, 12, 3>;
+                    case 13: return (void *) k_mvb<DT, 1, 13, 3>;
+                    case 14: return (void *) k_mvb<DT, 1, 14, 3>;
+                    case 15: return (void *) k_mvb<DT, 1, 15, 3>;
+                    default: break;
+                }
+            }
+            return (void *) k_mvb<DT, 1, 16, 3>;
+        }
+        switch (W) {
+            case 3: return (void *) k_mvb<DT, 1, 3, 4>;
+            case 5: return (void *) k_mvb<DT, 1, 5, 4>;
+            case 6: return (void *) k_mvb<DT, 1, 6, 4>;
+            case 7: return (void *) k_mvb<DT, 1, 7, 4>;
+            default: break;
+        }
+        if constexpr (DT != Q8_0) {
+            switch (W) {
+                case 9: return (void *) k_mvb<DT, 1, 9, 4>;
+                case 10: return (void *) k_mvb<DT, 1, 10, 4>;
+                case 11: return (void *) k_mvb<DT, 1, 11, 4>;
+                case 12: return (void *) k_mvb<DT, 1, 12, 4>;
+                default: break;
+            }
         }
     }
     return W >= 16 ? (void *) k_mvb<DT, RG, 16, 4> : W >= 8 ? (void *) k_mvb<DT, RG, 8, 4> : (void *) k_mvb<DT, RG, 4, 4>;
