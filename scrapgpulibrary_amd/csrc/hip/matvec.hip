@@ -2459,6 +2459,9 @@ hipError_t launch_matvec(const MatArgs * mats, int nmat, int cu_count, hipStream
         const bool q4 = dt == Q4_K || dt == Q4_0;
         // (past 32 steps of K, 16-row tiles: the 32- and 48-row forms spill at 3-4 steps per wave)
         int rg = q4 && rows * slices >= (int64_t) 96 * cu_count ? 3 : q4 && rows * slices >= (int64_t) tuning("SCRAPGPU_HIP_MV_RG2_ROWS", 24) * cu_count ? 2 : 1;
+        // MUL_MAT_ID pairs: 16-row tiles (the Qwen3-30B-A3B MoE token's Q4_K gate+up pairs, 8 x
+        // 1536 rows: 32-row tiles 0.480 ms per 48-layer token, 16-row ones 0.474-0.475; A/B on one box)
+        if (L.ids != nullptr && tuning("SCRAPGPU_HIP_MV_ID_RG1", 1)) rg = 1;
         if (const int fr = tuning("SCRAPGPU_HIP_MV_RG", 0)) rg = fr >= 3 ? 3 : fr >= 2 ? 2 : 1;
         if (nst > 32) rg = 1; // (also over the override)
         // 3 steps per wave for 33..48 steps on 16 waves (below: as many waves as K needs)
